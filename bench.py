@@ -1,0 +1,243 @@
+"""Benchmark of the FADE tiered-KV hot path on one MI355X.
+
+One step = one fused tiered decode-attention call (one query token per
+(batch row, query head)) over the whole synthetic cache of BASELINE
+config 1: Llama-3-8B-shaped layer, batch 16, 32 query / 8 KV heads,
+head_dim 128, 8192 cached tokens = 4 fp16 sinks + 8124 INT4 middle tokens
+(per-channel K / per-token V scales, the reference format) + 64 fp16 recent.
+
+The timed loop rotates over several cache instances (>= 512 MB together)
+so the 256 MB Infinity Cache cannot hold the working set; inputs are
+resident in HBM before timing starts.  Prints one JSON line.
+
+  python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from fade_amd import quant as fq  # noqa: E402
+from fade_amd import rotated_quant as frq  # noqa: E402
+from fade_amd.kernels.tiered_attn import MiddleTier, TieredDecodePlan  # noqa: E402
+from fade_amd.synthetic import CONFIGS, kv_tensors  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "fused INT4 tiered decode attn latency (µs) + achieved HBM GB/s vs peak, 1 GPU"
+N_INSTANCES = 4
+
+
+def decode_bytes(cfg, fmt: str) -> int:
+    """Algorithmic bytes of one decode call: each KV byte once, plus q in and out."""
+    D, ns_nr, mid = cfg.D, cfg.n_sink + cfg.recent, cfg.mid
+    per_head = ns_nr * D * 4
+    if fmt == "int4":
+        per_head += mid * D + 2 * D + 2 * mid
+    elif fmt == "k4v2":  # reference literal: int8 V codes, S padded to 64, [G, D] fp16 scales
+        pad = -(-mid // 64) * 64
+        per_head += mid * D // 2 + 2 * D + pad * D + (pad // 64) * D * 2
+    elif fmt == "rot2":  # rotated K2/V2: 2-bit packed codes, K per-channel + V per-token scales
+        per_head += mid * D // 4 * 2 + 2 * D + 2 * mid
+    elif fmt == "fp16":
+        per_head += mid * D * 4
+    return cfg.B * cfg.Hkv * per_head + 2 * cfg.B * cfg.Hq * D * 2
+
+
+def build_instances(cfg, fmt: str, dev, seed: int, n: int):
+    """Quantize the middle tier once on the GPU, then clone it into n distinct allocations."""
+    q, k, v = kv_tensors(cfg.B, cfg.Hkv, cfg.S, cfg.D, seed=seed, Hq=cfg.Hq)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    del k, v
+    ns, nr, S = cfg.n_sink, cfg.recent, cfg.S
+    km, vm = kd[:, :, ns : S - nr].contiguous(), vd[:, :, ns : S - nr].contiguous()
+    sink = (kd[:, :, :ns].contiguous(), vd[:, :, :ns].contiguous())
+    rec = (kd[:, :, S - nr :].contiguous(), vd[:, :, S - nr :].contiguous())
+    pre = None
+    if fmt == "int4":
+        kq, ks = fq.quant_k_int4(km)
+        vq, vs = fq.quant_v_int4(vm)
+        mid = MiddleTier("int4", kq, vq, ks, vs)
+    elif fmt == "k4v2":
+        kq, ks = fq.quant_k_int4(km)
+        vq, vs = fq.quant_int2_padded(vm, 64)
+        mid = MiddleTier("k4v2", kq, vq, ks, vs, group=64, length=cfg.mid)
+    elif fmt == "rot2":
+        R = torch.from_numpy(np.load(os.path.join(ROOT, "tests", "golden", "rotation_d128_seed42.npy"))).to(dev)
+        kq, ks = frq.rotated_quant_k(km, R, 2)
+        vq, vs = frq.rotated_quant_v(vm, R, 2)
+        mid = MiddleTier("sym", kq, vq, ks, vs, k_bits=2, v_bits=2)
+        pre = R
+    else:
+        mid = MiddleTier("fp16", km, vm)
+    del kd, vd
+    plans = []
+    for _ in range(n):
+        m = MiddleTier(mid.fmt, *(t.clone() if t is not None else None for t in
+                                  (mid.k_codes, mid.v_codes, mid.k_scale, mid.v_scale, mid.k_zero, mid.v_zero)),
+                       k_bits=mid.k_bits, v_bits=mid.v_bits, group=mid.group, length=mid.length)
+        qq = qd if pre is None else (qd.float() @ pre.T).to(torch.float16)
+        s = tuple(t.clone() for t in sink) if pre is None else tuple((t.float() @ pre.T).half() for t in sink)
+        r = tuple(t.clone() for t in rec) if pre is None else tuple((t.float() @ pre.T).half() for t in rec)
+        plans.append(TieredDecodePlan(qq, s, m, r))
+    return plans
+
+
+def time_plans(plans, steps: int, warmup: int, stream):
+    """Back-to-back launches rotating over instances; per-call HIP events on the launch stream."""
+    for i in range(warmup):
+        plans[i % len(plans)].run(stream.cuda_stream)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        for i in range(steps):
+            ev[i][0].record(stream)
+            plans[i % len(plans)].run(stream.cuda_stream)
+            ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    per_call = np.array([a.elapsed_time(b) for a, b in ev])  # ms
+    span_ms = ev[0][0].elapsed_time(ev[-1][1])
+    return wall_ms / steps, float(np.median(per_call)), float(per_call.mean()), span_ms / steps
+
+
+def cpu_baseline(cfg, seed: int):
+    """The oracle's dequantize + concatenate + fp32 SDPA on a bounded sample (two batch rows)."""
+    from oracle import attention as oatt
+    from oracle import quant as oq
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover
+        threads = 1
+    rows = 2
+    q, k, v = kv_tensors(rows, cfg.Hkv, cfg.S, cfg.D, seed=seed, Hq=cfg.Hq)
+    q, k, v = q.numpy(), k.numpy(), v.numpy()
+    ns, nr, S = cfg.n_sink, cfg.recent, cfg.S
+    kq, ks = oq.quant_k_int4(k[:, :, ns : S - nr])
+    vq, vs = oq.quant_v_int4(v[:, :, ns : S - nr])
+    mid = {"fmt": "int4", "kq": kq, "ks": ks, "vq": vq, "vs": vs}
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        K, V = oatt.materialize(k[:, :, :ns], v[:, :, :ns], mid, k[:, :, S - nr :], v[:, :, S - nr :])
+        oatt.sdpa_fp32(q, K.astype(np.float32), V.astype(np.float32))
+        times.append(time.perf_counter() - t0)
+    per_call_us = float(np.median(times)) * 1e6 * cfg.B / rows
+    return {
+        "value": round(per_call_us, 1),
+        "unit": "us per decode call (config 1, extrapolated from the sample)",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"{rows} of {cfg.B} batch rows of config 1, median of 3 runs of oracle dequant+cat+fp32 SDPA, "
+        f"scaled x{cfg.B // rows}; host has {os.cpu_count()} logical CPUs",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="only the config-1 INT4 line")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            "bench.py: this build measures one GPU; the decode path shards by batch / kv head "
+            "(no exchange) and is not run across GPUs here.",
+            file=sys.stderr,
+        )
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(dev)
+    cfg = CONFIGS[1]
+
+    plans = build_instances(cfg, "int4", dev, 1001, N_INSTANCES)
+    ms_step, med_ms, mean_ms, span_ms = time_plans(plans, args.steps, args.warmup, stream)
+    nbytes = decode_bytes(cfg, "int4")
+    achieved = nbytes / (mean_ms * 1e-3) / 1e9
+    del plans
+    torch.cuda.empty_cache()
+
+    extra = {}
+    if not args.no_extra:
+        fp = build_instances(cfg, "fp16", dev, 1001, N_INSTANCES)
+        _, fmed, fmean, _ = time_plans(fp, args.steps, args.warmup, stream)
+        fb = decode_bytes(cfg, "fp16")
+        extra["c1_fp16_flash_decode"] = {
+            "us": round(fmean * 1e3, 2), "GBps": round(fb / (fmean * 1e-3) / 1e9, 1), "bytes": fb,
+            "int4_speedup": round(fmean / mean_ms, 2),
+        }
+        del fp
+        torch.cuda.empty_cache()
+        c2 = CONFIGS[2]
+        for fmt in ("k4v2", "int4", "rot2"):
+            pl = build_instances(c2, fmt, dev, 1002, N_INSTANCES)
+            _, m2, mean2, _ = time_plans(pl, max(20, args.steps // 2), args.warmup, stream)
+            b2 = decode_bytes(c2, fmt)
+            extra[f"c2_32k_{fmt}"] = {
+                "us": round(mean2 * 1e3, 2), "GBps": round(b2 / (mean2 * 1e-3) / 1e9, 1), "bytes": b2,
+                "frac_of_peak": round(b2 / (mean2 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 3),
+            }
+            del pl
+            torch.cuda.empty_cache()
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "decode_c1_int4_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_call")
+
+    line = {
+        "metric": METRIC,
+        "value": round(mean_ms * 1e3, 2),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 codes / fp16 tiers, fp32 accumulate",
+        "data": "synthetic (seeded N(0,1) K*LogNormal(0,0.5) channel scales, V, Q)",
+        "config": {
+            "workload": "config 1: fused tiered decode, B=16, Hq=32, Hkv=8, D=128, S=8192 "
+            "(4 fp16 sink + 8124 INT4 + 64 fp16 recent), reference INT4 format",
+            "instances_rotated": N_INSTANCES,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_call": nbytes,
+            "timed": "HIP events around each call (split kernel + combine) on the launch stream",
+            "median_us": round(med_ms * 1e3, 2),
+        },
+        "extra": extra,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(cfg, 1001)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

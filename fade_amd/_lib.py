@@ -1,0 +1,195 @@
+"""ctypes binding of ``libfade_hip.so`` (the C ABI declared in ``include/fade_hip.h``).
+
+The library is loaded after ``import torch`` so that it binds to the HIP
+runtime torch already mapped (one runtime per process).  There is no CPU
+fallback: every op in this package raises when the library is missing or
+when it is handed a CPU tensor.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libfade_hip.so")
+
+FADE_OK = 0
+FADE_ERUNTIME = -1
+FADE_EINVAL = -22
+
+AXIS_CHANNEL = 0
+AXIS_TOKEN = 1
+
+MID_NONE = 0
+MID_FP16 = 1
+MID_SYM = 2
+MID_K4V2G = 3
+MID_ASYM = 4
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_p = ctypes.c_void_p
+_pi64 = ctypes.POINTER(ctypes.c_int64)
+
+
+class Fp16Tier(ctypes.Structure):
+    _fields_ = [
+        ("k", _p),
+        ("v", _p),
+        ("len", _i64),
+        ("k_sb", _i64),
+        ("k_sh", _i64),
+        ("k_ss", _i64),
+        ("v_sb", _i64),
+        ("v_sh", _i64),
+        ("v_ss", _i64),
+    ]
+
+
+class MidTier(ctypes.Structure):
+    _fields_ = [
+        ("fmt", _i32),
+        ("k_bits", _i32),
+        ("v_bits", _i32),
+        ("group", _i32),
+        ("len", _i64),
+        ("v_rows", _i64),
+        ("k_codes", _p),
+        ("k_scale", _p),
+        ("k_zero", _p),
+        ("v_codes", _p),
+        ("v_scale", _p),
+        ("v_zero", _p),
+    ]
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", _i64),
+        ("Hq", _i64),
+        ("Hkv", _i64),
+        ("D", _i64),
+        ("q", _p),
+        ("q_sb", _i64),
+        ("q_sh", _i64),
+        ("out", _p),
+        ("o_sb", _i64),
+        ("o_sh", _i64),
+        ("sm_scale", ctypes.c_float),
+        ("sink", Fp16Tier),
+        ("mid", MidTier),
+        ("recent", Fp16Tier),
+        ("n_splits", _i32),
+        ("kernel", _i32),
+        ("workspace", _p),
+        ("workspace_bytes", _i64),
+    ]
+
+
+# name -> argtypes; every function returns int (status) unless listed in _RESTYPES.
+_SIGNATURES: dict[str, list] = {
+    "fade_hip_abi_version": [],
+    "fade_hip_last_error": [],
+    "fade_pack_codes": [_p, _i64, _i64, _i32, _p, _p],
+    "fade_unpack_codes": [_p, _i64, _i64, _i32, _p, _p],
+    "fade_quant_k_int4_workspace_bytes": [_i64, _i64, _i64, _i64, _pi64],
+    "fade_quant_k_int4": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p],
+    "fade_quant_v_int4": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p],
+    "fade_dequant_sym": [_p, _p, _i32, _i32, _i64, _i64, _i64, _i64, _p, _p],
+    "fade_quant_int2_grouped": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p],
+    "fade_dequant_int2_grouped": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
+    "fade_quant_rotated_workspace_bytes": [_i64, _i64, _i64, _i64, _i32, _pi64],
+    "fade_quant_rotated": [_p, _i64, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _i64, _p],
+    "fade_quant_asym": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p],
+    "fade_dequant_asym": [_p, _p, _p, _i32, _i32, _i64, _i64, _i64, _i64, _p, _p],
+    "fade_rerope_gather": [
+        _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+        _p, _i64, _p, _p, _p, _p, _p, _p, _p,
+    ],
+    "fade_tiered_decode_workspace_bytes": [ctypes.POINTER(DecodeArgs), _pi64],
+    "fade_tiered_decode_attn": [ctypes.POINTER(DecodeArgs), _p],
+}
+_RESTYPES = {"fade_hip_last_error": ctypes.c_char_p}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raise if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"fade_amd: HIP library not found at {LIB_PATH}; build it with "
+                    "`python -c 'import __graft_entry__ as g; g.build()'` or "
+                    "`make -C fade_amd/csrc`"
+                )
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, argtypes in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = argtypes
+                fn.restype = _RESTYPES.get(name, ctypes.c_int)
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == FADE_OK:
+        return
+    msg = load().fade_hip_last_error()
+    msg = msg.decode() if msg else what
+    if rc == FADE_EINVAL:
+        raise ValueError(msg)
+    raise RuntimeError(f"{what}: {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args), name)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_gpu(*tensors: torch.Tensor | None, op: str = "fade_amd") -> None:
+    """Reject CPU tensors: the hot path has no CPU implementation."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                f"{op}: the MI355X kernels need GPU tensors (got a tensor on {t.device}); "
+                "fade_amd has no CPU fallback"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"{op}: tensors are on different devices ({dev} vs {t.device})")
+
+
+def require_f16(t: torch.Tensor, op: str) -> None:
+    if t.dtype != torch.float16:
+        raise ValueError(f"{op}: expected a float16 tensor, got {t.dtype}")
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)

@@ -1,0 +1,687 @@
+"""Tiered KV cache on MI355X kernels (drop-in for fade/cache.py's ``TieredKVCache``).
+
+Per layer the cache holds fp16 sinks, a packed middle tier and an fp16
+recent window (plus an optional INT2 tier), with the same state fields,
+HF ``Cache`` protocol and tier API as the reference (fade/cache.py:52-1230).
+What changes is where the work runs:
+
+  * quantize + pack, dequantize, grouped INT2: ``libfade_hip.so`` kernels;
+  * eviction re-RoPE: one fused gather/un-RoPE/re-RoPE pass over the kept
+    rows only (``fade_rerope_gather``) instead of fp32 passes over all S;
+  * ``decode_attention(q, layer_idx)``: attention straight from the tiers
+    (``fade_tiered_decode_attn``) without the dequantize + ``torch.cat``
+    materialization that ``update()`` performs for HF's attention modules.
+"""
+
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass
+from pathlib import Path
+
+import torch
+from torch import Tensor
+from transformers.cache_utils import DynamicCache
+
+from . import _lib
+from .backends import AsymGroupBackend, QuantBackend, RotatedINT4Backend, SymmetricINT4Backend, get_backend
+from .quant import (
+    DEFAULT_INT2_GROUP_SIZE,
+    dequant_int2_trimmed,
+    dequant_int4,
+    quant_int2_padded,
+    quant_k_int4,
+    quant_v_int4,
+)
+from .rope import RopeScheme, Vanilla, rerope_gather
+
+DEFAULT_N_SINK: int = 4
+DEFAULT_RECENT_WINDOW: int = 128
+DEFAULT_INT4_BUDGET: int | None = None
+DEFAULT_INT2_BUDGET: int = 0
+DEFAULT_ROPE_THETA: float = 10000.0
+DEFAULT_FP16_PREALLOC: int = 128
+DEFAULT_MAX_DEQUANT_AGE: int | None = None
+
+TIER_FP16: int = 0
+TIER_INT4: int = 1
+TIER_INT2: int = 2
+TIER_EVICT: int = 3
+TIER_PQ: int = 4
+
+
+@dataclass
+class LayerState:
+    """Per-layer tier state (fade/cache.py:52-133).  ``*_pos`` hold absolute positions.
+
+    Invariant: the position-ordered cache is ``sink | middle | fp16 recent``.
+    """
+
+    sink_k: Tensor | None = None
+    sink_v: Tensor | None = None
+    sink_pos: Tensor | None = None
+    fp16_k: Tensor | None = None
+    fp16_v: Tensor | None = None
+    fp16_pos: Tensor | None = None
+    int4_kq: Tensor | None = None
+    int4_ks: Tensor | None = None
+    int4_vq: Tensor | None = None
+    int4_vs: Tensor | None = None
+    int4_pos: Tensor | None = None
+    int2_kq: Tensor | None = None
+    int2_ks: Tensor | None = None
+    int2_vq: Tensor | None = None
+    int2_vs: Tensor | None = None
+    int2_pos: Tensor | None = None
+    int2_actual_count: int = 0
+    int2_group_size: int = DEFAULT_INT2_GROUP_SIZE
+    sink_count: int = 0
+    next_position: int = 0
+    int4_k_deq: Tensor | None = None
+    int4_v_deq: Tensor | None = None
+    int2_k_deq: Tensor | None = None
+    int2_v_deq: Tensor | None = None
+    _fp16_buf_k: Tensor | None = None
+    _fp16_buf_v: Tensor | None = None
+    _fp16_buf_pos: Tensor | None = None
+    _fp16_len: int = 0
+    _dequant_age: int = 0
+    backend_k: dict | None = None
+    backend_v: dict | None = None
+    backend_pos: Tensor | None = None
+    _compressed_bytes: int = 0
+
+    def total_seq_length(self) -> int:
+        return sum(
+            int(p.shape[0])
+            for p in (self.sink_pos, self.fp16_pos, self.int4_pos, self.int2_pos, self.backend_pos)
+            if p is not None
+        )
+
+
+def _sel(x: Tensor, idx: Tensor) -> Tensor:
+    return x.index_select(-2, idx).contiguous()
+
+
+class TieredKVCache(DynamicCache):
+    """Tiered KV cache with attention-aware compression (fade/cache.py:136-225).
+
+    Shared-tier mode (``tiers`` is ``[S]`` for all rows and heads) and
+    per-sequence mode (``apply_tier_assignment_per_sequence``) as in the
+    reference.  Only float16 caches are supported by the kernels.
+    """
+
+    def __init__(
+        self,
+        n_sink: int = DEFAULT_N_SINK,
+        recent_window: int = DEFAULT_RECENT_WINDOW,
+        int4_budget: int | None = DEFAULT_INT4_BUDGET,
+        int2_budget: int = DEFAULT_INT2_BUDGET,
+        dtype: torch.dtype = torch.float16,
+        cache_dequant: bool = True,
+        rope_theta: float = DEFAULT_ROPE_THETA,
+        head_dim: int | None = None,
+        batch_size: int | None = None,
+        rope_scheme: RopeScheme | None = None,
+        middle_k_bits: int = 4,
+        middle_v_bits: int = 4,
+        quant_backend: str | QuantBackend = "int4",
+    ) -> None:
+        super().__init__()
+        if dtype != torch.float16:
+            raise ValueError(f"fade_amd TieredKVCache supports dtype=torch.float16 only, got {dtype}")
+        self.n_sink = n_sink
+        self.recent_window = recent_window
+        self.int4_budget = int4_budget
+        self.int2_budget = int2_budget
+        self.dtype = dtype
+        self.cache_dequant = cache_dequant
+        self.rope_theta = rope_theta
+        self.head_dim = head_dim
+        self.batch_size = batch_size
+        self.max_dequant_age = DEFAULT_MAX_DEQUANT_AGE
+        self.middle_k_bits = middle_k_bits
+        self.middle_v_bits = middle_v_bits
+        if isinstance(quant_backend, str):
+            self._quant_backend: QuantBackend = get_backend(quant_backend, head_dim=head_dim or 64)
+        else:
+            self._quant_backend = quant_backend
+        self._rope_scheme = rope_scheme
+        self._skip_layers: set[int] = set()
+        self._layers: list[LayerState] = []
+
+    # transformers 5.x defines a read-only ``Cache.batch_size``; the tiered cache
+    # pins the batch size on the first update (fade/cache.py:367-373).
+    @property
+    def batch_size(self) -> int | None:
+        return self.__dict__.get("_pinned_batch_size")
+
+    @batch_size.setter
+    def batch_size(self, value: int | None) -> None:
+        self.__dict__["_pinned_batch_size"] = value
+
+    # ------------------------------------------------------------ bookkeeping
+    def set_skip_layers(self, layer_indices) -> None:
+        self._skip_layers = set(layer_indices)
+
+    @property
+    def managed_layers(self) -> set[int]:
+        return {i for i in range(len(self._layers)) if i not in self._skip_layers}
+
+    def is_managed(self, layer_idx: int) -> bool:
+        return layer_idx not in self._skip_layers
+
+    def _ensure_rope_scheme(self) -> RopeScheme:
+        if self._rope_scheme is None:
+            self._rope_scheme = Vanilla(theta=self.rope_theta, head_dim=self.head_dim or 64)
+        return self._rope_scheme
+
+    @property
+    def rope_scheme(self) -> RopeScheme:
+        return self._ensure_rope_scheme()
+
+    # --------------------------------------------------------------- HF API
+    def update(self, key_states: Tensor, value_states: Tensor, layer_idx: int, cache_kwargs: dict | None = None):
+        """Append new K/V to the fp16 tier and return the full cache in position order."""
+        if key_states.dim() != 4:
+            raise ValueError(f"key_states must be [B, H, S, D]; got shape {tuple(key_states.shape)}")
+        if key_states.shape != value_states.shape:
+            raise ValueError(f"K/V shape mismatch: {tuple(key_states.shape)} vs {tuple(value_states.shape)}")
+        batch = int(key_states.shape[0])
+        if self.batch_size is None:
+            self.batch_size = batch
+        elif self.batch_size != batch:
+            raise ValueError(f"batch size mismatch: cache pinned to B={self.batch_size} but got B={batch}")
+        if self.head_dim is None:
+            self.head_dim = int(key_states.shape[-1])
+        self._ensure_layer(layer_idx)
+        self._append_fp16(key_states, value_states, layer_idx)
+        return self._materialize(layer_idx)
+
+    def get_seq_length(self, layer_idx: int = 0) -> int:
+        if layer_idx >= len(self._layers):
+            return 0
+        return self._layers[layer_idx].total_seq_length()
+
+    def get_mask_sizes(self, cache_position, layer_idx: int = 0) -> tuple[int, int]:
+        q = cache_position if isinstance(cache_position, int) else int(cache_position.shape[0])
+        return self.get_seq_length(layer_idx) + q, 0
+
+    def __len__(self) -> int:
+        return len(self._layers)
+
+    # ---------------------------------------------------------------- bytes
+    def storage_bytes(self) -> int:
+        keys = (
+            "fp16_k", "fp16_v", "int4_kq", "int4_vq", "int4_ks", "int4_vs", "int4_k_deq", "int4_v_deq",
+            "int2_kq", "int2_vq", "int2_ks", "int2_vs", "int2_k_deq", "int2_v_deq",
+        )
+        return sum(
+            int(t.element_size() * t.numel()) for s in self._layers for t in (getattr(s, k) for k in keys) if t is not None
+        )
+
+    @staticmethod
+    def _layer_compressed_bytes(state: LayerState) -> int:
+        keys = (
+            "sink_k", "sink_v", "fp16_k", "fp16_v", "int4_kq", "int4_vq", "int4_ks", "int4_vs",
+            "int2_kq", "int2_vq", "int2_ks", "int2_vs",
+        )
+        total = sum(int(t.element_size() * t.numel()) for t in (getattr(state, k) for k in keys) if t is not None)
+        for d in (state.backend_k, state.backend_v):
+            if isinstance(d, dict):
+                total += sum(int(v.element_size() * v.numel()) for v in d.values() if isinstance(v, Tensor))
+        return total
+
+    def compressed_storage_bytes(self) -> int:
+        if self._layers and any(s._compressed_bytes > 0 for s in self._layers):
+            return sum(s._compressed_bytes for s in self._layers)
+        return sum(self._layer_compressed_bytes(s) for s in self._layers)
+
+    # ----------------------------------------------------------- checkpoint
+    _LAYER_TENSOR_KEYS = (
+        "sink_k", "sink_v", "sink_pos", "fp16_k", "fp16_v", "fp16_pos", "int4_kq", "int4_ks", "int4_vq",
+        "int4_vs", "int4_pos", "int2_kq", "int2_ks", "int2_vq", "int2_vs", "int2_pos",
+    )
+    _LAYER_SCALAR_KEYS = ("int2_actual_count", "int2_group_size", "sink_count", "next_position")
+
+    def cache_state_dict(self) -> dict:
+        """Essential compressed form, on the CPU, same keys as fade/cache.py:510-534."""
+        sd: dict = {
+            "n_layers": len(self._layers),
+            "n_sink": self.n_sink,
+            "recent_window": self.recent_window,
+            "int4_budget": self.int4_budget,
+            "int2_budget": self.int2_budget,
+            "batch_size": self.batch_size,
+            "head_dim": self.head_dim,
+            "dtype": str(self.dtype),
+        }
+        for i, st in enumerate(self._layers):
+            for k in self._LAYER_TENSOR_KEYS:
+                v = getattr(st, k)
+                if v is not None:
+                    sd[f"layer.{i}.{k}"] = v.cpu()
+            for k in self._LAYER_SCALAR_KEYS:
+                sd[f"layer.{i}.{k}"] = getattr(st, k)
+        return sd
+
+    def load_cache_state_dict(self, sd: dict, device: torch.device | str | None = None) -> None:
+        """Restore from ``cache_state_dict`` output (fade/cache.py:536-559)."""
+        self._layers = []
+        for i in range(sd["n_layers"]):
+            st = LayerState()
+            for k in self._LAYER_TENSOR_KEYS:
+                v = sd.get(f"layer.{i}.{k}")
+                if v is not None:
+                    setattr(st, k, v.to(device) if device is not None else v)
+            for k in self._LAYER_SCALAR_KEYS:
+                v = sd.get(f"layer.{i}.{k}")
+                if v is not None:
+                    setattr(st, k, v)
+            self._layers.append(st)
+        if sd.get("batch_size") is not None:
+            self.batch_size = sd["batch_size"]
+        if sd.get("head_dim") is not None:
+            self.head_dim = sd["head_dim"]
+
+    def dump_debug(self, path: str | Path) -> None:
+        layers = []
+        for i, st in enumerate(self._layers):
+            d = {
+                "layer_idx": i,
+                "sink_count": st.sink_count,
+                "next_position": st.next_position,
+                "fp16_count": 0 if st.fp16_pos is None else int(st.fp16_pos.shape[0]),
+                "int4_count": 0 if st.int4_pos is None else int(st.int4_pos.shape[0]),
+                "int2_count": 0 if st.int2_pos is None else int(st.int2_pos.shape[0]),
+                "int2_actual_count": st.int2_actual_count,
+                "total_seq_length": st.total_seq_length(),
+            }
+            for name in ("sink", "fp16", "int4", "int2"):
+                pos = getattr(st, f"{name}_pos")
+                if pos is not None:
+                    d[f"{name}_positions"] = pos.tolist()
+            layers.append(d)
+        snap = {
+            "n_layers": len(self._layers), "n_sink": self.n_sink, "recent_window": self.recent_window,
+            "int4_budget": self.int4_budget, "int2_budget": self.int2_budget, "batch_size": self.batch_size,
+            "head_dim": self.head_dim, "layers": layers,
+        }
+        Path(path).write_text(json.dumps(snap, indent=2), encoding="utf-8")
+
+    # ------------------------------------------------------------ internals
+    def _ensure_layer(self, layer_idx: int) -> None:
+        while len(self._layers) <= layer_idx:
+            self._layers.append(LayerState())
+
+    def _append_fp16(self, k: Tensor, v: Tensor, layer_idx: int) -> None:
+        """Append to the doubling fp16 buffer (fade/cache.py:608-670)."""
+        st = self._layers[layer_idx]
+        n = int(k.shape[-2])
+        new_pos = torch.arange(st.next_position, st.next_position + n, device=k.device)
+        st.next_position += n
+        if st._fp16_buf_k is None:
+            have = 0 if st.fp16_k is None else int(st.fp16_k.shape[-2])
+            need = have + n
+            cap = max(DEFAULT_FP16_PREALLOC, need)
+            B, H, _, D = k.shape
+            st._fp16_buf_k = torch.empty(B, H, cap, D, dtype=k.dtype, device=k.device)
+            st._fp16_buf_v = torch.empty(B, H, cap, D, dtype=v.dtype, device=v.device)
+            st._fp16_buf_pos = torch.empty(cap, dtype=torch.long, device=k.device)
+            if have:
+                st._fp16_buf_k[:, :, :have] = st.fp16_k
+                st._fp16_buf_v[:, :, :have] = st.fp16_v
+                st._fp16_buf_pos[:have] = st.fp16_pos
+            st._fp16_buf_k[:, :, have:need] = k
+            st._fp16_buf_v[:, :, have:need] = v
+            st._fp16_buf_pos[have:need] = new_pos
+            st._fp16_len = need
+        else:
+            old, new = st._fp16_len, st._fp16_len + n
+            cap = st._fp16_buf_k.shape[-2]
+            if new > cap:
+                cap2 = max(cap * 2, new)
+                B, H, _, D = st._fp16_buf_k.shape
+                bk = torch.empty(B, H, cap2, D, dtype=k.dtype, device=k.device)
+                bv = torch.empty(B, H, cap2, D, dtype=v.dtype, device=v.device)
+                bp = torch.empty(cap2, dtype=torch.long, device=k.device)
+                bk[:, :, :old] = st._fp16_buf_k[:, :, :old]
+                bv[:, :, :old] = st._fp16_buf_v[:, :, :old]
+                bp[:old] = st._fp16_buf_pos[:old]
+                st._fp16_buf_k, st._fp16_buf_v, st._fp16_buf_pos = bk, bv, bp
+            st._fp16_buf_k[:, :, old:new] = k
+            st._fp16_buf_v[:, :, old:new] = v
+            st._fp16_buf_pos[old:new] = new_pos
+            st._fp16_len = new
+        ln = st._fp16_len
+        st.fp16_k = st._fp16_buf_k[:, :, :ln]
+        st.fp16_v = st._fp16_buf_v[:, :, :ln]
+        st.fp16_pos = st._fp16_buf_pos[:ln]
+        st._dequant_age += 1
+
+    def _materialize(self, layer_idx: int) -> tuple[Tensor, Tensor]:
+        ks, vs = self._assemble_parts(self._layers[layer_idx], want_positions=False)
+        if not ks:
+            raise RuntimeError(f"No cache state for layer {layer_idx}")
+        return torch.cat(ks, dim=-2), torch.cat(vs, dim=-2)
+
+    def _all_in_position_order(self, layer_idx: int) -> tuple[Tensor, Tensor, Tensor]:
+        ks, vs, ps = self._assemble_parts(self._layers[layer_idx], want_positions=True)
+        if not ks:
+            raise RuntimeError(f"No cache state for layer {layer_idx}")
+        return torch.cat(ks, dim=-2), torch.cat(vs, dim=-2), torch.cat(ps, dim=0)
+
+    def _assemble_parts(self, st: LayerState, want_positions: bool):
+        """sink | middle (INT4 + backend + INT2 merged by position) | recent (fade/cache.py:715-808)."""
+        ks, vs, ps = [], [], []
+        nsk = st.sink_count
+        if st.sink_k is not None:
+            ks.append(st.sink_k)
+            vs.append(st.sink_v)
+            ps.append(st.sink_pos)
+        elif st.fp16_k is not None and nsk > 0:
+            ks.append(st.fp16_k[..., :nsk, :])
+            vs.append(st.fp16_v[..., :nsk, :])
+            ps.append(st.fp16_pos[:nsk])
+        mk, mv, mp = [], [], []
+        if st.int4_kq is not None:
+            k4, v4 = self._get_int4_dequant(st)
+            mk.append(k4)
+            mv.append(v4)
+            mp.append(st.int4_pos)
+        if st.backend_k is not None:
+            mk.append(self._quant_backend.decompress_k(st.backend_k, dtype=self.dtype))
+            mv.append(self._quant_backend.decompress_v(st.backend_v, dtype=self.dtype))
+            mp.append(st.backend_pos)
+        if st.int2_kq is not None:
+            k2, v2 = self._get_int2_dequant(st)
+            mk.append(k2)
+            mv.append(v2)
+            mp.append(st.int2_pos)
+        if len(mk) == 1:
+            ks.append(mk[0])
+            vs.append(mv[0])
+            ps.append(mp[0])
+        elif mk:
+            order = torch.cat(mp).argsort()
+            ks.append(torch.cat(mk, dim=-2).index_select(-2, order))
+            vs.append(torch.cat(mv, dim=-2).index_select(-2, order))
+            ps.append(torch.cat(mp)[order])
+        if st.fp16_k is not None:
+            start = 0 if st.sink_k is not None else nsk
+            if start < int(st.fp16_k.shape[-2]):
+                ks.append(st.fp16_k[..., start:, :])
+                vs.append(st.fp16_v[..., start:, :])
+                ps.append(st.fp16_pos[start:])
+        return (ks, vs, ps) if want_positions else (ks, vs)
+
+    def _get_int4_dequant(self, st: LayerState) -> tuple[Tensor, Tensor]:
+        """fade/cache.py:810-842 (cached fp16 copy when ``cache_dequant``)."""
+        if self.max_dequant_age is not None and st._dequant_age > self.max_dequant_age and st.int4_k_deq is not None:
+            st.int4_k_deq = st.int4_v_deq = None
+        if self.cache_dequant and st.int4_k_deq is not None:
+            return st.int4_k_deq, st.int4_v_deq
+        k = dequant_int4(st.int4_kq, st.int4_ks)
+        if self.middle_v_bits == 4:
+            v = dequant_int4(st.int4_vq, st.int4_vs)
+        else:
+            n = int(st.int4_pos.shape[0])
+            v = dequant_int2_trimmed(st.int4_vq, st.int4_vs, n, DEFAULT_INT2_GROUP_SIZE)
+        if self.cache_dequant:
+            st.int4_k_deq, st.int4_v_deq = k, v
+            st._dequant_age = 0
+        return k, v
+
+    def _get_int2_dequant(self, st: LayerState) -> tuple[Tensor, Tensor]:
+        """fade/cache.py:861-876."""
+        if self.cache_dequant and st.int2_k_deq is not None:
+            return st.int2_k_deq, st.int2_v_deq
+        n, g = st.int2_actual_count, st.int2_group_size
+        k = dequant_int2_trimmed(st.int2_kq, st.int2_ks, n, g)
+        v = dequant_int2_trimmed(st.int2_vq, st.int2_vs, n, g)
+        if self.cache_dequant:
+            st.int2_k_deq, st.int2_v_deq = k, v
+        return k, v
+
+    # ------------------------------------------------------- tier movement
+    def _rerope_kept(self, k_full, v_full, pos_full, keep_idx, n_kept):
+        """Un-RoPE kept rows at their old positions and re-RoPE them at 0..n_kept-1."""
+        scheme = self._ensure_rope_scheme()
+        new_pos = torch.arange(n_kept, dtype=torch.long)
+        cos_o, sin_o = scheme.host_cos_sin(pos_full.cpu(), self.dtype)
+        cos_n, sin_n = scheme.host_cos_sin(new_pos, self.dtype)
+        k_kept, v_kept = rerope_gather(k_full, v_full, keep_idx, cos_o, sin_o, cos_n, sin_n)
+        return k_kept, v_kept, new_pos.to(pos_full.device)
+
+    def _store_middle(self, st: LayerState, k_sub: Tensor, v_sub: Tensor, pos: Tensor) -> None:
+        if isinstance(self._quant_backend, SymmetricINT4Backend):
+            st.int4_kq, st.int4_ks = quant_k_int4(k_sub)
+            if self.middle_v_bits == 4:
+                st.int4_vq, st.int4_vs = quant_v_int4(v_sub)
+            else:
+                st.int4_vq, st.int4_vs = quant_int2_padded(v_sub, DEFAULT_INT2_GROUP_SIZE)
+            st.int4_pos = pos
+            st.backend_k = st.backend_v = st.backend_pos = None
+        else:
+            st.backend_k = self._quant_backend.compress_k(k_sub)
+            st.backend_v = self._quant_backend.compress_v(v_sub)
+            st.backend_pos = pos
+            st.int4_kq = st.int4_vq = st.int4_ks = st.int4_vs = st.int4_pos = None
+
+    def _reseed_fp16_buffer(self, st: LayerState) -> None:
+        n = 0 if st.fp16_k is None else int(st.fp16_k.shape[-2])
+        if n > 0 and st._fp16_buf_k is not None and n <= st._fp16_buf_k.shape[-2]:
+            st._fp16_buf_k[:, :, :n] = st.fp16_k
+            st._fp16_buf_v[:, :, :n] = st.fp16_v
+            st._fp16_buf_pos[:n] = st.fp16_pos
+            st._fp16_len = n
+            st.fp16_k = st._fp16_buf_k[:, :, :n]
+            st.fp16_v = st._fp16_buf_v[:, :, :n]
+            st.fp16_pos = st._fp16_buf_pos[:n]
+        else:
+            st._fp16_buf_k = st._fp16_buf_v = st._fp16_buf_pos = None
+            st._fp16_len = 0
+
+    def apply_tier_assignment(self, layer_idx: int, tiers: Tensor, scores: Tensor | None = None) -> None:
+        """Move tokens between tiers (fade/cache.py:881-1057).
+
+        Evicted tokens are dropped; the survivors are re-RoPE'd from their
+        old absolute positions to contiguous positions ``0..n_kept-1`` in
+        one fused pass, then split into fp16 / INT4 / INT2 and requantized.
+        """
+        del scores
+        st = self._layers[layer_idx]
+        k_full, v_full, pos_full = self._all_in_position_order(layer_idx)
+        S = int(pos_full.shape[0])
+        if int(tiers.shape[0]) != S:
+            raise ValueError(f"tiers length {int(tiers.shape[0])} != cache length {S} for layer {layer_idx}")
+        tiers = tiers.to(pos_full.device)
+        keep = tiers != TIER_EVICT
+        n_kept = int(keep.sum().item())
+        if n_kept < S:
+            keep_idx = keep.nonzero(as_tuple=False).squeeze(-1)
+            k_full, v_full, pos_full = self._rerope_kept(k_full, v_full, pos_full, keep_idx, n_kept)
+            tiers = tiers[keep]
+            st.next_position = n_kept
+
+        fp16_idx = (tiers == TIER_FP16).nonzero(as_tuple=False).squeeze(-1)
+        if fp16_idx.numel() > 0:
+            fk, fv, fp = _sel(k_full, fp16_idx), _sel(v_full, fp16_idx), pos_full.index_select(0, fp16_idx)
+            ns = min(self.n_sink, int(fp16_idx.numel()))
+            if ns > 0:
+                st.sink_k, st.sink_v, st.sink_pos = fk[..., :ns, :], fv[..., :ns, :], fp[:ns]
+            else:
+                st.sink_k = st.sink_v = st.sink_pos = None
+            if ns < int(fp16_idx.numel()):
+                st.fp16_k, st.fp16_v, st.fp16_pos = fk[..., ns:, :], fv[..., ns:, :], fp[ns:]
+            else:
+                st.fp16_k = st.fp16_v = st.fp16_pos = None
+        else:
+            st.fp16_k = st.fp16_v = st.fp16_pos = None
+            st.sink_k = st.sink_v = st.sink_pos = None
+        self._reseed_fp16_buffer(st)
+
+        int4_idx = (tiers == TIER_INT4).nonzero(as_tuple=False).squeeze(-1)
+        if int4_idx.numel() > 0:
+            self._store_middle(st, _sel(k_full, int4_idx), _sel(v_full, int4_idx), pos_full.index_select(0, int4_idx))
+        else:
+            st.int4_kq = st.int4_vq = st.int4_ks = st.int4_vs = st.int4_pos = None
+            st.backend_k = st.backend_v = st.backend_pos = None
+
+        int2_idx = (tiers == TIER_INT2).nonzero(as_tuple=False).squeeze(-1)
+        if int2_idx.numel() > 0:
+            g = DEFAULT_INT2_GROUP_SIZE
+            st.int2_kq, st.int2_ks = quant_int2_padded(_sel(k_full, int2_idx), g)
+            st.int2_vq, st.int2_vs = quant_int2_padded(_sel(v_full, int2_idx), g)
+            st.int2_pos = pos_full.index_select(0, int2_idx)
+            st.int2_actual_count = int(int2_idx.numel())
+            st.int2_group_size = g
+        else:
+            st.int2_kq = st.int2_vq = st.int2_ks = st.int2_vs = st.int2_pos = None
+            st.int2_actual_count = 0
+        if bool((tiers == TIER_PQ).any()):
+            raise RuntimeError("TIER_PQ is not supported by fade_amd (no product-quantization tier)")
+
+        st.int4_k_deq = st.int4_v_deq = st.int2_k_deq = st.int2_v_deq = None
+        st._compressed_bytes = self._layer_compressed_bytes(st)
+        st.sink_count = 0 if st.sink_pos is None else int(st.sink_pos.shape[0])
+
+    def apply_tier_assignment_per_sequence(self, layer_idx: int, tiers_per_row: Tensor, scores=None) -> None:
+        """Per-row tiers ``[B, S]`` with zero-padding to the longest row (fade/cache.py:1059-1230)."""
+        del scores
+        st = self._layers[layer_idx]
+        k_full, v_full, pos_full = self._all_in_position_order(layer_idx)
+        B, H, _, D = k_full.shape
+        S = int(pos_full.shape[0])
+        if tiers_per_row.dim() != 2 or tiers_per_row.shape[0] != B:
+            raise ValueError(f"tiers_per_row must be [B={B}, S={S}], got {tuple(tiers_per_row.shape)}")
+        if tiers_per_row.shape[1] != S:
+            raise ValueError(f"tiers_per_row S dim {tiers_per_row.shape[1]} != cache length {S}")
+        dev = k_full.device
+        tiers_per_row = tiers_per_row.to(dev)
+        rows = {"fk": [], "fv": [], "fp": [], "ik": [], "iv": [], "ip": []}
+        min_next = S
+        for b in range(B):
+            rt = tiers_per_row[b]
+            rk, rv, rp = k_full[b : b + 1], v_full[b : b + 1], pos_full
+            keep = rt != TIER_EVICT
+            n_kept = int(keep.sum().item())
+            if n_kept < S:
+                keep_idx = keep.nonzero(as_tuple=False).squeeze(-1)
+                rk, rv, rp = self._rerope_kept(rk, rv, pos_full, keep_idx, n_kept)
+                rt = rt[keep]
+                min_next = min(min_next, n_kept)
+            for tier, kk, vk, pk in ((TIER_FP16, "fk", "fv", "fp"), (TIER_INT4, "ik", "iv", "ip")):
+                idx = (rt == tier).nonzero(as_tuple=False).squeeze(-1)
+                rows[kk].append(rk.index_select(-2, idx))
+                rows[vk].append(rv.index_select(-2, idx))
+                rows[pk].append(rp[idx])
+
+        def pad_stack(lst):
+            n = max(int(r.shape[-2]) for r in lst)
+            if n == 0:
+                return None
+            out = torch.zeros(B, H, n, D, dtype=lst[0].dtype, device=dev)
+            for b, r in enumerate(lst):
+                out[b : b + 1, :, : r.shape[-2]] = r
+            return out
+
+        def first_pos(lst):
+            n = max(int(r.shape[0]) for r in lst)
+            return None if n == 0 else lst[0][:n]
+
+        fk = pad_stack(rows["fk"])
+        if fk is not None:
+            st.fp16_k, st.fp16_v, st.fp16_pos = fk, pad_stack(rows["fv"]), first_pos(rows["fp"])
+        else:
+            st.fp16_k = st.fp16_v = st.fp16_pos = None
+        self._reseed_fp16_buffer(st)
+        ik = pad_stack(rows["ik"])
+        if ik is not None:
+            iv = pad_stack(rows["iv"])
+            st.int4_kq, st.int4_ks = quant_k_int4(ik)
+            if self.middle_v_bits == 4:
+                st.int4_vq, st.int4_vs = quant_v_int4(iv)
+            else:
+                st.int4_vq, st.int4_vs = quant_int2_padded(iv, DEFAULT_INT2_GROUP_SIZE)
+            st.int4_pos = first_pos(rows["ip"])
+        else:
+            st.int4_kq = st.int4_vq = st.int4_ks = st.int4_vs = st.int4_pos = None
+        st.int2_kq = st.int2_vq = st.int2_ks = st.int2_vs = st.int2_pos = None
+        st.int2_actual_count = 0
+        st.int4_k_deq = st.int4_v_deq = st.int2_k_deq = st.int2_v_deq = None
+        st.next_position = min_next
+        st.sink_count = 0 if st.fp16_pos is None else min(self.n_sink, int(st.fp16_pos.shape[0]))
+
+    # ----------------------------------------------------- fused attention
+    def decode_attention(self, q: Tensor, layer_idx: int, sm_scale: float | None = None) -> Tensor:
+        """Single-token attention of ``q`` [B, Hq, 1, D] straight from this layer's tiers.
+
+        Covers the layouts the fused kernel reads in place: sink + recent fp16
+        with an INT4 (reference format), INT4-K/INT2-V, rotated or
+        asymmetric middle tier.  An INT2 tier alongside the middle tier
+        interleaves positions and is not supported here.
+        """
+        from .kernels.tiered_attn import MiddleTier, tiered_decode_attention
+
+        st = self._layers[layer_idx]
+        if st.int2_kq is not None:
+            raise RuntimeError("decode_attention: the INT2 tier is not read by the fused kernel; use update()")
+        if st.sink_k is not None:
+            sink = (st.sink_k, st.sink_v)
+            recent = None if st.fp16_k is None else (st.fp16_k, st.fp16_v)
+        elif st.fp16_k is not None:
+            ns = st.sink_count
+            sink = (st.fp16_k[..., :ns, :], st.fp16_v[..., :ns, :]) if ns > 0 else None
+            recent = (st.fp16_k[..., ns:, :], st.fp16_v[..., ns:, :])
+        else:
+            sink = recent = None
+        mid = None
+        post_rotate = None
+        if st.int4_kq is not None:
+            if self.middle_v_bits == 4:
+                mid = MiddleTier("int4", st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs)
+            else:
+                mid = MiddleTier(
+                    "k4v2", st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs,
+                    group=DEFAULT_INT2_GROUP_SIZE, length=int(st.int4_pos.shape[0]),
+                )
+        elif st.backend_k is not None:
+            be = self._quant_backend
+            bk, bv = st.backend_k, st.backend_v
+            if isinstance(be, RotatedINT4Backend):
+                if be.bits == 3:
+                    raise RuntimeError("decode_attention: 3-bit rotated codes are not read by the fused kernel")
+                R = be._get_R(q.device)
+                mid = MiddleTier(
+                    "sym", bk["packed"], bv["packed"], bk["scale"].to(torch.float16),
+                    bv["scale"].to(torch.float16), k_bits=be.bits, v_bits=be.bits,
+                )
+                q = (q.float() @ R.T).to(torch.float16)
+                post_rotate = R
+            elif isinstance(be, AsymGroupBackend):
+                mid = MiddleTier(
+                    "asym", bk["packed"], bv["packed"], bk["scale"], bv["scale"], bk["zero"], bv["zero"],
+                    k_bits=be.bits, v_bits=be.bits, group=be.group,
+                )
+            else:
+                raise RuntimeError(f"decode_attention: backend {be.name} is not read by the fused kernel")
+        if post_rotate is not None:
+            # Sink/recent are unrotated fp16; attend in the rotated basis for all tiers.
+            sink = None if sink is None else tuple((t.float() @ post_rotate.T).to(torch.float16) for t in sink)
+            recent = None if recent is None else tuple((t.float() @ post_rotate.T).to(torch.float16) for t in recent)
+        out = tiered_decode_attention(q, sink, mid, recent, sm_scale)
+        if post_rotate is not None:
+            out = (out.float() @ post_rotate).to(torch.float16)
+        return out
+
+
+__all__ = [
+    "LayerState",
+    "TIER_EVICT",
+    "TIER_FP16",
+    "TIER_INT2",
+    "TIER_INT4",
+    "TIER_PQ",
+    "TieredKVCache",
+]

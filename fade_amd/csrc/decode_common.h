@@ -1,0 +1,80 @@
+// Shared definitions of the tiered decode attention kernels.
+#pragma once
+
+#include "fade_common.h"
+
+namespace fade {
+namespace decode {
+
+constexpr int kD = 128;   // head_dim of every attention kernel
+constexpr int kMaxG = 8;  // max query heads per kv head
+
+struct Fp16Tier {
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t len;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+};
+
+struct MidTier {
+  int fmt, k_bits, v_bits, group;
+  int64_t len, v_rows;
+  const uint8_t* k_codes;
+  const uint16_t* k_scale;
+  const uint16_t* k_zero;
+  const uint8_t* v_codes;
+  const uint16_t* v_scale;
+  const uint16_t* v_zero;
+};
+
+struct Params {
+  int64_t B, Hq, Hkv;
+  int G;
+  const uint16_t* q;
+  int64_t q_sb, q_sh;
+  float scale_log2;  // sm_scale * log2(e): softmax runs in the exp2 domain
+  Fp16Tier sink, recent;
+  MidTier mid;
+  int64_t total;             // sink.len + mid.len + recent.len
+  int64_t tokens_per_split;  // multiple of the kernel tile
+  int n_splits;
+  float* ws_ml;   // [B][Hq][n_splits][2]  (m, l)
+  float* ws_acc;  // [B][Hq][n_splits][kD] unnormalized output
+};
+
+// Signed symmetric code of channel d in a packed row (fade/quant.py:26-43,
+// fade/rotated_quant.py:35-48 layouts).
+__device__ __forceinline__ int sym_code_at(const uint8_t* row, int d, int bits) {
+  if (bits == 4) {
+    const int byte = row[d >> 1];
+    const int n = (d & 1) ? (byte & 0xF) : (byte >> 4);
+    return n - ((n & 8) << 1);
+  }
+  const int byte = row[d >> 2];
+  const int n = (byte >> (6 - 2 * (d & 3))) & 3;
+  return n - ((n & 2) << 1);
+}
+
+// Unsigned code of channel d in an asymmetric packed row.
+__device__ __forceinline__ int asym_code_at(const uint8_t* row, int d, int bits) {
+  if (bits == 4) {
+    const int byte = row[d >> 1];
+    return (d & 1) ? (byte & 0xF) : (byte >> 4);
+  }
+  const int byte = row[d >> 2];
+  return (byte >> (6 - 2 * (d & 3))) & 3;
+}
+
+__global__ void decode_combine_kernel(const float* __restrict__ ws_ml,
+                                      const float* __restrict__ ws_acc, int n_splits, int64_t Hq,
+                                      uint16_t* __restrict__ out, int64_t o_sb, int64_t o_sh);
+
+int launch_valu(const Params& p, hipStream_t st);
+// Matrix-core kernel; returns FADE_EINVAL when the middle format is not handled.
+int launch_mfma(const Params& p, hipStream_t st);
+bool mfma_supports(const Params& p);
+int mfma_tile();
+
+}  // namespace decode
+}  // namespace fade

@@ -1,0 +1,754 @@
+// Quantize + bit-pack kernels for the FADE middle tier (gfx950).
+//
+// Every lane owns 8 consecutive elements of a row (one 16-byte fp16 load),
+// so a D=128 row is 16 lanes and a wavefront covers 4 rows per iteration;
+// per-row reductions are lane shuffles inside the 16-lane group and the
+// packed codes leave as one 4-byte (INT4) or 2-byte (INT2) store per lane.
+//
+// Arithmetic follows the reference's torch semantics bit for bit
+// (fade/quant.py:61-150, fade/rotated_quant.py:106-173):
+//   fp16 inputs: each op is evaluated in fp32 and rounded to fp16, and
+//     qmax / absmax is reciprocal-then-multiply (two roundings);
+//   fp32 (rotated) inputs: each op one fp32 rounding.
+// This file is compiled with -ffp-contract=off and IEEE fp32 division.
+#include "fade_common.h"
+
+namespace fade {
+namespace {
+
+constexpr int kBlock = 256;
+enum { MODE_F16 = 0, MODE_F32 = 1 };
+
+template <int BITS>
+struct QRange;
+// Bytes one lane (8 codes) occupies in a packed row; 3-bit codes stay raw int8.
+template <int BITS>
+constexpr int lane_bytes() { return BITS == 3 ? 8 : BITS; }
+template <>
+struct QRange<4> {
+  static constexpr int lo = -8, hi = 7;
+};
+template <>
+struct QRange<3> {
+  static constexpr int lo = -4, hi = 3;
+};
+template <>
+struct QRange<2> {
+  static constexpr int lo = -2, hi = 1;
+};
+
+__device__ __forceinline__ void load8(const uint16_t* p, float* v) {
+  const uint4 w = *reinterpret_cast<const uint4*>(p);
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = h2f(static_cast<uint16_t>(u[i] & 0xFFFFu));
+    v[2 * i + 1] = h2f(static_cast<uint16_t>(u[i] >> 16));
+  }
+}
+__device__ __forceinline__ void load8(const float* p, float* v) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// inv = qmax / absmax, scale = absmax / qmax in the reference's rounding.
+template <int MODE, int QMAX>
+__device__ __forceinline__ void sym_params(float absmax, float& inv, uint16_t& scale_h) {
+  if (MODE == MODE_F16) {
+    // clamp(min=1e-8) is a no-op on fp16 (1e-8 rounds to zero).
+    const float r = round_f16(1.0f / absmax);
+    inv = round_f16(r * static_cast<float>(QMAX));
+    scale_h = f2h(absmax / static_cast<float>(QMAX));
+  } else {
+    const float a = fmaxf(absmax, 1e-8f);
+    const float r = 1.0f / a;
+    inv = r * static_cast<float>(QMAX);
+    scale_h = f2h(a / static_cast<float>(QMAX));
+  }
+}
+
+// round-half-even(x * inv), NaN -> 0 (torch CPU int8 cast), clamped.
+template <int MODE, int QLO, int QHI>
+__device__ __forceinline__ int sym_code(float x, float inv) {
+  float p = x * inv;
+  if (MODE == MODE_F16) p = round_f16(p);
+  float q = rintf(p);
+  if (q != q) return 0;
+  q = fminf(fmaxf(q, static_cast<float>(QLO)), static_cast<float>(QHI));
+  return static_cast<int>(q);
+}
+
+// Store 8 codes of one lane in the packed layout for BITS.
+template <int BITS>
+__device__ __forceinline__ void store_codes(uint8_t* dst, const int* c) {
+  if (BITS == 4) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w |= static_cast<uint32_t>(((c[2 * j] & 0xF) << 4) | (c[2 * j + 1] & 0xF)) << (8 * j);
+    *reinterpret_cast<uint32_t*>(dst) = w;
+  } else if (BITS == 2) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      w |= static_cast<uint32_t>(((c[4 * j] & 3) << 6) | ((c[4 * j + 1] & 3) << 4) |
+                                 ((c[4 * j + 2] & 3) << 2) | (c[4 * j + 3] & 3))
+           << (8 * j);
+    *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(w);
+  } else {  // raw int8 (3-bit rotated codes are not packed by the reference)
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lo |= static_cast<uint32_t>(c[j] & 0xFF) << (8 * j);
+      hi |= static_cast<uint32_t>(c[4 + j] & 0xFF) << (8 * j);
+    }
+    *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+  }
+}
+
+// Unpack 8 signed codes of one lane.
+template <int BITS>
+__device__ __forceinline__ void load_codes(const uint8_t* src, int* c) {
+  if (BITS == 4) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(src);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int b = (w >> (8 * j)) & 0xFF;
+      const int hi = b >> 4, lo = b & 0xF;
+      c[2 * j] = hi - ((hi & 8) << 1);
+      c[2 * j + 1] = lo - ((lo & 8) << 1);
+    }
+  } else if (BITS == 2) {
+    const uint32_t w = *reinterpret_cast<const uint16_t*>(src);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int b = (w >> (8 * j)) & 0xFF;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int v = (b >> (6 - 2 * k)) & 3;
+        c[4 * j + k] = v - ((v & 2) << 1);
+      }
+    }
+  } else {
+    const uint2 w = *reinterpret_cast<const uint2*>(src);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c[j] = static_cast<int8_t>((w.x >> (8 * j)) & 0xFF);
+      c[4 + j] = static_cast<int8_t>((w.y >> (8 * j)) & 0xFF);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- per token
+template <typename InT, int MODE, int BITS, int LPR>
+__global__ __launch_bounds__(kBlock) void quant_token_kernel(const InT* __restrict__ x, int64_t rows,
+                                                             int64_t H, int64_t S, int64_t sb,
+                                                             int64_t sh, int64_t ss,
+                                                             uint8_t* __restrict__ packed,
+                                                             uint16_t* __restrict__ scale) {
+  constexpr int RP = kBlock / LPR;
+  constexpr int D = LPR * 8;
+  constexpr int ROW_BYTES = LPR * lane_bytes<BITS>();
+  const int c = threadIdx.x % LPR;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; r < rows;
+       r += static_cast<int64_t>(gridDim.x) * RP) {
+    float v[8];
+    load8(x + row_offset(r, H, S, sb, sh, ss) + c * 8, v);
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(v[j]));
+    a = group_max<LPR>(a);
+    float inv;
+    uint16_t sc;
+    sym_params<MODE, QRange<BITS>::hi>(a, inv, sc);
+    int code[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) code[j] = sym_code<MODE, QRange<BITS>::lo, QRange<BITS>::hi>(v[j], inv);
+    store_codes<BITS>(packed + r * ROW_BYTES + c * lane_bytes<BITS>(), code);
+    if (c == 0) scale[r] = sc;
+  }
+}
+
+// -------------------------------------------------------------- per channel
+// Pass 1: column absmax of each S-block -> partial[bh][block][d] (fp32).
+template <typename InT, int LPR>
+__global__ __launch_bounds__(kBlock) void colmax_kernel(const InT* __restrict__ x, int64_t H,
+                                                        int64_t S, int64_t sb, int64_t sh,
+                                                        int64_t ss, int64_t rows_per_block,
+                                                        float* __restrict__ partial) {
+  constexpr int RP = kBlock / LPR;
+  constexpr int D = LPR * 8;
+  const int64_t bh = blockIdx.y;
+  const int c = threadIdx.x % LPR, rs = threadIdx.x / LPR;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
+  const int64_t s1 = s0 + rows_per_block < S ? s0 + rows_per_block : S;
+  const InT* base = x + (bh / H) * sb + (bh % H) * sh + c * 8;
+  float m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t s = s0 + rs; s < s1; s += RP) {
+    float v[8];
+    load8(base + s * ss, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m[j] = fmaxf(m[j], fabsf(v[j]));
+  }
+  __shared__ float red[RP * D];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) red[rs * D + c * 8 + j] = m[j];
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += kBlock) {
+    float mm = 0.0f;
+    for (int r = 0; r < RP; ++r) mm = fmaxf(mm, red[r * D + d]);
+    partial[(bh * gridDim.x + blockIdx.x) * D + d] = mm;
+  }
+}
+
+// Pass 2: finish the column absmax, emit the scale, quantize this S-block.
+template <typename InT, int MODE, int BITS, int LPR>
+__global__ __launch_bounds__(kBlock) void quant_channel_kernel(
+    const InT* __restrict__ x, int64_t H, int64_t S, int64_t sb, int64_t sh, int64_t ss,
+    int64_t rows_per_block, const float* __restrict__ partial, uint8_t* __restrict__ packed,
+    uint16_t* __restrict__ scale) {
+  constexpr int RP = kBlock / LPR;
+  constexpr int D = LPR * 8;
+  constexpr int ROW_BYTES = LPR * lane_bytes<BITS>();
+  const int64_t bh = blockIdx.y;
+  const int nsb = gridDim.x;
+  __shared__ float inv_s[D];
+  for (int d = threadIdx.x; d < D; d += kBlock) {
+    float a = 0.0f;
+    for (int k = 0; k < nsb; ++k) a = fmaxf(a, partial[(bh * nsb + k) * D + d]);
+    float inv;
+    uint16_t sc;
+    sym_params<MODE, QRange<BITS>::hi>(a, inv, sc);
+    inv_s[d] = inv;
+    if (blockIdx.x == 0) scale[bh * D + d] = sc;
+  }
+  __syncthreads();
+  const int c = threadIdx.x % LPR, rs = threadIdx.x / LPR;
+  float iv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) iv[j] = inv_s[c * 8 + j];
+  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
+  const int64_t s1 = s0 + rows_per_block < S ? s0 + rows_per_block : S;
+  const InT* base = x + (bh / H) * sb + (bh % H) * sh + c * 8;
+  for (int64_t s = s0 + rs; s < s1; s += RP) {
+    float v[8];
+    load8(base + s * ss, v);
+    int code[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) code[j] = sym_code<MODE, QRange<BITS>::lo, QRange<BITS>::hi>(v[j], iv[j]);
+    store_codes<BITS>(packed + (bh * S + s) * ROW_BYTES + c * lane_bytes<BITS>(), code);
+  }
+}
+
+// ---------------------------------------------------------- dequant (sym)
+template <int BITS, int LPR>
+__global__ __launch_bounds__(kBlock) void dequant_sym_kernel(const uint8_t* __restrict__ packed,
+                                                             const uint16_t* __restrict__ scale,
+                                                             int axis, int64_t rows, int64_t S,
+                                                             uint16_t* __restrict__ out) {
+  constexpr int RP = kBlock / LPR;
+  constexpr int D = LPR * 8;
+  constexpr int ROW_BYTES = LPR * lane_bytes<BITS>();
+  const int c = threadIdx.x % LPR;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; r < rows;
+       r += static_cast<int64_t>(gridDim.x) * RP) {
+    int code[8];
+    load_codes<BITS>(packed + r * ROW_BYTES + c * lane_bytes<BITS>(), code);
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float s0, s1;
+      if (axis == FADE_AXIS_TOKEN) {
+        s0 = s1 = h2f(scale[r]);
+      } else {
+        const int64_t bh = r / S;
+        s0 = h2f(scale[bh * D + c * 8 + 2 * j]);
+        s1 = h2f(scale[bh * D + c * 8 + 2 * j + 1]);
+      }
+      w[j] = static_cast<uint32_t>(f2h(static_cast<float>(code[2 * j]) * s0)) |
+             (static_cast<uint32_t>(f2h(static_cast<float>(code[2 * j + 1]) * s1)) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + r * D + c * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// ------------------------------------------------ grouped INT2 (reference)
+// One block per (group, b*h); one thread per channel.  Rows >= S are zero.
+__global__ void quant_int2_grouped_kernel(const uint16_t* __restrict__ x, int64_t H, int64_t S,
+                                          int64_t S_pad, int64_t sb, int64_t sh, int64_t ss,
+                                          int group, int8_t* __restrict__ codes,
+                                          uint16_t* __restrict__ scale) {
+  const int d = threadIdx.x;
+  const int D = blockDim.x;
+  const int64_t g = blockIdx.x, bh = blockIdx.y;
+  const int64_t G = gridDim.x;
+  const uint16_t* base = x + (bh / H) * sb + (bh % H) * sh + d;
+  float a = 0.0f;
+  for (int i = 0; i < group; ++i) {
+    const int64_t s = g * group + i;
+    const float v = s < S ? h2f(base[s * ss]) : 0.0f;
+    a = fmaxf(a, fabsf(v));
+  }
+  float inv;
+  uint16_t sc;
+  sym_params<MODE_F16, 1>(a, inv, sc);
+  scale[(bh * G + g) * D + d] = sc;
+  for (int i = 0; i < group; ++i) {
+    const int64_t s = g * group + i;
+    const float v = s < S ? h2f(base[s * ss]) : 0.0f;
+    codes[(bh * S_pad + s) * D + d] = static_cast<int8_t>(sym_code<MODE_F16, -2, 1>(v, inv));
+  }
+}
+
+__global__ void dequant_int2_grouped_kernel(const int8_t* __restrict__ codes,
+                                            const uint16_t* __restrict__ scale, int64_t BH,
+                                            int64_t S_pad, int64_t D, int64_t group, int64_t S_out,
+                                            uint16_t* __restrict__ out) {
+  const int64_t n = BH * S_out * D;
+  const int64_t G = S_pad / group;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t d = i % D;
+    const int64_t s = (i / D) % S_out;
+    const int64_t bh = i / (D * S_out);
+    const float q = static_cast<float>(codes[(bh * S_pad + s) * D + d]);
+    out[i] = f2h(q * h2f(scale[(bh * G + s / group) * D + d]));
+  }
+}
+
+// ------------------------------------------------------ asymmetric groups
+template <int BITS, int LPG, int LPR>
+__global__ __launch_bounds__(kBlock) void quant_asym_kernel(const uint16_t* __restrict__ x,
+                                                            int64_t rows, int64_t H, int64_t S,
+                                                            int64_t sb, int64_t sh, int64_t ss,
+                                                            uint8_t* __restrict__ packed,
+                                                            uint16_t* __restrict__ scale,
+                                                            uint16_t* __restrict__ zero) {
+  constexpr int RP = kBlock / LPR;
+  constexpr int D = LPR * 8;
+  constexpr int NG = LPR / LPG;  // groups per row
+  constexpr int ROW_BYTES = D * BITS / 8;
+  constexpr float QMAXU = static_cast<float>((1 << BITS) - 1);
+  const int c = threadIdx.x % LPR;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; r < rows;
+       r += static_cast<int64_t>(gridDim.x) * RP) {
+    float v[8];
+    load8(x + row_offset(r, H, S, sb, sh, ss) + c * 8, v);
+    float mn = v[0], mx = v[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) {
+      mn = fminf(mn, v[j]);
+      mx = fmaxf(mx, v[j]);
+    }
+    mn = group_min<LPG>(mn);
+    mx = group_max<LPG>(mx);
+    const uint16_t sc = f2h((mx - mn) / QMAXU);
+    const float s = h2f(sc);
+    int code[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (s == 0.0f) {
+        code[j] = 0;
+      } else {
+        const float t = rintf((v[j] - mn) / s);
+        code[j] = static_cast<int>(fminf(fmaxf(t, 0.0f), QMAXU));
+      }
+    }
+    uint8_t* dst = packed + r * ROW_BYTES + c * BITS;
+    if (BITS == 4) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w |= static_cast<uint32_t>((code[2 * j] << 4) | code[2 * j + 1]) << (8 * j);
+      *reinterpret_cast<uint32_t*>(dst) = w;
+    } else {
+      uint32_t w = 0;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        w |= static_cast<uint32_t>((code[4 * j] << 6) | (code[4 * j + 1] << 4) |
+                                   (code[4 * j + 2] << 2) | code[4 * j + 3])
+             << (8 * j);
+      *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(w);
+    }
+    if (c % LPG == 0) {
+      scale[r * NG + c / LPG] = sc;
+      zero[r * NG + c / LPG] = f2h(mn);
+    }
+  }
+}
+
+template <int BITS, int LPG, int LPR>
+__global__ __launch_bounds__(kBlock) void dequant_asym_kernel(const uint8_t* __restrict__ packed,
+                                                              const uint16_t* __restrict__ scale,
+                                                              const uint16_t* __restrict__ zero,
+                                                              int64_t rows,
+                                                              uint16_t* __restrict__ out) {
+  constexpr int RP = kBlock / LPR;
+  constexpr int D = LPR * 8;
+  constexpr int NG = LPR / LPG;
+  constexpr int ROW_BYTES = D * BITS / 8;
+  const int c = threadIdx.x % LPR;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; r < rows;
+       r += static_cast<int64_t>(gridDim.x) * RP) {
+    const float s = h2f(scale[r * NG + c / LPG]);
+    const float z = h2f(zero[r * NG + c / LPG]);
+    const uint8_t* src = packed + r * ROW_BYTES + c * BITS;
+    int code[8];
+    if (BITS == 4) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(src);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        code[2 * j] = (w >> (8 * j + 4)) & 0xF;
+        code[2 * j + 1] = (w >> (8 * j)) & 0xF;
+      }
+    } else {
+      const uint32_t w = *reinterpret_cast<const uint16_t*>(src);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) code[4 * j + k] = (w >> (8 * j + 6 - 2 * k)) & 3;
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = static_cast<float>(code[2 * j]) * s + z;
+      const float b = static_cast<float>(code[2 * j + 1]) * s + z;
+      w[j] = static_cast<uint32_t>(f2h(a)) | (static_cast<uint32_t>(f2h(b)) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + r * D + c * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// ------------------------------------------------------- pack / unpack
+template <int BITS>
+__global__ void pack_kernel(const int8_t* __restrict__ q, int64_t n8, uint8_t* __restrict__ out) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n8;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const uint2 w = *reinterpret_cast<const uint2*>(q + i * 8);
+    int c[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c[j] = static_cast<int8_t>((w.x >> (8 * j)) & 0xFF);
+      c[4 + j] = static_cast<int8_t>((w.y >> (8 * j)) & 0xFF);
+    }
+    store_codes<BITS>(out + i * BITS, c);
+  }
+}
+
+template <int BITS>
+__global__ void unpack_kernel(const uint8_t* __restrict__ packed, int64_t n8, int8_t* __restrict__ q) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n8;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int c[8];
+    load_codes<BITS>(packed + i * BITS, c);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lo |= static_cast<uint32_t>(c[j] & 0xFF) << (8 * j);
+      hi |= static_cast<uint32_t>(c[4 + j] & 0xFF) << (8 * j);
+    }
+    *reinterpret_cast<uint2*>(q + i * 8) = make_uint2(lo, hi);
+  }
+}
+
+// ---------------------------------------------------------------- host side
+int check_dims(const char* fn, int64_t B, int64_t H, int64_t S, int64_t D) {
+  if (B < 0 || H < 0 || S < 0) return einval("%s: negative size (B=%lld H=%lld S=%lld)", fn, (long long)B, (long long)H, (long long)S);
+  if (D != 64 && D != 128 && D != 256)
+    return einval("%s: head_dim must be 64, 128 or 256, got %lld", fn, (long long)D);
+  return FADE_OK;
+}
+
+int grid_for_rows(int64_t rows, int lpr) {
+  const int64_t rp = kBlock / lpr;
+  const int64_t g = cdiv(rows, rp);
+  return static_cast<int>(g < 16384 ? (g > 0 ? g : 1) : 16384);
+}
+
+// S-blocking of the two-pass per-channel quantizer (shared with the workspace query).
+void channel_blocking(int64_t BH, int64_t S, int64_t* nsb, int64_t* rows_per_block) {
+  int64_t target = BH > 0 ? 2048 / BH : 1;
+  if (target < 1) target = 1;
+  int64_t n = cdiv(S, 64);
+  if (n > target) n = target;
+  if (n < 1) n = 1;
+  int64_t rpb = cdiv(S, n);
+  if (rpb < 1) rpb = 1;
+  *rows_per_block = rpb;
+  *nsb = cdiv(S, rpb) > 0 ? cdiv(S, rpb) : 1;
+}
+
+#define FADE_DISPATCH_LPR(D, ...)           \
+  switch (D) {                              \
+    case 64: { constexpr int LPR = 8; __VA_ARGS__; } break;   \
+    case 128: { constexpr int LPR = 16; __VA_ARGS__; } break; \
+    default: { constexpr int LPR = 32; __VA_ARGS__; } break;  \
+  }
+
+template <typename InT, int MODE, int BITS>
+int launch_channel(const char* fn, const InT* x, int64_t B, int64_t H, int64_t S, int64_t D,
+                   int64_t sb, int64_t sh, int64_t ss, void* packed, void* scale, void* ws,
+                   int64_t ws_bytes, hipStream_t st) {
+  const int64_t BH = B * H;
+  if (BH == 0) return FADE_OK;
+  if (S == 0) return einval("%s: S must be > 0 for a per-channel scale", fn);
+  int64_t nsb, rpb;
+  channel_blocking(BH, S, &nsb, &rpb);
+  const int64_t need = BH * nsb * D * static_cast<int64_t>(sizeof(float));
+  if (ws == nullptr || ws_bytes < need)
+    return einval("%s: workspace too small (%lld < %lld bytes)", fn, (long long)ws_bytes, (long long)need);
+  if (BH > 65535) return einval("%s: B*H=%lld exceeds 65535", fn, (long long)BH);
+  dim3 grid(static_cast<unsigned>(nsb), static_cast<unsigned>(BH));
+  FADE_DISPATCH_LPR(D, {
+    hipLaunchKernelGGL((colmax_kernel<InT, LPR>), grid, dim3(kBlock), 0, st, x, H, S, sb, sh, ss,
+                       rpb, static_cast<float*>(ws));
+    hipLaunchKernelGGL((quant_channel_kernel<InT, MODE, BITS, LPR>), grid, dim3(kBlock), 0, st, x,
+                       H, S, sb, sh, ss, rpb, static_cast<const float*>(ws),
+                       static_cast<uint8_t*>(packed), static_cast<uint16_t*>(scale));
+  });
+  return check_launch(fn);
+}
+
+template <typename InT, int MODE, int BITS>
+int launch_token(const char* fn, const InT* x, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                 int64_t sh, int64_t ss, void* packed, void* scale, hipStream_t st) {
+  const int64_t rows = B * H * S;
+  if (rows == 0) return FADE_OK;
+  FADE_DISPATCH_LPR(D, {
+    hipLaunchKernelGGL((quant_token_kernel<InT, MODE, BITS, LPR>), dim3(grid_for_rows(rows, LPR)),
+                       dim3(kBlock), 0, st, x, rows, H, S, sb, sh, ss,
+                       static_cast<uint8_t*>(packed), static_cast<uint16_t*>(scale));
+  });
+  return check_launch(fn);
+}
+
+bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+}  // namespace
+}  // namespace fade
+
+using namespace fade;
+
+FADE_API int fade_pack_codes(const void* q_i8, int64_t n_rows, int64_t D, int32_t bits,
+                             void* packed_u8, void* stream) {
+  if (bits != 4 && bits != 2) return einval("fade_pack_codes: bits must be 4 or 2, got %d", bits);
+  if (D % 8 != 0) return einval("fade_pack_codes: last dim must be a multiple of 8, got %lld", (long long)D);
+  const int64_t n8 = n_rows * D / 8;
+  if (n8 == 0) return FADE_OK;
+  const int grid = static_cast<int>(cdiv(n8, 256) < 16384 ? cdiv(n8, 256) : 16384);
+  if (bits == 4)
+    hipLaunchKernelGGL(pack_kernel<4>, dim3(grid), dim3(256), 0, as_stream(stream),
+                       static_cast<const int8_t*>(q_i8), n8, static_cast<uint8_t*>(packed_u8));
+  else
+    hipLaunchKernelGGL(pack_kernel<2>, dim3(grid), dim3(256), 0, as_stream(stream),
+                       static_cast<const int8_t*>(q_i8), n8, static_cast<uint8_t*>(packed_u8));
+  return check_launch("fade_pack_codes");
+}
+
+FADE_API int fade_unpack_codes(const void* packed_u8, int64_t n_rows, int64_t D, int32_t bits,
+                               void* q_i8, void* stream) {
+  if (bits != 4 && bits != 2) return einval("fade_unpack_codes: bits must be 4 or 2, got %d", bits);
+  if (D % 8 != 0) return einval("fade_unpack_codes: last dim must be a multiple of 8, got %lld", (long long)D);
+  const int64_t n8 = n_rows * D / 8;
+  if (n8 == 0) return FADE_OK;
+  const int grid = static_cast<int>(cdiv(n8, 256) < 16384 ? cdiv(n8, 256) : 16384);
+  if (bits == 4)
+    hipLaunchKernelGGL(unpack_kernel<4>, dim3(grid), dim3(256), 0, as_stream(stream),
+                       static_cast<const uint8_t*>(packed_u8), n8, static_cast<int8_t*>(q_i8));
+  else
+    hipLaunchKernelGGL(unpack_kernel<2>, dim3(grid), dim3(256), 0, as_stream(stream),
+                       static_cast<const uint8_t*>(packed_u8), n8, static_cast<int8_t*>(q_i8));
+  return check_launch("fade_unpack_codes");
+}
+
+FADE_API int fade_quant_k_int4_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D,
+                                               int64_t* bytes) {
+  if (bytes == nullptr) return einval("fade_quant_k_int4_workspace_bytes: null output");
+  int64_t nsb, rpb;
+  channel_blocking(B * H, S, &nsb, &rpb);
+  *bytes = B * H * nsb * D * static_cast<int64_t>(sizeof(float));
+  return FADE_OK;
+}
+
+FADE_API int fade_quant_k_int4(const void* k_f16, int64_t B, int64_t H, int64_t S, int64_t D,
+                               int64_t sb, int64_t sh, int64_t ss, void* packed_u8, void* scale_f16,
+                               void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = check_dims("fade_quant_k_int4", B, H, S, D);
+  if (rc) return rc;
+  if (!aligned(k_f16, 16) || (sb | sh | ss) % 8 != 0)
+    return einval("fade_quant_k_int4: input must be 16-byte aligned with strides a multiple of 8");
+  return launch_channel<uint16_t, MODE_F16, 4>("fade_quant_k_int4", static_cast<const uint16_t*>(k_f16),
+                                               B, H, S, D, sb, sh, ss, packed_u8, scale_f16,
+                                               workspace, workspace_bytes, as_stream(stream));
+}
+
+FADE_API int fade_quant_v_int4(const void* v_f16, int64_t B, int64_t H, int64_t S, int64_t D,
+                               int64_t sb, int64_t sh, int64_t ss, void* packed_u8, void* scale_f16,
+                               void* stream) {
+  int rc = check_dims("fade_quant_v_int4", B, H, S, D);
+  if (rc) return rc;
+  if (!aligned(v_f16, 16) || (sb | sh | ss) % 8 != 0)
+    return einval("fade_quant_v_int4: input must be 16-byte aligned with strides a multiple of 8");
+  return launch_token<uint16_t, MODE_F16, 4>("fade_quant_v_int4", static_cast<const uint16_t*>(v_f16),
+                                             B, H, S, D, sb, sh, ss, packed_u8, scale_f16,
+                                             as_stream(stream));
+}
+
+FADE_API int fade_dequant_sym(const void* packed_u8, const void* scale_f16, int32_t bits,
+                              int32_t axis, int64_t B, int64_t H, int64_t S, int64_t D,
+                              void* out_f16, void* stream) {
+  int rc = check_dims("fade_dequant_sym", B, H, S, D);
+  if (rc) return rc;
+  if (bits != 4 && bits != 3 && bits != 2)
+    return einval("fade_dequant_sym: bits must be 4, 3 or 2, got %d", bits);
+  if (axis != FADE_AXIS_CHANNEL && axis != FADE_AXIS_TOKEN)
+    return einval("fade_dequant_sym: bad axis %d", axis);
+  const int64_t rows = B * H * S;
+  if (rows == 0) return FADE_OK;
+  FADE_DISPATCH_LPR(D, {
+    if (bits == 4)
+      hipLaunchKernelGGL((dequant_sym_kernel<4, LPR>), dim3(grid_for_rows(rows, LPR)), dim3(kBlock), 0,
+                         as_stream(stream), static_cast<const uint8_t*>(packed_u8),
+                         static_cast<const uint16_t*>(scale_f16), axis, rows, S,
+                         static_cast<uint16_t*>(out_f16));
+    else if (bits == 3)
+      hipLaunchKernelGGL((dequant_sym_kernel<3, LPR>), dim3(grid_for_rows(rows, LPR)), dim3(kBlock), 0,
+                         as_stream(stream), static_cast<const uint8_t*>(packed_u8),
+                         static_cast<const uint16_t*>(scale_f16), axis, rows, S,
+                         static_cast<uint16_t*>(out_f16));
+    else
+      hipLaunchKernelGGL((dequant_sym_kernel<2, LPR>), dim3(grid_for_rows(rows, LPR)), dim3(kBlock), 0,
+                         as_stream(stream), static_cast<const uint8_t*>(packed_u8),
+                         static_cast<const uint16_t*>(scale_f16), axis, rows, S,
+                         static_cast<uint16_t*>(out_f16));
+  });
+  return check_launch("fade_dequant_sym");
+}
+
+FADE_API int fade_quant_int2_grouped(const void* x_f16, int64_t B, int64_t H, int64_t S,
+                                     int64_t S_pad, int64_t D, int64_t sb, int64_t sh, int64_t ss,
+                                     int64_t group, void* codes_i8, void* scale_f16, void* stream) {
+  int rc = check_dims("fade_quant_int2_grouped", B, H, S, D);
+  if (rc) return rc;
+  if (group < 1 || S_pad % group != 0 || S_pad < S)
+    return einval("S=%lld must be divisible by group_size=%lld", (long long)S_pad, (long long)group);
+  const int64_t BH = B * H, G = S_pad / group;
+  if (BH == 0 || G == 0) return FADE_OK;
+  if (BH > 65535) return einval("fade_quant_int2_grouped: B*H=%lld exceeds 65535", (long long)BH);
+  hipLaunchKernelGGL(quant_int2_grouped_kernel, dim3(static_cast<unsigned>(G), static_cast<unsigned>(BH)),
+                     dim3(static_cast<unsigned>(D)), 0, as_stream(stream),
+                     static_cast<const uint16_t*>(x_f16), H, S, S_pad, sb, sh, ss,
+                     static_cast<int>(group), static_cast<int8_t*>(codes_i8),
+                     static_cast<uint16_t*>(scale_f16));
+  return check_launch("fade_quant_int2_grouped");
+}
+
+FADE_API int fade_dequant_int2_grouped(const void* codes_i8, const void* scale_f16, int64_t B,
+                                       int64_t H, int64_t S_pad, int64_t D, int64_t group,
+                                       int64_t S_out, void* out_f16, void* stream) {
+  if (group < 1 || S_pad % group != 0 || S_out > S_pad || S_out < 0)
+    return einval("fade_dequant_int2_grouped: bad sizes (S_pad=%lld group=%lld S_out=%lld)",
+                  (long long)S_pad, (long long)group, (long long)S_out);
+  const int64_t n = B * H * S_out * D;
+  if (n == 0) return FADE_OK;
+  const int grid = static_cast<int>(cdiv(n, 256) < 16384 ? cdiv(n, 256) : 16384);
+  hipLaunchKernelGGL(dequant_int2_grouped_kernel, dim3(grid), dim3(256), 0, as_stream(stream),
+                     static_cast<const int8_t*>(codes_i8), static_cast<const uint16_t*>(scale_f16),
+                     B * H, S_pad, D, group, S_out, static_cast<uint16_t*>(out_f16));
+  return check_launch("fade_dequant_int2_grouped");
+}
+
+FADE_API int fade_quant_rotated_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D,
+                                                int32_t axis, int64_t* bytes) {
+  if (bytes == nullptr) return einval("fade_quant_rotated_workspace_bytes: null output");
+  if (axis == FADE_AXIS_TOKEN) {
+    *bytes = 0;
+    return FADE_OK;
+  }
+  return fade_quant_k_int4_workspace_bytes(B, H, S, D, bytes);
+}
+
+FADE_API int fade_quant_rotated(const float* x_rot, int64_t B, int64_t H, int64_t S, int64_t D,
+                                int32_t bits, int32_t axis, void* packed, void* scale_f16,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = check_dims("fade_quant_rotated", B, H, S, D);
+  if (rc) return rc;
+  if (!aligned(x_rot, 16)) return einval("fade_quant_rotated: input must be 16-byte aligned");
+  const int64_t sb = H * S * D, sh = S * D, ss = D;
+  hipStream_t st = as_stream(stream);
+  const char* fn = "fade_quant_rotated";
+  if (axis == FADE_AXIS_TOKEN) {
+    switch (bits) {
+      case 4: return launch_token<float, MODE_F32, 4>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale_f16, st);
+      case 3: return launch_token<float, MODE_F32, 3>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale_f16, st);
+      case 2: return launch_token<float, MODE_F32, 2>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale_f16, st);
+      default: return einval("fade_quant_rotated: bits must be 2, 3 or 4, got %d", bits);
+    }
+  }
+  if (axis != FADE_AXIS_CHANNEL) return einval("fade_quant_rotated: bad axis %d", axis);
+  switch (bits) {
+    case 4: return launch_channel<float, MODE_F32, 4>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale_f16, workspace, workspace_bytes, st);
+    case 3: return launch_channel<float, MODE_F32, 3>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale_f16, workspace, workspace_bytes, st);
+    case 2: return launch_channel<float, MODE_F32, 2>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale_f16, workspace, workspace_bytes, st);
+    default: return einval("fade_quant_rotated: bits must be 2, 3 or 4, got %d", bits);
+  }
+}
+
+#define FADE_DISPATCH_ASYM(bits, group, D, ...)                                        \
+  do {                                                                                         \
+    if ((bits) != 4 && (bits) != 2) return einval("asym: bits must be 4 or 2, got %d", (bits)); \
+    if ((group) != 16 && (group) != 32 && (group) != 64)                                       \
+      return einval("asym: group must be 16, 32 or 64, got %d", (group));                     \
+    if ((D) % (group) != 0) return einval("asym: D must be divisible by group");              \
+    FADE_DISPATCH_LPR(D, {                                                                     \
+      if ((bits) == 4) {                                                                       \
+        constexpr int BITS = 4;                                                                \
+        if ((group) == 16) { constexpr int LPG = 2; __VA_ARGS__; }                             \
+        else if ((group) == 32) { constexpr int LPG = 4; __VA_ARGS__; }                        \
+        else { constexpr int LPG = 8; __VA_ARGS__; }                                           \
+      } else {                                                                                 \
+        constexpr int BITS = 2;                                                                \
+        if ((group) == 16) { constexpr int LPG = 2; __VA_ARGS__; }                             \
+        else if ((group) == 32) { constexpr int LPG = 4; __VA_ARGS__; }                        \
+        else { constexpr int LPG = 8; __VA_ARGS__; }                                           \
+      }                                                                                        \
+    });                                                                                        \
+  } while (0)
+
+FADE_API int fade_quant_asym(const void* x_f16, int64_t B, int64_t H, int64_t S, int64_t D,
+                             int64_t sb, int64_t sh, int64_t ss, int32_t bits, int32_t group,
+                             void* packed_u8, void* scale_f16, void* zero_f16, void* stream) {
+  int rc = check_dims("fade_quant_asym", B, H, S, D);
+  if (rc) return rc;
+  if (!aligned(x_f16, 16) || (sb | sh | ss) % 8 != 0)
+    return einval("fade_quant_asym: input must be 16-byte aligned with strides a multiple of 8");
+  const int64_t rows = B * H * S;
+  if (rows == 0) return FADE_OK;
+  FADE_DISPATCH_ASYM(bits, group, D,
+                     hipLaunchKernelGGL((quant_asym_kernel<BITS, LPG, LPR>),
+                                         dim3(grid_for_rows(rows, LPR)), dim3(kBlock), 0,
+                                         as_stream(stream), static_cast<const uint16_t*>(x_f16),
+                                         rows, H, S, sb, sh, ss, static_cast<uint8_t*>(packed_u8),
+                                         static_cast<uint16_t*>(scale_f16),
+                                         static_cast<uint16_t*>(zero_f16)));
+  return check_launch("fade_quant_asym");
+}
+
+FADE_API int fade_dequant_asym(const void* packed_u8, const void* scale_f16, const void* zero_f16,
+                               int32_t bits, int32_t group, int64_t B, int64_t H, int64_t S,
+                               int64_t D, void* out_f16, void* stream) {
+  int rc = check_dims("fade_dequant_asym", B, H, S, D);
+  if (rc) return rc;
+  const int64_t rows = B * H * S;
+  if (rows == 0) return FADE_OK;
+  FADE_DISPATCH_ASYM(bits, group, D,
+                     hipLaunchKernelGGL((dequant_asym_kernel<BITS, LPG, LPR>),
+                                         dim3(grid_for_rows(rows, LPR)), dim3(kBlock), 0,
+                                         as_stream(stream), static_cast<const uint8_t*>(packed_u8),
+                                         static_cast<const uint16_t*>(scale_f16),
+                                         static_cast<const uint16_t*>(zero_f16), rows,
+                                         static_cast<uint16_t*>(out_f16)));
+  return check_launch("fade_dequant_asym");
+}

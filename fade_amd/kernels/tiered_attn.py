@@ -1,0 +1,170 @@
+"""Fused decode attention over the tiered cache (sink fp16 | packed middle | recent fp16).
+
+The reference never fuses the tiers: every decode step dequantizes the
+middle tier, ``torch.cat``s sink | middle | recent into fresh fp16 K/V and
+runs SDPA (fade/cache.py:683-842).  ``tiered_decode_attention`` reads the
+packed middle tier in place through ``fade_tiered_decode_attn``.
+
+``TieredDecodePlan`` binds the tensors once and re-launches with a single
+C call, which is what the decode loop (and the benchmark) uses.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+
+_FMT = {
+    "fp16": _lib.MID_FP16,
+    "int4": _lib.MID_SYM,
+    "sym": _lib.MID_SYM,
+    "k4v2": _lib.MID_K4V2G,
+    "asym": _lib.MID_ASYM,
+}
+
+
+@dataclass
+class MiddleTier:
+    """Packed middle tier in one of the formats of ``include/fade_hip.h``.
+
+    fmt ``"int4"``/``"sym"``: ``k_codes``/``v_codes`` [B,Hkv,S,D*bits/8] u8,
+    ``k_scale`` [B,Hkv,1,D], ``v_scale`` [B,Hkv,S,1] (fp16).
+    fmt ``"k4v2"``: INT4 K as above; ``v_codes`` int8 [B,Hkv,S_pad,D] and
+    ``v_scale`` [B,Hkv,S_pad/group,D] (reference INT2-V, fade/cache.py:983-988).
+    fmt ``"asym"``: codes [B,Hkv,S,D*bits/8], scale/zero [B,Hkv,S,D/group].
+    fmt ``"fp16"``: ``k_codes``/``v_codes`` fp16 [B,Hkv,S,D].
+    """
+
+    fmt: str
+    k_codes: Tensor
+    v_codes: Tensor
+    k_scale: Tensor | None = None
+    v_scale: Tensor | None = None
+    k_zero: Tensor | None = None
+    v_zero: Tensor | None = None
+    k_bits: int = 4
+    v_bits: int = 4
+    group: int = 64
+    length: int | None = None
+
+    @property
+    def n_tokens(self) -> int:
+        return int(self.k_codes.shape[2]) if self.length is None else int(self.length)
+
+    def tensors(self):
+        return [t for t in (self.k_codes, self.v_codes, self.k_scale, self.v_scale, self.k_zero, self.v_zero) if t is not None]
+
+
+def _fp16_tier(kv: tuple[Tensor, Tensor] | None) -> _lib.Fp16Tier:
+    t = _lib.Fp16Tier()
+    if kv is None or kv[0] is None or kv[0].shape[2] == 0:
+        return t
+    k, v = kv
+    if k.dtype != torch.float16 or v.dtype != torch.float16:
+        raise ValueError("sink/recent tiers must be float16")
+    if k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise ValueError("sink/recent tiers need a contiguous head_dim axis")
+    t.k, t.v, t.len = k.data_ptr(), v.data_ptr(), int(k.shape[2])
+    t.k_sb, t.k_sh, t.k_ss = k.stride(0), k.stride(1), k.stride(2)
+    t.v_sb, t.v_sh, t.v_ss = v.stride(0), v.stride(1), v.stride(2)
+    return t
+
+
+def _mid_tier(mid: MiddleTier | None) -> _lib.MidTier:
+    m = _lib.MidTier()
+    if mid is None or mid.n_tokens == 0:
+        m.fmt = _lib.MID_NONE
+        return m
+    if mid.fmt not in _FMT:
+        raise ValueError(f"unknown middle format {mid.fmt!r}")
+    for t in mid.tensors():
+        if not t.is_contiguous():
+            raise ValueError("middle-tier tensors must be contiguous")
+    m.fmt = _FMT[mid.fmt]
+    m.k_bits, m.v_bits, m.group = mid.k_bits, mid.v_bits, mid.group
+    m.len = mid.n_tokens
+    m.v_rows = int(mid.v_codes.shape[2])
+    m.k_codes, m.v_codes = mid.k_codes.data_ptr(), mid.v_codes.data_ptr()
+    m.k_scale, m.v_scale = _lib.ptr(mid.k_scale), _lib.ptr(mid.v_scale)
+    m.k_zero, m.v_zero = _lib.ptr(mid.k_zero), _lib.ptr(mid.v_zero)
+    return m
+
+
+class TieredDecodePlan:
+    """Validated launch of the tiered decode kernel for fixed tensors.
+
+    Holds references to every tensor it points at, the output and the
+    workspace; ``run()`` enqueues the kernels on the current stream.
+    """
+
+    def __init__(
+        self,
+        q: Tensor,
+        sink: tuple[Tensor, Tensor] | None,
+        mid: MiddleTier | None,
+        recent: tuple[Tensor, Tensor] | None,
+        sm_scale: float | None = None,
+        out: Tensor | None = None,
+        n_splits: int = 0,
+        kernel: int = 0,
+    ) -> None:
+        if q.dim() != 4 or q.shape[2] != 1:
+            raise ValueError(f"q must be [B, Hq, 1, D], got {tuple(q.shape)}")
+        tensors = [q] + ([*sink] if sink else []) + ([*recent] if recent else []) + (mid.tensors() if mid else [])
+        _lib.require_gpu(*tensors, op="tiered_decode_attention")
+        _lib.require_f16(q, "tiered_decode_attention")
+        B, Hq, _, D = q.shape
+        ref = sink[0] if sink else (recent[0] if recent else mid.k_codes)
+        Hkv = int(ref.shape[1])
+        if q.stride(-1) != 1:
+            q = q.contiguous()
+        if out is None:
+            out = torch.empty(B, Hq, 1, D, dtype=torch.float16, device=q.device)
+        self._keep = (q, sink, mid, recent, out)
+        a = _lib.DecodeArgs()
+        a.B, a.Hq, a.Hkv, a.D = B, Hq, Hkv, D
+        a.q, a.q_sb, a.q_sh = q.data_ptr(), q.stride(0), q.stride(1)
+        a.out, a.o_sb, a.o_sh = out.data_ptr(), out.stride(0), out.stride(1)
+        a.sm_scale = float(1.0 / math.sqrt(D) if sm_scale is None else sm_scale)
+        a.sink, a.mid, a.recent = _fp16_tier(sink), _mid_tier(mid), _fp16_tier(recent)
+        a.n_splits, a.kernel = int(n_splits), int(kernel)
+        lib = _lib.load()
+        nb = ctypes.c_int64(0)
+        _lib.check(lib.fade_tiered_decode_workspace_bytes(ctypes.byref(a), nb), "fade_tiered_decode_workspace_bytes")
+        self.workspace = _lib.workspace(nb.value, q.device)
+        a.workspace, a.workspace_bytes = self.workspace.data_ptr(), self.workspace.numel()
+        self.args = a
+        self.out = out
+        self._fn = lib.fade_tiered_decode_attn
+        self._argp = ctypes.byref(a)
+
+    def run(self, stream: int | None = None) -> Tensor:
+        s = torch.cuda.current_stream(self.out.device).cuda_stream if stream is None else stream
+        _lib.check(self._fn(self._argp, s), "fade_tiered_decode_attn")
+        return self.out
+
+
+def tiered_decode_attention(
+    q: Tensor,
+    sink: tuple[Tensor, Tensor] | None,
+    mid: MiddleTier | None,
+    recent: tuple[Tensor, Tensor] | None,
+    sm_scale: float | None = None,
+    n_splits: int = 0,
+    kernel: int = 0,
+) -> Tensor:
+    """Decode attention of ``q`` [B,Hq,1,D] over the tiered cache; returns fp16 [B,Hq,1,D].
+
+    Query head ``h`` attends to KV head ``h // (Hq // Hkv)`` (the reference's
+    ``repeat_interleave`` GQA mapping, fade/kernels/fused_int4_attn.py:306-312).
+    """
+    return TieredDecodePlan(q, sink, mid, recent, sm_scale, n_splits=n_splits, kernel=kernel).run()
+
+
+__all__ = ["MiddleTier", "TieredDecodePlan", "tiered_decode_attention"]

@@ -1,0 +1,174 @@
+/*
+ * fade_hip.h -- C ABI of libfade_hip.so, the MI355X (gfx950) kernels behind
+ * the FADE tiered-KV hot path.
+ *
+ * Conventions
+ *   - Every tensor argument is a device pointer.  Sizes and strides are
+ *     int64 element counts; the last (head_dim) axis is always unit-stride.
+ *   - "stream" is a hipStream_t (NULL = the legacy default stream).  All
+ *     work is enqueued asynchronously on it; nothing allocates device
+ *     memory.  Entry points that need scratch take a caller-provided
+ *     workspace whose size the matching *_workspace_bytes() call returns.
+ *   - Return value: FADE_OK (0) or a negative code; fade_hip_last_error()
+ *     returns a message for the calling thread's last failure.
+ *     FADE_EINVAL marks a bad argument (the Python layer raises ValueError,
+ *     as the reference does for shape errors); FADE_ERUNTIME a HIP failure
+ *     (RuntimeError).
+ *   - fp16 tensors are IEEE binary16 (torch.float16); fp32 are IEEE binary32.
+ *
+ * Reference interfaces replaced (Omodaka9375/fade, pure Python + Triton)
+ * are cited per entry point as file:line.  The reference has no FFI: the
+ * binding a maintainer would add is the ctypes layer in fade_amd/_lib.py.
+ */
+#ifndef FADE_HIP_H
+#define FADE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FADE_OK 0
+#define FADE_ERUNTIME (-1)
+#define FADE_EINVAL (-22)
+
+#define FADE_ABI_VERSION 1
+
+/* Quantization axes. */
+#define FADE_AXIS_CHANNEL 0 /* one scale per (b, h, d): reduce over S (K)  */
+#define FADE_AXIS_TOKEN 1   /* one scale per (b, h, s): reduce over D (V)  */
+
+/* Middle-tier formats understood by the attention kernels. */
+#define FADE_MID_NONE 0 /* no middle tier                                      */
+#define FADE_MID_FP16 1 /* fp16 K/V (flash-decode comparator)                  */
+#define FADE_MID_SYM 2  /* symmetric packed codes, K per-channel scale [B,H,1,D],
+                           V per-token scale [B,H,S,1]; bits 4 (nibbles, high =
+                           even index) or 2 (four per byte, first in bits 7:6).
+                           fade/quant.py:61-92, fade/rotated_quant.py:106-173   */
+#define FADE_MID_K4V2G 3 /* K as FADE_MID_SYM 4-bit; V literal grouped INT2:
+                           int8 codes [B,H,S_pad,D], scale [B,H,S_pad/64,D]
+                           (fade/cache.py:983-988, fade/quant.py:130-150)       */
+#define FADE_MID_ASYM 4 /* per-token asymmetric groups along D (build format):
+                           codes [B,H,S,D*bits/8], scale/zero [B,H,S,D/group]   */
+
+int fade_hip_abi_version(void);
+const char* fade_hip_last_error(void);
+
+/* ---------------- bit packing (fade/quant.py:26-58, rotated_quant.py:35-69) */
+/* q: int8 codes, n_rows x D contiguous; packed: n_rows x D*bits/8.  bits 4|2 */
+int fade_pack_codes(const void* q_i8, int64_t n_rows, int64_t D, int32_t bits, void* packed_u8,
+                    void* stream);
+int fade_unpack_codes(const void* packed_u8, int64_t n_rows, int64_t D, int32_t bits, void* q_i8,
+                      void* stream);
+
+/* ---------------- symmetric INT4 on fp16 (fade/quant.py:61-92) ------------ */
+/* K [B,H,S,D] fp16 with strides (sb, sh, ss) -> packed [B,H,S,D/2] u8 and
+ * scale [B,H,1,D] fp16.  Two passes over S (column absmax, then codes). */
+int fade_quant_k_int4_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D, int64_t* bytes);
+int fade_quant_k_int4(const void* k_f16, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                      int64_t sh, int64_t ss, void* packed_u8, void* scale_f16, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+/* V [B,H,S,D] fp16 -> packed [B,H,S,D/2] u8 and scale [B,H,S,1] fp16. */
+int fade_quant_v_int4(const void* v_f16, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                      int64_t sh, int64_t ss, void* packed_u8, void* scale_f16, void* stream);
+
+/* Dequantize symmetric packed codes: out = fp16(code * scale)
+ * (fade/quant.py:124-127, rotated_quant.py:142-143).  axis selects the
+ * scale layout ([B,H,1,D] for CHANNEL, [B,H,S,1] for TOKEN); bits 4|2. */
+int fade_dequant_sym(const void* packed_u8, const void* scale_f16, int32_t bits, int32_t axis,
+                     int64_t B, int64_t H, int64_t S, int64_t D, void* out_f16, void* stream);
+
+/* ---------------- grouped INT2, reference literal (fade/quant.py:95-176) --- */
+/* x [B,H,S,D] fp16 (rows >= S read as zero, i.e. pad_to_group fused) ->
+ * codes int8 [B,H,S_pad,D], scale [B,H,S_pad/group,D] fp16. */
+int fade_quant_int2_grouped(const void* x_f16, int64_t B, int64_t H, int64_t S, int64_t S_pad,
+                            int64_t D, int64_t sb, int64_t sh, int64_t ss, int64_t group,
+                            void* codes_i8, void* scale_f16, void* stream);
+/* codes [B,H,S_pad,D] -> out [B,H,S_out,D] fp16 (rows beyond S_out trimmed). */
+int fade_dequant_int2_grouped(const void* codes_i8, const void* scale_f16, int64_t B, int64_t H,
+                              int64_t S_pad, int64_t D, int64_t group, int64_t S_out,
+                              void* out_f16, void* stream);
+
+/* ---------------- rotated symmetric on fp32 (fade/rotated_quant.py:106-173) */
+/* x_rot [B,H,S,D] fp32 contiguous (x.float() @ R.T) -> packed codes at
+ * bits 4|2 (3 = raw int8) and fp16 scale ([B,H,1,D] or [B,H,S,1]). */
+int fade_quant_rotated_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D, int32_t axis,
+                                       int64_t* bytes);
+int fade_quant_rotated(const float* x_rot, int64_t B, int64_t H, int64_t S, int64_t D,
+                       int32_t bits, int32_t axis, void* packed, void* scale_f16, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/* ---------------- asymmetric per-token groups (build format, no reference
+ * counterpart: BASELINE's "asymmetric group-32 scale/zero") ------------- */
+int fade_quant_asym(const void* x_f16, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                    int64_t sh, int64_t ss, int32_t bits, int32_t group, void* packed_u8,
+                    void* scale_f16, void* zero_f16, void* stream);
+int fade_dequant_asym(const void* packed_u8, const void* scale_f16, const void* zero_f16,
+                      int32_t bits, int32_t group, int64_t B, int64_t H, int64_t S, int64_t D,
+                      void* out_f16, void* stream);
+
+/* ---------------- eviction re-RoPE (fade/cache.py:911-935, 283-311) ------- */
+/* For each kept row j (keep_idx[j] ascending, int64):
+ *   k_out[b,h,j] = fp16(apply(fp16(inverse(k[b,h,keep_idx[j]], cos_old[keep_idx[j]],
+ *                  sin_old[keep_idx[j]])), cos_new[j], sin_new[j]))
+ *   v_out[b,h,j] = v[b,h,keep_idx[j]]
+ * cos/sin tables fp32 [S,D] (old) and [n_kept,D] (new).  v may be NULL. */
+int fade_rerope_gather(const void* k_f16, int64_t ksb, int64_t ksh, int64_t kss, const void* v_f16,
+                       int64_t vsb, int64_t vsh, int64_t vss, int64_t B, int64_t H, int64_t S,
+                       int64_t D, const int64_t* keep_idx, int64_t n_kept, const float* cos_old,
+                       const float* sin_old, const float* cos_new, const float* sin_new,
+                       void* k_out_f16, void* v_out_f16, void* stream);
+
+/* ---------------- tiered decode attention --------------------------------- */
+/* fp16 tier (sink or recent): K/V [B,Hkv,len,D] with element strides. */
+typedef struct fade_fp16_tier {
+  const void* k;
+  const void* v;
+  int64_t len;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+} fade_fp16_tier;
+
+/* Middle tier; all tensors contiguous in the layouts listed above. */
+typedef struct fade_mid_tier {
+  int32_t fmt;    /* FADE_MID_* */
+  int32_t k_bits; /* 4 or 2 (SYM/ASYM) */
+  int32_t v_bits; /* 4 or 2 (SYM/ASYM) */
+  int32_t group;  /* ASYM group along D; K4V2G group along S (64) */
+  int64_t len;    /* tokens */
+  int64_t v_rows; /* K4V2G: padded row count of the V codes (>= len) */
+  const void* k_codes;
+  const void* k_scale;
+  const void* k_zero;
+  const void* v_codes;
+  const void* v_scale;
+  const void* v_zero;
+} fade_mid_tier;
+
+typedef struct fade_decode_args {
+  int64_t B, Hq, Hkv, D;       /* D must be 128; Hq % Hkv == 0; Hq/Hkv <= 8 */
+  const void* q;               /* [B,Hq,1,D] fp16 */
+  int64_t q_sb, q_sh;
+  void* out;                   /* [B,Hq,1,D] fp16 */
+  int64_t o_sb, o_sh;
+  float sm_scale;              /* usually 1/sqrt(D) */
+  fade_fp16_tier sink;         /* tokens [0, sink.len) */
+  fade_mid_tier mid;           /* next mid.len tokens */
+  fade_fp16_tier recent;       /* last recent.len tokens */
+  int32_t n_splits;            /* 0 = choose automatically */
+  int32_t kernel;              /* 0 = auto, 1 = portable VALU kernel */
+  void* workspace;
+  int64_t workspace_bytes;
+} fade_decode_args;
+
+/* Replaces dequantize + torch.cat (fade/cache.py:683-842) + SDPA and the
+ * Triton fused_int4_sdpa decode path (fade/kernels/fused_int4_attn.py:277-342). */
+int fade_tiered_decode_workspace_bytes(const fade_decode_args* args, int64_t* bytes);
+int fade_tiered_decode_attn(const fade_decode_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FADE_HIP_H */

@@ -1,0 +1,157 @@
+"""GPU tests of the tiered cache: HF update protocol, eviction + re-RoPE + requant
+composed exactly as fade/cache.py:881-1057 does, and fused decode vs materialize."""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from fade_amd import FadeConfig, TieredKVCache, create_tiered_cache
+from fade_amd.cache import TIER_EVICT, TIER_FP16, TIER_INT4
+from fade_amd.policy import _assign_one_layer, reassign_tiers_by_position
+from fade_amd.rope import Vanilla
+from fade_amd.synthetic import exp_scores, kv_tensors
+from oracle import attention as oatt
+from oracle import quant as oq
+from oracle import rope as orope
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_reassign(k, v, pos, tiers, scheme, n_sink):
+    """The composed state change of apply_tier_assignment, restated with the oracle."""
+    keep = np.nonzero(tiers != TIER_EVICT)[0]
+    n = keep.size
+    if n < k.shape[2]:
+        co, so = scheme.host_cos_sin(torch.from_numpy(pos))
+        cn, sn = scheme.host_cos_sin(torch.arange(n))
+        k, v = orope.rerope_gather(k, v, keep, co.numpy(), so.numpy(), cn.numpy(), sn.numpy())
+        tiers, pos = tiers[keep], np.arange(n)
+    f = np.nonzero(tiers == TIER_FP16)[0]
+    i4 = np.nonzero(tiers == TIER_INT4)[0]
+    kq, ks = oq.quant_k_int4(k[:, :, i4])
+    vq, vs = oq.quant_v_int4(v[:, :, i4])
+    return {"fp16_k": k[:, :, f], "fp16_v": v[:, :, f], "kq": kq, "ks": ks, "vq": vq, "vs": vs,
+            "int4_pos": pos[i4], "fp16_pos": pos[f], "n_sink": min(n_sink, f.size)}
+
+
+def test_update_materializes_in_position_order(dev):
+    print("case cache update", flush=True)
+    _, k, v = kv_tensors(2, 4, 50, 128, seed=1)
+    c = TieredKVCache(n_sink=4, recent_window=8)
+    K, V = c.update(k[:, :, :40].to(dev), v[:, :, :40].to(dev), 0)
+    K, V = c.update(k[:, :, 40:].to(dev), v[:, :, 40:].to(dev), 0)
+    assert torch.equal(K.cpu(), k) and torch.equal(V.cpu(), v)
+    assert c.get_seq_length(0) == 50 and c.get_mask_sizes(1, 0) == (51, 0)
+    with pytest.raises(ValueError, match="batch size mismatch"):
+        c.update(k[:1, :, :1].to(dev), v[:1, :, :1].to(dev), 0)
+
+
+@pytest.mark.parametrize("budget", [None, 400])
+def test_apply_tier_assignment_matches_oracle_composition(dev, budget):
+    """Config-3 flow (Qwen2.5-7B shape, theta 1e6): eviction, re-RoPE, requant bit-exact."""
+    print(f"case cache reassign budget={budget}", flush=True)
+    B, Hkv, S, D = 2, 4, 1024, 128
+    _, k, v = kv_tensors(B, Hkv, S, D, seed=1003)
+    scheme = Vanilla(theta=1e6, head_dim=D)
+    cos, sin = scheme.host_cos_sin(torch.arange(S))
+    k = torch.from_numpy(orope.apply_rope(k.numpy(), cos.numpy(), sin.numpy()))
+    c = TieredKVCache(n_sink=4, recent_window=64, int4_budget=budget, rope_scheme=scheme, head_dim=D)
+    c.update(k.to(dev), v.to(dev), 0)
+    scores = exp_scores(S, seed=2003)
+    tiers = _assign_one_layer(S, scores, 4, 64, budget, 0)
+    c.apply_tier_assignment(0, tiers)
+    o = _oracle_reassign(k.numpy(), v.numpy(), np.arange(S), tiers.numpy(), scheme, 4)
+    st = c._layers[0]
+    assert np.array_equal(st.int4_kq.cpu().numpy(), o["kq"]) and np.array_equal(st.int4_vq.cpu().numpy(), o["vq"])
+    assert np.array_equal(st.int4_ks.cpu().numpy().view(np.uint16), o["ks"].view(np.uint16))
+    assert np.array_equal(st.int4_vs.cpu().numpy().view(np.uint16), o["vs"].view(np.uint16))
+    ns = o["n_sink"]
+    assert st.sink_count == ns
+    assert np.array_equal(st.sink_k.cpu().numpy().view(np.uint16), o["fp16_k"][:, :, :ns].view(np.uint16))
+    assert np.array_equal(st.fp16_k.cpu().numpy().view(np.uint16), o["fp16_k"][:, :, ns:].view(np.uint16))
+    assert np.array_equal(st.int4_pos.cpu().numpy(), o["int4_pos"])
+    n_kept = int((tiers != TIER_EVICT).sum())
+    assert c.get_seq_length(0) == n_kept and st.next_position == (n_kept if budget else S)
+
+    # decode straight from the tiers == SDPA over the materialized cache
+    q = torch.randn(B, 28, 1, D, generator=torch.Generator().manual_seed(3)).to(torch.float16)
+    Kn, Vn = c.update(k[:, :, :1].to(dev), v[:, :, :1].to(dev), 0)
+    fused = c.decode_attention(q.to(dev), 0).float().cpu().numpy()
+    ref = oatt.sdpa_fp32(q.numpy(), Kn.cpu().numpy(), Vn.cpu().numpy())
+    assert np.abs(fused - ref).max() <= 2e-3
+
+    # a second reassignment requantizes from dequantized values (fade/cache.py:976-989)
+    S2 = c.get_seq_length(0)
+    tiers2 = _assign_one_layer(S2, torch.arange(S2, dtype=torch.float32), 4, 64, 200, 0)
+    Kp, Vp = Kn.cpu().numpy(), Vn.cpu().numpy()
+    pos2 = np.concatenate([st.sink_pos.cpu().numpy(), st.int4_pos.cpu().numpy(), st.fp16_pos.cpu().numpy()])
+    c.apply_tier_assignment(0, tiers2)
+    o2 = _oracle_reassign(Kp, Vp, pos2, tiers2.numpy(), scheme, 4)
+    st = c._layers[0]
+    assert np.array_equal(st.int4_kq.cpu().numpy(), o2["kq"]) and np.array_equal(st.int4_vq.cpu().numpy(), o2["vq"])
+
+
+def test_k4v2_cache_decode(dev):
+    print("case cache k4v2", flush=True)
+    _, k, v = kv_tensors(1, 8, 700, 128, seed=4)
+    c = TieredKVCache(n_sink=4, recent_window=256, middle_v_bits=2)
+    c.update(k.to(dev), v.to(dev), 0)
+    c.apply_tier_assignment(0, _assign_one_layer(700, torch.zeros(700), 4, 256, None, 0))
+    st = c._layers[0]
+    assert st.int4_vq.dtype == torch.int8 and st.int4_vq.shape[2] % 64 == 0
+    q = torch.randn(1, 32, 1, 128, generator=torch.Generator().manual_seed(5)).to(torch.float16)
+    K, V = c._materialize(0)
+    fused = c.decode_attention(q.to(dev), 0).float().cpu().numpy()
+    ref = oatt.sdpa_fp32(q.numpy(), K.cpu().numpy(), V.cpu().numpy())
+    assert np.abs(fused - ref).max() <= 2e-3
+
+
+@pytest.mark.parametrize("backend", ["rotated", "int4_asym_g32"])
+def test_backend_caches_decode(dev, backend):
+    print(f"case cache backend={backend}", flush=True)
+    _, k, v = kv_tensors(1, 8, 600, 128, seed=6)
+    cfg = FadeConfig(quant_backend=backend)
+    c = TieredKVCache(head_dim=128, **cfg.to_cache_kwargs())
+    c.update(k.to(dev), v.to(dev), 0)
+    reassign_tiers_by_position(c, 1)
+    q = torch.randn(1, 32, 1, 128, generator=torch.Generator().manual_seed(7)).to(torch.float16)
+    K, V = c._materialize(0)
+    fused = c.decode_attention(q.to(dev), 0).float().cpu().numpy()
+    ref = oatt.sdpa_fp32(q.numpy(), K.cpu().numpy(), V.cpu().numpy())
+    assert np.abs(fused - ref).max() <= 2e-3
+
+
+def test_per_sequence_assignment_and_checkpoint(dev):
+    print("case cache per-sequence", flush=True)
+    _, k, v = kv_tensors(2, 2, 300, 128, seed=8)
+    c = TieredKVCache(n_sink=4, recent_window=32, int4_budget=100)
+    c.update(k.to(dev), v.to(dev), 0)
+    g = torch.Generator().manual_seed(9)
+    t = torch.stack([_assign_one_layer(300, torch.rand(300, generator=g), 4, 32, 100, 0) for _ in range(2)])
+    c.apply_tier_assignment_per_sequence(0, t)
+    assert c._layers[0].int4_kq.shape[2] == 100
+    sd = c.cache_state_dict()
+    c2 = TieredKVCache(n_sink=4, recent_window=32, int4_budget=100)
+    c2.load_cache_state_dict(sd, device=dev)
+    K1, V1 = c._materialize(0)
+    K2, V2 = c2._materialize(0)
+    assert torch.equal(K1, K2) and torch.equal(V1, V2)
+
+
+def test_create_tiered_cache_from_hf_config(dev):
+    print("case create_tiered_cache", flush=True)
+    from transformers import AutoConfig
+
+    cfg = AutoConfig.for_model("qwen2", hidden_size=256, num_attention_heads=2, num_key_value_heads=1,
+                               num_hidden_layers=2, intermediate_size=512, vocab_size=100, rope_theta=1e6)
+    model = type("M", (), {"config": cfg})()
+    c = create_tiered_cache(model, config=FadeConfig.balanced())
+    assert c.head_dim == 128 and c.int4_budget == 400 and c.rope_scheme.theta == 1e6
+    _, k, v = kv_tensors(1, 1, 10, 128, seed=1)
+    K, _ = c.update(k.to(dev), v.to(dev), 0)
+    assert K.shape == (1, 1, 10, 128)
+    q = torch.randn(1, 2, 1, 128).to(torch.float16)
+    out = c.decode_attention(q.to(dev), 0)
+    ref = F.scaled_dot_product_attention(q.float(), k.float().repeat_interleave(2, 1), v.float().repeat_interleave(2, 1))
+    assert (out.float().cpu() - ref).abs().max() <= 2e-3

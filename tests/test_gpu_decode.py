@@ -1,0 +1,158 @@
+"""GPU parity of the fused tiered decode attention against the oracle.
+
+Tolerance: max-abs 2e-3 on the fp16 output against fp32 attention over the
+oracle's dequantized tiers (the bar BASELINE.json states for attention).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from fade_amd import quant as fq
+from fade_amd import rotated_quant as frq
+from fade_amd.kernels import MiddleTier, check_fused_parity, fused_int4_sdpa, tiered_decode_attention
+from fade_amd.synthetic import kv_tensors
+from oracle import attention as oatt
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+ATOL = 2e-3
+
+
+def _case(B, Hq, Hkv, S, ns, nr, seed):
+    q, k, v = kv_tensors(B, Hkv, S, 128, seed=seed, Hq=Hq)
+    return q.numpy(), k.numpy(), v.numpy(), ns, nr
+
+
+def _run(dev, q, k, v, ns, nr, mid_gpu, mid_oracle, kernel=0, n_splits=0):
+    S = k.shape[2]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    sink = (t(k[:, :, :ns]), t(v[:, :, :ns])) if ns else None
+    rec = (t(k[:, :, S - nr :]), t(v[:, :, S - nr :])) if nr else None
+    out = tiered_decode_attention(t(q), sink, mid_gpu, rec, kernel=kernel, n_splits=n_splits)
+    ref = oatt.tiered_decode(q, k[:, :, :ns], v[:, :, :ns], mid_oracle, k[:, :, S - nr :], v[:, :, S - nr :])
+    return np.abs(out.float().cpu().numpy() - ref).max()
+
+
+def _int4_mid(dev, k, v, ns, nr):
+    S = k.shape[2]
+    km, vm = k[:, :, ns : S - nr], v[:, :, ns : S - nr]
+    kq, ks = fq.quant_k_int4(torch.from_numpy(np.ascontiguousarray(km)).to(dev))
+    vq, vs = fq.quant_v_int4(torch.from_numpy(np.ascontiguousarray(vm)).to(dev))
+    okq, oks = oq.quant_k_int4(km)
+    ovq, ovs = oq.quant_v_int4(vm)
+    return MiddleTier("int4", kq, vq, ks, vs), {"fmt": "int4", "kq": okq, "ks": oks, "vq": ovq, "vs": ovs}
+
+
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,S,ns,nr",
+    [
+        (1, 32, 8, 2048, 4, 64),  # config 0
+        (2, 28, 4, 700, 4, 64),  # GQA 7 (Qwen2.5-7B heads)
+        (1, 8, 8, 130, 0, 0),  # MHA, middle only, ragged tile
+        (3, 16, 4, 5, 2, 2),  # tiny: one middle token
+        (1, 32, 8, 333, 4, 256),  # config 2 windows
+    ],
+)
+@pytest.mark.parametrize("kernel", [0, 1])
+def test_tiered_decode_int4(dev, B, Hq, Hkv, S, ns, nr, kernel):
+    print(f"case decode int4 B={B} Hq={Hq} Hkv={Hkv} S={S} ns={ns} nr={nr} kernel={kernel}", flush=True)
+    q, k, v, ns, nr = _case(B, Hq, Hkv, S, ns, nr, seed=1000 + S)
+    mid, omid = _int4_mid(dev, k, v, ns, nr)
+    err = _run(dev, q, k, v, ns, nr, mid, omid, kernel=kernel)
+    assert err <= ATOL, err
+
+
+@pytest.mark.parametrize("n_splits", [1, 3, 64])
+def test_tiered_decode_split_counts(dev, n_splits):
+    print(f"case decode splits={n_splits}", flush=True)
+    q, k, v, ns, nr = _case(1, 32, 8, 1500, 4, 64, seed=5)
+    mid, omid = _int4_mid(dev, k, v, ns, nr)
+    assert _run(dev, q, k, v, ns, nr, mid, omid, n_splits=n_splits) <= ATOL
+
+
+def test_tiered_decode_fp16_middle_flash_decode(dev):
+    print("case decode fp16 comparator", flush=True)
+    q, k, v, ns, nr = _case(2, 32, 8, 1024, 4, 64, seed=6)
+    S = k.shape[2]
+    km, vm = k[:, :, ns : S - nr], v[:, :, ns : S - nr]
+    mid = MiddleTier("fp16", torch.from_numpy(np.ascontiguousarray(km)).to(dev),
+                     torch.from_numpy(np.ascontiguousarray(vm)).to(dev))
+    assert _run(dev, q, k, v, ns, nr, mid, {"fmt": "fp16", "k": km, "v": vm}) <= ATOL
+
+
+def test_tiered_decode_k4_v2_literal(dev):
+    """Config-2 parity format: INT4 K + reference grouped INT2 V (int8 codes, [G, D] scales)."""
+    print("case decode k4v2", flush=True)
+    q, k, v, ns, nr = _case(1, 32, 8, 1200, 4, 256, seed=7)
+    S = k.shape[2]
+    km, vm = k[:, :, ns : S - nr], v[:, :, ns : S - nr]
+    n = km.shape[2]
+    kq, ks = fq.quant_k_int4(torch.from_numpy(np.ascontiguousarray(km)).to(dev))
+    vq, vs = fq.quant_int2_padded(torch.from_numpy(np.ascontiguousarray(vm)).to(dev), 64)
+    okq, oks = oq.quant_k_int4(km)
+    ovq, ovs = oq.quant_int2_grouped(oq.pad_to_group(vm, 64)[0], 64)
+    mid = MiddleTier("k4v2", kq, vq, ks, vs, group=64, length=n)
+    omid = {"fmt": "k4v2", "kq": okq, "ks": oks, "vq": ovq, "vs": ovs, "group": 64}
+    assert _run(dev, q, k, v, ns, nr, mid, omid) <= ATOL
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_tiered_decode_rotated(dev, bits):
+    """Rotated K/V codes: attend in the rotated basis (q R^T, o R) -- the reference rounds
+    k_hat through fp16 after rotating back, which the 2e-3 bar absorbs."""
+    print(f"case decode rotated bits={bits}", flush=True)
+    R = torch.from_numpy(np.load(__file__.rsplit("/", 1)[0] + "/golden/rotation_d128_seed42.npy")).to(dev)
+    q, k, v, ns, nr = _case(1, 32, 8, 900, 0, 0, seed=8)
+    kt, vt = torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev)
+    kp, ks = frq.rotated_quant_k(kt, R, bits)
+    vp, vs = frq.rotated_quant_v(vt, R, bits)
+    mid = MiddleTier("sym", kp, vp, ks, vs, k_bits=bits, v_bits=bits)
+    qt = torch.from_numpy(q).to(dev)
+    q_rot = (qt.float() @ R.T).to(torch.float16)
+    out = (tiered_decode_attention(q_rot, None, mid, None).float() @ R).cpu().numpy()
+    omid = {"fmt": "rot", "kq": kp.cpu().numpy(), "ks": ks.cpu().numpy(), "vq": vp.cpu().numpy(),
+            "vs": vs.cpu().numpy(), "R": R.cpu().numpy(), "k_bits": bits, "v_bits": bits}
+    ref = oatt.tiered_decode(q, k[:, :, :0], v[:, :, :0], omid, k[:, :, :0], v[:, :, :0])
+    assert np.abs(out - ref).max() <= ATOL
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_tiered_decode_asym(dev, bits):
+    print(f"case decode asym bits={bits}", flush=True)
+    q, k, v, ns, nr = _case(2, 32, 8, 800, 4, 64, seed=9)
+    S = k.shape[2]
+    km, vm = k[:, :, ns : S - nr], v[:, :, ns : S - nr]
+    kp, ksc, kz = fq.quant_asym(torch.from_numpy(np.ascontiguousarray(km)).to(dev), bits, 32)
+    vp, vsc, vz = fq.quant_asym(torch.from_numpy(np.ascontiguousarray(vm)).to(dev), bits, 32)
+    mid = MiddleTier("asym", kp, vp, ksc, vsc, kz, vz, k_bits=bits, v_bits=bits, group=32)
+    okp, oks, okz = oq.quant_asym_group(km, bits, 32)
+    ovp, ovs, ovz = oq.quant_asym_group(vm, bits, 32)
+    omid = {"fmt": "asym", "kq": okp, "ks": oks, "kz": okz, "vq": ovp, "vs": ovs, "vz": ovz,
+            "k_bits": bits, "v_bits": bits, "group": 32}
+    assert _run(dev, q, k, v, ns, nr, mid, omid) <= ATOL
+
+
+def test_fused_int4_sdpa_api_and_parity_helper(dev):
+    print("case fused_int4_sdpa", flush=True)
+    res = check_fused_parity()
+    assert res["passed"], res
+    q, k, v, _, _ = _case(2, 8, 2, 300, 0, 0, seed=10)
+    kq, ks = oq.quant_k_int4(k)
+    vq, vs = oq.quant_v_int4(v)
+    t = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    out = fused_int4_sdpa(t(q), t(kq), t(ks), t(vq), t(vs))
+    ref = oatt.tiered_decode(q, None, {"fmt": "int4", "kq": kq, "ks": ks, "vq": vq, "vs": vs}, None, None)
+    assert out.shape == (2, 8, 1, 128) and out.dtype == torch.float16
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= ATOL
+
+
+def test_decode_errors(dev):
+    print("case decode errors", flush=True)
+    q = torch.zeros(1, 6, 1, 128, dtype=torch.float16, device=dev)
+    k = torch.zeros(1, 4, 10, 128, dtype=torch.float16, device=dev)
+    with pytest.raises(ValueError, match="not a multiple"):
+        tiered_decode_attention(q, (k, k), None, None)
+    q = torch.zeros(1, 4, 1, 128, dtype=torch.float16, device=dev)
+    with pytest.raises(ValueError, match="empty"):
+        tiered_decode_attention(q, (k[:, :, :0], k[:, :, :0]), None, None)
