@@ -11,8 +11,9 @@ int64_t total_tokens(const fade_decode_args* a) { return a->sink.len + a->mid.le
 
 // Split the token range so that B*Hkv*n_splits workgroups cover the 256 CUs
 // several times over, in multiples of the kernel's token tile.
-void plan_splits(const fade_decode_args* a, int tile, int64_t* n_splits, int64_t* tps) {
-  const int64_t total = total_tokens(a);
+void plan_splits(const fade_decode_args* a, int tile, int64_t* n_splits, int64_t* tps,
+                 int64_t total_override = -1) {
+  const int64_t total = total_override >= 0 ? total_override : total_tokens(a);
   const int64_t pairs = a->B * a->Hkv;
   int64_t want = a->n_splits > 0 ? a->n_splits : cdiv(2048, pairs > 0 ? pairs : 1);
   const int64_t max_splits = cdiv(total, tile) > 0 ? cdiv(total, tile) : 1;
@@ -132,9 +133,9 @@ FADE_API int fade_tiered_decode_workspace_bytes(const fade_decode_args* a, int64
   if (rc) return rc;
   if (bytes == nullptr) return einval("fade_tiered_decode_workspace_bytes: null output");
   const Params p = to_params(a);
-  const int tile = use_mfma(a, p) ? mfma_tile() : 64;
+  const bool mfma = use_mfma(a, p);
   int64_t n, tps;
-  plan_splits(a, tile, &n, &tps);
+  plan_splits(a, mfma ? mfma_tile() : 64, &n, &tps, mfma ? mfma_tiles(p) * mfma_tile() : -1);
   *bytes = ml_bytes(a, n) + a->B * a->Hq * n * kD * 4;
   return FADE_OK;
 }
@@ -146,9 +147,8 @@ FADE_API int fade_tiered_decode_attn(const fade_decode_args* a, void* stream) {
   const bool mfma = use_mfma(a, p);
   if (a->kernel == 2 && !mfma)
     return einval("fade_tiered_decode_attn: the matrix-core kernel does not handle middle format %d", p.mid.fmt);
-  const int tile = mfma ? mfma_tile() : 64;
   int64_t n, tps;
-  plan_splits(a, tile, &n, &tps);
+  plan_splits(a, mfma ? mfma_tile() : 64, &n, &tps, mfma ? mfma_tiles(p) * mfma_tile() : -1);
   const int64_t need = ml_bytes(a, n) + a->B * a->Hq * n * kD * 4;
   if (a->workspace == nullptr || a->workspace_bytes < need)
     return einval("fade_tiered_decode_attn: workspace too small (%lld < %lld bytes)",

@@ -75,6 +75,8 @@ int launch_valu(const Params& p, hipStream_t st);
 int launch_mfma(const Params& p, hipStream_t st);
 bool mfma_supports(const Params& p);
 int mfma_tile();
+// Number of 64-token tiles the matrix-core kernel walks (fp16 tokens, then packed).
+int64_t mfma_tiles(const Params& p);
 
 }  // namespace decode
 }  // namespace fade

@@ -1,13 +1,456 @@
-// Matrix-core (MFMA) tiered decode kernel -- not enabled yet; every format
-// runs the portable kernel in decode.hip.
+// Matrix-core (MFMA) tiered decode attention for gfx950.
+//
+// One workgroup = 4 wavefronts serving one (batch row, kv head, split); each
+// wavefront walks its own 64-token tiles with its own online-softmax state
+// and the four are merged through LDS at the end.  The whole GQA group of
+// query heads rides in the 16 rows of every MFMA, so each KV byte is read
+// once.  Per 64-token tile:
+//
+//   QK^T  int8 MFMA 16x16x64.  A = K codes of 16 tokens (a lane's 16-byte
+//         load of a packed row becomes 32 offset-binary int8 codes u = c + 8,
+//         two k-steps); B = the query, pre-scaled by the per-channel K scale,
+//         quantized to 16 bits and split into two int8 digits (hi*256 + lo).
+//         score = hi_acc*256 + lo_acc - 8*sum(q_int), exact in int32.
+//   PV    f16 MFMA 16x16x32.  A = P * v_scale[token] (fp16); B = V codes
+//         staged through LDS and transposed by ds_read_b64_tr_b4 (each lane
+//         receives one channel of 16 tokens), turned into fp16 with the
+//         0x6400 | nibble trick.
+//
+// fp16 tiles (sink + recent tokens, or every tile of the fp16 comparator)
+// use an f16 MFMA for QK^T and direct fp16 V loads; they accumulate into the
+// same fragments.
+//
+// Fragment bookkeeping (lane = 16*g + n, C fragment row = 4*g + i):
+//   QK m-tile j, A row m  <->  token 16*(m/4) + 4*j + (m%4) of the tile
+//   score reg i of m-tile j in lane (h=n, g)  <->  token 16*g + 4*j + i
+//   PV k-step s, lane (., g), VGPR v  <->  tokens (16g + 8s + v, 16g + 8s + v + 4)
+//   O n-tile c, column n  <->  channel 16*c + (n ^ 1)
+#include <math.h>
+
 #include "decode_common.h"
 
 namespace fade {
 namespace decode {
+namespace {
 
-bool mfma_supports(const Params&) { return false; }
-int mfma_tile() { return 64; }
-int launch_mfma(const Params& p, hipStream_t st) { return launch_valu(p, st); }
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kTileT = 64;
+constexpr int kVPitch = 80;  // LDS bytes per staged V row: 64 data + 16 pad (conflict-free tr4)
+constexpr float kQMax = 32000.0f;
+constexpr int kV16Pitch = 136;  // halfs per staged fp16 V row (16 rows = 4352 B fit the V tile buffer)
+
+__device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+__device__ __forceinline__ f16x2 u2h2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
+__device__ __forceinline__ uint32_t h22u(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Offset-binary int8 codes (u = c + 8) of one packed dword: lo nibbles
+// (odd channels) and hi nibbles (even channels), four bytes each.
+__device__ __forceinline__ void nib_to_u8(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const uint32_t x = w ^ 0x88888888u;
+  lo = x & 0x0F0F0F0Fu;
+  hi = (x >> 4) & 0x0F0F0F0Fu;
+}
+
+// fp16 pairs (nibble v, nibble v+4) of 8 two's-complement codes, v = 0..3.
+__device__ __forceinline__ void nib8_to_f16(uint32_t w, f16x2* out) {
+  const uint32_t x = w ^ 0x88888888u;
+  const f16x2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+#pragma unroll
+  for (int v = 0; v < 4; ++v) out[v] = u2h2(((x >> (4 * v)) & 0x000F000Fu) | 0x64006400u) + bias;
+}
+
+struct FpTok {  // one fp16 token row (K and V pointers)
+  const uint16_t* k;
+  const uint16_t* v;
+};
+
+// Row pointers of virtual fp16 token f: sink, (fp16 middle), recent.
+template <bool MID_F16>
+__device__ __forceinline__ FpTok fp16_token(const Params& p, int64_t b, int64_t kvh, int64_t f) {
+  FpTok r;
+  const int64_t ns = p.sink.len;
+  if (f < ns) {
+    r.k = p.sink.k + b * p.sink.k_sb + kvh * p.sink.k_sh + f * p.sink.k_ss;
+    r.v = p.sink.v + b * p.sink.v_sb + kvh * p.sink.v_sh + f * p.sink.v_ss;
+    return r;
+  }
+  f -= ns;
+  if (MID_F16) {
+    if (f < p.mid.len) {
+      const int64_t row = (b * p.Hkv + kvh) * p.mid.len + f;
+      r.k = reinterpret_cast<const uint16_t*>(p.mid.k_codes) + row * kD;
+      r.v = reinterpret_cast<const uint16_t*>(p.mid.v_codes) + row * kD;
+      return r;
+    }
+    f -= p.mid.len;
+  }
+  r.k = p.recent.k + b * p.recent.k_sb + kvh * p.recent.k_sh + f * p.recent.k_ss;
+  r.v = p.recent.v + b * p.recent.v_sb + kvh * p.recent.v_sh + f * p.recent.v_ss;
+  return r;
+}
+
+template <bool MID_F16>
+__global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
+  const int split = blockIdx.x;
+  const int64_t kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n16 = lane & 15, grp = lane >> 4;
+  const int G = p.G;
+  const int64_t bkv = b * p.Hkv + kvh;
+  const int64_t M = MID_F16 ? 0 : p.mid.len;                  // packed middle tokens
+  const int64_t F = p.total - M;                               // fp16 tokens
+  const int64_t nF = (F + kTileT - 1) / kTileT;
+
+  __shared__ __attribute__((aligned(16))) uint8_t vtile[kWaves][kTileT * kVPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t vs_s[kWaves][kTileT];
+  __shared__ __attribute__((aligned(16))) float alpha_s[kWaves][16];
+  __shared__ float red_m[kWaves][16], red_l[kWaves][16];
+  __shared__ __attribute__((aligned(16))) uint16_t q16_s[16][kD + 8];
+
+  // ---- query operands (lane = head n16, k-group grp) ----
+  const bool hvalid = n16 < G;
+  uint4 qraw[4];
+  {
+    const uint16_t* qp = p.q + b * p.q_sb + (kvh * G + (hvalid ? n16 : 0)) * p.q_sh + 32 * grp;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qraw[c] = hvalid ? ldg16(qp + 8 * c) : make_uint4(0, 0, 0, 0);
+  }
+  // fp16 query rows for the fp16 tiles' QK^T (B operand read from LDS when needed)
+  if (wave == 0) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) *reinterpret_cast<uint4*>(&q16_s[n16][32 * grp + 8 * c]) = qraw[c];
+  }
+  i32x4 qd_hi[2], qd_lo[2];  // int8 digits of q * k_scale for the packed middle
+  int corr = 0;
+  float qscale = 0.0f;
+  if (!MID_F16 && M > 0) {
+    float qf[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t u[4] = {qraw[c].x, qraw[c].y, qraw[c].z, qraw[c].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qf[8 * c + 2 * e] = h2f(static_cast<uint16_t>(u[e] & 0xFFFFu));
+        qf[8 * c + 2 * e + 1] = h2f(static_cast<uint16_t>(u[e] >> 16));
+      }
+    }
+    const uint16_t* ksp = p.mid.k_scale + bkv * kD + 32 * grp;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint4 w = ldg16(ksp + 8 * c);
+      const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qf[8 * c + 2 * e] *= h2f(static_cast<uint16_t>(u[e] & 0xFFFFu));
+        qf[8 * c + 2 * e + 1] *= h2f(static_cast<uint16_t>(u[e] >> 16));
+      }
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 32; ++d) mx = fmaxf(mx, fabsf(qf[d]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float inv = mx > 0.0f ? kQMax / mx : 0.0f;
+    qscale = mx > 0.0f ? (mx / kQMax) * p.scale_log2 : 0.0f;
+    int qi[32];
+    int sum = 0;
+#pragma unroll
+    for (int d = 0; d < 32; ++d) {
+      qi[d] = static_cast<int>(rintf(qf[d] * inv));
+      sum += qi[d];
+    }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    corr = 8 * sum;
+    // k-step ks, dword js, byte e  <->  channel 32*grp + 8*(2ks + js/2) + 2e + (js even ? 1 : 0)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int js = 0; js < 4; ++js) {
+        uint32_t whi = 0, wlo = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int dl = 8 * (2 * ks + js / 2) + 2 * e + ((js % 2 == 0) ? 1 : 0);
+          const int hi = (qi[dl] + 128) >> 8;
+          const int lo = qi[dl] - hi * 256;
+          whi |= static_cast<uint32_t>(hi & 0xFF) << (8 * e);
+          wlo |= static_cast<uint32_t>(lo & 0xFF) << (8 * e);
+        }
+        qd_hi[ks][js] = static_cast<int>(whi);
+        qd_lo[ks][js] = static_cast<int>(wlo);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) qd_hi[ks] = qd_lo[ks] = i32x4{0, 0, 0, 0};
+  }
+
+  // ---- tiles of this split; wave w takes tiles w, w+4, ... ----
+  const int64_t tiles_per_split = p.tokens_per_split / kTileT;
+  const int64_t t0 = static_cast<int64_t>(split) * tiles_per_split;
+  const int64_t nT = nF + (M + kTileT - 1) / kTileT;
+  const int64_t t1 = t0 + tiles_per_split < nT ? t0 + tiles_per_split : nT;
+
+  __syncthreads();
+  float m_run = -INFINITY, l_lane = 0.0f;
+  f32x4 acc[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) acc[c] = f32x4{0, 0, 0, 0};
+
+  uint8_t* my_vtile = vtile[wave];
+  for (int64_t tau = t0 + wave; tau < t1; tau += kWaves) {
+    float s[4][4];
+    float vsc[16];  // V scale of tokens 16*grp + 0..15 (1 for fp16 tiles)
+    bool is_f16 = tau < nF;
+    __builtin_amdgcn_wave_barrier();
+    if (!is_f16) {
+      // -------------------------------------------------- packed INT4 tile
+      const int64_t m0 = (tau - nF) * kTileT;
+      const uint8_t* kc = p.mid.k_codes + bkv * M * 64;
+      const uint8_t* vc = p.mid.v_codes + bkv * M * 64;
+      // stage V codes (rows 16k + lane/4, 16-byte chunk lane%4) and V scales
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = 16 * k + (lane >> 2);
+        const int64_t row = m0 + r < M ? m0 + r : M - 1;
+        *reinterpret_cast<uint4*>(my_vtile + r * kVPitch + 16 * (lane & 3)) = ldg16(vc + row * 64 + 16 * (lane & 3));
+      }
+      vs_s[wave][lane] = m0 + lane < M ? p.mid.v_scale[bkv * M + m0 + lane] : static_cast<uint16_t>(0);
+      // QK^T on the matrix cores
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int rloc = 16 * (n16 >> 2) + 4 * j + (n16 & 3);
+        const int64_t row = m0 + rloc < M ? m0 + rloc : M - 1;
+        const uint4 w = ldg16(kc + row * 64 + 16 * grp);
+        uint32_t lo0, hi0, lo1, hi1, lo2, hi2, lo3, hi3;
+        nib_to_u8(w.x, lo0, hi0);
+        nib_to_u8(w.y, lo1, hi1);
+        nib_to_u8(w.z, lo2, hi2);
+        nib_to_u8(w.w, lo3, hi3);
+        const i32x4 a0 = {static_cast<int>(lo0), static_cast<int>(hi0), static_cast<int>(lo1), static_cast<int>(hi1)};
+        const i32x4 a1 = {static_cast<int>(lo2), static_cast<int>(hi2), static_cast<int>(lo3), static_cast<int>(hi3)};
+        i32x4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
+        chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qd_hi[0], chi, 0, 0, 0);
+        chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, qd_hi[1], chi, 0, 0, 0);
+        clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qd_lo[0], clo, 0, 0, 0);
+        clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, qd_lo[1], clo, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t tok = m0 + 16 * grp + 4 * j + i;
+          const int si = chi[i] * 256 + clo[i] - corr;
+          s[j][i] = tok < M ? static_cast<float>(si) * qscale : -INFINITY;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int k = 0; k < 16; ++k) vsc[k] = h2f(vs_s[wave][16 * grp + k]);
+    } else {
+      // -------------------------------------------------- fp16 tile
+      const int64_t f0 = tau * kTileT;
+#pragma unroll 1
+      for (int j = 0; j < 4; ++j) {
+        const int rloc = 16 * (n16 >> 2) + 4 * j + (n16 & 3);
+        const int64_t f = f0 + rloc < F ? f0 + rloc : F - 1;
+        const uint16_t* kr = fp16_token<MID_F16>(p, b, kvh, f).k + 32 * grp;
+        f32x4 c4 = {0, 0, 0, 0};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const f16x8 qb = *reinterpret_cast<const f16x8*>(&q16_s[n16][32 * grp + 8 * ks]);
+          c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ldg16(kr + 8 * ks)), qb, c4, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t tok = f0 + 16 * grp + 4 * j + i;
+          s[j][i] = tok < F ? c4[i] * p.scale_log2 : -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 16; ++k) vsc[k] = 1.0f;
+    }
+
+    // ---- online softmax for head n16 over the tile's 64 tokens ----
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[j][i]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
+    float psum = 0.0f;
+    float pw[4][4];
+    f16x2 pa[2][4];  // A operand of PV: k-step s, VGPR v = tokens (16g+8s+v, 16g+8s+v+4)
+#pragma unroll
+    for (int sk = 0; sk < 2; ++sk) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float p0 = m_new == -INFINITY ? 0.0f : exp2f(s[2 * sk][v] - m_new);
+        const float p1 = m_new == -INFINITY ? 0.0f : exp2f(s[2 * sk + 1][v] - m_new);
+        psum += p0 + p1;
+        pw[2 * sk][v] = p0;
+        pw[2 * sk + 1][v] = p1;
+        pa[sk][v] = f16x2{static_cast<_Float16>(p0 * vsc[8 * sk + v]), static_cast<_Float16>(p1 * vsc[8 * sk + v + 4])};
+      }
+    }
+    l_lane = l_lane * alpha + psum;
+    m_run = m_new;
+    if (grp == 0) alpha_s[wave][n16] = alpha;
+    __builtin_amdgcn_wave_barrier();
+    const f32x4 al = *reinterpret_cast<const f32x4*>(&alpha_s[wave][4 * grp]);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] *= al;
+
+    // ---- PV on the matrix cores ----
+    const f16x8 pa0 = __builtin_bit_cast(f16x8, pa[0]);
+    const f16x8 pa1 = __builtin_bit_cast(f16x8, pa[1]);
+    if (!is_f16) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const i32x2 x = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
+            (lds_i32x2*)((lds_u8*)my_vtile + (16 * grp + n16) * kVPitch + 8 * c));
+        f16x2 vb0[4], vb1[4];
+        nib8_to_f16(static_cast<uint32_t>(x[0]), vb0);
+        nib8_to_f16(static_cast<uint32_t>(x[1]), vb1);
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa0, __builtin_bit_cast(f16x8, vb0), acc[c], 0, 0, 0);
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa1, __builtin_bit_cast(f16x8, vb1), acc[c], 0, 0, 0);
+      }
+    } else {
+      // fp16 V in four 16-token chunks through LDS; chunk q = tokens 16g + 4q + i
+      const int64_t f0 = tau * kTileT;
+      uint16_t* vt16 = reinterpret_cast<uint16_t*>(my_vtile);
+#pragma unroll 1
+      for (int q = 0; q < 4; ++q) {
+        __builtin_amdgcn_wave_barrier();
+        {
+          const int r = lane >> 2;  // staged row: g = r/4, i = r%4
+          const int64_t tok = f0 + 16 * (r >> 2) + 4 * q + (r & 3);
+          const uint16_t* src = fp16_token<MID_F16>(p, b, kvh, tok < F ? tok : F - 1).v + 32 * (lane & 3);
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            *reinterpret_cast<uint4*>(vt16 + r * kV16Pitch + 32 * (lane & 3) + 8 * c) = ldg16(src + 8 * c);
+        }
+        __builtin_amdgcn_wave_barrier();
+        const f16x4 pa4 = {static_cast<_Float16>(pw[q][0]), static_cast<_Float16>(pw[q][1]),
+                           static_cast<_Float16>(pw[q][2]), static_cast<_Float16>(pw[q][3])};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const int d = 16 * c + (n16 ^ 1);
+          const f16x4 vb = {__builtin_bit_cast(_Float16, vt16[(4 * grp + 0) * kV16Pitch + d]),
+                            __builtin_bit_cast(_Float16, vt16[(4 * grp + 1) * kV16Pitch + d]),
+                            __builtin_bit_cast(_Float16, vt16[(4 * grp + 2) * kV16Pitch + d]),
+                            __builtin_bit_cast(_Float16, vt16[(4 * grp + 3) * kV16Pitch + d])};
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa4, vb, acc[c], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // ---- merge the four wavefronts, write this split's partial ----
+  float l_tot = l_lane;
+  l_tot += __shfl_xor(l_tot, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  if (grp == 0) {
+    red_m[wave][n16] = m_run;
+    red_l[wave][n16] = l_tot;
+  }
+  __syncthreads();
+  float* red_acc = reinterpret_cast<float*>(&vtile[0][0]);  // [wave][h < G][128]
+  {
+    // scale of each of this lane's accumulator rows (heads 4*grp + i)
+    float wscale[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * grp + i;
+      float Mh = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) Mh = fmaxf(Mh, red_m[w][h]);
+      wscale[i] = (Mh == -INFINITY || red_m[wave][h] == -INFINITY) ? 0.0f : exp2f(red_m[wave][h] - Mh);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int h = 4 * grp + i;
+        if (h < G) red_acc[(wave * G + h) * kD + 16 * c + (n16 ^ 1)] = acc[c][i] * wscale[i];
+      }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < G * kD; idx += kThreads) {
+    const int h = idx / kD, d = idx % kD;
+    float Mh = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) Mh = fmaxf(Mh, red_m[w][h]);
+    float o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) o += red_acc[(w * G + h) * kD + d];
+    const int64_t pidx = (b * p.Hq + kvh * G + h) * p.n_splits + split;
+    p.ws_acc[pidx * kD + d] = o;
+    if (d == 0) {
+      float L = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w)
+        if (red_m[w][h] != -INFINITY) L += red_l[w][h] * exp2f(red_m[w][h] - Mh);
+      p.ws_ml[2 * pidx] = Mh;
+      p.ws_ml[2 * pidx + 1] = L;
+    }
+  }
+}
+
+bool aligned16(const void* x) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0; }
+
+bool fp16_tier_ok(const Fp16Tier& t) {
+  if (t.len == 0) return true;
+  return aligned16(t.k) && aligned16(t.v) && ((t.k_sb | t.k_sh | t.k_ss | t.v_sb | t.v_sh | t.v_ss) % 8 == 0);
+}
+
+}  // namespace
+
+bool mfma_supports(const Params& p) {
+  if (!fp16_tier_ok(p.sink) || !fp16_tier_ok(p.recent)) return false;
+  if (p.G > kMaxG) return false;
+  if (reinterpret_cast<uintptr_t>(p.q) % 16 || p.q_sb % 8 || p.q_sh % 8) return false;
+  switch (p.mid.fmt) {
+    case FADE_MID_NONE:
+      return true;
+    case FADE_MID_FP16:
+      return aligned16(p.mid.k_codes) && aligned16(p.mid.v_codes);
+    case FADE_MID_SYM:
+      return p.mid.k_bits == 4 && p.mid.v_bits == 4 && aligned16(p.mid.k_codes) && aligned16(p.mid.v_codes) &&
+             aligned16(p.mid.k_scale);
+    default:
+      return false;
+  }
+}
+
+int mfma_tile() { return kTileT; }
+
+// Token tiles: fp16 tokens first (sink, [fp16 middle], recent), then packed middle tiles.
+int64_t mfma_tiles(const Params& p) {
+  const bool mid_f16 = p.mid.fmt == FADE_MID_FP16 || p.mid.fmt == FADE_MID_NONE;
+  const int64_t M = mid_f16 ? 0 : p.mid.len;
+  return cdiv(p.total - M, kTileT) + cdiv(M, kTileT);
+}
+
+int launch_mfma(const Params& p, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv), static_cast<unsigned>(p.B));
+  if (p.mid.fmt == FADE_MID_FP16 || p.mid.fmt == FADE_MID_NONE)
+    hipLaunchKernelGGL(decode_mfma_kernel<true>, grid, dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL(decode_mfma_kernel<false>, grid, dim3(kThreads), 0, st, p);
+  return check_launch("fade_tiered_decode_attn(mfma)");
+}
 
 }  // namespace decode
 }  // namespace fade

@@ -142,7 +142,7 @@ def test_fused_int4_sdpa_api_and_parity_helper(dev):
     vq, vs = oq.quant_v_int4(v)
     t = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
     out = fused_int4_sdpa(t(q), t(kq), t(ks), t(vq), t(vs))
-    ref = oatt.tiered_decode(q, None, {"fmt": "int4", "kq": kq, "ks": ks, "vq": vq, "vs": vs}, None, None)
+    ref = oatt.tiered_decode(q, None, None, {"fmt": "int4", "kq": kq, "ks": ks, "vq": vq, "vs": vs}, None, None)
     assert out.shape == (2, 8, 1, 128) and out.dtype == torch.float16
     assert np.abs(out.float().cpu().numpy() - ref).max() <= ATOL
 
