@@ -9,13 +9,16 @@ namespace {
 
 int64_t total_tokens(const fade_decode_args* a) { return a->sink.len + a->mid.len + a->recent.len; }
 
-// Split the token range so that B*Hkv*n_splits workgroups cover the 256 CUs
-// several times over, in multiples of the kernel's token tile.
+// Split the token range into n_splits pieces (multiples of the kernel's token
+// tile) so that B*Hkv*n_splits workgroups fill the 256 CUs: the matrix-core
+// kernel runs two 4-wave workgroups per CU, so ~512 workgroups is one full
+// wave of the machine (measured best for configs 1 and 2); the portable
+// kernel wants more, smaller workgroups.
 void plan_splits(const fade_decode_args* a, int tile, int64_t* n_splits, int64_t* tps,
-                 int64_t total_override = -1) {
+                 int64_t total_override = -1, int64_t target_wgs = 2048) {
   const int64_t total = total_override >= 0 ? total_override : total_tokens(a);
   const int64_t pairs = a->B * a->Hkv;
-  int64_t want = a->n_splits > 0 ? a->n_splits : cdiv(2048, pairs > 0 ? pairs : 1);
+  int64_t want = a->n_splits > 0 ? a->n_splits : (target_wgs + pairs / 2) / (pairs > 0 ? pairs : 1);
   const int64_t max_splits = cdiv(total, tile) > 0 ? cdiv(total, tile) : 1;
   if (want > max_splits) want = max_splits;
   if (want < 1) want = 1;
@@ -135,7 +138,7 @@ FADE_API int fade_tiered_decode_workspace_bytes(const fade_decode_args* a, int64
   const Params p = to_params(a);
   const bool mfma = use_mfma(a, p);
   int64_t n, tps;
-  plan_splits(a, mfma ? mfma_tile() : 64, &n, &tps, mfma ? mfma_tiles(p) * mfma_tile() : -1);
+  plan_splits(a, mfma ? mfma_tile() : 64, &n, &tps, mfma ? mfma_tiles(p) * mfma_tile() : -1, mfma ? 512 : 2048);
   *bytes = ml_bytes(a, n) + a->B * a->Hq * n * kD * 4;
   return FADE_OK;
 }
@@ -148,7 +151,7 @@ FADE_API int fade_tiered_decode_attn(const fade_decode_args* a, void* stream) {
   if (a->kernel == 2 && !mfma)
     return einval("fade_tiered_decode_attn: the matrix-core kernel does not handle middle format %d", p.mid.fmt);
   int64_t n, tps;
-  plan_splits(a, mfma ? mfma_tile() : 64, &n, &tps, mfma ? mfma_tiles(p) * mfma_tile() : -1);
+  plan_splits(a, mfma ? mfma_tile() : 64, &n, &tps, mfma ? mfma_tiles(p) * mfma_tile() : -1, mfma ? 512 : 2048);
   const int64_t need = ml_bytes(a, n) + a->B * a->Hq * n * kD * 4;
   if (a->workspace == nullptr || a->workspace_bytes < need)
     return einval("fade_tiered_decode_attn: workspace too small (%lld < %lld bytes)",

@@ -47,6 +47,7 @@ constexpr int kWaves = 4;
 constexpr int kTileT = 64;
 constexpr int kVPitch = 80;  // LDS bytes per staged V row: 64 data + 16 pad (conflict-free tr4)
 constexpr float kQMax = 32000.0f;
+constexpr float kNegBig = -1.0e30f;  // running-max sentinel (finite: no inf-inf guards)
 constexpr int kV16Pitch = 136;  // halfs per staged fp16 V row (16 rows = 4352 B fit the V tile buffer)
 
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
@@ -62,12 +63,16 @@ __device__ __forceinline__ void nib_to_u8(uint32_t w, uint32_t& lo, uint32_t& hi
   hi = (x >> 4) & 0x0F0F0F0Fu;
 }
 
-// fp16 pairs (nibble v, nibble v+4) of 8 two's-complement codes, v = 0..3.
-__device__ __forceinline__ void nib8_to_f16(uint32_t w, f16x2* out) {
-  const uint32_t x = w ^ 0x88888888u;
-  const f16x2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-#pragma unroll
-  for (int v = 0; v < 4; ++v) out[v] = u2h2(((x >> (4 * v)) & 0x000F000Fu) | 0x64006400u) + bias;
+// fp16 pairs (nibble v, nibble v+4), v = 0..3, of 8 two's-complement codes c,
+// as the values 48 + 2c: the nibble moves to mantissa bits 6..9 of 32.0
+// (0x5000, ulp 1/32, so one code step is 2.0) and bit 3 is flipped
+// (c + 8 = offset binary).  Two bit ops per pair; the constant 48 per token
+// is removed once at the end with an MFMA-accumulated sum of P.
+__device__ __forceinline__ void nib8_to_f16(uint32_t w, uint32_t* out) {
+  out[0] = ((w << 6) & 0x03C003C0u) ^ 0x52005200u;
+  out[1] = ((w << 2) & 0x03C003C0u) ^ 0x52005200u;
+  out[2] = ((w >> 2) & 0x03C003C0u) ^ 0x52005200u;
+  out[3] = ((w >> 6) & 0x03C003C0u) ^ 0x52005200u;
 }
 
 struct FpTok {  // one fp16 token row (K and V pointers)
@@ -203,36 +208,156 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   const int64_t t1 = t0 + tiles_per_split < nT ? t0 + tiles_per_split : nT;
 
   __syncthreads();
-  float m_run = -INFINITY, l_lane = 0.0f;
+  // acc holds 2 * sum(P V) + 48 * sum_{packed tiles}(P'), acc48 the 48 * sum(P') part.
+  float m_run = kNegBig, l_lane = 0.0f;
   f32x4 acc[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) acc[c] = f32x4{0, 0, 0, 0};
+  f32x4 acc48 = {0, 0, 0, 0};
 
   uint8_t* my_vtile = vtile[wave];
-  for (int64_t tau = t0 + wave; tau < t1; tau += kWaves) {
-    float s[4][4];
-    float vsc[16];  // V scale of tokens 16*grp + 0..15 (1 for fp16 tiles)
-    bool is_f16 = tau < nF;
-    __builtin_amdgcn_wave_barrier();
-    if (!is_f16) {
-      // -------------------------------------------------- packed INT4 tile
-      const int64_t m0 = (tau - nF) * kTileT;
-      const uint8_t* kc = p.mid.k_codes + bkv * M * 64;
-      const uint8_t* vc = p.mid.v_codes + bkv * M * 64;
-      // stage V codes (rows 16k + lane/4, 16-byte chunk lane%4) and V scales
+
+  // Online-softmax update of head n16 with the 64 scores s of one tile; P
+  // (times the V scale) leaves as the two PV A operands, plain P in pw.
+  // Online-softmax update of head n16 with the 64 scores of one tile.  P
+  // times pscale[token] leaves as the two PV A operands (fp16), plain P in pw.
+  // Accumulators are rescaled only when some head's running max rises.
+  auto softmax_tile = [&](float (&sc)[4][4], const float* pscale, float (&pw)[4][4], f16x8& pa0, f16x8& pa1) {
+    float tmax = sc[0][0];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int r = 16 * k + (lane >> 2);
-        const int64_t row = m0 + r < M ? m0 + r : M - 1;
-        *reinterpret_cast<uint4*>(my_vtile + r * kVPitch + 16 * (lane & 3)) = ldg16(vc + row * 64 + 16 * (lane & 3));
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[j][i]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run) != 0) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_lane *= alpha;
+      m_run = m_new;
+      if (grp == 0) alpha_s[wave][n16] = alpha;
+      __builtin_amdgcn_wave_barrier();
+      const f32x4 al = *reinterpret_cast<const f32x4*>(&alpha_s[wave][4 * grp]);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[c] *= al;
+      acc48 *= al;
+    }
+    float psum = 0.0f;
+    f16x2 pa[2][4];  // k-step s, VGPR v = tokens (16g+8s+v, 16g+8s+v+4)
+#pragma unroll
+    for (int sk = 0; sk < 2; ++sk) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float p0 = __builtin_amdgcn_exp2f(sc[2 * sk][v] - m_run);
+        const float p1 = __builtin_amdgcn_exp2f(sc[2 * sk + 1][v] - m_run);
+        psum += p0 + p1;
+        pw[2 * sk][v] = p0;
+        pw[2 * sk + 1][v] = p1;
+        pa[sk][v] = f16x2{static_cast<_Float16>(p0 * pscale[8 * sk + v]), static_cast<_Float16>(p1 * pscale[8 * sk + v + 4])};
       }
-      vs_s[wave][lane] = m0 + lane < M ? p.mid.v_scale[bkv * M + m0 + lane] : static_cast<uint16_t>(0);
-      // QK^T on the matrix cores
+    }
+    l_lane += psum;
+    pa0 = __builtin_bit_cast(f16x8, pa[0]);
+    pa1 = __builtin_bit_cast(f16x8, pa[1]);
+  };
+
+  // -------------------------------------------------------------- fp16 tiles
+  const int64_t f_end = t1 < nF ? t1 : nF;
+  for (int64_t tau = t0 + wave; tau < f_end; tau += kWaves) {
+    float sc[4][4], pw[4][4], vsc[16];
+    const int64_t f0 = tau * kTileT;
+#pragma unroll 1
+    for (int j = 0; j < 4; ++j) {
+      const int rloc = 16 * (n16 >> 2) + 4 * j + (n16 & 3);
+      const int64_t f = f0 + rloc < F ? f0 + rloc : F - 1;
+      const uint16_t* kr = fp16_token<MID_F16>(p, b, kvh, f).k + 32 * grp;
+      f32x4 c4 = {0, 0, 0, 0};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const f16x8 qb = *reinterpret_cast<const f16x8*>(&q16_s[n16][32 * grp + 8 * ks]);
+        c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ldg16(kr + 8 * ks)), qb, c4, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t tok = f0 + 16 * grp + 4 * j + i;
+        sc[j][i] = tok < F ? c4[i] * p.scale_log2 : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) vsc[k] = 2.0f;
+    f16x8 pa0, pa1;
+    softmax_tile(sc, vsc, pw, pa0, pa1);
+    // fp16 V in four 16-token chunks through LDS; chunk q = tokens 16g + 4q + i
+    uint16_t* vt16 = reinterpret_cast<uint16_t*>(my_vtile);
+#pragma unroll 1
+    for (int q = 0; q < 4; ++q) {
+      __builtin_amdgcn_wave_barrier();
+      {
+        const int r = lane >> 2;  // staged row: g = r/4, i = r%4
+        const int64_t tok = f0 + 16 * (r >> 2) + 4 * q + (r & 3);
+        const uint16_t* src = fp16_token<MID_F16>(p, b, kvh, tok < F ? tok : F - 1).v + 32 * (lane & 3);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          *reinterpret_cast<uint4*>(vt16 + r * kV16Pitch + 32 * (lane & 3) + 8 * c) = ldg16(src + 8 * c);
+      }
+      __builtin_amdgcn_wave_barrier();
+      const f16x4 pa4 = {static_cast<_Float16>(2.0f * pw[q][0]), static_cast<_Float16>(2.0f * pw[q][1]),
+                         static_cast<_Float16>(2.0f * pw[q][2]), static_cast<_Float16>(2.0f * pw[q][3])};
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int d = 16 * c + (n16 ^ 1);
+        const f16x4 vb = {__builtin_bit_cast(_Float16, vt16[(4 * grp + 0) * kV16Pitch + d]),
+                          __builtin_bit_cast(_Float16, vt16[(4 * grp + 1) * kV16Pitch + d]),
+                          __builtin_bit_cast(_Float16, vt16[(4 * grp + 2) * kV16Pitch + d]),
+                          __builtin_bit_cast(_Float16, vt16[(4 * grp + 3) * kV16Pitch + d])};
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa4, vb, acc[c], 0, 0, 0);
+      }
+    }
+  }
+
+  // ------------------------------------------ packed INT4 tiles, pipelined
+  // The next tile's K codes, V codes and V scales are loaded into registers
+  // while the current tile is on the matrix cores.
+  int64_t tau = t0 + wave;
+  if (tau < nF) tau += ((nF - tau + kWaves - 1) / kWaves) * kWaves;
+  if (!MID_F16 && tau < t1) {
+    const uint8_t* kc = p.mid.k_codes + bkv * M * 64;
+    const uint8_t* vc = p.mid.v_codes + bkv * M * 64;
+    const uint16_t* vsg = p.mid.v_scale + bkv * M;
+    uint4 kq[4], vq[4];
+    uint16_t vsv;
+    auto load_tile = [&](int64_t t, uint4 (&kr)[4], uint4 (&vr)[4], uint16_t& vs1) {
+      const int64_t m0 = (t - nF) * kTileT;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int rloc = 16 * (n16 >> 2) + 4 * j + (n16 & 3);
         const int64_t row = m0 + rloc < M ? m0 + rloc : M - 1;
-        const uint4 w = ldg16(kc + row * 64 + 16 * grp);
+        kr[j] = ldg16(kc + row * 64 + 16 * grp);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = 16 * k + (lane >> 2);
+        const int64_t row = m0 + r < M ? m0 + r : M - 1;
+        vr[k] = ldg16(vc + row * 64 + 16 * (lane & 3));
+      }
+      vs1 = m0 + lane < M ? vsg[m0 + lane] : static_cast<uint16_t>(0);
+    };
+    load_tile(tau, kq, vq, vsv);
+    for (; tau < t1; tau += kWaves) {
+      const int64_t m0 = (tau - nF) * kTileT;
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        *reinterpret_cast<uint4*>(my_vtile + (16 * k + (lane >> 2)) * kVPitch + 16 * (lane & 3)) = vq[k];
+      vs_s[wave][lane] = vsv;
+      uint4 kn[4], vn[4];
+      uint16_t vsn = 0;
+      const int64_t nxt = tau + kWaves;
+      if (nxt < t1) load_tile(nxt, kn, vn, vsn);
+      float sc[4][4], pw[4][4], vsc[16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 w = kq[j];
         uint32_t lo0, hi0, lo1, hi1, lo2, hi2, lo3, hi3;
         nib_to_u8(w.x, lo0, hi0);
         nib_to_u8(w.y, lo1, hi1);
@@ -246,114 +371,51 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
         clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qd_lo[0], clo, 0, 0, 0);
         clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, qd_lo[1], clo, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int64_t tok = m0 + 16 * grp + 4 * j + i;
-          const int si = chi[i] * 256 + clo[i] - corr;
-          s[j][i] = tok < M ? static_cast<float>(si) * qscale : -INFINITY;
-        }
+        for (int i = 0; i < 4; ++i) sc[j][i] = static_cast<float>(chi[i] * 256 + clo[i] - corr) * qscale;
+      }
+      if (m0 + kTileT > M) {  // partial last tile: mask tokens past the middle tier
+        const int valid = static_cast<int>(M - m0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (16 * grp + 4 * j + i >= valid) sc[j][i] = -INFINITY;
       }
       __builtin_amdgcn_wave_barrier();
+      {
+        const uint4 v0 = *reinterpret_cast<const uint4*>(&vs_s[wave][16 * grp]);
+        const uint4 v1 = *reinterpret_cast<const uint4*>(&vs_s[wave][16 * grp + 8]);
+        const uint32_t u[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-      for (int k = 0; k < 16; ++k) vsc[k] = h2f(vs_s[wave][16 * grp + k]);
-    } else {
-      // -------------------------------------------------- fp16 tile
-      const int64_t f0 = tau * kTileT;
-#pragma unroll 1
-      for (int j = 0; j < 4; ++j) {
-        const int rloc = 16 * (n16 >> 2) + 4 * j + (n16 & 3);
-        const int64_t f = f0 + rloc < F ? f0 + rloc : F - 1;
-        const uint16_t* kr = fp16_token<MID_F16>(p, b, kvh, f).k + 32 * grp;
-        f32x4 c4 = {0, 0, 0, 0};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const f16x8 qb = *reinterpret_cast<const f16x8*>(&q16_s[n16][32 * grp + 8 * ks]);
-          c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ldg16(kr + 8 * ks)), qb, c4, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int64_t tok = f0 + 16 * grp + 4 * j + i;
-          s[j][i] = tok < F ? c4[i] * p.scale_log2 : -INFINITY;
+        for (int k = 0; k < 8; ++k) {
+          vsc[2 * k] = h2f(static_cast<uint16_t>(u[k] & 0xFFFFu));
+          vsc[2 * k + 1] = h2f(static_cast<uint16_t>(u[k] >> 16));
         }
       }
-#pragma unroll
-      for (int k = 0; k < 16; ++k) vsc[k] = 1.0f;
-    }
-
-    // ---- online softmax for head n16 over the tile's 64 tokens ----
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[j][i]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
-    float psum = 0.0f;
-    float pw[4][4];
-    f16x2 pa[2][4];  // A operand of PV: k-step s, VGPR v = tokens (16g+8s+v, 16g+8s+v+4)
-#pragma unroll
-    for (int sk = 0; sk < 2; ++sk) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float p0 = m_new == -INFINITY ? 0.0f : exp2f(s[2 * sk][v] - m_new);
-        const float p1 = m_new == -INFINITY ? 0.0f : exp2f(s[2 * sk + 1][v] - m_new);
-        psum += p0 + p1;
-        pw[2 * sk][v] = p0;
-        pw[2 * sk + 1][v] = p1;
-        pa[sk][v] = f16x2{static_cast<_Float16>(p0 * vsc[8 * sk + v]), static_cast<_Float16>(p1 * vsc[8 * sk + v + 4])};
-      }
-    }
-    l_lane = l_lane * alpha + psum;
-    m_run = m_new;
-    if (grp == 0) alpha_s[wave][n16] = alpha;
-    __builtin_amdgcn_wave_barrier();
-    const f32x4 al = *reinterpret_cast<const f32x4*>(&alpha_s[wave][4 * grp]);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) acc[c] *= al;
-
-    // ---- PV on the matrix cores ----
-    const f16x8 pa0 = __builtin_bit_cast(f16x8, pa[0]);
-    const f16x8 pa1 = __builtin_bit_cast(f16x8, pa[1]);
-    if (!is_f16) {
+      f16x8 pa0, pa1;
+      softmax_tile(sc, vsc, pw, pa0, pa1);
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         const i32x2 x = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
             (lds_i32x2*)((lds_u8*)my_vtile + (16 * grp + n16) * kVPitch + 8 * c));
-        f16x2 vb0[4], vb1[4];
+        uint32_t vb0[4], vb1[4];
         nib8_to_f16(static_cast<uint32_t>(x[0]), vb0);
         nib8_to_f16(static_cast<uint32_t>(x[1]), vb1);
         acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa0, __builtin_bit_cast(f16x8, vb0), acc[c], 0, 0, 0);
         acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa1, __builtin_bit_cast(f16x8, vb1), acc[c], 0, 0, 0);
       }
-    } else {
-      // fp16 V in four 16-token chunks through LDS; chunk q = tokens 16g + 4q + i
-      const int64_t f0 = tau * kTileT;
-      uint16_t* vt16 = reinterpret_cast<uint16_t*>(my_vtile);
-#pragma unroll 1
-      for (int q = 0; q < 4; ++q) {
-        __builtin_amdgcn_wave_barrier();
-        {
-          const int r = lane >> 2;  // staged row: g = r/4, i = r%4
-          const int64_t tok = f0 + 16 * (r >> 2) + 4 * q + (r & 3);
-          const uint16_t* src = fp16_token<MID_F16>(p, b, kvh, tok < F ? tok : F - 1).v + 32 * (lane & 3);
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            *reinterpret_cast<uint4*>(vt16 + r * kV16Pitch + 32 * (lane & 3) + 8 * c) = ldg16(src + 8 * c);
-        }
-        __builtin_amdgcn_wave_barrier();
-        const f16x4 pa4 = {static_cast<_Float16>(pw[q][0]), static_cast<_Float16>(pw[q][1]),
-                           static_cast<_Float16>(pw[q][2]), static_cast<_Float16>(pw[q][3])};
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const int d = 16 * c + (n16 ^ 1);
-          const f16x4 vb = {__builtin_bit_cast(_Float16, vt16[(4 * grp + 0) * kV16Pitch + d]),
-                            __builtin_bit_cast(_Float16, vt16[(4 * grp + 1) * kV16Pitch + d]),
-                            __builtin_bit_cast(_Float16, vt16[(4 * grp + 2) * kV16Pitch + d]),
-                            __builtin_bit_cast(_Float16, vt16[(4 * grp + 3) * kV16Pitch + d])};
-          acc[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa4, vb, acc[c], 0, 0, 0);
-        }
+      {  // 48 * sum(P') per head, accumulated exactly like acc
+        const _Float16 h48 = static_cast<_Float16>(48.0f);
+        const f16x8 b48 = {h48, h48, h48, h48, h48, h48, h48, h48};
+        acc48 = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa0, b48, acc48, 0, 0, 0);
+        acc48 = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa1, b48, acc48, 0, 0, 0);
       }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        kq[k] = kn[k];
+        vq[k] = vn[k];
+      }
+      vsv = vsn;
     }
   }
 
@@ -376,14 +438,14 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       float Mh = -INFINITY;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) Mh = fmaxf(Mh, red_m[w][h]);
-      wscale[i] = (Mh == -INFINITY || red_m[wave][h] == -INFINITY) ? 0.0f : exp2f(red_m[wave][h] - Mh);
+      wscale[i] = 0.5f * exp2f(red_m[wave][h] - Mh);
     }
 #pragma unroll
     for (int c = 0; c < 8; ++c)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int h = 4 * grp + i;
-        if (h < G) red_acc[(wave * G + h) * kD + 16 * c + (n16 ^ 1)] = acc[c][i] * wscale[i];
+        if (h < G) red_acc[(wave * G + h) * kD + 16 * c + (n16 ^ 1)] = (acc[c][i] - acc48[i]) * wscale[i];
       }
   }
   __syncthreads();
@@ -400,8 +462,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
     if (d == 0) {
       float L = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w)
-        if (red_m[w][h] != -INFINITY) L += red_l[w][h] * exp2f(red_m[w][h] - Mh);
+      for (int w = 0; w < kWaves; ++w) L += red_l[w][h] * exp2f(red_m[w][h] - Mh);
       p.ws_ml[2 * pidx] = Mh;
       p.ws_ml[2 * pidx + 1] = L;
     }
