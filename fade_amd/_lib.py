@@ -15,7 +15,9 @@ import threading
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libfade_hip.so")
+# FADE_HIP_LIB points at an alternative build of the same library (e.g. an
+# installed copy); the default is the in-tree build.
+LIB_PATH = os.environ.get("FADE_HIP_LIB") or os.path.join(_HERE, "libfade_hip.so")
 
 FADE_OK = 0
 FADE_ERUNTIME = -1

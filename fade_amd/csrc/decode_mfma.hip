@@ -45,12 +45,27 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8;
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kTileT = 64;
-constexpr int kVPitch = 80;  // LDS bytes per staged V row: 64 data + 16 pad (conflict-free tr4)
+constexpr int kStages = 2;
+constexpr int kStageK = 0, kStageV = 4096, kStageVS = 8192;
+constexpr int kStageBytes = 8192 + 256;  // the 2-byte DMA writes one dword per lane
 constexpr float kQMax = 32000.0f;
 constexpr float kNegBig = -1.0e30f;  // running-max sentinel (finite: no inf-inf guards)
 constexpr int kV16Pitch = 136;  // halfs per staged fp16 V row (16 rows = 4352 B fit the V tile buffer)
 
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Direct HBM -> LDS load per lane: 16 bytes land at lds_base + 16*i; a 2-byte
+// load lands zero-extended in the dword at lds_base + 4*i.  Issued as inline asm so that the only waits on these
+// loads are the explicit per-stage s_waitcnt vmcnt of the packed-tile loop
+// (the compiler cannot tell two ring stages apart and would wait for both).
+// Register-destination loads stay correct: any wait the compiler emits for
+// them also covers older LDS loads and at worst over-waits for newer ones.
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma2(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_ushort %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
+}
 
 __device__ __forceinline__ f16x2 u2h2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
 __device__ __forceinline__ uint32_t h22u(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
@@ -109,7 +124,8 @@ template <bool MID_F16>
 __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   const int split = blockIdx.x;
   const int64_t kvh = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, grp = lane >> 4;
   const int G = p.G;
   const int64_t bkv = b * p.Hkv + kvh;
@@ -117,8 +133,10 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   const int64_t F = p.total - M;                               // fp16 tokens
   const int64_t nF = (F + kTileT - 1) / kTileT;
 
-  __shared__ __attribute__((aligned(16))) uint8_t vtile[kWaves][kTileT * kVPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t vs_s[kWaves][kTileT];
+  // Per-wave ring of kStages stages; a stage holds one packed tile:
+  // K codes (4 KB) | V codes (4 KB) | V scales (64 dwords), swizzled 16-byte units.
+  __shared__ __attribute__((aligned(16))) uint8_t ring0[kWaves][kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t ring1[kWaves][kStageBytes];
   __shared__ __attribute__((aligned(16))) float alpha_s[kWaves][16];
   __shared__ float red_m[kWaves][16], red_l[kWaves][16];
   __shared__ __attribute__((aligned(16))) uint16_t q16_s[16][kD + 8];
@@ -215,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   for (int c = 0; c < 8; ++c) acc[c] = f32x4{0, 0, 0, 0};
   f32x4 acc48 = {0, 0, 0, 0};
 
-  uint8_t* my_vtile = vtile[wave];
+  uint8_t* my_vtile = ring0[wave];  // fp16 tiles stage V chunks here (before the packed ring starts)
 
   // Online-softmax update of head n16 with the 64 scores s of one tile; P
   // (times the V scale) leaves as the two PV A operands, plain P in pw.
@@ -316,48 +334,49 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   }
 
   // ------------------------------------------ packed INT4 tiles, pipelined
-  // The next tile's K codes, V codes and V scales are loaded into registers
-  // while the current tile is on the matrix cores.
+  // Tile codes and scales move HBM -> LDS with direct global_load_lds
+  // (16 bytes per lane, no VGPRs), kStages tiles ahead of the math.
+  // 16-byte units are swizzled so the K-operand reads (16 lanes = 16 rows,
+  // one chunk) and the tr4 V reads (16 consecutive rows, one 8-byte half)
+  // hit 16 different bank groups:
+  //   K unit (row r, chunk q) at 4r + (q ^ ((r >> 4) & 3))
+  //   V unit (row r, chunk q) at 4r + (q ^ ((r >> 2) & 3))
   int64_t tau = t0 + wave;
   if (tau < nF) tau += ((nF - tau + kWaves - 1) / kWaves) * kWaves;
   if (!MID_F16 && tau < t1) {
     const uint8_t* kc = p.mid.k_codes + bkv * M * 64;
     const uint8_t* vc = p.mid.v_codes + bkv * M * 64;
     const uint16_t* vsg = p.mid.v_scale + bkv * M;
-    uint4 kq[4], vq[4];
-    uint16_t vsv;
-    auto load_tile = [&](int64_t t, uint4 (&kr)[4], uint4 (&vr)[4], uint16_t& vs1) {
+    auto issue = [&](int64_t t, uint32_t st) {
       const int64_t m0 = (t - nF) * kTileT;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int rloc = 16 * (n16 >> 2) + 4 * j + (n16 & 3);
-        const int64_t row = m0 + rloc < M ? m0 + rloc : M - 1;
-        kr[j] = ldg16(kc + row * 64 + 16 * grp);
-      }
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int r = 16 * k + (lane >> 2);
         const int64_t row = m0 + r < M ? m0 + r : M - 1;
-        vr[k] = ldg16(vc + row * 64 + 16 * (lane & 3));
+        const int qk = (lane & 3) ^ k;
+        lds_dma16(kc + row * 64 + 16 * qk, st + kStageK + 1024 * k);
+        const int qv = (lane & 3) ^ ((lane >> 4) & 3);
+        lds_dma16(vc + row * 64 + 16 * qv, st + kStageV + 1024 * k);
       }
-      vs1 = m0 + lane < M ? vsg[m0 + lane] : static_cast<uint16_t>(0);
+      const int64_t vrow = m0 + lane < M ? m0 + lane : M - 1;
+      lds_dma2(vsg + vrow, st + kStageVS);
     };
-    load_tile(tau, kq, vq, vsv);
-    for (; tau < t1; tau += kWaves) {
-      const int64_t m0 = (tau - nF) * kTileT;
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        *reinterpret_cast<uint4*>(my_vtile + (16 * k + (lane >> 2)) * kVPitch + 16 * (lane & 3)) = vq[k];
-      vs_s[wave][lane] = vsv;
-      uint4 kn[4], vn[4];
-      uint16_t vsn = 0;
-      const int64_t nxt = tau + kWaves;
-      if (nxt < t1) load_tile(nxt, kn, vn, vsn);
+    constexpr int kOpsPerStage = 9;
+    // vmcnt operand of s_waitcnt with expcnt / lgkmcnt left unconstrained
+    auto wait_vm = [](bool keep_one_stage) {
+      if (keep_one_stage) __builtin_amdgcn_s_waitcnt((kOpsPerStage & 15) | (7 << 4) | (15 << 8));
+      else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+    };
+    // One packed tile from stage buffer st (a distinct __shared__ array per
+    // stage, so the compiler's LDS-DMA waits stay per stage).
+    auto compute = [&](int64_t t, const uint8_t* st, lds_u8* st_lds) {
+      const int64_t m0 = (t - nF) * kTileT;
       float sc[4][4], pw[4][4], vsc[16];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint4 w = kq[j];
+        const int rloc = 16 * (n16 >> 2) + 4 * j + (n16 & 3);
+        const int unit = 4 * rloc + (grp ^ ((rloc >> 4) & 3));
+        const uint4 w = *reinterpret_cast<const uint4*>(st + kStageK + 16 * unit);
         uint32_t lo0, hi0, lo1, hi1, lo2, hi2, lo3, hi3;
         nib_to_u8(w.x, lo0, hi0);
         nib_to_u8(w.y, lo1, hi1);
@@ -381,23 +400,23 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
           for (int i = 0; i < 4; ++i)
             if (16 * grp + 4 * j + i >= valid) sc[j][i] = -INFINITY;
       }
-      __builtin_amdgcn_wave_barrier();
-      {
-        const uint4 v0 = *reinterpret_cast<const uint4*>(&vs_s[wave][16 * grp]);
-        const uint4 v1 = *reinterpret_cast<const uint4*>(&vs_s[wave][16 * grp + 8]);
-        const uint32_t u[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+      {  // V scale of token k sits in the low half of dword k
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          vsc[2 * k] = h2f(static_cast<uint16_t>(u[k] & 0xFFFFu));
-          vsc[2 * k + 1] = h2f(static_cast<uint16_t>(u[k] >> 16));
+        for (int c = 0; c < 4; ++c) {
+          const uint4 v = *reinterpret_cast<const uint4*>(st + kStageVS + 64 * grp + 16 * c);
+          vsc[4 * c + 0] = h2f(static_cast<uint16_t>(v.x & 0xFFFFu));
+          vsc[4 * c + 1] = h2f(static_cast<uint16_t>(v.y & 0xFFFFu));
+          vsc[4 * c + 2] = h2f(static_cast<uint16_t>(v.z & 0xFFFFu));
+          vsc[4 * c + 3] = h2f(static_cast<uint16_t>(v.w & 0xFFFFu));
         }
       }
       f16x8 pa0, pa1;
       softmax_tile(sc, vsc, pw, pa0, pa1);
+      const int vrow = 16 * grp + n16;
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const i32x2 x = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
-            (lds_i32x2*)((lds_u8*)my_vtile + (16 * grp + n16) * kVPitch + 8 * c));
+        const int unit = 4 * vrow + ((c >> 1) ^ ((vrow >> 2) & 3));
+        const i32x2 x = __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2*)(st_lds + kStageV + 16 * unit + 8 * (c & 1)));
         uint32_t vb0[4], vb1[4];
         nib8_to_f16(static_cast<uint32_t>(x[0]), vb0);
         nib8_to_f16(static_cast<uint32_t>(x[1]), vb1);
@@ -410,12 +429,28 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
         acc48 = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa0, b48, acc48, 0, 0, 0);
         acc48 = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa1, b48, acc48, 0, 0, 0);
       }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        kq[k] = kn[k];
-        vq[k] = vn[k];
-      }
-      vsv = vsn;
+      // every LDS read of this stage has returned before it is refilled
+      __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4));
+      __builtin_amdgcn_wave_barrier();
+    };
+    lds_u8* st0 = (lds_u8*)&ring0[wave][0];
+    lds_u8* st1 = (lds_u8*)&ring1[wave][0];
+    const uint32_t a0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(st0)));
+    const uint32_t a1 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(st1)));
+    issue(tau, a0);
+    if (tau + kWaves < t1) issue(tau + kWaves, a1);
+    while (tau < t1) {
+      wait_vm(tau + kWaves < t1);
+      __builtin_amdgcn_wave_barrier();
+      compute(tau, &ring0[wave][0], st0);
+      if (tau + 2 * kWaves < t1) issue(tau + 2 * kWaves, a0);
+      tau += kWaves;
+      if (tau >= t1) break;
+      wait_vm(tau + kWaves < t1);
+      __builtin_amdgcn_wave_barrier();
+      compute(tau, &ring1[wave][0], st1);
+      if (tau + 2 * kWaves < t1) issue(tau + 2 * kWaves, a1);
+      tau += kWaves;
     }
   }
 
@@ -428,7 +463,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
     red_l[wave][n16] = l_tot;
   }
   __syncthreads();
-  float* red_acc = reinterpret_cast<float*>(&vtile[0][0]);  // [wave][h < G][128]
+  float* red_acc = reinterpret_cast<float*>(&ring0[0][0]);  // [wave][h < G][128] (spans ring0, ring1)
   {
     // scale of each of this lane's accumulator rows (heads 4*grp + i)
     float wscale[4];
