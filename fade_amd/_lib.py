@@ -194,4 +194,5 @@ def require_f16(t: torch.Tensor, op: str) -> None:
 
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
-    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+    """Scratch for one kernel family; zero-filled (the decode split counters start at zero)."""
+    return torch.zeros(max(int(nbytes), 1), dtype=torch.uint8, device=device)

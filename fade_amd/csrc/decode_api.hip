@@ -28,8 +28,21 @@ void plan_splits(const fade_decode_args* a, int tile, int64_t* n_splits, int64_t
   *n_splits = cdiv(total, t) > 0 ? cdiv(total, t) : 1;
 }
 
-int64_t ml_bytes(const fade_decode_args* a, int64_t n) {
-  return ((a->B * a->Hq * n * 2 * 4 + 255) / 256) * 256;
+int64_t round256(int64_t x) { return ((x + 255) / 256) * 256; }
+
+// Workspace: [counters: B*Hkv u32][ml: rows*n*2 f32][acc: rows*n*kD f32], rows
+// covering both partial layouts (B*Hq per query head, or B*Hkv*4).
+struct WsLayout {
+  int64_t counters, ml, acc, total;
+};
+WsLayout ws_layout(const fade_decode_args* a, int64_t n) {
+  const int64_t rows = a->B * (a->Hq > a->Hkv * 4 ? a->Hq : a->Hkv * 4);
+  WsLayout w;
+  w.counters = 0;
+  w.ml = round256(a->B * a->Hkv * 4);
+  w.acc = w.ml + round256(rows * n * 2 * 4);
+  w.total = w.acc + rows * n * kD * 4;
+  return w;
 }
 
 int validate(const fade_decode_args* a) {
@@ -82,7 +95,7 @@ int validate(const fade_decode_args* a) {
         return einval("fade_tiered_decode_attn: unknown middle format %d", m.fmt);
     }
   }
-  if (a->kernel < 0 || a->kernel > 2) return einval("fade_tiered_decode_attn: kernel must be 0, 1 or 2");
+  if (a->kernel < 0 || a->kernel > 3) return einval("fade_tiered_decode_attn: kernel must be 0, 1, 2 or 3");
   return FADE_OK;
 }
 
@@ -124,9 +137,43 @@ Params to_params(const fade_decode_args* a) {
   return p;
 }
 
-bool use_mfma(const fade_decode_args* a, const Params& p) {
-  if (a->kernel == 1) return false;
-  return mfma_supports(p);
+enum class Kern { kValu, kMfma, kInt4 };
+
+// kernel: 0 auto, 1 portable VALU, 2 matrix-core (INT4 kernel when it applies),
+// 3 the general matrix-core kernel.
+Kern choose(const fade_decode_args* a, const Params& p) {
+  if (a->kernel == 1) return Kern::kValu;
+  if (a->kernel != 3 && int4_supports(p)) return Kern::kInt4;
+  if (mfma_supports(p)) return Kern::kMfma;
+  return Kern::kValu;
+}
+
+struct Plan {
+  Kern k;
+  int64_t n, tps, n_f16_tiles, tiles_per_split;
+};
+
+Plan make_plan(const fade_decode_args* a, const Params& p) {
+  Plan pl{};
+  pl.k = choose(a, p);
+  if (pl.k == Kern::kInt4) {
+    // One machine-wide wave of resident workgroups; tiles of either kind cost
+    // about the same bytes (8 KB), so splits take equal tile counts.
+    const int64_t nT = int4_tiles(p);
+    const int64_t pairs = a->B * a->Hkv;
+    int64_t want = a->n_splits > 0 ? a->n_splits : (int4_resident_wgs() + pairs / 2) / pairs;
+    if (want > nT) want = nT;
+    if (want < 1) want = 1;
+    pl.tiles_per_split = cdiv(nT, want);
+    pl.n = cdiv(nT, pl.tiles_per_split);
+    pl.n_f16_tiles = int4_fp16_tiles(p);
+    pl.tps = 0;
+    return pl;
+  }
+  const bool mfma = pl.k == Kern::kMfma;
+  plan_splits(a, mfma ? mfma_tile() : 64, &pl.n, &pl.tps, mfma ? mfma_tiles(p) * mfma_tile() : -1,
+              mfma ? 512 : 2048);
+  return pl;
 }
 
 }  // namespace
@@ -136,10 +183,8 @@ FADE_API int fade_tiered_decode_workspace_bytes(const fade_decode_args* a, int64
   if (rc) return rc;
   if (bytes == nullptr) return einval("fade_tiered_decode_workspace_bytes: null output");
   const Params p = to_params(a);
-  const bool mfma = use_mfma(a, p);
-  int64_t n, tps;
-  plan_splits(a, mfma ? mfma_tile() : 64, &n, &tps, mfma ? mfma_tiles(p) * mfma_tile() : -1, mfma ? 512 : 2048);
-  *bytes = ml_bytes(a, n) + a->B * a->Hq * n * kD * 4;
+  const Plan pl = make_plan(a, p);
+  *bytes = ws_layout(a, pl.n).total;
   return FADE_OK;
 }
 
@@ -147,22 +192,31 @@ FADE_API int fade_tiered_decode_attn(const fade_decode_args* a, void* stream) {
   int rc = validate(a);
   if (rc) return rc;
   Params p = to_params(a);
-  const bool mfma = use_mfma(a, p);
-  if (a->kernel == 2 && !mfma)
-    return einval("fade_tiered_decode_attn: the matrix-core kernel does not handle middle format %d", p.mid.fmt);
-  int64_t n, tps;
-  plan_splits(a, mfma ? mfma_tile() : 64, &n, &tps, mfma ? mfma_tiles(p) * mfma_tile() : -1, mfma ? 512 : 2048);
-  const int64_t need = ml_bytes(a, n) + a->B * a->Hq * n * kD * 4;
-  if (a->workspace == nullptr || a->workspace_bytes < need)
+  const Plan pl = make_plan(a, p);
+  if ((a->kernel == 2 || a->kernel == 3) && pl.k == Kern::kValu)
+    return einval("fade_tiered_decode_attn: the matrix-core kernels do not handle this middle tier (format %d)",
+                  p.mid.fmt);
+  const WsLayout ws = ws_layout(a, pl.n);
+  if (a->workspace == nullptr || a->workspace_bytes < ws.total)
     return einval("fade_tiered_decode_attn: workspace too small (%lld < %lld bytes)",
-                  (long long)a->workspace_bytes, (long long)need);
-  if (n > 65535) return einval("fade_tiered_decode_attn: too many splits");
-  p.n_splits = static_cast<int>(n);
-  p.tokens_per_split = tps;
-  p.ws_ml = static_cast<float*>(a->workspace);
-  p.ws_acc = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + ml_bytes(a, n));
+                  (long long)a->workspace_bytes, (long long)ws.total);
+  if (pl.n > 65535) return einval("fade_tiered_decode_attn: too many splits");
+  char* wsb = static_cast<char*>(a->workspace);
+  p.n_splits = static_cast<int>(pl.n);
+  p.tokens_per_split = pl.tps;
+  p.ws_ml = reinterpret_cast<float*>(wsb + ws.ml);
+  p.ws_acc = reinterpret_cast<float*>(wsb + ws.acc);
   hipStream_t st = as_stream(stream);
-  rc = mfma ? launch_mfma(p, st) : launch_valu(p, st);
+  if (pl.k == Kern::kInt4) {
+    p.out = static_cast<uint16_t*>(a->out);
+    p.o_sb = a->o_sb;
+    p.o_sh = a->o_sh;
+    p.n_f16_tiles = pl.n_f16_tiles;
+    p.tiles_per_split = pl.tiles_per_split;
+    p.counters = reinterpret_cast<uint32_t*>(wsb + ws.counters);
+    return launch_int4(p, st);
+  }
+  rc = pl.k == Kern::kMfma ? launch_mfma(p, st) : launch_valu(p, st);
   if (rc) return rc;
   const int64_t rows = a->B * a->Hq;
   hipLaunchKernelGGL(decode_combine_kernel, dim3(static_cast<unsigned>(rows)), dim3(kD), 0, st,

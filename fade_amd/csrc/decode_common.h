@@ -39,8 +39,14 @@ struct Params {
   int64_t total;             // sink.len + mid.len + recent.len
   int64_t tokens_per_split;  // multiple of the kernel tile
   int n_splits;
-  float* ws_ml;   // [B][Hq][n_splits][2]  (m, l)
-  float* ws_acc;  // [B][Hq][n_splits][kD] unnormalized output
+  float* ws_ml;   // [B][Hq][n_splits][2]  (m, l); INT4 kernel: [B*Hkv][n_splits][4][2]
+  float* ws_acc;  // [B][Hq][n_splits][kD] unnormalized output; INT4 kernel: [B*Hkv][n_splits][4][kD]
+  // INT4 kernel only
+  uint16_t* out;
+  int64_t o_sb, o_sh;
+  int64_t n_f16_tiles;      // 16-token fp16 tiles ahead of the packed 64-token tiles
+  int64_t tiles_per_split;  // tiles (either kind) per split
+  uint32_t* counters;       // [B*Hkv] finished splits; zero between calls
 };
 
 // Signed symmetric code of channel d in a packed row (fade/quant.py:26-43,
@@ -74,6 +80,13 @@ int launch_valu(const Params& p, hipStream_t st);
 // Matrix-core kernel; returns FADE_EINVAL when the middle format is not handled.
 int launch_mfma(const Params& p, hipStream_t st);
 bool mfma_supports(const Params& p);
+// INT4 (reference format, K4/V4 symmetric) kernel for GQA groups of <= 4 heads,
+// with the split merge fused in (no combine launch).
+bool int4_supports(const Params& p);
+int int4_fp16_tiles(const Params& p);
+int64_t int4_tiles(const Params& p);
+int int4_resident_wgs();
+int launch_int4(const Params& p, hipStream_t st);
 int mfma_tile();
 // Number of 64-token tiles the matrix-core kernel walks (fp16 tokens, then packed).
 int64_t mfma_tiles(const Params& p);

@@ -1,0 +1,591 @@
+// Matrix-core decode attention over a reference-format INT4 middle tier
+// (per-channel K scales, per-token V scales; fade/quant.py:61-92) for GQA
+// groups of up to four query heads per kv head, gfx950.
+//
+// Workgroup = 4 wavefronts serving one (batch row, kv head, split); wave w
+// walks tiles w, w+4, ... of the split with its own online softmax; the four
+// are merged through LDS, and the last workgroup of a (batch row, kv head)
+// to finish merges the splits (no second launch).
+//
+// Block-diagonal tile layout.  A packed tile is 64 tokens = four 16-token
+// sub-tiles s.  QK^T runs on int8 MFMA 16x16x64 whose k dimension carries 16
+// channels of each of the four sub-tiles (k = 16*sigma + j) and whose 16
+// columns are (head h, sub-tile s) = 4h + s; the query operand is zero unless
+// s == sigma, so C[m][4h+s] = score(head h, token 16s + m).  With four heads
+// every lane then owns four real scores:
+//
+//   lane = 16g + 4h + s, register i   <->   head h, token 16s + 4g + i
+//
+// which is also, unchanged, the A operand layout of the f16 MFMA 16x16x32 of
+// P*V (rows 4h+s, k slots 8g..8g+7 = sub-tiles (sa, sb) x 4 tokens), and the
+// PV accumulator lands as lane (n, g), register i  <->  head g, sub-tile i,
+// channel n: the sum over sub-tiles is lane-local.  Softmax work per token
+// is therefore done once, by one lane (not by 16 lanes of mostly padding).
+//
+// K codes: lane l loads the 64-byte row of token l straight into VGPRs; the
+// two's-complement nibbles become int8 16*c with one AND (high nibbles) or a
+// shift+AND (low nibbles), and the factor 16 is folded into the score scale.
+// The query times the per-channel K scale is quantized per head to 16 bits
+// and split into two int8 digits (hi*256 + lo); score = hi_acc*256 + lo_acc.
+//
+// V codes: HBM -> LDS by direct loads (swizzled 16-byte units), transposed
+// by ds_read_b64_tr_b4 so that each lane receives one channel of 16 tokens,
+// turned into fp16 64 + u (u = c + 8 in mantissa bits 4..7) with a shift and
+// an AND-OR; P is pre-multiplied by the per-token V scale, and the constant
+// 72 per token is removed at the end through an MFMA-accumulated 72 * sum(P').
+//
+// fp16 tokens (sink + recent) form 16-token tiles handled with f16 MFMAs in
+// the same fragment layout (sub-tile 0 only).
+#include <math.h>
+
+#include "decode_common.h"
+
+namespace fade {
+namespace decode {
+namespace {
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kTile = 64;                // tokens of a packed tile
+constexpr int kMini = 16;                // tokens of an fp16 tile
+// One ring stage holds one tile: K codes [64 rows][64 B] (fp16 tile: K rows
+// [16][256 B]) | V codes (fp16 tile: V rows) | V scales, one dword per token.
+constexpr int kStageK = 0, kStageV = 4096, kStageVS = 8192;
+constexpr int kStageBytes = 8192 + 256;
+constexpr int kOpsPerTile = 9;           // direct-to-LDS loads issued per tile (either kind)
+constexpr int kQdZero = 8 * 2 * 4 * 16;  // zero operand after the [ks][digit][head][16 B] query digits
+constexpr float kQMax = 32000.0f;
+constexpr float kNegBig = -1.0e30f;      // running-max sentinel (finite: no inf - inf)
+constexpr float kTau = 8.0f;             // the running max moves only when a score exceeds it by kTau (log2)
+
+// s_waitcnt immediate: at most n vector-memory ops outstanding (expcnt, lgkmcnt untouched).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kLgkm0 = 15 | (3 << 14) | (7 << 4);  // lgkmcnt(0) only
+
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma2(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_ushort %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
+}
+// Same with a wave-uniform base address and a 32-bit per-lane byte offset.
+__device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma2(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_ushort %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
+}
+
+// Eight two's-complement nibbles -> fp16 pairs (nibble j, nibble j+4) of value
+// 72 + c: the nibble goes to mantissa bits 4..7 of 64.0 (0x5400, one code step
+// = 1.0) and its top bit is flipped (c + 8, offset binary).  mask = 0x00F000F0
+// and cst = 0x54805480 arrive in registers so that each pair is one v_bitop3
+// ((a & mask) ^ cst) after a shift.
+__device__ __forceinline__ void v_nibbles_to_f16(uint32_t w, uint32_t mask, uint32_t cst, uint32_t (&o)[4]) {
+  o[0] = ((w << 4) & mask) ^ cst;
+  o[1] = (w & mask) ^ cst;
+  o[2] = ((w >> 4) & mask) ^ cst;
+  o[3] = ((w >> 8) & mask) ^ cst;
+}
+
+struct FpRow {
+  const uint16_t* k;
+  const uint16_t* v;
+};
+
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// LDS (two 8.25 KB ring stages per wave, ~71 KB per workgroup) allows two
+// workgroups per CU; registers are sized for that (two waves per SIMD).
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_int4_kernel(Params p) {
+  const int split = blockIdx.x;
+  const int64_t kvh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n16 = lane & 15, g = lane >> 4;
+  const int hq = n16 >> 2, sq = n16 & 3;  // head / sub-tile of this lane's scores
+  const int G = p.G;
+  const int64_t bkv = b * p.Hkv + kvh;
+  const int64_t M = p.mid.len;
+  const int64_t F = p.total - M;
+  const int64_t nFt = p.n_f16_tiles;
+  const int64_t nT = nFt + (M + kTile - 1) / kTile;
+  const int64_t t0 = static_cast<int64_t>(split) * p.tiles_per_split;
+  const int64_t t1 = t0 + p.tiles_per_split < nT ? t0 + p.tiles_per_split : nT;
+  // this wave's tiles: t0 + wave + 4i, i < n_w
+  const int n_w = t0 + wave < t1 ? static_cast<int>((t1 - t0 - wave + kWaves - 1) / kWaves) : 0;
+
+  __shared__ __attribute__((aligned(16))) uint8_t ring0[kWaves][kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t ring1[kWaves][kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint32_t qraw_s[4][kD / 2];  // fp16 query rows
+  __shared__ __attribute__((aligned(16))) uint32_t ksraw_s[kWaves][kD / 2];  // K scales (one copy per wave)
+  __shared__ __attribute__((aligned(16))) uint8_t qd_s[kQdZero + 16];
+  __shared__ float qsc_s[4];
+  __shared__ float red_m[kWaves][4], red_l[kWaves][4];
+  __shared__ int last_s;
+
+  const uint8_t* kc = p.mid.k_codes + bkv * M * 64;
+  const uint8_t* vc = p.mid.v_codes + bkv * M * 64;
+  const uint16_t* vsg = p.mid.v_scale + bkv * M;
+  // fp16 tiers as (uniform) locals: the lambdas below must not read the kernel
+  // arguments through a pointer (that becomes a per-lane global load whose
+  // compiler-inserted vmcnt wait would also wait for the tile prefetches).
+  const int64_t ns = p.sink.len;
+  const uint16_t* const sk = p.sink.k + b * p.sink.k_sb + kvh * p.sink.k_sh;
+  const uint16_t* const sv = p.sink.v + b * p.sink.v_sb + kvh * p.sink.v_sh;
+  const int64_t sk_ss = p.sink.k_ss, sv_ss = p.sink.v_ss;
+  const uint16_t* const rk = p.recent.k + b * p.recent.k_sb + kvh * p.recent.k_sh;
+  const uint16_t* const rv = p.recent.v + b * p.recent.v_sb + kvh * p.recent.v_sh;
+  const int64_t rk_ss = p.recent.k_ss, rv_ss = p.recent.v_ss;
+  const float scale_log2 = p.scale_log2;
+  auto fp16row = [&](int64_t f) {
+    FpRow r;
+    if (f < ns) {
+      r.k = sk + f * sk_ss;
+      r.v = sv + f * sv_ss;
+    } else {
+      r.k = rk + (f - ns) * rk_ss;
+      r.v = rv + (f - ns) * rv_ss;
+    }
+    return r;
+  };
+  lds_u8* const sp0 = (lds_u8*)&ring0[wave][0];
+  lds_u8* const sp1 = (lds_u8*)&ring1[wave][0];
+  const uint32_t st0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sp0)));
+  const uint32_t st1 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sp1)));
+
+  // ---- loads of one tile into a ring stage (exactly kOpsPerTile per tile) ----
+  // Packed tile: 16-byte unit q of K row r at LDS unit 4r + (q ^ ((r >> 2) & 3)),
+  // of V row r at 4r + (q ^ ((r >> 4) ^ (r >> 2)) & 3); rows past the tier are
+  // clamped to its last row (masked later).  fp16 tile: K row r unit u at
+  // 16r + (u ^ r), V rows unswizzled.
+  uint32_t voff[4], koff[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    voff[k] = (16 * k + (lane >> 2)) * 64 + 16 * ((lane & 3) ^ ((k ^ (lane >> 4)) & 3));
+    koff[k] = (16 * k + (lane >> 2)) * 64 + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
+  }
+  auto issue = [&](int64_t tt, uint32_t st) {
+    if (tt >= nFt) {
+      const int64_t m0 = (tt - nFt) * kTile;
+      const uint8_t* kb = kc + m0 * 64;
+      const uint8_t* vb = vc + m0 * 64;
+      const uint16_t* sb = vsg + m0;
+      uint32_t so = 2u * lane, vo[4] = {voff[0], voff[1], voff[2], voff[3]};
+      uint32_t ko[4] = {koff[0], koff[1], koff[2], koff[3]};
+      if (m0 + kTile > M) {
+        const int lim = static_cast<int>(M - 1 - m0);
+        so = 2u * (lane < lim ? lane : lim);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int r = 16 * k + (lane >> 2);
+          const int rr = r < lim ? r : lim;
+          vo[k] = rr * 64 + 16 * ((lane & 3) ^ ((k ^ (lane >> 4)) & 3));
+          ko[k] = rr * 64 + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) lds_dma16(kb, ko[k], st + kStageK + 1024 * k);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) lds_dma16(vb, vo[k], st + kStageV + 1024 * k);
+      lds_dma2(sb, so, st + kStageVS);
+    } else {
+      const int64_t f0 = tt * kMini;
+      const int vf = static_cast<int>(F - f0 < kMini ? F - f0 : kMini);
+      const int u = lane & 15;
+      const uint16_t* vr = nullptr;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int row = 4 * k + (lane >> 4);
+        const FpRow fr = fp16row(f0 + (row < vf ? row : vf - 1));
+        lds_dma16(fr.k + 8 * (u ^ row), st + kStageK + 1024 * k);
+        lds_dma16(fr.v + 8 * u, st + kStageV + 1024 * k);
+        vr = fr.v;
+      }
+      lds_dma2(vr, st + kStageVS);  // filler: every tile issues the same number of loads
+    }
+  };
+
+  // ---- prologue: query rows and K scales first, then the first two tiles ----
+  {
+    const uint32_t qa = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&qraw_s[wave][0])));
+    const uint32_t ka = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&ksraw_s[wave][0])));
+    if (wave < G) lds_dma4(p.q + b * p.q_sb + (kvh * G + wave) * p.q_sh + 2 * lane, qa);
+    else qraw_s[wave][lane] = 0u;
+    lds_dma4(p.mid.k_scale + bkv * kD + 2 * lane, ka);
+  }
+  if (n_w > 0) issue(t0 + wave, st0);
+  if (n_w > 1) issue(t0 + wave + kWaves, st1);
+  if (n_w > 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kOpsPerTile));
+  else if (n_w > 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kOpsPerTile));
+  else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  __builtin_amdgcn_wave_barrier();
+
+  // ---- query digits: wave h handles head h (channels 2*lane, 2*lane+1) ----
+  {
+    const int h = wave;
+    const uint32_t qq = qraw_s[h][lane], ks = ksraw_s[h][lane];
+    const float qf0 = h2f(static_cast<uint16_t>(qq & 0xFFFFu)) * h2f(static_cast<uint16_t>(ks & 0xFFFFu));
+    const float qf1 = h2f(static_cast<uint16_t>(qq >> 16)) * h2f(static_cast<uint16_t>(ks >> 16));
+    const float mx = group_max<64>(fmaxf(fabsf(qf0), fabsf(qf1)));
+    const float inv = mx > 0.0f ? kQMax / mx : 0.0f;
+    const int qi[2] = {static_cast<int>(rintf(qf0 * inv)), static_cast<int>(rintf(qf1 * inv))};
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      // channel d -> k-step d/16, operand byte j (see the K operand assembly below)
+      const int d = 2 * lane + e;
+      const int ksd = d >> 4, r = d & 15;
+      const int j = 4 * (2 * (r >> 3) + (r & 1)) + ((r & 7) >> 1);
+      const int hi = (qi[e] + 128) >> 8;
+      const int lo = qi[e] - 256 * hi;
+      qd_s[(2 * ksd + 0) * 64 + h * 16 + j] = static_cast<uint8_t>(hi & 0xFF);
+      qd_s[(2 * ksd + 1) * 64 + h * 16 + j] = static_cast<uint8_t>(lo & 0xFF);
+    }
+    if (lane == 0) qsc_s[h] = mx > 0.0f ? (mx / kQMax) * p.scale_log2 * 0.0625f : 0.0f;
+    if (tid < 4) reinterpret_cast<uint32_t*>(&qd_s[kQdZero])[tid] = 0u;
+  }
+  __syncthreads();
+
+  const float qsc = qsc_s[hq];
+  // query operands of the QK^T MFMAs (zero unless this lane's column block matches its k group)
+  i32x4 qdh[8], qdl[8];
+  {
+    const bool qlane = (sq == g) && (hq < G);
+    const uint8_t* qbase = qd_s + (qlane ? hq * 16 : kQdZero);
+    const int qstride = qlane ? 64 : 0;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      qdh[ks] = *reinterpret_cast<const i32x4*>(qbase + (2 * ks) * qstride);
+      qdl[ks] = *reinterpret_cast<const i32x4*>(qbase + (2 * ks + 1) * qstride);
+    }
+  }
+  const uint16_t* q16 = reinterpret_cast<const uint16_t*>(&qraw_s[hq][0]);
+
+  float m_run = kNegBig, l_run = 0.0f;
+  f32x4 acc[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) acc[c] = f32x4{0, 0, 0, 0};
+  f32x4 acc_off = {0, 0, 0, 0};
+
+  // Online-softmax step for this lane's four log2-domain scores x (absolute);
+  // pr = the unnormalized probabilities relative to the running max.
+  auto softmax4 = [&](float (&x)[4], float (&pr)[4]) {
+    const float lmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    if (__builtin_amdgcn_ballot_w64(lmax - m_run > kTau) != 0) {
+      float tmax = lmax;
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+      const float ag = __shfl(alpha, 4 * g, 64);  // accumulator rows of lane (n, g) belong to head g
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[c] *= ag;
+      acc_off *= ag;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_exp2f(x[i] - m_run);
+    l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+  };
+
+  // ---- fp16 tile (16 tokens) from a ring stage ----
+  auto fp16_tile = [&](int64_t t, const lds_u8* sp) {
+    const int64_t f0 = t * kMini;
+    const int vf = static_cast<int>(F - f0 < kMini ? F - f0 : kMini);
+    // QK^T in the plain layout: k = 32 channels (8 per lane group), columns
+    // 4h + s repeat head h for every s; the s != 0 copies are masked below.
+    f32x4 c4 = {0, 0, 0, 0};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x4 a = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+          sp + kStageK + 256 * n16 + 16 * ((4 * ks + g) ^ n16));
+      const uint4 bq = *reinterpret_cast<const uint4*>(q16 + 32 * ks + 8 * g);
+      c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, bq), c4, 0,
+                                                  0, 0);
+    }
+    float x[4], pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = (sq == 0 && 4 * g + i < vf) ? c4[i] * scale_log2 : -INFINITY;
+    softmax4(x, pr);
+    const uint32_t pk0 = sq == 0 ? pack_f16(pr[0], pr[1]) : 0u;
+    const uint32_t pk1 = sq == 0 ? pack_f16(pr[2], pr[3]) : 0u;
+    const f16x4 a4 = __builtin_bit_cast(f16x4, i32x2{static_cast<int>(pk0), static_cast<int>(pk1)});
+    const __attribute__((address_space(3))) uint16_t* v16 =
+        reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(sp + kStageV);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int col = 16 * c + (n16 ^ 1);
+      const f16x4 vb = {__builtin_bit_cast(_Float16, v16[(4 * g + 0) * kD + col]),
+                        __builtin_bit_cast(_Float16, v16[(4 * g + 1) * kD + col]),
+                        __builtin_bit_cast(_Float16, v16[(4 * g + 2) * kD + col]),
+                        __builtin_bit_cast(_Float16, v16[(4 * g + 3) * kD + col])};
+      acc[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(a4, vb, acc[c], 0, 0, 0);
+    }
+  };
+
+  // ---- packed INT4 tile from a ring stage ----
+  // tr4 read addresses: as source lane s' = n16 of group g this lane fetches
+  // row 16*sigma + 4g + i, where slot k = ((s'&3)<<1)|((s'>>2)&1) of pair s'>>3
+  // gives sigma = 2*(s'>>3) + (k>>2), i = k&3.
+  uint32_t vrd[4];
+  {
+    const int kk = ((n16 & 3) << 1) | ((n16 >> 2) & 1);
+    const int sigma = 2 * (n16 >> 3) + (kk >> 2);
+    const int r = 16 * sigma + 4 * g + (kk & 3);
+    const int sw = (sigma ^ g) & 3;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) vrd[qq] = kStageV + 16 * (4 * r + (qq ^ sw));
+  }
+  uint32_t krd[4];  // K row `lane`, 16-byte unit q
+#pragma unroll
+  for (int qq = 0; qq < 4; ++qq) krd[qq] = kStageK + 16 * (4 * lane + (qq ^ ((lane >> 2) & 3)));
+  const uint32_t vs_rd = kStageVS + 4 * (16 * sq + 4 * g);
+  const uint32_t z = 0u;
+  uint32_t vmask, vcst;  // register-resident constants of v_nibbles_to_f16
+  asm volatile("s_mov_b32 %0, 0x00F000F0" : "=s"(vmask));
+  asm volatile("v_mov_b32 %0, 0x54805480" : "=v"(vcst));
+  const f16x8 b72 = __builtin_bit_cast(f16x8, u32x4{0x54805480u, 0x54805480u, 0x54805480u, 0x54805480u});
+
+  auto packed_tile = [&](int64_t t, const lds_u8* sp) {
+    // QK^T: A = K codes of token `lane` as int8 16*c (high nibbles: AND; low: shift + AND)
+    i32x4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const u32x4 kv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + krd[qq]);
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int ks = 2 * qq + h2;
+        const uint32_t w0 = kv[2 * h2], w1 = kv[2 * h2 + 1];
+        const i32x4 a = {static_cast<int>(w0 & 0xF0F0F0F0u), static_cast<int>((w0 << 4) & 0xF0F0F0F0u),
+                         static_cast<int>(w1 & 0xF0F0F0F0u), static_cast<int>((w1 << 4) & 0xF0F0F0F0u)};
+        chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdh[ks], chi, 0, 0, 0);
+        clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdl[ks], clo, 0, 0, 0);
+      }
+    }
+    const int64_t m0 = (t - nFt) * kTile;
+    float x[4], pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = static_cast<float>(chi[i] * 256 + clo[i]) * qsc;
+    if (m0 + kTile > M) {
+      const int valid = static_cast<int>(M - m0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (16 * sq + 4 * g + i >= valid) x[i] = -INFINITY;
+    }
+    softmax4(x, pr);
+    // P' = P * v_scale (scales sit in the low halves of the stage's scale dwords)
+    uint32_t pk0, pk1;
+    {
+      const u32x4 sv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd);
+      pk0 = pack_f16(pr[0] * h2f(static_cast<uint16_t>(sv[0])), pr[1] * h2f(static_cast<uint16_t>(sv[1])));
+      pk1 = pack_f16(pr[2] * h2f(static_cast<uint16_t>(sv[2])), pr[3] * h2f(static_cast<uint16_t>(sv[3])));
+    }
+    const f16x8 a0 = __builtin_bit_cast(f16x8, u32x4{sq == 0 ? pk0 : z, sq == 0 ? pk1 : z, sq == 1 ? pk0 : z, sq == 1 ? pk1 : z});
+    const f16x8 a1 = __builtin_bit_cast(f16x8, u32x4{sq == 2 ? pk0 : z, sq == 2 ? pk1 : z, sq == 3 ? pk0 : z, sq == 3 ? pk1 : z});
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const i32x2 xv = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
+          reinterpret_cast<lds_i32x2*>(const_cast<lds_u8*>(sp) + vrd[c >> 1] + 8 * (c & 1)));
+      uint32_t b0[4], b1[4];
+      v_nibbles_to_f16(static_cast<uint32_t>(xv[0]), vmask, vcst, b0);
+      v_nibbles_to_f16(static_cast<uint32_t>(xv[1]), vmask, vcst, b1);
+      acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(f16x8, b0), acc[c], 0, 0, 0);
+      acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(f16x8, b1), acc[c], 0, 0, 0);
+    }
+    acc_off = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b72, acc_off, 0, 0, 0);
+    acc_off = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b72, acc_off, 0, 0, 0);
+  };
+
+  // ---- main loop: two stages, two tiles in flight ----
+  auto step = [&](int i, const lds_u8* sp, uint32_t st) {
+    const int64_t t = t0 + wave + static_cast<int64_t>(kWaves) * i;
+    if (i + 1 < n_w) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kOpsPerTile));  // tile i landed, i+1 in flight
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __builtin_amdgcn_wave_barrier();
+    if (t < nFt) fp16_tile(t, sp);
+    else packed_tile(t, sp);
+    __builtin_amdgcn_s_waitcnt(kLgkm0);  // every LDS read of this stage has returned
+    __builtin_amdgcn_wave_barrier();
+    if (i + 2 < n_w) issue(t + 2 * kWaves, st);
+  };
+  for (int i = 0; i < n_w; i += 2) {
+    step(i, sp0, st0);
+    if (i + 1 < n_w) step(i + 1, sp1, st1);
+  }
+
+  // ---- merge the four wavefronts ----
+  float lsum = l_run;
+  lsum += __shfl_xor(lsum, 1, 64);
+  lsum += __shfl_xor(lsum, 2, 64);
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  if (g == 0 && sq == 0) {
+    red_m[wave][hq] = m_run;
+    red_l[wave][hq] = lsum;
+  }
+  __syncthreads();
+  float* red_o = reinterpret_cast<float*>(&ring0[0][0]);  // [wave][4 heads][128]
+  {
+    float Mg = red_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) Mg = fmaxf(Mg, red_m[w][g]);
+    const float wsc = exp2f(red_m[wave][g] - Mg);
+    const float off = (acc_off[0] + acc_off[1]) + (acc_off[2] + acc_off[3]);
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+      red_o[(wave * 4 + g) * kD + 16 * c + (n16 ^ 1)] = (((acc[c][0] + acc[c][1]) + (acc[c][2] + acc[c][3])) - off) * wsc;
+  }
+  __syncthreads();
+  const int n = p.n_splits;
+  for (int idx = tid; idx < G * kD; idx += kThreads) {
+    const int h = idx >> 7, d = idx & (kD - 1);
+    float Mh = red_m[0][h];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) Mh = fmaxf(Mh, red_m[w][h]);
+    float o = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      o += red_o[(w * 4 + h) * kD + d];
+      L += red_l[w][h] * exp2f(red_m[w][h] - Mh);
+    }
+    if (n == 1) {
+      p.out[b * p.o_sb + (kvh * G + h) * p.o_sh + d] = f2h(o / L);
+    } else {
+      const int64_t pi = (bkv * n + split) * 4 + h;
+      store_agent(&p.ws_acc[pi * kD + d], o);
+      if (d == 0) {
+        store_agent(&p.ws_ml[2 * pi], Mh);
+        store_agent(&p.ws_ml[2 * pi + 1], L);
+      }
+    }
+  }
+  if (n == 1) return;
+
+  // ---- the last workgroup of this (batch row, kv head) merges the splits ----
+  // Partials, counter and the merge reads are device-coherent accesses
+  // (agent-scope atomics: per-instruction coherence, no whole-L2 write-back or
+  // invalidate).  Order: each thread's partial stores complete (vmcnt(0))
+  // before the barrier, the barrier before the counter increment, and the
+  // merge loads issue only after the increment has returned.
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&p.counters[bkv], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_s = prev == static_cast<uint32_t>(n - 1);
+  }
+  __syncthreads();
+  if (!last_s) return;
+  for (int idx = tid; idx < G * kD; idx += kThreads) {
+    const int h = idx >> 7, d = idx & (kD - 1);
+    const int64_t p0 = bkv * n * 4 + h;
+    // splits in batches of 8 whose loads all issue before any is used
+    float Mh = kNegBig, o = 0.0f, L = 0.0f;
+    for (int s0 = 0; s0 < n; s0 += 8) {
+      float mm[8], ll[8], aa[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t pi = p0 + 4 * (s0 + j < n ? s0 + j : s0);
+        mm[j] = load_agent(&p.ws_ml[2 * pi]);
+        ll[j] = load_agent(&p.ws_ml[2 * pi + 1]);
+        aa[j] = load_agent(&p.ws_acc[pi * kD + d]);
+      }
+      float bm = kNegBig;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < n) bm = fmaxf(bm, mm[j]);
+      const float Mn = fmaxf(Mh, bm);
+      const float r = exp2f(Mh - Mn);
+      o *= r;
+      L *= r;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (s0 + j < n) {
+          const float w = exp2f(mm[j] - Mn);
+          L += ll[j] * w;
+          o += aa[j] * w;
+        }
+      }
+      Mh = Mn;
+    }
+    p.out[b * p.o_sb + (kvh * G + h) * p.o_sh + d] = f2h(o / L);
+  }
+  if (tid == 0) __hip_atomic_store(&p.counters[bkv], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+bool aligned(const void* x, uintptr_t a) { return (reinterpret_cast<uintptr_t>(x) & (a - 1)) == 0; }
+
+bool fp16_tier_ok(const Fp16Tier& t) {
+  if (t.len == 0) return true;
+  return aligned(t.k, 16) && aligned(t.v, 16) && ((t.k_sb | t.k_sh | t.k_ss | t.v_sb | t.v_sh | t.v_ss) % 8 == 0);
+}
+
+}  // namespace
+
+bool int4_supports(const Params& p) {
+  if (p.mid.fmt != FADE_MID_SYM || p.mid.k_bits != 4 || p.mid.v_bits != 4 || p.mid.len <= 0) return false;
+  if (p.G > 4) return false;
+  if (!fp16_tier_ok(p.sink) || !fp16_tier_ok(p.recent)) return false;
+  if (!aligned(p.q, 16) || p.q_sb % 8 || p.q_sh % 8) return false;
+  return aligned(p.mid.k_codes, 16) && aligned(p.mid.v_codes, 16) && aligned(p.mid.k_scale, 4) &&
+         aligned(p.mid.v_scale, 2);
+}
+
+int int4_fp16_tiles(const Params& p) {
+  const int64_t F = p.total - p.mid.len;
+  return static_cast<int>(cdiv(F, kMini));
+}
+
+int64_t int4_tiles(const Params& p) { return int4_fp16_tiles(p) + cdiv(p.mid.len, kTile); }
+
+int int4_resident_wgs() {
+  static int cached = 0;
+  if (cached > 0) return cached;
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_int4_kernel, kThreads, 0) != hipSuccess ||
+      cus <= 0 || per_cu <= 0) {
+    (void)hipGetLastError();
+    return 512;
+  }
+  cached = cus * per_cu;
+  return cached;
+}
+
+int launch_int4(const Params& p, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv), static_cast<unsigned>(p.B));
+  hipLaunchKernelGGL(decode_int4_kernel, grid, dim3(kThreads), 0, st, p);
+  return check_launch("fade_tiered_decode_attn(int4)");
+}
+
+}  // namespace decode
+}  // namespace fade

@@ -157,8 +157,10 @@ typedef struct fade_decode_args {
   fade_mid_tier mid;           /* next mid.len tokens */
   fade_fp16_tier recent;       /* last recent.len tokens */
   int32_t n_splits;            /* 0 = choose automatically */
-  int32_t kernel;              /* 0 = auto, 1 = portable VALU kernel */
-  void* workspace;
+  int32_t kernel;              /* 0 = auto, 1 = portable VALU kernel, 2 = matrix-core kernels
+                                  only, 3 = the general matrix-core kernel (no INT4 fast path) */
+  void* workspace;             /* zero-filled before its first use; every call leaves its
+                                  split counters at zero again */
   int64_t workspace_bytes;
 } fade_decode_args;
 

@@ -54,13 +54,52 @@ def _int4_mid(dev, k, v, ns, nr):
         (1, 32, 8, 333, 4, 256),  # config 2 windows
     ],
 )
-@pytest.mark.parametrize("kernel", [0, 1])
+@pytest.mark.parametrize("kernel", [0, 1, 3])
 def test_tiered_decode_int4(dev, B, Hq, Hkv, S, ns, nr, kernel):
     print(f"case decode int4 B={B} Hq={Hq} Hkv={Hkv} S={S} ns={ns} nr={nr} kernel={kernel}", flush=True)
     q, k, v, ns, nr = _case(B, Hq, Hkv, S, ns, nr, seed=1000 + S)
     mid, omid = _int4_mid(dev, k, v, ns, nr)
     err = _run(dev, q, k, v, ns, nr, mid, omid, kernel=kernel)
     assert err <= ATOL, err
+
+
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,S,ns,nr",
+    [
+        (2, 8, 4, 777, 4, 64),  # G=2: padded head columns
+        (1, 12, 4, 1000, 0, 0),  # G=3, no fp16 tiers
+        (2, 8, 8, 600, 1, 0),  # G=1, sink only
+        (1, 4, 1, 300, 0, 37),  # one kv head, ragged recent window
+        (2, 32, 8, 4096, 4, 64),  # config-1 shape, shorter
+    ],
+)
+def test_tiered_decode_int4_fast_path_shapes(dev, B, Hq, Hkv, S, ns, nr):
+    """GQA groups of 1..4 heads take the INT4 kernel with the fused split merge."""
+    print(f"case decode int4 fast B={B} Hq={Hq} Hkv={Hkv} S={S} ns={ns} nr={nr}", flush=True)
+    q, k, v, ns, nr = _case(B, Hq, Hkv, S, ns, nr, seed=2000 + S)
+    mid, omid = _int4_mid(dev, k, v, ns, nr)
+    for n_splits in (0, 1, 5):
+        assert _run(dev, q, k, v, ns, nr, mid, omid, kernel=2, n_splits=n_splits) <= ATOL, n_splits
+
+
+def test_tiered_decode_int4_plan_replays(dev):
+    """Repeated launches of one plan reuse the workspace: the split counters reset every call."""
+    from fade_amd.kernels.tiered_attn import TieredDecodePlan
+
+    print("case decode int4 plan replays", flush=True)
+    q, k, v, ns, nr = _case(2, 32, 8, 3000, 4, 64, seed=11)
+    S = k.shape[2]
+    mid, omid = _int4_mid(dev, k, v, ns, nr)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    plan = TieredDecodePlan(t(q), (t(k[:, :, :ns]), t(v[:, :, :ns])), mid, (t(k[:, :, S - nr :]), t(v[:, :, S - nr :])))
+    outs = [plan.run().clone() for _ in range(4)]
+    torch.cuda.synchronize()
+    ref = oatt.tiered_decode(q, k[:, :, :ns], v[:, :, :ns], omid, k[:, :, S - nr :], v[:, :, S - nr :])
+    for o in outs:
+        assert torch.equal(o, outs[0])
+    assert np.abs(outs[0].float().cpu().numpy() - ref).max() <= ATOL
+    counters = plan.workspace[: 2 * 8 * 4].view(torch.int32)
+    assert int(counters.abs().sum()) == 0
 
 
 @pytest.mark.parametrize("n_splits", [1, 3, 64])
