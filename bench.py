@@ -146,6 +146,72 @@ def cpu_baseline(cfg, seed: int):
     }
 
 
+COPY_MIB = 256
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_int4_c1_traffic.json")
+
+
+def pmc_pass(steps: int) -> int:
+    """Short run for ``rocprofv3 --pmc``: a plain copy of known size (the counter
+    calibration), then ``steps`` config-1 INT4 decode calls."""
+    dev = torch.device("cuda:0")
+    src = torch.ones(COPY_MIB << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    plans = build_instances(CONFIGS[1], "int4", dev, 1001, N_INSTANCES)
+    for i in range(steps):
+        plans[i % len(plans)].run()
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_pass": True, "copy_MiB": COPY_MIB, "decode_calls": steps}))
+    return 0
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the decode kernel, scaled by
+    what the same counters read for the copy kernel (which moves COPY_MIB each way)."""
+    import csv
+
+    def per_kernel(d: str, counter: str):
+        path = None
+        for root, _, files in os.walk(d):
+            for f in files:
+                if f.endswith("counter_collection.csv"):
+                    path = os.path.join(root, f)
+        if path is None:
+            raise SystemExit(f"no counter_collection.csv under {d}")
+        rows = []
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == counter:
+                    rows.append((r["Kernel_Name"], float(r["Counter_Value"])))
+        return rows
+
+    out = {"unit": "bytes per dispatch", "copy_bytes_each_way": COPY_MIB << 20}
+    for counter, d, key in (("FETCH_SIZE", fetch_dir, "fetch"), ("WRITE_SIZE", write_dir, "write")):
+        rows = per_kernel(d, counter)
+        # the calibration copies are the three largest copy dispatches of the run
+        copy = sorted((v for k, v in rows if "copy" in k.lower()), reverse=True)[:3]
+        dec = [v for k, v in rows if "decode_int4_kernel" in k]
+        if len(copy) < 3 or not dec:
+            raise SystemExit(f"{counter}: calibration copy or decode kernel missing in {d}")
+        copy_kib = float(np.median(copy))
+        factor = (COPY_MIB << 10) / copy_kib
+        dec_kib = float(np.mean(dec))
+        out[f"{key}_counter_KiB"] = round(dec_kib, 1)
+        out[f"{key}_copy_counter_KiB"] = round(copy_kib, 1)
+        out[f"{key}_scale"] = round(factor, 4)
+        out[f"{key}_bytes"] = int(dec_kib * 1024 * factor)
+    out["hbm_bytes_per_call"] = out["fetch_bytes"] + out["write_bytes"]
+    out["algorithmic_bytes_per_call"] = decode_bytes(CONFIGS[1], "int4")
+    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    print(json.dumps(out))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -153,7 +219,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="only the config-1 INT4 line")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="copy calibration + --steps decode calls, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn two rocprofv3 --pmc output folders into " + os.path.relpath(TRAFFIC_FILE, ROOT))
     args = ap.parse_args()
+    if args.summarize_pmc:
+        return summarize_pmc(*args.summarize_pmc)
     if args.gpus != 1:
         print(
             "bench.py: this build measures one GPU; the decode path shards by batch / kv head "
@@ -161,6 +233,8 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+    if args.pmc_pass:
+        return pmc_pass(args.steps)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(dev)
@@ -197,9 +271,8 @@ def main() -> int:
             torch.cuda.empty_cache()
 
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "decode_c1_int4_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_call")
 
     line = {
@@ -228,7 +301,7 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
             "algorithmic_bytes_per_call": nbytes,
-            "timed": "HIP events around each call (split kernel + combine) on the launch stream",
+            "timed": "HIP events around each call on the launch stream (one kernel: decode_int4_kernel, split merge fused)",
             "median_us": round(med_ms * 1e3, 2),
         },
         "extra": extra,
