@@ -34,6 +34,12 @@
 // an AND-OR; P is pre-multiplied by the per-token V scale, and the constant
 // 72 per token is removed at the end through an MFMA-accumulated 72 * sum(P').
 //
+// 2-bit variant (rotated backend, fade/rotated_quant.py:35-88,106-187: K per
+// channel, V per token, four codes per byte MSB-first): K codes become int8
+// 64*c (shift + AND per code position); a tr4 read now gives each lane two
+// channels of 16 tokens (one nibble = two codes), each code becomes the fp16
+// value 4 + u (u = c + 2 in mantissa bits 8..9), the per-token offset is 6.
+//
 // fp16 tokens (sink + recent) form 16-token tiles handled with f16 MFMAs in
 // the same fragment layout (sub-tile 0 only).
 #include <math.h>
@@ -61,7 +67,10 @@ constexpr int kMini = 16;                // tokens of an fp16 tile
 // [16][256 B]) | V codes (fp16 tile: V rows) | V scales, one dword per token.
 constexpr int kStageK = 0, kStageV = 4096, kStageVS = 8192;
 constexpr int kStageBytes = 8192 + 256;
-constexpr int kOpsPerTile = 9;           // direct-to-LDS loads issued per tile (either kind)
+constexpr int kOpsF16 = 9;               // direct-to-LDS loads issued per fp16 tile
+// ... and per packed tile: K + V codes in 1 KB loads, plus one for the V scales
+template <int BITS>
+constexpr int ops_packed() { return BITS == 4 ? 9 : 5; }
 constexpr int kQdZero = 8 * 2 * 4 * 16;  // zero operand after the [ks][digit][head][16 B] query digits
 constexpr float kQMax = 32000.0f;
 constexpr float kNegBig = -1.0e30f;      // running-max sentinel (finite: no inf - inf)
@@ -95,6 +104,32 @@ __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
 }
 
+// Output column n of channel tile c (PV accumulator) <-> head-dim channel.
+// 4-bit: a tr4 read gives lane n the nibble of channel 16c + (n ^ 1).  2-bit:
+// chunk c/2 of 32 channels, lane n holds the codes of channels
+// 4(n/2) + 2(1 - n%2) + {0, 1} (first / second code of the nibble = c%2).
+template <int BITS>
+__device__ __forceinline__ int out_channel(int c, int n) {
+  if (BITS == 4) return 16 * c + (n ^ 1);
+  return 32 * (c >> 1) + 4 * (n >> 1) + 2 * (1 - (n & 1)) + (c & 1);
+}
+
+// Two's-complement 2-bit codes of eight nibbles (first code in bits 2..3 of a
+// nibble, second in bits 0..1) -> fp16 pairs (nibble j, nibble j+4) of value
+// 6 + c: the code goes to mantissa bits 8..9 of 4.0 (0x4400) with its sign bit
+// flipped (c + 2); mask = 0x03000300, cst = 0x46004600.
+__device__ __forceinline__ void v2_nibbles_to_f16(uint32_t w, uint32_t mask, uint32_t cst, uint32_t (&of)[4],
+                                                  uint32_t (&os)[4]) {
+  of[0] = ((w << 6) & mask) ^ cst;
+  of[1] = ((w << 2) & mask) ^ cst;
+  of[2] = ((w >> 2) & mask) ^ cst;
+  of[3] = ((w >> 6) & mask) ^ cst;
+  os[0] = ((w << 8) & mask) ^ cst;
+  os[1] = ((w << 4) & mask) ^ cst;
+  os[2] = (w & mask) ^ cst;
+  os[3] = ((w >> 4) & mask) ^ cst;
+}
+
 // Eight two's-complement nibbles -> fp16 pairs (nibble j, nibble j+4) of value
 // 72 + c: the nibble goes to mantissa bits 4..7 of 64.0 (0x5400, one code step
 // = 1.0) and its top bit is flipped (c + 8, offset binary).  mask = 0x00F000F0
@@ -123,7 +158,10 @@ __device__ __forceinline__ float load_agent(const float* p) {
 
 // LDS (two 8.25 KB ring stages per wave, ~71 KB per workgroup) allows two
 // workgroups per CU; registers are sized for that (two waves per SIMD).
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_int4_kernel(Params p) {
+template <int BITS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_sym_kernel(Params p) {
+  constexpr int kOps = ops_packed<BITS>();
+  constexpr int kRowBytes = 128 * BITS / 8;  // packed row of one token
   const int split = blockIdx.x;
   const int64_t kvh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -150,8 +188,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   __shared__ float red_m[kWaves][4], red_l[kWaves][4];
   __shared__ int last_s;
 
-  const uint8_t* kc = p.mid.k_codes + bkv * M * 64;
-  const uint8_t* vc = p.mid.v_codes + bkv * M * 64;
+  const uint8_t* kc = p.mid.k_codes + bkv * M * kRowBytes;
+  const uint8_t* vc = p.mid.v_codes + bkv * M * kRowBytes;
   const uint16_t* vsg = p.mid.v_scale + bkv * M;
   // fp16 tiers as (uniform) locals: the lambdas below must not read the kernel
   // arguments through a pointer (that becomes a per-lane global load whose
@@ -180,7 +218,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const uint32_t st0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sp0)));
   const uint32_t st1 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sp1)));
 
-  // ---- loads of one tile into a ring stage (exactly kOpsPerTile per tile) ----
+  // ---- loads of one tile into a ring stage (kOps per packed tile, kOpsF16 per fp16 tile) ----
   // Packed tile: 16-byte unit q of K row r at LDS unit 4r + (q ^ ((r >> 2) & 3)),
   // of V row r at 4r + (q ^ ((r >> 4) ^ (r >> 2)) & 3); rows past the tier are
   // clamped to its last row (masked later).  fp16 tile: K row r unit u at
@@ -194,26 +232,43 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   auto issue = [&](int64_t tt, uint32_t st) {
     if (tt >= nFt) {
       const int64_t m0 = (tt - nFt) * kTile;
-      const uint8_t* kb = kc + m0 * 64;
-      const uint8_t* vb = vc + m0 * 64;
+      const uint8_t* kb = kc + m0 * kRowBytes;
+      const uint8_t* vb = vc + m0 * kRowBytes;
       const uint16_t* sb = vsg + m0;
-      uint32_t so = 2u * lane, vo[4] = {voff[0], voff[1], voff[2], voff[3]};
-      uint32_t ko[4] = {koff[0], koff[1], koff[2], koff[3]};
-      if (m0 + kTile > M) {
-        const int lim = static_cast<int>(M - 1 - m0);
-        so = 2u * (lane < lim ? lane : lim);
+      const int lim = m0 + kTile > M ? static_cast<int>(M - 1 - m0) : kTile - 1;
+      const uint32_t so = 2u * (lane < lim ? lane : lim);
+      if (BITS == 4) {
+        uint32_t vo[4] = {voff[0], voff[1], voff[2], voff[3]};
+        uint32_t ko[4] = {koff[0], koff[1], koff[2], koff[3]};
+        if (lim < kTile - 1) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int r = 16 * k + (lane >> 2);
+          for (int k = 0; k < 4; ++k) {
+            const int r = 16 * k + (lane >> 2);
+            const int rr = r < lim ? r : lim;
+            vo[k] = rr * 64 + 16 * ((lane & 3) ^ ((k ^ (lane >> 4)) & 3));
+            ko[k] = rr * 64 + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) lds_dma16(kb, ko[k], st + kStageK + 1024 * k);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) lds_dma16(vb, vo[k], st + kStageV + 1024 * k);
+      } else {
+        // 32-byte rows: K row r at 32r (natural order); V row r unit u at
+        // 2r + (u ^ ((r >> 4) & 1)) (spreads the tr4 reads over more banks)
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const int r = 32 * k + (lane >> 1);
           const int rr = r < lim ? r : lim;
-          vo[k] = rr * 64 + 16 * ((lane & 3) ^ ((k ^ (lane >> 4)) & 3));
-          ko[k] = rr * 64 + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
+          lds_dma16(kb, rr * 32 + 16 * (lane & 1), st + kStageK + 1024 * k);
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const int r = 32 * k + (lane >> 1);
+          const int rr = r < lim ? r : lim;
+          lds_dma16(vb, rr * 32 + 16 * ((lane & 1) ^ ((r >> 4) & 1)), st + kStageV + 1024 * k);
         }
       }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) lds_dma16(kb, ko[k], st + kStageK + 1024 * k);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) lds_dma16(vb, vo[k], st + kStageV + 1024 * k);
       lds_dma2(sb, so, st + kStageVS);
     } else {
       const int64_t f0 = tt * kMini;
@@ -240,11 +295,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     else qraw_s[wave][lane] = 0u;
     lds_dma4(p.mid.k_scale + bkv * kD + 2 * lane, ka);
   }
+  auto ops_of = [&](int i) { return i < n_w ? (t0 + wave + kWaves * i < nFt ? kOpsF16 : kOps) : 0; };
+  // s_waitcnt needs an immediate: the outstanding-op counts that can occur
+  auto wait_vm = [&](int n) {
+    if (n == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    else if (n == kOps) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kOps));
+    else if (n == kOpsF16) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kOpsF16));
+    else if (n == 2 * kOps) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kOps));
+    else if (n == kOps + kOpsF16) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kOps + kOpsF16));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kOpsF16));
+  };
   if (n_w > 0) issue(t0 + wave, st0);
   if (n_w > 1) issue(t0 + wave + kWaves, st1);
-  if (n_w > 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kOpsPerTile));
-  else if (n_w > 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kOpsPerTile));
-  else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  wait_vm(ops_of(0) + ops_of(1));  // the query and K-scale loads have landed
   __builtin_amdgcn_wave_barrier();
 
   // ---- query digits: wave h handles head h (channels 2*lane, 2*lane+1) ----
@@ -261,13 +324,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       // channel d -> k-step d/16, operand byte j (see the K operand assembly below)
       const int d = 2 * lane + e;
       const int ksd = d >> 4, r = d & 15;
-      const int j = 4 * (2 * (r >> 3) + (r & 1)) + ((r & 7) >> 1);
+      const int j = BITS == 4 ? 4 * (2 * (r >> 3) + (r & 1)) + ((r & 7) >> 1) : 4 * (r & 3) + (r >> 2);
       const int hi = (qi[e] + 128) >> 8;
       const int lo = qi[e] - 256 * hi;
       qd_s[(2 * ksd + 0) * 64 + h * 16 + j] = static_cast<uint8_t>(hi & 0xFF);
       qd_s[(2 * ksd + 1) * 64 + h * 16 + j] = static_cast<uint8_t>(lo & 0xFF);
     }
-    if (lane == 0) qsc_s[h] = mx > 0.0f ? (mx / kQMax) * p.scale_log2 * 0.0625f : 0.0f;
+    // the K operand carries 16*c (4-bit) or 64*c (2-bit)
+    if (lane == 0) qsc_s[h] = mx > 0.0f ? (mx / kQMax) * p.scale_log2 * (BITS == 4 ? 0.0625f : 0.015625f) : 0.0f;
     if (tid < 4) reinterpret_cast<uint32_t*>(&qd_s[kQdZero])[tid] = 0u;
   }
   __syncthreads();
@@ -343,7 +407,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(sp + kStageV);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      const int col = 16 * c + (n16 ^ 1);
+      const int col = out_channel<BITS>(c, n16);
       const f16x4 vb = {__builtin_bit_cast(_Float16, v16[(4 * g + 0) * kD + col]),
                         __builtin_bit_cast(_Float16, v16[(4 * g + 1) * kD + col]),
                         __builtin_bit_cast(_Float16, v16[(4 * g + 2) * kD + col]),
@@ -352,7 +416,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   };
 
-  // ---- packed INT4 tile from a ring stage ----
+  // ---- packed tile from a ring stage ----
   // tr4 read addresses: as source lane s' = n16 of group g this lane fetches
   // row 16*sigma + 4g + i, where slot k = ((s'&3)<<1)|((s'>>2)&1) of pair s'>>3
   // gives sigma = 2*(s'>>3) + (k>>2), i = k&3.
@@ -361,34 +425,65 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int kk = ((n16 & 3) << 1) | ((n16 >> 2) & 1);
     const int sigma = 2 * (n16 >> 3) + (kk >> 2);
     const int r = 16 * sigma + 4 * g + (kk & 3);
-    const int sw = (sigma ^ g) & 3;
+    if (BITS == 4) {
+      const int sw = (sigma ^ g) & 3;
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) vrd[qq] = kStageV + 16 * (4 * r + (qq ^ sw));
+      for (int qq = 0; qq < 4; ++qq) vrd[qq] = kStageV + 16 * (4 * r + (qq ^ sw));
+    } else {
+      // chunk c4 (8 bytes) of row r: unit c4/2 at position (c4/2) ^ (sigma & 1)
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) vrd[c4] = kStageV + 32 * r + 16 * ((c4 >> 1) ^ (sigma & 1)) + 8 * (c4 & 1);
+    }
   }
   uint32_t krd[4];  // K row `lane`, 16-byte unit q
 #pragma unroll
-  for (int qq = 0; qq < 4; ++qq) krd[qq] = kStageK + 16 * (4 * lane + (qq ^ ((lane >> 2) & 3)));
+  for (int qq = 0; qq < 4; ++qq)
+    krd[qq] = BITS == 4 ? kStageK + 16 * (4 * lane + (qq ^ ((lane >> 2) & 3))) : kStageK + 32 * lane + 16 * (qq & 1);
   const uint32_t vs_rd = kStageVS + 4 * (16 * sq + 4 * g);
   const uint32_t z = 0u;
-  uint32_t vmask, vcst;  // register-resident constants of v_nibbles_to_f16
-  asm volatile("s_mov_b32 %0, 0x00F000F0" : "=s"(vmask));
-  asm volatile("v_mov_b32 %0, 0x54805480" : "=v"(vcst));
-  const f16x8 b72 = __builtin_bit_cast(f16x8, u32x4{0x54805480u, 0x54805480u, 0x54805480u, 0x54805480u});
+  uint32_t vmask, vcst;  // register-resident constants of the V code conversion
+  if (BITS == 4) {
+    asm volatile("s_mov_b32 %0, 0x00F000F0" : "=s"(vmask));
+    asm volatile("v_mov_b32 %0, 0x54805480" : "=v"(vcst));
+  } else {
+    asm volatile("s_mov_b32 %0, 0x03000300" : "=s"(vmask));
+    asm volatile("v_mov_b32 %0, 0x46004600" : "=v"(vcst));
+  }
+  // per-token offset of the fp16 V values: 72 (4-bit) or 6 (2-bit)
+  const uint32_t offv = BITS == 4 ? 0x54805480u : 0x46004600u;
+  const f16x8 boff = __builtin_bit_cast(f16x8, u32x4{offv, offv, offv, offv});
 
   auto packed_tile = [&](int64_t t, const lds_u8* sp) {
-    // QK^T: A = K codes of token `lane` as int8 16*c (high nibbles: AND; low: shift + AND)
+    // QK^T: A = K codes of token `lane` as int8 (16*c or 64*c)
     i32x4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
+    if (BITS == 4) {
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      const u32x4 kv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + krd[qq]);
+      for (int qq = 0; qq < 4; ++qq) {
+        const u32x4 kv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + krd[qq]);
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const int ks = 2 * qq + h2;
-        const uint32_t w0 = kv[2 * h2], w1 = kv[2 * h2 + 1];
-        const i32x4 a = {static_cast<int>(w0 & 0xF0F0F0F0u), static_cast<int>((w0 << 4) & 0xF0F0F0F0u),
-                         static_cast<int>(w1 & 0xF0F0F0F0u), static_cast<int>((w1 << 4) & 0xF0F0F0F0u)};
-        chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdh[ks], chi, 0, 0, 0);
-        clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdl[ks], clo, 0, 0, 0);
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const int ks = 2 * qq + h2;
+          const uint32_t w0 = kv[2 * h2], w1 = kv[2 * h2 + 1];
+          const i32x4 a = {static_cast<int>(w0 & 0xF0F0F0F0u), static_cast<int>((w0 << 4) & 0xF0F0F0F0u),
+                           static_cast<int>(w1 & 0xF0F0F0F0u), static_cast<int>((w1 << 4) & 0xF0F0F0F0u)};
+          chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdh[ks], chi, 0, 0, 0);
+          clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdl[ks], clo, 0, 0, 0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int qq = 0; qq < 2; ++qq) {
+        const u32x4 kv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + krd[qq]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // k-step 4qq+e: dword i, byte j <-> channel 16ks + 4j + i
+          const int ks = 4 * qq + e;
+          const uint32_t w = kv[e];
+          const i32x4 a = {static_cast<int>(w & 0xC0C0C0C0u), static_cast<int>((w << 2) & 0xC0C0C0C0u),
+                           static_cast<int>((w << 4) & 0xC0C0C0C0u), static_cast<int>((w << 6) & 0xC0C0C0C0u)};
+          chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdh[ks], chi, 0, 0, 0);
+          clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdl[ks], clo, 0, 0, 0);
+        }
       }
     }
     const int64_t m0 = (t - nFt) * kTile;
@@ -411,25 +506,41 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     const f16x8 a0 = __builtin_bit_cast(f16x8, u32x4{sq == 0 ? pk0 : z, sq == 0 ? pk1 : z, sq == 1 ? pk0 : z, sq == 1 ? pk1 : z});
     const f16x8 a1 = __builtin_bit_cast(f16x8, u32x4{sq == 2 ? pk0 : z, sq == 2 ? pk1 : z, sq == 3 ? pk0 : z, sq == 3 ? pk1 : z});
+    if (BITS == 4) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const i32x2 xv = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
-          reinterpret_cast<lds_i32x2*>(const_cast<lds_u8*>(sp) + vrd[c >> 1] + 8 * (c & 1)));
-      uint32_t b0[4], b1[4];
-      v_nibbles_to_f16(static_cast<uint32_t>(xv[0]), vmask, vcst, b0);
-      v_nibbles_to_f16(static_cast<uint32_t>(xv[1]), vmask, vcst, b1);
-      acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(f16x8, b0), acc[c], 0, 0, 0);
-      acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(f16x8, b1), acc[c], 0, 0, 0);
+      for (int c = 0; c < 8; ++c) {
+        const i32x2 xv = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
+            reinterpret_cast<lds_i32x2*>(const_cast<lds_u8*>(sp) + vrd[c >> 1] + 8 * (c & 1)));
+        uint32_t b0[4], b1[4];
+        v_nibbles_to_f16(static_cast<uint32_t>(xv[0]), vmask, vcst, b0);
+        v_nibbles_to_f16(static_cast<uint32_t>(xv[1]), vmask, vcst, b1);
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(f16x8, b0), acc[c], 0, 0, 0);
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(f16x8, b1), acc[c], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) {
+        const i32x2 xv = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
+            reinterpret_cast<lds_i32x2*>(const_cast<lds_u8*>(sp) + vrd[c4]));
+        uint32_t f0[4], s0[4], f1[4], s1[4];
+        v2_nibbles_to_f16(static_cast<uint32_t>(xv[0]), vmask, vcst, f0, s0);
+        v2_nibbles_to_f16(static_cast<uint32_t>(xv[1]), vmask, vcst, f1, s1);
+        acc[2 * c4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(f16x8, f0), acc[2 * c4], 0, 0, 0);
+        acc[2 * c4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(f16x8, f1), acc[2 * c4], 0, 0, 0);
+        acc[2 * c4 + 1] =
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(f16x8, s0), acc[2 * c4 + 1], 0, 0, 0);
+        acc[2 * c4 + 1] =
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(f16x8, s1), acc[2 * c4 + 1], 0, 0, 0);
+      }
     }
-    acc_off = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b72, acc_off, 0, 0, 0);
-    acc_off = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b72, acc_off, 0, 0, 0);
+    acc_off = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, boff, acc_off, 0, 0, 0);
+    acc_off = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, boff, acc_off, 0, 0, 0);
   };
 
   // ---- main loop: two stages, two tiles in flight ----
   auto step = [&](int i, const lds_u8* sp, uint32_t st) {
     const int64_t t = t0 + wave + static_cast<int64_t>(kWaves) * i;
-    if (i + 1 < n_w) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kOpsPerTile));  // tile i landed, i+1 in flight
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    wait_vm(ops_of(i + 1));  // tile i landed; tile i+1 (if any) may still be in flight
     __builtin_amdgcn_wave_barrier();
     if (t < nFt) fp16_tile(t, sp);
     else packed_tile(t, sp);
@@ -462,7 +573,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const float off = (acc_off[0] + acc_off[1]) + (acc_off[2] + acc_off[3]);
 #pragma unroll
     for (int c = 0; c < 8; ++c)
-      red_o[(wave * 4 + g) * kD + 16 * c + (n16 ^ 1)] = (((acc[c][0] + acc[c][1]) + (acc[c][2] + acc[c][3])) - off) * wsc;
+      red_o[(wave * 4 + g) * kD + out_channel<BITS>(c, n16)] =
+          (((acc[c][0] + acc[c][1]) + (acc[c][2] + acc[c][3])) - off) * wsc;
   }
   __syncthreads();
   const int n = p.n_splits;
@@ -551,7 +663,8 @@ bool fp16_tier_ok(const Fp16Tier& t) {
 }  // namespace
 
 bool int4_supports(const Params& p) {
-  if (p.mid.fmt != FADE_MID_SYM || p.mid.k_bits != 4 || p.mid.v_bits != 4 || p.mid.len <= 0) return false;
+  if (p.mid.fmt != FADE_MID_SYM || p.mid.k_bits != p.mid.v_bits || p.mid.len <= 0) return false;
+  if (p.mid.k_bits != 4 && p.mid.k_bits != 2) return false;
   if (p.G > 4) return false;
   if (!fp16_tier_ok(p.sink) || !fp16_tier_ok(p.recent)) return false;
   if (!aligned(p.q, 16) || p.q_sb % 8 || p.q_sh % 8) return false;
@@ -572,7 +685,7 @@ int int4_resident_wgs() {
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_int4_kernel, kThreads, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sym_kernel<4>, kThreads, 0) != hipSuccess ||
       cus <= 0 || per_cu <= 0) {
     (void)hipGetLastError();
     return 512;
@@ -583,7 +696,10 @@ int int4_resident_wgs() {
 
 int launch_int4(const Params& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv), static_cast<unsigned>(p.B));
-  hipLaunchKernelGGL(decode_int4_kernel, grid, dim3(kThreads), 0, st, p);
+  if (p.mid.k_bits == 4)
+    hipLaunchKernelGGL(decode_sym_kernel<4>, grid, dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL(decode_sym_kernel<2>, grid, dim3(kThreads), 0, st, p);
   return check_launch("fade_tiered_decode_attn(int4)");
 }
 

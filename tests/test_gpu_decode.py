@@ -156,6 +156,42 @@ def test_tiered_decode_rotated(dev, bits):
     assert np.abs(out - ref).max() <= ATOL
 
 
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,S,ns,nr,n_splits",
+    [
+        (1, 32, 8, 1500, 4, 64, 0),
+        (2, 8, 4, 777, 4, 64, 3),  # G=2
+        (1, 4, 1, 300, 0, 37, 1),  # one kv head, ragged recent window
+        (2, 12, 4, 2000, 4, 256, 0),  # G=3, config-2 windows
+    ],
+)
+def test_tiered_decode_sym2_fast_path(dev, B, Hq, Hkv, S, ns, nr, n_splits):
+    """Rotated 2-bit middle tier (K per channel, V per token) on the matrix-core kernel.
+
+    Attention runs in the rotated basis: q, sink and recent are rotated (fp32 x @ R^T,
+    rounded to fp16) and the oracle dequantizes the codes with R = I, so the check is
+    the kernel's attention over exactly the tiers it was given."""
+    print(f"case decode sym2 B={B} Hq={Hq} Hkv={Hkv} S={S} ns={ns} nr={nr} splits={n_splits}", flush=True)
+    R = torch.from_numpy(np.load(__file__.rsplit("/", 1)[0] + "/golden/rotation_d128_seed42.npy")).to(dev)
+    q, k, v, ns, nr = _case(B, Hq, Hkv, S, ns, nr, seed=3000 + S)
+    rot = lambda a: (torch.from_numpy(np.ascontiguousarray(a)).to(dev).float() @ R.T).to(torch.float16)  # noqa: E731
+    qr, kr, vr = rot(q), rot(k), rot(v)
+    km = torch.from_numpy(np.ascontiguousarray(k[:, :, ns : S - nr])).to(dev)
+    vm = torch.from_numpy(np.ascontiguousarray(v[:, :, ns : S - nr])).to(dev)
+    kp, ks = frq.rotated_quant_k(km, R, 2)
+    vp, vs = frq.rotated_quant_v(vm, R, 2)
+    mid = MiddleTier("sym", kp, vp, ks, vs, k_bits=2, v_bits=2)
+    sink = (kr[:, :, :ns].contiguous(), vr[:, :, :ns].contiguous()) if ns else None
+    rec = (kr[:, :, S - nr :].contiguous(), vr[:, :, S - nr :].contiguous()) if nr else None
+    out = tiered_decode_attention(qr, sink, mid, rec, kernel=2, n_splits=n_splits).float().cpu().numpy()
+    eye = np.eye(128, dtype=np.float32)
+    omid = {"fmt": "rot", "kq": kp.cpu().numpy(), "ks": ks.cpu().numpy(), "vq": vp.cpu().numpy(),
+            "vs": vs.cpu().numpy(), "R": eye, "k_bits": 2, "v_bits": 2}
+    krn, vrn, qrn = kr.cpu().numpy(), vr.cpu().numpy(), qr.cpu().numpy()
+    ref = oatt.tiered_decode(qrn, krn[:, :, :ns], vrn[:, :, :ns], omid, krn[:, :, S - nr :], vrn[:, :, S - nr :])
+    assert np.abs(out - ref).max() <= ATOL
+
+
 @pytest.mark.parametrize("bits", [4, 2])
 def test_tiered_decode_asym(dev, bits):
     print(f"case decode asym bits={bits}", flush=True)
