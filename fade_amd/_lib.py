@@ -92,6 +92,31 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", _i64),
+        ("Hq", _i64),
+        ("Hkv", _i64),
+        ("D", _i64),
+        ("Sq", _i64),
+        ("q", _p),
+        ("q_sb", _i64),
+        ("q_sh", _i64),
+        ("q_ss", _i64),
+        ("out", _p),
+        ("o_sb", _i64),
+        ("o_sh", _i64),
+        ("o_ss", _i64),
+        ("sm_scale", ctypes.c_float),
+        ("lens", _p),
+        ("order", _p),
+        ("sink", Fp16Tier),
+        ("mid", MidTier),
+        ("recent", Fp16Tier),
+        ("chunk", Fp16Tier),
+    ]
+
+
 # name -> argtypes; every function returns int (status) unless listed in _RESTYPES.
 _SIGNATURES: dict[str, list] = {
     "fade_hip_abi_version": [],
@@ -114,6 +139,7 @@ _SIGNATURES: dict[str, list] = {
     ],
     "fade_tiered_decode_workspace_bytes": [ctypes.POINTER(DecodeArgs), _pi64],
     "fade_tiered_decode_attn": [ctypes.POINTER(DecodeArgs), _p],
+    "fade_tiered_prefill_attn": [ctypes.POINTER(PrefillArgs), _p],
 }
 _RESTYPES = {"fade_hip_last_error": ctypes.c_char_p}
 

@@ -1,0 +1,97 @@
+"""Ragged tiered prefill attention (``fade_tiered_prefill_attn``).
+
+The reference has no prefill kernel: a chunk goes through
+``TieredKVCache.update`` (fade/cache.py:347-379), which returns the
+materialized ``[sink | dequantized middle | recent | chunk]`` K/V
+(fade/cache.py:683-842), and the model runs causal SDPA over it with the
+mask aligned bottom-right (the chunk is the last ``Sq`` keys).  This op reads
+the tiers in place, per batch row with its own tier lengths.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+from .tiered_attn import MiddleTier, _fp16_tier, _mid_tier
+
+
+class TieredPrefillPlan:
+    """Validated launch for fixed tensors; ``run()`` enqueues one kernel.
+
+    Args:
+        q: [B, Hq, Sq, 128] fp16 queries of the chunk.
+        chunk: (K, V) [B, Hkv, Sq, 128] fp16, the chunk's own keys/values.
+        sink, recent: (K, V) [B, Hkv, cap, 128] fp16 padded along S, or None.
+        mid: reference INT4 middle tier (``MiddleTier("int4", ...)``) with
+            codes padded to a common row count, or None.
+        lens: int32 [B, 3] (sink, middle, recent tokens used by each row);
+            default: every row uses the full capacities.
+        order: optional int32 [B] dispatch order of the batch rows (longest first).
+    """
+
+    def __init__(
+        self,
+        q: Tensor,
+        chunk: tuple[Tensor, Tensor],
+        sink: tuple[Tensor, Tensor] | None = None,
+        mid: MiddleTier | None = None,
+        recent: tuple[Tensor, Tensor] | None = None,
+        lens: Tensor | None = None,
+        order: Tensor | None = None,
+        sm_scale: float | None = None,
+        out: Tensor | None = None,
+    ) -> None:
+        if q.dim() != 4:
+            raise ValueError(f"q must be [B, Hq, Sq, D], got {tuple(q.shape)}")
+        tensors = [q, *chunk] + ([*sink] if sink else []) + ([*recent] if recent else []) + (mid.tensors() if mid else [])
+        _lib.require_gpu(*tensors, op="tiered_prefill_attention")
+        _lib.require_f16(q, "tiered_prefill_attention")
+        B, Hq, Sq, D = q.shape
+        Hkv = int(chunk[0].shape[1])
+        if tuple(chunk[0].shape) != (B, Hkv, Sq, D) or chunk[1].shape != chunk[0].shape:
+            raise ValueError(f"chunk K/V must be [B, Hkv, Sq={Sq}, D]")
+        if mid is not None and mid.fmt not in ("int4", "sym"):
+            raise ValueError("the prefill kernel reads the reference INT4 middle tier")
+        if q.stride(-1) != 1:
+            q = q.contiguous()
+        caps = [int(sink[0].shape[2]) if sink else 0, mid.n_tokens if mid else 0, int(recent[0].shape[2]) if recent else 0]
+        if lens is None:
+            lens = torch.tensor([caps] * B, dtype=torch.int32, device=q.device)
+        lens = lens.to(device=q.device, dtype=torch.int32).contiguous()
+        if tuple(lens.shape) != (B, 3):
+            raise ValueError(f"lens must be int32 [B={B}, 3]")
+        if order is not None:
+            order = order.to(device=q.device, dtype=torch.int32).contiguous()
+        if out is None:
+            out = torch.empty(B, Hq, Sq, D, dtype=torch.float16, device=q.device)
+        self._keep = (q, chunk, sink, mid, recent, lens, order, out)
+        a = _lib.PrefillArgs()
+        a.B, a.Hq, a.Hkv, a.D, a.Sq = B, Hq, Hkv, D, Sq
+        a.q, a.q_sb, a.q_sh, a.q_ss = q.data_ptr(), q.stride(0), q.stride(1), q.stride(2)
+        a.out, a.o_sb, a.o_sh, a.o_ss = out.data_ptr(), out.stride(0), out.stride(1), out.stride(2)
+        a.sm_scale = float(1.0 / math.sqrt(D) if sm_scale is None else sm_scale)
+        a.lens = lens.data_ptr()
+        a.order = order.data_ptr() if order is not None else None
+        a.sink, a.mid, a.recent, a.chunk = _fp16_tier(sink), _mid_tier(mid), _fp16_tier(recent), _fp16_tier(chunk)
+        self.args = a
+        self.out = out
+        self._fn = _lib.load().fade_tiered_prefill_attn
+        self._argp = ctypes.byref(a)
+
+    def run(self, stream: int | None = None) -> Tensor:
+        s = torch.cuda.current_stream(self.out.device).cuda_stream if stream is None else stream
+        _lib.check(self._fn(self._argp, s), "fade_tiered_prefill_attn")
+        return self.out
+
+
+def tiered_prefill_attention(q, chunk, sink=None, mid=None, recent=None, lens=None, order=None, sm_scale=None) -> Tensor:
+    """Causal attention of a chunk over each row's tiered cache; returns fp16 [B, Hq, Sq, 128]."""
+    return TieredPrefillPlan(q, chunk, sink, mid, recent, lens, order, sm_scale).run()
+
+
+__all__ = ["TieredPrefillPlan", "tiered_prefill_attention"]

@@ -169,6 +169,33 @@ typedef struct fade_decode_args {
 int fade_tiered_decode_workspace_bytes(const fade_decode_args* args, int64_t* bytes);
 int fade_tiered_decode_attn(const fade_decode_args* args, void* stream);
 
+/* ---------------- ragged tiered prefill attention -------------------------- */
+/* A chunk of Sq new tokens per batch row attends to that row's cache
+ * [sink | middle | recent] followed by the chunk itself, bottom-right causal:
+ * query j of row b sees cache tokens and chunk tokens 0..j.  Tier tensors are
+ * padded along S (row b uses the first lens[3b+0..2] tokens of sink / middle /
+ * recent); the middle tier is FADE_MID_SYM 4-bit or FADE_MID_NONE.  D = 128,
+ * Hq/Hkv <= 4.  `order` (optional, device int32 [B]) lists batch rows in the
+ * order their workgroups are dispatched (longest first balances the tail).
+ * Replaces the reference's prefill path: update() returning the materialized
+ * tiers (fade/cache.py:347-379,683-842) followed by causal SDPA in the model. */
+typedef struct fade_prefill_args {
+  int64_t B, Hq, Hkv, D, Sq;
+  const void* q;  /* [B,Hq,Sq,D] fp16 */
+  int64_t q_sb, q_sh, q_ss;
+  void* out;      /* [B,Hq,Sq,D] fp16 */
+  int64_t o_sb, o_sh, o_ss;
+  float sm_scale;
+  const int32_t* lens;  /* device [B][3]: sink, middle, recent tokens of each row */
+  const int32_t* order; /* device [B] or NULL */
+  fade_fp16_tier sink;  /* len = padded capacity */
+  fade_mid_tier mid;    /* len = padded capacity (rows of the code tensors) */
+  fade_fp16_tier recent;
+  fade_fp16_tier chunk; /* the chunk's own K/V, len = Sq */
+} fade_prefill_args;
+
+int fade_tiered_prefill_attn(const fade_prefill_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

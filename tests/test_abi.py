@@ -59,6 +59,32 @@ def test_ctypes_struct_layout_matches_c(tmp_path):
     assert got == want
 
 
+def test_prefill_struct_layout_matches_c(tmp_path):
+    src = tmp_path / "layout_p.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "fade_hip.h"\n'
+        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu\\n\", sizeof(fade_prefill_args),"
+        " offsetof(fade_prefill_args, sm_scale), offsetof(fade_prefill_args, lens), offsetof(fade_prefill_args, sink),"
+        " offsetof(fade_prefill_args, mid), offsetof(fade_prefill_args, chunk)); return 0;}\n"
+    )
+    exe = tmp_path / "layout_p"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    A = _lib.PrefillArgs
+    assert got == [ctypes.sizeof(A), A.sm_scale.offset, A.lens.offset, A.sink.offset, A.mid.offset, A.chunk.offset]
+
+
+def test_prefill_argument_errors():
+    lib = _lib.load()
+    a = _lib.PrefillArgs()
+    a.B, a.Hq, a.Hkv, a.D, a.Sq = 2, 32, 4, 128, 16
+    assert lib.fade_tiered_prefill_attn(ctypes.byref(a), None) == _lib.FADE_EINVAL
+    assert b"Hq/Hkv <= 4" in lib.fade_hip_last_error()
+    a.Hkv = 8
+    assert lib.fade_tiered_prefill_attn(ctypes.byref(a), None) == _lib.FADE_EINVAL
+    assert b"null q, out or lens" in lib.fade_hip_last_error()
+
+
 def test_argument_errors_come_back_as_value_errors():
     """Validation runs before any GPU work, so it is testable without a device."""
     lib = _lib.load()
