@@ -111,6 +111,37 @@ def time_plans(plans, steps: int, warmup: int, stream):
     return wall_ms / steps, float(np.median(per_call)), float(per_call.mean()), span_ms / steps
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_case(dev, seed: int = 1004):
+    """Config 4: 32 rows, cached lengths ~U[512, 16384], 128-token chunk, 32/8 heads, reference INT4
+    middle tier (sink 4, recent 64).  Codes, scales and fp16 tiers are random device tensors (the
+    kernel's timing does not depend on their values); rows are dispatched longest first."""
+    from fade_amd.kernels.prefill import TieredPrefillPlan
+
+    B, Hq, Hkv, D, Sq, ns, nr = 32, 32, 8, 128, 128, 4, 64
+    gen = torch.Generator().manual_seed(seed)
+    L = torch.randint(512, 16385, (B,), generator=gen)
+    nm = L - ns - nr
+    cap = int(nm.max())
+    g = torch.Generator(device=dev).manual_seed(seed)
+    rnd = lambda *shape: torch.randn(*shape, generator=g, device=dev).to(torch.float16)  # noqa: E731
+    codes = lambda: torch.randint(0, 256, (B, Hkv, cap, D // 2), generator=g, device=dev, dtype=torch.uint8)  # noqa: E731
+    from fade_amd.kernels import MiddleTier
+
+    mid = MiddleTier("int4", codes(), codes(), (rnd(B, Hkv, 1, D).abs() * 0.3 + 0.05), (rnd(B, Hkv, cap, 1).abs() * 0.3 + 0.05))
+    lens = torch.stack([torch.full((B,), ns), nm, torch.full((B,), nr)], dim=1).to(torch.int32)
+    order = torch.argsort(L, descending=True).to(torch.int32)
+    plan = TieredPrefillPlan(rnd(B, Hq, Sq, D), (rnd(B, Hkv, Sq, D), rnd(B, Hkv, Sq, D)), (rnd(B, Hkv, ns, D), rnd(B, Hkv, ns, D)),
+                             mid, (rnd(B, Hkv, nr, D), rnd(B, Hkv, nr, D)), lens=lens, order=order)
+    # useful MACs: every (query head, query j) row against its L_b + j + 1 visible keys, QK^T and PV
+    j = torch.arange(Sq, dtype=torch.float64)
+    flops = float(sum(Hq * (L[b] + j + 1).sum() * D * 4 for b in range(B)))
+    nbytes = int(B * Hkv * (nm.sum() / B * D + 2 * D + 2 * nm.sum() / B + (ns + nr + Sq) * D * 4) + 2 * B * Hq * Sq * D * 2)
+    return plan, flops, nbytes
+
+
 def cpu_baseline(cfg, seed: int):
     """The oracle's dequantize + concatenate + fp32 SDPA on a bounded sample (two batch rows)."""
     from oracle import attention as oatt
@@ -257,6 +288,15 @@ def main() -> int:
             "int4_speedup": round(fmean / mean_ms, 2),
         }
         del fp
+        torch.cuda.empty_cache()
+        pf, pflops, pbytes = prefill_case(dev)
+        _, _, pmean, _ = time_plans([pf], max(10, args.steps // 10), 5, stream)
+        extra["c4_prefill_ragged"] = {
+            "us": round(pmean * 1e3, 1), "TFLOPs": round(pflops / (pmean * 1e-3) / 1e12, 1),
+            "mfma_frac_f16_dense": round(pflops / (pmean * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 3),
+            "useful_flops": pflops, "GBps": round(pbytes / (pmean * 1e-3) / 1e9, 1),
+        }
+        del pf
         torch.cuda.empty_cache()
         c2 = CONFIGS[2]
         for fmt in ("k4v2", "int4", "rot2"):
