@@ -48,6 +48,9 @@ def decode_bytes(cfg, fmt: str) -> int:
         per_head += mid * D // 2 + 2 * D + pad * D + (pad // 64) * D * 2
     elif fmt == "rot2":  # rotated K2/V2: 2-bit packed codes, K per-channel + V per-token scales
         per_head += mid * D // 4 * 2 + 2 * D + 2 * mid
+    elif fmt.startswith("asym"):  # asym group-32 "asymKV": codes + fp16 scale and zero per token and group
+        kb, vb = int(fmt[4]), int(fmt[5])
+        per_head += mid * (D * kb // 8 + D * vb // 8 + 2 * (D // 32) * 2 * 2)
     elif fmt == "fp16":
         per_head += mid * D * 4
     return cfg.B * cfg.Hkv * per_head + 2 * cfg.B * cfg.Hq * D * 2
@@ -77,6 +80,11 @@ def build_instances(cfg, fmt: str, dev, seed: int, n: int):
         vq, vs = frq.rotated_quant_v(vm, R, 2)
         mid = MiddleTier("sym", kq, vq, ks, vs, k_bits=2, v_bits=2)
         pre = R
+    elif fmt.startswith("asym"):
+        kb, vb = int(fmt[4]), int(fmt[5])
+        kq, ks, kz = fq.quant_asym(km, kb, 32)
+        vq, vs, vz = fq.quant_asym(vm, vb, 32)
+        mid = MiddleTier("asym", kq, vq, ks, vs, kz, vz, k_bits=kb, v_bits=vb, group=32)
     else:
         mid = MiddleTier("fp16", km, vm)
     del kd, vd
@@ -223,7 +231,7 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
         rows = per_kernel(d, counter)
         # the calibration copies are the three largest copy dispatches of the run
         copy = sorted((v for k, v in rows if "copy" in k.lower()), reverse=True)[:3]
-        dec = [v for k, v in rows if "decode_int4_kernel" in k]
+        dec = [v for k, v in rows if "decode_packed_kernel" in k]
         if len(copy) < 3 or not dec:
             raise SystemExit(f"{counter}: calibration copy or decode kernel missing in {d}")
         copy_kib = float(np.median(copy))
@@ -289,6 +297,16 @@ def main() -> int:
         }
         del fp
         torch.cuda.empty_cache()
+        # config 1 in the format BASELINE states (asymmetric group-32 INT4 K and V)
+        pa = build_instances(cfg, "asym44", dev, 1001, N_INSTANCES)
+        _, _, amean, _ = time_plans(pa, args.steps, args.warmup, stream)
+        ab = decode_bytes(cfg, "asym44")
+        extra["c1_asym_g32_k4v4"] = {
+            "us": round(amean * 1e3, 2), "GBps": round(ab / (amean * 1e-3) / 1e9, 1), "bytes": ab,
+            "frac_of_peak": round(ab / (amean * 1e-3) / 1e9 / HBM_PEAK_GBPS, 3),
+        }
+        del pa
+        torch.cuda.empty_cache()
         pf, pflops, pbytes = prefill_case(dev)
         _, _, pmean, _ = time_plans([pf], max(10, args.steps // 10), 5, stream)
         extra["c4_prefill_ragged"] = {
@@ -299,7 +317,7 @@ def main() -> int:
         del pf
         torch.cuda.empty_cache()
         c2 = CONFIGS[2]
-        for fmt in ("k4v2", "int4", "rot2"):
+        for fmt in ("asym42", "k4v2", "int4", "rot2"):  # asym42: the format BASELINE states for config 2
             pl = build_instances(c2, fmt, dev, 1002, N_INSTANCES)
             _, m2, mean2, _ = time_plans(pl, max(20, args.steps // 2), args.warmup, stream)
             b2 = decode_bytes(c2, fmt)
@@ -341,7 +359,7 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
             "algorithmic_bytes_per_call": nbytes,
-            "timed": "HIP events around each call on the launch stream (one kernel: decode_int4_kernel, split merge fused)",
+            "timed": "HIP events around each call on the launch stream (one kernel: decode_packed_kernel<4,4,false>, split merge fused)",
             "median_us": round(med_ms * 1e3, 2),
         },
         "extra": extra,

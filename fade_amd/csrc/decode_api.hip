@@ -161,7 +161,7 @@ Plan make_plan(const fade_decode_args* a, const Params& p) {
     // about the same bytes (8 KB), so splits take equal tile counts.
     const int64_t nT = int4_tiles(p);
     const int64_t pairs = a->B * a->Hkv;
-    int64_t want = a->n_splits > 0 ? a->n_splits : (int4_resident_wgs() + pairs / 2) / pairs;
+    int64_t want = a->n_splits > 0 ? a->n_splits : (int4_resident_wgs(p) + pairs / 2) / pairs;
     if (want > nT) want = nT;
     if (want < 1) want = 1;
     pl.tiles_per_split = cdiv(nT, want);

@@ -80,12 +80,13 @@ int launch_valu(const Params& p, hipStream_t st);
 // Matrix-core kernel; returns FADE_EINVAL when the middle format is not handled.
 int launch_mfma(const Params& p, hipStream_t st);
 bool mfma_supports(const Params& p);
-// INT4 (reference format, K4/V4 symmetric) kernel for GQA groups of <= 4 heads,
-// with the split merge fused in (no combine launch).
+// Packed-tier kernel for GQA groups of <= 4 heads (reference INT4 and rotated
+// 2-bit formats, asymmetric group-32 formats), with the split merge fused in
+// (no combine launch).
 bool int4_supports(const Params& p);
 int int4_fp16_tiles(const Params& p);
 int64_t int4_tiles(const Params& p);
-int int4_resident_wgs();
+int int4_resident_wgs(const Params& p);  // resident workgroups of the kernel instance for p
 int launch_int4(const Params& p, hipStream_t st);
 int mfma_tile();
 // Number of 64-token tiles the matrix-core kernel walks (fp16 tokens, then packed).

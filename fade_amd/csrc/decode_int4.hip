@@ -1,6 +1,7 @@
-// Matrix-core decode attention over a reference-format INT4 middle tier
-// (per-channel K scales, per-token V scales; fade/quant.py:61-92) for GQA
-// groups of up to four query heads per kv head, gfx950.
+// Matrix-core decode attention over a packed middle tier for GQA groups of up
+// to four query heads per kv head, gfx950: the reference INT4 format
+// (per-channel K scales, per-token V scales; fade/quant.py:61-92), the rotated
+// 2-bit format, and the asymmetric group-32 build formats.
 //
 // Workgroup = 4 wavefronts serving one (batch row, kv head, split); wave w
 // walks tiles w, w+4, ... of the split with its own online softmax; the four
@@ -40,6 +41,16 @@
 // channels of 16 tokens (one nibble = two codes), each code becomes the fp16
 // value 4 + u (u = c + 2 in mantissa bits 8..9), the per-token offset is 6.
 //
+// Asymmetric group-32 formats (build format; per-token scale and zero for
+// each 32-channel group, unsigned codes): the K operand carries the codes as
+// offset binary (16*(u - 8) or 64*(u - 2), one extra XOR folded into the
+// AND), the QK^T MFMAs accumulate each channel group separately, and the
+// score is sum_g s_g * qsc * (hi*256 + lo + 128*sum(q digits of g)) plus
+// sum_g z_g * sum(q of g).  On the V side P is multiplied by each group's
+// per-token scale (four P' operands) and the zero points accumulate
+// lane-locally as sum_t p_t * z_t,g.  The query digits are read from LDS
+// per tile (registers go to the per-group accumulators instead).
+//
 // fp16 tokens (sink + recent) form 16-token tiles handled with f16 MFMAs in
 // the same fragment layout (sub-tile 0 only).
 #include <math.h>
@@ -63,14 +74,22 @@ constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kTile = 64;                // tokens of a packed tile
 constexpr int kMini = 16;                // tokens of an fp16 tile
-// One ring stage holds one tile: K codes [64 rows][64 B] (fp16 tile: K rows
-// [16][256 B]) | V codes (fp16 tile: V rows) | V scales, one dword per token.
-constexpr int kStageK = 0, kStageV = 4096, kStageVS = 8192;
-constexpr int kStageBytes = 8192 + 256;
-constexpr int kOpsF16 = 9;               // direct-to-LDS loads issued per fp16 tile
-// ... and per packed tile: K + V codes in 1 KB loads, plus one for the V scales
-template <int BITS>
-constexpr int ops_packed() { return BITS == 4 ? 9 : 5; }
+constexpr int kGroups = 4;               // 32-channel groups of the asymmetric formats
+// One ring stage holds one tile: K codes at 0 (fp16 tile: K rows [16][256 B]),
+// V codes at 4096 (fp16 tile: V rows [16][256 B]), then the per-token metadata:
+// reference formats: V scales, one dword per token, at 8192;
+// asymmetric formats: K scale | K zero | V scale | V zero, [64 tokens][4 groups]
+// fp16 each, right after the V codes.
+constexpr int kStageK = 0, kStageV = 4096;
+template <int KB, int VB, bool ASYM>
+struct Stage {
+  static constexpr int kMeta = ASYM ? kStageV + 1024 * VB : 8192;
+  static constexpr int kBytes = ASYM ? (kMeta + 2048 > 8192 ? kMeta + 2048 : 8192) : 8192 + 256;
+  // direct-to-LDS loads per packed tile (K and V codes in 1 KB loads, then the
+  // metadata: one 2-byte load, or eight dword loads) and per fp16 tile
+  static constexpr int kOps = KB + VB + (ASYM ? 8 : 1);
+  static constexpr int kOpsF16 = ASYM ? 8 : 9;
+};
 constexpr int kQdZero = 8 * 2 * 4 * 16;  // zero operand after the [ks][digit][head][16 B] query digits
 constexpr float kQMax = 32000.0f;
 constexpr float kNegBig = -1.0e30f;      // running-max sentinel (finite: no inf - inf)
@@ -96,6 +115,10 @@ __device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint
 }
 __device__ __forceinline__ void lds_dma2(const void* sbase, uint32_t voff, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_ushort %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
                : "memory", "m0");
 }
 
@@ -156,12 +179,19 @@ __device__ __forceinline__ float load_agent(const float* p) {
                                                      __HIP_MEMORY_SCOPE_AGENT));
 }
 
-// LDS (two 8.25 KB ring stages per wave, ~71 KB per workgroup) allows two
-// workgroups per CU; registers are sized for that (two waves per SIMD).
-template <int BITS>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_sym_kernel(Params p) {
-  constexpr int kOps = ops_packed<BITS>();
-  constexpr int kRowBytes = 128 * BITS / 8;  // packed row of one token
+__device__ __forceinline__ float half_of(uint32_t dw, int hi) {
+  return h2f(static_cast<uint16_t>(hi ? dw >> 16 : dw & 0xFFFFu));
+}
+
+// LDS: two ring stages per wave (8.25 KB for the reference formats, 8 or 10 KB
+// for the asymmetric ones); at <= 80 KB per workgroup two workgroups share a
+// CU, and registers are sized for that (two waves per SIMD).
+template <int KB, int VB, bool ASYM>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_packed_kernel(
+    Params p) {
+  using S = Stage<KB, VB, ASYM>;
+  constexpr int kOps = S::kOps, kOpsF16 = S::kOpsF16, kMeta = S::kMeta;
+  constexpr int kRowK = 16 * KB, kRowV = 16 * VB;  // packed row bytes of one token
   const int split = blockIdx.x;
   const int64_t kvh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -179,18 +209,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // this wave's tiles: t0 + wave + 4i, i < n_w
   const int n_w = t0 + wave < t1 ? static_cast<int>((t1 - t0 - wave + kWaves - 1) / kWaves) : 0;
 
-  __shared__ __attribute__((aligned(16))) uint8_t ring0[kWaves][kStageBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t ring1[kWaves][kStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t ring0[kWaves][S::kBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t ring1[kWaves][S::kBytes];
   __shared__ __attribute__((aligned(16))) uint32_t qraw_s[4][kD / 2];  // fp16 query rows
-  __shared__ __attribute__((aligned(16))) uint32_t ksraw_s[kWaves][kD / 2];  // K scales (one copy per wave)
+  __shared__ __attribute__((aligned(16))) uint32_t ksraw_s[ASYM ? 1 : kWaves][kD / 2];  // K scales per wave
   __shared__ __attribute__((aligned(16))) uint8_t qd_s[kQdZero + 16];
   __shared__ float qsc_s[4];
+  __shared__ int qoff_s[4][kGroups];    // asymmetric: 128 * sum of the query digits of a group
+  __shared__ float qg_s[4][kGroups];    // asymmetric: sum of the query of a group (log2 domain)
   __shared__ float red_m[kWaves][4], red_l[kWaves][4];
   __shared__ int last_s;
 
-  const uint8_t* kc = p.mid.k_codes + bkv * M * kRowBytes;
-  const uint8_t* vc = p.mid.v_codes + bkv * M * kRowBytes;
-  const uint16_t* vsg = p.mid.v_scale + bkv * M;
+  const uint8_t* kc = p.mid.k_codes + bkv * M * kRowK;
+  const uint8_t* vc = p.mid.v_codes + bkv * M * kRowV;
+  // reference formats: V scale per token; asymmetric: [token][4 groups] scale / zero
+  const uint16_t* vsg = p.mid.v_scale + bkv * M * (ASYM ? kGroups : 1);
+  const uint16_t* ksg = ASYM ? p.mid.k_scale + bkv * M * kGroups : nullptr;
+  const uint16_t* kzg = ASYM ? p.mid.k_zero + bkv * M * kGroups : nullptr;
+  const uint16_t* vzg = ASYM ? p.mid.v_zero + bkv * M * kGroups : nullptr;
   // fp16 tiers as (uniform) locals: the lambdas below must not read the kernel
   // arguments through a pointer (that becomes a per-lane global load whose
   // compiler-inserted vmcnt wait would also wait for the tile prefetches).
@@ -219,7 +255,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const uint32_t st1 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sp1)));
 
   // ---- loads of one tile into a ring stage (kOps per packed tile, kOpsF16 per fp16 tile) ----
-  // Packed tile: 16-byte unit q of K row r at LDS unit 4r + (q ^ ((r >> 2) & 3)),
+  // Packed tile, 4-bit codes: 16-byte unit q of K row r at LDS unit 4r + (q ^ ((r >> 2) & 3)),
   // of V row r at 4r + (q ^ ((r >> 4) ^ (r >> 2)) & 3); rows past the tier are
   // clamped to its last row (masked later).  fp16 tile: K row r unit u at
   // 16r + (u ^ r), V rows unswizzled.
@@ -232,36 +268,44 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   auto issue = [&](int64_t tt, uint32_t st) {
     if (tt >= nFt) {
       const int64_t m0 = (tt - nFt) * kTile;
-      const uint8_t* kb = kc + m0 * kRowBytes;
-      const uint8_t* vb = vc + m0 * kRowBytes;
-      const uint16_t* sb = vsg + m0;
+      const uint8_t* kb = kc + m0 * kRowK;
+      const uint8_t* vb = vc + m0 * kRowV;
       const int lim = m0 + kTile > M ? static_cast<int>(M - 1 - m0) : kTile - 1;
-      const uint32_t so = 2u * (lane < lim ? lane : lim);
-      if (BITS == 4) {
-        uint32_t vo[4] = {voff[0], voff[1], voff[2], voff[3]};
+      if (KB == 4) {
         uint32_t ko[4] = {koff[0], koff[1], koff[2], koff[3]};
         if (lim < kTile - 1) {
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             const int r = 16 * k + (lane >> 2);
             const int rr = r < lim ? r : lim;
-            vo[k] = rr * 64 + 16 * ((lane & 3) ^ ((k ^ (lane >> 4)) & 3));
             ko[k] = rr * 64 + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
           }
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k) lds_dma16(kb, ko[k], st + kStageK + 1024 * k);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) lds_dma16(vb, vo[k], st + kStageV + 1024 * k);
       } else {
-        // 32-byte rows: K row r at 32r (natural order); V row r unit u at
-        // 2r + (u ^ ((r >> 4) & 1)) (spreads the tr4 reads over more banks)
+        // 32-byte K rows in natural order
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           const int r = 32 * k + (lane >> 1);
           const int rr = r < lim ? r : lim;
           lds_dma16(kb, rr * 32 + 16 * (lane & 1), st + kStageK + 1024 * k);
         }
+      }
+      if (VB == 4) {
+        uint32_t vo[4] = {voff[0], voff[1], voff[2], voff[3]};
+        if (lim < kTile - 1) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int r = 16 * k + (lane >> 2);
+            const int rr = r < lim ? r : lim;
+            vo[k] = rr * 64 + 16 * ((lane & 3) ^ ((k ^ (lane >> 4)) & 3));
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) lds_dma16(vb, vo[k], st + kStageV + 1024 * k);
+      } else {
+        // 32-byte V rows: row r unit u at 2r + (u ^ ((r >> 4) & 1)) (spreads the tr4 reads over more banks)
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           const int r = 32 * k + (lane >> 1);
@@ -269,7 +313,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
           lds_dma16(vb, rr * 32 + 16 * ((lane & 1) ^ ((r >> 4) & 1)), st + kStageV + 1024 * k);
         }
       }
-      lds_dma2(sb, so, st + kStageVS);
+      if constexpr (ASYM) {
+        // [token][4 groups] fp16 = 8 bytes per token; dword loads (lane = token pair half)
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const int r = 32 * k + (lane >> 1);
+          const uint32_t o = 8u * (r < lim ? r : lim) + 4u * (lane & 1);
+          lds_dma4(ksg + 4 * m0, o, st + kMeta + 256 * k);
+          lds_dma4(kzg + 4 * m0, o, st + kMeta + 512 + 256 * k);
+          lds_dma4(vsg + 4 * m0, o, st + kMeta + 1024 + 256 * k);
+          lds_dma4(vzg + 4 * m0, o, st + kMeta + 1536 + 256 * k);
+        }
+      } else {
+        const uint32_t so = 2u * (lane < lim ? lane : lim);
+        lds_dma2(vsg + m0, so, st + kMeta);
+      }
     } else {
       const int64_t f0 = tt * kMini;
       const int vf = static_cast<int>(F - f0 < kMini ? F - f0 : kMini);
@@ -283,17 +341,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         lds_dma16(fr.v + 8 * u, st + kStageV + 1024 * k);
         vr = fr.v;
       }
-      lds_dma2(vr, st + kStageVS);  // filler: every tile issues the same number of loads
+      if constexpr (!ASYM) lds_dma2(vr, st + kMeta);  // filler: as many loads as a packed tile
     }
   };
 
-  // ---- prologue: query rows and K scales first, then the first two tiles ----
+  // ---- prologue: query rows (and K scales) first, then the first two tiles ----
   {
     const uint32_t qa = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&qraw_s[wave][0])));
-    const uint32_t ka = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&ksraw_s[wave][0])));
     if (wave < G) lds_dma4(p.q + b * p.q_sb + (kvh * G + wave) * p.q_sh + 2 * lane, qa);
     else qraw_s[wave][lane] = 0u;
-    lds_dma4(p.mid.k_scale + bkv * kD + 2 * lane, ka);
+    if constexpr (!ASYM) {
+      const uint32_t ka = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&ksraw_s[wave][0])));
+      lds_dma4(p.mid.k_scale + bkv * kD + 2 * lane, ka);
+    }
   }
   auto ops_of = [&](int i) { return i < n_w ? (t0 + wave + kWaves * i < nFt ? kOpsF16 : kOps) : 0; };
   // s_waitcnt needs an immediate: the outstanding-op counts that can occur
@@ -307,15 +367,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   };
   if (n_w > 0) issue(t0 + wave, st0);
   if (n_w > 1) issue(t0 + wave + kWaves, st1);
-  wait_vm(ops_of(0) + ops_of(1));  // the query and K-scale loads have landed
+  wait_vm(ops_of(0) + ops_of(1));  // the query (and K-scale) loads have landed
   __builtin_amdgcn_wave_barrier();
 
   // ---- query digits: wave h handles head h (channels 2*lane, 2*lane+1) ----
   {
     const int h = wave;
-    const uint32_t qq = qraw_s[h][lane], ks = ksraw_s[h][lane];
-    const float qf0 = h2f(static_cast<uint16_t>(qq & 0xFFFFu)) * h2f(static_cast<uint16_t>(ks & 0xFFFFu));
-    const float qf1 = h2f(static_cast<uint16_t>(qq >> 16)) * h2f(static_cast<uint16_t>(ks >> 16));
+    const uint32_t qq = qraw_s[h][lane];
+    float qf0 = h2f(static_cast<uint16_t>(qq & 0xFFFFu)), qf1 = h2f(static_cast<uint16_t>(qq >> 16));
+    if constexpr (!ASYM) {
+      const uint32_t ks = ksraw_s[h][lane];
+      qf0 *= h2f(static_cast<uint16_t>(ks & 0xFFFFu));
+      qf1 *= h2f(static_cast<uint16_t>(ks >> 16));
+    }
     const float mx = group_max<64>(fmaxf(fabsf(qf0), fabsf(qf1)));
     const float inv = mx > 0.0f ? kQMax / mx : 0.0f;
     const int qi[2] = {static_cast<int>(rintf(qf0 * inv)), static_cast<int>(rintf(qf1 * inv))};
@@ -324,29 +388,62 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       // channel d -> k-step d/16, operand byte j (see the K operand assembly below)
       const int d = 2 * lane + e;
       const int ksd = d >> 4, r = d & 15;
-      const int j = BITS == 4 ? 4 * (2 * (r >> 3) + (r & 1)) + ((r & 7) >> 1) : 4 * (r & 3) + (r >> 2);
+      const int j = KB == 4 ? 4 * (2 * (r >> 3) + (r & 1)) + ((r & 7) >> 1) : 4 * (r & 3) + (r >> 2);
       const int hi = (qi[e] + 128) >> 8;
       const int lo = qi[e] - 256 * hi;
       qd_s[(2 * ksd + 0) * 64 + h * 16 + j] = static_cast<uint8_t>(hi & 0xFF);
       qd_s[(2 * ksd + 1) * 64 + h * 16 + j] = static_cast<uint8_t>(lo & 0xFF);
     }
+    if constexpr (ASYM) {
+      // per 32-channel group (16 lanes): the digit sum restores the offset-binary
+      // K operand (16*(u-8) or 64*(u-2) -> 16*u or 64*u: + 128 * sum of digits),
+      // and the query sum multiplies the zero points
+      int si = qi[0] + qi[1];
+      float sf = qf0 + qf1;
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        si += __shfl_xor(si, o, 64);
+        sf += __shfl_xor(sf, o, 64);
+      }
+      if ((lane & 15) == 0) {
+        qoff_s[h][lane >> 4] = 128 * si;
+        qg_s[h][lane >> 4] = sf * p.scale_log2;
+      }
+    }
     // the K operand carries 16*c (4-bit) or 64*c (2-bit)
-    if (lane == 0) qsc_s[h] = mx > 0.0f ? (mx / kQMax) * p.scale_log2 * (BITS == 4 ? 0.0625f : 0.015625f) : 0.0f;
+    if (lane == 0) qsc_s[h] = mx > 0.0f ? (mx / kQMax) * p.scale_log2 * (KB == 4 ? 0.0625f : 0.015625f) : 0.0f;
     if (tid < 4) reinterpret_cast<uint32_t*>(&qd_s[kQdZero])[tid] = 0u;
   }
   __syncthreads();
 
   const float qsc = qsc_s[hq];
-  // query operands of the QK^T MFMAs (zero unless this lane's column block matches its k group)
-  i32x4 qdh[8], qdl[8];
-  {
-    const bool qlane = (sq == g) && (hq < G);
-    const uint8_t* qbase = qd_s + (qlane ? hq * 16 : kQdZero);
-    const int qstride = qlane ? 64 : 0;
+  // query operands of the QK^T MFMAs (zero unless this lane's column block
+  // matches its k group): registers for the reference formats, LDS reads per
+  // tile for the asymmetric ones
+  const bool qlane = (sq == g) && (hq < G);
+  const lds_u8* const qd_l = (const lds_u8*)&qd_s[0] + (qlane ? hq * 16 : kQdZero);
+  const int qstride = qlane ? 64 : 0;
+  i32x4 qdh[ASYM ? 1 : 8], qdl[ASYM ? 1 : 8];
+  if constexpr (!ASYM) {
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      qdh[ks] = *reinterpret_cast<const i32x4*>(qbase + (2 * ks) * qstride);
-      qdl[ks] = *reinterpret_cast<const i32x4*>(qbase + (2 * ks + 1) * qstride);
+      qdh[ks] = *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(qd_l + (2 * ks) * qstride);
+      qdl[ks] = *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(qd_l + (2 * ks + 1) * qstride);
+    }
+  }
+  auto qdig = [&](int ks, int digit) -> i32x4 {
+    if constexpr (ASYM)
+      return *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(qd_l + (2 * ks + digit) * qstride);
+    else
+      return digit ? qdl[ks] : qdh[ks];
+  };
+  int qoff[kGroups];
+  float qgv[kGroups];
+  if constexpr (ASYM) {
+#pragma unroll
+    for (int gi = 0; gi < kGroups; ++gi) {
+      qoff[gi] = qoff_s[hq][gi];
+      qgv[gi] = qg_s[hq][gi];
     }
   }
   const uint16_t* q16 = reinterpret_cast<const uint16_t*>(&qraw_s[hq][0]);
@@ -355,7 +452,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   f32x4 acc[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) acc[c] = f32x4{0, 0, 0, 0};
-  f32x4 acc_off = {0, 0, 0, 0};
+  // offset accumulators (one per channel group for the asymmetric formats) and
+  // the lane-local zero-point sums of the asymmetric formats
+  constexpr int kOffs = ASYM ? kGroups : 1;
+  f32x4 acc_off[kOffs];
+  float zacc[kGroups];
+#pragma unroll
+  for (int gi = 0; gi < kOffs; ++gi) acc_off[gi] = f32x4{0, 0, 0, 0};
+#pragma unroll
+  for (int gi = 0; gi < kGroups; ++gi) zacc[gi] = 0.0f;
 
   // Online-softmax step for this lane's four log2-domain scores x (absolute);
   // pr = the unnormalized probabilities relative to the running max.
@@ -374,7 +479,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       const float ag = __shfl(alpha, 4 * g, 64);  // accumulator rows of lane (n, g) belong to head g
 #pragma unroll
       for (int c = 0; c < 8; ++c) acc[c] *= ag;
-      acc_off *= ag;
+#pragma unroll
+      for (int gi = 0; gi < kOffs; ++gi) acc_off[gi] *= ag;
+      if constexpr (ASYM) {
+#pragma unroll
+        for (int gi = 0; gi < kGroups; ++gi) zacc[gi] *= alpha;
+      }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_exp2f(x[i] - m_run);
@@ -407,7 +517,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(sp + kStageV);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      const int col = out_channel<BITS>(c, n16);
+      const int col = out_channel<VB>(c, n16);
       const f16x4 vb = {__builtin_bit_cast(_Float16, v16[(4 * g + 0) * kD + col]),
                         __builtin_bit_cast(_Float16, v16[(4 * g + 1) * kD + col]),
                         __builtin_bit_cast(_Float16, v16[(4 * g + 2) * kD + col]),
@@ -425,7 +535,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int kk = ((n16 & 3) << 1) | ((n16 >> 2) & 1);
     const int sigma = 2 * (n16 >> 3) + (kk >> 2);
     const int r = 16 * sigma + 4 * g + (kk & 3);
-    if (BITS == 4) {
+    if (VB == 4) {
       const int sw = (sigma ^ g) & 3;
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) vrd[qq] = kStageV + 16 * (4 * r + (qq ^ sw));
@@ -438,58 +548,129 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   uint32_t krd[4];  // K row `lane`, 16-byte unit q
 #pragma unroll
   for (int qq = 0; qq < 4; ++qq)
-    krd[qq] = BITS == 4 ? kStageK + 16 * (4 * lane + (qq ^ ((lane >> 2) & 3))) : kStageK + 32 * lane + 16 * (qq & 1);
-  const uint32_t vs_rd = kStageVS + 4 * (16 * sq + 4 * g);
+    krd[qq] = KB == 4 ? kStageK + 16 * (4 * lane + (qq ^ ((lane >> 2) & 3))) : kStageK + 32 * lane + 16 * (qq & 1);
+  // this lane's tokens 16*sq + 4g + i: V scales (reference) or the four
+  // [token][group] metadata arrays (asymmetric), 8 bytes per token
+  const uint32_t vs_rd = ASYM ? kMeta + 8 * (16 * sq + 4 * g) : kMeta + 4 * (16 * sq + 4 * g);
   const uint32_t z = 0u;
   uint32_t vmask, vcst;  // register-resident constants of the V code conversion
-  if (BITS == 4) {
+  if (VB == 4) {
     asm volatile("s_mov_b32 %0, 0x00F000F0" : "=s"(vmask));
-    asm volatile("v_mov_b32 %0, 0x54805480" : "=v"(vcst));
+    if (ASYM) asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(vcst));
+    else asm volatile("v_mov_b32 %0, 0x54805480" : "=v"(vcst));
   } else {
     asm volatile("s_mov_b32 %0, 0x03000300" : "=s"(vmask));
-    asm volatile("v_mov_b32 %0, 0x46004600" : "=v"(vcst));
+    if (ASYM) asm volatile("v_mov_b32 %0, 0x44004400" : "=v"(vcst));
+    else asm volatile("v_mov_b32 %0, 0x46004600" : "=v"(vcst));
   }
-  // per-token offset of the fp16 V values: 72 (4-bit) or 6 (2-bit)
-  const uint32_t offv = BITS == 4 ? 0x54805480u : 0x46004600u;
+  // per-token offset of the fp16 V values: 72 / 6 (two's complement codes) or
+  // 64 / 4 (unsigned codes of the asymmetric formats)
+  const uint32_t offv = VB == 4 ? (ASYM ? 0x54005400u : 0x54805480u) : (ASYM ? 0x44004400u : 0x46004600u);
   const f16x8 boff = __builtin_bit_cast(f16x8, u32x4{offv, offv, offv, offv});
+  // K codes -> int8 operand: two's complement (x & m) or offset binary ((x & m) ^ 0x80)
+  constexpr uint32_t kFlip = ASYM ? 0x80808080u : 0u;
 
   auto packed_tile = [&](int64_t t, const lds_u8* sp) {
-    // QK^T: A = K codes of token `lane` as int8 (16*c or 64*c)
-    i32x4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
-    if (BITS == 4) {
+    float x[4], pr[4];
+    if constexpr (!ASYM) {
+      // QK^T: A = K codes of token `lane` as int8 (16*c or 64*c)
+      i32x4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
+      if (KB == 4) {
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const u32x4 kv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + krd[qq]);
+        for (int qq = 0; qq < 4; ++qq) {
+          const u32x4 kv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + krd[qq]);
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          const int ks = 2 * qq + h2;
-          const uint32_t w0 = kv[2 * h2], w1 = kv[2 * h2 + 1];
-          const i32x4 a = {static_cast<int>(w0 & 0xF0F0F0F0u), static_cast<int>((w0 << 4) & 0xF0F0F0F0u),
-                           static_cast<int>(w1 & 0xF0F0F0F0u), static_cast<int>((w1 << 4) & 0xF0F0F0F0u)};
-          chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdh[ks], chi, 0, 0, 0);
-          clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdl[ks], clo, 0, 0, 0);
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const int ks = 2 * qq + h2;
+            const uint32_t w0 = kv[2 * h2], w1 = kv[2 * h2 + 1];
+            const i32x4 a = {static_cast<int>(w0 & 0xF0F0F0F0u), static_cast<int>((w0 << 4) & 0xF0F0F0F0u),
+                             static_cast<int>(w1 & 0xF0F0F0F0u), static_cast<int>((w1 << 4) & 0xF0F0F0F0u)};
+            chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig(ks, 0), chi, 0, 0, 0);
+            clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig(ks, 1), clo, 0, 0, 0);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq) {
+          const u32x4 kv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + krd[qq]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            // k-step 4qq+e: dword i, byte j <-> channel 16ks + 4j + i
+            const int ks = 4 * qq + e;
+            const uint32_t w = kv[e];
+            const i32x4 a = {static_cast<int>(w & 0xC0C0C0C0u), static_cast<int>((w << 2) & 0xC0C0C0C0u),
+                             static_cast<int>((w << 4) & 0xC0C0C0C0u), static_cast<int>((w << 6) & 0xC0C0C0C0u)};
+            chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig(ks, 0), chi, 0, 0, 0);
+            clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig(ks, 1), clo, 0, 0, 0);
+          }
         }
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = static_cast<float>(chi[i] * 256 + clo[i]) * qsc;
     } else {
+      // per-group integer dot products, combined with the token's group scale and zero
+      const u32x4 ks01 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd);
+      const u32x4 ks23 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd + 16);
+      const u32x4 kz01 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd + 512);
+      const u32x4 kz23 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd + 528);
+      // token i, group gi: dword 2*(i&1) + (gi>>1) of the (i>>1) vector, half gi&1
+      auto meta = [&](const u32x4& v01, const u32x4& v23, int i, int gi) {
+        const uint32_t dw = (i < 2 ? v01 : v23)[2 * (i & 1) + (gi >> 1)];
+        return half_of(dw, gi & 1);
+      };
+      float xs[4] = {0, 0, 0, 0}, xz[4] = {0, 0, 0, 0};
+      auto group_done = [&](int gi, const i32x4& chi, const i32x4& clo) {
 #pragma unroll
-      for (int qq = 0; qq < 2; ++qq) {
-        const u32x4 kv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + krd[qq]);
+        for (int i = 0; i < 4; ++i) {
+          const float dg = static_cast<float>(chi[i] * 256 + clo[i] + qoff[gi]);
+          xs[i] = fmaf(meta(ks01, ks23, i, gi), dg, xs[i]);
+          xz[i] = fmaf(meta(kz01, kz23, i, gi), qgv[gi], xz[i]);
+        }
+      };
+      if (KB == 4) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // k-step 4qq+e: dword i, byte j <-> channel 16ks + 4j + i
-          const int ks = 4 * qq + e;
-          const uint32_t w = kv[e];
-          const i32x4 a = {static_cast<int>(w & 0xC0C0C0C0u), static_cast<int>((w << 2) & 0xC0C0C0C0u),
-                           static_cast<int>((w << 4) & 0xC0C0C0C0u), static_cast<int>((w << 6) & 0xC0C0C0C0u)};
-          chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdh[ks], chi, 0, 0, 0);
-          clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdl[ks], clo, 0, 0, 0);
+        for (int qq = 0; qq < 4; ++qq) {  // 16-byte unit qq = channel group qq
+          const u32x4 kv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + krd[qq]);
+          i32x4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const int ks = 2 * qq + h2;
+            const uint32_t w0 = kv[2 * h2], w1 = kv[2 * h2 + 1];
+            const i32x4 a = {static_cast<int>((w0 & 0xF0F0F0F0u) ^ kFlip),
+                             static_cast<int>(((w0 << 4) & 0xF0F0F0F0u) ^ kFlip),
+                             static_cast<int>((w1 & 0xF0F0F0F0u) ^ kFlip),
+                             static_cast<int>(((w1 << 4) & 0xF0F0F0F0u) ^ kFlip)};
+            chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig(ks, 0), chi, 0, 0, 0);
+            clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig(ks, 1), clo, 0, 0, 0);
+          }
+          group_done(qq, chi, clo);
+        }
+      } else {
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq) {
+          const u32x4 kv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + krd[qq]);
+#pragma unroll
+          for (int e2 = 0; e2 < 2; ++e2) {  // channel group 2qq + e2 = k-steps 4qq + 2e2 + {0, 1}
+            i32x4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
+#pragma unroll
+            for (int e1 = 0; e1 < 2; ++e1) {
+              const int e = 2 * e2 + e1, ks = 4 * qq + e;
+              const uint32_t w = kv[e];
+              const i32x4 a = {static_cast<int>((w & 0xC0C0C0C0u) ^ kFlip),
+                               static_cast<int>(((w << 2) & 0xC0C0C0C0u) ^ kFlip),
+                               static_cast<int>(((w << 4) & 0xC0C0C0C0u) ^ kFlip),
+                               static_cast<int>(((w << 6) & 0xC0C0C0C0u) ^ kFlip)};
+              chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig(ks, 0), chi, 0, 0, 0);
+              clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig(ks, 1), clo, 0, 0, 0);
+            }
+            group_done(2 * qq + e2, chi, clo);
+          }
         }
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = fmaf(xs[i], qsc, xz[i]);
     }
     const int64_t m0 = (t - nFt) * kTile;
-    float x[4], pr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = static_cast<float>(chi[i] * 256 + clo[i]) * qsc;
     if (m0 + kTile > M) {
       const int valid = static_cast<int>(M - m0);
 #pragma unroll
@@ -497,44 +678,70 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         if (16 * sq + 4 * g + i >= valid) x[i] = -INFINITY;
     }
     softmax4(x, pr);
-    // P' = P * v_scale (scales sit in the low halves of the stage's scale dwords)
-    uint32_t pk0, pk1;
-    {
+    // P' = P * v_scale: one operand pair (a0, a1) per V scale group
+    constexpr int kPs = ASYM ? kGroups : 1;
+    f16x8 a0[kPs], a1[kPs];
+    if constexpr (!ASYM) {
+      // scales sit in the low halves of the stage's scale dwords
       const u32x4 sv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd);
-      pk0 = pack_f16(pr[0] * h2f(static_cast<uint16_t>(sv[0])), pr[1] * h2f(static_cast<uint16_t>(sv[1])));
-      pk1 = pack_f16(pr[2] * h2f(static_cast<uint16_t>(sv[2])), pr[3] * h2f(static_cast<uint16_t>(sv[3])));
+      const uint32_t pk0 = pack_f16(pr[0] * h2f(static_cast<uint16_t>(sv[0])), pr[1] * h2f(static_cast<uint16_t>(sv[1])));
+      const uint32_t pk1 = pack_f16(pr[2] * h2f(static_cast<uint16_t>(sv[2])), pr[3] * h2f(static_cast<uint16_t>(sv[3])));
+      a0[0] = __builtin_bit_cast(f16x8, u32x4{sq == 0 ? pk0 : z, sq == 0 ? pk1 : z, sq == 1 ? pk0 : z, sq == 1 ? pk1 : z});
+      a1[0] = __builtin_bit_cast(f16x8, u32x4{sq == 2 ? pk0 : z, sq == 2 ? pk1 : z, sq == 3 ? pk0 : z, sq == 3 ? pk1 : z});
+    } else {
+      const u32x4 vs01 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd + 1024);
+      const u32x4 vs23 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd + 1040);
+      const u32x4 vz01 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd + 1536);
+      const u32x4 vz23 = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd + 1552);
+      auto meta = [&](const u32x4& v01, const u32x4& v23, int i, int gi) {
+        const uint32_t dw = (i < 2 ? v01 : v23)[2 * (i & 1) + (gi >> 1)];
+        return half_of(dw, gi & 1);
+      };
+#pragma unroll
+      for (int gi = 0; gi < kGroups; ++gi) {
+        const uint32_t pk0 = pack_f16(pr[0] * meta(vs01, vs23, 0, gi), pr[1] * meta(vs01, vs23, 1, gi));
+        const uint32_t pk1 = pack_f16(pr[2] * meta(vs01, vs23, 2, gi), pr[3] * meta(vs01, vs23, 3, gi));
+        a0[gi] = __builtin_bit_cast(f16x8, u32x4{sq == 0 ? pk0 : z, sq == 0 ? pk1 : z, sq == 1 ? pk0 : z, sq == 1 ? pk1 : z});
+        a1[gi] = __builtin_bit_cast(f16x8, u32x4{sq == 2 ? pk0 : z, sq == 2 ? pk1 : z, sq == 3 ? pk0 : z, sq == 3 ? pk1 : z});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) zacc[gi] = fmaf(pr[i], meta(vz01, vz23, i, gi), zacc[gi]);
+      }
     }
-    const f16x8 a0 = __builtin_bit_cast(f16x8, u32x4{sq == 0 ? pk0 : z, sq == 0 ? pk1 : z, sq == 1 ? pk0 : z, sq == 1 ? pk1 : z});
-    const f16x8 a1 = __builtin_bit_cast(f16x8, u32x4{sq == 2 ? pk0 : z, sq == 2 ? pk1 : z, sq == 3 ? pk0 : z, sq == 3 ? pk1 : z});
-    if (BITS == 4) {
+    // channel tile c lies in 32-channel group c >> 1 (both code widths)
+    if (VB == 4) {
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
+        const int gp = ASYM ? c >> 1 : 0;
         const i32x2 xv = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
             reinterpret_cast<lds_i32x2*>(const_cast<lds_u8*>(sp) + vrd[c >> 1] + 8 * (c & 1)));
         uint32_t b0[4], b1[4];
         v_nibbles_to_f16(static_cast<uint32_t>(xv[0]), vmask, vcst, b0);
         v_nibbles_to_f16(static_cast<uint32_t>(xv[1]), vmask, vcst, b1);
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(f16x8, b0), acc[c], 0, 0, 0);
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(f16x8, b1), acc[c], 0, 0, 0);
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[gp], __builtin_bit_cast(f16x8, b0), acc[c], 0, 0, 0);
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[gp], __builtin_bit_cast(f16x8, b1), acc[c], 0, 0, 0);
       }
     } else {
 #pragma unroll
       for (int c4 = 0; c4 < 4; ++c4) {
+        const int gp = ASYM ? c4 : 0;
         const i32x2 xv = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
             reinterpret_cast<lds_i32x2*>(const_cast<lds_u8*>(sp) + vrd[c4]));
         uint32_t f0[4], s0[4], f1[4], s1[4];
         v2_nibbles_to_f16(static_cast<uint32_t>(xv[0]), vmask, vcst, f0, s0);
         v2_nibbles_to_f16(static_cast<uint32_t>(xv[1]), vmask, vcst, f1, s1);
-        acc[2 * c4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(f16x8, f0), acc[2 * c4], 0, 0, 0);
-        acc[2 * c4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(f16x8, f1), acc[2 * c4], 0, 0, 0);
+        acc[2 * c4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[gp], __builtin_bit_cast(f16x8, f0), acc[2 * c4], 0, 0, 0);
+        acc[2 * c4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[gp], __builtin_bit_cast(f16x8, f1), acc[2 * c4], 0, 0, 0);
         acc[2 * c4 + 1] =
-            __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(f16x8, s0), acc[2 * c4 + 1], 0, 0, 0);
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[gp], __builtin_bit_cast(f16x8, s0), acc[2 * c4 + 1], 0, 0, 0);
         acc[2 * c4 + 1] =
-            __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(f16x8, s1), acc[2 * c4 + 1], 0, 0, 0);
+            __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[gp], __builtin_bit_cast(f16x8, s1), acc[2 * c4 + 1], 0, 0, 0);
       }
     }
-    acc_off = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, boff, acc_off, 0, 0, 0);
-    acc_off = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, boff, acc_off, 0, 0, 0);
+#pragma unroll
+    for (int gp = 0; gp < kPs; ++gp) {
+      acc_off[gp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[gp], boff, acc_off[gp], 0, 0, 0);
+      acc_off[gp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[gp], boff, acc_off[gp], 0, 0, 0);
+    }
   };
 
   // ---- main loop: two stages, two tiles in flight ----
@@ -559,6 +766,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   lsum += __shfl_xor(lsum, 2, 64);
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
+  // zero-point sums of head hq (score lanes), then of head g (accumulator lanes)
+  float zs[kGroups];
+  if constexpr (ASYM) {
+#pragma unroll
+    for (int gi = 0; gi < kGroups; ++gi) {
+      float zz = zacc[gi];
+      zz += __shfl_xor(zz, 1, 64);
+      zz += __shfl_xor(zz, 2, 64);
+      zz += __shfl_xor(zz, 16, 64);
+      zz += __shfl_xor(zz, 32, 64);
+      zs[gi] = __shfl(zz, 4 * g, 64);
+    }
+  }
   if (g == 0 && sq == 0) {
     red_m[wave][hq] = m_run;
     red_l[wave][hq] = lsum;
@@ -570,11 +790,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) Mg = fmaxf(Mg, red_m[w][g]);
     const float wsc = exp2f(red_m[wave][g] - Mg);
-    const float off = (acc_off[0] + acc_off[1]) + (acc_off[2] + acc_off[3]);
+    float off[kOffs];
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
-      red_o[(wave * 4 + g) * kD + out_channel<BITS>(c, n16)] =
-          (((acc[c][0] + acc[c][1]) + (acc[c][2] + acc[c][3])) - off) * wsc;
+    for (int gp = 0; gp < kOffs; ++gp) off[gp] = (acc_off[gp][0] + acc_off[gp][1]) + (acc_off[gp][2] + acc_off[gp][3]);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float o = ((acc[c][0] + acc[c][1]) + (acc[c][2] + acc[c][3])) - off[ASYM ? c >> 1 : 0];
+      if constexpr (ASYM) o += zs[c >> 1];
+      red_o[(wave * 4 + g) * kD + out_channel<VB>(c, n16)] = o * wsc;
+    }
   }
   __syncthreads();
   const int n = p.n_splits;
@@ -663,13 +887,22 @@ bool fp16_tier_ok(const Fp16Tier& t) {
 }  // namespace
 
 bool int4_supports(const Params& p) {
-  if (p.mid.fmt != FADE_MID_SYM || p.mid.k_bits != p.mid.v_bits || p.mid.len <= 0) return false;
-  if (p.mid.k_bits != 4 && p.mid.k_bits != 2) return false;
-  if (p.G > 4) return false;
+  const MidTier& m = p.mid;
+  if (m.len <= 0 || p.G > 4) return false;
+  if ((m.k_bits != 4 && m.k_bits != 2) || (m.v_bits != 4 && m.v_bits != 2)) return false;
+  if (m.fmt == FADE_MID_SYM) {
+    if (m.k_bits != m.v_bits) return false;
+    if (!aligned(m.k_scale, 4) || !aligned(m.v_scale, 2)) return false;
+  } else if (m.fmt == FADE_MID_ASYM) {
+    if (m.group != 32) return false;
+    if (!aligned(m.k_scale, 4) || !aligned(m.k_zero, 4) || !aligned(m.v_scale, 4) || !aligned(m.v_zero, 4))
+      return false;
+  } else {
+    return false;
+  }
   if (!fp16_tier_ok(p.sink) || !fp16_tier_ok(p.recent)) return false;
   if (!aligned(p.q, 16) || p.q_sb % 8 || p.q_sh % 8) return false;
-  return aligned(p.mid.k_codes, 16) && aligned(p.mid.v_codes, 16) && aligned(p.mid.k_scale, 4) &&
-         aligned(p.mid.v_scale, 2);
+  return aligned(m.k_codes, 16) && aligned(m.v_codes, 16);
 }
 
 int int4_fp16_tiles(const Params& p) {
@@ -679,28 +912,49 @@ int int4_fp16_tiles(const Params& p) {
 
 int64_t int4_tiles(const Params& p) { return int4_fp16_tiles(p) + cdiv(p.mid.len, kTile); }
 
-int int4_resident_wgs() {
-  static int cached = 0;
-  if (cached > 0) return cached;
+namespace {
+
+typedef void (*PackedKernel)(Params);
+
+// The kernel instance for a middle tier int4_supports accepted.
+PackedKernel packed_kernel(const Params& p, int* index) {
+  const bool asym = p.mid.fmt == FADE_MID_ASYM;
+  const int kb = p.mid.k_bits, vb = p.mid.v_bits;
+  if (!asym) {
+    *index = kb == 4 ? 0 : 1;
+    return kb == 4 ? decode_packed_kernel<4, 4, false> : decode_packed_kernel<2, 2, false>;
+  }
+  if (kb == 4 && vb == 4) { *index = 2; return decode_packed_kernel<4, 4, true>; }
+  if (kb == 4 && vb == 2) { *index = 3; return decode_packed_kernel<4, 2, true>; }
+  if (kb == 2 && vb == 2) { *index = 4; return decode_packed_kernel<2, 2, true>; }
+  *index = 5;
+  return decode_packed_kernel<2, 4, true>;
+}
+
+}  // namespace
+
+int int4_resident_wgs(const Params& p) {
+  static int cached[6] = {0, 0, 0, 0, 0, 0};
+  int idx = 0;
+  const PackedKernel k = packed_kernel(p, &idx);
+  if (cached[idx] > 0) return cached[idx];
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_sym_kernel<4>, kThreads, 0) != hipSuccess ||
-      cus <= 0 || per_cu <= 0) {
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, 0) != hipSuccess || cus <= 0 ||
+      per_cu <= 0) {
     (void)hipGetLastError();
     return 512;
   }
-  cached = cus * per_cu;
-  return cached;
+  cached[idx] = cus * per_cu;
+  return cached[idx];
 }
 
 int launch_int4(const Params& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv), static_cast<unsigned>(p.B));
-  if (p.mid.k_bits == 4)
-    hipLaunchKernelGGL(decode_sym_kernel<4>, grid, dim3(kThreads), 0, st, p);
-  else
-    hipLaunchKernelGGL(decode_sym_kernel<2>, grid, dim3(kThreads), 0, st, p);
-  return check_launch("fade_tiered_decode_attn(int4)");
+  int idx = 0;
+  hipLaunchKernelGGL(packed_kernel(p, &idx), grid, dim3(kThreads), 0, st, p);
+  return check_launch("fade_tiered_decode_attn(packed)");
 }
 
 }  // namespace decode

@@ -192,20 +192,48 @@ def test_tiered_decode_sym2_fast_path(dev, B, Hq, Hkv, S, ns, nr, n_splits):
     assert np.abs(out - ref).max() <= ATOL
 
 
-@pytest.mark.parametrize("bits", [4, 2])
-def test_tiered_decode_asym(dev, bits):
-    print(f"case decode asym bits={bits}", flush=True)
-    q, k, v, ns, nr = _case(2, 32, 8, 800, 4, 64, seed=9)
+def _asym_mid(dev, k, v, ns, nr, k_bits, v_bits):
     S = k.shape[2]
     km, vm = k[:, :, ns : S - nr], v[:, :, ns : S - nr]
-    kp, ksc, kz = fq.quant_asym(torch.from_numpy(np.ascontiguousarray(km)).to(dev), bits, 32)
-    vp, vsc, vz = fq.quant_asym(torch.from_numpy(np.ascontiguousarray(vm)).to(dev), bits, 32)
-    mid = MiddleTier("asym", kp, vp, ksc, vsc, kz, vz, k_bits=bits, v_bits=bits, group=32)
-    okp, oks, okz = oq.quant_asym_group(km, bits, 32)
-    ovp, ovs, ovz = oq.quant_asym_group(vm, bits, 32)
+    kp, ksc, kz = fq.quant_asym(torch.from_numpy(np.ascontiguousarray(km)).to(dev), k_bits, 32)
+    vp, vsc, vz = fq.quant_asym(torch.from_numpy(np.ascontiguousarray(vm)).to(dev), v_bits, 32)
+    mid = MiddleTier("asym", kp, vp, ksc, vsc, kz, vz, k_bits=k_bits, v_bits=v_bits, group=32)
+    okp, oks, okz = oq.quant_asym_group(km, k_bits, 32)
+    ovp, ovs, ovz = oq.quant_asym_group(vm, v_bits, 32)
     omid = {"fmt": "asym", "kq": okp, "ks": oks, "kz": okz, "vq": ovp, "vs": ovs, "vz": ovz,
-            "k_bits": bits, "v_bits": bits, "group": 32}
-    assert _run(dev, q, k, v, ns, nr, mid, omid) <= ATOL
+            "k_bits": k_bits, "v_bits": v_bits, "group": 32}
+    return mid, omid
+
+
+@pytest.mark.parametrize("k_bits,v_bits", [(4, 4), (4, 2), (2, 2), (2, 4)])
+@pytest.mark.parametrize("kernel", [0, 1])
+def test_tiered_decode_asym(dev, k_bits, v_bits, kernel):
+    """Asymmetric group-32 middle tier (build format): matrix-core path (0) and portable kernel (1)."""
+    print(f"case decode asym K{k_bits}V{v_bits} kernel={kernel}", flush=True)
+    q, k, v, ns, nr = _case(2, 32, 8, 800, 4, 64, seed=9)
+    mid, omid = _asym_mid(dev, k, v, ns, nr, k_bits, v_bits)
+    assert _run(dev, q, k, v, ns, nr, mid, omid, kernel=kernel) <= ATOL
+
+
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,S,ns,nr,n_splits,k_bits,v_bits",
+    [
+        (1, 32, 8, 2048, 4, 64, 0, 4, 4),  # config 0 as BASELINE states it
+        (2, 8, 4, 777, 4, 64, 3, 4, 2),  # G=2, ragged last tile
+        (1, 4, 1, 301, 0, 37, 1, 4, 2),  # one kv head, odd middle length, one split
+        (2, 12, 4, 2000, 4, 256, 0, 4, 2),  # G=3, config-2 windows
+        (1, 8, 8, 65, 0, 0, 0, 2, 2),  # MHA, middle only, one token past a tile
+        (3, 16, 4, 5, 2, 2, 0, 4, 4),  # one middle token
+        (1, 32, 8, 1200, 4, 256, 5, 2, 4),
+    ],
+)
+def test_tiered_decode_asym_fast_path(dev, B, Hq, Hkv, S, ns, nr, n_splits, k_bits, v_bits):
+    """The matrix-core kernel is required (kernel=2) for the group-32 asymmetric formats."""
+    print(f"case decode asym fast B={B} Hq={Hq} Hkv={Hkv} S={S} ns={ns} nr={nr} splits={n_splits} "
+          f"K{k_bits}V{v_bits}", flush=True)
+    q, k, v, ns, nr = _case(B, Hq, Hkv, S, ns, nr, seed=5000 + S)
+    mid, omid = _asym_mid(dev, k, v, ns, nr, k_bits, v_bits)
+    assert _run(dev, q, k, v, ns, nr, mid, omid, kernel=2, n_splits=n_splits) <= ATOL
 
 
 def test_fused_int4_sdpa_api_and_parity_helper(dev):
