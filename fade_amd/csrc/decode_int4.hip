@@ -81,14 +81,15 @@ constexpr int kGroups = 4;               // 32-channel groups of the asymmetric 
 // asymmetric formats: K scale | K zero | V scale | V zero, [64 tokens][4 groups]
 // fp16 each, right after the V codes.
 constexpr int kStageK = 0, kStageV = 4096;
-template <int KB, int VB, bool ASYM>
+enum { kFmtSym = 0, kFmtAsym = 1, kFmtLit = 2 };
+template <int KB, int VB, int FMT>
 struct Stage {
-  static constexpr int kMeta = ASYM ? kStageV + 1024 * VB : 8192;
-  static constexpr int kBytes = ASYM ? (kMeta + 2048 > 8192 ? kMeta + 2048 : 8192) : 8192 + 256;
+  static constexpr int kMeta = FMT == kFmtAsym ? kStageV + 1024 * VB : (FMT == kFmtLit ? kStageV + 8192 : 8192);
+  static constexpr int kBytes = FMT == kFmtAsym ? (kMeta + 2048 > 8192 ? kMeta + 2048 : 8192) : kMeta + 256;
   // direct-to-LDS loads per packed tile (K and V codes in 1 KB loads, then the
-  // metadata: one 2-byte load, or eight dword loads) and per fp16 tile
-  static constexpr int kOps = KB + VB + (ASYM ? 8 : 1);
-  static constexpr int kOpsF16 = ASYM ? 8 : 9;
+  // metadata: one 2-byte or dword load, or eight dword loads) and per fp16 tile
+  static constexpr int kOps = KB + VB + (FMT == kFmtAsym ? 8 : 1);
+  static constexpr int kOpsF16 = FMT == kFmtSym ? 9 : 8;
 };
 constexpr int kQdZero = 8 * 2 * 4 * 16;  // zero operand after the [ks][digit][head][16 B] query digits
 constexpr float kQMax = 32000.0f;
@@ -128,11 +129,13 @@ __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
 }
 
 // Output column n of channel tile c (PV accumulator) <-> head-dim channel.
+// 8-bit (literal INT2 V): channel 16c + n.
 // 4-bit: a tr4 read gives lane n the nibble of channel 16c + (n ^ 1).  2-bit:
 // chunk c/2 of 32 channels, lane n holds the codes of channels
 // 4(n/2) + 2(1 - n%2) + {0, 1} (first / second code of the nibble = c%2).
 template <int BITS>
 __device__ __forceinline__ int out_channel(int c, int n) {
+  if (BITS == 8) return 16 * c + n;  // tr8 reads: lane n holds channel 16c + n
   if (BITS == 4) return 16 * c + (n ^ 1);
   return 32 * (c >> 1) + 4 * (n >> 1) + 2 * (1 - (n & 1)) + (c & 1);
 }
@@ -183,13 +186,21 @@ __device__ __forceinline__ float half_of(uint32_t dw, int hi) {
   return h2f(static_cast<uint16_t>(hi ? dw >> 16 : dw & 0xFFFFu));
 }
 
-// LDS: two ring stages per wave (8.25 KB for the reference formats, 8 or 10 KB
-// for the asymmetric ones); at <= 80 KB per workgroup two workgroups share a
-// CU, and registers are sized for that (two waves per SIMD).
-template <int KB, int VB, bool ASYM>
+// Literal INT2 V rows (128 B, eight 16-byte units) in LDS: unit u of row r
+// sits at unit u ^ lit_swz(r), so that the 16 rows one tr8 read pass touches
+// (rows 16a + 4g + i, a and g in {0, 1} or {2, 3} ...) fall in distinct banks.
+__device__ __forceinline__ int lit_swz(int r) { return ((r >> 1) & 3) | ((r >> 2) & 4); }
+
+// LDS: two ring stages per wave (8.25 KB for the reference INT4 / 2-bit
+// formats, 8 or 10 KB for the asymmetric ones, 12.25 KB for literal INT2 V);
+// at <= 80 KB per workgroup two workgroups share a CU, and registers are sized
+// for that (two waves per SIMD).
+template <int KB, int VB, int FMT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_packed_kernel(
     Params p) {
-  using S = Stage<KB, VB, ASYM>;
+  constexpr bool ASYM = FMT == kFmtAsym;  // asymmetric group-32 formats
+  constexpr bool LIT = FMT == kFmtLit;    // K4 + literal grouped INT2 V (int8 codes)
+  using S = Stage<KB, VB, FMT>;
   constexpr int kOps = S::kOps, kOpsF16 = S::kOpsF16, kMeta = S::kMeta;
   constexpr int kRowK = 16 * KB, kRowV = 16 * VB;  // packed row bytes of one token
   const int split = blockIdx.x;
@@ -221,9 +232,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   __shared__ int last_s;
 
   const uint8_t* kc = p.mid.k_codes + bkv * M * kRowK;
-  const uint8_t* vc = p.mid.v_codes + bkv * M * kRowV;
+  // literal INT2 V: [v_rows][128] int8 codes and [v_rows / 64][128] scales per
+  // (batch row, kv head), v_rows = the middle length padded to 64 (pad rows are 0)
+  const uint8_t* vc = p.mid.v_codes + bkv * (LIT ? p.mid.v_rows : M) * kRowV;
   // reference formats: V scale per token; asymmetric: [token][4 groups] scale / zero
-  const uint16_t* vsg = p.mid.v_scale + bkv * M * (ASYM ? kGroups : 1);
+  const uint16_t* vsg =
+      LIT ? p.mid.v_scale + bkv * (p.mid.v_rows / kTile) * kD : p.mid.v_scale + bkv * M * (ASYM ? kGroups : 1);
   const uint16_t* ksg = ASYM ? p.mid.k_scale + bkv * M * kGroups : nullptr;
   const uint16_t* kzg = ASYM ? p.mid.k_zero + bkv * M * kGroups : nullptr;
   const uint16_t* vzg = ASYM ? p.mid.v_zero + bkv * M * kGroups : nullptr;
@@ -292,7 +306,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
           lds_dma16(kb, rr * 32 + 16 * (lane & 1), st + kStageK + 1024 * k);
         }
       }
-      if (VB == 4) {
+      if (VB == 8) {
+        // 8 KB of int8 codes; the padded tier has all 64 rows of the tile
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int r = 8 * k + (lane >> 3);
+          lds_dma16(vb, r * 128 + 16 * ((lane & 7) ^ lit_swz(r)), st + kStageV + 1024 * k);
+        }
+      } else if (VB == 4) {
         uint32_t vo[4] = {voff[0], voff[1], voff[2], voff[3]};
         if (lim < kTile - 1) {
 #pragma unroll
@@ -324,6 +345,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
           lds_dma4(vsg + 4 * m0, o, st + kMeta + 1024 + 256 * k);
           lds_dma4(vzg + 4 * m0, o, st + kMeta + 1536 + 256 * k);
         }
+      } else if constexpr (LIT) {
+        lds_dma4(vsg + (m0 / kTile) * kD, 4u * lane, st + kMeta);  // the tile's scale row
       } else {
         const uint32_t so = 2u * (lane < lim ? lane : lim);
         lds_dma2(vsg + m0, so, st + kMeta);
@@ -341,7 +364,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         lds_dma16(fr.v + 8 * u, st + kStageV + 1024 * k);
         vr = fr.v;
       }
-      if constexpr (!ASYM) lds_dma2(vr, st + kMeta);  // filler: as many loads as a packed tile
+      if constexpr (FMT == kFmtSym) lds_dma2(vr, st + kMeta);  // filler: as many loads as a packed tile
     }
   };
 
@@ -535,7 +558,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int kk = ((n16 & 3) << 1) | ((n16 >> 2) & 1);
     const int sigma = 2 * (n16 >> 3) + (kk >> 2);
     const int r = 16 * sigma + 4 * g + (kk & 3);
-    if (VB == 4) {
+    if (VB == 8) {
+      // tr8: output lane p, byte j <- byte p % 8 of source lane 2j + p / 8.  Source
+      // lane s reads half s & 1 of channel unit c of the row holding slot
+      // pi(s >> 1), pi = (0 2 1 3 4 6 5 7), so that the fp16 pairs below come out
+      // in slot order; slot k <-> token 16 (k >> 2) + 4g + (k & 3) (+32 for a1).
+      const int j = n16 >> 1;
+      const int k = (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1);
+      const int r0 = 16 * (k >> 2) + 4 * g + (k & 3);
+      vrd[0] = kStageV + 128 * r0 + 8 * (n16 & 1);
+      vrd[1] = lit_swz(r0);
+      vrd[2] = kStageV + 128 * (r0 + 32) + 8 * (n16 & 1);
+      vrd[3] = lit_swz(r0 + 32);
+    } else if (VB == 4) {
       const int sw = (sigma ^ g) & 3;
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) vrd[qq] = kStageV + 16 * (4 * r + (qq ^ sw));
@@ -554,7 +589,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const uint32_t vs_rd = ASYM ? kMeta + 8 * (16 * sq + 4 * g) : kMeta + 4 * (16 * sq + 4 * g);
   const uint32_t z = 0u;
   uint32_t vmask, vcst;  // register-resident constants of the V code conversion
-  if (VB == 4) {
+  if (VB == 8) {
+    asm volatile("s_mov_b32 %0, 0x03000300" : "=s"(vmask));
+    asm volatile("v_mov_b32 %0, 0x46004600" : "=v"(vcst));
+  } else if (VB == 4) {
     asm volatile("s_mov_b32 %0, 0x00F000F0" : "=s"(vmask));
     if (ASYM) asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(vcst));
     else asm volatile("v_mov_b32 %0, 0x54805480" : "=v"(vcst));
@@ -566,6 +604,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // per-token offset of the fp16 V values: 72 / 6 (two's complement codes) or
   // 64 / 4 (unsigned codes of the asymmetric formats)
   const uint32_t offv = VB == 4 ? (ASYM ? 0x54005400u : 0x54805480u) : (ASYM ? 0x44004400u : 0x46004600u);
+  // literal INT2 V: the tile's per-channel scales of this lane's output channels
+  const uint32_t lsc_rd = kMeta + 2 * n16;
   const f16x8 boff = __builtin_bit_cast(f16x8, u32x4{offv, offv, offv, offv});
   // K codes -> int8 operand: two's complement (x & m) or offset binary ((x & m) ^ 0x80)
   constexpr uint32_t kFlip = ASYM ? 0x80808080u : 0u;
@@ -681,7 +721,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // P' = P * v_scale: one operand pair (a0, a1) per V scale group
     constexpr int kPs = ASYM ? kGroups : 1;
     f16x8 a0[kPs], a1[kPs];
-    if constexpr (!ASYM) {
+    if constexpr (LIT) {
+      // per-channel V scales apply after the tile's PV products
+      const uint32_t pk0 = pack_f16(pr[0], pr[1]), pk1 = pack_f16(pr[2], pr[3]);
+      a0[0] = __builtin_bit_cast(f16x8, u32x4{sq == 0 ? pk0 : z, sq == 0 ? pk1 : z, sq == 1 ? pk0 : z, sq == 1 ? pk1 : z});
+      a1[0] = __builtin_bit_cast(f16x8, u32x4{sq == 2 ? pk0 : z, sq == 2 ? pk1 : z, sq == 3 ? pk0 : z, sq == 3 ? pk1 : z});
+    } else if constexpr (!ASYM) {
       // scales sit in the low halves of the stage's scale dwords
       const u32x4 sv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd);
       const uint32_t pk0 = pack_f16(pr[0] * h2f(static_cast<uint16_t>(sv[0])), pr[1] * h2f(static_cast<uint16_t>(sv[1])));
@@ -708,7 +753,37 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
     }
     // channel tile c lies in 32-channel group c >> 1 (both code widths)
-    if (VB == 4) {
+    if (VB == 8) {
+      // literal INT2 V: ternary int8 codes c -> fp16 6 + c (low two bits, sign
+      // bit flipped, into mantissa bits 8..9 of 4.0).  Each tile's products
+      // are offset-corrected (6 * sum P) and scaled per channel before they
+      // join the running accumulator.
+      f32x4 toff = {0, 0, 0, 0};
+      toff = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[0], boff, toff, 0, 0, 0);
+      toff = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[0], boff, toff, 0, 0, 0);
+      const __attribute__((address_space(3))) uint16_t* lsc =
+          reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(sp + lsc_rd);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const i32x2 x0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            reinterpret_cast<lds_i32x2*>(const_cast<lds_u8*>(sp) + vrd[0] + 16 * (c ^ vrd[1])));
+        const i32x2 x1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            reinterpret_cast<lds_i32x2*>(const_cast<lds_u8*>(sp) + vrd[2] + 16 * (c ^ vrd[3])));
+        const uint32_t w0 = static_cast<uint32_t>(x0[0]), w1 = static_cast<uint32_t>(x0[1]);
+        const uint32_t w2 = static_cast<uint32_t>(x1[0]), w3 = static_cast<uint32_t>(x1[1]);
+        // bytes (0, 2) -> slots (0, 1), bytes (1, 3) -> slots (2, 3)
+        const u32x4 b0 = {((w0 << 8) & vmask) ^ vcst, (w0 & vmask) ^ vcst, ((w1 << 8) & vmask) ^ vcst,
+                          (w1 & vmask) ^ vcst};
+        const u32x4 b1 = {((w2 << 8) & vmask) ^ vcst, (w2 & vmask) ^ vcst, ((w3 << 8) & vmask) ^ vcst,
+                          (w3 & vmask) ^ vcst};
+        f32x4 tc = {0, 0, 0, 0};
+        tc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[0], __builtin_bit_cast(f16x8, b0), tc, 0, 0, 0);
+        tc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[0], __builtin_bit_cast(f16x8, b1), tc, 0, 0, 0);
+        const float sc = h2f(lsc[16 * c]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[c][i] = fmaf(sc, tc[i] - toff[i], acc[c][i]);
+      }
+    } else if (VB == 4) {
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         const int gp = ASYM ? c >> 1 : 0;
@@ -737,10 +812,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[gp], __builtin_bit_cast(f16x8, s1), acc[2 * c4 + 1], 0, 0, 0);
       }
     }
+    if constexpr (!LIT) {
 #pragma unroll
-    for (int gp = 0; gp < kPs; ++gp) {
-      acc_off[gp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[gp], boff, acc_off[gp], 0, 0, 0);
-      acc_off[gp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[gp], boff, acc_off[gp], 0, 0, 0);
+      for (int gp = 0; gp < kPs; ++gp) {
+        acc_off[gp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[gp], boff, acc_off[gp], 0, 0, 0);
+        acc_off[gp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[gp], boff, acc_off[gp], 0, 0, 0);
+      }
     }
   };
 
@@ -889,12 +966,17 @@ bool fp16_tier_ok(const Fp16Tier& t) {
 bool int4_supports(const Params& p) {
   const MidTier& m = p.mid;
   if (m.len <= 0 || p.G > 4) return false;
-  if ((m.k_bits != 4 && m.k_bits != 2) || (m.v_bits != 4 && m.v_bits != 2)) return false;
+  const bool bits_ok = (m.k_bits == 4 || m.k_bits == 2) && (m.v_bits == 4 || m.v_bits == 2);
   if (m.fmt == FADE_MID_SYM) {
+    if (!bits_ok) return false;
     if (m.k_bits != m.v_bits) return false;
     if (!aligned(m.k_scale, 4) || !aligned(m.v_scale, 2)) return false;
+  } else if (m.fmt == FADE_MID_K4V2G) {
+    // K as the reference INT4 format; V literal int8 codes in 64-token groups
+    if (m.group != kTile || m.v_rows < m.len || m.v_rows % kTile) return false;
+    if (!aligned(m.k_scale, 4) || !aligned(m.v_scale, 4)) return false;
   } else if (m.fmt == FADE_MID_ASYM) {
-    if (m.group != 32) return false;
+    if (!bits_ok || m.group != 32) return false;
     if (!aligned(m.k_scale, 4) || !aligned(m.k_zero, 4) || !aligned(m.v_scale, 4) || !aligned(m.v_zero, 4))
       return false;
   } else {
@@ -918,23 +1000,26 @@ typedef void (*PackedKernel)(Params);
 
 // The kernel instance for a middle tier int4_supports accepted.
 PackedKernel packed_kernel(const Params& p, int* index) {
-  const bool asym = p.mid.fmt == FADE_MID_ASYM;
   const int kb = p.mid.k_bits, vb = p.mid.v_bits;
-  if (!asym) {
-    *index = kb == 4 ? 0 : 1;
-    return kb == 4 ? decode_packed_kernel<4, 4, false> : decode_packed_kernel<2, 2, false>;
+  if (p.mid.fmt == FADE_MID_K4V2G) {
+    *index = 6;
+    return decode_packed_kernel<4, 8, kFmtLit>;
   }
-  if (kb == 4 && vb == 4) { *index = 2; return decode_packed_kernel<4, 4, true>; }
-  if (kb == 4 && vb == 2) { *index = 3; return decode_packed_kernel<4, 2, true>; }
-  if (kb == 2 && vb == 2) { *index = 4; return decode_packed_kernel<2, 2, true>; }
+  if (p.mid.fmt == FADE_MID_SYM) {
+    *index = kb == 4 ? 0 : 1;
+    return kb == 4 ? decode_packed_kernel<4, 4, kFmtSym> : decode_packed_kernel<2, 2, kFmtSym>;
+  }
+  if (kb == 4 && vb == 4) { *index = 2; return decode_packed_kernel<4, 4, kFmtAsym>; }
+  if (kb == 4 && vb == 2) { *index = 3; return decode_packed_kernel<4, 2, kFmtAsym>; }
+  if (kb == 2 && vb == 2) { *index = 4; return decode_packed_kernel<2, 2, kFmtAsym>; }
   *index = 5;
-  return decode_packed_kernel<2, 4, true>;
+  return decode_packed_kernel<2, 4, kFmtAsym>;
 }
 
 }  // namespace
 
 int int4_resident_wgs(const Params& p) {
-  static int cached[6] = {0, 0, 0, 0, 0, 0};
+  static int cached[7] = {0, 0, 0, 0, 0, 0, 0};
   int idx = 0;
   const PackedKernel k = packed_kernel(p, &idx);
   if (cached[idx] > 0) return cached[idx];

@@ -120,10 +120,22 @@ def test_tiered_decode_fp16_middle_flash_decode(dev):
     assert _run(dev, q, k, v, ns, nr, mid, {"fmt": "fp16", "k": km, "v": vm}) <= ATOL
 
 
-def test_tiered_decode_k4_v2_literal(dev):
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,S,ns,nr,n_splits,kernel",
+    [
+        (1, 32, 8, 1200, 4, 256, 0, 0),  # config-2 windows, auto kernel choice
+        (1, 32, 8, 1200, 4, 256, 0, 1),  # portable kernel
+        (2, 8, 4, 777, 4, 64, 3, 2),  # G=2, ragged last group of 64
+        (1, 4, 1, 301, 0, 37, 1, 2),  # one kv head, one split
+        (2, 12, 4, 2000, 4, 64, 0, 2),  # G=3
+        (3, 16, 4, 5, 2, 2, 0, 2),  # one middle token (one padded group)
+    ],
+)
+def test_tiered_decode_k4_v2_literal(dev, B, Hq, Hkv, S, ns, nr, n_splits, kernel):
     """Config-2 parity format: INT4 K + reference grouped INT2 V (int8 codes, [G, D] scales)."""
-    print("case decode k4v2", flush=True)
-    q, k, v, ns, nr = _case(1, 32, 8, 1200, 4, 256, seed=7)
+    print(f"case decode k4v2 B={B} Hq={Hq} Hkv={Hkv} S={S} ns={ns} nr={nr} splits={n_splits} kernel={kernel}",
+          flush=True)
+    q, k, v, ns, nr = _case(B, Hq, Hkv, S, ns, nr, seed=7 + S)
     S = k.shape[2]
     km, vm = k[:, :, ns : S - nr], v[:, :, ns : S - nr]
     n = km.shape[2]
@@ -133,7 +145,7 @@ def test_tiered_decode_k4_v2_literal(dev):
     ovq, ovs = oq.quant_int2_grouped(oq.pad_to_group(vm, 64)[0], 64)
     mid = MiddleTier("k4v2", kq, vq, ks, vs, group=64, length=n)
     omid = {"fmt": "k4v2", "kq": okq, "ks": oks, "vq": ovq, "vs": ovs, "group": 64}
-    assert _run(dev, q, k, v, ns, nr, mid, omid) <= ATOL
+    assert _run(dev, q, k, v, ns, nr, mid, omid, kernel=kernel, n_splits=n_splits) <= ATOL
 
 
 @pytest.mark.parametrize("bits", [2, 4])
