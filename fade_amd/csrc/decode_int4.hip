@@ -917,39 +917,52 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   __syncthreads();
   if (!last_s) return;
-  for (int idx = tid; idx < G * kD; idx += kThreads) {
-    const int h = idx >> 7, d = idx & (kD - 1);
-    const int64_t p0 = bkv * n * 4 + h;
-    // splits in batches of 8 whose loads all issue before any is used
-    float Mh = kNegBig, o = 0.0f, L = 0.0f;
-    for (int s0 = 0; s0 < n; s0 += 8) {
-      float mm[8], ll[8], aa[8];
+  {
+    // thread (d, h0) merges heads h0 and h0 + 2 of channel d; the loads of a
+    // batch of 16 splits for both heads all issue before any is used
+    constexpr int kB = 16;
+    const int d = tid & (kD - 1), h0 = tid >> 7;
+    const int64_t p0 = bkv * n * 4;
+    float Mh[2] = {kNegBig, kNegBig}, o[2] = {0.0f, 0.0f}, L[2] = {0.0f, 0.0f};
+    for (int s0 = 0; s0 < n; s0 += kB) {
+      float mm[2][kB], ll[2][kB], aa[2][kB];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t pi = p0 + 4 * (s0 + j < n ? s0 + j : s0);
-        mm[j] = load_agent(&p.ws_ml[2 * pi]);
-        ll[j] = load_agent(&p.ws_ml[2 * pi + 1]);
-        aa[j] = load_agent(&p.ws_acc[pi * kD + d]);
-      }
-      float bm = kNegBig;
+      for (int e = 0; e < 2; ++e) {
+        const int h = h0 + 2 * e < G ? h0 + 2 * e : h0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (s0 + j < n) bm = fmaxf(bm, mm[j]);
-      const float Mn = fmaxf(Mh, bm);
-      const float r = exp2f(Mh - Mn);
-      o *= r;
-      L *= r;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (s0 + j < n) {
-          const float w = exp2f(mm[j] - Mn);
-          L += ll[j] * w;
-          o += aa[j] * w;
+        for (int j = 0; j < kB; ++j) {
+          const int64_t pi = p0 + 4 * (s0 + j < n ? s0 + j : s0) + h;
+          mm[e][j] = load_agent(&p.ws_ml[2 * pi]);
+          ll[e][j] = load_agent(&p.ws_ml[2 * pi + 1]);
+          aa[e][j] = load_agent(&p.ws_acc[pi * kD + d]);
         }
       }
-      Mh = Mn;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        float bm = kNegBig;
+#pragma unroll
+        for (int j = 0; j < kB; ++j)
+          if (s0 + j < n) bm = fmaxf(bm, mm[e][j]);
+        const float Mn = fmaxf(Mh[e], bm);
+        const float r = exp2f(Mh[e] - Mn);
+        o[e] *= r;
+        L[e] *= r;
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          if (s0 + j < n) {
+            const float w = exp2f(mm[e][j] - Mn);
+            L[e] += ll[e][j] * w;
+            o[e] += aa[e][j] * w;
+          }
+        }
+        Mh[e] = Mn;
+      }
     }
-    p.out[b * p.o_sb + (kvh * G + h) * p.o_sh + d] = f2h(o / L);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int h = h0 + 2 * e;
+      if (h < G) p.out[b * p.o_sb + (kvh * G + h) * p.o_sh + d] = f2h(o[e] / L[e]);
+    }
   }
   if (tid == 0) __hip_atomic_store(&p.counters[bkv], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
