@@ -359,7 +359,7 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
             "algorithmic_bytes_per_call": nbytes,
-            "timed": "HIP events around each call on the launch stream (one kernel: decode_packed_kernel<4,4,false>, split merge fused)",
+            "timed": "HIP events around each call on the launch stream (one kernel: decode_packed_kernel<4,4,kFmtSym,4>, split merge fused)",
             "median_us": round(med_ms * 1e3, 2),
         },
         "extra": extra,

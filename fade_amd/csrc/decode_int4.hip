@@ -1,12 +1,14 @@
 // Matrix-core decode attention over a packed middle tier for GQA groups of up
 // to four query heads per kv head, gfx950: the reference INT4 format
 // (per-channel K scales, per-token V scales; fade/quant.py:61-92), the rotated
-// 2-bit format, and the asymmetric group-32 build formats.
+// 2-bit format, the reference K4 + literal grouped INT2 V format
+// (fade/quant.py:130-150) and the asymmetric group-32 build formats.
 //
-// Workgroup = 4 wavefronts serving one (batch row, kv head, split); wave w
-// walks tiles w, w+4, ... of the split with its own online softmax; the four
-// are merged through LDS, and the last workgroup of a (batch row, kv head)
-// to finish merges the splits (no second launch).
+// Workgroup = NW wavefronts serving one (batch row, kv head, split).  Each
+// wave runs its own online softmax over the tiles it takes: two fixed ones,
+// then tiles claimed one at a time from an LDS counter, so faster waves take
+// more.  The waves are merged through LDS, and the last workgroup of a
+// (batch row, kv head) to finish merges the splits (no second launch).
 //
 // Block-diagonal tile layout.  A packed tile is 64 tokens = four 16-token
 // sub-tiles s.  QK^T runs on int8 MFMA 16x16x64 whose k dimension carries 16
@@ -70,8 +72,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
+constexpr int kHeads = 4;               // query heads per kv head the layout serves
 constexpr int kTile = 64;                // tokens of a packed tile
 constexpr int kMini = 16;                // tokens of an fp16 tile
 constexpr int kGroups = 4;               // 32-channel groups of the asymmetric formats
@@ -192,12 +193,13 @@ __device__ __forceinline__ float half_of(uint32_t dw, int hi) {
 __device__ __forceinline__ int lit_swz(int r) { return ((r >> 1) & 3) | ((r >> 2) & 4); }
 
 // LDS: two ring stages per wave (8.25 KB for the reference INT4 / 2-bit
-// formats, 8 or 10 KB for the asymmetric ones, 12.25 KB for literal INT2 V);
-// at <= 80 KB per workgroup two workgroups share a CU, and registers are sized
-// for that (two waves per SIMD).
-template <int KB, int VB, int FMT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_packed_kernel(
+// formats, 8 or 10 KB for the asymmetric ones, 12.25 KB for literal INT2 V).
+// NW waves per workgroup (4, 6 or 8; see packed_kernel); registers are sized
+// for two waves per SIMD.
+template <int KB, int VB, int FMT, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_packed_kernel(
     Params p) {
+  constexpr int kWaves = NW, kThreads = 64 * NW;
   constexpr bool ASYM = FMT == kFmtAsym;  // asymmetric group-32 formats
   constexpr bool LIT = FMT == kFmtLit;    // K4 + literal grouped INT2 V (int8 codes)
   using S = Stage<KB, VB, FMT>;
@@ -217,13 +219,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int64_t nT = nFt + (M + kTile - 1) / kTile;
   const int64_t t0 = static_cast<int64_t>(split) * p.tiles_per_split;
   const int64_t t1 = t0 + p.tiles_per_split < nT ? t0 + p.tiles_per_split : nT;
-  // this wave's tiles: t0 + wave + 4i, i < n_w
-  const int n_w = t0 + wave < t1 ? static_cast<int>((t1 - t0 - wave + kWaves - 1) / kWaves) : 0;
+  // Tiles of the split: the first two of each wave are t0 + wave and
+  // t0 + NW + wave; after that waves claim tiles t0 + 2 NW + c in order
+  // through an LDS counter, so that a wave that runs faster (e.g. the older
+  // wave of a SIMD, which wins issue arbitration) takes more of them.
+  const int n = p.n_splits;
+  __shared__ int claim_s;
+  if (tid == 0) claim_s = 0;
 
   __shared__ __attribute__((aligned(16))) uint8_t ring0[kWaves][S::kBytes];
   __shared__ __attribute__((aligned(16))) uint8_t ring1[kWaves][S::kBytes];
-  __shared__ __attribute__((aligned(16))) uint32_t qraw_s[4][kD / 2];  // fp16 query rows
-  __shared__ __attribute__((aligned(16))) uint32_t ksraw_s[ASYM ? 1 : kWaves][kD / 2];  // K scales per wave
+  __shared__ __attribute__((aligned(16))) uint32_t qraw_s[kHeads][kD / 2];  // fp16 query rows
+  __shared__ __attribute__((aligned(16))) uint32_t ksraw_s[ASYM ? 1 : kHeads][kD / 2];  // K scales (waves 0..3)
   __shared__ __attribute__((aligned(16))) uint8_t qd_s[kQdZero + 16];
   __shared__ float qsc_s[4];
   __shared__ int qoff_s[4][kGroups];    // asymmetric: 128 * sum of the query digits of a group
@@ -372,29 +379,31 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   {
     const uint32_t qa = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&qraw_s[wave][0])));
     if (wave < G) lds_dma4(p.q + b * p.q_sb + (kvh * G + wave) * p.q_sh + 2 * lane, qa);
-    else qraw_s[wave][lane] = 0u;
-    if constexpr (!ASYM) {
+    else if (wave < kHeads) qraw_s[wave][lane] = 0u;
+    if (!ASYM && wave < kHeads) {
       const uint32_t ka = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&ksraw_s[wave][0])));
       lds_dma4(p.mid.k_scale + bkv * kD + 2 * lane, ka);
     }
   }
-  auto ops_of = [&](int i) { return i < n_w ? (t0 + wave + kWaves * i < nFt ? kOpsF16 : kOps) : 0; };
+  auto ops_t = [&](int64_t t) { return t < t1 ? (t < nFt ? kOpsF16 : kOps) : 0; };
   // s_waitcnt needs an immediate: the outstanding-op counts that can occur
-  auto wait_vm = [&](int n) {
-    if (n == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    else if (n == kOps) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kOps));
-    else if (n == kOpsF16) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kOpsF16));
-    else if (n == 2 * kOps) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kOps));
-    else if (n == kOps + kOpsF16) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kOps + kOpsF16));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kOpsF16));
+  auto wait_vm = [&](int c) {
+    constexpr int A = kOps, F = kOpsF16;
+    if (c == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    else if (c == A) __builtin_amdgcn_s_waitcnt(vmcnt_imm(A));
+    else if (c == F) __builtin_amdgcn_s_waitcnt(vmcnt_imm(F));
+    else if (c == 2 * A) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * A));
+    else if (c == A + F) __builtin_amdgcn_s_waitcnt(vmcnt_imm(A + F));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * F));
   };
-  if (n_w > 0) issue(t0 + wave, st0);
-  if (n_w > 1) issue(t0 + wave + kWaves, st1);
-  wait_vm(ops_of(0) + ops_of(1));  // the query (and K-scale) loads have landed
+  int64_t ta = t0 + wave, tb = t0 + kWaves + wave;  // tiles in stages 0 and 1
+  if (ta < t1) issue(ta, st0);
+  if (tb < t1) issue(tb, st1);
+  wait_vm(ops_t(ta) + ops_t(tb));  // the query (and K-scale) loads have landed
   __builtin_amdgcn_wave_barrier();
 
-  // ---- query digits: wave h handles head h (channels 2*lane, 2*lane+1) ----
-  {
+  // ---- query digits: wave h < 4 handles head h (channels 2*lane, 2*lane+1) ----
+  if (wave < kHeads) {
     const int h = wave;
     const uint32_t qq = qraw_s[h][lane];
     float qf0 = h2f(static_cast<uint16_t>(qq & 0xFFFFu)), qf1 = h2f(static_cast<uint16_t>(qq >> 16));
@@ -822,22 +831,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   };
 
   // ---- main loop: two stages, two tiles in flight ----
-  auto step = [&](int i, const lds_u8* sp, uint32_t st) {
-    const int64_t t = t0 + wave + static_cast<int64_t>(kWaves) * i;
-    wait_vm(ops_of(i + 1));  // tile i landed; tile i+1 (if any) may still be in flight
+  // step: tile `cur` sits in stage (sp, st), `nxt` (if any) is in flight behind
+  // it; afterwards the stage is refilled with a newly claimed tile, returned
+  // (>= t1 when the split is exhausted; claims only grow).
+  auto step = [&](int64_t cur, int64_t nxt, const lds_u8* sp, uint32_t st) -> int64_t {
+    wait_vm(ops_t(nxt));  // `cur` landed
     __builtin_amdgcn_wave_barrier();
-    if (t < nFt) fp16_tile(t, sp);
-    else packed_tile(t, sp);
+    if (cur < nFt) fp16_tile(cur, sp);
+    else packed_tile(cur, sp);
     __builtin_amdgcn_s_waitcnt(kLgkm0);  // every LDS read of this stage has returned
     __builtin_amdgcn_wave_barrier();
-    if (i + 2 < n_w) issue(t + 2 * kWaves, st);
+    int c = 0;
+    if (lane == 0) c = __hip_atomic_fetch_add(&claim_s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const int64_t nt = t0 + 2 * kWaves + __builtin_amdgcn_readfirstlane(c);
+    if (nt < t1) issue(nt, st);
+    return nt;
   };
-  for (int i = 0; i < n_w; i += 2) {
-    step(i, sp0, st0);
-    if (i + 1 < n_w) step(i + 1, sp1, st1);
+  while (ta < t1) {
+    const int64_t na = step(ta, tb, sp0, st0);
+    if (tb >= t1) break;
+    tb = step(tb, na, sp1, st1);
+    ta = na;
   }
 
-  // ---- merge the four wavefronts ----
+  // ---- merge the wavefronts of the workgroup ----
   float lsum = l_run;
   lsum += __shfl_xor(lsum, 1, 64);
   lsum += __shfl_xor(lsum, 2, 64);
@@ -861,7 +878,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     red_l[wave][hq] = lsum;
   }
   __syncthreads();
-  float* red_o = reinterpret_cast<float*>(&ring0[0][0]);  // [wave][4 heads][128]
+  float* red_o = reinterpret_cast<float*>(&ring0[0][0]);  // [wave][4 heads][128] (NW * 2 KB)
   {
     float Mg = red_m[0][g];
 #pragma unroll
@@ -878,7 +895,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   }
   __syncthreads();
-  const int n = p.n_splits;
   for (int idx = tid; idx < G * kD; idx += kThreads) {
     const int h = idx >> 7, d = idx & (kD - 1);
     float Mh = red_m[0][h];
@@ -918,17 +934,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   __syncthreads();
   if (!last_s) return;
   {
-    // thread (d, h0) merges heads h0 and h0 + 2 of channel d; the loads of a
-    // batch of 16 splits for both heads all issue before any is used
-    constexpr int kB = 16;
-    const int d = tid & (kD - 1), h0 = tid >> 7;
+    // thread tid merges items (head, channel) tid + e * kThreads; the loads of
+    // a batch of 16 splits for all its items issue before any is used
+    constexpr int kB = 16, kE = (kHeads * kD + kThreads - 1) / kThreads;
     const int64_t p0 = bkv * n * 4;
-    float Mh[2] = {kNegBig, kNegBig}, o[2] = {0.0f, 0.0f}, L[2] = {0.0f, 0.0f};
-    for (int s0 = 0; s0 < n; s0 += kB) {
-      float mm[2][kB], ll[2][kB], aa[2][kB];
+    float Mh[kE], o[kE], L[kE];
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int h = h0 + 2 * e < G ? h0 + 2 * e : h0;
+    for (int e = 0; e < kE; ++e) {
+      Mh[e] = kNegBig;
+      o[e] = 0.0f;
+      L[e] = 0.0f;
+    }
+    for (int s0 = 0; s0 < n; s0 += kB) {
+      float mm[kE][kB], ll[kE][kB], aa[kE][kB];
+#pragma unroll
+      for (int e = 0; e < kE; ++e) {
+        const int idx = tid + e * kThreads;
+        const int h = idx < G * kD ? idx >> 7 : 0, d = idx & (kD - 1);
 #pragma unroll
         for (int j = 0; j < kB; ++j) {
           const int64_t pi = p0 + 4 * (s0 + j < n ? s0 + j : s0) + h;
@@ -938,7 +960,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
       }
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
+      for (int e = 0; e < kE; ++e) {
         float bm = kNegBig;
 #pragma unroll
         for (int j = 0; j < kB; ++j)
@@ -959,9 +981,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
     }
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int h = h0 + 2 * e;
-      if (h < G) p.out[b * p.o_sb + (kvh * G + h) * p.o_sh + d] = f2h(o[e] / L[e]);
+    for (int e = 0; e < kE; ++e) {
+      const int idx = tid + e * kThreads;
+      if (idx < G * kD) p.out[b * p.o_sb + (kvh * G + (idx >> 7)) * p.o_sh + (idx & (kD - 1))] = f2h(o[e] / L[e]);
     }
   }
   if (tid == 0) __hip_atomic_store(&p.counters[bkv], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1011,47 +1033,51 @@ namespace {
 
 typedef void (*PackedKernel)(Params);
 
-// The kernel instance for a middle tier int4_supports accepted.
-PackedKernel packed_kernel(const Params& p, int* index) {
+struct Choice {
+  PackedKernel k;
+  int waves;  // wavefronts per workgroup (one workgroup per CU)
+  int index;
+};
+
+// The kernel instance for a middle tier int4_supports accepted (wave counts
+// measured best on MI355X): the reference INT4 format runs two 4-wave
+// workgroups per CU; the others one workgroup per CU, of eight waves where two
+// stages per wave fit the 160 KB of LDS, six for the 10 and 12.25 KB stages.
+Choice packed_kernel(const Params& p) {
   const int kb = p.mid.k_bits, vb = p.mid.v_bits;
-  if (p.mid.fmt == FADE_MID_K4V2G) {
-    *index = 6;
-    return decode_packed_kernel<4, 8, kFmtLit>;
-  }
+  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6>, 6, 6};
   if (p.mid.fmt == FADE_MID_SYM) {
-    *index = kb == 4 ? 0 : 1;
-    return kb == 4 ? decode_packed_kernel<4, 4, kFmtSym> : decode_packed_kernel<2, 2, kFmtSym>;
+    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4>, 4, 0};  // two workgroups per CU
+    return {decode_packed_kernel<2, 2, kFmtSym, 8>, 8, 1};
   }
-  if (kb == 4 && vb == 4) { *index = 2; return decode_packed_kernel<4, 4, kFmtAsym>; }
-  if (kb == 4 && vb == 2) { *index = 3; return decode_packed_kernel<4, 2, kFmtAsym>; }
-  if (kb == 2 && vb == 2) { *index = 4; return decode_packed_kernel<2, 2, kFmtAsym>; }
-  *index = 5;
-  return decode_packed_kernel<2, 4, kFmtAsym>;
+  if (kb == 4 && vb == 4) return {decode_packed_kernel<4, 4, kFmtAsym, 6>, 6, 2};
+  if (kb == 4 && vb == 2) return {decode_packed_kernel<4, 2, kFmtAsym, 8>, 8, 3};
+  if (kb == 2 && vb == 2) return {decode_packed_kernel<2, 2, kFmtAsym, 8>, 8, 4};
+  return {decode_packed_kernel<2, 4, kFmtAsym, 6>, 6, 5};
 }
 
 }  // namespace
 
 int int4_resident_wgs(const Params& p) {
   static int cached[7] = {0, 0, 0, 0, 0, 0, 0};
-  int idx = 0;
-  const PackedKernel k = packed_kernel(p, &idx);
-  if (cached[idx] > 0) return cached[idx];
+  const Choice c = packed_kernel(p);
+  if (cached[c.index] > 0) return cached[c.index];
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, 0) != hipSuccess || cus <= 0 ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, c.k, 64 * c.waves, 0) != hipSuccess || cus <= 0 ||
       per_cu <= 0) {
     (void)hipGetLastError();
-    return 512;
+    return 256;
   }
-  cached[idx] = cus * per_cu;
-  return cached[idx];
+  cached[c.index] = cus * per_cu;
+  return cached[c.index];
 }
 
 int launch_int4(const Params& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv), static_cast<unsigned>(p.B));
-  int idx = 0;
-  hipLaunchKernelGGL(packed_kernel(p, &idx), grid, dim3(kThreads), 0, st, p);
+  const Choice c = packed_kernel(p);
+  hipLaunchKernelGGL(c.k, grid, dim3(64 * c.waves), 0, st, p);
   return check_launch("fade_tiered_decode_attn(packed)");
 }
 
