@@ -16,6 +16,7 @@ resident in HBM before timing starts.  Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -27,6 +28,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+from fade_amd import _lib  # noqa: E402
 from fade_amd import quant as fq  # noqa: E402
 from fade_amd import rotated_quant as frq  # noqa: E402
 from fade_amd.kernels.tiered_attn import MiddleTier, TieredDecodePlan  # noqa: E402
@@ -120,6 +122,105 @@ def time_plans(plans, steps: int, warmup: int, stream):
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+class CallPlan:
+    """One C-ABI call with preallocated arguments; ``run(stream)`` enqueues it."""
+
+    def __init__(self, name: str, args_fn, keep):
+        self.fn = getattr(_lib.load(), name)
+        self.name, self.args_fn, self._keep = name, args_fn, keep
+
+    def run(self, stream: int | None = None) -> None:
+        s = torch.cuda.current_stream().cuda_stream if stream is None else stream
+        _lib.check(self.fn(*self.args_fn(s)), self.name)
+
+
+def quant_cases(dev):
+    """Middle-tier quantizers at full size: config 1 (reference INT4 K and V) and
+    config 2 (asymmetric group-32 K4 / V2).  Bytes: fp16 read once + codes and
+    scales written (a two-phase kernel's re-read of K is not counted)."""
+    out = []
+    c1 = CONFIGS[1]
+    _, k, v = kv_tensors(c1.B, c1.Hkv, c1.S, c1.D, seed=1001, Hq=c1.Hq)
+    km = k[:, :, c1.n_sink : c1.S - c1.recent].contiguous().to(dev)
+    vm = v[:, :, c1.n_sink : c1.S - c1.recent].contiguous().to(dev)
+    del k, v
+    B, H, S, D = km.shape
+    kp = torch.empty(B, H, S, D // 2, dtype=torch.uint8, device=dev)
+    ks = torch.empty(B, H, 1, D, dtype=torch.float16, device=dev)
+    nb = ctypes.c_int64(0)
+    _lib.check(_lib.load().fade_quant_k_int4_workspace_bytes(B, H, S, D, nb), "ws")
+    ws = _lib.workspace(nb.value, dev)
+    st = (km.stride(0), km.stride(1), km.stride(2))
+    out.append(("c1_quant_k_int4", CallPlan("fade_quant_k_int4", lambda s_: (
+        km.data_ptr(), B, H, S, D, *st, kp.data_ptr(), ks.data_ptr(), ws.data_ptr(), ws.numel(), s_),
+        (km, kp, ks, ws)), km.numel() * 2 + kp.numel() + ks.numel() * 2))
+    vp = torch.empty(B, H, S, D // 2, dtype=torch.uint8, device=dev)
+    vs = torch.empty(B, H, S, 1, dtype=torch.float16, device=dev)
+    out.append(("c1_quant_v_int4", CallPlan("fade_quant_v_int4", lambda s_: (
+        vm.data_ptr(), B, H, S, D, *st, vp.data_ptr(), vs.data_ptr(), s_), (vm, vp, vs)),
+        vm.numel() * 2 + vp.numel() + vs.numel() * 2))
+    c2 = CONFIGS[2]
+    _, k2, v2 = kv_tensors(c2.B, c2.Hkv, c2.S, c2.D, seed=1002, Hq=c2.Hq)
+    for name, x, bits in (("c2_quant_asym_k4", k2, 4), ("c2_quant_asym_v2", v2, 2)):
+        xm = x[:, :, c2.n_sink : c2.S - c2.recent].contiguous().to(dev)
+        B, H, S, D = xm.shape
+        pk = torch.empty(B, H, S, D * bits // 8, dtype=torch.uint8, device=dev)
+        sc = torch.empty(B, H, S, D // 32, dtype=torch.float16, device=dev)
+        zp = torch.empty_like(sc)
+        xs = (xm.stride(0), xm.stride(1), xm.stride(2))
+        out.append((name, CallPlan("fade_quant_asym", lambda s_, xm=xm, pk=pk, sc=sc, zp=zp, xs=xs, bits=bits, sh=(B, H, S, D): (
+            xm.data_ptr(), *sh, *xs, bits, 32, pk.data_ptr(), sc.data_ptr(), zp.data_ptr(), s_), (xm, pk, sc, zp)),
+            xm.numel() * 2 + pk.numel() + 2 * sc.numel() * 2))
+    return out
+
+
+def rerope_case(dev):
+    """Config 3: eviction re-RoPE of the kept rows (K un-RoPE at the old
+    positions, re-RoPE at 0..n_kept-1) plus the V gather, B=8, Hkv=4, S=4096,
+    kept = 4 sink + 400 highest-scoring middle + 64 recent rows."""
+    from fade_amd.rope import Vanilla
+    from fade_amd.synthetic import exp_scores
+
+    B, H, S, D = 8, 4, 4096, 128
+    _, k, v = kv_tensors(B, H, S, D, seed=1003, Hq=28)
+    rope = Vanilla(theta=1.0e6, head_dim=D)
+    cos_o, sin_o = rope.host_cos_sin(torch.arange(S))
+    kf = k.float()
+    half = D // 2
+    rot = torch.cat((-kf[..., half:], kf[..., :half]), dim=-1)
+    k_post = (kf * cos_o + rot * sin_o).half()  # K after RoPE at positions 0..S-1
+    sc = exp_scores(S, 1003)
+    mid = torch.arange(4, S - 64)
+    top = mid[torch.argsort(sc[4 : S - 64], descending=True)[:400]]
+    keep = torch.sort(torch.cat((torch.arange(4), top, torch.arange(S - 64, S)))).values
+    n = int(keep.numel())
+    cos_n, sin_n = rope.host_cos_sin(torch.arange(n))
+    kd, vd, kp = k_post.to(dev), v.to(dev), keep.to(dev)
+    tabs = [t.contiguous().to(dev) for t in (cos_o, sin_o, cos_n, sin_n)]
+    ko = torch.empty(B, H, n, D, dtype=torch.float16, device=dev)
+    vo = torch.empty_like(ko)
+    plan = CallPlan("fade_rerope_gather", lambda s_: (
+        kd.data_ptr(), *kd.stride()[:3], vd.data_ptr(), *vd.stride()[:3], B, H, S, D, kp.data_ptr(), n,
+        *(t.data_ptr() for t in tabs), ko.data_ptr(), vo.data_ptr(), s_), (kd, vd, kp, tabs, ko, vo))
+    return plan, 4 * B * H * n * D * 2, n
+
+
+def copy_peak(dev, stream) -> float:
+    """Device-to-device copy of 1 GiB (read + write), GB/s: the measured streaming ceiling."""
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            dst.copy_(src)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(10):
+            dst.copy_(src)
+        b.record(stream)
+    torch.cuda.synchronize()
+    return 2 * (1 << 30) * 10 / (a.elapsed_time(b) * 1e-3) / 1e9
 
 
 def prefill_case(dev, seed: int = 1004):
@@ -315,6 +416,18 @@ def main() -> int:
             "useful_flops": pflops, "GBps": round(pbytes / (pmean * 1e-3) / 1e9, 1),
         }
         del pf
+        torch.cuda.empty_cache()
+        for name, plan, nbytes_q in quant_cases(dev):
+            _, _, qmean, _ = time_plans([plan], max(20, args.steps // 4), 5, stream)
+            extra[name] = {"us": round(qmean * 1e3, 2), "GBps": round(nbytes_q / (qmean * 1e-3) / 1e9, 1),
+                           "bytes": nbytes_q, "frac_of_peak": round(nbytes_q / (qmean * 1e-3) / 1e9 / HBM_PEAK_GBPS, 3)}
+        torch.cuda.empty_cache()
+        rp, rbytes, n_kept = rerope_case(dev)
+        _, _, rmean, _ = time_plans([rp], max(20, args.steps // 4), 5, stream)
+        extra["c3_rerope_gather"] = {"us": round(rmean * 1e3, 2), "GBps": round(rbytes / (rmean * 1e-3) / 1e9, 1),
+                                     "bytes": rbytes, "n_kept": n_kept}
+        del rp
+        extra["copy_peak_GBps"] = round(copy_peak(dev, stream), 1)
         torch.cuda.empty_cache()
         c2 = CONFIGS[2]
         for fmt in ("asym42", "k4v2", "int4", "rot2"):  # asym42: the format BASELINE states for config 2
