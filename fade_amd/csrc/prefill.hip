@@ -6,19 +6,23 @@
 // the reference's materialized tiers, fade/cache.py:347-379,683-842).
 //
 // Workgroup = (32-query block, kv head, batch row); wave w serves query head
-// kvh*G + w (G <= 4), its 32 query rows as two 16-row M tiles.  The virtual
-// key sequence (cache, then chunk) is walked in 64-token tiles.  All 256
-// threads fetch a tile (thread = one token x 32 channels), dequantize middle
-// codes exactly as the reference does (fp16(code * scale)), and store fp16
-// K [token][channel] and V^T [channel][token] in LDS (double-buffered: the
-// next tile's global loads fly while the current one is computed).
+// kvh*G + w (G <= 4), its 32 query rows as two 16-row M tiles.  The row's key
+// sequence is walked in 64-token tiles that never straddle a tier (sink,
+// middle, recent, then the chunk).  All 256 threads fetch a tile (thread =
+// one token x 32 channels) into double-buffered LDS (the next tile's global
+// loads fly while the current one is computed): fp16 K and V rows as they
+// are; middle-tier codes dequantized exactly as the reference does,
+// fp16(code * scale), with three packed operations per pair of codes (72 + c
+// by one bit operation, - 72, * scale).  K and V rows keep channels in the
+// order the code conversion produces (1 5 0 4 3 7 2 6 within every 8
+// channels); the query and the output use the same order.
 //
 // Per tile and wave:
 //   S^T = K Q^T     f16 MFMA 16x16x32, A = K rows (16 keys), B = Q^T (16 rows);
 //                   lane (n, g), register i  <->  query row n, key 4g + i
 //   online softmax  row n's max/sum: lane-local over 16 keys, then 2 shuffles
 //   O += P V        f16 MFMA 16x16x32, A = P straight from the S^T registers
-//                   (key blocks paired), B = V^T rows from LDS
+//                   (key blocks paired), B = V rows via ds_read_b64_tr_b16
 // Each K and V fragment read from LDS feeds both M tiles.
 #include <math.h>
 
@@ -29,16 +33,19 @@ namespace prefill {
 namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kD = 128;
 constexpr int kThreads = 256;
 constexpr int kQB = 32;       // queries per workgroup
 constexpr int kKT = 64;       // keys per tile
-constexpr int kKPitch = 136;  // halves per K row in LDS (conflict-free 16-byte reads)
-constexpr int kVPitch = 72;   // halves per V^T row in LDS
+constexpr int kKPitch = 136;  // halves per K row in LDS (16-byte reads of 16 rows: distinct banks)
+constexpr int kVPitch = 144;  // halves per V row in LDS (tr16 reads of 4 rows x 4 chunks: distinct banks)
 constexpr float kNegBig = -1.0e30f;
 constexpr float kTau = 8.0f;  // the running max moves only when a score exceeds it by kTau (log2)
 
@@ -67,18 +74,25 @@ struct PParams {
   const uint16_t* vs;
 };
 
-__device__ __forceinline__ uint32_t pack2(_Float16 a, _Float16 b) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+// Eight two's-complement nibbles (one dword of packed codes, high nibble =
+// even channel) -> four fp16 pairs of value 72 + c: the nibble goes to
+// mantissa bits 4..7 of 64.0 (one code step = 1.0) with its top bit flipped.
+// The pairs come out as channels (1,5), (0,4), (3,7), (2,6) of the dword:
+// K and V rows are stored in LDS in that order within every 8-channel group.
+__device__ __forceinline__ void nib_to_f16(uint32_t w, uint32_t (&o)[4]) {
+  o[0] = ((w << 4) & 0x00F000F0u) ^ 0x54805480u;
+  o[1] = (w & 0x00F000F0u) ^ 0x54805480u;
+  o[2] = ((w >> 4) & 0x00F000F0u) ^ 0x54805480u;
+  o[3] = ((w >> 8) & 0x00F000F0u) ^ 0x54805480u;
 }
-
-// Signed nibbles of one packed byte (high nibble = even channel) as fp16.
-__device__ __forceinline__ void nib2(uint32_t byte, _Float16& even, _Float16& odd) {
-  const int hi = static_cast<int>(static_cast<int8_t>(byte & 0xFFu)) >> 4;
-  const int lo = static_cast<int>((byte & 0xFu) << 28) >> 28;
-  even = static_cast<_Float16>(hi);
-  odd = static_cast<_Float16>(lo);
+// Eight fp16 channels (natural order, dwords = channel pairs) -> the stored order.
+__device__ __forceinline__ u32x4 to_stored(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3) {
+  return u32x4{__builtin_amdgcn_perm(d2, d0, 0x07060302u), __builtin_amdgcn_perm(d2, d0, 0x05040100u),
+               __builtin_amdgcn_perm(d3, d1, 0x07060302u), __builtin_amdgcn_perm(d3, d1, 0x05040100u)};
 }
+// Channel of stored half h within an 8-channel group.
+// (1 5 0 4 3 7 2 6, one nibble per h)
+__device__ __forceinline__ int stored_channel(int h) { return (0x62734051 >> (4 * h)) & 0xF; }
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PParams p) {
   const int qb = blockIdx.x;
@@ -98,119 +112,120 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int ns = clampi(__builtin_amdgcn_readfirstlane(p.lens[3 * b + 0]), p.sink_cap);
   const int nm = clampi(__builtin_amdgcn_readfirstlane(p.lens[3 * b + 1]), p.mid_cap);
   const int nr = clampi(__builtin_amdgcn_readfirstlane(p.lens[3 * b + 2]), p.recent_cap);
-  const int L = ns + nm + nr;  // cache tokens of this row
   const int Sq = static_cast<int>(p.Sq);
   const int j0 = qb * kQB;
   const int jn = Sq - j0 < kQB ? Sq - j0 : kQB;  // queries of this block
-  const int t_end = L + j0 + jn;                 // keys any query of the block can see
-  const int n_tiles = (t_end + kKT - 1) / kKT;
+  const int cv = j0 + jn;                        // chunk keys any query of the block can see
+  // Key tiles never straddle a tier: sink, middle, recent, chunk tiles in turn.
+  const int nts = (ns + kKT - 1) / kKT, ntm = (nm + kKT - 1) / kKT, ntr = (nr + kKT - 1) / kKT;
+  const int n_tiles = nts + ntm + ntr + (cv + kKT - 1) / kKT;
+  struct TileRef {
+    int seg, base, cnt;  // segment (0 sink, 1 middle, 2 recent, 3 chunk), first key, keys
+  };
+  auto tile_of = [&](int t) {
+    TileRef r;
+    int len;
+    if (t < nts) {
+      r.seg = 0; r.base = kKT * t; len = ns;
+    } else if (t < nts + ntm) {
+      r.seg = 1; r.base = kKT * (t - nts); len = nm;
+    } else if (t < nts + ntm + ntr) {
+      r.seg = 2; r.base = kKT * (t - nts - ntm); len = nr;
+    } else {
+      r.seg = 3; r.base = kKT * (t - nts - ntm - ntr); len = cv;
+    }
+    r.cnt = len - r.base < kKT ? len - r.base : kKT;
+    return r;
+  };
 
   __shared__ __attribute__((aligned(16))) uint16_t kt[2][kKT][kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[2][kD][kVPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[2][kKT][kVPitch];
 
   // ---- tile fetch: thread = token r of the tile, channels 32*cp .. 32*cp+31 ----
   const int r = tid >> 2, cp = tid & 3;
-  uint32_t ksc[16];  // fp16 K scales of this thread's channels (middle tier)
-  if (p.has_mid) {
-    const uint4* s4 = reinterpret_cast<const uint4*>(p.ks + bkv * kD + 32 * cp);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 w = s4[i];
-      ksc[4 * i + 0] = w.x;
-      ksc[4 * i + 1] = w.y;
-      ksc[4 * i + 2] = w.z;
-      ksc[4 * i + 3] = w.w;
-    }
-  }
-  // sink / recent / chunk row pointers of this (b, kv head)
   const uint16_t* sk = p.sink.k + b * p.sink.k_sb + kvh * p.sink.k_sh;
   const uint16_t* sv = p.sink.v + b * p.sink.v_sb + kvh * p.sink.v_sh;
   const uint16_t* rk = p.recent.k + b * p.recent.k_sb + kvh * p.recent.k_sh;
   const uint16_t* rv = p.recent.v + b * p.recent.v_sb + kvh * p.recent.v_sh;
   const uint16_t* ck = p.chunk.k + b * p.chunk.k_sb + kvh * p.chunk.k_sh;
-  const uint16_t* cv = p.chunk.v + b * p.chunk.v_sb + kvh * p.chunk.v_sh;
+  const uint16_t* cvp = p.chunk.v + b * p.chunk.v_sb + kvh * p.chunk.v_sh;
   const int64_t sk_ss = p.sink.k_ss, sv_ss = p.sink.v_ss, rk_ss = p.recent.k_ss, rv_ss = p.recent.v_ss;
   const int64_t ck_ss = p.chunk.k_ss, cv_ss = p.chunk.v_ss;
   const uint8_t* kq = p.kq + bkv * p.mid_cap * 64;
   const uint8_t* vq = p.vq + bkv * p.mid_cap * 64;
   const uint16_t* vsr = p.vs + bkv * p.mid_cap;
 
-  uint4 fk[4], fv[4];  // fetched K / V (fp16 rows: 64 bytes; middle codes: 16 bytes in fk[0] / fv[0])
-  int fkind = 0;       // 0 none, 1 fp16 row, 2 middle codes
-  uint16_t fvs = 0;    // V scale of a middle token
-  auto fetch = [&](int t) {
-    const int v = t * kKT + r;
-    fkind = 0;
-    const uint16_t* kp = nullptr;
-    const uint16_t* vp = nullptr;
-    if (v < ns) {
-      kp = sk + v * sk_ss;
-      vp = sv + v * sv_ss;
-    } else if (v < ns + nm) {
-      const int m = v - ns;
-      fk[0] = *reinterpret_cast<const uint4*>(kq + static_cast<int64_t>(m) * 64 + 16 * cp);
-      fv[0] = *reinterpret_cast<const uint4*>(vq + static_cast<int64_t>(m) * 64 + 16 * cp);
-      fvs = vsr[m];
-      fkind = 2;
-    } else if (v < L) {
-      kp = rk + (v - ns - nm) * rk_ss;
-      vp = rv + (v - ns - nm) * rv_ss;
-    } else if (v < L + Sq) {
-      kp = ck + (v - L) * ck_ss;
-      vp = cv + (v - L) * cv_ss;
-    }
-    if (kp != nullptr) {
-      const uint4* k4 = reinterpret_cast<const uint4*>(kp + 32 * cp);
-      const uint4* v4 = reinterpret_cast<const uint4*>(vp + 32 * cp);
+  // K scales of this thread's 32 channels as fp16 pairs, in the stored order
+  uint32_t ksc[16];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        fk[i] = k4[i];
-        fv[i] = v4[i];
-      }
-      fkind = 1;
+  for (int i = 0; i < 4; ++i) {
+    uint4 w = make_uint4(0, 0, 0, 0);
+    if (p.has_mid) w = *reinterpret_cast<const uint4*>(p.ks + bkv * kD + 32 * cp + 8 * i);
+    const u32x4 st = to_stored(w.x, w.y, w.z, w.w);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ksc[4 * i + e] = st[e];
+  }
+  uint4 fk[4], fv[4];  // fetched K / V (fp16 rows: 64 bytes; middle codes: 16 bytes in fk[0] / fv[0])
+  int fmid = 0;
+  uint32_t fvs = 0;    // V scale of a middle token, as an fp16 pair
+  auto fetch = [&](int t) {
+    const TileRef tr = tile_of(t);
+    const int key = tr.base + r;
+    const bool ok = r < tr.cnt;
+    fmid = tr.seg == 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fk[i] = fv[i] = make_uint4(0, 0, 0, 0);
+    fvs = 0;
+    if (!ok) return;
+    if (tr.seg == 1) {
+      fk[0] = *reinterpret_cast<const uint4*>(kq + static_cast<int64_t>(key) * 64 + 16 * cp);
+      fv[0] = *reinterpret_cast<const uint4*>(vq + static_cast<int64_t>(key) * 64 + 16 * cp);
+      fvs = static_cast<uint32_t>(vsr[key]) * 0x00010001u;
+      return;
+    }
+    const uint16_t* kp = tr.seg == 0 ? sk + key * sk_ss : (tr.seg == 2 ? rk + key * rk_ss : ck + key * ck_ss);
+    const uint16_t* vp = tr.seg == 0 ? sv + key * sv_ss : (tr.seg == 2 ? rv + key * rv_ss : cvp + key * cv_ss);
+    const uint4* k4 = reinterpret_cast<const uint4*>(kp + 32 * cp);
+    const uint4* v4 = reinterpret_cast<const uint4*>(vp + 32 * cp);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fk[i] = k4[i];
+      fv[i] = v4[i];
     }
   };
   auto store = [&](int buf) {
-    uint32_t kw[16], vw[16];
-    if (fkind == 1) {
+    if (fmid) {
+      // codes -> fp16 72 + c -> c -> fp16(c * scale), already in the stored channel order
+      const uint32_t kw[4] = {fk[0].x, fk[0].y, fk[0].z, fk[0].w};
+      const uint32_t vw[4] = {fv[0].x, fv[0].y, fv[0].z, fv[0].w};
+      const f16x2 m72 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+      const f16x2 vs2 = __builtin_bit_cast(f16x2, fvs);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        kw[4 * i + 0] = fk[i].x; kw[4 * i + 1] = fk[i].y; kw[4 * i + 2] = fk[i].z; kw[4 * i + 3] = fk[i].w;
-        vw[4 * i + 0] = fv[i].x; vw[4 * i + 1] = fv[i].y; vw[4 * i + 2] = fv[i].z; vw[4 * i + 3] = fv[i].w;
-      }
-    } else if (fkind == 2) {
-      // fp16(code * scale): the reference's dequantization (fade/quant.py:124-127)
-      const _Float16 vscale = __builtin_bit_cast(_Float16, fvs);
-      const uint32_t kb4[4] = {fk[0].x, fk[0].y, fk[0].z, fk[0].w};
-      const uint32_t vb4[4] = {fv[0].x, fv[0].y, fv[0].z, fv[0].w};
+        uint32_t o[4];
+        u32x4 kd, vd;
+        nib_to_f16(kw[i], o);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint32_t kbyte = (kb4[i >> 2] >> (8 * (i & 3))) & 0xFFu;
-        const uint32_t vbyte = (vb4[i >> 2] >> (8 * (i & 3))) & 0xFFu;
-        _Float16 ke, ko, ve, vo;
-        nib2(kbyte, ke, ko);
-        nib2(vbyte, ve, vo);
-        const uint32_t s2 = ksc[i];
-        const _Float16 se = __builtin_bit_cast(_Float16, static_cast<uint16_t>(s2 & 0xFFFFu));
-        const _Float16 so = __builtin_bit_cast(_Float16, static_cast<uint16_t>(s2 >> 16));
-        kw[i] = pack2(ke * se, ko * so);
-        vw[i] = pack2(ve * vscale, vo * vscale);
+        for (int e = 0; e < 4; ++e)
+          kd[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[e]) + m72) *
+                                                   __builtin_bit_cast(f16x2, ksc[4 * i + e]));
+        nib_to_f16(vw[i], o);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          vd[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[e]) + m72) * vs2);
+        *reinterpret_cast<u32x4*>(&kt[buf][r][32 * cp + 8 * i]) = kd;
+        *reinterpret_cast<u32x4*>(&vt[buf][r][32 * cp + 8 * i]) = vd;
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) kw[i] = vw[i] = 0u;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<u32x4*>(&kt[buf][r][32 * cp + 8 * i]) = u32x4{kw[4 * i], kw[4 * i + 1], kw[4 * i + 2], kw[4 * i + 3]};
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      vt[buf][32 * cp + 2 * i][r] = static_cast<uint16_t>(vw[i] & 0xFFFFu);
-      vt[buf][32 * cp + 2 * i + 1][r] = static_cast<uint16_t>(vw[i] >> 16);
+      for (int i = 0; i < 4; ++i) {
+        *reinterpret_cast<u32x4*>(&kt[buf][r][32 * cp + 8 * i]) = to_stored(fk[i].x, fk[i].y, fk[i].z, fk[i].w);
+        *reinterpret_cast<u32x4*>(&vt[buf][r][32 * cp + 8 * i]) = to_stored(fv[i].x, fv[i].y, fv[i].z, fv[i].w);
+      }
     }
   };
 
-  // ---- query fragments: rows j0 + 16*mt + n16, B operand of S^T = K Q^T ----
+  // ---- query fragments: rows j0 + 16*mt + n16, B operand of S^T = K Q^T, stored channel order ----
   const bool active = wave < G;
   const int64_t h = kvh * G + (active ? wave : 0);
   f16x8 qf[2][4];
@@ -221,7 +236,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const uint4 w = (active && j < Sq) ? *reinterpret_cast<const uint4*>(qr + 32 * ks + 8 * g) : make_uint4(0, 0, 0, 0);
-      qf[mt][ks] = __builtin_bit_cast(f16x8, w);
+      qf[mt][ks] = __builtin_bit_cast(f16x8, to_stored(w.x, w.y, w.z, w.w));
     }
   }
 
@@ -234,6 +249,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const float sl2 = p.scale_log2;
 
   auto compute = [&](int t, int buf) {
+    const TileRef tr = tile_of(t);
     // S^T for both M tiles; each K fragment feeds both
     f32x4 s[2][4];
 #pragma unroll
@@ -252,15 +268,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const int jq = j0 + 16 * mt + n16;  // this lane's query (column n16)
-      const int lim = L + jq;             // last visible key
+      // key kk of the tile is visible when kk < cnt and, in the chunk, base + kk <= jq
+      const int lim = tr.seg == 3 ? (jq - tr.base + 1 < tr.cnt ? jq - tr.base + 1 : tr.cnt) : tr.cnt;
       float x[4][4];
       float lmax = kNegBig;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int v = t * kKT + 16 * kb + 4 * g + i;
-          x[kb][i] = v <= lim ? s[mt][kb][i] * sl2 : -INFINITY;
+          const int kk = 16 * kb + 4 * g + i;
+          x[kb][i] = kk < lim ? s[mt][kb][i] * sl2 : -INFINITY;
           lmax = fmaxf(lmax, x[kb][i]);
         }
       lmax = fmaxf(lmax, __shfl_xor(lmax, 16, 64));
@@ -294,14 +311,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         pa[mt][pp] = f16x8{ph[2 * pp][0], ph[2 * pp][1], ph[2 * pp][2], ph[2 * pp][3],
                            ph[2 * pp + 1][0], ph[2 * pp + 1][1], ph[2 * pp + 1][2], ph[2 * pp + 1][3]};
     }
-    // O += P V; each V fragment feeds both M tiles
+    // O += P V.  B operand via tr16 reads of V rows: source lane s of group g
+    // points at key 32 pp + 16 half + 4 g + (s >> 2), channels 16 c + 4 (s & 3);
+    // lane n then holds stored channel 16 c + n of the four keys.
+    const int vr0 = 4 * g + (n16 >> 2), vcol = 4 * (n16 & 3);
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp)
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(&vt[buf][16 * c + n16][16 * (2 * pp) + 4 * g]);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(&vt[buf][16 * c + n16][16 * (2 * pp + 1) + 4 * g]);
-        const f16x8 bv = __builtin_bit_cast(f16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            reinterpret_cast<lds_i16x4*>((__attribute__((address_space(3))) uint16_t*)&vt[buf][32 * pp + vr0][16 * c + vcol])));
+        const f16x4 hi = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            reinterpret_cast<lds_i16x4*>((__attribute__((address_space(3))) uint16_t*)&vt[buf][32 * pp + 16 + vr0][16 * c + vcol])));
+        const f16x8 bv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[0][pp], bv, acc[0][c], 0, 0, 0);
         acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[1][pp], bv, acc[1][c], 0, 0, 0);
       }
@@ -319,7 +341,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 
   if (!active) return;
-  // ---- normalize and store: accumulator lane (channel n16, g), register i <-> row 4g + i ----
+  // ---- normalize and store: accumulator lane (stored channel n16, g), register i <-> row 4g + i ----
+  const int ch = 8 * (n16 >> 3) + stored_channel(n16 & 7);
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
     float l = l_run[mt];
@@ -333,7 +356,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         uint16_t* orow = p.out + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(j) * p.o_ss;
         const float inv = 1.0f / li;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) orow[16 * c + n16] = f2h(acc[mt][c][i] * inv);
+        for (int c = 0; c < 8; ++c) orow[16 * c + ch] = f2h(acc[mt][c][i] * inv);
       }
     }
   }
