@@ -247,44 +247,51 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int c = 0; c < 8; ++c) acc[mt][c] = f32x4{0, 0, 0, 0};
   float m_run[2] = {kNegBig, kNegBig}, l_run[2] = {0.0f, 0.0f};
   const float sl2 = p.scale_log2;
+  const float tau_raw = kTau / sl2;  // the lazy-rescale margin in raw score units
 
   auto compute = [&](int t, int buf) {
     const TileRef tr = tile_of(t);
-    // S^T for both M tiles; each K fragment feeds both
+    // S^T for both M tiles (raw scores q.k); each K fragment feeds both
     f32x4 s[2][4];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) s[mt][kb] = f32x4{0, 0, 0, 0};
+    const f32x4 zero4 = {0, 0, 0, 0};
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const f16x8 a = *reinterpret_cast<const f16x8*>(&kt[buf][16 * kb + n16][32 * ks + 8 * g]);
-        s[0][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[0][ks], s[0][kb], 0, 0, 0);
-        s[1][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[1][ks], s[1][kb], 0, 0, 0);
+        s[0][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[0][ks], ks ? s[0][kb] : zero4, 0, 0, 0);
+        s[1][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[1][ks], ks ? s[1][kb] : zero4, 0, 0, 0);
       }
+    // every key of a full cache tile is visible to every query of the block
+    const bool full = tr.seg != 3 && tr.cnt == kKT;
     f16x8 pa[2][2];  // PV A operands: [M tile][key-block pair]
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      const int jq = j0 + 16 * mt + n16;  // this lane's query (column n16)
-      // key kk of the tile is visible when kk < cnt and, in the chunk, base + kk <= jq
-      const int lim = tr.seg == 3 ? (jq - tr.base + 1 < tr.cnt ? jq - tr.base + 1 : tr.cnt) : tr.cnt;
       float x[4][4];
+      if (full) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[kb][i] = s[mt][kb][i];
+      } else {
+        const int jq = j0 + 16 * mt + n16;  // this lane's query (column n16)
+        // key kk of the tile is visible when kk < cnt and, in the chunk, base + kk <= jq
+        const int lim = tr.seg == 3 ? (jq - tr.base + 1 < tr.cnt ? jq - tr.base + 1 : tr.cnt) : tr.cnt;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[kb][i] = 16 * kb + 4 * g + i < lim ? s[mt][kb][i] : -INFINITY;
+      }
       float lmax = kNegBig;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kk = 16 * kb + 4 * g + i;
-          x[kb][i] = kk < lim ? s[mt][kb][i] * sl2 : -INFINITY;
-          lmax = fmaxf(lmax, x[kb][i]);
-        }
+        lmax = fmaxf(fmaxf(lmax, fmaxf(x[kb][0], x[kb][1])), fmaxf(x[kb][2], x[kb][3]));
       lmax = fmaxf(lmax, __shfl_xor(lmax, 16, 64));
       lmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
-      if (__builtin_amdgcn_ballot_w64(lmax - m_run[mt] > kTau) != 0) {
+      // running max m_run in raw score units; probabilities exp2((x - m) * scale)
+      if (__builtin_amdgcn_ballot_w64(lmax - m_run[mt] > tau_raw) != 0) {
         const float m_new = fmaxf(m_run[mt], lmax);
-        const float alpha = __builtin_amdgcn_exp2f(m_run[mt] - m_new);
+        const float alpha = __builtin_amdgcn_exp2f((m_run[mt] - m_new) * sl2);
         m_run[mt] = m_new;
         l_run[mt] *= alpha;
         // accumulator row 4g + i lives in lanes whose column n16 is that row
@@ -297,11 +304,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
       float ps = 0.0f;
       _Float16 ph[4][4];
+      const float nm = -m_run[mt] * sl2;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float pv = __builtin_amdgcn_exp2f(x[kb][i] - m_run[mt]);
+          const float pv = __builtin_amdgcn_exp2f(fmaf(x[kb][i], sl2, nm));
           ps += pv;
           ph[kb][i] = static_cast<_Float16>(pv);
         }
