@@ -149,6 +149,9 @@ class TieredKVCache(DynamicCache):
         self._rope_scheme = rope_scheme
         self._skip_layers: set[int] = set()
         self._layers: list[LayerState] = []
+        # fused mode (attn_implementation="fade"): update() appends only and the
+        # layer's attention reads the tiers in place (fade_amd/hf_attention.py)
+        self.fused = False
 
     # transformers 5.x defines a read-only ``Cache.batch_size``; the tiered cache
     # pins the batch size on the first update (fade/cache.py:367-373).
@@ -196,6 +199,11 @@ class TieredKVCache(DynamicCache):
             self.head_dim = int(key_states.shape[-1])
         self._ensure_layer(layer_idx)
         self._append_fp16(key_states, value_states, layer_idx)
+        if self.fused:
+            from .hf_attention import set_active_cache
+
+            set_active_cache(self)
+            return key_states, value_states
         return self._materialize(layer_idx)
 
     def get_seq_length(self, layer_idx: int = 0) -> int:
@@ -614,6 +622,48 @@ class TieredKVCache(DynamicCache):
         st.sink_count = 0 if st.fp16_pos is None else min(self.n_sink, int(st.fp16_pos.shape[0]))
 
     # ----------------------------------------------------- fused attention
+    def attend(self, q: Tensor, layer_idx: int, sm_scale: float | None = None) -> Tensor:
+        """Attention of ``q`` [B, Hq, Sq, D] over this layer's tiers (the ``"fade"``
+        attention implementation): one token per row -> ``decode_attention``; a
+        chunk -> ``prefill_attention``.  Returns fp16 [B, Hq, Sq, D]."""
+        if int(q.shape[2]) == 1:
+            return self.decode_attention(q, layer_idx, sm_scale)
+        return self.prefill_attention(q, layer_idx, sm_scale)
+
+    def _fp16_split(self, st: LayerState):
+        """(sink, rest) fp16 K/V pairs of a layer, whether or not the sink has been split off."""
+        if st.sink_k is not None:
+            return (st.sink_k, st.sink_v), (None if st.fp16_k is None else (st.fp16_k, st.fp16_v))
+        if st.fp16_k is None:
+            return None, None
+        ns = st.sink_count
+        sink = (st.fp16_k[..., :ns, :], st.fp16_v[..., :ns, :]) if ns > 0 else None
+        return sink, (st.fp16_k[..., ns:, :], st.fp16_v[..., ns:, :])
+
+    def prefill_attention(self, q: Tensor, layer_idx: int, sm_scale: float | None = None) -> Tensor:
+        """Causal attention of a chunk ``q`` [B, Hq, Sq, D] whose K/V are the last Sq
+        tokens of this layer's fp16 tier (just appended by ``update``), over
+        ``[sink | INT4 middle | recent | chunk]`` with the ragged prefill kernel."""
+        from .kernels.prefill import tiered_prefill_attention
+        from .kernels.tiered_attn import MiddleTier
+
+        st = self._layers[layer_idx]
+        Sq = int(q.shape[2])
+        sink, rest = self._fp16_split(st)
+        if rest is None or int(rest[0].shape[-2]) < Sq:
+            raise RuntimeError("prefill_attention: the chunk's K/V must be the last Sq tokens of the fp16 tier")
+        if st.int2_kq is not None or st.backend_k is not None or (st.int4_kq is not None and self.middle_v_bits != 4):
+            raise NotImplementedError(
+                "prefill_attention: the fused prefill reads fp16 tiers and the reference INT4 middle tier only"
+            )
+        n_rest = int(rest[0].shape[-2]) - Sq
+        recent = None if n_rest == 0 else (rest[0][..., :n_rest, :], rest[1][..., :n_rest, :])
+        chunk = (rest[0][..., n_rest:, :], rest[1][..., n_rest:, :])
+        mid = None
+        if st.int4_kq is not None:
+            mid = MiddleTier("int4", st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs)
+        return tiered_prefill_attention(q, chunk, sink, mid, recent, sm_scale=sm_scale)
+
     def decode_attention(self, q: Tensor, layer_idx: int, sm_scale: float | None = None) -> Tensor:
         """Single-token attention of ``q`` [B, Hq, 1, D] straight from this layer's tiers.
 

@@ -8,6 +8,7 @@ import torch
 
 from .cache import TieredKVCache
 from .config import FadeConfig
+from .hf_attention import uses_fade_attention
 from .rope import extract_rope_scheme
 
 _RECURRENT_TYPES = {"mamba", "mamba2", "rwkv", "rwkv5", "rwkv6", "xlstm"}
@@ -40,6 +41,8 @@ def create_tiered_cache(model, dtype: torch.dtype = torch.float16, config: FadeC
         kw.update(config.to_cache_kwargs())
     kw.update(kwargs)
     cache = TieredKVCache(dtype=dtype, rope_theta=scheme.theta, head_dim=head_dim, rope_scheme=scheme, **kw)
+    # attn_implementation="fade": attention reads the tiers in place (no materialized K/V)
+    cache.fused = uses_fade_attention(model)
     layer_types = getattr(text_cfg, "layer_types", None)
     if layer_types is not None:
         skip = {i for i, t in enumerate(layer_types) if t not in ("full_attention", "sliding_attention")}

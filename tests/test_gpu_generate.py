@@ -1,0 +1,148 @@
+"""HF generate() on the fused tiered kernels (attn_implementation="fade").
+
+Pins from the reference's own tests, on a tiny random-init Qwen2 (no
+downloads; head_dim 128 as the kernels require, fp16 on the GPU):
+  * greedy generate == a manual greedy loop (tests/test_generate.py:88-117);
+  * with no eviction the first token equals a plain DynamicCache's
+    (tests/test_eval_gate.py:104-138);
+  * batched == unbatched (tests/test_integration.py:87-151).
+Plus: the fused path's logits against the materialized path (the same cache
+class returning dequantized K/V to the model's SDPA), with and without an
+INT4 middle tier, and a check that the kernels actually ran.
+"""
+
+import pytest
+import torch
+
+from fade_amd import create_tiered_cache
+from fade_amd.cache import TIER_FP16, TIER_INT4
+
+pytestmark = pytest.mark.gpu
+
+
+def _tiny_model(dev, impl):
+    from transformers import AutoConfig, AutoModelForCausalLM
+
+    cfg = AutoConfig.for_model(
+        "qwen2", vocab_size=128, hidden_size=512, intermediate_size=256, num_hidden_layers=2,
+        num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=256, rope_theta=10000.0,
+        tie_word_embeddings=True,
+    )
+    torch.manual_seed(0)
+    model = AutoModelForCausalLM.from_config(cfg, attn_implementation="sdpa")
+    model.to(device=dev, dtype=torch.float16).eval()
+    model.set_attn_implementation(impl)
+    return model, cfg
+
+
+def _cache(model, **kw):
+    kw = {"n_sink": 2, "recent_window": 8, "int4_budget": None, "int2_budget": 0, **kw}
+    return create_tiered_cache(model, dtype=torch.float16, **kw)
+
+
+def _steps(model, cache, ids, n, middle_after_prompt=False):
+    """Prompt forward + n greedy decode steps; returns the list of logits."""
+    logits = []
+    with torch.no_grad():
+        out = model(ids, past_key_values=cache, use_cache=True)
+        logits.append(out.logits[:, -1].float())
+        if middle_after_prompt:
+            for li in range(len(cache)):
+                S = cache.get_seq_length(li)
+                tiers = torch.full((S,), TIER_INT4, dtype=torch.long, device=ids.device)
+                tiers[: cache.n_sink] = TIER_FP16
+                tiers[S - 4 :] = TIER_FP16
+                cache.apply_tier_assignment(li, tiers)
+        tok = out.logits[:, -1:].argmax(-1)
+        for _ in range(n):
+            out = model(tok, past_key_values=cache, use_cache=True)
+            logits.append(out.logits[:, -1].float())
+            tok = out.logits[:, -1:].argmax(-1)
+    return logits
+
+
+def test_fused_cache_mode_and_kernels_run(dev, monkeypatch):
+    print("case generate fused mode", flush=True)
+    model, cfg = _tiny_model(dev, "fade")
+    cache = _cache(model)
+    assert cache.fused
+    calls = {"decode": 0, "prefill": 0}
+    import fade_amd.kernels.prefill as kp
+    import fade_amd.kernels.tiered_attn as kt
+
+    real_d, real_p = kt.tiered_decode_attention, kp.tiered_prefill_attention
+
+    def d(*a, **k):
+        calls["decode"] += 1
+        return real_d(*a, **k)
+
+    def p(*a, **k):
+        calls["prefill"] += 1
+        return real_p(*a, **k)
+
+    monkeypatch.setattr(kt, "tiered_decode_attention", d)
+    monkeypatch.setattr(kp, "tiered_prefill_attention", p)
+    ids = torch.randint(0, cfg.vocab_size, (1, 12), device=dev)
+    _steps(model, cache, ids, 2)
+    assert calls["prefill"] == cfg.num_hidden_layers and calls["decode"] == 2 * cfg.num_hidden_layers
+    # nothing was materialized
+    assert all(st.int4_k_deq is None for st in cache._layers)
+
+
+@pytest.mark.parametrize("middle", [False, True])
+def test_fused_logits_match_materialized(dev, middle):
+    print(f"case generate fused vs materialized middle={middle}", flush=True)
+    model, cfg = _tiny_model(dev, "fade")
+    ids = torch.randint(0, cfg.vocab_size, (2, 40), device=dev)
+    fused = _steps(model, _cache(model), ids, 3, middle_after_prompt=middle)
+    model.set_attn_implementation("sdpa")
+    ref_cache = _cache(model)
+    assert not ref_cache.fused
+    ref = _steps(model, ref_cache, ids, 3, middle_after_prompt=middle)
+    for a, b in zip(fused, ref):
+        assert (a - b).abs().max().item() <= 2e-2
+
+
+def test_generate_greedy_matches_manual_loop(dev):
+    print("case generate greedy vs manual", flush=True)
+    model, cfg = _tiny_model(dev, "fade")
+    ids = torch.randint(0, cfg.vocab_size, (1, 8), device=dev)
+    gen = model.generate(ids, past_key_values=_cache(model), max_new_tokens=4, do_sample=False)
+    cache = _cache(model)
+    toks = []
+    with torch.no_grad():
+        out = model(ids, past_key_values=cache, use_cache=True)
+        tok = out.logits[:, -1:].argmax(-1)
+        toks.append(tok)
+        for _ in range(3):
+            out = model(tok, past_key_values=cache, use_cache=True)
+            tok = out.logits[:, -1:].argmax(-1)
+            toks.append(tok)
+    manual = torch.cat([ids, *toks], dim=-1)
+    n = min(gen.shape[1], manual.shape[1])
+    assert torch.equal(gen[:, :n], manual[:, :n])
+
+
+def test_first_token_matches_dynamic_cache(dev):
+    print("case generate first token vs DynamicCache", flush=True)
+    from transformers import DynamicCache
+
+    model, cfg = _tiny_model(dev, "fade")
+    ids = torch.randint(0, cfg.vocab_size, (1, 16), device=dev)
+    with torch.no_grad():
+        a = model(ids, past_key_values=_cache(model), use_cache=True).logits[:, -1].float()
+        model.set_attn_implementation("sdpa")
+        b = model(ids, past_key_values=DynamicCache(), use_cache=True).logits[:, -1].float()
+    assert a.argmax(-1).tolist() == b.argmax(-1).tolist()
+    assert (a - b).abs().max().item() <= 2e-2
+
+
+def test_batched_equals_unbatched(dev):
+    print("case generate batched vs unbatched", flush=True)
+    model, cfg = _tiny_model(dev, "fade")
+    ids = torch.randint(0, cfg.vocab_size, (2, 24), device=dev)
+    both = _steps(model, _cache(model), ids, 2, middle_after_prompt=True)
+    for r in range(2):
+        one = _steps(model, _cache(model), ids[r : r + 1], 2, middle_after_prompt=True)
+        for a, b in zip(both, one):
+            assert (a[r] - b[0]).abs().max().item() <= 2e-3

@@ -122,3 +122,28 @@ def test_kernels_refuse_cpu_tensors():
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         rerope_gather(x, x, torch.arange(2), torch.ones(8, 128), torch.zeros(8, 128), torch.ones(2, 128),
                       torch.zeros(2, 128))
+
+
+def test_fade_attention_registration_and_fused_update():
+    """The "fade" attention/mask implementations are registered, the mask
+    function rejects padding, and a fused cache's update() appends without
+    materializing (host plumbing only; the kernels run in the GPU tests)."""
+    from transformers import AttentionInterface
+    from transformers.masking_utils import AttentionMaskInterface
+
+    from fade_amd import TieredKVCache
+    from fade_amd.hf_attention import active_cache, fade_mask
+
+    assert "fade" in AttentionInterface._global_mapping
+    assert "fade" in AttentionMaskInterface._global_mapping
+    assert fade_mask(2, 1, 9, attention_mask=torch.ones(2, 9, dtype=torch.bool)) is None
+    with pytest.raises(ValueError, match="padded"):
+        fade_mask(2, 1, 9, attention_mask=torch.tensor([[1] * 9, [0] + [1] * 8], dtype=torch.bool))
+    cache = TieredKVCache(n_sink=2, recent_window=4)
+    cache.fused = True
+    k = torch.randn(1, 2, 5, 128).half()
+    v = torch.randn(1, 2, 5, 128).half()
+    rk, rv = cache.update(k, v, 0)
+    assert rk is k and rv is v
+    assert cache.get_seq_length(0) == 5
+    assert active_cache() is cache
