@@ -58,6 +58,7 @@
 #include <math.h>
 
 #include "decode_common.h"
+#include "lds_dma.h"
 
 namespace fade {
 namespace decode {
@@ -96,33 +97,6 @@ constexpr int kQdZero = 8 * 2 * 4 * 16;  // zero operand after the [ks][digit][h
 constexpr float kQMax = 32000.0f;
 constexpr float kNegBig = -1.0e30f;      // running-max sentinel (finite: no inf - inf)
 constexpr float kTau = 8.0f;             // the running max moves only when a score exceeds it by kTau (log2)
-
-// s_waitcnt immediate: at most n vector-memory ops outstanding (expcnt, lgkmcnt untouched).
-constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-constexpr int kLgkm0 = 15 | (3 << 14) | (7 << 4);  // lgkmcnt(0) only
-
-__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
-}
-__device__ __forceinline__ void lds_dma2(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_ushort %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
-}
-__device__ __forceinline__ void lds_dma4(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
-}
-// Same with a wave-uniform base address and a 32-bit per-lane byte offset.
-__device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void lds_dma2(const void* sbase, uint32_t voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_ushort %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void lds_dma4(const void* sbase, uint32_t voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
-               : "memory", "m0");
-}
 
 __device__ __forceinline__ uint32_t pack_f16(float a, float b) {
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
