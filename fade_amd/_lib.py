@@ -131,6 +131,8 @@ _SIGNATURES: dict[str, list] = {
     "fade_dequant_int2_grouped": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
     "fade_quant_rotated_workspace_bytes": [_i64, _i64, _i64, _i64, _i32, _pi64],
     "fade_quant_rotated": [_p, _i64, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _i64, _p],
+    "fade_rotate_quant_workspace_bytes": [_i64, _i64, _i64, _i64, _i32, _pi64],
+    "fade_rotate_quant": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i32, _i32, _p, _p, _p, _i64, _p],
     "fade_quant_asym": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p],
     "fade_dequant_asym": [_p, _p, _p, _i32, _i32, _i64, _i64, _i64, _i64, _p, _p],
     "fade_rerope_gather": [

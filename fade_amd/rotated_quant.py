@@ -1,13 +1,19 @@
 """Rotation-then-quantize for K/V (fade/rotated_quant.py), on MI355X kernels.
 
-``x_rot = x.float() @ R.T`` is a plain fp32 GEMM (rocBLAS through torch);
-the quantizer that follows (fp32 absmax, ``inv = reciprocal(absmax) * qmax``,
-round-half-even, clamp, bit-pack) runs in ``fade_quant_rotated`` and is
-bit-exact given ``x_rot``.  Dequantize is ``fp16(code * scale)`` in
-``fade_dequant_sym`` followed by the fp32 ``@ R`` GEMM.
+fp16 K/V with head_dim 128 go through ``fade_rotate_quant``: one fused kernel
+(two for per-channel K) computes ``x_rot = x @ R.T`` on the matrix cores with
+R split into fp16 hi/lo parts (fp32-GEMM accuracy) and quantizes it in place
+(fp32 absmax, ``inv = reciprocal(absmax) * qmax``, round-half-even, clamp,
+bit-pack); x_rot never reaches HBM.  Other shapes and dtypes take the two-step
+path: an fp32 GEMM through torch, then ``fade_quant_rotated``, which is
+bit-exact given ``x_rot`` (``quant_rotated_given``).  Dequantize is
+``fp16(code * scale)`` in ``fade_dequant_sym`` followed by the fp32 ``@ R``
+GEMM.
 """
 
 from __future__ import annotations
+
+import ctypes
 
 import torch
 from torch import Tensor
@@ -43,29 +49,78 @@ def _rotate(x: Tensor, R: Tensor) -> Tensor:
     return (x.float() @ R.to(x.device, dtype=torch.float32).T).contiguous()
 
 
-def _quant_rotated(x: Tensor, R: Tensor, bits: int, axis: int, op: str):
+def _alloc_out(shape, bits: int, axis: int, device):
+    B, H, S, D = shape
+    row = D if bits == 3 else D * bits // 8
+    packed = torch.empty(B, H, S, row, dtype=torch.int8 if bits == 3 else torch.uint8, device=device)
+    scale_shape = (B, H, 1, D) if axis == _lib.AXIS_CHANNEL else (B, H, S, 1)
+    scale = torch.empty(scale_shape, dtype=torch.float16, device=device)
+    return packed, scale
+
+
+def _check(x: Tensor, bits: int, op: str) -> None:
     if bits not in _BIT_PARAMS:
         raise ValueError(f"bits must be 2, 3 or 4, got {bits}")
     if x.dim() != 4:
         raise ValueError(f"{op}: expected [B, H, S, D], got shape {tuple(x.shape)}")
     _lib.require_gpu(x, op=op)
-    B, H, S, D = x.shape
-    x_rot = _rotate(x, R)
-    row = D if bits == 3 else D * bits // 8
-    packed = torch.empty(B, H, S, row, dtype=torch.int8 if bits == 3 else torch.uint8, device=x.device)
-    scale_shape = (B, H, 1, D) if axis == _lib.AXIS_CHANNEL else (B, H, S, 1)
-    scale = torch.empty(scale_shape, dtype=torch.float16, device=x.device)
-    if x.numel() == 0:
-        return packed, scale.to(x.dtype)
-    import ctypes
 
+
+def quant_rotated_given(x_rot: Tensor, bits: int, axis: int, op: str = "quant_rotated_given"):
+    """Quantize an already-rotated fp32 tensor [B, H, S, D] (fade/rotated_quant.py:121-131 with
+    ``axis=AXIS_CHANNEL``, 163-173 with ``AXIS_TOKEN``); bit-exact with the reference given x_rot.
+    Returns (packed, fp16 scale)."""
+    _check(x_rot, bits, op)
+    x_rot = x_rot.float().contiguous()
+    B, H, S, D = x_rot.shape
+    packed, scale = _alloc_out(x_rot.shape, bits, axis, x_rot.device)
+    if x_rot.numel() == 0:
+        return packed, scale
     nb = ctypes.c_int64(0)
     _lib.check(_lib.load().fade_quant_rotated_workspace_bytes(B, H, S, D, axis, nb), op)
-    ws = _lib.workspace(nb.value, x.device)
+    ws = _lib.workspace(nb.value, x_rot.device)
     _lib.call(
         "fade_quant_rotated", x_rot.data_ptr(), B, H, S, D, bits, axis, packed.data_ptr(),
-        scale.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(x),
+        scale.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(x_rot),
     )
+    return packed, scale
+
+
+def _fused_ok(x: Tensor) -> bool:
+    return (
+        x.dtype == torch.float16
+        and x.shape[-1] == 128
+        and x.stride(-1) == 1
+        and all(st % 8 == 0 for st in x.stride()[:3])
+        and x.data_ptr() % 16 == 0
+    )
+
+
+def _rotate_quant_fused(x: Tensor, R: Tensor, bits: int, axis: int, op: str):
+    B, H, S, D = x.shape
+    packed, scale = _alloc_out(x.shape, bits, axis, x.device)
+    if x.numel() == 0:
+        return packed, scale
+    Rd = R.to(x.device, dtype=torch.float32).contiguous()
+    nb = ctypes.c_int64(0)
+    _lib.check(_lib.load().fade_rotate_quant_workspace_bytes(B, H, S, D, axis, nb), op)
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=x.device) if nb.value else None
+    sb, sh, ss, _ = x.stride()
+    _lib.call(
+        "fade_rotate_quant", x.data_ptr(), B, H, S, D, sb, sh, ss, Rd.data_ptr(), bits, axis,
+        packed.data_ptr(), scale.data_ptr(), _lib.ptr(ws), nb.value, _lib.stream_of(x),
+    )
+    return packed, scale
+
+
+def _quant_rotated(x: Tensor, R: Tensor, bits: int, axis: int, op: str):
+    _check(x, bits, op)
+    if tuple(R.shape) != (x.shape[-1], x.shape[-1]):
+        raise ValueError(f"{op}: R must be [{x.shape[-1]}, {x.shape[-1]}], got {tuple(R.shape)}")
+    if _fused_ok(x):
+        packed, scale = _rotate_quant_fused(x, R, bits, axis, op)
+    else:
+        packed, scale = quant_rotated_given(_rotate(x, R), bits, axis, op)
     return packed, scale.to(x.dtype)
 
 
@@ -100,6 +155,7 @@ def rotated_dequant_v(packed, scale, R, bits: int = 4, dtype=torch.float16) -> T
 
 
 __all__ = [
+    "quant_rotated_given",
     "rotated_dequant_k",
     "rotated_dequant_v",
     "rotated_quant_k",

@@ -99,6 +99,20 @@ int fade_quant_rotated(const float* x_rot, int64_t B, int64_t H, int64_t S, int6
                        int32_t bits, int32_t axis, void* packed, void* scale_f16, void* workspace,
                        int64_t workspace_bytes, void* stream);
 
+/* Fused rotate + quantize (fade/rotated_quant.py:106-131 K, 148-173 V) for
+ * fp16 x [B,H,S,128] (element strides sb/sh/ss, rows 16-byte aligned) and
+ * R fp32 [128,128] row-major on the device: x_rot = x @ R^T on f16 matrix
+ * cores with R split hi/lo (fp32-GEMM accuracy), then the same quantizer and
+ * layouts as fade_quant_rotated.  Codes can differ from an fp32 GEMM's only
+ * where x_rot * inv lies within GEMM rounding of a half-integer.
+ * Workspace: axis CHANNEL only, size from the _workspace_bytes query. */
+int fade_rotate_quant_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D, int32_t axis,
+                                      int64_t* bytes);
+int fade_rotate_quant(const void* x_f16, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                      int64_t sh, int64_t ss, const float* R, int32_t bits, int32_t axis,
+                      void* packed, void* scale_f16, void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
 /* ---------------- asymmetric per-token groups (build format, no reference
  * counterpart: BASELINE's "asymmetric group-32 scale/zero") ------------- */
 int fade_quant_asym(const void* x_f16, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,

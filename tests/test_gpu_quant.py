@@ -4,6 +4,7 @@ import numpy as np
 import pytest
 import torch
 
+from fade_amd import _lib
 from fade_amd import quant as fq
 from fade_amd import rotated_quant as frq
 from fade_amd.synthetic import kv_tensors
@@ -129,8 +130,8 @@ def test_rotated_quant_bit_exact_given_rotation(dev, bits):
     xr = x_rot.cpu().numpy()
     ref_rot = x.cpu().float().numpy() @ R.numpy().T
     assert np.abs(xr - ref_rot).max() < 1e-4
-    kp, ks = frq.rotated_quant_k(x, R.to(dev), bits)
-    vp, vs = frq.rotated_quant_v(x, R.to(dev), bits)
+    kp, ks = frq.quant_rotated_given(x_rot, bits, _lib.AXIS_CHANNEL)
+    vp, vs = frq.quant_rotated_given(x_rot, bits, _lib.AXIS_TOKEN)
     okp, oks = oq.rotated_quant_codes(xr, bits, "channel")
     ovp, ovs = oq.rotated_quant_codes(xr, bits, "token")
     assert np.array_equal(kp.cpu().numpy().view(np.uint8), okp.view(np.uint8))
@@ -139,6 +140,86 @@ def test_rotated_quant_bit_exact_given_rotation(dev, bits):
     assert np.array_equal(_u16(vs.cpu().numpy()), _u16(ovs))
     deq = frq.rotated_dequant_rot(kp, ks, bits).cpu().numpy()
     assert np.array_equal(_u16(deq), _u16(oq.rotated_dequant_rot(okp, oks, bits)))
+
+
+def _check_fused_rotated(x16, R, bits, axis, packed, scale):
+    """Fused rotate+quant against the oracle's quantizer on an fp64 rotation.
+
+    The kernel's x_rot is an fp32-accurate GEMM (x exact, R split into fp16 hi/lo),
+    so it differs from the fp64 product by ~1e-6 relative.  The fp16 scales must agree
+    to one fp16 ulp (exactly, except where absmax / qmax rounds at a tie), and a code
+    may differ only by one, and only where the fp64 value of x_rot * inv lies within
+    1e-3 of a rounding boundary (a wrong channel, row or scale moves codes by whole
+    units far from any boundary)."""
+    xr64 = x16.astype(np.float64) @ R.astype(np.float64).T
+    ocodes_p, oscale = oq.rotated_quant_codes(xr64.astype(np.float32), bits, axis)
+    s_got = scale.astype(np.float32)
+    s_ref = oscale.astype(np.float32)
+    assert s_got.shape == s_ref.shape
+    ulp = np.abs(np.spacing(oscale)).astype(np.float32)
+    assert np.all(np.abs(s_got - s_ref) <= ulp), "scale off by more than one fp16 ulp"
+    qmax = {4: 7, 3: 3, 2: 1}[bits]
+    red = -2 if axis == "channel" else -1
+    absmax = np.maximum(np.abs(xr64.astype(np.float32)).max(axis=red, keepdims=True), np.float32(1e-8))
+    # a differing scale: absmax / qmax (fp64) sits at the fp16 rounding midpoint of the two
+    s64 = np.maximum(np.abs(xr64).max(axis=red, keepdims=True), 1e-8) / qmax
+    mid = (s_got.astype(np.float64) + s_ref.astype(np.float64)) / 2
+    sbad = s_got != s_ref
+    assert np.all(np.abs(s64 - mid)[sbad] <= 1e-5 * s64[sbad]), "scale differs away from an fp16 tie"
+    got = oq.unpack_bits(packed, bits).astype(np.int32)
+    ref = oq.unpack_bits(ocodes_p, bits).astype(np.int32)
+    t = xr64 * (np.float64(qmax) / absmax.astype(np.float64))
+    near = np.abs(np.abs(t - np.floor(t)) - 0.5) < 1e-3
+    bad = got != ref
+    assert np.all(np.abs(got - ref)[bad] == 1)
+    assert np.all(near[bad]), f"{int((bad & ~near).sum())} codes differ away from a rounding boundary"
+    assert bad.mean() < 1e-3
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("shape", [(2, 3, 70, 128), (1, 8, 2000, 128), (1, 1, 5, 128)])
+def test_rotate_quant_fused(dev, bits, shape):
+    """fade_rotate_quant (fused MFMA rotation + quantize), K per-channel and V per-token,
+    on a contiguous tensor and on the strided middle slice the cache quantizes."""
+    print(f"case rotate_quant_fused bits={bits} shape={shape}", flush=True)
+    R = np.load(__file__.rsplit("/", 1)[0] + "/golden/rotation_d128_seed42.npy")
+    Rd = torch.from_numpy(R).to(dev)
+    x16 = _edge_tensor(shape, 7)
+    xt = torch.from_numpy(x16).to(dev)
+    assert frq._fused_ok(xt)
+    kp, ks = frq.rotated_quant_k(xt, Rd, bits)
+    vp, vs = frq.rotated_quant_v(xt, Rd, bits)
+    _check_fused_rotated(x16, R, bits, "channel", kp.cpu().numpy(), ks.cpu().numpy())
+    _check_fused_rotated(x16, R, bits, "token", vp.cpu().numpy(), vs.cpu().numpy())
+    # strided view: rows 3 .. S-2 of a bigger tensor (the cache's middle tier)
+    S = shape[2]
+    if S > 8:
+        big = torch.from_numpy(_edge_tensor((shape[0], shape[1], S + 5, 128), 8)).to(dev)
+        view = big[:, :, 3 : S - 2]
+        assert not view.is_contiguous() and frq._fused_ok(view)
+        xv = view.cpu().numpy()
+        kp, ks = frq.rotated_quant_k(view, Rd, bits)
+        vp, vs = frq.rotated_quant_v(view, Rd, bits)
+        _check_fused_rotated(xv, R, bits, "channel", kp.cpu().numpy(), ks.cpu().numpy())
+        _check_fused_rotated(xv, R, bits, "token", vp.cpu().numpy(), vs.cpu().numpy())
+
+
+def test_rotate_quant_fused_rejects(dev):
+    """Argument checks of the C-ABI entry (no launch)."""
+    import ctypes
+
+    lib = _lib.load()
+    nb = ctypes.c_int64(0)
+    assert lib.fade_rotate_quant_workspace_bytes(1, 1, 10, 64, _lib.AXIS_TOKEN, nb) != 0
+    assert lib.fade_rotate_quant_workspace_bytes(1, 1, 10, 128, 7, nb) != 0
+    assert lib.fade_rotate_quant_workspace_bytes(1, 2, 1000, 128, _lib.AXIS_CHANNEL, nb) == 0 and nb.value > 0
+    x = torch.zeros(1, 2, 1000, 128, dtype=torch.float16, device=dev)
+    R = torch.eye(128, device=dev)
+    pk = torch.empty(1, 2, 1000, 64, dtype=torch.uint8, device=dev)
+    sc = torch.empty(1, 2, 1, 128, dtype=torch.float16, device=dev)
+    rc = lib.fade_rotate_quant(x.data_ptr(), 1, 2, 1000, 128, 2000 * 128, 1000 * 128, 128, R.data_ptr(), 4,
+                               _lib.AXIS_CHANNEL, pk.data_ptr(), sc.data_ptr(), None, 0, None)
+    assert rc != 0 and "workspace" in lib.fade_hip_last_error().decode()
 
 
 @pytest.mark.parametrize("bits", [4, 2])
