@@ -137,9 +137,10 @@ class CallPlan:
 
 
 def quant_cases(dev):
-    """Middle-tier quantizers at full size: config 1 (reference INT4 K and V) and
-    config 2 (asymmetric group-32 K4 / V2).  Bytes: fp16 read once + codes and
-    scales written (a two-phase kernel's re-read of K is not counted)."""
+    """Middle-tier quantizers at full size: config 1 (reference INT4 K and V),
+    config 2 (asymmetric group-32 K4 / V2) and config 2's rotated 2-bit K / V
+    (fused rotation + quantize).  Bytes: fp16 read once + codes and scales
+    written (a two-phase kernel's re-read of K is not counted)."""
     out = []
     c1 = CONFIGS[1]
     _, k, v = kv_tensors(c1.B, c1.Hkv, c1.S, c1.D, seed=1001, Hq=c1.Hq)
@@ -153,13 +154,14 @@ def quant_cases(dev):
     _lib.check(_lib.load().fade_quant_k_int4_workspace_bytes(B, H, S, D, nb), "ws")
     ws = _lib.workspace(nb.value, dev)
     st = (km.stride(0), km.stride(1), km.stride(2))
-    out.append(("c1_quant_k_int4", CallPlan("fade_quant_k_int4", lambda s_: (
-        km.data_ptr(), B, H, S, D, *st, kp.data_ptr(), ks.data_ptr(), ws.data_ptr(), ws.numel(), s_),
+    # every lambda binds its arguments as defaults: later cases rebind these names
+    out.append(("c1_quant_k_int4", CallPlan("fade_quant_k_int4", lambda s_, km=km, kp=kp, ks=ks, ws=ws, st=st, sh=(B, H, S, D): (
+        km.data_ptr(), *sh, *st, kp.data_ptr(), ks.data_ptr(), ws.data_ptr(), ws.numel(), s_),
         (km, kp, ks, ws)), km.numel() * 2 + kp.numel() + ks.numel() * 2))
     vp = torch.empty(B, H, S, D // 2, dtype=torch.uint8, device=dev)
     vs = torch.empty(B, H, S, 1, dtype=torch.float16, device=dev)
-    out.append(("c1_quant_v_int4", CallPlan("fade_quant_v_int4", lambda s_: (
-        vm.data_ptr(), B, H, S, D, *st, vp.data_ptr(), vs.data_ptr(), s_), (vm, vp, vs)),
+    out.append(("c1_quant_v_int4", CallPlan("fade_quant_v_int4", lambda s_, vm=vm, vp=vp, vs=vs, st=st, sh=(B, H, S, D): (
+        vm.data_ptr(), *sh, *st, vp.data_ptr(), vs.data_ptr(), s_), (vm, vp, vs)),
         vm.numel() * 2 + vp.numel() + vs.numel() * 2))
     c2 = CONFIGS[2]
     _, k2, v2 = kv_tensors(c2.B, c2.Hkv, c2.S, c2.D, seed=1002, Hq=c2.Hq)
@@ -173,6 +175,21 @@ def quant_cases(dev):
         out.append((name, CallPlan("fade_quant_asym", lambda s_, xm=xm, pk=pk, sc=sc, zp=zp, xs=xs, bits=bits, sh=(B, H, S, D): (
             xm.data_ptr(), *sh, *xs, bits, 32, pk.data_ptr(), sc.data_ptr(), zp.data_ptr(), s_), (xm, pk, sc, zp)),
             xm.numel() * 2 + pk.numel() + 2 * sc.numel() * 2))
+    # rotated backend at config 2's 2-bit middle tier: fused MFMA rotation + quantize
+    R = torch.from_numpy(np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden",
+                                              "rotation_d128_seed42.npy"))).to(dev)
+    for name, x, axis in (("c2_rotate_quant_k2", k2, _lib.AXIS_CHANNEL), ("c2_rotate_quant_v2", v2, _lib.AXIS_TOKEN)):
+        xm = x[:, :, c2.n_sink : c2.S - c2.recent].contiguous().to(dev)
+        B, H, S, D = xm.shape
+        pk = torch.empty(B, H, S, D // 4, dtype=torch.uint8, device=dev)
+        sc = torch.empty(B * H * (S if axis == _lib.AXIS_TOKEN else D), dtype=torch.float16, device=dev)
+        nb = ctypes.c_int64(0)
+        _lib.check(_lib.load().fade_rotate_quant_workspace_bytes(B, H, S, D, axis, nb), "ws")
+        ws = _lib.workspace(nb.value, dev)
+        xs = (xm.stride(0), xm.stride(1), xm.stride(2))
+        out.append((name, CallPlan("fade_rotate_quant", lambda s_, xm=xm, pk=pk, sc=sc, ws=ws, xs=xs, axis=axis, sh=(B, H, S, D), R=R: (
+            xm.data_ptr(), *sh, *xs, R.data_ptr(), 2, axis, pk.data_ptr(), sc.data_ptr(), ws.data_ptr(), ws.numel(), s_),
+            (xm, pk, sc, ws, R)), xm.numel() * 2 + pk.numel() + sc.numel() * 2))
     return out
 
 
