@@ -15,6 +15,7 @@ What changes is where the work runs:
 
 from __future__ import annotations
 
+import ctypes
 import json
 from dataclasses import dataclass
 from pathlib import Path
@@ -152,6 +153,11 @@ class TieredKVCache(DynamicCache):
         # fused mode (attn_implementation="fade"): update() appends only and the
         # layer's attention reads the tiers in place (fade_amd/hf_attention.py)
         self.fused = False
+        # apply_tier_assignment on the device for the reference INT4 layout
+        self.device_reassign = True
+        self._rope_tab_key = None
+        self._rope_tab = None
+        self._last_reassign_counts = None
 
     # transformers 5.x defines a read-only ``Cache.batch_size``; the tiered cache
     # pins the batch size on the first update (fade/cache.py:367-373).
@@ -490,15 +496,197 @@ class TieredKVCache(DynamicCache):
             st._fp16_buf_k = st._fp16_buf_v = st._fp16_buf_pos = None
             st._fp16_len = 0
 
-    def apply_tier_assignment(self, layer_idx: int, tiers: Tensor, scores: Tensor | None = None) -> None:
+    def _rope_tables(self, rows: int, device) -> tuple[Tensor, Tensor]:
+        """cos/sin fp32 ``[rows, D]`` for positions ``0..rows-1`` on ``device`` (the last
+        table is kept: every layer of one reassignment round uses the same one)."""
+        key = (rows, str(device))
+        if self._rope_tab_key != key:
+            cos, sin = self._ensure_rope_scheme().host_cos_sin(torch.arange(rows, dtype=torch.long), self.dtype)
+            # pinned + non_blocking: an upload that does not wait for the device
+            self._rope_tab = tuple(t.contiguous().pin_memory().to(device, non_blocking=True) for t in (cos, sin))
+            self._rope_tab_key = key
+        return self._rope_tab
+
+    def _device_reassign_ok(self, st: LayerState) -> bool:
+        k = st.sink_k if st.sink_k is not None else st.fp16_k
+        if k is None and st.int4_kq is None:
+            return False
+        dev = (k if k is not None else st.int4_kq).device
+        return (
+            self.device_reassign
+            and dev.type == "cuda"
+            and isinstance(self._quant_backend, SymmetricINT4Backend)
+            and self.middle_k_bits == 4
+            and self.middle_v_bits == 4
+            and st.int2_kq is None
+            and st.backend_k is None
+        )
+
+    @staticmethod
+    def _host_tier_counts(tiers: Tensor) -> tuple[int, int, int] | None:
+        """(n_fp16, n_int4, n_int2) of a host tiers tensor, or None if it holds other values."""
+        t = tiers.to(torch.long)
+        n = [int((t == c).sum()) for c in (TIER_FP16, TIER_INT4, TIER_INT2, TIER_EVICT)]
+        if sum(n) != int(t.numel()):
+            return None
+        return n[0], n[1], n[2]
+
+    def _apply_tier_assignment_device(self, layer_idx: int, tiers: Tensor, counts) -> bool:
+        """``apply_tier_assignment`` on the device for the reference INT4 layout.
+
+        ``fade_reassign_plan`` ranks every token of the position-ordered layer,
+        ``fade_reassign_gather`` moves the kept ones (dequantizing middle rows and
+        re-RoPE-ing K in registers) straight into the new sink, recent buffer and
+        an fp16 middle staging tensor, which the INT4 quantizers encode.  No
+        host sync when the tier counts are known on the host (a host ``tiers``
+        tensor, or ``counts``); otherwise one 16-byte read of the device counts.
+        Returns False (nothing changed) when the assignment holds INT2 tokens.
+        """
+        st = self._layers[layer_idx]
+        if st.sink_k is not None:
+            sink = (st.sink_k, st.sink_v)
+            rec_start = 0
+        else:
+            nsk = st.sink_count if st.fp16_k is not None else 0
+            sink = (st.fp16_k[..., :nsk, :], st.fp16_v[..., :nsk, :]) if nsk > 0 else None
+            rec_start = nsk
+        rec = None
+        if st.fp16_k is not None and rec_start < int(st.fp16_k.shape[-2]):
+            rec = (st.fp16_k[..., rec_start:, :], st.fp16_v[..., rec_start:, :])
+        ref = sink[0] if sink is not None else (rec[0] if rec is not None else None)
+        if ref is None:
+            B, H, _, half = st.int4_kq.shape
+            D = 2 * half
+        else:
+            B, H, _, D = ref.shape
+        dev = st.int4_kq.device if ref is None else ref.device
+        ns_old = 0 if sink is None else int(sink[0].shape[-2])
+        nm_old = 0 if st.int4_kq is None else int(st.int4_kq.shape[-2])
+        nr_old = 0 if rec is None else int(rec[0].shape[-2])
+        S = ns_old + nm_old + nr_old
+        if int(tiers.shape[0]) != S:
+            raise ValueError(f"tiers length {int(tiers.shape[0])} != cache length {S} for layer {layer_idx}")
+        if counts is None and tiers.device.type == "cpu":
+            counts = self._host_tier_counts(tiers)
+            if counts is None:
+                return False
+        if counts is not None and counts[2] > 0:
+            return False
+        pos_parts = [p for p in (
+            None if sink is None else (st.sink_pos if st.sink_k is not None else st.fp16_pos[:ns_old]),
+            st.int4_pos,
+            None if rec is None else st.fp16_pos[rec_start:],
+        ) if p is not None]
+        pos_old = torch.cat(pos_parts).to(device=dev, dtype=torch.long).contiguous()
+        tiers_d = tiers.to(dtype=torch.long).contiguous()
+        if tiers_d.device != dev:
+            tiers_d = (tiers_d.pin_memory() if tiers_d.device.type == "cpu" else tiers_d).to(dev, non_blocking=True)
+        dst = torch.empty(S, dtype=torch.int32, device=dev)
+        newpos = torch.empty(S, dtype=torch.int32, device=dev)
+        pos_new = torch.empty(3, max(S, 1), dtype=torch.long, device=dev)
+        cnt = torch.empty(4, dtype=torch.int32, device=dev)
+        stream = _lib.stream_of(tiers_d)
+        _lib.call("fade_reassign_plan", tiers_d.data_ptr(), S, self.n_sink, pos_old.data_ptr(), dst.data_ptr(),
+                  newpos.data_ptr(), pos_new[0].data_ptr(), pos_new[1].data_ptr(), pos_new[2].data_ptr(),
+                  cnt.data_ptr(), stream)
+        if counts is None:
+            c = cnt.cpu().tolist()  # the one host sync: tiers were on the device
+            if c[3] != 0:
+                return False
+            n_fp16, n_int4 = c[0], c[1]
+        else:
+            n_fp16, n_int4 = int(counts[0]), int(counts[1])
+        n_kept = n_fp16 + n_int4
+        n_sink_new = min(self.n_sink, n_fp16)
+        n_rec_new = n_fp16 - n_sink_new
+        kd = dict(dtype=torch.float16, device=dev)
+        out_sink = (torch.empty(B, H, n_sink_new, D, **kd), torch.empty(B, H, n_sink_new, D, **kd)) if n_sink_new else None
+        old_cap = 0 if st._fp16_buf_k is None else int(st._fp16_buf_k.shape[-2])
+        cap = max(DEFAULT_FP16_PREALLOC, n_rec_new, old_cap)
+        buf = (torch.empty(B, H, cap, D, **kd), torch.empty(B, H, cap, D, **kd)) if n_rec_new else None
+        mid = (torch.empty(B, H, n_int4, D, **kd), torch.empty(B, H, n_int4, D, **kd)) if n_int4 else None
+        tab = self._rope_tables(st.next_position, dev) if n_kept < S else None
+
+        def cf(t):  # K and V of a tier share strides in the kernel
+            return t if t[0].stride() == t[1].stride() else (t[0].contiguous(), t[1].contiguous())
+
+        sink = None if sink is None else cf(sink)
+        rec = None if rec is None else cf(rec)
+        a = _lib.ReassignArgs()
+        a.B, a.H, a.D, a.S = B, H, D, S
+        a.n_sink_old, a.n_mid_old = ns_old, nm_old
+        if sink is not None:
+            a.sink_k, a.sink_v = sink[0].data_ptr(), sink[1].data_ptr()
+            a.sink_sb, a.sink_sh, a.sink_ss = sink[0].stride()[:3]
+        if nm_old:
+            mids = [t.contiguous() for t in (st.int4_kq, st.int4_ks, st.int4_vq, st.int4_vs)]
+            a.mid_kq, a.mid_ks, a.mid_vq, a.mid_vs = (t.data_ptr() for t in mids)
+        if rec is not None:
+            a.rec_k, a.rec_v = rec[0].data_ptr(), rec[1].data_ptr()
+            a.rec_sb, a.rec_sh, a.rec_ss = rec[0].stride()[:3]
+        a.dst, a.newpos, a.counts, a.pos_old = dst.data_ptr(), newpos.data_ptr(), cnt.data_ptr(), pos_old.data_ptr()
+        if tab is not None:
+            a.cos_tab, a.sin_tab, a.table_rows = tab[0].data_ptr(), tab[1].data_ptr(), int(tab[0].shape[0])
+        if out_sink is not None:
+            a.out_sink_k, a.out_sink_v, a.cap_sink = out_sink[0].data_ptr(), out_sink[1].data_ptr(), n_sink_new
+        if buf is not None:
+            a.out_rec_k, a.out_rec_v = buf[0].data_ptr(), buf[1].data_ptr()
+            a.out_rec_sb, a.out_rec_sh, a.out_rec_ss = buf[0].stride()[:3]
+            a.cap_rec = n_rec_new
+        if mid is not None:
+            a.out_mid_k, a.out_mid_v, a.cap_mid = mid[0].data_ptr(), mid[1].data_ptr(), n_int4
+        _lib.check(_lib.load().fade_reassign_gather(ctypes.byref(a), stream), "fade_reassign_gather")
+
+        # new state (the same fields as the host path)
+        if out_sink is not None:
+            st.sink_k, st.sink_v, st.sink_pos = out_sink[0], out_sink[1], pos_new[0, :n_sink_new]
+        else:
+            st.sink_k = st.sink_v = st.sink_pos = None
+        if buf is not None:
+            bp = torch.empty(cap, dtype=torch.long, device=dev)
+            bp[:n_rec_new] = pos_new[1, :n_rec_new]
+            st._fp16_buf_k, st._fp16_buf_v, st._fp16_buf_pos = buf[0], buf[1], bp
+            st._fp16_len = n_rec_new
+            st.fp16_k, st.fp16_v, st.fp16_pos = buf[0][:, :, :n_rec_new], buf[1][:, :, :n_rec_new], bp[:n_rec_new]
+        else:
+            st.fp16_k = st.fp16_v = st.fp16_pos = None
+            st._fp16_buf_k = st._fp16_buf_v = st._fp16_buf_pos = None
+            st._fp16_len = 0
+        if mid is not None:
+            st.int4_kq, st.int4_ks = quant_k_int4(mid[0])
+            st.int4_vq, st.int4_vs = quant_v_int4(mid[1])
+            st.int4_pos = pos_new[2, :n_int4]
+        else:
+            st.int4_kq = st.int4_vq = st.int4_ks = st.int4_vs = st.int4_pos = None
+        st.backend_k = st.backend_v = st.backend_pos = None
+        st.int2_kq = st.int2_vq = st.int2_ks = st.int2_vs = st.int2_pos = None
+        st.int2_actual_count = 0
+        if n_kept < S:
+            st.next_position = n_kept
+        st.int4_k_deq = st.int4_v_deq = st.int2_k_deq = st.int2_v_deq = None
+        st._compressed_bytes = self._layer_compressed_bytes(st)
+        st.sink_count = n_sink_new
+        self._last_reassign_counts = cnt
+        return True
+
+    def apply_tier_assignment(
+        self, layer_idx: int, tiers: Tensor, scores: Tensor | None = None, *, counts=None
+    ) -> None:
         """Move tokens between tiers (fade/cache.py:881-1057).
 
         Evicted tokens are dropped; the survivors are re-RoPE'd from their
         old absolute positions to contiguous positions ``0..n_kept-1`` in
         one fused pass, then split into fp16 / INT4 / INT2 and requantized.
+
+        Layers holding the reference INT4 layout on the GPU take the device
+        path (``_apply_tier_assignment_device``, same results); ``counts`` =
+        ``(n_fp16, n_int4, n_int2)`` of ``tiers``, when the caller knows them,
+        spares the host sync a device ``tiers`` tensor would otherwise need.
         """
         del scores
         st = self._layers[layer_idx]
+        if self._device_reassign_ok(st) and self._apply_tier_assignment_device(layer_idx, tiers, counts):
+            return
         k_full, v_full, pos_full = self._all_in_position_order(layer_idx)
         S = int(pos_full.shape[0])
         if int(tiers.shape[0]) != S:

@@ -1,0 +1,266 @@
+// Device-side tier reassignment (fade/cache.py:881-1057, shared tiers, the
+// reference INT4 middle format).
+//
+// The reference materializes the whole layer in position order (dequantized
+// middle included), reads the number of kept tokens back to the host, un-RoPEs
+// every row, index_selects the kept rows, re-RoPEs them, then splits the
+// survivors with three more nonzero() calls (each a host sync) and
+// requantizes the middle tier.  Here:
+//
+//   plan    one workgroup scans tiers[S] (two passes over per-thread runs and
+//           one block scan) and writes, per source token j, its destination
+//           (sink / recent / middle slot) and its rank among the kept
+//           tokens, the new position arrays and the tier counts;
+//   gather  one thread per (row, channel pair i, i + D/2) reads the source
+//           row in place -- sink or recent fp16, or a middle row dequantized
+//           in registers as fp16(fp16(code) * fp16(scale)) -- un-RoPEs /
+//           re-RoPEs K with the reference's rounding when tokens were
+//           evicted (three separately rounded fp32 ops per rotation, fp16 in
+//           between; -ffp-contract=off) and stores K and V straight into the
+//           new tiers (the middle into an fp16 staging tensor that the
+//           quantizers then encode).
+//
+// Destination writes are bounded by the capacities the host allocated; a
+// slot beyond them is skipped and flagged in counts[3] (never an
+// out-of-range store).
+#include "fade_common.h"
+
+namespace fade {
+namespace {
+
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanWaves = kPlanThreads / 64;
+constexpr int64_t kTierFp16 = 0, kTierInt4 = 1, kTierInt2 = 2, kTierEvict = 3;
+constexpr int kClsShift = 28;
+constexpr int32_t kSlotMask = (1 << kClsShift) - 1;
+
+// Exclusive scan of a 64-bit value over the block (lane shuffles + LDS).
+__device__ __forceinline__ uint64_t block_exclusive_scan(uint64_t v, uint64_t* wtot, uint64_t* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint64_t inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t u = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += u;
+  }
+  if (lane == 63) wtot[wave] = inc;
+  __syncthreads();
+  if (wave == 0) {
+    uint64_t w = lane < kPlanWaves ? wtot[lane] : 0;
+    uint64_t winc = w;
+#pragma unroll
+    for (int o = 1; o < kPlanWaves; o <<= 1) {
+      const uint64_t u = __shfl_up(winc, o, 64);
+      if (lane >= o) winc += u;
+    }
+    if (lane < kPlanWaves) wtot[lane] = winc - w;  // exclusive wave offsets
+    if (lane == kPlanWaves - 1) *total = winc;
+  }
+  __syncthreads();
+  return wtot[wave] + inc - v;
+}
+
+// counts = {n_fp16, n_int4, n_kept, status}; status bit 0: an INT2 token,
+// bit 1: a value outside {FP16, INT4, INT2, EVICT}.
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int64_t* __restrict__ tiers, int64_t S,
+                                                            int64_t n_sink, const int64_t* __restrict__ pos_old,
+                                                            int32_t* __restrict__ dst, int32_t* __restrict__ newpos,
+                                                            int64_t* __restrict__ pos_sink,
+                                                            int64_t* __restrict__ pos_recent,
+                                                            int64_t* __restrict__ pos_mid, int32_t* __restrict__ counts) {
+  __shared__ uint64_t wtot[kPlanWaves];
+  __shared__ uint64_t total_s;
+  __shared__ int status_s;
+  if (threadIdx.x == 0) status_s = 0;
+  const int64_t per = (S + kPlanThreads - 1) / kPlanThreads;
+  const int64_t j0 = static_cast<int64_t>(threadIdx.x) * per;
+  const int64_t j1 = j0 + per < S ? j0 + per : S;
+  uint32_t nf = 0, ni = 0;
+  int bad = 0;
+  for (int64_t j = j0; j < j1; ++j) {
+    const int64_t v = tiers[j];
+    if (v == kTierFp16) ++nf;
+    else if (v == kTierInt4) ++ni;
+    else if (v == kTierInt2) bad |= 1;
+    else if (v != kTierEvict) bad |= 2;
+  }
+  __syncthreads();  // status_s initialised
+  if (bad) atomicOr(&status_s, bad);
+  const uint64_t ex = block_exclusive_scan(static_cast<uint64_t>(nf) | (static_cast<uint64_t>(ni) << 32), wtot, &total_s);
+  const uint64_t tot = total_s;
+  const int64_t n_fp16 = static_cast<int64_t>(tot & 0xFFFFFFFFu), n_int4 = static_cast<int64_t>(tot >> 32);
+  const int64_t n_kept = n_fp16 + n_int4;
+  const bool evicted = n_kept < S;
+  int64_t f = static_cast<int64_t>(ex & 0xFFFFFFFFu), m = static_cast<int64_t>(ex >> 32);
+  for (int64_t j = j0; j < j1; ++j) {
+    const int64_t v = tiers[j];
+    int32_t d = -1, np = -1;
+    if (v == kTierFp16 || v == kTierInt4) {
+      np = static_cast<int32_t>(f + m);
+      const int64_t p = evicted ? f + m : pos_old[j];
+      if (v == kTierFp16) {
+        if (f < n_sink) {
+          d = static_cast<int32_t>(f);
+          pos_sink[f] = p;
+        } else {
+          d = (1 << kClsShift) | static_cast<int32_t>(f - n_sink);
+          pos_recent[f - n_sink] = p;
+        }
+        ++f;
+      } else {
+        d = (2 << kClsShift) | static_cast<int32_t>(m);
+        pos_mid[m] = p;
+        ++m;
+      }
+    }
+    dst[j] = d;
+    newpos[j] = np;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    counts[0] = static_cast<int32_t>(n_fp16);
+    counts[1] = static_cast<int32_t>(n_int4);
+    counts[2] = static_cast<int32_t>(n_kept);
+    counts[3] = status_s;
+  }
+}
+
+__device__ __forceinline__ float nib(uint32_t byte, bool high) {
+  const int c = high ? static_cast<int>(byte >> 4) : static_cast<int>(byte & 0xF);
+  return static_cast<float>(c - ((c & 8) << 1));
+}
+
+// One thread per (source row j, channel pair i, i + D/2) of one (b, h).
+__global__ __launch_bounds__(256) void gather_kernel(FadeReassignArgs a) {
+  int32_t* status = a.counts + 3;
+  const int D = static_cast<int>(a.D), half = D / 2;
+  const int rows_per_block = blockDim.x / half;
+  const int i = threadIdx.x % half;
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * rows_per_block + threadIdx.x / half;
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / a.H, h = bh % a.H;
+  if (j >= a.S) return;
+  const int32_t d = a.dst[j];
+  if (d < 0) return;
+  const int cls = d >> kClsShift;
+  const int64_t slot = d & kSlotMask;
+  // source pair
+  float k0, k1;
+  uint16_t v0, v1;
+  if (j < a.n_sink_old || j >= a.n_sink_old + a.n_mid_old) {
+    const bool sink = j < a.n_sink_old;
+    const int64_t r = sink ? j : j - a.n_sink_old - a.n_mid_old;
+    const uint16_t* kb = static_cast<const uint16_t*>(sink ? a.sink_k : a.rec_k);
+    const uint16_t* vb = static_cast<const uint16_t*>(sink ? a.sink_v : a.rec_v);
+    const int64_t off = sink ? b * a.sink_sb + h * a.sink_sh + r * a.sink_ss : b * a.rec_sb + h * a.rec_sh + r * a.rec_ss;
+    k0 = h2f(kb[off + i]);
+    k1 = h2f(kb[off + i + half]);
+    v0 = vb[off + i];
+    v1 = vb[off + i + half];
+  } else {
+    // reference INT4: K per-channel scale [B,H,1,D], V per-token scale [B,H,mid,1]
+    const int64_t r = j - a.n_sink_old;
+    const uint8_t* kq = static_cast<const uint8_t*>(a.mid_kq) + (bh * a.n_mid_old + r) * half;
+    const uint8_t* vq = static_cast<const uint8_t*>(a.mid_vq) + (bh * a.n_mid_old + r) * half;
+    const uint16_t* ks = static_cast<const uint16_t*>(a.mid_ks) + bh * D;
+    const float vs = h2f(static_cast<const uint16_t*>(a.mid_vs)[bh * a.n_mid_old + r]);
+    const bool hi0 = (i & 1) == 0, hi1 = ((i + half) & 1) == 0;  // even channel: high nibble
+    k0 = round_f16(nib(kq[i >> 1], hi0) * h2f(ks[i]));
+    k1 = round_f16(nib(kq[(i + half) >> 1], hi1) * h2f(ks[i + half]));
+    v0 = f2h(nib(vq[i >> 1], hi0) * vs);
+    v1 = f2h(nib(vq[(i + half) >> 1], hi1) * vs);
+  }
+  uint16_t ko0, ko1;
+  if (a.counts[2] < a.S) {
+    // un-RoPE at the old position (k*cos - rotate_half(k)*sin), fp16, then
+    // RoPE at the new one (k*cos + rotate_half(k)*sin), fp16
+    const int64_t po = a.pos_old[j], pn = a.newpos[j];
+    if (po < 0 || po >= a.table_rows || pn < 0 || pn >= a.table_rows) {
+      atomicOr(status, 4);
+      return;
+    }
+    const float* co = a.cos_tab + po * D;
+    const float* so = a.sin_tab + po * D;
+    const float u0 = round_f16(k0 * co[i] - (-k1) * so[i]);
+    const float u1 = round_f16(k1 * co[i + half] - k0 * so[i + half]);
+    const float* cn = a.cos_tab + pn * D;
+    const float* sn = a.sin_tab + pn * D;
+    ko0 = f2h(u0 * cn[i] + (-u1) * sn[i]);
+    ko1 = f2h(u1 * cn[i + half] + u0 * sn[i + half]);
+  } else {
+    ko0 = f2h(k0);
+    ko1 = f2h(k1);
+  }
+  uint16_t *kd, *vd;
+  int64_t off;
+  if (cls == 0) {
+    if (slot >= a.cap_sink) { atomicOr(status, 8); return; }
+    kd = static_cast<uint16_t*>(a.out_sink_k);
+    vd = static_cast<uint16_t*>(a.out_sink_v);
+    off = (bh * a.cap_sink + slot) * D;
+  } else if (cls == 1) {
+    if (slot >= a.cap_rec) { atomicOr(status, 8); return; }
+    kd = static_cast<uint16_t*>(a.out_rec_k);
+    vd = static_cast<uint16_t*>(a.out_rec_v);
+    off = b * a.out_rec_sb + h * a.out_rec_sh + slot * a.out_rec_ss;
+  } else {
+    if (slot >= a.cap_mid) { atomicOr(status, 8); return; }
+    kd = static_cast<uint16_t*>(a.out_mid_k);
+    vd = static_cast<uint16_t*>(a.out_mid_v);
+    off = (bh * a.cap_mid + slot) * D;
+  }
+  kd[off + i] = ko0;
+  kd[off + i + half] = ko1;
+  vd[off + i] = v0;
+  vd[off + i + half] = v1;
+}
+
+}  // namespace
+}  // namespace fade
+
+using namespace fade;
+
+FADE_API int fade_reassign_plan(const int64_t* tiers, int64_t S, int64_t n_sink, const int64_t* pos_old,
+                                int32_t* dst, int32_t* newpos, int64_t* pos_sink, int64_t* pos_recent,
+                                int64_t* pos_mid, int32_t* counts, void* stream) {
+  const char* fn = "fade_reassign_plan";
+  if (S < 0 || n_sink < 0) return einval("%s: negative S or n_sink", fn);
+  if (S >= (1LL << 30)) return einval("%s: S=%lld too large", fn, (long long)S);
+  if (counts == nullptr) return einval("%s: null counts", fn);
+  if (S > 0 && (tiers == nullptr || pos_old == nullptr || dst == nullptr || newpos == nullptr || pos_sink == nullptr ||
+                pos_recent == nullptr || pos_mid == nullptr))
+    return einval("%s: null pointer", fn);
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, as_stream(stream), tiers, S, n_sink, pos_old, dst,
+                     newpos, pos_sink, pos_recent, pos_mid, counts);
+  return check_launch(fn);
+}
+
+FADE_API int fade_reassign_gather(const FadeReassignArgs* args, void* stream) {
+  const char* fn = "fade_reassign_gather";
+  if (args == nullptr) return einval("%s: null argument", fn);
+  const FadeReassignArgs& a = *args;
+  if (a.D <= 0 || a.D % 2 != 0 || a.D > 512) return einval("%s: head_dim must be even and <= 512", fn);
+  if (a.B < 0 || a.H < 0 || a.S < 0 || a.n_sink_old < 0 || a.n_mid_old < 0 ||
+      a.n_sink_old + a.n_mid_old > a.S)
+    return einval("%s: inconsistent tier lengths", fn);
+  if (a.dst == nullptr || a.newpos == nullptr || a.counts == nullptr || a.pos_old == nullptr)
+    return einval("%s: null plan pointer", fn);
+  if (a.n_mid_old > 0 && (a.mid_kq == nullptr || a.mid_ks == nullptr || a.mid_vq == nullptr || a.mid_vs == nullptr))
+    return einval("%s: null middle tier", fn);
+  if ((a.n_sink_old > 0 && (a.sink_k == nullptr || a.sink_v == nullptr)) ||
+      (a.S - a.n_sink_old - a.n_mid_old > 0 && (a.rec_k == nullptr || a.rec_v == nullptr)))
+    return einval("%s: null fp16 tier", fn);
+  if ((a.cap_sink > 0 && (a.out_sink_k == nullptr || a.out_sink_v == nullptr)) ||
+      (a.cap_rec > 0 && (a.out_rec_k == nullptr || a.out_rec_v == nullptr)) ||
+      (a.cap_mid > 0 && (a.out_mid_k == nullptr || a.out_mid_v == nullptr)))
+    return einval("%s: null output", fn);
+  if (a.table_rows > 0 && (a.cos_tab == nullptr || a.sin_tab == nullptr)) return einval("%s: null RoPE table", fn);
+  const int64_t BH = a.B * a.H;
+  if (BH == 0 || a.S == 0) return FADE_OK;
+  if (BH > 65535) return einval("%s: B*H=%lld exceeds 65535", fn, (long long)BH);
+  const int half = static_cast<int>(a.D / 2);
+  const int rpb = half >= 256 ? 1 : 256 / half;
+  const dim3 grid(static_cast<unsigned>(cdiv(a.S, rpb)), static_cast<unsigned>(BH));
+  hipLaunchKernelGGL(gather_kernel, grid, dim3(rpb * half), 0, as_stream(stream), a);
+  return check_launch(fn);
+}

@@ -134,6 +134,63 @@ int fade_rerope_gather(const void* k_f16, int64_t ksb, int64_t ksh, int64_t kss,
                        const float* sin_old, const float* cos_new, const float* sin_new,
                        void* k_out_f16, void* v_out_f16, void* stream);
 
+/* ---------------- device-side tier reassignment --------------------------- */
+/* fade/cache.py:881-1057 (apply_tier_assignment, shared tiers) for the
+ * reference INT4 middle tier, without materializing the layer.
+ *
+ * fade_reassign_plan: tiers int64 [S] (TIER_FP16 0 / INT4 1 / INT2 2 / EVICT 3)
+ * in the cache's position order, pos_old int64 [S].  Writes dst int32 [S]
+ * (-1 evicted, else cls << 28 | slot with cls 0 sink, 1 recent, 2 middle; the
+ * first n_sink FP16 tokens are the sink), newpos int32 [S] (rank among kept
+ * tokens), the new positions of each tier (pos_sink / pos_recent / pos_mid,
+ * capacity S each: old positions, or 0..n_kept-1 when tokens are evicted) and
+ * counts int32 [4] = {n_fp16, n_int4, n_kept, status} (status bit 0: INT2
+ * tokens present -- not handled here; bit 1: an unknown tier value). */
+int fade_reassign_plan(const int64_t* tiers, int64_t S, int64_t n_sink, const int64_t* pos_old,
+                       int32_t* dst, int32_t* newpos, int64_t* pos_sink, int64_t* pos_recent,
+                       int64_t* pos_mid, int32_t* counts, void* stream);
+
+/* fade_reassign_gather: moves every kept token of the current tiers (in
+ * position order: sink rows, middle rows, recent rows) to its destination.
+ * Middle rows are dequantized as fp16(fp16(code) * fp16(scale)); K rows are
+ * un-RoPE'd at pos_old and re-RoPE'd at newpos (fp16 between, as the
+ * reference) when counts[2] < S, using cos/sin tables fp32 [table_rows, D]
+ * indexed by position.  Sink and middle outputs are contiguous
+ * [B,H,cap,D]; the recent output has element strides.  Writes beyond a
+ * capacity are skipped and set status bit 3 (bit 2: a position outside the
+ * tables). */
+typedef struct FadeReassignArgs {
+  int64_t B, H, D, S;
+  int64_t n_sink_old, n_mid_old; /* recent = S - sink - middle */
+  const void* sink_k;
+  const void* sink_v;
+  int64_t sink_sb, sink_sh, sink_ss; /* element strides shared by sink K and V */
+  const void* mid_kq;                /* [B,H,mid,D/2] u8, high nibble = even channel */
+  const void* mid_ks;                /* [B,H,1,D] fp16 */
+  const void* mid_vq;                /* [B,H,mid,D/2] u8 */
+  const void* mid_vs;                /* [B,H,mid,1] fp16 */
+  const void* rec_k;
+  const void* rec_v;
+  int64_t rec_sb, rec_sh, rec_ss;
+  const int32_t* dst;
+  const int32_t* newpos;
+  int32_t* counts; /* from fade_reassign_plan; status ORed into counts[3] */
+  const int64_t* pos_old;
+  const float* cos_tab;
+  const float* sin_tab;
+  int64_t table_rows;
+  void* out_sink_k;
+  void* out_sink_v;
+  int64_t cap_sink;
+  void* out_rec_k;
+  void* out_rec_v;
+  int64_t out_rec_sb, out_rec_sh, out_rec_ss, cap_rec;
+  void* out_mid_k;
+  void* out_mid_v;
+  int64_t cap_mid;
+} FadeReassignArgs;
+int fade_reassign_gather(const FadeReassignArgs* args, void* stream);
+
 /* ---------------- tiered decode attention --------------------------------- */
 /* fp16 tier (sink or recent): K/V [B,Hkv,len,D] with element strides. */
 typedef struct fade_fp16_tier {
