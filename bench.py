@@ -224,6 +224,45 @@ def rerope_case(dev):
     return plan, 4 * B * H * n * D * 2, n
 
 
+def reassign_case(dev, n_inst: int = 8):
+    """Config 3 tier reassignment of one layer, wall-clock per call (host work and
+    syncs included), device path vs the host path (the reference's op sequence):
+    B=8, Hkv=4; a cache of 4 sink + 3964 INT4 + 128 fp16 recent tokens (4096)
+    keeps 4 sink + the 400 best-scoring middle + 64 recent (eviction, re-RoPE,
+    middle requantized)."""
+    from fade_amd.cache import TieredKVCache
+    from fade_amd.policy import _assign_one_layer
+    from fade_amd.synthetic import exp_scores
+
+    B, H, D = 8, 4, 128
+    _, k, v = kv_tensors(B, H, 4096, D, seed=1003, Hq=28)
+    kd, vd = k.to(dev), v.to(dev)
+    tiers0 = _assign_one_layer(4032, torch.zeros(4032), 4, 64, None, 0)
+    tiers = _assign_one_layer(4096, exp_scores(4096, 1003), 4, 64, 400, 0)
+    out = {}
+    for name, device_path in (("device", True), ("host", False)):
+        caches = []
+        for _ in range(n_inst):
+            c = TieredKVCache(n_sink=4, recent_window=64, int4_budget=400, int2_budget=0, head_dim=D)
+            c.device_reassign = device_path
+            c.update(kd[:, :, :4032], vd[:, :, :4032], 0)
+            c.apply_tier_assignment(0, tiers0)
+            c.update(kd[:, :, 4032:], vd[:, :, 4032:], 0)
+            caches.append(c)
+        caches[0].apply_tier_assignment(0, tiers)  # warm-up (RoPE table, allocator)
+        torch.cuda.synchronize()
+        times = []
+        for c in caches[1:]:
+            t0 = time.perf_counter()
+            c.apply_tier_assignment(0, tiers)
+            torch.cuda.synchronize()
+            times.append((time.perf_counter() - t0) * 1e6)
+        out[name] = round(float(np.median(times)), 1)
+        del caches
+        torch.cuda.empty_cache()
+    return out
+
+
 def copy_peak(dev, stream) -> float:
     """Device-to-device copy of 1 GiB (read + write), GB/s: the measured streaming ceiling."""
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -444,6 +483,9 @@ def main() -> int:
         extra["c3_rerope_gather"] = {"us": round(rmean * 1e3, 2), "GBps": round(rbytes / (rmean * 1e-3) / 1e9, 1),
                                      "bytes": rbytes, "n_kept": n_kept}
         del rp
+        ra = reassign_case(dev)
+        extra["c3_reassign_layer_wall_us"] = {"device_path": ra["device"], "host_path": ra["host"],
+                                              "speedup": round(ra["host"] / ra["device"], 2)}
         extra["copy_peak_GBps"] = round(copy_peak(dev, stream), 1)
         torch.cuda.empty_cache()
         c2 = CONFIGS[2]

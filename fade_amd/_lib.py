@@ -126,7 +126,7 @@ class ReassignArgs(ctypes.Structure):
         ("sink_k", _p), ("sink_v", _p), ("sink_sb", _i64), ("sink_sh", _i64), ("sink_ss", _i64),
         ("mid_kq", _p), ("mid_ks", _p), ("mid_vq", _p), ("mid_vs", _p),
         ("rec_k", _p), ("rec_v", _p), ("rec_sb", _i64), ("rec_sh", _i64), ("rec_ss", _i64),
-        ("dst", _p), ("newpos", _p), ("counts", _p), ("pos_old", _p),
+        ("dst", _p), ("newpos", _p), ("src_of", _p), ("rows", _i64), ("counts", _p), ("pos_old", _p),
         ("cos_tab", _p), ("sin_tab", _p), ("table_rows", _i64),
         ("out_sink_k", _p), ("out_sink_v", _p), ("cap_sink", _i64),
         ("out_rec_k", _p), ("out_rec_v", _p), ("out_rec_sb", _i64), ("out_rec_sh", _i64), ("out_rec_ss", _i64),
@@ -159,7 +159,7 @@ _SIGNATURES: dict[str, list] = {
     ],
     "fade_tiered_decode_workspace_bytes": [ctypes.POINTER(DecodeArgs), _pi64],
     "fade_tiered_decode_attn": [ctypes.POINTER(DecodeArgs), _p],
-    "fade_reassign_plan": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p],
+    "fade_reassign_plan": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
     "fade_reassign_gather": [ctypes.POINTER(ReassignArgs), _p],
     "fade_tiered_prefill_attn": [ctypes.POINTER(PrefillArgs), _p],
 }

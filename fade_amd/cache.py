@@ -100,6 +100,10 @@ class LayerState:
         )
 
 
+# device RoPE tables of the device-side reassignment: (scheme, dtype, device) -> (cos, sin)
+_ROPE_TABLES: dict = {}
+
+
 def _sel(x: Tensor, idx: Tensor) -> Tensor:
     return x.index_select(-2, idx).contiguous()
 
@@ -155,8 +159,6 @@ class TieredKVCache(DynamicCache):
         self.fused = False
         # apply_tier_assignment on the device for the reference INT4 layout
         self.device_reassign = True
-        self._rope_tab_key = None
-        self._rope_tab = None
         self._last_reassign_counts = None
 
     # transformers 5.x defines a read-only ``Cache.batch_size``; the tiered cache
@@ -497,15 +499,22 @@ class TieredKVCache(DynamicCache):
             st._fp16_len = 0
 
     def _rope_tables(self, rows: int, device) -> tuple[Tensor, Tensor]:
-        """cos/sin fp32 ``[rows, D]`` for positions ``0..rows-1`` on ``device`` (the last
-        table is kept: every layer of one reassignment round uses the same one)."""
-        key = (rows, str(device))
-        if self._rope_tab_key != key:
-            cos, sin = self._ensure_rope_scheme().host_cos_sin(torch.arange(rows, dtype=torch.long), self.dtype)
+        """cos/sin fp32 ``[R, D]`` (R >= rows) for positions ``0..R-1`` on ``device``.
+
+        A row depends only on its position, so one table serves every layer and
+        every later round until positions outgrow it: R is ``rows`` rounded up to
+        a power of two (at least 4096), and the last table per (scheme, dtype,
+        device) is kept at module level."""
+        scheme = self._ensure_rope_scheme()
+        key = (repr(scheme), str(self.dtype), str(device))
+        tab = _ROPE_TABLES.get(key)
+        if tab is None or int(tab[0].shape[0]) < rows:
+            cap = max(4096, 1 << max(0, rows - 1).bit_length())
+            cos, sin = scheme.host_cos_sin(torch.arange(cap, dtype=torch.long), self.dtype)
             # pinned + non_blocking: an upload that does not wait for the device
-            self._rope_tab = tuple(t.contiguous().pin_memory().to(device, non_blocking=True) for t in (cos, sin))
-            self._rope_tab_key = key
-        return self._rope_tab
+            tab = tuple(t.contiguous().pin_memory().to(device, non_blocking=True) for t in (cos, sin))
+            _ROPE_TABLES[key] = tab
+        return tab
 
     def _device_reassign_ok(self, st: LayerState) -> bool:
         k = st.sink_k if st.sink_k is not None else st.fp16_k
@@ -583,12 +592,13 @@ class TieredKVCache(DynamicCache):
             tiers_d = (tiers_d.pin_memory() if tiers_d.device.type == "cpu" else tiers_d).to(dev, non_blocking=True)
         dst = torch.empty(S, dtype=torch.int32, device=dev)
         newpos = torch.empty(S, dtype=torch.int32, device=dev)
+        src_of = torch.empty(max(S, 1), dtype=torch.int32, device=dev)
         pos_new = torch.empty(3, max(S, 1), dtype=torch.long, device=dev)
         cnt = torch.empty(4, dtype=torch.int32, device=dev)
         stream = _lib.stream_of(tiers_d)
         _lib.call("fade_reassign_plan", tiers_d.data_ptr(), S, self.n_sink, pos_old.data_ptr(), dst.data_ptr(),
-                  newpos.data_ptr(), pos_new[0].data_ptr(), pos_new[1].data_ptr(), pos_new[2].data_ptr(),
-                  cnt.data_ptr(), stream)
+                  newpos.data_ptr(), src_of.data_ptr(), pos_new[0].data_ptr(), pos_new[1].data_ptr(),
+                  pos_new[2].data_ptr(), cnt.data_ptr(), stream)
         if counts is None:
             c = cnt.cpu().tolist()  # the one host sync: tiers were on the device
             if c[3] != 0:
@@ -624,7 +634,8 @@ class TieredKVCache(DynamicCache):
         if rec is not None:
             a.rec_k, a.rec_v = rec[0].data_ptr(), rec[1].data_ptr()
             a.rec_sb, a.rec_sh, a.rec_ss = rec[0].stride()[:3]
-        a.dst, a.newpos, a.counts, a.pos_old = dst.data_ptr(), newpos.data_ptr(), cnt.data_ptr(), pos_old.data_ptr()
+        a.dst, a.newpos, a.src_of, a.rows = dst.data_ptr(), newpos.data_ptr(), src_of.data_ptr(), n_kept
+        a.counts, a.pos_old = cnt.data_ptr(), pos_old.data_ptr()
         if tab is not None:
             a.cos_tab, a.sin_tab, a.table_rows = tab[0].data_ptr(), tab[1].data_ptr(), int(tab[0].shape[0])
         if out_sink is not None:

@@ -11,7 +11,7 @@
 //           one block scan) and writes, per source token j, its destination
 //           (sink / recent / middle slot) and its rank among the kept
 //           tokens, the new position arrays and the tier counts;
-//   gather  one thread per (row, channel pair i, i + D/2) reads the source
+//   gather  one thread per (kept token, channel pair i, i + D/2) reads the source
 //           row in place -- sink or recent fp16, or a middle row dequantized
 //           in registers as fp16(fp16(code) * fp16(scale)) -- un-RoPEs /
 //           re-RoPEs K with the reference's rounding when tokens were
@@ -65,6 +65,7 @@ __device__ __forceinline__ uint64_t block_exclusive_scan(uint64_t v, uint64_t* w
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int64_t* __restrict__ tiers, int64_t S,
                                                             int64_t n_sink, const int64_t* __restrict__ pos_old,
                                                             int32_t* __restrict__ dst, int32_t* __restrict__ newpos,
+                                                            int32_t* __restrict__ src_of,
                                                             int64_t* __restrict__ pos_sink,
                                                             int64_t* __restrict__ pos_recent,
                                                             int64_t* __restrict__ pos_mid, int32_t* __restrict__ counts) {
@@ -97,6 +98,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int64_t* __res
     int32_t d = -1, np = -1;
     if (v == kTierFp16 || v == kTierInt4) {
       np = static_cast<int32_t>(f + m);
+      src_of[f + m] = static_cast<int32_t>(j);
       const int64_t p = evicted ? f + m : pos_old[j];
       if (v == kTierFp16) {
         if (f < n_sink) {
@@ -130,16 +132,19 @@ __device__ __forceinline__ float nib(uint32_t byte, bool high) {
   return static_cast<float>(c - ((c & 8) << 1));
 }
 
-// One thread per (source row j, channel pair i, i + D/2) of one (b, h).
+// One thread per (kept token, channel pair i, i + D/2) of one (b, h); the
+// grid covers `rows` kept ranks (the host's count, or S when it has none).
 __global__ __launch_bounds__(256) void gather_kernel(FadeReassignArgs a) {
   int32_t* status = a.counts + 3;
   const int D = static_cast<int>(a.D), half = D / 2;
   const int rows_per_block = blockDim.x / half;
   const int i = threadIdx.x % half;
-  const int64_t j = static_cast<int64_t>(blockIdx.x) * rows_per_block + threadIdx.x / half;
+  const int64_t rank = static_cast<int64_t>(blockIdx.x) * rows_per_block + threadIdx.x / half;
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / a.H, h = bh % a.H;
-  if (j >= a.S) return;
+  if (rank >= a.counts[2] || rank >= a.S) return;
+  const int64_t j = a.src_of[rank];
+  if (j < 0 || j >= a.S) return;
   const int32_t d = a.dst[j];
   if (d < 0) return;
   const int cls = d >> kClsShift;
@@ -221,17 +226,17 @@ __global__ __launch_bounds__(256) void gather_kernel(FadeReassignArgs a) {
 using namespace fade;
 
 FADE_API int fade_reassign_plan(const int64_t* tiers, int64_t S, int64_t n_sink, const int64_t* pos_old,
-                                int32_t* dst, int32_t* newpos, int64_t* pos_sink, int64_t* pos_recent,
-                                int64_t* pos_mid, int32_t* counts, void* stream) {
+                                int32_t* dst, int32_t* newpos, int32_t* src_of, int64_t* pos_sink,
+                                int64_t* pos_recent, int64_t* pos_mid, int32_t* counts, void* stream) {
   const char* fn = "fade_reassign_plan";
   if (S < 0 || n_sink < 0) return einval("%s: negative S or n_sink", fn);
   if (S >= (1LL << 30)) return einval("%s: S=%lld too large", fn, (long long)S);
   if (counts == nullptr) return einval("%s: null counts", fn);
-  if (S > 0 && (tiers == nullptr || pos_old == nullptr || dst == nullptr || newpos == nullptr || pos_sink == nullptr ||
-                pos_recent == nullptr || pos_mid == nullptr))
+  if (S > 0 && (tiers == nullptr || pos_old == nullptr || dst == nullptr || newpos == nullptr || src_of == nullptr ||
+                pos_sink == nullptr || pos_recent == nullptr || pos_mid == nullptr))
     return einval("%s: null pointer", fn);
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, as_stream(stream), tiers, S, n_sink, pos_old, dst,
-                     newpos, pos_sink, pos_recent, pos_mid, counts);
+                     newpos, src_of, pos_sink, pos_recent, pos_mid, counts);
   return check_launch(fn);
 }
 
@@ -243,7 +248,7 @@ FADE_API int fade_reassign_gather(const FadeReassignArgs* args, void* stream) {
   if (a.B < 0 || a.H < 0 || a.S < 0 || a.n_sink_old < 0 || a.n_mid_old < 0 ||
       a.n_sink_old + a.n_mid_old > a.S)
     return einval("%s: inconsistent tier lengths", fn);
-  if (a.dst == nullptr || a.newpos == nullptr || a.counts == nullptr || a.pos_old == nullptr)
+  if (a.dst == nullptr || a.newpos == nullptr || a.src_of == nullptr || a.counts == nullptr || a.pos_old == nullptr)
     return einval("%s: null plan pointer", fn);
   if (a.n_mid_old > 0 && (a.mid_kq == nullptr || a.mid_ks == nullptr || a.mid_vq == nullptr || a.mid_vs == nullptr))
     return einval("%s: null middle tier", fn);
@@ -260,7 +265,8 @@ FADE_API int fade_reassign_gather(const FadeReassignArgs* args, void* stream) {
   if (BH > 65535) return einval("%s: B*H=%lld exceeds 65535", fn, (long long)BH);
   const int half = static_cast<int>(a.D / 2);
   const int rpb = half >= 256 ? 1 : 256 / half;
-  const dim3 grid(static_cast<unsigned>(cdiv(a.S, rpb)), static_cast<unsigned>(BH));
+  const int64_t rows = a.rows > 0 && a.rows < a.S ? a.rows : a.S;
+  const dim3 grid(static_cast<unsigned>(cdiv(rows, rpb)), static_cast<unsigned>(BH));
   hipLaunchKernelGGL(gather_kernel, grid, dim3(rpb * half), 0, as_stream(stream), a);
   return check_launch(fn);
 }

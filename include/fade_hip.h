@@ -142,16 +142,17 @@ int fade_rerope_gather(const void* k_f16, int64_t ksb, int64_t ksh, int64_t kss,
  * in the cache's position order, pos_old int64 [S].  Writes dst int32 [S]
  * (-1 evicted, else cls << 28 | slot with cls 0 sink, 1 recent, 2 middle; the
  * first n_sink FP16 tokens are the sink), newpos int32 [S] (rank among kept
- * tokens), the new positions of each tier (pos_sink / pos_recent / pos_mid,
+ * tokens), src_of int32 [S] (source index of each kept rank), the new positions of each tier (pos_sink / pos_recent / pos_mid,
  * capacity S each: old positions, or 0..n_kept-1 when tokens are evicted) and
  * counts int32 [4] = {n_fp16, n_int4, n_kept, status} (status bit 0: INT2
  * tokens present -- not handled here; bit 1: an unknown tier value). */
 int fade_reassign_plan(const int64_t* tiers, int64_t S, int64_t n_sink, const int64_t* pos_old,
-                       int32_t* dst, int32_t* newpos, int64_t* pos_sink, int64_t* pos_recent,
-                       int64_t* pos_mid, int32_t* counts, void* stream);
+                       int32_t* dst, int32_t* newpos, int32_t* src_of, int64_t* pos_sink,
+                       int64_t* pos_recent, int64_t* pos_mid, int32_t* counts, void* stream);
 
 /* fade_reassign_gather: moves every kept token of the current tiers (in
- * position order: sink rows, middle rows, recent rows) to its destination.
+ * position order: sink rows, middle rows, recent rows) to its destination;
+ * one pass over the kept tokens (src_of), at most counts[2] of them.
  * Middle rows are dequantized as fp16(fp16(code) * fp16(scale)); K rows are
  * un-RoPE'd at pos_old and re-RoPE'd at newpos (fp16 between, as the
  * reference) when counts[2] < S, using cos/sin tables fp32 [table_rows, D]
@@ -174,6 +175,8 @@ typedef struct FadeReassignArgs {
   int64_t rec_sb, rec_sh, rec_ss;
   const int32_t* dst;
   const int32_t* newpos;
+  const int32_t* src_of;
+  int64_t rows;    /* kept tokens if the caller knows the count, else 0 (grid covers S) */
   int32_t* counts; /* from fade_reassign_plan; status ORed into counts[3] */
   const int64_t* pos_old;
   const float* cos_tab;
