@@ -89,6 +89,7 @@ class DecodeArgs(ctypes.Structure):
         ("kernel", _i32),
         ("workspace", _p),
         ("workspace_bytes", _i64),
+        ("lens", _p),
     ]
 
 

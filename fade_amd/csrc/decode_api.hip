@@ -134,6 +134,7 @@ Params to_params(const fade_decode_args* a) {
   p.mid.v_scale = static_cast<const uint16_t*>(m.v_scale);
   p.mid.v_zero = static_cast<const uint16_t*>(m.v_zero);
   p.total = total_tokens(a);
+  p.lens = a->lens;
   return p;
 }
 
@@ -196,6 +197,9 @@ FADE_API int fade_tiered_decode_attn(const fade_decode_args* a, void* stream) {
   if ((a->kernel == 2 || a->kernel == 3) && pl.k == Kern::kValu)
     return einval("fade_tiered_decode_attn: the matrix-core kernels do not handle this middle tier (format %d)",
                   p.mid.fmt);
+  if (a->lens != nullptr && pl.k != Kern::kInt4)
+    return einval("fade_tiered_decode_attn: per-row lengths need the matrix-core INT4 kernel "
+                  "(middle tier FADE_MID_SYM or FADE_MID_ASYM, GQA <= 4)");
   const WsLayout ws = ws_layout(a, pl.n);
   if (a->workspace == nullptr || a->workspace_bytes < ws.total)
     return einval("fade_tiered_decode_attn: workspace too small (%lld < %lld bytes)",

@@ -47,6 +47,7 @@ struct Params {
   int64_t n_f16_tiles;      // 16-token fp16 tiles ahead of the packed 64-token tiles
   int64_t tiles_per_split;  // tiles (either kind) per split
   uint32_t* counters;       // [B*Hkv] finished splits; zero between calls
+  const int32_t* lens;      // optional [B][3] per-row sink / middle / recent lengths
 };
 
 // Signed symmetric code of channel d in a packed row (fade/quant.py:26-43,

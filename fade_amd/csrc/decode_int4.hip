@@ -187,9 +187,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   const int hq = n16 >> 2, sq = n16 & 3;  // head / sub-tile of this lane's scores
   const int G = p.G;
   const int64_t bkv = b * p.Hkv + kvh;
-  const int64_t M = p.mid.len;
-  const int64_t F = p.total - M;
-  const int64_t nFt = p.n_f16_tiles;
+  // Mc: rows of the middle tensors per (batch row, kv head); M, ns, F: this
+  // row's middle, sink and fp16 token counts (per-row lengths when given,
+  // clamped to the capacities)
+  const int64_t Mc = p.mid.len;
+  int64_t M = Mc, ns = p.sink.len, F = p.total - Mc;
+  int64_t nFt = p.n_f16_tiles;
+  if (p.lens != nullptr) {
+    const int64_t ls = __builtin_amdgcn_readfirstlane(p.lens[3 * b]);
+    const int64_t lm = __builtin_amdgcn_readfirstlane(p.lens[3 * b + 1]);
+    const int64_t lr = __builtin_amdgcn_readfirstlane(p.lens[3 * b + 2]);
+    ns = ls < 0 ? 0 : (ls < p.sink.len ? ls : p.sink.len);
+    M = lm < 0 ? 0 : (lm < Mc ? lm : Mc);
+    F = ns + (lr < 0 ? 0 : (lr < p.recent.len ? lr : p.recent.len));
+    nFt = (F + kMini - 1) / kMini;
+  }
   const int64_t nT = nFt + (M + kTile - 1) / kTile;
   const int64_t t0 = static_cast<int64_t>(split) * p.tiles_per_split;
   const int64_t t1 = t0 + p.tiles_per_split < nT ? t0 + p.tiles_per_split : nT;
@@ -212,20 +224,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   __shared__ float red_m[kWaves][4], red_l[kWaves][4];
   __shared__ int last_s;
 
-  const uint8_t* kc = p.mid.k_codes + bkv * M * kRowK;
+  const uint8_t* kc = p.mid.k_codes + bkv * Mc * kRowK;
   // literal INT2 V: [v_rows][128] int8 codes and [v_rows / 64][128] scales per
   // (batch row, kv head), v_rows = the middle length padded to 64 (pad rows are 0)
-  const uint8_t* vc = p.mid.v_codes + bkv * (LIT ? p.mid.v_rows : M) * kRowV;
+  const uint8_t* vc = p.mid.v_codes + bkv * (LIT ? p.mid.v_rows : Mc) * kRowV;
   // reference formats: V scale per token; asymmetric: [token][4 groups] scale / zero
   const uint16_t* vsg =
-      LIT ? p.mid.v_scale + bkv * (p.mid.v_rows / kTile) * kD : p.mid.v_scale + bkv * M * (ASYM ? kGroups : 1);
-  const uint16_t* ksg = ASYM ? p.mid.k_scale + bkv * M * kGroups : nullptr;
-  const uint16_t* kzg = ASYM ? p.mid.k_zero + bkv * M * kGroups : nullptr;
-  const uint16_t* vzg = ASYM ? p.mid.v_zero + bkv * M * kGroups : nullptr;
+      LIT ? p.mid.v_scale + bkv * (p.mid.v_rows / kTile) * kD : p.mid.v_scale + bkv * Mc * (ASYM ? kGroups : 1);
+  const uint16_t* ksg = ASYM ? p.mid.k_scale + bkv * Mc * kGroups : nullptr;
+  const uint16_t* kzg = ASYM ? p.mid.k_zero + bkv * Mc * kGroups : nullptr;
+  const uint16_t* vzg = ASYM ? p.mid.v_zero + bkv * Mc * kGroups : nullptr;
   // fp16 tiers as (uniform) locals: the lambdas below must not read the kernel
   // arguments through a pointer (that becomes a per-lane global load whose
   // compiler-inserted vmcnt wait would also wait for the tile prefetches).
-  const int64_t ns = p.sink.len;
   const uint16_t* const sk = p.sink.k + b * p.sink.k_sb + kvh * p.sink.k_sh;
   const uint16_t* const sv = p.sink.v + b * p.sink.v_sb + kvh * p.sink.v_sh;
   const int64_t sk_ss = p.sink.k_ss, sv_ss = p.sink.v_ss;

@@ -113,9 +113,14 @@ class TieredDecodePlan:
         out: Tensor | None = None,
         n_splits: int = 0,
         kernel: int = 0,
+        lens: Tensor | None = None,
     ) -> None:
         if q.dim() != 4 or q.shape[2] != 1:
             raise ValueError(f"q must be [B, Hq, 1, D], got {tuple(q.shape)}")
+        if lens is not None:
+            if lens.dim() != 2 or lens.shape[1] != 3 or lens.shape[0] != q.shape[0]:
+                raise ValueError(f"lens must be [B, 3] (sink, middle, recent per row), got {tuple(lens.shape)}")
+            lens = lens.to(device=q.device, dtype=torch.int32).contiguous()
         tensors = [q] + ([*sink] if sink else []) + ([*recent] if recent else []) + (mid.tensors() if mid else [])
         _lib.require_gpu(*tensors, op="tiered_decode_attention")
         _lib.require_f16(q, "tiered_decode_attention")
@@ -126,7 +131,7 @@ class TieredDecodePlan:
             q = q.contiguous()
         if out is None:
             out = torch.empty(B, Hq, 1, D, dtype=torch.float16, device=q.device)
-        self._keep = (q, sink, mid, recent, out)
+        self._keep = (q, sink, mid, recent, out, lens)
         a = _lib.DecodeArgs()
         a.B, a.Hq, a.Hkv, a.D = B, Hq, Hkv, D
         a.q, a.q_sb, a.q_sh = q.data_ptr(), q.stride(0), q.stride(1)
@@ -134,6 +139,7 @@ class TieredDecodePlan:
         a.sm_scale = float(1.0 / math.sqrt(D) if sm_scale is None else sm_scale)
         a.sink, a.mid, a.recent = _fp16_tier(sink), _mid_tier(mid), _fp16_tier(recent)
         a.n_splits, a.kernel = int(n_splits), int(kernel)
+        a.lens = _lib.ptr(lens)
         lib = _lib.load()
         nb = ctypes.c_int64(0)
         _lib.check(lib.fade_tiered_decode_workspace_bytes(ctypes.byref(a), nb), "fade_tiered_decode_workspace_bytes")
@@ -158,13 +164,17 @@ def tiered_decode_attention(
     sm_scale: float | None = None,
     n_splits: int = 0,
     kernel: int = 0,
+    lens: Tensor | None = None,
 ) -> Tensor:
     """Decode attention of ``q`` [B,Hq,1,D] over the tiered cache; returns fp16 [B,Hq,1,D].
 
     Query head ``h`` attends to KV head ``h // (Hq // Hkv)`` (the reference's
     ``repeat_interleave`` GQA mapping, fade/kernels/fused_int4_attn.py:306-312).
+    ``lens`` [B, 3] (sink, middle, recent tokens per row; device or host int)
+    makes the batch ragged: row b attends to the first ``lens[b]`` rows of each
+    tier, whose tensors are then padded capacities.
     """
-    return TieredDecodePlan(q, sink, mid, recent, sm_scale, n_splits=n_splits, kernel=kernel).run()
+    return TieredDecodePlan(q, sink, mid, recent, sm_scale, n_splits=n_splits, kernel=kernel, lens=lens).run()
 
 
 __all__ = ["MiddleTier", "TieredDecodePlan", "tiered_decode_attention"]

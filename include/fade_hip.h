@@ -236,6 +236,11 @@ typedef struct fade_decode_args {
   void* workspace;             /* zero-filled before its first use; every call leaves its
                                   split counters at zero again */
   int64_t workspace_bytes;
+  const int32_t* lens;         /* optional device [B][3]: sink, middle, recent tokens of each
+                                  row (ragged batch; each at most the tier's len, which is then
+                                  the padded capacity of its tensors; every row >= 1 token).
+                                  NULL: every row has the tiers' full lengths.  Ragged rows
+                                  need the matrix-core INT4 kernel (SYM / ASYM formats). */
 } fade_decode_args;
 
 /* Replaces dequantize + torch.cat (fade/cache.py:683-842) + SDPA and the

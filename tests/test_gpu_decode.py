@@ -271,3 +271,55 @@ def test_decode_errors(dev):
     q = torch.zeros(1, 4, 1, 128, dtype=torch.float16, device=dev)
     with pytest.raises(ValueError, match="empty"):
         tiered_decode_attention(q, (k[:, :, :0], k[:, :, :0]), None, None)
+
+
+def _row_slice_mid(omid, b, lm):
+    """The oracle middle tier of batch row b restricted to its first lm tokens."""
+    out = {}
+    for key, val in omid.items():
+        if not isinstance(val, np.ndarray):
+            out[key] = val
+        elif key == "ks" and omid["fmt"] == "int4":
+            out[key] = val[b : b + 1]  # per-channel K scale [B,H,1,D]
+        else:
+            out[key] = val[b : b + 1, :, :lm]
+    return out
+
+
+@pytest.mark.parametrize("fmt", ["int4", "asym42"])
+@pytest.mark.parametrize("n_splits", [0, 1, 7])
+def test_tiered_decode_ragged_lens(dev, fmt, n_splits):
+    """Per-row tier lengths (ragged batch): row b attends to the first lens[b] rows of
+    each padded tier; each row is checked against the oracle over its own tokens."""
+    print(f"case decode ragged {fmt} n_splits={n_splits}", flush=True)
+    ns_c, mc, nr_c = 4, 600, 64
+    S = ns_c + mc + nr_c
+    B = 5
+    q, k, v, _, _ = _case(B, 16, 4, S, ns_c, nr_c, seed=77)
+    if fmt == "int4":
+        mid, omid = _int4_mid(dev, k, v, ns_c, nr_c)
+    else:
+        mid, omid = _asym_mid(dev, k, v, ns_c, nr_c, 4, 2)
+    lens = np.array([[4, 600, 64], [2, 130, 17], [4, 1, 0], [0, 333, 64], [1, 0, 5]], dtype=np.int32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    sink = (t(k[:, :, :ns_c]), t(v[:, :, :ns_c]))
+    rec = (t(k[:, :, S - nr_c :]), t(v[:, :, S - nr_c :]))
+    out = tiered_decode_attention(t(q), sink, mid, rec, lens=t(lens), n_splits=n_splits).float().cpu().numpy()
+    for b, (ls, lm, lr) in enumerate(lens):
+        ref = oatt.tiered_decode(
+            q[b : b + 1], k[b : b + 1, :, :ls], v[b : b + 1, :, :ls], _row_slice_mid(omid, b, lm),
+            k[b : b + 1, :, S - nr_c : S - nr_c + lr], v[b : b + 1, :, S - nr_c : S - nr_c + lr],
+        )
+        err = np.abs(out[b : b + 1] - ref).max()
+        assert err <= ATOL, (b, err)
+
+
+def test_tiered_decode_ragged_lens_rejected_on_other_kernels(dev):
+    """Per-row lengths are a matrix-core INT4 kernel feature; the portable kernel refuses them."""
+    q, k, v, ns, nr = _case(1, 8, 4, 200, 4, 16, seed=3)
+    mid, _ = _int4_mid(dev, k, v, ns, nr)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    lens = torch.tensor([[4, 100, 16]], dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError, match="per-row lengths"):
+        tiered_decode_attention(t(q), (t(k[:, :, :4]), t(v[:, :, :4])), mid, (t(k[:, :, 184:]), t(v[:, :, 184:])),
+                                lens=lens, kernel=1)
