@@ -66,6 +66,8 @@ class MidTier(ctypes.Structure):
         ("v_codes", _p),
         ("v_scale", _p),
         ("v_zero", _p),
+        ("pages", _p),
+        ("pages_per_row", _i64),
     ]
 
 

@@ -94,6 +94,13 @@ int validate(const fade_decode_args* a) {
       default:
         return einval("fade_tiered_decode_attn: unknown middle format %d", m.fmt);
     }
+    if (m.pages != nullptr) {
+      if (m.fmt != FADE_MID_SYM && m.fmt != FADE_MID_ASYM)
+        return einval("fade_tiered_decode_attn: paged middle tiers are FADE_MID_SYM or FADE_MID_ASYM");
+      if (m.pages_per_row < cdiv(m.len, 64))
+        return einval("fade_tiered_decode_attn: pages_per_row=%lld < %lld tiles of the middle tier",
+                      (long long)m.pages_per_row, (long long)cdiv(m.len, 64));
+    }
   }
   if (a->kernel < 0 || a->kernel > 3) return einval("fade_tiered_decode_attn: kernel must be 0, 1, 2 or 3");
   return FADE_OK;
@@ -133,6 +140,8 @@ Params to_params(const fade_decode_args* a) {
   p.mid.v_codes = static_cast<const uint8_t*>(m.v_codes);
   p.mid.v_scale = static_cast<const uint16_t*>(m.v_scale);
   p.mid.v_zero = static_cast<const uint16_t*>(m.v_zero);
+  p.mid.pages = m.pages;
+  p.mid.pages_per_row = m.pages_per_row;
   p.total = total_tokens(a);
   p.lens = a->lens;
   return p;
@@ -165,6 +174,8 @@ Plan make_plan(const fade_decode_args* a, const Params& p) {
     int64_t want = a->n_splits > 0 ? a->n_splits : (int4_resident_wgs(p) + pairs / 2) / pairs;
     if (want > nT) want = nT;
     if (want < 1) want = 1;
+    // paged middle tier: a split's page ids fit the workgroup's kPageSlots
+    if (p.mid.pages != nullptr && want < cdiv(nT, kPageSlots)) want = cdiv(nT, kPageSlots);
     pl.tiles_per_split = cdiv(nT, want);
     pl.n = cdiv(nT, pl.tiles_per_split);
     pl.n_f16_tiles = int4_fp16_tiles(p);
@@ -197,9 +208,9 @@ FADE_API int fade_tiered_decode_attn(const fade_decode_args* a, void* stream) {
   if ((a->kernel == 2 || a->kernel == 3) && pl.k == Kern::kValu)
     return einval("fade_tiered_decode_attn: the matrix-core kernels do not handle this middle tier (format %d)",
                   p.mid.fmt);
-  if (a->lens != nullptr && pl.k != Kern::kInt4)
-    return einval("fade_tiered_decode_attn: per-row lengths need the matrix-core INT4 kernel "
-                  "(middle tier FADE_MID_SYM or FADE_MID_ASYM, GQA <= 4)");
+  if ((a->lens != nullptr || a->mid.pages != nullptr) && pl.k != Kern::kInt4)
+    return einval("fade_tiered_decode_attn: per-row lengths and paged middle tiers need the matrix-core INT4 "
+                  "kernel (middle tier FADE_MID_SYM or FADE_MID_ASYM, GQA <= 4)");
   const WsLayout ws = ws_layout(a, pl.n);
   if (a->workspace == nullptr || a->workspace_bytes < ws.total)
     return einval("fade_tiered_decode_attn: workspace too small (%lld < %lld bytes)",

@@ -26,7 +26,12 @@ struct MidTier {
   const uint8_t* v_codes;
   const uint16_t* v_scale;
   const uint16_t* v_zero;
+  const int32_t* pages;  // optional [B][pages_per_row] page of each 64-token tile (paged pools)
+  int64_t pages_per_row;
 };
+
+// Page slots a workgroup of the INT4 kernel holds (its split's middle tiles).
+constexpr int kPageSlots = 256;
 
 struct Params {
   int64_t B, Hq, Hkv;

@@ -224,16 +224,31 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   __shared__ float red_m[kWaves][4], red_l[kWaves][4];
   __shared__ int last_s;
 
-  const uint8_t* kc = p.mid.k_codes + bkv * Mc * kRowK;
+  // Paged middle tier: per-token tensors are pools [page][Hkv][64][...] and
+  // the split's page ids (middle tiles mt_lo .. of this row) sit in LDS, read
+  // with plain loads before any tile DMA is in flight.  Unpaged: the row's
+  // block of Mc token rows.
+  const bool paged = !LIT && p.mid.pages != nullptr;
+  __shared__ int32_t pages_s[kPageSlots];
+  const int64_t mt_lo = (t0 > nFt ? t0 : nFt) - nFt;
+  if (paged) {
+    const int64_t mt_hi = (t1 > nFt ? t1 : nFt) - nFt;
+    const int64_t cnt = mt_hi - mt_lo < kPageSlots ? mt_hi - mt_lo : kPageSlots;
+    for (int64_t i = tid; i < cnt; i += kThreads) pages_s[i] = p.mid.pages[b * p.mid.pages_per_row + mt_lo + i];
+    __syncthreads();
+  }
+  const int64_t rb0 = paged ? 0 : bkv * Mc;  // token-row base of the row's block
+  const uint8_t* kc = p.mid.k_codes + rb0 * kRowK;
   // literal INT2 V: [v_rows][128] int8 codes and [v_rows / 64][128] scales per
   // (batch row, kv head), v_rows = the middle length padded to 64 (pad rows are 0)
-  const uint8_t* vc = p.mid.v_codes + bkv * (LIT ? p.mid.v_rows : Mc) * kRowV;
+  const uint8_t* vc = p.mid.v_codes + (LIT ? bkv * p.mid.v_rows : rb0) * kRowV;
   // reference formats: V scale per token; asymmetric: [token][4 groups] scale / zero
   const uint16_t* vsg =
-      LIT ? p.mid.v_scale + bkv * (p.mid.v_rows / kTile) * kD : p.mid.v_scale + bkv * Mc * (ASYM ? kGroups : 1);
-  const uint16_t* ksg = ASYM ? p.mid.k_scale + bkv * Mc * kGroups : nullptr;
-  const uint16_t* kzg = ASYM ? p.mid.k_zero + bkv * Mc * kGroups : nullptr;
-  const uint16_t* vzg = ASYM ? p.mid.v_zero + bkv * Mc * kGroups : nullptr;
+      LIT ? p.mid.v_scale + bkv * (p.mid.v_rows / kTile) * kD : p.mid.v_scale + rb0 * (ASYM ? kGroups : 1);
+  const uint16_t* ksg = ASYM ? p.mid.k_scale + rb0 * kGroups : nullptr;
+  const uint16_t* kzg = ASYM ? p.mid.k_zero + rb0 * kGroups : nullptr;
+  const uint16_t* vzg = ASYM ? p.mid.v_zero + rb0 * kGroups : nullptr;
+  const int64_t Hkv = p.Hkv;
   // fp16 tiers as (uniform) locals: the lambdas below must not read the kernel
   // arguments through a pointer (that becomes a per-lane global load whose
   // compiler-inserted vmcnt wait would also wait for the tile prefetches).
@@ -273,9 +288,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   }
   auto issue = [&](int64_t tt, uint32_t st) {
     if (tt >= nFt) {
-      const int64_t m0 = (tt - nFt) * kTile;
-      const uint8_t* kb = kc + m0 * kRowK;
-      const uint8_t* vb = vc + m0 * kRowV;
+      const int64_t m0 = (tt - nFt) * kTile;  // the tile's first token of the row's middle
+      int64_t r0 = m0;                        // its first row in the tensors
+      if (paged) {
+        const int64_t slot = tt - nFt - mt_lo;
+        r0 = (static_cast<int64_t>(pages_s[slot < kPageSlots ? slot : kPageSlots - 1]) * Hkv + kvh) * kTile;
+      }
+      const uint8_t* kb = kc + r0 * kRowK;
+      const uint8_t* vb = vc + r0 * kRowV;
       const int lim = m0 + kTile > M ? static_cast<int>(M - 1 - m0) : kTile - 1;
       if (KB == 4) {
         uint32_t ko[4] = {koff[0], koff[1], koff[2], koff[3]};
@@ -332,16 +352,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         for (int k = 0; k < 2; ++k) {
           const int r = 32 * k + (lane >> 1);
           const uint32_t o = 8u * (r < lim ? r : lim) + 4u * (lane & 1);
-          lds_dma4(ksg + 4 * m0, o, st + kMeta + 256 * k);
-          lds_dma4(kzg + 4 * m0, o, st + kMeta + 512 + 256 * k);
-          lds_dma4(vsg + 4 * m0, o, st + kMeta + 1024 + 256 * k);
-          lds_dma4(vzg + 4 * m0, o, st + kMeta + 1536 + 256 * k);
+          lds_dma4(ksg + 4 * r0, o, st + kMeta + 256 * k);
+          lds_dma4(kzg + 4 * r0, o, st + kMeta + 512 + 256 * k);
+          lds_dma4(vsg + 4 * r0, o, st + kMeta + 1024 + 256 * k);
+          lds_dma4(vzg + 4 * r0, o, st + kMeta + 1536 + 256 * k);
         }
       } else if constexpr (LIT) {
         lds_dma4(vsg + (m0 / kTile) * kD, 4u * lane, st + kMeta);  // the tile's scale row
       } else {
         const uint32_t so = 2u * (lane < lim ? lane : lim);
-        lds_dma2(vsg + m0, so, st + kMeta);
+        lds_dma2(vsg + r0, so, st + kMeta);
       }
     } else {
       const int64_t f0 = tt * kMini;

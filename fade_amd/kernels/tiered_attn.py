@@ -39,6 +39,11 @@ class MiddleTier:
     ``v_scale`` [B,Hkv,S_pad/group,D] (reference INT2-V, fade/cache.py:983-988).
     fmt ``"asym"``: codes [B,Hkv,S,D*bits/8], scale/zero [B,Hkv,S,D/group].
     fmt ``"fp16"``: ``k_codes``/``v_codes`` fp16 [B,Hkv,S,D].
+
+    Paged (``"int4"``/``"sym"``/``"asym"``, decode only): ``pages`` int32
+    [B, pages_per_row] holds the page of each 64-token tile of a row, and every
+    per-token tensor is a pool [n_pages, Hkv, 64, ...] (``paginate_middle``
+    builds one); ``length`` is the longest row's middle.
     """
 
     fmt: str
@@ -52,13 +57,15 @@ class MiddleTier:
     v_bits: int = 4
     group: int = 64
     length: int | None = None
+    pages: Tensor | None = None
 
     @property
     def n_tokens(self) -> int:
         return int(self.k_codes.shape[2]) if self.length is None else int(self.length)
 
     def tensors(self):
-        return [t for t in (self.k_codes, self.v_codes, self.k_scale, self.v_scale, self.k_zero, self.v_zero) if t is not None]
+        return [t for t in (self.k_codes, self.v_codes, self.k_scale, self.v_scale, self.k_zero, self.v_zero,
+                            self.pages) if t is not None]
 
 
 def _fp16_tier(kv: tuple[Tensor, Tensor] | None) -> _lib.Fp16Tier:
@@ -93,7 +100,58 @@ def _mid_tier(mid: MiddleTier | None) -> _lib.MidTier:
     m.k_codes, m.v_codes = mid.k_codes.data_ptr(), mid.v_codes.data_ptr()
     m.k_scale, m.v_scale = _lib.ptr(mid.k_scale), _lib.ptr(mid.v_scale)
     m.k_zero, m.v_zero = _lib.ptr(mid.k_zero), _lib.ptr(mid.v_zero)
+    if mid.pages is not None:
+        if mid.length is None:
+            raise ValueError("a paged middle tier needs length (the longest row's middle)")
+        if mid.pages.dtype != torch.int32 or mid.pages.dim() != 2:
+            raise ValueError("pages must be int32 [B, pages_per_row]")
+        m.pages, m.pages_per_row = mid.pages.data_ptr(), int(mid.pages.shape[1])
     return m
+
+
+def paginate_middle(mid: MiddleTier, lens_mid, order=None) -> MiddleTier:
+    """A padded ``"int4"``/``"sym"``/``"asym"`` middle tier ([B, Hkv, S, ...] per token)
+    as a paged one: row b's ``lens_mid[b]`` tokens go to ``ceil(lens_mid[b] / 64)``
+    pages of one pool shared by the rows.  ``order`` (a permutation of the page
+    ids) places the pages anywhere in the pool; default: in row order."""
+    if mid.fmt not in ("int4", "sym", "asym") or mid.pages is not None:
+        raise ValueError("paginate_middle takes an unpaged int4 / sym / asym middle tier")
+    lens = [int(x) for x in lens_mid]
+    B, H, S = (int(d) for d in mid.k_codes.shape[:3])
+    if len(lens) != B or any(x < 0 or x > S for x in lens):
+        raise ValueError(f"lens_mid must give 0..{S} tokens for each of {B} rows")
+    counts = [-(-x // 64) for x in lens]
+    n_pages = max(1, sum(counts))
+    ppr = max(1, max(counts))
+    ids = torch.arange(n_pages) if order is None else torch.as_tensor(order, dtype=torch.long)
+    dev = mid.k_codes.device
+    table = torch.zeros(B, ppr, dtype=torch.int32)
+    src_b, src_t, dst = [], [], []
+    k = 0
+    for b, c in enumerate(counts):
+        for t in range(c):
+            table[b, t] = int(ids[k])
+            src_b.append(b)
+            src_t.append(t)
+            dst.append(int(ids[k]))
+            k += 1
+
+    def pool(x: Tensor | None) -> Tensor | None:
+        if x is None:
+            return x
+        pad = -(-S // 64) * 64 - S
+        xp = torch.nn.functional.pad(x, (0, 0, 0, pad)) if pad else x
+        tiles = xp.reshape(B, H, -1, 64, x.shape[-1])  # [B, H, tiles, 64, ...]
+        out = torch.zeros(n_pages, H, 64, x.shape[-1], dtype=x.dtype, device=dev)
+        if dst:
+            out[torch.tensor(dst, device=dev)] = tiles[torch.tensor(src_b, device=dev), :,
+                                                       torch.tensor(src_t, device=dev)]
+        return out
+
+    k_scale = mid.k_scale if mid.fmt != "asym" else pool(mid.k_scale)  # SYM K scale: per row [B,Hkv,1,D]
+    return MiddleTier(mid.fmt, pool(mid.k_codes), pool(mid.v_codes), k_scale, pool(mid.v_scale),
+                      pool(mid.k_zero), pool(mid.v_zero), k_bits=mid.k_bits, v_bits=mid.v_bits, group=mid.group,
+                      length=max(lens) if lens else 0, pages=table.to(dev))
 
 
 class TieredDecodePlan:
@@ -177,4 +235,4 @@ def tiered_decode_attention(
     return TieredDecodePlan(q, sink, mid, recent, sm_scale, n_splits=n_splits, kernel=kernel, lens=lens).run()
 
 
-__all__ = ["MiddleTier", "TieredDecodePlan", "tiered_decode_attention"]
+__all__ = ["MiddleTier", "TieredDecodePlan", "paginate_middle", "tiered_decode_attention"]

@@ -218,6 +218,14 @@ typedef struct fade_mid_tier {
   const void* v_codes;
   const void* v_scale;
   const void* v_zero;
+  /* Optional paged layout (decode only; FADE_MID_SYM or FADE_MID_ASYM): pages
+   * is device int32 [B][pages_per_row], the page of each 64-token middle tile
+   * of a row.  Every per-token tensor (codes, SYM V scale, ASYM scale/zero) is
+   * then a pool [n_pages][Hkv][64][...] shared by the rows; the SYM K scale
+   * stays [B,Hkv,1,D].  len = the longest row's middle (per-row lengths come
+   * from the decode args' lens). */
+  const int32_t* pages;
+  int64_t pages_per_row;
 } fade_mid_tier;
 
 typedef struct fade_decode_args {

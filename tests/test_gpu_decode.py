@@ -323,3 +323,39 @@ def test_tiered_decode_ragged_lens_rejected_on_other_kernels(dev):
     with pytest.raises(ValueError, match="per-row lengths"):
         tiered_decode_attention(t(q), (t(k[:, :, :4]), t(v[:, :, :4])), mid, (t(k[:, :, 184:]), t(v[:, :, 184:])),
                                 lens=lens, kernel=1)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "asym42"])
+def test_tiered_decode_paged_middle(dev, fmt):
+    """Paged middle tier: rows' 64-token tiles scattered over a shared pool in a
+    shuffled order; the result equals the padded ragged layout bit for bit and the
+    oracle over each row's own tokens."""
+    from fade_amd.kernels.tiered_attn import paginate_middle
+
+    print(f"case decode paged {fmt}", flush=True)
+    ns_c, mc, nr_c = 4, 600, 64
+    S = ns_c + mc + nr_c
+    B = 5
+    q, k, v, _, _ = _case(B, 16, 4, S, ns_c, nr_c, seed=78)
+    if fmt == "int4":
+        mid, omid = _int4_mid(dev, k, v, ns_c, nr_c)
+    else:
+        mid, omid = _asym_mid(dev, k, v, ns_c, nr_c, 4, 2)
+    lens = np.array([[4, 600, 64], [2, 130, 17], [4, 1, 0], [0, 333, 64], [1, 0, 5]], dtype=np.int32)
+    n_pages = sum(-(-int(x) // 64) for x in lens[:, 1])
+    order = np.random.default_rng(0).permutation(n_pages)
+    paged = paginate_middle(mid, lens[:, 1], order=order)
+    assert paged.k_codes.shape[0] == n_pages  # the pool holds exactly the rows' pages
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    sink = (t(k[:, :, :ns_c]), t(v[:, :, :ns_c]))
+    rec = (t(k[:, :, S - nr_c :]), t(v[:, :, S - nr_c :]))
+    out_p = tiered_decode_attention(t(q), sink, paged, rec, lens=t(lens), n_splits=3)
+    out_r = tiered_decode_attention(t(q), sink, mid, rec, lens=t(lens), n_splits=3)
+    assert torch.equal(out_p, out_r)
+    out = out_p.float().cpu().numpy()
+    for b, (ls, lm, lr) in enumerate(lens):
+        ref = oatt.tiered_decode(
+            q[b : b + 1], k[b : b + 1, :, :ls], v[b : b + 1, :, :ls], _row_slice_mid(omid, b, lm),
+            k[b : b + 1, :, S - nr_c : S - nr_c + lr], v[b : b + 1, :, S - nr_c : S - nr_c + lr],
+        )
+        assert np.abs(out[b : b + 1] - ref).max() <= ATOL, b
