@@ -307,6 +307,36 @@ def prefill_case(dev, seed: int = 1004):
     return plan, flops, nbytes
 
 
+def ragged_decode_case(dev, seed: int = 1004):
+    """Config 4's batch decoding one token: 32 rows, L_b ~U[512, 16384], 32/8 heads, reference
+    INT4 middle (sink 4, recent 64).  Three layouts of the same tokens: per-row lengths over
+    padded tensors, a paged middle tier (64-token pages of one pool), and every row padded to
+    the longest (what a zero-padded per-sequence cache reads).  Bytes: each row's own tokens."""
+    from fade_amd.kernels import MiddleTier
+    from fade_amd.kernels.tiered_attn import paginate_middle
+
+    B, Hq, Hkv, D, ns, nr = 32, 32, 8, 128, 4, 64
+    gen = torch.Generator().manual_seed(seed)
+    L = torch.randint(512, 16385, (B,), generator=gen)
+    nm = L - ns - nr
+    cap = int(nm.max())
+    g = torch.Generator(device=dev).manual_seed(seed)
+    rnd = lambda *shape: torch.randn(*shape, generator=g, device=dev).to(torch.float16)  # noqa: E731
+    codes = lambda: torch.randint(0, 256, (B, Hkv, cap, D // 2), generator=g, device=dev, dtype=torch.uint8)  # noqa: E731
+    mid = MiddleTier("int4", codes(), codes(), rnd(B, Hkv, 1, D).abs() * 0.3 + 0.05, rnd(B, Hkv, cap, 1).abs() * 0.3 + 0.05)
+    sink, rec = (rnd(B, Hkv, ns, D), rnd(B, Hkv, ns, D)), (rnd(B, Hkv, nr, D), rnd(B, Hkv, nr, D))
+    q = rnd(B, Hq, 1, D)
+    lens = torch.stack([torch.full((B,), ns), nm, torch.full((B,), nr)], dim=1).to(torch.int32).to(dev)
+    paged = paginate_middle(mid, nm.tolist())
+    plans = {
+        "lens": TieredDecodePlan(q, sink, mid, rec, lens=lens),
+        "paged": TieredDecodePlan(q, sink, paged, rec, lens=lens),
+        "padded_to_max": TieredDecodePlan(q, sink, mid, rec),
+    }
+    nbytes = int(Hkv * (B * (ns + nr) * D * 4 + int(nm.sum()) * (D + 2) + B * 2 * D) + 2 * B * Hq * D * 2)
+    return plans, nbytes, int(paged.k_codes.shape[0])
+
+
 def cpu_baseline(cfg, seed: int):
     """The oracle's dequantize + concatenate + fp32 SDPA on a bounded sample (two batch rows)."""
     from oracle import attention as oatt
@@ -483,6 +513,16 @@ def main() -> int:
         extra["c3_rerope_gather"] = {"us": round(rmean * 1e3, 2), "GBps": round(rbytes / (rmean * 1e-3) / 1e9, 1),
                                      "bytes": rbytes, "n_kept": n_kept}
         del rp
+        rplans, rdb, n_pages = ragged_decode_case(dev)
+        rd = {}
+        for name, plan in rplans.items():
+            _, _, rmean_d, _ = time_plans([plan], max(20, args.steps // 4), 5, stream)
+            rd[name] = round(rmean_d * 1e3, 2)
+        extra["c4_ragged_decode"] = {"us": rd, "bytes_own_tokens": rdb, "pool_pages": n_pages,
+                                     "GBps_lens": round(rdb / (rd["lens"] * 1e-6) / 1e9, 1),
+                                     "GBps_paged": round(rdb / (rd["paged"] * 1e-6) / 1e9, 1)}
+        del rplans
+        torch.cuda.empty_cache()
         ra = reassign_case(dev)
         extra["c3_reassign_layer_wall_us"] = {"device_path": ra["device"], "host_path": ra["host"],
                                               "speedup": round(ra["host"] / ra["device"], 2)}

@@ -126,6 +126,7 @@ class ReassignArgs(ctypes.Structure):
     _fields_ = [
         ("B", _i64), ("H", _i64), ("D", _i64), ("S", _i64),
         ("n_sink_old", _i64), ("n_mid_old", _i64),
+        ("src_lens", _p), ("plan_rows", _i64), ("pos_old_rs", _i64), ("n_rec_cap", _i64),
         ("sink_k", _p), ("sink_v", _p), ("sink_sb", _i64), ("sink_sh", _i64), ("sink_ss", _i64),
         ("mid_kq", _p), ("mid_ks", _p), ("mid_vq", _p), ("mid_vs", _p),
         ("rec_k", _p), ("rec_v", _p), ("rec_sb", _i64), ("rec_sh", _i64), ("rec_ss", _i64),
@@ -162,7 +163,7 @@ _SIGNATURES: dict[str, list] = {
     ],
     "fade_tiered_decode_workspace_bytes": [ctypes.POINTER(DecodeArgs), _pi64],
     "fade_tiered_decode_attn": [ctypes.POINTER(DecodeArgs), _p],
-    "fade_reassign_plan": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    "fade_reassign_plan": [_p, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p],
     "fade_reassign_gather": [ctypes.POINTER(ReassignArgs), _p],
     "fade_tiered_prefill_attn": [ctypes.POINTER(PrefillArgs), _p],
 }

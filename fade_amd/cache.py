@@ -91,8 +91,15 @@ class LayerState:
     backend_v: dict | None = None
     backend_pos: Tensor | None = None
     _compressed_bytes: int = 0
+    # ragged layout (TieredKVCache.ragged_layout): per-row tier lengths, device
+    # int32 [B, 3] (sink, middle, recent) and its host mirror; the tier tensors
+    # are padded capacities and row b's token j (position order) sits at position j
+    lens: Tensor | None = None
+    lens_host: list | None = None
 
     def total_seq_length(self) -> int:
+        if self.lens_host is not None:
+            return max((sum(r) for r in self.lens_host), default=0)
         return sum(
             int(p.shape[0])
             for p in (self.sink_pos, self.fp16_pos, self.int4_pos, self.int2_pos, self.backend_pos)
@@ -159,6 +166,10 @@ class TieredKVCache(DynamicCache):
         self.fused = False
         # apply_tier_assignment on the device for the reference INT4 layout
         self.device_reassign = True
+        # apply_tier_assignment_per_sequence keeps each row's own tokens (per-row
+        # tier lengths, attention over them only) instead of the reference's
+        # zero-padded rows (fade/cache.py:1145-1159)
+        self.ragged_layout = False
         self._last_reassign_counts = None
 
     # transformers 5.x defines a read-only ``Cache.batch_size``; the tiered cache
@@ -262,6 +273,8 @@ class TieredKVCache(DynamicCache):
 
     def cache_state_dict(self) -> dict:
         """Essential compressed form, on the CPU, same keys as fade/cache.py:510-534."""
+        if any(st.lens is not None for st in self._layers):
+            raise NotImplementedError("cache_state_dict: the ragged layout has no reference checkpoint form")
         sd: dict = {
             "n_layers": len(self._layers),
             "n_sink": self.n_sink,
@@ -330,9 +343,40 @@ class TieredKVCache(DynamicCache):
         while len(self._layers) <= layer_idx:
             self._layers.append(LayerState())
 
+    def _append_fp16_ragged(self, st: LayerState, k: Tensor, v: Tensor) -> None:
+        """Ragged layout: row b's new tokens go to its own recent slots lens[b, 2].. ."""
+        n = int(k.shape[-2])
+        B, H, _, D = k.shape
+        have = max(r[2] for r in st.lens_host)
+        cap = 0 if st._fp16_buf_k is None else int(st._fp16_buf_k.shape[-2])
+        if have + n > cap:
+            cap2 = max(2 * cap, have + n, DEFAULT_FP16_PREALLOC)
+            bk = torch.zeros(B, H, cap2, D, dtype=k.dtype, device=k.device)
+            bv = torch.zeros(B, H, cap2, D, dtype=v.dtype, device=v.device)
+            if cap:
+                bk[:, :, :cap] = st._fp16_buf_k
+                bv[:, :, :cap] = st._fp16_buf_v
+            st._fp16_buf_k, st._fp16_buf_v = bk, bv
+        rows = torch.arange(B, device=k.device)
+        for i in range(n):
+            slot = st.lens[:, 2].long() + i
+            st._fp16_buf_k[rows, :, slot] = k[:, :, i]
+            st._fp16_buf_v[rows, :, slot] = v[:, :, i]
+        st.lens[:, 2] += n
+        for r in st.lens_host:
+            r[2] += n
+        top = max(r[2] for r in st.lens_host)
+        st._fp16_len = top
+        st.fp16_k, st.fp16_v = st._fp16_buf_k[:, :, :top], st._fp16_buf_v[:, :, :top]
+        st.next_position = max(st.next_position, st.total_seq_length())
+        st._dequant_age += 1
+
     def _append_fp16(self, k: Tensor, v: Tensor, layer_idx: int) -> None:
         """Append to the doubling fp16 buffer (fade/cache.py:608-670)."""
         st = self._layers[layer_idx]
+        if st.lens is not None:
+            self._append_fp16_ragged(st, k, v)
+            return
         n = int(k.shape[-2])
         new_pos = torch.arange(st.next_position, st.next_position + n, device=k.device)
         st.next_position += n
@@ -375,7 +419,34 @@ class TieredKVCache(DynamicCache):
         st.fp16_pos = st._fp16_buf_pos[:ln]
         st._dequant_age += 1
 
+    def _materialize_ragged(self, st: LayerState) -> tuple[Tensor, Tensor]:
+        """Ragged layout: row b = its sink | middle | recent tokens, zero-padded at the end
+        to the longest row."""
+        ref = st.fp16_k if st.fp16_k is not None else (st.sink_k if st.sink_k is not None else None)
+        if st.int4_kq is not None:
+            mk, mv = self._get_int4_dequant(st)
+            ref = mk if ref is None else ref
+        B, H, _, D = ref.shape
+        top = st.total_seq_length()
+        ko = torch.zeros(B, H, top, D, dtype=self.dtype, device=ref.device)
+        vo = torch.zeros_like(ko)
+        for b, (ls, lm, lr) in enumerate(st.lens_host):
+            parts = []
+            if ls:
+                parts.append((st.sink_k[b, :, :ls], st.sink_v[b, :, :ls]))
+            if lm:
+                parts.append((mk[b, :, :lm], mv[b, :, :lm]))
+            if lr:
+                parts.append((st.fp16_k[b, :, :lr], st.fp16_v[b, :, :lr]))
+            if parts:
+                n = ls + lm + lr
+                ko[b, :, :n] = torch.cat([p[0] for p in parts], dim=-2)
+                vo[b, :, :n] = torch.cat([p[1] for p in parts], dim=-2)
+        return ko, vo
+
     def _materialize(self, layer_idx: int) -> tuple[Tensor, Tensor]:
+        if self._layers[layer_idx].lens is not None:
+            return self._materialize_ragged(self._layers[layer_idx])
         ks, vs = self._assemble_parts(self._layers[layer_idx], want_positions=False)
         if not ks:
             raise RuntimeError(f"No cache state for layer {layer_idx}")
@@ -596,9 +667,9 @@ class TieredKVCache(DynamicCache):
         pos_new = torch.empty(3, max(S, 1), dtype=torch.long, device=dev)
         cnt = torch.empty(4, dtype=torch.int32, device=dev)
         stream = _lib.stream_of(tiers_d)
-        _lib.call("fade_reassign_plan", tiers_d.data_ptr(), S, self.n_sink, pos_old.data_ptr(), dst.data_ptr(),
-                  newpos.data_ptr(), src_of.data_ptr(), pos_new[0].data_ptr(), pos_new[1].data_ptr(),
-                  pos_new[2].data_ptr(), cnt.data_ptr(), stream)
+        _lib.call("fade_reassign_plan", tiers_d.data_ptr(), 0, 1, S, self.n_sink, pos_old.data_ptr(), 0,
+                  dst.data_ptr(), newpos.data_ptr(), src_of.data_ptr(), pos_new[0].data_ptr(),
+                  pos_new[1].data_ptr(), pos_new[2].data_ptr(), cnt.data_ptr(), stream)
         if counts is None:
             c = cnt.cpu().tolist()  # the one host sync: tiers were on the device
             if c[3] != 0:
@@ -625,6 +696,7 @@ class TieredKVCache(DynamicCache):
         a = _lib.ReassignArgs()
         a.B, a.H, a.D, a.S = B, H, D, S
         a.n_sink_old, a.n_mid_old = ns_old, nm_old
+        a.plan_rows = 1
         if sink is not None:
             a.sink_k, a.sink_v = sink[0].data_ptr(), sink[1].data_ptr()
             a.sink_sb, a.sink_sh, a.sink_ss = sink[0].stride()[:3]
@@ -696,6 +768,8 @@ class TieredKVCache(DynamicCache):
         """
         del scores
         st = self._layers[layer_idx]
+        if st.lens is not None:
+            raise NotImplementedError("this layer holds the ragged layout: use apply_tier_assignment_per_sequence")
         if self._device_reassign_ok(st) and self._apply_tier_assignment_device(layer_idx, tiers, counts):
             return
         k_full, v_full, pos_full = self._all_in_position_order(layer_idx)
@@ -753,10 +827,162 @@ class TieredKVCache(DynamicCache):
         st._compressed_bytes = self._layer_compressed_bytes(st)
         st.sink_count = 0 if st.sink_pos is None else int(st.sink_pos.shape[0])
 
-    def apply_tier_assignment_per_sequence(self, layer_idx: int, tiers_per_row: Tensor, scores=None) -> None:
-        """Per-row tiers ``[B, S]`` with zero-padding to the longest row (fade/cache.py:1059-1230)."""
-        del scores
+    def _apply_per_sequence_ragged(self, layer_idx: int, tiers_per_row: Tensor) -> None:
+        """Per-row tiers ``[B, S]`` into the ragged layout: each row keeps exactly its own
+        tokens (per-row tier lengths in ``LayerState.lens``), re-RoPE'd to positions
+        0..n_kept-1 where it evicted.  One plan per row (``fade_reassign_plan``), one
+        gather of every row's kept tokens (``fade_reassign_gather``), then the INT4
+        quantizers over the zero-padded middle (per (row, head) channel scales over
+        the row's own tokens)."""
         st = self._layers[layer_idx]
+        if not isinstance(self._quant_backend, SymmetricINT4Backend) or self.middle_v_bits != 4 \
+                or st.int2_kq is not None or st.backend_k is not None:
+            raise NotImplementedError("ragged_layout: the reference INT4 middle tier only (no INT2 tier / backend)")
+        if st.lens is None:
+            if st.sink_k is not None:
+                sink, rec_start = (st.sink_k, st.sink_v), 0
+            else:
+                nsk = st.sink_count if st.fp16_k is not None else 0
+                sink = (st.fp16_k[..., :nsk, :], st.fp16_v[..., :nsk, :]) if nsk > 0 else None
+                rec_start = nsk
+            rec = None
+            if st.fp16_k is not None and rec_start < int(st.fp16_k.shape[-2]):
+                rec = (st.fp16_k[..., rec_start:, :], st.fp16_v[..., rec_start:, :])
+            ns_c = 0 if sink is None else int(sink[0].shape[-2])
+            nm_c = 0 if st.int4_kq is None else int(st.int4_kq.shape[-2])
+            nr_c = 0 if rec is None else int(rec[0].shape[-2])
+            S = ns_c + nm_c + nr_c
+            pos_parts = [p for p in (
+                None if sink is None else (st.sink_pos if st.sink_k is not None else st.fp16_pos[:ns_c]),
+                st.int4_pos, None if rec is None else st.fp16_pos[rec_start:],
+            ) if p is not None]
+            pos_old = torch.cat(pos_parts).to(torch.long).contiguous()
+            table_rows = st.next_position
+            row_len = None
+        else:
+            sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
+            rec = None if st.fp16_k is None else (st.fp16_k, st.fp16_v)
+            ns_c = 0 if sink is None else int(sink[0].shape[-2])
+            nm_c = 0 if st.int4_kq is None else int(st.int4_kq.shape[-2])
+            nr_c = 0 if rec is None else int(rec[0].shape[-2])
+            row_len = [sum(r) for r in st.lens_host]
+            S = max(row_len)
+            table_rows = S
+        ref = next(t for t in (None if sink is None else sink[0], None if rec is None else rec[0], st.int4_kq)
+                   if t is not None)
+        B, H = int(ref.shape[0]), int(ref.shape[1])
+        D = 2 * int(ref.shape[-1]) if ref is st.int4_kq else int(ref.shape[-1])
+        dev = ref.device
+        if st.lens is not None:
+            pos_old = torch.arange(max(S, 1), dtype=torch.long, device=dev)
+        if tiers_per_row.dim() != 2 or tiers_per_row.shape[0] != B:
+            raise ValueError(f"tiers_per_row must be [B={B}, S={S}], got {tuple(tiers_per_row.shape)}")
+        if tiers_per_row.shape[1] != S:
+            raise ValueError(f"tiers_per_row S dim {tiers_per_row.shape[1]} != cache length {S}")
+        rows_counts = None
+        if tiers_per_row.device.type == "cpu":
+            t = tiers_per_row.to(torch.long)
+            rows_counts = []
+            for b in range(B):
+                if row_len is not None and bool((t[b, row_len[b]:] != TIER_EVICT).any()):
+                    raise ValueError(f"row {b} has {row_len[b]} tokens; tiers past them must be TIER_EVICT")
+                c = self._host_tier_counts(t[b])
+                if c is None or c[2] > 0:
+                    raise NotImplementedError("ragged_layout: tiers must be FP16, INT4 or EVICT")
+                rows_counts.append(c)
+        tiers_d = tiers_per_row.to(dtype=torch.long).contiguous()
+        if tiers_d.device != dev:
+            tiers_d = (tiers_d.pin_memory() if tiers_d.device.type == "cpu" else tiers_d).to(dev, non_blocking=True)
+        i32 = dict(dtype=torch.int32, device=dev)
+        dst, newpos, src_of = (torch.empty(B, max(S, 1), **i32) for _ in range(3))
+        pos_new = torch.empty(3, B, max(S, 1), dtype=torch.long, device=dev)
+        cnt = torch.empty(B, 4, **i32)
+        stream = _lib.stream_of(tiers_d)
+        _lib.call("fade_reassign_plan", tiers_d.data_ptr(), S, B, S, self.n_sink, pos_old.data_ptr(), 0,
+                  dst.data_ptr(), newpos.data_ptr(), src_of.data_ptr(), pos_new[0].data_ptr(),
+                  pos_new[1].data_ptr(), pos_new[2].data_ptr(), cnt.data_ptr(), stream)
+        if rows_counts is None:
+            c = cnt.cpu().tolist()  # device tiers: one read of the per-row counts
+            if any(r[3] & 3 for r in c):
+                raise NotImplementedError("ragged_layout: tiers must be FP16, INT4 or EVICT")
+            rows_counts = [(r[0], r[1], 0) for r in c]
+        new_lens = [[min(self.n_sink, f), i4, f - min(self.n_sink, f)] for f, i4, _ in rows_counts]
+        cs = max(r[0] for r in new_lens)
+        cm = max(r[1] for r in new_lens)
+        cr = max(r[2] for r in new_lens)
+        kd = dict(dtype=torch.float16, device=dev)
+        out_sink = (torch.zeros(B, H, cs, D, **kd), torch.zeros(B, H, cs, D, **kd)) if cs else None
+        cap = max(DEFAULT_FP16_PREALLOC, cr)
+        buf = (torch.zeros(B, H, cap, D, **kd), torch.zeros(B, H, cap, D, **kd))
+        mid = (torch.zeros(B, H, cm, D, **kd), torch.zeros(B, H, cm, D, **kd)) if cm else None
+        evicting = any(f + i4 < (S if row_len is None else row_len[b]) for b, (f, i4, _) in enumerate(rows_counts))
+        tab = self._rope_tables(max(table_rows, S), dev) if evicting else None
+        src_lens = st.lens
+
+        def cf(tt):
+            return tt if tt[0].stride() == tt[1].stride() else (tt[0].contiguous(), tt[1].contiguous())
+
+        sink = None if sink is None else cf(sink)
+        rec = None if rec is None else cf(rec)
+        a = _lib.ReassignArgs()
+        a.B, a.H, a.D, a.S = B, H, D, S
+        a.n_sink_old, a.n_mid_old, a.n_rec_cap = ns_c, nm_c, nr_c
+        a.src_lens, a.plan_rows, a.pos_old_rs = _lib.ptr(src_lens), B, 0
+        if sink is not None:
+            a.sink_k, a.sink_v = sink[0].data_ptr(), sink[1].data_ptr()
+            a.sink_sb, a.sink_sh, a.sink_ss = sink[0].stride()[:3]
+        if nm_c:
+            mids = [t.contiguous() for t in (st.int4_kq, st.int4_ks, st.int4_vq, st.int4_vs)]
+            a.mid_kq, a.mid_ks, a.mid_vq, a.mid_vs = (t.data_ptr() for t in mids)
+        if rec is not None:
+            a.rec_k, a.rec_v = rec[0].data_ptr(), rec[1].data_ptr()
+            a.rec_sb, a.rec_sh, a.rec_ss = rec[0].stride()[:3]
+        a.dst, a.newpos, a.src_of, a.rows = dst.data_ptr(), newpos.data_ptr(), src_of.data_ptr(), S
+        a.counts, a.pos_old = cnt.data_ptr(), pos_old.data_ptr()
+        if tab is not None:
+            a.cos_tab, a.sin_tab, a.table_rows = tab[0].data_ptr(), tab[1].data_ptr(), int(tab[0].shape[0])
+        if out_sink is not None:
+            a.out_sink_k, a.out_sink_v, a.cap_sink = out_sink[0].data_ptr(), out_sink[1].data_ptr(), cs
+        a.out_rec_k, a.out_rec_v = buf[0].data_ptr(), buf[1].data_ptr()
+        a.out_rec_sb, a.out_rec_sh, a.out_rec_ss = buf[0].stride()[:3]
+        a.cap_rec = cap
+        if mid is not None:
+            a.out_mid_k, a.out_mid_v, a.cap_mid = mid[0].data_ptr(), mid[1].data_ptr(), cm
+        _lib.check(_lib.load().fade_reassign_gather(ctypes.byref(a), stream), "fade_reassign_gather")
+
+        st.sink_k, st.sink_v = (out_sink[0], out_sink[1]) if out_sink is not None else (None, None)
+        st._fp16_buf_k, st._fp16_buf_v, st._fp16_buf_pos = buf[0], buf[1], None
+        st._fp16_len = cr
+        st.fp16_k, st.fp16_v = buf[0][:, :, :cr], buf[1][:, :, :cr]
+        if mid is not None:
+            st.int4_kq, st.int4_ks = quant_k_int4(mid[0])
+            st.int4_vq, st.int4_vs = quant_v_int4(mid[1])
+        else:
+            st.int4_kq = st.int4_vq = st.int4_ks = st.int4_vs = None
+        st.sink_pos = st.fp16_pos = st.int4_pos = None
+        st.backend_k = st.backend_v = st.backend_pos = None
+        st.int2_kq = st.int2_vq = st.int2_ks = st.int2_vs = st.int2_pos = None
+        st.int2_actual_count = 0
+        st.lens = torch.tensor(new_lens, dtype=torch.int32).pin_memory().to(dev, non_blocking=True)
+        st.lens_host = new_lens
+        st.next_position = st.total_seq_length()
+        st.sink_count = cs
+        st.int4_k_deq = st.int4_v_deq = st.int2_k_deq = st.int2_v_deq = None
+        st._compressed_bytes = self._layer_compressed_bytes(st)
+        self._last_reassign_counts = cnt
+
+    def apply_tier_assignment_per_sequence(self, layer_idx: int, tiers_per_row: Tensor, scores=None) -> None:
+        """Per-row tiers ``[B, S]`` with zero-padding to the longest row (fade/cache.py:1059-1230).
+
+        With ``ragged_layout`` set, rows keep exactly their own tokens instead
+        (``_apply_per_sequence_ragged``) and attention reads only those."""
+        del scores
+        if self.ragged_layout:
+            self._apply_per_sequence_ragged(layer_idx, tiers_per_row)
+            return
+        st = self._layers[layer_idx]
+        if st.lens is not None:
+            raise NotImplementedError("this layer holds the ragged layout; set ragged_layout to reassign it")
         k_full, v_full, pos_full = self._all_in_position_order(layer_idx)
         B, H, _, D = k_full.shape
         S = int(pos_full.shape[0])
@@ -847,6 +1073,8 @@ class TieredKVCache(DynamicCache):
         from .kernels.tiered_attn import MiddleTier
 
         st = self._layers[layer_idx]
+        if st.lens is not None:
+            raise NotImplementedError("prefill_attention: a chunk over the ragged layout is not supported")
         Sq = int(q.shape[2])
         sink, rest = self._fp16_split(st)
         if rest is None or int(rest[0].shape[-2]) < Sq:
@@ -874,6 +1102,17 @@ class TieredKVCache(DynamicCache):
         from .kernels.tiered_attn import MiddleTier, tiered_decode_attention
 
         st = self._layers[layer_idx]
+        if st.lens is not None:
+            if st.int4_kq is not None:
+                mid = MiddleTier("int4", st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs)
+            else:  # the ragged kernel needs a middle format: one zero row no row reads (lens 0)
+                B, H = int(q.shape[0]), int((st.fp16_k if st.fp16_k is not None else st.sink_k).shape[1])
+                z8 = torch.zeros(B, H, 1, 64, dtype=torch.uint8, device=q.device)
+                mid = MiddleTier("int4", z8, z8.clone(), torch.zeros(B, H, 1, 128, dtype=torch.float16, device=q.device),
+                                 torch.zeros(B, H, 1, 1, dtype=torch.float16, device=q.device))
+            sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
+            recent = None if st.fp16_k is None or st.fp16_k.shape[-2] == 0 else (st.fp16_k, st.fp16_v)
+            return tiered_decode_attention(q, sink, mid, recent, sm_scale, lens=st.lens)
         if st.int2_kq is not None:
             raise RuntimeError("decode_attention: the INT2 tier is not read by the fused kernel; use update()")
         if st.sink_k is not None:

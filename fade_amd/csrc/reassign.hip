@@ -7,7 +7,7 @@
 // survivors with three more nonzero() calls (each a host sync) and
 // requantizes the middle tier.  Here:
 //
-//   plan    one workgroup scans tiers[S] (two passes over per-thread runs and
+//   plan    one workgroup per row of tiers scans it (two passes over per-thread runs and
 //           one block scan) and writes, per source token j, its destination
 //           (sink / recent / middle slot) and its rank among the kept
 //           tokens, the new position arrays and the tier counts;
@@ -62,8 +62,9 @@ __device__ __forceinline__ uint64_t block_exclusive_scan(uint64_t v, uint64_t* w
 
 // counts = {n_fp16, n_int4, n_kept, status}; status bit 0: an INT2 token,
 // bit 1: a value outside {FP16, INT4, INT2, EVICT}.
-__global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int64_t* __restrict__ tiers, int64_t S,
-                                                            int64_t n_sink, const int64_t* __restrict__ pos_old,
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int64_t* __restrict__ tiers, int64_t tiers_rs,
+                                                            int64_t S, int64_t n_sink,
+                                                            const int64_t* __restrict__ pos_old, int64_t pos_old_rs,
                                                             int32_t* __restrict__ dst, int32_t* __restrict__ newpos,
                                                             int32_t* __restrict__ src_of,
                                                             int64_t* __restrict__ pos_sink,
@@ -72,6 +73,16 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int64_t* __res
   __shared__ uint64_t wtot[kPlanWaves];
   __shared__ uint64_t total_s;
   __shared__ int status_s;
+  // one workgroup per plan row (batch row of a per-row assignment)
+  const int64_t row = blockIdx.x;
+  tiers += row * tiers_rs;
+  dst += row * S;
+  newpos += row * S;
+  src_of += row * S;
+  pos_sink += row * S;
+  pos_recent += row * S;
+  pos_mid += row * S;
+  counts += 4 * row;
   if (threadIdx.x == 0) status_s = 0;
   const int64_t per = (S + kPlanThreads - 1) / kPlanThreads;
   const int64_t j0 = static_cast<int64_t>(threadIdx.x) * per;
@@ -99,7 +110,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const int64_t* __res
     if (v == kTierFp16 || v == kTierInt4) {
       np = static_cast<int32_t>(f + m);
       src_of[f + m] = static_cast<int32_t>(j);
-      const int64_t p = evicted ? f + m : pos_old[j];
+      const int64_t p = evicted ? f + m : pos_old[pos_old_rs * row + j];
       if (v == kTierFp16) {
         if (f < n_sink) {
           d = static_cast<int32_t>(f);
@@ -135,26 +146,44 @@ __device__ __forceinline__ float nib(uint32_t byte, bool high) {
 // One thread per (kept token, channel pair i, i + D/2) of one (b, h); the
 // grid covers `rows` kept ranks (the host's count, or S when it has none).
 __global__ __launch_bounds__(256) void gather_kernel(FadeReassignArgs a) {
-  int32_t* status = a.counts + 3;
   const int D = static_cast<int>(a.D), half = D / 2;
   const int rows_per_block = blockDim.x / half;
   const int i = threadIdx.x % half;
   const int64_t rank = static_cast<int64_t>(blockIdx.x) * rows_per_block + threadIdx.x / half;
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / a.H, h = bh % a.H;
-  if (rank >= a.counts[2] || rank >= a.S) return;
-  const int64_t j = a.src_of[rank];
+  // the plan of this batch row (a shared assignment has one)
+  const int64_t pr = a.plan_rows > 1 ? b : 0;
+  const int32_t* counts = a.counts + 4 * pr;
+  int32_t* status = a.counts + 4 * pr + 3;
+  const int32_t* dst = a.dst + pr * a.S;
+  const int32_t* newpos = a.newpos + pr * a.S;
+  if (rank >= counts[2] || rank >= a.S) return;
+  const int64_t j = a.src_of[pr * a.S + rank];
   if (j < 0 || j >= a.S) return;
-  const int32_t d = a.dst[j];
+  const int32_t d = dst[j];
   if (d < 0) return;
   const int cls = d >> kClsShift;
   const int64_t slot = d & kSlotMask;
+  // this row's partition of the position order into sink | middle | recent,
+  // and its token count (tokens were evicted from it iff it keeps fewer)
+  int64_t nso = a.n_sink_old, nmo = a.n_mid_old, Sb = a.S;
+  if (a.src_lens != nullptr) {
+    nso = a.src_lens[3 * b];
+    nmo = a.src_lens[3 * b + 1];
+    const int64_t nro = a.src_lens[3 * b + 2];
+    Sb = nso + nmo + nro;
+    if (nso < 0 || nso > a.n_sink_old || nmo < 0 || nmo > a.n_mid_old || nro < 0 || nro > a.n_rec_cap || j >= Sb) {
+      atomicOr(status, 16);  // a kept token the row does not have
+      return;
+    }
+  }
   // source pair
   float k0, k1;
   uint16_t v0, v1;
-  if (j < a.n_sink_old || j >= a.n_sink_old + a.n_mid_old) {
-    const bool sink = j < a.n_sink_old;
-    const int64_t r = sink ? j : j - a.n_sink_old - a.n_mid_old;
+  if (j < nso || j >= nso + nmo) {
+    const bool sink = j < nso;
+    const int64_t r = sink ? j : j - nso - nmo;
     const uint16_t* kb = static_cast<const uint16_t*>(sink ? a.sink_k : a.rec_k);
     const uint16_t* vb = static_cast<const uint16_t*>(sink ? a.sink_v : a.rec_v);
     const int64_t off = sink ? b * a.sink_sb + h * a.sink_sh + r * a.sink_ss : b * a.rec_sb + h * a.rec_sh + r * a.rec_ss;
@@ -164,7 +193,7 @@ __global__ __launch_bounds__(256) void gather_kernel(FadeReassignArgs a) {
     v1 = vb[off + i + half];
   } else {
     // reference INT4: K per-channel scale [B,H,1,D], V per-token scale [B,H,mid,1]
-    const int64_t r = j - a.n_sink_old;
+    const int64_t r = j - nso;
     const uint8_t* kq = static_cast<const uint8_t*>(a.mid_kq) + (bh * a.n_mid_old + r) * half;
     const uint8_t* vq = static_cast<const uint8_t*>(a.mid_vq) + (bh * a.n_mid_old + r) * half;
     const uint16_t* ks = static_cast<const uint16_t*>(a.mid_ks) + bh * D;
@@ -176,10 +205,10 @@ __global__ __launch_bounds__(256) void gather_kernel(FadeReassignArgs a) {
     v1 = f2h(nib(vq[(i + half) >> 1], hi1) * vs);
   }
   uint16_t ko0, ko1;
-  if (a.counts[2] < a.S) {
+  if (counts[2] < Sb) {
     // un-RoPE at the old position (k*cos - rotate_half(k)*sin), fp16, then
     // RoPE at the new one (k*cos + rotate_half(k)*sin), fp16
-    const int64_t po = a.pos_old[j], pn = a.newpos[j];
+    const int64_t po = a.pos_old[a.pos_old_rs * b + j], pn = newpos[j];
     if (po < 0 || po >= a.table_rows || pn < 0 || pn >= a.table_rows) {
       atomicOr(status, 4);
       return;
@@ -225,18 +254,22 @@ __global__ __launch_bounds__(256) void gather_kernel(FadeReassignArgs a) {
 
 using namespace fade;
 
-FADE_API int fade_reassign_plan(const int64_t* tiers, int64_t S, int64_t n_sink, const int64_t* pos_old,
-                                int32_t* dst, int32_t* newpos, int32_t* src_of, int64_t* pos_sink,
-                                int64_t* pos_recent, int64_t* pos_mid, int32_t* counts, void* stream) {
+FADE_API int fade_reassign_plan(const int64_t* tiers, int64_t tiers_row_stride, int64_t rows, int64_t S,
+                                int64_t n_sink, const int64_t* pos_old, int64_t pos_old_row_stride, int32_t* dst,
+                                int32_t* newpos,
+                                int32_t* src_of, int64_t* pos_sink, int64_t* pos_recent, int64_t* pos_mid,
+                                int32_t* counts, void* stream) {
   const char* fn = "fade_reassign_plan";
   if (S < 0 || n_sink < 0) return einval("%s: negative S or n_sink", fn);
+  if (rows < 1 || rows > 65535) return einval("%s: rows=%lld out of range", fn, (long long)rows);
   if (S >= (1LL << 30)) return einval("%s: S=%lld too large", fn, (long long)S);
   if (counts == nullptr) return einval("%s: null counts", fn);
   if (S > 0 && (tiers == nullptr || pos_old == nullptr || dst == nullptr || newpos == nullptr || src_of == nullptr ||
                 pos_sink == nullptr || pos_recent == nullptr || pos_mid == nullptr))
     return einval("%s: null pointer", fn);
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, as_stream(stream), tiers, S, n_sink, pos_old, dst,
-                     newpos, src_of, pos_sink, pos_recent, pos_mid, counts);
+  hipLaunchKernelGGL(plan_kernel, dim3(static_cast<unsigned>(rows)), dim3(kPlanThreads), 0, as_stream(stream), tiers,
+                     tiers_row_stride, S, n_sink, pos_old, pos_old_row_stride, dst, newpos, src_of, pos_sink, pos_recent,
+                     pos_mid, counts);
   return check_launch(fn);
 }
 
@@ -245,15 +278,16 @@ FADE_API int fade_reassign_gather(const FadeReassignArgs* args, void* stream) {
   if (args == nullptr) return einval("%s: null argument", fn);
   const FadeReassignArgs& a = *args;
   if (a.D <= 0 || a.D % 2 != 0 || a.D > 512) return einval("%s: head_dim must be even and <= 512", fn);
-  if (a.B < 0 || a.H < 0 || a.S < 0 || a.n_sink_old < 0 || a.n_mid_old < 0 ||
-      a.n_sink_old + a.n_mid_old > a.S)
+  if (a.B < 0 || a.H < 0 || a.S < 0 || a.n_sink_old < 0 || a.n_mid_old < 0 || a.n_rec_cap < 0 ||
+      (a.src_lens == nullptr && a.n_sink_old + a.n_mid_old > a.S))
     return einval("%s: inconsistent tier lengths", fn);
   if (a.dst == nullptr || a.newpos == nullptr || a.src_of == nullptr || a.counts == nullptr || a.pos_old == nullptr)
     return einval("%s: null plan pointer", fn);
   if (a.n_mid_old > 0 && (a.mid_kq == nullptr || a.mid_ks == nullptr || a.mid_vq == nullptr || a.mid_vs == nullptr))
     return einval("%s: null middle tier", fn);
+  const int64_t rec_rows = a.src_lens != nullptr ? a.n_rec_cap : a.S - a.n_sink_old - a.n_mid_old;
   if ((a.n_sink_old > 0 && (a.sink_k == nullptr || a.sink_v == nullptr)) ||
-      (a.S - a.n_sink_old - a.n_mid_old > 0 && (a.rec_k == nullptr || a.rec_v == nullptr)))
+      (rec_rows > 0 && (a.rec_k == nullptr || a.rec_v == nullptr)))
     return einval("%s: null fp16 tier", fn);
   if ((a.cap_sink > 0 && (a.out_sink_k == nullptr || a.out_sink_v == nullptr)) ||
       (a.cap_rec > 0 && (a.out_rec_k == nullptr || a.out_rec_v == nullptr)) ||
@@ -263,6 +297,7 @@ FADE_API int fade_reassign_gather(const FadeReassignArgs* args, void* stream) {
   const int64_t BH = a.B * a.H;
   if (BH == 0 || a.S == 0) return FADE_OK;
   if (BH > 65535) return einval("%s: B*H=%lld exceeds 65535", fn, (long long)BH);
+  if (a.plan_rows != 1 && a.plan_rows != a.B) return einval("%s: plan_rows must be 1 or B", fn);
   const int half = static_cast<int>(a.D / 2);
   const int rpb = half >= 256 ? 1 : 256 / half;
   const int64_t rows = a.rows > 0 && a.rows < a.S ? a.rows : a.S;

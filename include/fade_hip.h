@@ -138,17 +138,21 @@ int fade_rerope_gather(const void* k_f16, int64_t ksb, int64_t ksh, int64_t kss,
 /* fade/cache.py:881-1057 (apply_tier_assignment, shared tiers) for the
  * reference INT4 middle tier, without materializing the layer.
  *
- * fade_reassign_plan: tiers int64 [S] (TIER_FP16 0 / INT4 1 / INT2 2 / EVICT 3)
- * in the cache's position order, pos_old int64 [S].  Writes dst int32 [S]
+ * fade_reassign_plan: tiers int64 [rows][S] (TIER_FP16 0 / INT4 1 / INT2 2 /
+ * EVICT 3; row stride 0 and rows 1 for a shared assignment, fade/cache.py:881;
+ * rows B for a per-row one, fade/cache.py:1059) in the cache's position
+ * order, pos_old int64 [S] (row stride 0) or [rows][S].  Per row, writes dst int32 [S]
  * (-1 evicted, else cls << 28 | slot with cls 0 sink, 1 recent, 2 middle; the
  * first n_sink FP16 tokens are the sink), newpos int32 [S] (rank among kept
  * tokens), src_of int32 [S] (source index of each kept rank), the new positions of each tier (pos_sink / pos_recent / pos_mid,
  * capacity S each: old positions, or 0..n_kept-1 when tokens are evicted) and
  * counts int32 [4] = {n_fp16, n_int4, n_kept, status} (status bit 0: INT2
- * tokens present -- not handled here; bit 1: an unknown tier value). */
-int fade_reassign_plan(const int64_t* tiers, int64_t S, int64_t n_sink, const int64_t* pos_old,
-                       int32_t* dst, int32_t* newpos, int32_t* src_of, int64_t* pos_sink,
-                       int64_t* pos_recent, int64_t* pos_mid, int32_t* counts, void* stream);
+ * tokens present -- not handled here; bit 1: an unknown tier value); every
+ * per-row output is [rows][S] ([rows][4] for counts). */
+int fade_reassign_plan(const int64_t* tiers, int64_t tiers_row_stride, int64_t rows, int64_t S,
+                       int64_t n_sink, const int64_t* pos_old, int64_t pos_old_row_stride, int32_t* dst,
+                       int32_t* newpos, int32_t* src_of, int64_t* pos_sink, int64_t* pos_recent,
+                       int64_t* pos_mid, int32_t* counts, void* stream);
 
 /* fade_reassign_gather: moves every kept token of the current tiers (in
  * position order: sink rows, middle rows, recent rows) to its destination;
@@ -162,7 +166,14 @@ int fade_reassign_plan(const int64_t* tiers, int64_t S, int64_t n_sink, const in
  * tables). */
 typedef struct FadeReassignArgs {
   int64_t B, H, D, S;
-  int64_t n_sink_old, n_mid_old; /* recent = S - sink - middle */
+  int64_t n_sink_old, n_mid_old; /* recent = S - sink - middle; with src_lens: the capacities
+                                    (rows of the sink / middle tensors) */
+  const int32_t* src_lens;       /* optional device [B][3]: each row's current sink / middle /
+                                    recent tokens (a ragged layout); row b's position order is
+                                    its own sink | middle | recent, tokens past them absent */
+  int64_t plan_rows;             /* 1: one shared plan; B: the plan of row b */
+  int64_t pos_old_rs;            /* row stride of pos_old (0: shared) */
+  int64_t n_rec_cap;             /* with src_lens: rows of the recent tensors */
   const void* sink_k;
   const void* sink_v;
   int64_t sink_sb, sink_sh, sink_ss; /* element strides shared by sink K and V */

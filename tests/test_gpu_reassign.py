@@ -119,3 +119,103 @@ def test_reassign_int2_falls_back(dev):
     assert devc._last_reassign_counts is None
     _same(host, devc, "int2")
     assert devc._layers[0].int2_actual_count == 5
+
+
+RAGGED_FIELDS = (("sink_k", 0), ("sink_v", 0), ("int4_kq", 1), ("int4_vq", 1), ("int4_vs", 1), ("fp16_k", 2),
+                 ("fp16_v", 2))
+
+
+def _single_row_caches(B, n_sink, recent):
+    out = []
+    for _ in range(B):
+        c = TieredKVCache(n_sink=n_sink, recent_window=recent, int4_budget=None, int2_budget=0, head_dim=128)
+        c.device_reassign = False  # the host path (the reference's op sequence)
+        out.append(c)
+    return out
+
+
+def _check_rows(rag, singles, what):
+    st = rag._layers[0]
+    assert st.lens is not None
+    assert st.lens.cpu().tolist() == st.lens_host
+    for b, one in enumerate(singles):
+        s1 = one._layers[0]
+        ls, lm, lr = st.lens_host[b]
+        # the single-row cache splits sink / recent the same way once reassigned
+        k1 = {"sink_k": s1.sink_k, "sink_v": s1.sink_v, "fp16_k": s1.fp16_k, "fp16_v": s1.fp16_v,
+              "int4_kq": s1.int4_kq, "int4_vq": s1.int4_vq, "int4_vs": s1.int4_vs}
+        n = (ls, lm, lr)
+        for f, tier in RAGGED_FIELDS:
+            x = getattr(st, f)
+            y = k1[f]
+            ny = 0 if y is None else int(y.shape[-2])
+            assert ny == n[tier], f"{what}: row {b} {f}: {ny} rows vs lens {n[tier]}"
+            if ny:
+                assert torch.equal(x[b : b + 1, :, :ny].cpu(), y.cpu()), f"{what}: row {b} {f} differs"
+        if lm:
+            assert torch.equal(st.int4_ks[b : b + 1].cpu(), s1.int4_ks.cpu()), f"{what}: row {b} K scale"
+        assert rag.get_seq_length(0) == max(sum(r) for r in st.lens_host)
+        ko, vo = rag._materialize(0)
+        k1m, v1m = one._materialize(0)
+        tot = ls + lm + lr
+        assert torch.equal(ko[b : b + 1, :, :tot].cpu(), k1m.cpu()) and torch.equal(vo[b : b + 1, :, :tot].cpu(), v1m.cpu())
+        assert not ko[b, :, tot:].any()
+
+
+def test_ragged_layout_matches_single_rows(dev):
+    """Ragged per-row reassignment (device) == each row alone through the host path, through
+    reassignment, appends, a second reassignment and decode."""
+    print("case ragged layout", flush=True)
+    B, H, n_sink, recent = 3, 2, 4, 16
+    rag = TieredKVCache(n_sink=n_sink, recent_window=recent, int4_budget=None, int2_budget=0, head_dim=128)
+    rag.ragged_layout = True
+    singles = _single_row_caches(B, n_sink, recent)
+    g = torch.Generator().manual_seed(11)
+    k = (torch.randn(B, H, 180, 128, generator=g) * torch.exp(torch.randn(128, generator=g) * 0.5)).half().to(dev)
+    v = torch.randn(B, H, 180, 128, generator=g).half().to(dev)
+    rag.update(k, v, 0)
+    for b, c in enumerate(singles):
+        c.update(k[b : b + 1], v[b : b + 1], 0)
+    rng = np.random.default_rng(3)
+    budgets = [30, None, 90]
+
+    def reassign(row_len):
+        S = max(row_len)
+        tiers = torch.full((B, S), TIER_EVICT, dtype=torch.long)
+        for b in range(B):
+            sc = torch.from_numpy(rng.exponential(size=row_len[b]).astype(np.float32))
+            t = _assign_one_layer(row_len[b], sc, n_sink, recent, budgets[b], 0)
+            tiers[b, : row_len[b]] = t
+            singles[b].apply_tier_assignment(0, t)
+        rag.apply_tier_assignment_per_sequence(0, tiers)
+
+    reassign([180] * B)
+    _check_rows(rag, singles, "first reassignment")
+    for step in range(3):
+        kn = torch.randn(B, H, 1, 128, generator=g).half().to(dev)
+        vn = torch.randn(B, H, 1, 128, generator=g).half().to(dev)
+        rag.update(kn, vn, 0)
+        for b, c in enumerate(singles):
+            c.update(kn[b : b + 1], vn[b : b + 1], 0)
+    _check_rows(rag, singles, "appends")
+    reassign([sum(r) for r in rag._layers[0].lens_host])
+    _check_rows(rag, singles, "second reassignment")
+    q = torch.randn(B, 8, 1, 128, generator=g).half().to(dev)
+    out = rag.decode_attention(q, 0)
+    for b, c in enumerate(singles):
+        ref = c.decode_attention(q[b : b + 1], 0)
+        assert (out[b : b + 1].float() - ref.float()).abs().max().item() <= 2e-3, b
+
+
+def test_ragged_layout_rejects_shared_calls(dev):
+    """A ragged layer refuses the shared-tier entry point and the checkpoint form."""
+    rag = TieredKVCache(n_sink=2, recent_window=4, int4_budget=None, int2_budget=0, head_dim=128)
+    rag.ragged_layout = True
+    kv = torch.randn(2, 2, 20, 128).half().to(dev)
+    rag.update(kv, kv, 0)
+    tiers = _assign_one_layer(20, torch.zeros(20), 2, 4, None, 0)
+    rag.apply_tier_assignment_per_sequence(0, tiers.unsqueeze(0).expand(2, -1).contiguous())
+    with pytest.raises(NotImplementedError):
+        rag.apply_tier_assignment(0, tiers)
+    with pytest.raises(NotImplementedError):
+        rag.cache_state_dict()
