@@ -359,3 +359,35 @@ def test_tiered_decode_paged_middle(dev, fmt):
             k[b : b + 1, :, S - nr_c : S - nr_c + lr], v[b : b + 1, :, S - nr_c : S - nr_c + lr],
         )
         assert np.abs(out[b : b + 1] - ref).max() <= ATOL, b
+
+
+def test_tiered_decode_hip_graph_replays(dev):
+    """Decode captured in a HIP graph: every replay, with eager work and synchronizations in
+    between (a new query written in place), matches the eager call on the same inputs (to the
+    attention bar: waves claim tiles dynamically, so the summation order may differ)."""
+    from fade_amd.kernels import TieredDecodePlan
+
+    print("case decode graph replays", flush=True)
+    q, k, v, ns, nr = _case(2, 32, 8, 900, 4, 64, seed=31)
+    mid, _ = _int4_mid(dev, k, v, ns, nr)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    S = k.shape[2]
+    qd = t(q)
+    plan = TieredDecodePlan(qd, (t(k[:, :, :ns]), t(v[:, :, :ns])), mid, (t(k[:, :, S - nr :]), t(v[:, :, S - nr :])))
+    plan.run()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        plan.run(s.cuda_stream)
+    gen = torch.Generator().manual_seed(5)
+    for rep in range(4):
+        qd.copy_(torch.randn(qd.shape, generator=gen).half().to(dev))
+        eager = plan.run().clone()
+        torch.cuda.synchronize()
+        plan.out.zero_()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        assert (plan.out.float() - eager.float()).abs().max().item() <= ATOL, rep
+        assert plan.out.abs().sum().item() > 0, rep

@@ -147,3 +147,47 @@ def test_fade_attention_registration_and_fused_update():
     assert rk is k and rv is v
     assert cache.get_seq_length(0) == 5
     assert active_cache() is cache
+
+
+def test_paginate_middle_pools_pages_on_host():
+    """paginate_middle (host logic; runs on CPU tensors): every row's 64-token tiles land in
+    the pool pages its block table names, in any page order, and the SYM K scale stays per row."""
+    import torch
+
+    from fade_amd.kernels.tiered_attn import MiddleTier, paginate_middle
+
+    B, H, S = 3, 2, 150
+    g = torch.Generator().manual_seed(0)
+    kc = torch.randint(0, 256, (B, H, S, 64), generator=g, dtype=torch.uint8)
+    vc = torch.randint(0, 256, (B, H, S, 64), generator=g, dtype=torch.uint8)
+    ks = torch.rand(B, H, 1, 128, generator=g).half()
+    vs = torch.rand(B, H, S, 1, generator=g).half()
+    mid = MiddleTier("int4", kc, vc, ks, vs)
+    lens = [150, 64, 1]
+    order = [3, 0, 4, 1, 2]  # 3 + 1 + 1 pages, placed out of order
+    p = paginate_middle(mid, lens, order=order)
+    assert p.k_codes.shape == (5, H, 64, 64) and p.v_scale.shape == (5, H, 64, 1)
+    assert p.k_scale is ks and p.length == 150
+    assert p.pages.tolist() == [[3, 0, 4], [1, 0, 0], [2, 0, 0]]
+    for b, n in enumerate(lens):
+        for t in range(-(-n // 64)):
+            pg = int(p.pages[b, t])
+            rows = min(64, n - 64 * t)
+            assert torch.equal(p.k_codes[pg, :, :rows], kc[b, :, 64 * t : 64 * t + rows])
+            assert torch.equal(p.v_codes[pg, :, :rows], vc[b, :, 64 * t : 64 * t + rows])
+            assert torch.equal(p.v_scale[pg, :, :rows], vs[b, :, 64 * t : 64 * t + rows])
+
+
+def test_host_tier_counts_and_graph_split():
+    import torch
+
+    import bench
+    from fade_amd.cache import TIER_EVICT, TIER_FP16, TIER_INT2, TIER_INT4, TieredKVCache
+
+    t = torch.tensor([TIER_FP16, TIER_INT4, TIER_INT4, TIER_EVICT, TIER_INT2, TIER_FP16])
+    assert TieredKVCache._host_tier_counts(t) == (2, 2, 1)
+    assert TieredKVCache._host_tier_counts(torch.tensor([0, 7])) is None
+    for steps in (1, 5, 37, 64, 200, 1000):
+        calls, reps = bench.graph_split(steps)
+        assert calls * reps == steps and calls <= 32
+    assert bench.graph_split(200) == (20, 10)
