@@ -28,6 +28,7 @@
 #include <math.h>
 
 #include "decode_common.h"
+#include "lds_dma.h"
 
 namespace fade {
 namespace decode {
@@ -45,7 +46,6 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8;
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kTileT = 64;
-constexpr int kStages = 2;
 constexpr int kStageK = 0, kStageV = 4096, kStageVS = 8192;
 constexpr int kStageBytes = 8192 + 256;  // the 2-byte DMA writes one dword per lane
 constexpr float kQMax = 32000.0f;
@@ -54,21 +54,14 @@ constexpr int kV16Pitch = 136;  // halfs per staged fp16 V row (16 rows = 4352 B
 
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
-// Direct HBM -> LDS load per lane: 16 bytes land at lds_base + 16*i; a 2-byte
-// load lands zero-extended in the dword at lds_base + 4*i.  Issued as inline asm so that the only waits on these
-// loads are the explicit per-stage s_waitcnt vmcnt of the packed-tile loop
-// (the compiler cannot tell two ring stages apart and would wait for both).
-// Register-destination loads stay correct: any wait the compiler emits for
-// them also covers older LDS loads and at worst over-waits for newer ones.
-__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
-}
-__device__ __forceinline__ void lds_dma2(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_ushort %0, off" ::"v"(g), "s"(lds_base) : "memory", "m0");
-}
+// Direct HBM -> LDS loads (lds_dma.h): 16 bytes land at lds_base + 16*i; a
+// 2-byte load lands zero-extended in the dword at lds_base + 4*i.  Issued as
+// inline asm so that the only waits on these loads are the explicit per-stage
+// s_waitcnt vmcnt of the packed-tile loop (the compiler cannot tell two ring
+// stages apart and would wait for both).  Register-destination loads stay
+// correct: any wait the compiler emits for them also covers older LDS loads
+// and at worst over-waits for newer ones.
 
-__device__ __forceinline__ f16x2 u2h2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
-__device__ __forceinline__ uint32_t h22u(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
 
 // Offset-binary int8 codes (u = c + 8) of one packed dword: lo nibbles
 // (odd channels) and hi nibbles (even channels), four bytes each.
@@ -133,7 +126,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   const int64_t F = p.total - M;                               // fp16 tokens
   const int64_t nF = (F + kTileT - 1) / kTileT;
 
-  // Per-wave ring of kStages stages; a stage holds one packed tile:
+  // Per-wave ring of two stages; a stage holds one packed tile:
   // K codes (4 KB) | V codes (4 KB) | V scales (64 dwords), swizzled 16-byte units.
   __shared__ __attribute__((aligned(16))) uint8_t ring0[kWaves][kStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t ring1[kWaves][kStageBytes];
@@ -335,7 +328,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
 
   // ------------------------------------------ packed INT4 tiles, pipelined
   // Tile codes and scales move HBM -> LDS with direct global_load_lds
-  // (16 bytes per lane, no VGPRs), kStages tiles ahead of the math.
+  // (16 bytes per lane, no VGPRs), two tiles ahead of the math.
   // 16-byte units are swizzled so the K-operand reads (16 lanes = 16 rows,
   // one chunk) and the tr4 V reads (16 consecutive rows, one 8-byte half)
   // hit 16 different bank groups:

@@ -149,7 +149,6 @@ __global__ __launch_bounds__(kBlock) void quant_token_kernel(const InT* __restri
                                                              uint8_t* __restrict__ packed,
                                                              uint16_t* __restrict__ scale) {
   constexpr int RP = kBlock / LPR;
-  constexpr int D = LPR * 8;
   constexpr int ROW_BYTES = LPR * lane_bytes<BITS>();
   const int c = threadIdx.x % LPR;
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; r < rows;
