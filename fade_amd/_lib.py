@@ -68,6 +68,7 @@ class MidTier(ctypes.Structure):
         ("v_zero", _p),
         ("pages", _p),
         ("pages_per_row", _i64),
+        ("page_stride", _i64),
     ]
 
 

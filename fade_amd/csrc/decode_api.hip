@@ -100,6 +100,12 @@ int validate(const fade_decode_args* a) {
       if (m.pages_per_row < cdiv(m.len, 64))
         return einval("fade_tiered_decode_attn: pages_per_row=%lld < %lld tiles of the middle tier",
                       (long long)m.pages_per_row, (long long)cdiv(m.len, 64));
+      if (m.page_stride != 0) {
+        const int64_t need = 64 * 16 * (m.k_bits > m.v_bits ? m.k_bits : m.v_bits);
+        if (m.fmt != FADE_MID_SYM || m.page_stride < need || m.page_stride % 16 != 0)
+          return einval("fade_tiered_decode_attn: page_stride needs FADE_MID_SYM, a multiple of 16 and >= %lld",
+                        (long long)need);
+      }
     }
   }
   if (a->kernel < 0 || a->kernel > 3) return einval("fade_tiered_decode_attn: kernel must be 0, 1, 2 or 3");
@@ -142,6 +148,7 @@ Params to_params(const fade_decode_args* a) {
   p.mid.v_zero = static_cast<const uint16_t*>(m.v_zero);
   p.mid.pages = m.pages;
   p.mid.pages_per_row = m.pages_per_row;
+  p.mid.page_stride = m.pages != nullptr ? m.page_stride : 0;
   p.total = total_tokens(a);
   p.lens = a->lens;
   return p;

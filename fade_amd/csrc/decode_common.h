@@ -28,6 +28,7 @@ struct MidTier {
   const uint16_t* v_zero;
   const int32_t* pages;  // optional [B][pages_per_row] page of each 64-token tile (paged pools)
   int64_t pages_per_row;
+  int64_t page_stride;  // paged SYM: bytes between (page, kv head) blocks of every tensor, or 0
 };
 
 // Page slots a workgroup of the INT4 kernel holds (its split's middle tiles).

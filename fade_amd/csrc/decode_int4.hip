@@ -249,6 +249,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   const uint16_t* kzg = ASYM ? p.mid.k_zero + rb0 * kGroups : nullptr;
   const uint16_t* vzg = ASYM ? p.mid.v_zero + rb0 * kGroups : nullptr;
   const int64_t Hkv = p.Hkv;
+  const int64_t pstride = (!ASYM && paged) ? p.mid.page_stride : 0;
   // fp16 tiers as (uniform) locals: the lambdas below must not read the kernel
   // arguments through a pointer (that becomes a per-lane global load whose
   // compiler-inserted vmcnt wait would also wait for the tile prefetches).
@@ -290,12 +291,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     if (tt >= nFt) {
       const int64_t m0 = (tt - nFt) * kTile;  // the tile's first token of the row's middle
       int64_t r0 = m0;                        // its first row in the tensors
+      int64_t ob = -1;                        // byte offset of its (page, kv head) block, strided pools
       if (paged) {
         const int64_t slot = tt - nFt - mt_lo;
-        r0 = (static_cast<int64_t>(pages_s[slot < kPageSlots ? slot : kPageSlots - 1]) * Hkv + kvh) * kTile;
+        const int64_t blk = static_cast<int64_t>(pages_s[slot < kPageSlots ? slot : kPageSlots - 1]) * Hkv + kvh;
+        r0 = blk * kTile;
+        if (pstride) ob = blk * pstride;
       }
-      const uint8_t* kb = kc + r0 * kRowK;
-      const uint8_t* vb = vc + r0 * kRowV;
+      const uint8_t* kb = ob >= 0 ? kc + ob : kc + r0 * kRowK;
+      const uint8_t* vb = ob >= 0 ? vc + ob : vc + r0 * kRowV;
       const int lim = m0 + kTile > M ? static_cast<int>(M - 1 - m0) : kTile - 1;
       if (KB == 4) {
         uint32_t ko[4] = {koff[0], koff[1], koff[2], koff[3]};
@@ -361,7 +365,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         lds_dma4(vsg + (m0 / kTile) * kD, 4u * lane, st + kMeta);  // the tile's scale row
       } else {
         const uint32_t so = 2u * (lane < lim ? lane : lim);
-        lds_dma2(vsg + r0, so, st + kMeta);
+        lds_dma2(ob >= 0 ? reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(vsg) + ob) : vsg + r0, so,
+                 st + kMeta);
       }
     } else {
       const int64_t f0 = tt * kMini;

@@ -58,6 +58,7 @@ class MiddleTier:
     group: int = 64
     length: int | None = None
     pages: Tensor | None = None
+    page_stride: int = 0  # bytes between (page, kv head) blocks of an interleaved pool
 
     @property
     def n_tokens(self) -> int:
@@ -91,7 +92,7 @@ def _mid_tier(mid: MiddleTier | None) -> _lib.MidTier:
     if mid.fmt not in _FMT:
         raise ValueError(f"unknown middle format {mid.fmt!r}")
     for t in mid.tensors():
-        if not t.is_contiguous():
+        if not t.is_contiguous() and not mid.page_stride:
             raise ValueError("middle-tier tensors must be contiguous")
     m.fmt = _FMT[mid.fmt]
     m.k_bits, m.v_bits, m.group = mid.k_bits, mid.v_bits, mid.group
@@ -106,14 +107,18 @@ def _mid_tier(mid: MiddleTier | None) -> _lib.MidTier:
         if mid.pages.dtype != torch.int32 or mid.pages.dim() != 2:
             raise ValueError("pages must be int32 [B, pages_per_row]")
         m.pages, m.pages_per_row = mid.pages.data_ptr(), int(mid.pages.shape[1])
+        m.page_stride = int(mid.page_stride)
     return m
 
 
-def paginate_middle(mid: MiddleTier, lens_mid, order=None) -> MiddleTier:
+def paginate_middle(mid: MiddleTier, lens_mid, order=None, interleave: bool = False) -> MiddleTier:
     """A padded ``"int4"``/``"sym"``/``"asym"`` middle tier ([B, Hkv, S, ...] per token)
     as a paged one: row b's ``lens_mid[b]`` tokens go to ``ceil(lens_mid[b] / 64)``
     pages of one pool shared by the rows.  ``order`` (a permutation of the page
-    ids) places the pages anywhere in the pool; default: in row order."""
+    ids) places the pages anywhere in the pool; default: in row order.
+    ``interleave`` (``"int4"``/``"sym"``): one pool whose (page, kv head) blocks
+    hold [K codes | V codes | V scales] back to back, so a tile is one
+    contiguous read."""
     if mid.fmt not in ("int4", "sym", "asym") or mid.pages is not None:
         raise ValueError("paginate_middle takes an unpaged int4 / sym / asym middle tier")
     lens = [int(x) for x in lens_mid]
@@ -149,6 +154,28 @@ def paginate_middle(mid: MiddleTier, lens_mid, order=None) -> MiddleTier:
         return out
 
     k_scale = mid.k_scale if mid.fmt != "asym" else pool(mid.k_scale)  # SYM K scale: per row [B,Hkv,1,D]
+    if interleave:
+        if mid.fmt == "asym":
+            raise ValueError("interleave: int4 / sym middle tiers only")
+        kp, vp, sp = pool(mid.k_codes), pool(mid.v_codes), pool(mid.v_scale)
+        kb, vbytes, sb = kp[0, 0].numel(), vp[0, 0].numel(), sp[0, 0].numel() * 2
+        stride = -(-(kb + vbytes + sb) // 16) * 16
+        blk = torch.zeros(n_pages, H, stride, dtype=torch.uint8, device=dev)
+        blk[:, :, :kb] = kp.reshape(n_pages, H, kb)
+        blk[:, :, kb : kb + vbytes] = vp.reshape(n_pages, H, vbytes)
+        blk[:, :, kb + vbytes : kb + vbytes + sb] = sp.reshape(n_pages, H, -1).view(torch.uint8)
+        flat = blk.view(-1)
+        # views into the pool at each tensor's offset in a block (the kernel reads the
+        # first block's address and steps by `stride`)
+        kv = flat.as_strided(kp.shape, (H * stride, stride, kp.shape[-1], 1), 0)
+        vv = flat.as_strided(vp.shape, (H * stride, stride, vp.shape[-1], 1), kb)
+        tail = flat[kb + vbytes :]
+        half = tail[: (tail.numel() // 2) * 2].view(torch.float16)
+        vs = half.as_strided(sp.shape, (H * stride // 2, stride // 2, 1, 1))
+        out = MiddleTier(mid.fmt, kv, vv, k_scale, vs, k_bits=mid.k_bits, v_bits=mid.v_bits, group=mid.group,
+                         length=max(lens) if lens else 0, pages=table.to(dev), page_stride=stride)
+        out._pool = blk  # keeps the pool alive
+        return out
     return MiddleTier(mid.fmt, pool(mid.k_codes), pool(mid.v_codes), k_scale, pool(mid.v_scale),
                       pool(mid.k_zero), pool(mid.v_zero), k_bits=mid.k_bits, v_bits=mid.v_bits, group=mid.group,
                       length=max(lens) if lens else 0, pages=table.to(dev))

@@ -237,6 +237,11 @@ typedef struct fade_mid_tier {
    * from the decode args' lens). */
   const int32_t* pages;
   int64_t pages_per_row;
+  /* Paged FADE_MID_SYM only: bytes between consecutive (page, kv head) blocks
+   * of k_codes, v_codes and v_scale (which may then interleave in one pool,
+   * e.g. [K codes | V codes | V scales] per block: one request stream per
+   * tile); 0 = each tensor's own block size. */
+  int64_t page_stride;
 } fade_mid_tier;
 
 typedef struct fade_decode_args {
