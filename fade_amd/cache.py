@@ -170,6 +170,11 @@ class TieredKVCache(DynamicCache):
         # tier lengths, attention over them only) instead of the reference's
         # zero-padded rows (fade/cache.py:1145-1159)
         self.ragged_layout = False
+        # roadmap P4 (FADE v1.0 Release + Future Roadmap.md:30-34): at a reassignment,
+        # per-token codes of tokens that stay in the middle tier are kept as they are
+        # and only tokens entering it are quantized (no requantization of dequantized
+        # values); per-channel K scales still span the whole tier and are recomputed
+        self.incremental_quant = False
         self._last_reassign_counts = None
 
     # transformers 5.x defines a read-only ``Cache.batch_size``; the tiered cache
@@ -603,6 +608,19 @@ class TieredKVCache(DynamicCache):
         )
 
     @staticmethod
+    def _middle_sources(tiers: Tensor, ns_old: int, nm_old: int, keep_idx: Tensor | None = None):
+        """For the middle tier an assignment builds: (slots, old rows) of the tokens that were
+        already middle tokens, and the slots of the others.  ``tiers`` is the host
+        assignment over the kept tokens; ``keep_idx`` maps them back to the position
+        order before eviction."""
+        t = tiers.cpu()
+        mids = (t == TIER_INT4).nonzero(as_tuple=False).squeeze(-1)
+        src = mids if keep_idx is None else keep_idx.cpu()[mids]
+        was_mid = (src >= ns_old) & (src < ns_old + nm_old)
+        slots = torch.arange(int(mids.numel()))
+        return slots[was_mid], (src[was_mid] - ns_old), slots[~was_mid]
+
+    @staticmethod
     def _host_tier_counts(tiers: Tensor) -> tuple[int, int, int] | None:
         """(n_fp16, n_int4, n_int2) of a host tiers tensor, or None if it holds other values."""
         t = tiers.to(torch.long)
@@ -610,6 +628,40 @@ class TieredKVCache(DynamicCache):
         if sum(n) != int(t.numel()):
             return None
         return n[0], n[1], n[2]
+
+    def _incremental_v(self, tiers: Tensor, ns_old: int, nm_old: int, old_v, v_new_f16: Tensor):
+        """Per-token INT4 V of the new middle tier: old middle tokens keep their codes and
+        scales, the others are quantized from their fp16 values (``quant_v_int4``)."""
+        slots, rows, fresh = self._middle_sources(tiers, ns_old, nm_old)
+        B, H, n, D = v_new_f16.shape
+        dev = v_new_f16.device
+        vq = torch.empty(B, H, n, D // 2, dtype=torch.uint8, device=dev)
+        vs = torch.empty(B, H, n, 1, dtype=torch.float16, device=dev)
+        if slots.numel():
+            si, ri = slots.to(dev), rows.to(dev)
+            vq.index_copy_(2, si, old_v[0].index_select(2, ri))
+            vs.index_copy_(2, si, old_v[1].index_select(2, ri))
+        if fresh.numel():
+            fi = fresh.to(dev)
+            q, sc = quant_v_int4(v_new_f16.index_select(2, fi).contiguous())
+            vq.index_copy_(2, fi, q)
+            vs.index_copy_(2, fi, sc)
+        return vq, vs
+
+    @staticmethod
+    def _merge_compressed(old: dict, fresh: dict | None, slots: Tensor, rows: Tensor, fresh_slots: Tensor, n: int):
+        """Per-token compressed dict of n tokens: rows of ``old`` at ``slots``, rows of
+        ``fresh`` at ``fresh_slots`` (every tensor is [B, H, tokens, ...])."""
+        out = {}
+        for key, t in old.items():
+            dev = t.device
+            o = torch.empty(t.shape[0], t.shape[1], n, *t.shape[3:], dtype=t.dtype, device=dev)
+            if slots.numel():
+                o.index_copy_(2, slots.to(dev), t.index_select(2, rows.to(dev)))
+            if fresh is not None and fresh_slots.numel():
+                o.index_copy_(2, fresh_slots.to(dev), fresh[key])
+            out[key] = o
+        return out
 
     def _apply_tier_assignment_device(self, layer_idx: int, tiers: Tensor, counts) -> bool:
         """``apply_tier_assignment`` on the device for the reference INT4 layout.
@@ -623,6 +675,7 @@ class TieredKVCache(DynamicCache):
         Returns False (nothing changed) when the assignment holds INT2 tokens.
         """
         st = self._layers[layer_idx]
+        old_v = (st.int4_vq, st.int4_vs)
         if st.sink_k is not None:
             sink = (st.sink_k, st.sink_v)
             rec_start = 0
@@ -737,7 +790,10 @@ class TieredKVCache(DynamicCache):
             st._fp16_len = 0
         if mid is not None:
             st.int4_kq, st.int4_ks = quant_k_int4(mid[0])
-            st.int4_vq, st.int4_vs = quant_v_int4(mid[1])
+            if self.incremental_quant and old_v[0] is not None and tiers.device.type == "cpu":
+                st.int4_vq, st.int4_vs = self._incremental_v(tiers, ns_old, nm_old, old_v, mid[1])
+            else:
+                st.int4_vq, st.int4_vs = quant_v_int4(mid[1])
             st.int4_pos = pos_new[2, :n_int4]
         else:
             st.int4_kq = st.int4_vq = st.int4_ks = st.int4_vs = st.int4_pos = None
@@ -772,13 +828,21 @@ class TieredKVCache(DynamicCache):
             raise NotImplementedError("this layer holds the ragged layout: use apply_tier_assignment_per_sequence")
         if self._device_reassign_ok(st) and self._apply_tier_assignment_device(layer_idx, tiers, counts):
             return
+        # per-token backend codes that an incremental reassignment may keep
+        inc = None
+        if self.incremental_quant and isinstance(self._quant_backend, AsymGroupBackend) \
+                and st.backend_k is not None and st.int2_kq is None:
+            ns_old = st.sink_pos.shape[0] if st.sink_k is not None else (st.sink_count if st.fp16_k is not None else 0)
+            inc = (st.backend_k, st.backend_v, int(ns_old), int(st.backend_pos.shape[0]))
         k_full, v_full, pos_full = self._all_in_position_order(layer_idx)
         S = int(pos_full.shape[0])
         if int(tiers.shape[0]) != S:
             raise ValueError(f"tiers length {int(tiers.shape[0])} != cache length {S} for layer {layer_idx}")
+        tiers_host = tiers.cpu() if inc is not None else None
         tiers = tiers.to(pos_full.device)
         keep = tiers != TIER_EVICT
         n_kept = int(keep.sum().item())
+        keep_idx = None
         if n_kept < S:
             keep_idx = keep.nonzero(as_tuple=False).squeeze(-1)
             k_full, v_full, pos_full = self._rerope_kept(k_full, v_full, pos_full, keep_idx, n_kept)
@@ -803,7 +867,24 @@ class TieredKVCache(DynamicCache):
         self._reseed_fp16_buffer(st)
 
         int4_idx = (tiers == TIER_INT4).nonzero(as_tuple=False).squeeze(-1)
-        if int4_idx.numel() > 0:
+        if int4_idx.numel() > 0 and inc is not None:
+            # incremental (per-token backend): old middle tokens keep their codes (K only
+            # when nothing was evicted: re-RoPE changes K), the others are compressed
+            be = self._quant_backend
+            kept_tiers = tiers_host if keep_idx is None else tiers_host[keep_idx.cpu()]
+            slots, rows, fresh = self._middle_sources(kept_tiers, inc[2], inc[3], keep_idx)
+            n = int(int4_idx.numel())
+            fi = fresh.to(int4_idx.device)
+            fv = be.compress_v(_sel(v_full, int4_idx.index_select(0, fi))) if fresh.numel() else None
+            st.backend_v = self._merge_compressed(inc[1], fv, slots, rows, fresh, n)
+            if keep_idx is None:
+                fk = be.compress_k(_sel(k_full, int4_idx.index_select(0, fi))) if fresh.numel() else None
+                st.backend_k = self._merge_compressed(inc[0], fk, slots, rows, fresh, n)
+            else:
+                st.backend_k = be.compress_k(_sel(k_full, int4_idx))
+            st.backend_pos = pos_full.index_select(0, int4_idx)
+            st.int4_kq = st.int4_vq = st.int4_ks = st.int4_vs = st.int4_pos = None
+        elif int4_idx.numel() > 0:
             self._store_middle(st, _sel(k_full, int4_idx), _sel(v_full, int4_idx), pos_full.index_select(0, int4_idx))
         else:
             st.int4_kq = st.int4_vq = st.int4_ks = st.int4_vs = st.int4_pos = None

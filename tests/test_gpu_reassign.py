@@ -219,3 +219,86 @@ def test_ragged_layout_rejects_shared_calls(dev):
         rag.apply_tier_assignment(0, tiers)
     with pytest.raises(NotImplementedError):
         rag.cache_state_dict()
+
+
+@pytest.mark.parametrize("budget", [None, 50])
+def test_incremental_quant_int4_v(dev, budget):
+    """Reference INT4, device path, incremental_quant: K as without it (per-channel scales
+    span the tier); V of tokens already in the middle keeps its codes and scales; V of
+    tokens entering it equals the whole-tier requantization's."""
+    print(f"case incremental int4 budget={budget}", flush=True)
+    inc = TieredKVCache(n_sink=4, recent_window=16, int4_budget=budget, int2_budget=0, head_dim=128)
+    ref = TieredKVCache(n_sink=4, recent_window=16, int4_budget=budget, int2_budget=0, head_dim=128)
+    inc.incremental_quant = True
+    _append((inc, ref), 2, 2, 140, 21, dev)
+    rng = np.random.default_rng(21)
+    for rnd in range(3):
+        S = inc.get_seq_length(0)
+        tiers = _assign_one_layer(S, torch.from_numpy(rng.exponential(size=S).astype(np.float32)), 4, 16, budget, 0)
+        s0 = inc._layers[0]
+        if s0.sink_k is not None:
+            ns_old = int(s0.sink_k.shape[-2])
+        else:
+            ns_old = s0.sink_count if s0.fp16_k is not None else 0
+        nm_old = 0 if s0.int4_kq is None else int(s0.int4_kq.shape[-2])
+        old_vq, old_vs = s0.int4_vq, s0.int4_vs
+        inc.apply_tier_assignment(0, tiers)
+        ref.apply_tier_assignment(0, tiers)
+        a, b = inc._layers[0], ref._layers[0]
+        assert torch.equal(a.int4_kq, b.int4_kq) and torch.equal(a.int4_ks, b.int4_ks)
+        slots, rows, fresh = TieredKVCache._middle_sources(tiers, ns_old, nm_old)
+        if old_vq is not None and slots.numel():
+            assert torch.equal(a.int4_vq[:, :, slots.to(dev)], old_vq[:, :, rows.to(dev)])
+            assert torch.equal(a.int4_vs[:, :, slots.to(dev)], old_vs[:, :, rows.to(dev)])
+        if fresh.numel():
+            assert torch.equal(a.int4_vq[:, :, fresh.to(dev)], b.int4_vq[:, :, fresh.to(dev)])
+            assert torch.equal(a.int4_vs[:, :, fresh.to(dev)], b.int4_vs[:, :, fresh.to(dev)])
+        _append((inc, ref), 2, 2, 23, 121 + rnd, dev)
+    q = torch.randn(2, 8, 1, 128, generator=torch.Generator().manual_seed(4)).half().to(dev)
+    assert (inc.decode_attention(q, 0).float() - ref.decode_attention(q, 0).float()).abs().max().item() <= 2e-3
+
+
+@pytest.mark.parametrize("budget", [None, 50])
+def test_incremental_quant_asym_backend(dev, budget):
+    """Asym group-32 backend (per-token K and V), incremental_quant: tokens already in the
+    middle keep their codes (K only when nothing was evicted: re-RoPE changes K), tokens
+    entering it are compressed from their fp16 values, as the whole-tier path does."""
+    print(f"case incremental asym budget={budget}", flush=True)
+    kw = dict(n_sink=4, recent_window=16, int4_budget=budget, int2_budget=0, head_dim=128,
+              quant_backend="int4_asym_g32")
+    inc, ref = TieredKVCache(**kw), TieredKVCache(**kw)
+    inc.incremental_quant = True
+    _append((inc, ref), 2, 2, 140, 22, dev)
+    rng = np.random.default_rng(22)
+    for rnd in range(3):
+        S = inc.get_seq_length(0)
+        tiers = _assign_one_layer(S, torch.from_numpy(rng.exponential(size=S).astype(np.float32)), 4, 16, budget, 0)
+        s0 = inc._layers[0]
+        old = None
+        if s0.backend_k is not None:
+            ns_old = int(s0.sink_pos.shape[0]) if s0.sink_k is not None else (s0.sink_count if s0.fp16_k is not None else 0)
+            old = (s0.backend_k, s0.backend_v, ns_old, int(s0.backend_pos.shape[0]))
+        evicts = bool((tiers == TIER_EVICT).any())
+        inc.apply_tier_assignment(0, tiers)
+        ref.apply_tier_assignment(0, tiers)
+        a, b = inc._layers[0], ref._layers[0]
+        if old is None:
+            for key in a.backend_k:
+                assert torch.equal(a.backend_k[key], b.backend_k[key]) and torch.equal(a.backend_v[key], b.backend_v[key])
+        else:
+            keep_idx = (tiers != TIER_EVICT).nonzero().squeeze(-1) if evicts else None
+            kept = tiers if keep_idx is None else tiers[keep_idx]
+            slots, rows, fresh = TieredKVCache._middle_sources(kept, old[2], old[3], keep_idx)
+            for key in a.backend_v:
+                if slots.numel():
+                    assert torch.equal(a.backend_v[key][:, :, slots.to(dev)], old[1][key][:, :, rows.to(dev)])
+                    if not evicts:
+                        assert torch.equal(a.backend_k[key][:, :, slots.to(dev)], old[0][key][:, :, rows.to(dev)])
+                if fresh.numel():
+                    assert torch.equal(a.backend_v[key][:, :, fresh.to(dev)], b.backend_v[key][:, :, fresh.to(dev)])
+                    assert torch.equal(a.backend_k[key][:, :, fresh.to(dev)], b.backend_k[key][:, :, fresh.to(dev)])
+                if evicts:
+                    assert torch.equal(a.backend_k[key], b.backend_k[key])
+        _append((inc, ref), 2, 2, 23, 122 + rnd, dev)
+    q = torch.randn(2, 8, 1, 128, generator=torch.Generator().manual_seed(4)).half().to(dev)
+    assert (inc.decode_attention(q, 0).float() - ref.decode_attention(q, 0).float()).abs().max().item() <= 2e-3
