@@ -11,7 +11,10 @@
 // middle, recent, then the chunk).  All 256 threads fetch a tile (thread =
 // one token x 32 channels) into double-buffered LDS (the next tile's global
 // loads fly while the current one is computed): fp16 K and V rows as they
-// are; middle-tier codes dequantized exactly as the reference does,
+// are, through registers; middle-tier codes and V scales by direct
+// global -> LDS loads into a staging area (each thread's load lands the bytes
+// that thread converts, so no barrier is needed and no register is held
+// across the compute), then dequantized exactly as the reference does,
 // fp16(code * scale), with three packed operations per pair of codes (72 + c
 // by one bit operation, - 72, * scale).  K and V rows keep channels in the
 // order the code conversion produces (1 5 0 4 3 7 2 6 within every 8
@@ -27,6 +30,7 @@
 #include <math.h>
 
 #include "fade_common.h"
+#include "lds_dma.h"
 
 namespace fade {
 namespace prefill {
@@ -140,6 +144,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   __shared__ __attribute__((aligned(16))) uint16_t kt[2][kKT][kKPitch];
   __shared__ __attribute__((aligned(16))) uint16_t vt[2][kKT][kVPitch];
+  // middle-tile staging: thread tid's 16 bytes of K / V codes at 16 tid, its
+  // token's V scale in dword tid (a 2-byte direct load fills one dword per lane)
+  __shared__ __attribute__((aligned(16))) uint8_t stg_k[kThreads * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t stg_v[kThreads * 16];
+  __shared__ __attribute__((aligned(16))) uint32_t stg_s[kThreads];
 
   // ---- tile fetch: thread = token r of the tile, channels 32*cp .. 32*cp+31 ----
   const int r = tid >> 2, cp = tid & 3;
@@ -165,64 +174,92 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int e = 0; e < 4; ++e) ksc[4 * i + e] = st[e];
   }
-  uint4 fk[4], fv[4];  // fetched K / V (fp16 rows: 64 bytes; middle codes: 16 bytes in fk[0] / fv[0])
-  int fmid = 0;
-  uint32_t fvs = 0;    // V scale of a middle token, as an fp16 pair
-  auto fetch = [&](int t) {
-    const TileRef tr = tile_of(t);
-    const int key = tr.base + r;
+  int fok = 0;  // this thread's staged middle row is a real token of the tile
+  // staging slots of this wave's lanes (a direct load writes lane l's bytes at base + l * size)
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+  const uint32_t stk = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_k[16 * 64 * wave])));
+  const uint32_t stv = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_v[16 * 64 * wave])));
+  const uint32_t sts = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_s[64 * wave])));
+  // Middle tile: codes and V scale to the staging area.  Nothing waits for
+  // these loads before store_mid(), so they fly during the current tile's compute.
+  auto fetch_mid = [&](const TileRef& tr) {
     const bool ok = r < tr.cnt;
-    fmid = tr.seg == 1;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) fk[i] = fv[i] = make_uint4(0, 0, 0, 0);
-    fvs = 0;
-    if (!ok) return;
-    if (tr.seg == 1) {
-      fk[0] = *reinterpret_cast<const uint4*>(kq + static_cast<int64_t>(key) * 64 + 16 * cp);
-      fv[0] = *reinterpret_cast<const uint4*>(vq + static_cast<int64_t>(key) * 64 + 16 * cp);
-      fvs = static_cast<uint32_t>(vsr[key]) * 0x00010001u;
-      return;
+    fok = ok;
+    const int key = tr.base + (ok ? r : tr.cnt - 1);  // rows past the tile: a valid row, zeroed in store_mid()
+    lds_dma16(kq + static_cast<int64_t>(key) * 64 + 16 * cp, stk);
+    lds_dma16(vq + static_cast<int64_t>(key) * 64 + 16 * cp, stv);
+    lds_dma2(vsr + key, sts);
+  };
+  // staged codes -> fp16(code * scale) rows of K and V in LDS buffer buf
+  auto store_mid = [&](int buf) {
+    // the staging loads are the only vector-memory operations in flight here
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    uint4 kraw = *reinterpret_cast<const uint4*>(&stg_k[16 * tid]);
+    uint4 vraw = *reinterpret_cast<const uint4*>(&stg_v[16 * tid]);
+    uint32_t vsb = stg_s[tid] & 0xFFFFu;
+    if (!fok) {
+      kraw = vraw = make_uint4(0, 0, 0, 0);
+      vsb = 0;
     }
-    const uint16_t* kp = tr.seg == 0 ? sk + key * sk_ss : (tr.seg == 2 ? rk + key * rk_ss : ck + key * ck_ss);
-    const uint16_t* vp = tr.seg == 0 ? sv + key * sv_ss : (tr.seg == 2 ? rv + key * rv_ss : cvp + key * cv_ss);
-    const uint4* k4 = reinterpret_cast<const uint4*>(kp + 32 * cp);
-    const uint4* v4 = reinterpret_cast<const uint4*>(vp + 32 * cp);
+    // codes -> fp16 72 + c -> c -> fp16(c * scale), already in the stored channel order
+    const uint32_t kw[4] = {kraw.x, kraw.y, kraw.z, kraw.w};
+    const uint32_t vw[4] = {vraw.x, vraw.y, vraw.z, vraw.w};
+    const f16x2 m72 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+    const f16x2 vs2 = __builtin_bit_cast(f16x2, vsb * 0x00010001u);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      fk[i] = k4[i];
-      fv[i] = v4[i];
+      uint32_t o[4];
+      u32x4 kd, vd;
+      nib_to_f16(kw[i], o);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        kd[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[e]) + m72) *
+                                                 __builtin_bit_cast(f16x2, ksc[4 * i + e]));
+      nib_to_f16(vw[i], o);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        vd[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[e]) + m72) * vs2);
+      *reinterpret_cast<u32x4*>(&kt[buf][r][32 * cp + 8 * i]) = kd;
+      *reinterpret_cast<u32x4*>(&vt[buf][r][32 * cp + 8 * i]) = vd;
     }
   };
-  auto store = [&](int buf) {
-    if (fmid) {
-      // codes -> fp16 72 + c -> c -> fp16(c * scale), already in the stored channel order
-      const uint32_t kw[4] = {fk[0].x, fk[0].y, fk[0].z, fk[0].w};
-      const uint32_t vw[4] = {fv[0].x, fv[0].y, fv[0].z, fv[0].w};
-      const f16x2 m72 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
-      const f16x2 vs2 = __builtin_bit_cast(f16x2, fvs);
+  // fp16 tile (sink, recent or chunk: a few per row): loaded and stored at once
+  auto load_store_f16 = [&](const TileRef& tr, int buf) {
+    uint4 fk[4], fv[4];
+    const int key = tr.base + r;
+    if (r < tr.cnt) {
+      const uint16_t* kp = tr.seg == 0 ? sk + key * sk_ss : (tr.seg == 2 ? rk + key * rk_ss : ck + key * ck_ss);
+      const uint16_t* vp = tr.seg == 0 ? sv + key * sv_ss : (tr.seg == 2 ? rv + key * rv_ss : cvp + key * cv_ss);
+      const uint4* k4 = reinterpret_cast<const uint4*>(kp + 32 * cp);
+      const uint4* v4 = reinterpret_cast<const uint4*>(vp + 32 * cp);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        uint32_t o[4];
-        u32x4 kd, vd;
-        nib_to_f16(kw[i], o);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          kd[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[e]) + m72) *
-                                                   __builtin_bit_cast(f16x2, ksc[4 * i + e]));
-        nib_to_f16(vw[i], o);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          vd[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[e]) + m72) * vs2);
-        *reinterpret_cast<u32x4*>(&kt[buf][r][32 * cp + 8 * i]) = kd;
-        *reinterpret_cast<u32x4*>(&vt[buf][r][32 * cp + 8 * i]) = vd;
+        fk[i] = k4[i];
+        fv[i] = v4[i];
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        *reinterpret_cast<u32x4*>(&kt[buf][r][32 * cp + 8 * i]) = to_stored(fk[i].x, fk[i].y, fk[i].z, fk[i].w);
-        *reinterpret_cast<u32x4*>(&vt[buf][r][32 * cp + 8 * i]) = to_stored(fv[i].x, fv[i].y, fv[i].z, fv[i].w);
-      }
+      for (int i = 0; i < 4; ++i) fk[i] = fv[i] = make_uint4(0, 0, 0, 0);
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<u32x4*>(&kt[buf][r][32 * cp + 8 * i]) = to_stored(fk[i].x, fk[i].y, fk[i].z, fk[i].w);
+      *reinterpret_cast<u32x4*>(&vt[buf][r][32 * cp + 8 * i]) = to_stored(fv[i].x, fv[i].y, fv[i].z, fv[i].w);
+    }
+  };
+  // Tile t into LDS buffer buf: fp16 tiles complete here; a middle tile only
+  // starts (returns true) and completes in store_mid().
+  auto begin_tile = [&](int t, int buf) {
+    const TileRef tr = tile_of(t);
+    if (tr.seg == 1) {
+      fetch_mid(tr);
+      return true;
+    }
+    load_store_f16(tr, buf);
+    return false;
   };
 
   // ---- query fragments: rows j0 + 16*mt + n16, B operand of S^T = K Q^T, stored channel order ----
@@ -337,14 +374,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
   };
 
-  fetch(0);
-  store(0);
+  if (begin_tile(0, 0)) store_mid(0);
   __syncthreads();
   for (int t = 0; t < n_tiles; ++t) {
     const int buf = t & 1;
-    if (t + 1 < n_tiles) fetch(t + 1);
+    // the next tile goes to the other buffer, last read by the previous tile's compute
+    const bool mid_next = t + 1 < n_tiles && begin_tile(t + 1, buf ^ 1);
     if (active) compute(t, buf);
-    if (t + 1 < n_tiles) store(buf ^ 1);
+    if (mid_next) store_mid(buf ^ 1);
     __syncthreads();
   }
 
