@@ -432,6 +432,17 @@ def pmc_pass(steps: int) -> int:
     return 0
 
 
+def prefill_pass(calls: int) -> int:
+    """Short run for ``rocprofv3 --pmc`` on the config-4 ragged prefill: ``calls`` launches."""
+    dev = torch.device("cuda:0")
+    plan, _, _ = prefill_case(dev)
+    for _ in range(calls):
+        plan.run()
+    torch.cuda.synchronize()
+    print(json.dumps({"prefill_pass": True, "prefill_calls": calls}))
+    return 0
+
+
 def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
     """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the decode kernel, scaled by
     what the same counters read for the copy kernel (which moves COPY_MIB each way)."""
@@ -486,6 +497,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="only the config-1 INT4 line")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="copy calibration + --steps decode calls, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--prefill-pass", action="store_true",
+                    help="--steps config-4 prefill calls only, for rocprofv3 --pmc SQ counters")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc output folders into " + os.path.relpath(TRAFFIC_FILE, ROOT))
     args = ap.parse_args()
@@ -500,6 +513,8 @@ def main() -> int:
         return 2
     if args.pmc_pass:
         return pmc_pass(args.steps)
+    if args.prefill_pass:
+        return prefill_pass(args.steps)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(dev)
