@@ -249,3 +249,29 @@ def require_f16(t: torch.Tensor, op: str) -> None:
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     """Scratch for one kernel family; zero-filled (the decode split counters start at zero)."""
     return torch.zeros(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def scratch(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Uninitialized scratch, for kernels that write every byte of it they read."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+_STREAM_WS: dict = {}
+
+
+def stream_workspace(nbytes: int, device: torch.device, stream: int) -> torch.Tensor:
+    """Zero-filled decode workspace shared by the calls on one stream.
+
+    Those calls run one after another and each leaves the workspace's split
+    counters at zero, so one buffer per (device, stream, size) serves them all
+    without a fill per call.  Buffers are kept for the life of the process (a
+    graph that captured one keeps a valid address).  Calls on different streams
+    get different buffers.
+    """
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, int(stream), max(int(nbytes), 1))
+    ws = _STREAM_WS.get(key)
+    if ws is None:
+        ws = torch.zeros(key[2], dtype=torch.uint8, device=torch.device("cuda", idx))
+        _STREAM_WS[key] = ws
+    return ws

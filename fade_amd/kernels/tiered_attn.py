@@ -185,7 +185,10 @@ class TieredDecodePlan:
     """Validated launch of the tiered decode kernel for fixed tensors.
 
     Holds references to every tensor it points at, the output and the
-    workspace; ``run()`` enqueues the kernels on the current stream.
+    workspace; ``run()`` enqueues the kernels on the current stream.  With
+    ``stream`` given, the plan uses the zero-filled workspace shared by the
+    calls on that stream (``_lib.stream_workspace``) instead of its own, and
+    must then run on that stream.
     """
 
     def __init__(
@@ -199,6 +202,7 @@ class TieredDecodePlan:
         n_splits: int = 0,
         kernel: int = 0,
         lens: Tensor | None = None,
+        stream: int | None = None,
     ) -> None:
         if q.dim() != 4 or q.shape[2] != 1:
             raise ValueError(f"q must be [B, Hq, 1, D], got {tuple(q.shape)}")
@@ -228,7 +232,8 @@ class TieredDecodePlan:
         lib = _lib.load()
         nb = ctypes.c_int64(0)
         _lib.check(lib.fade_tiered_decode_workspace_bytes(ctypes.byref(a), nb), "fade_tiered_decode_workspace_bytes")
-        self.workspace = _lib.workspace(nb.value, q.device)
+        self.workspace = (_lib.workspace(nb.value, q.device) if stream is None
+                          else _lib.stream_workspace(nb.value, q.device, stream))
         a.workspace, a.workspace_bytes = self.workspace.data_ptr(), self.workspace.numel()
         self.args = a
         self.out = out
@@ -259,7 +264,9 @@ def tiered_decode_attention(
     makes the batch ragged: row b attends to the first ``lens[b]`` rows of each
     tier, whose tensors are then padded capacities.
     """
-    return TieredDecodePlan(q, sink, mid, recent, sm_scale, n_splits=n_splits, kernel=kernel, lens=lens).run()
+    s = torch.cuda.current_stream(q.device).cuda_stream
+    plan = TieredDecodePlan(q, sink, mid, recent, sm_scale, n_splits=n_splits, kernel=kernel, lens=lens, stream=s)
+    return plan.run(s)
 
 
 __all__ = ["MiddleTier", "TieredDecodePlan", "paginate_middle", "tiered_decode_attention"]

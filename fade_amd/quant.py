@@ -101,7 +101,7 @@ def quant_k_int4(k: Tensor) -> tuple[Tensor, Tensor]:
     lib = _lib.load()
     nb = ctypes_i64()
     _lib.check(lib.fade_quant_k_int4_workspace_bytes(B, H, S, D, nb), "fade_quant_k_int4_workspace_bytes")
-    ws = _lib.workspace(nb.value, k.device)
+    ws = _lib.scratch(nb.value, k.device)  # column partials: written in full before they are read
     sb, sh, ss = _strides_bhs(k)
     _lib.call(
         "fade_quant_k_int4", k.data_ptr(), B, H, S, D, sb, sh, ss, packed.data_ptr(),

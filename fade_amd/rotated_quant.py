@@ -78,7 +78,7 @@ def quant_rotated_given(x_rot: Tensor, bits: int, axis: int, op: str = "quant_ro
         return packed, scale
     nb = ctypes.c_int64(0)
     _lib.check(_lib.load().fade_quant_rotated_workspace_bytes(B, H, S, D, axis, nb), op)
-    ws = _lib.workspace(nb.value, x_rot.device)
+    ws = _lib.scratch(nb.value, x_rot.device)  # column partials: written in full before they are read
     _lib.call(
         "fade_quant_rotated", x_rot.data_ptr(), B, H, S, D, bits, axis, packed.data_ptr(),
         scale.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(x_rot),

@@ -95,11 +95,47 @@ def test_tiered_decode_int4_plan_replays(dev):
     outs = [plan.run().clone() for _ in range(4)]
     torch.cuda.synchronize()
     ref = oatt.tiered_decode(q, k[:, :, :ns], v[:, :, :ns], omid, k[:, :, S - nr :], v[:, :, S - nr :])
+    # waves claim tiles in the order they free a stage, so the fp32 sums may
+    # differ between runs in their last bits: every run against the oracle
     for o in outs:
-        assert torch.equal(o, outs[0])
-    assert np.abs(outs[0].float().cpu().numpy() - ref).max() <= ATOL
+        assert (o.float() - outs[0].float()).abs().max().item() <= 1e-3
+        assert np.abs(o.float().cpu().numpy() - ref).max() <= ATOL
     counters = plan.workspace[: 2 * 8 * 4].view(torch.int32)
     assert int(counters.abs().sum()) == 0
+
+
+def test_tiered_decode_shared_stream_workspace(dev):
+    """tiered_decode_attention reuses one zero-filled workspace per (device, stream, size):
+    calls of several shapes in turn, then on a second stream, all match the oracle and leave
+    the shared counters at zero."""
+    from fade_amd import _lib
+
+    print("case decode shared stream workspace", flush=True)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    cases = []
+    for seed, (B, S) in enumerate([(2, 3000), (1, 700), (2, 3000), (3, 1500)]):
+        q, k, v, ns, nr = _case(B, 32, 8, S, 4, 64, seed=40 + seed)
+        mid, omid = _int4_mid(dev, k, v, ns, nr)
+        ref = oatt.tiered_decode(q, k[:, :, :ns], v[:, :, :ns], omid, k[:, :, S - nr :], v[:, :, S - nr :])
+        args = (t(q), (t(k[:, :, :ns]), t(v[:, :, :ns])), mid, (t(k[:, :, S - nr :]), t(v[:, :, S - nr :])))
+        cases.append((args, ref))
+    side = torch.cuda.Stream(dev)
+    for rnd in range(2):
+        for args, ref in cases:
+            if rnd == 0:
+                out = tiered_decode_attention(*args)
+            else:
+                side.wait_stream(torch.cuda.current_stream(dev))
+                with torch.cuda.stream(side):
+                    out = tiered_decode_attention(*args)
+                torch.cuda.current_stream(dev).wait_stream(side)
+            torch.cuda.synchronize()
+            assert np.abs(out.float().cpu().numpy() - ref).max() <= ATOL
+    shared = [ws for key, ws in _lib._STREAM_WS.items() if key[0] == torch.device(dev).index or key[0] == 0]
+    assert shared
+    for ws in shared:
+        n_pairs = 3 * 8  # the largest batch here: its counters sit at the front of the workspace
+        assert int(ws[: 4 * n_pairs].view(torch.int32).abs().sum()) == 0
 
 
 @pytest.mark.parametrize("n_splits", [1, 3, 64])

@@ -85,7 +85,8 @@ def test_reassign_device_decode_matches(dev):
     host.apply_tier_assignment(0, tiers)
     devc.apply_tier_assignment(0, tiers)
     q = torch.randn(2, 8, 1, 128, generator=torch.Generator().manual_seed(9)).half().to(dev)
-    assert torch.equal(host.decode_attention(q, 0), devc.decode_attention(q, 0))
+    # identical caches; the decode's tile claiming may change the fp32 sum order
+    assert (host.decode_attention(q, 0).float() - devc.decode_attention(q, 0).float()).abs().max().item() <= 1e-3
 
 
 def test_reassign_device_no_host_sync(dev):
