@@ -20,13 +20,25 @@
 // order the code conversion produces (1 5 0 4 3 7 2 6 within every 8
 // channels); the query and the output use the same order.
 //
-// Per tile and wave:
-//   S^T = K Q^T     f16 MFMA 16x16x32, A = K rows (16 keys), B = Q^T (16 rows);
-//                   lane (n, g), register i  <->  query row n, key 4g + i
-//   online softmax  row n's max/sum: lane-local over 16 keys, then 2 shuffles
-//   O += P V        f16 MFMA 16x16x32, A = P straight from the S^T registers
-//                   (key blocks paired), B = V rows via ds_read_b64_tr_b16
-// Each K and V fragment read from LDS feeds both M tiles.
+// Per tile and wave (one 32-row M tile; 32x32x16 f16 MFMAs, which on gfx950
+// run at twice the rate of 16x16x32):
+//   S^T = K Q^T     A = K rows (32 keys x 16 channels), B = Q^T (registers);
+//                   lane (n, h) = (query n, half h), register i <-> key
+//                   32 kb + 8 (i / 4) + 4 h + i % 4
+//   online softmax  a query's 64 scores: lane-local over 32, one exchange with
+//                   lane n ^ 32
+//   O += P V        A = P straight from the S^T registers: registers
+//                   8 (s & 1) .. + 7 of key block s >> 1 are the k slots of
+//                   k-step s; B = 16-byte reads of V^T rows
+//
+// V is kept transposed in LDS (row = channel, natural order) with key k at
+// position swap23(k) (bits 2 and 3 exchanged), so that the eight keys of one
+// PV k slot group are adjacent.  Middle tiles reach that layout without a
+// pass through fp16 rows: wave w stages the codes and scales of keys
+// 16 w .. 16 w + 15, and a ds_read_b64_tr_b4 hands each lane one channel of
+// those 16 keys, which it dequantizes (fp16(code * scale), as the reference)
+// into two 16-byte runs of its V^T row.  fp16 tiles (a few per row) are
+// written transposed directly.
 #include <math.h>
 
 #include "fade_common.h"
@@ -40,16 +52,17 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
 constexpr int kD = 128;
 constexpr int kThreads = 256;
 constexpr int kQB = 32;       // queries per workgroup
 constexpr int kKT = 64;       // keys per tile
 constexpr int kKPitch = 136;  // halves per K row in LDS (16-byte reads of 16 rows: distinct banks)
-constexpr int kVPitch = 144;  // halves per V row in LDS (tr16 reads of 4 rows x 4 chunks: distinct banks)
+constexpr int kVtPitch = 72;  // halves per V^T row in LDS (16-byte accesses of 8 consecutive rows: distinct banks)
 constexpr float kNegBig = -1.0e30f;
 constexpr float kTau = 8.0f;  // the running max moves only when a score exceeds it by kTau (log2)
 
@@ -94,9 +107,8 @@ __device__ __forceinline__ u32x4 to_stored(uint32_t d0, uint32_t d1, uint32_t d2
   return u32x4{__builtin_amdgcn_perm(d2, d0, 0x07060302u), __builtin_amdgcn_perm(d2, d0, 0x05040100u),
                __builtin_amdgcn_perm(d3, d1, 0x07060302u), __builtin_amdgcn_perm(d3, d1, 0x05040100u)};
 }
-// Channel of stored half h within an 8-channel group.
-// (1 5 0 4 3 7 2 6, one nibble per h)
-__device__ __forceinline__ int stored_channel(int h) { return (0x62734051 >> (4 * h)) & 0xF; }
+// Position of key k (0..63) of a tile in a V^T row: bits 2 and 3 exchanged.
+__host__ __device__ constexpr int swap23(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PParams p) {
   const int qb = blockIdx.x;
@@ -143,9 +155,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   };
 
   __shared__ __attribute__((aligned(16))) uint16_t kt[2][kKT][kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[2][kKT][kVPitch];
-  // middle-tile staging: thread tid's 16 bytes of K / V codes at 16 tid, its
-  // token's V scale in dword tid (a 2-byte direct load fills one dword per lane)
+  __shared__ __attribute__((aligned(16))) uint16_t vtt[2][kD][kVtPitch];
+  __shared__ __attribute__((aligned(16))) float rowf[4][32];  // per-wave factors of the 32 query rows
+  // middle-tile staging: thread tid's 16 bytes of K codes at 16 tid; keys
+  // 16 w + rho (rho < 16) in stg_v[1024 w ..], 16-byte unit u of row rho at
+  // unit 4 rho + (u ^ ((rho >> 1) & 3)); their V scales in dwords 64 w + l,
+  // key 16 w + (l & 15) (a 2-byte direct load fills one dword per lane)
   __shared__ __attribute__((aligned(16))) uint8_t stg_k[kThreads * 16];
   __shared__ __attribute__((aligned(16))) uint8_t stg_v[kThreads * 16];
   __shared__ __attribute__((aligned(16))) uint32_t stg_s[kThreads];
@@ -190,40 +205,71 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     fok = ok;
     const int key = tr.base + (ok ? r : tr.cnt - 1);  // rows past the tile: a valid row, zeroed in store_mid()
     lds_dma16(kq + static_cast<int64_t>(key) * 64 + 16 * cp, stk);
-    lds_dma16(vq + static_cast<int64_t>(key) * 64 + 16 * cp, stv);
-    lds_dma2(vsr + key, sts);
+    // V: lane l of wave w fills unit l of the wave's block: row rho = l >> 2,
+    // source unit (l & 3) ^ ((rho >> 1) & 3).  Rows past the tile read the last
+    // valid key (finite; their probabilities are zero).
+    const int vr = lane >> 2;
+    const int vk = 16 * wave + vr, sk2 = 16 * wave + (lane & 15);
+    lds_dma16(vq + static_cast<int64_t>(tr.base + (vk < tr.cnt ? vk : tr.cnt - 1)) * 64 + 16 * ((lane & 3) ^ ((vr >> 1) & 3)),
+              stv);
+    lds_dma2(vsr + tr.base + (sk2 < tr.cnt ? sk2 : tr.cnt - 1), sts);
   };
   // staged codes -> fp16(code * scale) rows of K and V in LDS buffer buf
   auto store_mid = [&](int buf) {
     // the staging loads are the only vector-memory operations in flight here
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     uint4 kraw = *reinterpret_cast<const uint4*>(&stg_k[16 * tid]);
-    uint4 vraw = *reinterpret_cast<const uint4*>(&stg_v[16 * tid]);
-    uint32_t vsb = stg_s[tid] & 0xFFFFu;
-    if (!fok) {
-      kraw = vraw = make_uint4(0, 0, 0, 0);
-      vsb = 0;
-    }
+    if (!fok) kraw = make_uint4(0, 0, 0, 0);
     // codes -> fp16 72 + c -> c -> fp16(c * scale), already in the stored channel order
     const uint32_t kw[4] = {kraw.x, kraw.y, kraw.z, kraw.w};
-    const uint32_t vw[4] = {vraw.x, vraw.y, vraw.z, vraw.w};
     const f16x2 m72 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
-    const f16x2 vs2 = __builtin_bit_cast(f16x2, vsb * 0x00010001u);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t o[4];
-      u32x4 kd, vd;
+      u32x4 kd;
       nib_to_f16(kw[i], o);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         kd[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[e]) + m72) *
                                                  __builtin_bit_cast(f16x2, ksc[4 * i + e]));
-      nib_to_f16(vw[i], o);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        vd[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[e]) + m72) * vs2);
       *reinterpret_cast<u32x4*>(&kt[buf][r][32 * cp + 8 * i]) = kd;
-      *reinterpret_cast<u32x4*>(&vt[buf][r][32 * cp + 8 * i]) = vd;
+    }
+    // V.  Scales of the wave's keys by row rho (low 16 bits of dword 64 w + rho).
+    uint32_t sc[16];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const uint4 d = *reinterpret_cast<const uint4*>(&stg_s[64 * wave + 4 * q4]);
+      sc[4 * q4] = d.x;
+      sc[4 * q4 + 1] = d.y;
+      sc[4 * q4 + 2] = d.z;
+      sc[4 * q4 + 3] = d.w;
+    }
+    // As source lane s' = n16 of group g this lane points the tr4 read at row
+    // rho(s') = swap23(o(s')), o(s') = 2 (s' & 3) + ((s' >> 2) & 1) + 8 (s' >> 3),
+    // channel unit cu = 4 q + g: lane n then receives channel 16 cu + (n ^ 1)
+    // of those rows, nibble s' <-> position offset o(s'), so the fp16 pairs
+    // come out as position pairs (2 j, 2 j + 1), rows (swap23(2 j), + 1).
+    const int so = swap23(2 * (n16 & 3) + ((n16 >> 2) & 1) + 8 * (n16 >> 3));
+    const uint8_t* vrow = &stg_v[1024 * wave + 64 * so];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int cu = 4 * q + g;
+      const i32x2 xv = __builtin_amdgcn_ds_read_tr4_b64_v2i32(reinterpret_cast<lds_i32x2*>(
+          const_cast<lds_u8*>((const lds_u8*)(vrow + 16 * ((cu >> 1) ^ ((so >> 1) & 3)) + 8 * (cu & 1)))));
+      const int ch = 16 * cu + (n16 ^ 1);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        uint32_t o[4];
+        nib_to_f16(static_cast<uint32_t>(xv[half]), o);
+        u32x4 vd;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int ra = swap23(8 * half + 2 * j);
+          const uint32_t s2 = __builtin_amdgcn_perm(sc[ra + 1], sc[ra], 0x05040100u);
+          vd[j] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[j]) + m72) * __builtin_bit_cast(f16x2, s2));
+        }
+        *reinterpret_cast<u32x4*>(&vtt[buf][ch][16 * wave + 8 * half]) = vd;
+      }
     }
   };
   // fp16 tile (sink, recent or chunk: a few per row): loaded and stored at once
@@ -244,10 +290,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
       for (int i = 0; i < 4; ++i) fk[i] = fv[i] = make_uint4(0, 0, 0, 0);
     }
+    const int pr = swap23(r);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       *reinterpret_cast<u32x4*>(&kt[buf][r][32 * cp + 8 * i]) = to_stored(fk[i].x, fk[i].y, fk[i].z, fk[i].w);
-      *reinterpret_cast<u32x4*>(&vt[buf][r][32 * cp + 8 * i]) = to_stored(fv[i].x, fv[i].y, fv[i].z, fv[i].w);
+      const uint32_t vw[4] = {fv[i].x, fv[i].y, fv[i].z, fv[i].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        vtt[buf][32 * cp + 8 * i + e][pr] = static_cast<uint16_t>(vw[e >> 1] >> (16 * (e & 1)));
     }
   };
   // Tile t into LDS buffer buf: fp16 tiles complete here; a middle tile only
@@ -262,115 +312,106 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     return false;
   };
 
-  // ---- query fragments: rows j0 + 16*mt + n16, B operand of S^T = K Q^T, stored channel order ----
+  // ---- query fragments: B operand of S^T = K Q^T; lane (n32, h) holds query
+  // row j0 + n32, channels 16 ks + 8 h .. + 7 in the stored order ----
+  const int n32 = lane & 31, h = lane >> 5;
   const bool active = wave < G;
-  const int64_t h = kvh * G + (active ? wave : 0);
-  f16x8 qf[2][4];
+  const int64_t hq = kvh * G + (active ? wave : 0);
+  f16x8 qf[8];
+  {
+    const int j = j0 + n32;
+    const uint16_t* qr = p.q + b * p.q_sb + hq * p.q_sh + static_cast<int64_t>(j < Sq ? j : Sq - 1) * p.q_ss;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int j = j0 + 16 * mt + n16;
-    const uint16_t* qr = p.q + b * p.q_sb + h * p.q_sh + static_cast<int64_t>(j < Sq ? j : Sq - 1) * p.q_ss;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const uint4 w = (active && j < Sq) ? *reinterpret_cast<const uint4*>(qr + 32 * ks + 8 * g) : make_uint4(0, 0, 0, 0);
-      qf[mt][ks] = __builtin_bit_cast(f16x8, to_stored(w.x, w.y, w.z, w.w));
+    for (int ks = 0; ks < 8; ++ks) {
+      const uint4 w = (active && j < Sq) ? *reinterpret_cast<const uint4*>(qr + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+      qf[ks] = __builtin_bit_cast(f16x8, to_stored(w.x, w.y, w.z, w.w));
     }
   }
 
-  f32x4 acc[2][8];
+  // O accumulators: acc[cb] lane (n32, h), register i <-> query row 8 (i / 4) + 4 h + i % 4,
+  // channel 32 cb + n32
+  f32x16 acc[4];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-    for (int c = 0; c < 8; ++c) acc[mt][c] = f32x4{0, 0, 0, 0};
-  float m_run[2] = {kNegBig, kNegBig}, l_run[2] = {0.0f, 0.0f};
+    for (int i = 0; i < 16; ++i) acc[cb][i] = 0.0f;
+  float m_run = kNegBig, l_run = 0.0f;  // of query row n32 (the same in both halves; l_run over this half's keys)
   const float sl2 = p.scale_log2;
   const float tau_raw = kTau / sl2;  // the lazy-rescale margin in raw score units
+  float* const rf = &rowf[wave][0];
 
   auto compute = [&](int t, int buf) {
     const TileRef tr = tile_of(t);
-    // S^T for both M tiles (raw scores q.k); each K fragment feeds both
-    f32x4 s[2][4];
-    const f32x4 zero4 = {0, 0, 0, 0};
+    // S^T (raw scores q.k) for key blocks kb = 0, 1
+    f32x16 s[2];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(&kt[buf][16 * kb + n16][32 * ks + 8 * g]);
-        s[0][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[0][ks], ks ? s[0][kb] : zero4, 0, 0, 0);
-        s[1][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[1][ks], ks ? s[1][kb] : zero4, 0, 0, 0);
+      for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const f16x8 a = *reinterpret_cast<const f16x8*>(&kt[buf][32 * kb + n32][16 * ks + 8 * h]);
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], s[kb], 0, 0, 0);
       }
+    }
     // every key of a full cache tile is visible to every query of the block
     const bool full = tr.seg != 3 && tr.cnt == kKT;
-    f16x8 pa[2][2];  // PV A operands: [M tile][key-block pair]
+    if (!full) {
+      const int jq = j0 + n32;
+      // key kk of the tile is visible when kk < cnt and, in the chunk, base + kk <= jq
+      const int lim = tr.seg == 3 ? (jq - tr.base + 1 < tr.cnt ? jq - tr.base + 1 : tr.cnt) : tr.cnt;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      float x[4][4];
-      if (full) {
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) x[kb][i] = s[mt][kb][i];
-      } else {
-        const int jq = j0 + 16 * mt + n16;  // this lane's query (column n16)
-        // key kk of the tile is visible when kk < cnt and, in the chunk, base + kk <= jq
-        const int lim = tr.seg == 3 ? (jq - tr.base + 1 < tr.cnt ? jq - tr.base + 1 : tr.cnt) : tr.cnt;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) x[kb][i] = 16 * kb + 4 * g + i < lim ? s[mt][kb][i] : -INFINITY;
-      }
-      float lmax = kNegBig;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-        lmax = fmaxf(fmaxf(lmax, fmaxf(x[kb][0], x[kb][1])), fmaxf(x[kb][2], x[kb][3]));
-      lmax = fmaxf(lmax, __shfl_xor(lmax, 16, 64));
-      lmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
-      // running max m_run in raw score units; probabilities exp2((x - m) * scale)
-      if (__builtin_amdgcn_ballot_w64(lmax - m_run[mt] > tau_raw) != 0) {
-        const float m_new = fmaxf(m_run[mt], lmax);
-        const float alpha = __builtin_amdgcn_exp2f((m_run[mt] - m_new) * sl2);
-        m_run[mt] = m_new;
-        l_run[mt] *= alpha;
-        // accumulator row 4g + i lives in lanes whose column n16 is that row
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float ai = __shfl(alpha, 4 * g + i, 64);
-#pragma unroll
-          for (int c = 0; c < 8; ++c) acc[mt][c][i] *= ai;
-        }
-      }
-      float ps = 0.0f;
-      _Float16 ph[4][4];
-      const float nm = -m_run[mt] * sl2;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(x[kb][i], sl2, nm));
-          ps += pv;
-          ph[kb][i] = static_cast<_Float16>(pv);
-        }
-      l_run[mt] += ps;
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp)
-        pa[mt][pp] = f16x8{ph[2 * pp][0], ph[2 * pp][1], ph[2 * pp][2], ph[2 * pp][3],
-                           ph[2 * pp + 1][0], ph[2 * pp + 1][1], ph[2 * pp + 1][2], ph[2 * pp + 1][3]};
+        for (int i = 0; i < 16; ++i)
+          if (32 * kb + 8 * (i >> 2) + 4 * h + (i & 3) >= lim) s[kb][i] = -INFINITY;
     }
-    // O += P V.  B operand via tr16 reads of V rows: source lane s of group g
-    // points at key 32 pp + 16 half + 4 g + (s >> 2), channels 16 c + 4 (s & 3);
-    // lane n then holds stored channel 16 c + n of the four keys.
-    const int vr0 = 4 * g + (n16 >> 2), vcol = 4 * (n16 & 3);
+    float lmax = kNegBig;
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            reinterpret_cast<lds_i16x4*>((__attribute__((address_space(3))) uint16_t*)&vt[buf][32 * pp + vr0][16 * c + vcol])));
-        const f16x4 hi = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            reinterpret_cast<lds_i16x4*>((__attribute__((address_space(3))) uint16_t*)&vt[buf][32 * pp + 16 + vr0][16 * c + vcol])));
-        const f16x8 bv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[0][pp], bv, acc[0][c], 0, 0, 0);
-        acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[1][pp], bv, acc[1][c], 0, 0, 0);
+      for (int i = 0; i < 16; i += 2) lmax = fmaxf(lmax, fmaxf(s[kb][i], s[kb][i + 1]));
+    lmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
+    // running max in raw score units; probabilities exp2((x - m) * scale)
+    if (__builtin_amdgcn_ballot_w64(lmax - m_run > tau_raw) != 0) {
+      const float m_new = fmaxf(m_run, lmax);
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * sl2);
+      m_run = m_new;
+      l_run *= alpha;
+      // the accumulator rows of this lane belong to other lanes' queries: via LDS
+      if (h == 0) rf[n32] = alpha;
+      __builtin_amdgcn_s_waitcnt(kLgkm0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 a4 = *reinterpret_cast<const f32x4*>(&rf[8 * q + 4 * h]);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[cb][4 * q + i] *= a4[i];
+      }
+    }
+    const float nm = -m_run * sl2;
+    float ps = 0.0f;
+    f16x8 pa[4];  // PV A operands: k-step s = registers 8 (s & 1) .. + 7 of key block s >> 1
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float pv = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + j], sl2, nm));
+          ps += pv;
+          pa[2 * kb + hf][j] = static_cast<_Float16>(pv);
+        }
+    l_run += ps;
+    // O += P V.  B operand: lane (n32, h) reads channel 32 cb + n32 at V^T
+    // positions 16 s + 8 h .. + 7 (keys 16 s + 8 (j >> 2) + 4 h + (j & 3)).
+#pragma unroll
+    for (int ks2 = 0; ks2 < 4; ++ks2)
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const f16x8 bv = *reinterpret_cast<const f16x8*>(&vtt[buf][32 * cb + n32][16 * ks2 + 8 * h]);
+        acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[ks2], bv, acc[cb], 0, 0, 0);
       }
   };
 
@@ -386,22 +427,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 
   if (!active) return;
-  // ---- normalize and store: accumulator lane (stored channel n16, g), register i <-> row 4g + i ----
-  const int ch = 8 * (n16 >> 3) + stored_channel(n16 & 7);
+  // ---- normalize and store: 1 / l of each query row through LDS ----
+  {
+    const float lt = l_run + __shfl_xor(l_run, 32, 64);
+    if (h == 0) rf[n32] = 1.0f / lt;
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    float l = l_run[mt];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 inv4 = *reinterpret_cast<const f32x4*>(&rf[8 * q + 4 * h]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float li = __shfl(l, 4 * g + i, 64);
-      const int j = j0 + 16 * mt + 4 * g + i;
-      if (j < Sq) {
-        uint16_t* orow = p.out + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(j) * p.o_ss;
-        const float inv = 1.0f / li;
+      for (int i = 0; i < 4; ++i) {
+        const int j = j0 + 8 * q + 4 * h + i;
+        if (j < Sq) {
+          uint16_t* orow = p.out + b * p.o_sb + hq * p.o_sh + static_cast<int64_t>(j) * p.o_ss;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) orow[16 * c + ch] = f2h(acc[mt][c][i] * inv);
+          for (int cb = 0; cb < 4; ++cb) orow[32 * cb + n32] = f2h(acc[cb][4 * q + i] * inv4[i]);
+        }
       }
     }
   }
