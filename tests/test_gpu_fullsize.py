@@ -1,0 +1,175 @@
+"""Parity at the configurations' full sizes (configs 1-4).
+
+The oracle is too slow for a whole configuration, so each test combines
+- properties that hold at any size: code range, the largest element of every
+  quantization group mapping to +-7, the dequantization error bound, split
+  invariance, host path == device path;
+- exact checks on slices the oracle finishes in seconds. Outputs are
+  independent per batch row, and K scales are per (row, head), so the oracle
+  run on one or two rows is exact for those rows of the full-size GPU run.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from fade_amd import quant as fq
+from fade_amd.cache import TieredKVCache
+from fade_amd.kernels import MiddleTier, tiered_decode_attention
+from fade_amd.kernels.prefill import tiered_prefill_attention
+from fade_amd.policy import _assign_one_layer
+from fade_amd.synthetic import exp_scores, kv_tensors
+from oracle import attention as oatt
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+ATOL = 2e-3
+
+
+def _codes(packed: torch.Tensor) -> torch.Tensor:
+    """Two's-complement nibbles (high nibble = even channel) -> int8 codes."""
+    hi = (packed >> 4).to(torch.int8)
+    lo = (packed & 15).to(torch.int8)
+    c = torch.stack((hi, lo), dim=-1).flatten(-2)
+    return (c ^ 8) - 8
+
+
+def _quant_properties(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, group_dim: int):
+    """Symmetric INT4 invariants at full size; group_dim = the reduced axis (2: per channel, 3: per token)."""
+    c = _codes(packed)
+    assert int(c.min()) >= -7 and int(c.max()) <= 7, "codes outside [-7, 7]"
+    xa = x.float().abs()
+    amax = xa.amax(dim=group_dim, keepdim=True)
+    at_max = (xa == amax) & (amax > 0)
+    assert bool((c.abs()[at_max] == 7).all()), "a group's largest element does not map to +-7"
+    deq = (c.half() * scale).float()
+    err = (x.float() - deq).abs()
+    bound = 0.52 * scale.float().expand_as(err)
+    assert bool((err <= bound + 1e-7).all()), f"dequantization error above 0.52 scale: {float((err - bound).max())}"
+
+
+def _mid_dict(kq, ks, vq, vs):
+    return {"fmt": "int4", "kq": kq, "ks": ks, "vq": vq, "vs": vs}
+
+
+def _decode_case(dev, B, Hkv, S, ns, nr, seed, rows, check_quant=True):
+    print(f"case full-size decode B={B} Hkv={Hkv} S={S} rows={rows}", flush=True)
+    q, k, v = kv_tensors(B, Hkv, S, 128, seed=seed, Hq=32)
+    km, vm = k[:, :, ns : S - nr], v[:, :, ns : S - nr]
+    kmg, vmg = km.to(dev), vm.to(dev)
+    kq, ks = fq.quant_k_int4(kmg)
+    vq, vs = fq.quant_v_int4(vmg)
+    if check_quant:
+        _quant_properties(kmg, kq, ks, group_dim=2)
+        _quant_properties(vmg, vq, vs, group_dim=3)
+    del kmg, vmg
+    t = lambda a: a.contiguous().to(dev)  # noqa: E731
+    sink = (t(k[:, :, :ns]), t(v[:, :, :ns]))
+    rec = (t(k[:, :, S - nr :]), t(v[:, :, S - nr :]))
+    mid = MiddleTier("int4", kq, vq, ks, vs)
+    qg = q.to(dev)
+    out = tiered_decode_attention(qg, sink, mid, rec)
+    one = tiered_decode_attention(qg, sink, mid, rec, n_splits=1)
+    torch.cuda.synchronize()
+    assert (out.float() - one.float()).abs().max().item() <= ATOL, "one split differs from the default splits"
+    qn, kn, vn = q.numpy(), k.numpy(), v.numpy()
+    for b in rows:
+        okq, oks = oq.quant_k_int4(kn[b : b + 1, :, ns : S - nr])
+        ovq, ovs = oq.quant_v_int4(vn[b : b + 1, :, ns : S - nr])
+        assert np.array_equal(kq[b : b + 1].cpu().numpy(), okq), f"row {b}: K codes differ from the oracle"
+        assert np.array_equal(ks[b : b + 1].cpu().numpy().view(np.uint16), oks.view(np.uint16)), f"row {b}: K scales"
+        assert np.array_equal(vq[b : b + 1].cpu().numpy(), ovq), f"row {b}: V codes differ from the oracle"
+        assert np.array_equal(vs[b : b + 1].cpu().numpy().view(np.uint16), ovs.view(np.uint16)), f"row {b}: V scales"
+        ref = oatt.tiered_decode(qn[b : b + 1], kn[b : b + 1, :, :ns], vn[b : b + 1, :, :ns],
+                                 _mid_dict(okq, oks, ovq, ovs), kn[b : b + 1, :, S - nr :], vn[b : b + 1, :, S - nr :])
+        err = np.abs(out[b : b + 1].float().cpu().numpy() - ref).max()
+        assert err <= ATOL, f"row {b}: decode max-abs error {err}"
+
+
+def test_config1_full_quant_and_decode(dev):
+    """Config 1 (B=16, Hkv=8, S=8192, sink 4, recent 64): quantizer invariants over the whole tier,
+    codes and scales of rows 0 and 15 bit-exact with the oracle, their decode within 2e-3."""
+    _decode_case(dev, 16, 8, 8192, 4, 64, seed=1001, rows=(0, 15))
+
+
+def test_config2_full_decode(dev):
+    """Config 2 (B=4, S=32768, sink 4, recent 256): row 3 against the oracle."""
+    _decode_case(dev, 4, 8, 32768, 4, 256, seed=1002, rows=(3,), check_quant=False)
+
+
+FIELDS = ("sink_k", "sink_v", "sink_pos", "fp16_k", "fp16_v", "fp16_pos", "int4_kq", "int4_ks", "int4_vq",
+          "int4_vs", "int4_pos")
+
+
+def test_config3_full_reassignment_device_equals_host(dev):
+    """Config 3 (B=8, Hkv=4, S=4096, balanced windows 4 / 64 / 400): the device reassignment leaves
+    every tier bit-identical to the host path, through both steps (fill the middle, then evict)."""
+    print("case full-size reassignment config 3", flush=True)
+    B, H, S, D = 8, 4, 4096, 128
+    _, k, v = kv_tensors(B, H, S, D, seed=1003, Hq=28)
+    kd, vd = k.to(dev), v.to(dev)
+    caches = []
+    for dev_path in (False, True):
+        c = TieredKVCache(n_sink=4, recent_window=64, int4_budget=400, int2_budget=0, head_dim=D, rope_theta=1e6)
+        c.device_reassign = dev_path
+        caches.append(c)
+    first = S - 64
+    tiers0 = _assign_one_layer(first, torch.zeros(first), 4, 64, None, 0)
+    tiers1 = _assign_one_layer(S, exp_scores(S, 1003), 4, 64, 400, 0)
+    for c in caches:
+        c.update(kd[:, :, :first], vd[:, :, :first], 0)
+        c.apply_tier_assignment(0, tiers0)
+        c.update(kd[:, :, first:], vd[:, :, first:], 0)
+    for what, tiers in (("after the tier fill", None), ("after eviction", tiers1)):
+        if tiers is not None:
+            for c in caches:
+                c.apply_tier_assignment(0, tiers)
+        host, devc = (cc._layers[0] for cc in caches)
+        for f in FIELDS:
+            x, y = getattr(host, f), getattr(devc, f)
+            assert (x is None) == (y is None), f"{what}: {f} present in one path only"
+            if x is not None:
+                assert x.shape == y.shape and torch.equal(x.cpu(), y.cpu()), f"{what}: {f} differs"
+        assert host.next_position == devc.next_position and host.sink_count == devc.sink_count
+    assert caches[1].get_seq_length(0) == 4 + 400 + 64
+
+
+def test_config4_full_prefill_extreme_rows(dev):
+    """Config 4 (32 rows, L ~ U[512, 16384], chunk 128): the full ragged batch in one launch; its
+    longest and shortest rows against a float32 reference on the GPU."""
+    print("case full-size prefill config 4", flush=True)
+    B, Hq, Hkv, D, Sq, ns, nr = 32, 32, 8, 128, 128, 4, 64
+    gen = torch.Generator().manual_seed(1004)
+    L = torch.randint(512, 16385, (B,), generator=gen)
+    nm = L - ns - nr
+    cap = int(nm.max())
+    g = torch.Generator(device=dev).manual_seed(1004)
+    rnd = lambda *shape: torch.randn(*shape, generator=g, device=dev).to(torch.float16)  # noqa: E731
+    kq = torch.randint(0, 256, (B, Hkv, cap, D // 2), generator=g, device=dev, dtype=torch.uint8)
+    vq = torch.randint(0, 256, (B, Hkv, cap, D // 2), generator=g, device=dev, dtype=torch.uint8)
+    ks = rnd(B, Hkv, 1, D).abs() * 0.3 + 0.05
+    vs = rnd(B, Hkv, cap, 1).abs() * 0.3 + 0.05
+    q = rnd(B, Hq, Sq, D)
+    chunk = (rnd(B, Hkv, Sq, D), rnd(B, Hkv, Sq, D))
+    sink = (rnd(B, Hkv, ns, D), rnd(B, Hkv, ns, D))
+    rec = (rnd(B, Hkv, nr, D), rnd(B, Hkv, nr, D))
+    lens = torch.stack([torch.full((B,), ns), nm, torch.full((B,), nr)], dim=1).to(torch.int32)
+    order = torch.argsort(L, descending=True).to(torch.int32)
+    out = tiered_prefill_attention(q, chunk, sink, MiddleTier("int4", kq, vq, ks, vs), rec, lens=lens, order=order)
+    torch.cuda.synchronize()
+    for b in (int(order[0]), int(order[-1])):
+        m = int(nm[b])
+        kmid = (_codes(kq[b, :, :m]).half() * ks[b]).float()
+        vmid = (_codes(vq[b, :, :m]).half() * vs[b, :, :m]).float()
+        kk = torch.cat([sink[0][b].float(), kmid, rec[0][b].float(), chunk[0][b].float()], dim=1)
+        vv = torch.cat([sink[1][b].float(), vmid, rec[1][b].float(), chunk[1][b].float()], dim=1)
+        kk = kk.repeat_interleave(Hq // Hkv, dim=0)
+        vv = vv.repeat_interleave(Hq // Hkv, dim=0)
+        sc = torch.matmul(q[b].float(), kk.transpose(-1, -2).contiguous()) / np.sqrt(D)
+        tot = int(L[b]) + Sq
+        # bottom-right causal: query j sees cache keys and chunk keys 0..j
+        keep = torch.arange(tot, device=dev)[None, :] <= (int(L[b]) + torch.arange(Sq, device=dev))[:, None]
+        sc = sc.masked_fill(~keep[None], float("-inf"))
+        ref = torch.matmul(torch.softmax(sc, dim=-1), vv)
+        err = (out[b].float() - ref).abs().max().item()
+        assert err <= ATOL, f"row {b} (L={int(L[b])}): prefill max-abs error {err}"
