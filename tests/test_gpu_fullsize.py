@@ -173,3 +173,63 @@ def test_config4_full_prefill_extreme_rows(dev):
         ref = torch.matmul(torch.softmax(sc, dim=-1), vv)
         err = (out[b].float() - ref).abs().max().item()
         assert err <= ATOL, f"row {b} (L={int(L[b])}): prefill max-abs error {err}"
+
+
+def _asym_codes(packed: torch.Tensor, bits: int) -> torch.Tensor:
+    """Unsigned codes: 4-bit high nibble first; 2-bit four per byte, first code in the top bits."""
+    shifts = (4, 0) if bits == 4 else (6, 4, 2, 0)
+    mask = (1 << bits) - 1
+    return torch.stack([(packed >> s) & mask for s in shifts], dim=-1).flatten(-2)
+
+
+def test_config2_full_asym_quant(dev):
+    """Config 2 in BASELINE's format (asymmetric group-32; K 4-bit, V 2-bit) over the whole middle
+    tier: codes in range, every group's min -> 0 and max -> 2^bits - 1, dequantization error within
+    half a step plus fp16 rounding; batch row 2 bit-exact with the oracle."""
+    print("case full-size asym quant config 2", flush=True)
+    _, k, v = kv_tensors(4, 8, 32768, 128, seed=1002, Hq=32)
+    ns, nr = 4, 256
+    for x, bits in ((k[:, :, ns:-nr], 4), (v[:, :, ns:-nr], 2)):
+        xg = x.contiguous().to(dev)
+        p, s, z = fq.quant_asym(xg, bits, 32)
+        qmax = (1 << bits) - 1
+        c = _asym_codes(p, bits).view(*xg.shape[:3], 4, 32)
+        xr = xg.view(*xg.shape[:3], 4, 32)
+        live = (s > 0).unsqueeze(-1)
+        mn = xr.amin(dim=-1, keepdim=True)
+        mx = xr.amax(dim=-1, keepdim=True)
+        assert int(c.max()) <= qmax
+        assert bool((c[(xr == mn) & live] == 0).all()), "a group's minimum does not map to code 0"
+        assert bool((c[(xr == mx) & live] == qmax).all()), f"a group's maximum does not map to {qmax}"
+        d = fq.dequant_asym(p, s, z, bits, 32).float()
+        err = (xg.float() - d).abs().view(*xg.shape[:3], 4, 32)
+        bound = 0.51 * s.float().unsqueeze(-1) + d.abs().view_as(err) * 2.0**-10 + 1e-6
+        assert bool((err <= bound).all()), f"dequantization error above bound: {float((err - bound).max())}"
+        op, os_, oz = oq.quant_asym_group(x[2:3].numpy(), bits, 32)
+        assert np.array_equal(p[2:3].cpu().numpy(), op)
+        assert np.array_equal(s[2:3].cpu().numpy().view(np.uint16), os_.view(np.uint16))
+        assert np.array_equal(z[2:3].cpu().numpy().view(np.uint16), oz.view(np.uint16))
+
+
+def test_config2_full_rotated_quant(dev):
+    """Config 2 through the rotated backend's fused rotate + quantize (2-bit K per channel, V per
+    token) over the whole middle tier: no code hits -2; one (row, head) slice against the
+    oracle's quantizer on an fp64 rotation (tie-aware, as the small-size tests)."""
+    from fade_amd import rotated_quant as frq
+    from test_gpu_quant import _check_fused_rotated
+
+    print("case full-size rotated quant config 2", flush=True)
+    _, k, _ = kv_tensors(4, 8, 32768, 128, seed=1002, Hq=32)
+    x = k[:, :, 4:-256].contiguous()
+    R = np.load(__file__.rsplit("/", 1)[0] + "/golden/rotation_d128_seed42.npy")
+    Rd = torch.from_numpy(R).to(dev)
+    xg = x.to(dev)
+    kp, ks = frq.rotated_quant_k(xg, Rd, 2)
+    vp, vs = frq.rotated_quant_v(xg, Rd, 2)
+    for packed in (kp, vp):
+        fields = torch.stack([(packed >> sh) & 3 for sh in (6, 4, 2, 0)])
+        assert not bool((fields == 2).any()), "a 2-bit code is -2"
+    b, h = 1, 5
+    xs = x[b : b + 1, h : h + 1].numpy()
+    _check_fused_rotated(xs, R, 2, "channel", kp[b : b + 1, h : h + 1].cpu().numpy(), ks[b : b + 1, h : h + 1].cpu().numpy())
+    _check_fused_rotated(xs, R, 2, "token", vp[b : b + 1, h : h + 1].cpu().numpy(), vs[b : b + 1, h : h + 1].cpu().numpy())
