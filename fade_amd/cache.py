@@ -362,11 +362,11 @@ class TieredKVCache(DynamicCache):
                 bk[:, :, :cap] = st._fp16_buf_k
                 bv[:, :, :cap] = st._fp16_buf_v
             st._fp16_buf_k, st._fp16_buf_v = bk, bv
-        rows = torch.arange(B, device=k.device)
-        for i in range(n):
-            slot = st.lens[:, 2].long() + i
-            st._fp16_buf_k[rows, :, slot] = k[:, :, i]
-            st._fp16_buf_v[rows, :, slot] = v[:, :, i]
+        # one scatter per tensor: element [b, i] of the index pair is row b's slot lens[b, 2] + i
+        rows = torch.arange(B, device=k.device)[:, None]
+        slots = st.lens[:, 2].long()[:, None] + torch.arange(n, device=k.device)[None, :]
+        st._fp16_buf_k[rows, :, slots] = k.permute(0, 2, 1, 3)
+        st._fp16_buf_v[rows, :, slots] = v.permute(0, 2, 1, 3)
         st.lens[:, 2] += n
         for r in st.lens_host:
             r[2] += n
@@ -1155,7 +1155,7 @@ class TieredKVCache(DynamicCache):
 
         st = self._layers[layer_idx]
         if st.lens is not None:
-            raise NotImplementedError("prefill_attention: a chunk over the ragged layout is not supported")
+            return self._prefill_attention_ragged(q, st, sm_scale)
         Sq = int(q.shape[2])
         sink, rest = self._fp16_split(st)
         if rest is None or int(rest[0].shape[-2]) < Sq:
@@ -1171,6 +1171,32 @@ class TieredKVCache(DynamicCache):
         if st.int4_kq is not None:
             mid = MiddleTier("int4", st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs)
         return tiered_prefill_attention(q, chunk, sink, mid, recent, sm_scale=sm_scale)
+
+    def _prefill_attention_ragged(self, q: Tensor, st: LayerState, sm_scale: float | None) -> Tensor:
+        """``prefill_attention`` on a ragged layer: row b's chunk is the last Sq tokens of
+        its own recent tier (where ``update`` appended them), at a different offset in
+        every row.  Those rows are gathered into the chunk tensor; the kernel reads the
+        padded tiers with the row's sink / middle / recent lengths, recent minus Sq."""
+        from .kernels.prefill import tiered_prefill_attention
+        from .kernels.tiered_attn import MiddleTier
+
+        Sq = int(q.shape[2])
+        if st.fp16_k is None or min(r[2] for r in st.lens_host) < Sq:
+            raise RuntimeError("prefill_attention: the chunk's K/V must be the last Sq tokens of every row's recent tier")
+        if st.int2_kq is not None or st.backend_k is not None or (st.int4_kq is not None and self.middle_v_bits != 4):
+            raise NotImplementedError(
+                "prefill_attention: the fused prefill reads fp16 tiers and the reference INT4 middle tier only"
+            )
+        B = int(q.shape[0])
+        rows = torch.arange(B, device=q.device)[:, None]
+        idx = (st.lens[:, 2].long() - Sq)[:, None] + torch.arange(Sq, device=q.device)[None, :]
+        chunk = (st.fp16_k[rows, :, idx].permute(0, 2, 1, 3).contiguous(),
+                 st.fp16_v[rows, :, idx].permute(0, 2, 1, 3).contiguous())
+        lens = st.lens.clone()
+        lens[:, 2] -= Sq
+        sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
+        mid = None if st.int4_kq is None else MiddleTier("int4", st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs)
+        return tiered_prefill_attention(q, chunk, sink, mid, (st.fp16_k, st.fp16_v), lens=lens, sm_scale=sm_scale)
 
     def decode_attention(self, q: Tensor, layer_idx: int, sm_scale: float | None = None) -> Tensor:
         """Single-token attention of ``q`` [B, Hq, 1, D] straight from this layer's tiers.

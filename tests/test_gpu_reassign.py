@@ -208,6 +208,48 @@ def test_ragged_layout_matches_single_rows(dev):
         assert (out[b : b + 1].float() - ref.float()).abs().max().item() <= 2e-3, b
 
 
+def test_ragged_layout_chunk_prefill_matches_single_rows(dev):
+    """A prefill chunk over the ragged layout: rows with different tier lengths after per-row
+    reassignment, a multi-token chunk appended to every row, then prefill_attention over the
+    ragged layer == each row alone (standard layout) within 2e-3; a later decode agrees too."""
+    print("case ragged chunk prefill", flush=True)
+    B, H, Hq, n_sink, recent, Sq = 3, 2, 8, 4, 16, 40
+    rag = TieredKVCache(n_sink=n_sink, recent_window=recent, int4_budget=None, int2_budget=0, head_dim=128)
+    rag.ragged_layout = True
+    singles = _single_row_caches(B, n_sink, recent)
+    g = torch.Generator().manual_seed(12)
+    k = (torch.randn(B, H, 200, 128, generator=g) * torch.exp(torch.randn(128, generator=g) * 0.5)).half().to(dev)
+    v = torch.randn(B, H, 200, 128, generator=g).half().to(dev)
+    rag.update(k, v, 0)
+    for b, c in enumerate(singles):
+        c.update(k[b : b + 1], v[b : b + 1], 0)
+    rng = np.random.default_rng(4)
+    budgets = [25, None, 70]
+    tiers = torch.full((B, 200), TIER_EVICT, dtype=torch.long)
+    for b in range(B):
+        t = _assign_one_layer(200, torch.from_numpy(rng.exponential(size=200).astype(np.float32)), n_sink, recent,
+                              budgets[b], 0)
+        tiers[b] = t
+        singles[b].apply_tier_assignment(0, t)
+    rag.apply_tier_assignment_per_sequence(0, tiers)
+    assert len({sum(r) for r in rag._layers[0].lens_host}) == B  # three different row lengths
+    kc = torch.randn(B, H, Sq, 128, generator=g).half().to(dev)
+    vc = torch.randn(B, H, Sq, 128, generator=g).half().to(dev)
+    rag.update(kc, vc, 0)
+    for b, c in enumerate(singles):
+        c.update(kc[b : b + 1], vc[b : b + 1], 0)
+    _check_rows(rag, singles, "chunk append")
+    q = torch.randn(B, Hq, Sq, 128, generator=g).half().to(dev)
+    out = rag.prefill_attention(q, 0)
+    for b, c in enumerate(singles):
+        ref = c.prefill_attention(q[b : b + 1], 0)
+        assert (out[b : b + 1].float() - ref.float()).abs().max().item() <= 2e-3, f"row {b}"
+    qd = torch.randn(B, Hq, 1, 128, generator=g).half().to(dev)
+    outd = rag.decode_attention(qd, 0)
+    for b, c in enumerate(singles):
+        assert (outd[b : b + 1].float() - c.decode_attention(qd[b : b + 1], 0).float()).abs().max().item() <= 2e-3
+
+
 def test_ragged_layout_rejects_shared_calls(dev):
     """A ragged layer refuses the shared-tier entry point and the checkpoint form."""
     rag = TieredKVCache(n_sink=2, recent_window=4, int4_budget=None, int2_budget=0, head_dim=128)
