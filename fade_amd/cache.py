@@ -35,6 +35,7 @@ from .quant import (
     quant_k_int4,
     quant_v_int4,
 )
+from .pages import PAGE_TOKENS
 from .rope import RopeScheme, Vanilla, rerope_gather
 
 DEFAULT_N_SINK: int = 4
@@ -97,6 +98,13 @@ class LayerState:
     # are padded capacities and row b's token j (position order) sits at position j
     lens: Tensor | None = None
     lens_host: list | None = None
+    # paged middle tier (TieredKVCache.page_pool, ragged layout only): the INT4 codes and
+    # V scales live in 64-token pages of ``mid_pool``; ``mid_table`` is the block table
+    # (int32 [B, pages per row]), ``mid_pages`` each row's page ids; int4_ks stays per row
+    mid_table: Tensor | None = None
+    mid_pages: list | None = None
+    mid_pool: object | None = None
+    mid_page_bytes: int = 0
 
     def total_seq_length(self) -> int:
         if self.lens_host is not None:
@@ -176,6 +184,9 @@ class TieredKVCache(DynamicCache):
         # and only tokens entering it are quantized (no requantization of dequantized
         # values); per-channel K scales still span the whole tier and are recomputed
         self.incremental_quant = False
+        # ragged layout: a fade_amd.pages.MiddlePagePool to keep the middle tier in
+        # 64-token pages (per-row memory instead of padding to the longest row)
+        self.page_pool = None
         self._last_reassign_counts = None
 
     # transformers 5.x defines a read-only ``Cache.batch_size``; the tiered cache
@@ -251,7 +262,7 @@ class TieredKVCache(DynamicCache):
         )
         return sum(
             int(t.element_size() * t.numel()) for s in self._layers for t in (getattr(s, k) for k in keys) if t is not None
-        )
+        ) + sum(s.mid_page_bytes for s in self._layers)
 
     @staticmethod
     def _layer_compressed_bytes(state: LayerState) -> int:
@@ -260,6 +271,7 @@ class TieredKVCache(DynamicCache):
             "int2_kq", "int2_vq", "int2_ks", "int2_vs",
         )
         total = sum(int(t.element_size() * t.numel()) for t in (getattr(state, k) for k in keys) if t is not None)
+        total += state.mid_page_bytes
         for d in (state.backend_k, state.backend_v):
             if isinstance(d, dict):
                 total += sum(int(v.element_size() * v.numel()) for v in d.values() if isinstance(v, Tensor))
@@ -429,7 +441,7 @@ class TieredKVCache(DynamicCache):
         """Ragged layout: row b = its sink | middle | recent tokens, zero-padded at the end
         to the longest row."""
         ref = st.fp16_k if st.fp16_k is not None else (st.sink_k if st.sink_k is not None else None)
-        if st.int4_kq is not None:
+        if st.int4_kq is not None or st.mid_table is not None:
             mk, mv = self._get_int4_dequant(st)
             ref = mk if ref is None else ref
         B, H, _, D = ref.shape
@@ -514,9 +526,10 @@ class TieredKVCache(DynamicCache):
             st.int4_k_deq = st.int4_v_deq = None
         if self.cache_dequant and st.int4_k_deq is not None:
             return st.int4_k_deq, st.int4_v_deq
-        k = dequant_int4(st.int4_kq, st.int4_ks)
+        kq, ks, vq, vs = self._mid_padded(st)
+        k = dequant_int4(kq, ks)
         if self.middle_v_bits == 4:
-            v = dequant_int4(st.int4_vq, st.int4_vs)
+            v = dequant_int4(vq, vs)
         else:
             n = int(st.int4_pos.shape[0])
             v = dequant_int2_trimmed(st.int4_vq, st.int4_vs, n, DEFAULT_INT2_GROUP_SIZE)
@@ -524,6 +537,35 @@ class TieredKVCache(DynamicCache):
             st.int4_k_deq, st.int4_v_deq = k, v
             st._dequant_age = 0
         return k, v
+
+    @staticmethod
+    def _mid_padded(st: LayerState):
+        """(K codes, K scale, V codes, V scale) of the INT4 middle tier as padded
+        [B, Hkv, S, ...] tensors: the stored ones, or for a paged layer gathered from its
+        pool (bit-identical to what the unpaged layout stores); None without a middle."""
+        if st.mid_table is not None:
+            kq, vq, vs = st.mid_pool.gather(st.mid_table, max(r[1] for r in st.lens_host))
+            return kq, st.int4_ks, vq, vs
+        if st.int4_kq is None:
+            return None
+        return st.int4_kq, st.int4_ks, st.int4_vq, st.int4_vs
+
+    def _release_layer_pages(self, st: LayerState) -> None:
+        if st.mid_pages is not None:
+            st.mid_pool.free([i for row in st.mid_pages for i in row])
+        st.mid_table = st.mid_pages = st.mid_pool = None
+        st.mid_page_bytes = 0
+
+    def release_pages(self) -> None:
+        """Return every page this cache's layers hold to their pool and drop those
+        layers' middle tiers (for a finished sequence batch whose pool serves others)."""
+        for st in self._layers:
+            if st.mid_table is not None:
+                self._release_layer_pages(st)
+                st.int4_ks = st.int4_k_deq = st.int4_v_deq = None
+                st.lens_host = [[ls, 0, lr] for ls, _, lr in st.lens_host]
+                st.lens = torch.tensor(st.lens_host, dtype=torch.int32, device=st.lens.device)
+                st._compressed_bytes = self._layer_compressed_bytes(st)
 
     def _get_int2_dequant(self, st: LayerState) -> tuple[Tensor, Tensor]:
         """fade/cache.py:861-876."""
@@ -924,6 +966,7 @@ class TieredKVCache(DynamicCache):
         if not isinstance(self._quant_backend, SymmetricINT4Backend) or self.middle_v_bits != 4 \
                 or st.int2_kq is not None or st.backend_k is not None:
             raise NotImplementedError("ragged_layout: the reference INT4 middle tier only (no INT2 tier / backend)")
+        midp = self._mid_padded(st)  # a paged middle is read back as the padded tensors
         if st.lens is None:
             if st.sink_k is not None:
                 sink, rec_start = (st.sink_k, st.sink_v), 0
@@ -935,7 +978,7 @@ class TieredKVCache(DynamicCache):
             if st.fp16_k is not None and rec_start < int(st.fp16_k.shape[-2]):
                 rec = (st.fp16_k[..., rec_start:, :], st.fp16_v[..., rec_start:, :])
             ns_c = 0 if sink is None else int(sink[0].shape[-2])
-            nm_c = 0 if st.int4_kq is None else int(st.int4_kq.shape[-2])
+            nm_c = 0 if midp is None else int(midp[0].shape[-2])
             nr_c = 0 if rec is None else int(rec[0].shape[-2])
             S = ns_c + nm_c + nr_c
             pos_parts = [p for p in (
@@ -949,15 +992,16 @@ class TieredKVCache(DynamicCache):
             sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
             rec = None if st.fp16_k is None else (st.fp16_k, st.fp16_v)
             ns_c = 0 if sink is None else int(sink[0].shape[-2])
-            nm_c = 0 if st.int4_kq is None else int(st.int4_kq.shape[-2])
+            nm_c = 0 if midp is None else int(midp[0].shape[-2])
             nr_c = 0 if rec is None else int(rec[0].shape[-2])
             row_len = [sum(r) for r in st.lens_host]
             S = max(row_len)
             table_rows = S
-        ref = next(t for t in (None if sink is None else sink[0], None if rec is None else rec[0], st.int4_kq)
+        mkq = None if midp is None else midp[0]
+        ref = next(t for t in (None if sink is None else sink[0], None if rec is None else rec[0], mkq)
                    if t is not None)
         B, H = int(ref.shape[0]), int(ref.shape[1])
-        D = 2 * int(ref.shape[-1]) if ref is st.int4_kq else int(ref.shape[-1])
+        D = 2 * int(ref.shape[-1]) if ref is mkq else int(ref.shape[-1])
         dev = ref.device
         if st.lens is not None:
             pos_old = torch.arange(max(S, 1), dtype=torch.long, device=dev)
@@ -996,6 +1040,15 @@ class TieredKVCache(DynamicCache):
         cs = max(r[0] for r in new_lens)
         cm = max(r[1] for r in new_lens)
         cr = max(r[2] for r in new_lens)
+        pool = self.page_pool
+        if pool is not None:  # refuse before any state changes
+            if (pool.n_kv_heads, pool.head_dim) != (H, D):
+                raise ValueError(f"page pool holds {pool.n_kv_heads} KV heads x {pool.head_dim}, the layer {H} x {D}")
+            need = sum(-(-r[1] // PAGE_TOKENS) for r in new_lens)
+            held = 0 if st.mid_pool is not pool else sum(len(r) for r in st.mid_pages)
+            if need > pool.n_free + held:
+                raise RuntimeError(f"page pool exhausted: layer {layer_idx} needs {need} pages, "
+                                   f"{pool.n_free + held} available")
         kd = dict(dtype=torch.float16, device=dev)
         out_sink = (torch.zeros(B, H, cs, D, **kd), torch.zeros(B, H, cs, D, **kd)) if cs else None
         cap = max(DEFAULT_FP16_PREALLOC, cr)
@@ -1018,7 +1071,7 @@ class TieredKVCache(DynamicCache):
             a.sink_k, a.sink_v = sink[0].data_ptr(), sink[1].data_ptr()
             a.sink_sb, a.sink_sh, a.sink_ss = sink[0].stride()[:3]
         if nm_c:
-            mids = [t.contiguous() for t in (st.int4_kq, st.int4_ks, st.int4_vq, st.int4_vs)]
+            mids = [t.contiguous() for t in midp]
             a.mid_kq, a.mid_ks, a.mid_vq, a.mid_vs = (t.data_ptr() for t in mids)
         if rec is not None:
             a.rec_k, a.rec_v = rec[0].data_ptr(), rec[1].data_ptr()
@@ -1045,6 +1098,13 @@ class TieredKVCache(DynamicCache):
             st.int4_vq, st.int4_vs = quant_v_int4(mid[1])
         else:
             st.int4_kq = st.int4_vq = st.int4_ks = st.int4_vs = None
+        # the old pages were read above (stream order), so they can be handed out again
+        self._release_layer_pages(st)
+        if pool is not None and st.int4_kq is not None:
+            st.mid_table, st.mid_pages = pool.store(st.int4_kq, st.int4_vq, st.int4_vs, [r[1] for r in new_lens])
+            st.mid_pool = pool
+            st.mid_page_bytes = pool.page_bytes * sum(len(r) for r in st.mid_pages)
+            st.int4_kq = st.int4_vq = st.int4_vs = None
         st.sink_pos = st.fp16_pos = st.int4_pos = None
         st.backend_k = st.backend_v = st.backend_pos = None
         st.int2_kq = st.int2_vq = st.int2_ks = st.int2_vs = st.int2_pos = None
@@ -1200,7 +1260,8 @@ class TieredKVCache(DynamicCache):
         lens = st.lens.clone()
         lens[:, 2] -= Sq
         sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
-        mid = None if st.int4_kq is None else MiddleTier("int4", st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs)
+        midp = self._mid_padded(st)
+        mid = None if midp is None else MiddleTier("int4", midp[0], midp[2], midp[1], midp[3])
         return tiered_prefill_attention(q, chunk, sink, mid, (st.fp16_k, st.fp16_v), lens=lens, sm_scale=sm_scale)
 
     def decode_attention(self, q: Tensor, layer_idx: int, sm_scale: float | None = None) -> Tensor:
@@ -1215,7 +1276,11 @@ class TieredKVCache(DynamicCache):
 
         st = self._layers[layer_idx]
         if st.lens is not None:
-            if st.int4_kq is not None:
+            if st.mid_table is not None:  # paged: the kernel reads the pool through the block table
+                pool = st.mid_pool
+                mid = MiddleTier("int4", pool.k_codes, pool.v_codes, st.int4_ks, pool.v_scale,
+                                 length=max(r[1] for r in st.lens_host), pages=st.mid_table)
+            elif st.int4_kq is not None:
                 mid = MiddleTier("int4", st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs)
             else:  # the ragged kernel needs a middle format: one zero row no row reads (lens 0)
                 B, H = int(q.shape[0]), int((st.fp16_k if st.fp16_k is not None else st.sink_k).shape[1])
