@@ -93,6 +93,7 @@ class DecodeArgs(ctypes.Structure):
         ("workspace", _p),
         ("workspace_bytes", _i64),
         ("lens", _p),
+        ("deterministic", _i32),
     ]
 
 

@@ -151,6 +151,7 @@ Params to_params(const fade_decode_args* a) {
   p.mid.page_stride = m.pages != nullptr ? m.page_stride : 0;
   p.total = total_tokens(a);
   p.lens = a->lens;
+  p.deterministic = a->deterministic;
   return p;
 }
 

@@ -54,6 +54,7 @@ struct Params {
   int64_t tiles_per_split;  // tiles (either kind) per split
   uint32_t* counters;       // [B*Hkv] finished splits; zero between calls
   const int32_t* lens;      // optional [B][3] per-row sink / middle / recent lengths
+  int32_t deterministic;    // INT4 kernel: fixed round-robin tile order instead of claims
 };
 
 // Signed symmetric code of channel d in a packed row (fade/quant.py:26-43,

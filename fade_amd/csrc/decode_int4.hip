@@ -208,8 +208,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   // Tiles of the split: the first two of each wave are t0 + wave and
   // t0 + NW + wave; after that waves claim tiles t0 + 2 NW + c in order
   // through an LDS counter, so that a wave that runs faster (e.g. the older
-  // wave of a SIMD, which wins issue arbitration) takes more of them.
+  // wave of a SIMD, which wins issue arbitration) takes more of them.  With
+  // p.deterministic, wave w walks t0 + w, t0 + w + NW, ... instead, so the
+  // order of every fp32 sum is fixed.
   const int n = p.n_splits;
+  const bool det = p.deterministic != 0;
   __shared__ int claim_s;
   if (tid == 0) claim_s = 0;
 
@@ -851,9 +854,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     else packed_tile(cur, sp);
     __builtin_amdgcn_s_waitcnt(kLgkm0);  // every LDS read of this stage has returned
     __builtin_amdgcn_wave_barrier();
-    int c = 0;
-    if (lane == 0) c = __hip_atomic_fetch_add(&claim_s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    const int64_t nt = t0 + 2 * kWaves + __builtin_amdgcn_readfirstlane(c);
+    int64_t nt;
+    if (det) {  // wave w walks tiles t0 + w, t0 + w + NW, ... : cur's successor's successor
+      nt = cur + 2 * kWaves;
+    } else {
+      int c = 0;
+      if (lane == 0) c = __hip_atomic_fetch_add(&claim_s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      nt = t0 + 2 * kWaves + __builtin_amdgcn_readfirstlane(c);
+    }
     if (nt < t1) issue(nt, st);
     return nt;
   };

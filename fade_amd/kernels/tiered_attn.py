@@ -203,6 +203,7 @@ class TieredDecodePlan:
         kernel: int = 0,
         lens: Tensor | None = None,
         stream: int | None = None,
+        deterministic: bool | None = None,
     ) -> None:
         if q.dim() != 4 or q.shape[2] != 1:
             raise ValueError(f"q must be [B, Hq, 1, D], got {tuple(q.shape)}")
@@ -229,6 +230,9 @@ class TieredDecodePlan:
         a.sink, a.mid, a.recent = _fp16_tier(sink), _mid_tier(mid), _fp16_tier(recent)
         a.n_splits, a.kernel = int(n_splits), int(kernel)
         a.lens = _lib.ptr(lens)
+        if deterministic is None:
+            deterministic = torch.are_deterministic_algorithms_enabled()
+        a.deterministic = int(bool(deterministic))
         lib = _lib.load()
         nb = ctypes.c_int64(0)
         _lib.check(lib.fade_tiered_decode_workspace_bytes(ctypes.byref(a), nb), "fade_tiered_decode_workspace_bytes")
@@ -255,6 +259,7 @@ def tiered_decode_attention(
     n_splits: int = 0,
     kernel: int = 0,
     lens: Tensor | None = None,
+    deterministic: bool | None = None,
 ) -> Tensor:
     """Decode attention of ``q`` [B,Hq,1,D] over the tiered cache; returns fp16 [B,Hq,1,D].
 
@@ -263,9 +268,14 @@ def tiered_decode_attention(
     ``lens`` [B, 3] (sink, middle, recent tokens per row; device or host int)
     makes the batch ragged: row b attends to the first ``lens[b]`` rows of each
     tier, whose tensors are then padded capacities.
+    ``deterministic`` (default: ``torch.are_deterministic_algorithms_enabled()``)
+    makes repeated calls on the same inputs bitwise identical; otherwise the
+    INT4 kernel's waves claim tiles as they finish, and results can differ in
+    the last bits between calls.
     """
     s = torch.cuda.current_stream(q.device).cuda_stream
-    plan = TieredDecodePlan(q, sink, mid, recent, sm_scale, n_splits=n_splits, kernel=kernel, lens=lens, stream=s)
+    plan = TieredDecodePlan(q, sink, mid, recent, sm_scale, n_splits=n_splits, kernel=kernel, lens=lens, stream=s,
+                            deterministic=deterministic)
     return plan.run(s)
 
 

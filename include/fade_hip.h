@@ -265,6 +265,11 @@ typedef struct fade_decode_args {
                                   the padded capacity of its tensors; every row >= 1 token).
                                   NULL: every row has the tiers' full lengths.  Ragged rows
                                   need the matrix-core INT4 kernel (SYM / ASYM formats). */
+  int32_t deterministic;       /* nonzero: bitwise-reproducible results.  The matrix-core INT4
+                                  kernel's waves then walk their split's tiles in a fixed
+                                  round-robin order instead of claiming them as they finish
+                                  (the order of the fp32 sums then no longer depends on timing);
+                                  the other kernels are deterministic either way. */
 } fade_decode_args;
 
 /* Replaces dequantize + torch.cat (fade/cache.py:683-842) + SDPA and the

@@ -403,6 +403,41 @@ def test_tiered_decode_paged_middle(dev, fmt):
         assert np.abs(out[b : b + 1] - ref).max() <= ATOL, b
 
 
+@pytest.mark.parametrize("fmt", ["int4", "asym"])
+def test_tiered_decode_deterministic_repeats(dev, fmt):
+    """deterministic=True (or torch.use_deterministic_algorithms): repeated calls give
+    bitwise-identical outputs, still within the oracle's tolerance, and the paged and
+    padded ragged layouts of the same tokens give bitwise-identical outputs too."""
+    from fade_amd.kernels.tiered_attn import paginate_middle
+
+    print(f"case decode deterministic {fmt}", flush=True)
+    ns_c, mc, nr_c, B = 4, 1500, 64, 3
+    S = ns_c + mc + nr_c
+    q, k, v, _, _ = _case(B, 32, 8, S, ns_c, nr_c, seed=91)
+    mid, omid = _int4_mid(dev, k, v, ns_c, nr_c) if fmt == "int4" else _asym_mid(dev, k, v, ns_c, nr_c, 4, 4)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    sink = (t(k[:, :, :ns_c]), t(v[:, :, :ns_c]))
+    rec = (t(k[:, :, S - nr_c :]), t(v[:, :, S - nr_c :]))
+    qd = t(q)
+    outs = [tiered_decode_attention(qd, sink, mid, rec, n_splits=2, deterministic=True).clone() for _ in range(6)]
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    ref = oatt.tiered_decode(q, k[:, :, :ns_c], v[:, :, :ns_c], omid, k[:, :, S - nr_c :], v[:, :, S - nr_c :])
+    assert np.abs(outs[0].float().cpu().numpy() - ref).max() <= ATOL
+    prev = torch.are_deterministic_algorithms_enabled()
+    torch.use_deterministic_algorithms(True, warn_only=True)
+    try:
+        assert torch.equal(tiered_decode_attention(qd, sink, mid, rec, n_splits=2), outs[0])
+    finally:
+        torch.use_deterministic_algorithms(prev)
+    lens = np.array([[4, 1500, 64], [2, 700, 30], [4, 65, 1]], dtype=np.int32)
+    paged = paginate_middle(mid, lens[:, 1], order=np.random.default_rng(1).permutation(int(sum(-(-x // 64) for x in lens[:, 1]))))
+    out_p = [tiered_decode_attention(qd, sink, paged, rec, lens=t(lens), n_splits=2, deterministic=True) for _ in range(3)]
+    out_r = tiered_decode_attention(qd, sink, mid, rec, lens=t(lens), n_splits=2, deterministic=True)
+    for o in out_p:
+        assert torch.equal(o, out_r)
+
+
 def test_tiered_decode_hip_graph_replays(dev):
     """Decode captured in a HIP graph: every replay, with eager work and synchronizations in
     between (a new query written in place), matches the eager call on the same inputs (to the

@@ -97,6 +97,23 @@ def test_paged_middle_matches_unpaged(dev):
     _close(plain.decode_attention(q, 0), paged.decode_attention(q, 0), 1e-3, "decode after the second")
 
 
+def test_paged_decode_bitwise_equal_when_deterministic(dev):
+    """With torch.use_deterministic_algorithms, decode through the pages equals decode of
+    the padded layout bit for bit (same tiles, same fixed summation order)."""
+    print("case paged decode deterministic", flush=True)
+    plain, paged = _pair(dev)
+    _append((plain, paged), 350, 31, dev)
+    _reassign((plain, paged), [None, 90, 200], 32)
+    q = torch.randn(B, HQ, 1, D, generator=torch.Generator().manual_seed(33)).half().to(dev)
+    prev = torch.are_deterministic_algorithms_enabled()
+    torch.use_deterministic_algorithms(True, warn_only=True)
+    try:
+        a, b = plain.decode_attention(q, 0), paged.decode_attention(q, 0)
+        assert torch.equal(a, b) and torch.equal(b, paged.decode_attention(q, 0))
+    finally:
+        torch.use_deterministic_algorithms(prev)
+
+
 def test_paged_decode_matches_materialized_fp32(dev):
     """Decode through the block table against fp32 attention over each row's own
     materialized tokens (GQA: query head h reads KV head h // (Hq / Hkv))."""
