@@ -257,22 +257,32 @@ def scratch(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-_STREAM_WS: dict = {}
+_STREAM_WS: dict = {}  # (device, stream, B * Hkv) -> the current zero-filled buffer
+_STREAM_WS_OUTGROWN: list = []  # replaced buffers, kept alive for graphs that captured them
 
 
-def stream_workspace(nbytes: int, device: torch.device, stream: int) -> torch.Tensor:
+def stream_workspace(nbytes: int, device: torch.device, stream: int, pairs: int) -> torch.Tensor:
     """Zero-filled decode workspace shared by the calls on one stream.
 
-    Those calls run one after another and each leaves the workspace's split
-    counters at zero, so one buffer per (device, stream, size) serves them all
-    without a fill per call.  Buffers are kept for the life of the process (a
-    graph that captured one keeps a valid address).  Calls on different streams
-    get different buffers.
+    The decode workspace holds the split counters in its first
+    round256(4 * pairs) bytes (pairs = B * Hkv) and the partial results right
+    after them.  Every call leaves its counters at zero, so calls with the same
+    ``pairs`` can share one buffer whatever their other sizes: their partials
+    never reach the counter region.  Calls with another ``pairs`` get another
+    buffer (their partials could land where these counters sit).  Calls on one
+    stream run in order; different streams get different buffers.  A buffer
+    too small for a call is replaced by a zero-filled one of at least twice
+    its size; the old one is kept for the life of the process, as every buffer
+    is (a graph that captured one keeps a valid address).
     """
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    key = (idx, int(stream), max(int(nbytes), 1))
+    key = (idx, int(stream), int(pairs))
+    need = max(int(nbytes), 1)
     ws = _STREAM_WS.get(key)
-    if ws is None:
-        ws = torch.zeros(key[2], dtype=torch.uint8, device=torch.device("cuda", idx))
+    if ws is None or ws.numel() < need:
+        if ws is not None:
+            _STREAM_WS_OUTGROWN.append(ws)
+            need = max(need, 2 * ws.numel())
+        ws = torch.zeros(need, dtype=torch.uint8, device=torch.device("cuda", idx))
         _STREAM_WS[key] = ws
     return ws

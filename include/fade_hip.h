@@ -257,8 +257,13 @@ typedef struct fade_decode_args {
   int32_t n_splits;            /* 0 = choose automatically */
   int32_t kernel;              /* 0 = auto, 1 = portable VALU kernel, 2 = matrix-core kernels
                                   only, 3 = the general matrix-core kernel (no INT4 fast path) */
-  void* workspace;             /* zero-filled before its first use; every call leaves its
-                                  split counters at zero again */
+  void* workspace;             /* zero-filled before its first use.  Its first
+                                  round256(4*B*Hkv) bytes hold per-(row, kv head) split
+                                  counters, which every call leaves at zero again; partial
+                                  results follow them.  Later calls with the same B*Hkv can
+                                  reuse it as it is, whatever their other sizes; before a call
+                                  with another B*Hkv, zero its first round256(4*B*Hkv) bytes
+                                  (an earlier call's partials may lie there). */
   int64_t workspace_bytes;
   const int32_t* lens;         /* optional device [B][3]: sink, middle, recent tokens of each
                                   row (ragged batch; each at most the tier's len, which is then

@@ -105,15 +105,16 @@ def test_tiered_decode_int4_plan_replays(dev):
 
 
 def test_tiered_decode_shared_stream_workspace(dev):
-    """tiered_decode_attention reuses one zero-filled workspace per (device, stream, size):
-    calls of several shapes in turn, then on a second stream, all match the oracle and leave
-    the shared counters at zero."""
+    """tiered_decode_attention shares one zero-filled workspace per (device, stream, B*Hkv):
+    calls of several shapes in turn (same B*Hkv with different split layouts, a longer row
+    that outgrows its buffer, other B*Hkv), then on a second stream, all match the oracle
+    and leave every buffer's counters at zero."""
     from fade_amd import _lib
 
     print("case decode shared stream workspace", flush=True)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     cases = []
-    for seed, (B, S) in enumerate([(2, 3000), (1, 700), (2, 3000), (3, 1500)]):
+    for seed, (B, S) in enumerate([(2, 3000), (1, 700), (2, 9000), (2, 3000), (3, 1500), (10, 600), (2, 1200)]):
         q, k, v, ns, nr = _case(B, 32, 8, S, 4, 64, seed=40 + seed)
         mid, omid = _int4_mid(dev, k, v, ns, nr)
         ref = oatt.tiered_decode(q, k[:, :, :ns], v[:, :, :ns], omid, k[:, :, S - nr :], v[:, :, S - nr :])
@@ -131,11 +132,10 @@ def test_tiered_decode_shared_stream_workspace(dev):
                 torch.cuda.current_stream(dev).wait_stream(side)
             torch.cuda.synchronize()
             assert np.abs(out.float().cpu().numpy() - ref).max() <= ATOL
-    shared = [ws for key, ws in _lib._STREAM_WS.items() if key[0] == torch.device(dev).index or key[0] == 0]
-    assert shared
-    for ws in shared:
-        n_pairs = 3 * 8  # the largest batch here: its counters sit at the front of the workspace
-        assert int(ws[: 4 * n_pairs].view(torch.int32).abs().sum()) == 0
+    shared = {key: ws for key, ws in _lib._STREAM_WS.items() if key[0] == torch.device(dev).index or key[0] == 0}
+    assert {key[2] for key in shared} >= {8, 16, 24, 80}
+    for key, ws in shared.items():  # the counters of B*Hkv pairs sit at the front of the buffer
+        assert int(ws[: 4 * key[2]].view(torch.int32).abs().sum()) == 0
 
 
 @pytest.mark.parametrize("n_splits", [1, 3, 64])
