@@ -5,8 +5,10 @@
 // and to chunk tokens 0..j (bottom-right causal, as the model's SDPA over
 // the reference's materialized tiers, fade/cache.py:347-379,683-842).
 //
-// Workgroup = (32-query block, kv head, batch row); wave w serves query head
-// kvh*G + w (G <= 4), its 32 query rows as two 16-row M tiles.  The row's key
+// Workgroup = (32-query block and head pass, kv head, batch row); wave w
+// serves query head kvh*G + 4*pass + w (G = Hq/Hkv <= 8: one pass of up to 4
+// heads for G <= 4, two passes for G = 5..8), its 32 query rows as one 32-row
+// M tile.  The row's key
 // sequence is walked in 64-token tiles that never straddle a tier (sink,
 // middle, recent, then the chunk).  All 256 threads fetch a tile (thread =
 // one token x 32 channels) into double-buffered LDS (the next tile's global
@@ -74,7 +76,8 @@ struct Tier {
 
 struct PParams {
   int64_t B, Hq, Hkv, Sq;
-  int G;
+  int G;       // query heads per kv head (Hq / Hkv), <= 8
+  int passes;  // workgroups per (query block, kv head): ceil(G / 4)
   const uint16_t* q;
   int64_t q_sb, q_sh, q_ss;
   uint16_t* out;
@@ -111,7 +114,8 @@ __device__ __forceinline__ u32x4 to_stored(uint32_t d0, uint32_t d1, uint32_t d2
 __host__ __device__ constexpr int swap23(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PParams p) {
-  const int qb = blockIdx.x;
+  const int qb = blockIdx.x / p.passes;
+  const int h0 = 4 * (blockIdx.x - qb * p.passes);  // first query head (within the group) of this workgroup
   const int64_t kvh = blockIdx.y;
   int64_t b = blockIdx.z;
   if (p.order) {
@@ -121,7 +125,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, g = lane >> 4;
-  const int G = p.G;
+  const int G = p.G - h0 < 4 ? p.G - h0 : 4;  // query heads this workgroup serves
   const int64_t bkv = b * p.Hkv + kvh;
   // per-row tier lengths, clamped to the padded capacities (no read past a tier)
   auto clampi = [](int x, int64_t cap) { return x < 0 ? 0 : (x > cap ? static_cast<int>(cap) : x); };
@@ -316,7 +320,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // row j0 + n32, channels 16 ks + 8 h .. + 7 in the stored order ----
   const int n32 = lane & 31, h = lane >> 5;
   const bool active = wave < G;
-  const int64_t hq = kvh * G + (active ? wave : 0);
+  const int64_t hq = kvh * p.G + h0 + (active ? wave : 0);
   f16x8 qf[8];
   {
     const int j = j0 + n32;
@@ -476,8 +480,8 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   if (a->D != kD) return einval("fade_tiered_prefill_attn: head_dim must be %d, got %lld", kD, (long long)a->D);
   if (a->B <= 0 || a->Hq <= 0 || a->Hkv <= 0 || a->Sq <= 0)
     return einval("fade_tiered_prefill_attn: B, Hq, Hkv and Sq must be positive");
-  if (a->Hq % a->Hkv != 0 || a->Hq / a->Hkv > 4)
-    return einval("fade_tiered_prefill_attn: needs Hq %% Hkv == 0 and Hq/Hkv <= 4 (got %lld/%lld)",
+  if (a->Hq % a->Hkv != 0 || a->Hq / a->Hkv > 8)
+    return einval("fade_tiered_prefill_attn: needs Hq %% Hkv == 0 and Hq/Hkv <= 8 (got %lld/%lld)",
                   (long long)a->Hq, (long long)a->Hkv);
   if (a->B > 65535 || a->Hkv > 65535 || a->Sq > (1 << 24)) return einval("fade_tiered_prefill_attn: shape too large");
   if (a->q == nullptr || a->out == nullptr || a->lens == nullptr)
@@ -502,6 +506,7 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   p.Hkv = a->Hkv;
   p.Sq = a->Sq;
   p.G = static_cast<int>(a->Hq / a->Hkv);
+  p.passes = (p.G + 3) / 4;
   p.q = static_cast<const uint16_t*>(a->q);
   p.q_sb = a->q_sb; p.q_sh = a->q_sh; p.q_ss = a->q_ss;
   p.out = static_cast<uint16_t*>(a->out);
@@ -520,7 +525,8 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   p.ks = static_cast<const uint16_t*>(m.k_scale);
   p.vq = static_cast<const uint8_t*>(m.v_codes);
   p.vs = static_cast<const uint16_t*>(m.v_scale);
-  const dim3 grid(static_cast<unsigned>(cdiv(a->Sq, kQB)), static_cast<unsigned>(a->Hkv), static_cast<unsigned>(a->B));
+  const dim3 grid(static_cast<unsigned>(cdiv(a->Sq, kQB) * p.passes), static_cast<unsigned>(a->Hkv),
+                  static_cast<unsigned>(a->B));
   hipLaunchKernelGGL(prefill_kernel, grid, dim3(kThreads), 0, as_stream(stream), p);
   return check_launch("fade_tiered_prefill_attn");
 }

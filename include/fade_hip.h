@@ -288,7 +288,7 @@ int fade_tiered_decode_attn(const fade_decode_args* args, void* stream);
  * query j of row b sees cache tokens and chunk tokens 0..j.  Tier tensors are
  * padded along S (row b uses the first lens[3b+0..2] tokens of sink / middle /
  * recent); the middle tier is FADE_MID_SYM 4-bit or FADE_MID_NONE.  D = 128,
- * Hq/Hkv <= 4.  `order` (optional, device int32 [B]) lists batch rows in the
+ * Hq/Hkv <= 8.  `order` (optional, device int32 [B]) lists batch rows in the
  * order their workgroups are dispatched (longest first balances the tail).
  * Replaces the reference's prefill path: update() returning the materialized
  * tiers (fade/cache.py:347-379,683-842) followed by causal SDPA in the model. */

@@ -75,6 +75,9 @@ def _ragged(dev, B, Hq, Hkv, Sq, rows, seed, with_mid=True):
         (2, 8, 2, 40, [(4, 100, 64), (0, 0, 5)]),  # Sq not a multiple of 32; a row without middle
         (2, 8, 4, 17, [(1, 63, 1), (4, 64, 64)]),  # G=2, tile-boundary lengths
         (1, 4, 4, 64, [(0, 1, 0)]),  # MHA, one middle token
+        (2, 28, 4, 70, [(4, 500, 64), (2, 130, 20)]),  # G=7 (Qwen2.5-7B heads): two head passes
+        (1, 40, 8, 33, [(4, 200, 10)]),  # G=5: a second pass of one head
+        (1, 16, 2, 96, [(4, 300, 64)]),  # G=8
     ],
 )
 def test_tiered_prefill_ragged(dev, B, Hq, Hkv, Sq, rows):
