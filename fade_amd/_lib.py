@@ -257,7 +257,7 @@ def scratch(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-_STREAM_WS: dict = {}  # (device, stream, B * Hkv) -> the current zero-filled buffer
+_STREAM_WS: dict = {}  # (device, stream, counter slots) -> the current zero-filled buffer
 _STREAM_WS_OUTGROWN: list = []  # replaced buffers, kept alive for graphs that captured them
 
 
@@ -265,10 +265,11 @@ def stream_workspace(nbytes: int, device: torch.device, stream: int, pairs: int)
     """Zero-filled decode workspace shared by the calls on one stream.
 
     The decode workspace holds the split counters in its first
-    round256(4 * pairs) bytes (pairs = B * Hkv) and the partial results right
-    after them.  Every call leaves its counters at zero, so calls with the same
-    ``pairs`` can share one buffer whatever their other sizes: their partials
-    never reach the counter region.  Calls with another ``pairs`` get another
+    round256(4 * pairs) bytes (pairs = B * Hkv * ceil((Hq / Hkv) / 4), one per
+    kv pair and head pass) and the partial results right after them.  Every
+    call leaves its counters at zero, so calls with the same ``pairs`` can
+    share one buffer whatever their other sizes: their partials never reach
+    the counter region.  Calls with another ``pairs`` get another
     buffer (their partials could land where these counters sit).  Calls on one
     stream run in order; different streams get different buffers.  A buffer
     too small for a call is replaced by a zero-filled one of at least twice

@@ -30,16 +30,18 @@ void plan_splits(const fade_decode_args* a, int tile, int64_t* n_splits, int64_t
 
 int64_t round256(int64_t x) { return ((x + 255) / 256) * 256; }
 
-// Workspace: [counters: B*Hkv u32][ml: rows*n*2 f32][acc: rows*n*kD f32], rows
-// covering both partial layouts (B*Hq per query head, or B*Hkv*4).
+// Workspace: [counters: B*Hkv*P u32][ml: rows*n*2 f32][acc: rows*n*kD f32], rows
+// covering both partial layouts (B*Hq per query head, or B*Hkv*4*P); P =
+// ceil((Hq/Hkv) / 4) head passes of the INT4 kernel.
 struct WsLayout {
   int64_t counters, ml, acc, total;
 };
 WsLayout ws_layout(const fade_decode_args* a, int64_t n) {
-  const int64_t rows = a->B * (a->Hq > a->Hkv * 4 ? a->Hq : a->Hkv * 4);
+  const int64_t P = (a->Hq / a->Hkv + 3) / 4;
+  const int64_t rows = a->B * (a->Hq > a->Hkv * 4 * P ? a->Hq : a->Hkv * 4 * P);
   WsLayout w;
   w.counters = 0;
-  w.ml = round256(a->B * a->Hkv * 4);
+  w.ml = round256(a->B * a->Hkv * P * 4);
   w.acc = w.ml + round256(rows * n * 2 * 4);
   w.total = w.acc + rows * n * kD * 4;
   return w;
@@ -152,6 +154,7 @@ Params to_params(const fade_decode_args* a) {
   p.total = total_tokens(a);
   p.lens = a->lens;
   p.deterministic = a->deterministic;
+  p.passes = static_cast<int>((p.G + 3) / 4);
   return p;
 }
 
@@ -178,7 +181,7 @@ Plan make_plan(const fade_decode_args* a, const Params& p) {
     // One machine-wide wave of resident workgroups; tiles of either kind cost
     // about the same bytes (8 KB), so splits take equal tile counts.
     const int64_t nT = int4_tiles(p);
-    const int64_t pairs = a->B * a->Hkv;
+    const int64_t pairs = a->B * a->Hkv * p.passes;  // workgroups per split
     int64_t want = a->n_splits > 0 ? a->n_splits : (int4_resident_wgs(p) + pairs / 2) / pairs;
     if (want > nT) want = nT;
     if (want < 1) want = 1;
@@ -218,7 +221,7 @@ FADE_API int fade_tiered_decode_attn(const fade_decode_args* a, void* stream) {
                   p.mid.fmt);
   if ((a->lens != nullptr || a->mid.pages != nullptr) && pl.k != Kern::kInt4)
     return einval("fade_tiered_decode_attn: per-row lengths and paged middle tiers need the matrix-core INT4 "
-                  "kernel (middle tier FADE_MID_SYM or FADE_MID_ASYM, GQA <= 4)");
+                  "kernel (middle tier FADE_MID_SYM or FADE_MID_ASYM, GQA <= 8)");
   const WsLayout ws = ws_layout(a, pl.n);
   if (a->workspace == nullptr || a->workspace_bytes < ws.total)
     return einval("fade_tiered_decode_attn: workspace too small (%lld < %lld bytes)",

@@ -55,6 +55,7 @@ struct Params {
   uint32_t* counters;       // [B*Hkv] finished splits; zero between calls
   const int32_t* lens;      // optional [B][3] per-row sink / middle / recent lengths
   int32_t deterministic;    // INT4 kernel: fixed round-robin tile order instead of claims
+  int passes;               // INT4 kernel: head passes per kv head, ceil(G / 4): 1 or 2
 };
 
 // Signed symmetric code of channel d in a packed row (fade/quant.py:26-43,

@@ -180,13 +180,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   constexpr int kOps = S::kOps, kOpsF16 = S::kOpsF16, kMeta = S::kMeta;
   constexpr int kRowK = 16 * KB, kRowV = 16 * VB;  // packed row bytes of one token
   const int split = blockIdx.x;
-  const int64_t kvh = blockIdx.y, b = blockIdx.z;
+  // blockIdx.y = (kv head, head pass): a pass serves up to 4 of the kv head's
+  // G query heads, from head h0 of the group (G = 5..8 takes two passes)
+  const int pl2 = p.passes - 1;  // log2 of the pass count (1 or 2 passes)
+  const int64_t kvh = blockIdx.y >> pl2, b = blockIdx.z;
+  const int h0 = 4 * static_cast<int>(blockIdx.y & pl2);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, g = lane >> 4;
   const int hq = n16 >> 2, sq = n16 & 3;  // head / sub-tile of this lane's scores
-  const int G = p.G;
-  const int64_t bkv = b * p.Hkv + kvh;
+  const int G = p.G - h0 < kHeads ? p.G - h0 : kHeads;  // query heads of this pass
+  const int64_t bkv = b * p.Hkv + kvh;                    // the kv pair: tier addressing
+  const int64_t slot = (bkv << pl2) + (h0 >> 2);          // split counter / partials of this pass
   // Mc: rows of the middle tensors per (batch row, kv head); M, ns, F: this
   // row's middle, sink and fp16 token counts (per-row lengths when given,
   // clamped to the capacities)
@@ -391,7 +396,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   // ---- prologue: query rows (and K scales) first, then the first two tiles ----
   {
     const uint32_t qa = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&qraw_s[wave][0])));
-    if (wave < G) lds_dma4(p.q + b * p.q_sb + (kvh * G + wave) * p.q_sh + 2 * lane, qa);
+    if (wave < G) lds_dma4(p.q + b * p.q_sb + (kvh * p.G + h0 + wave) * p.q_sh + 2 * lane, qa);
     else if (wave < kHeads) qraw_s[wave][lane] = 0u;
     if (!ASYM && wave < kHeads) {
       const uint32_t ka = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&ksraw_s[wave][0])));
@@ -925,9 +930,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
       L += red_l[w][h] * exp2f(red_m[w][h] - Mh);
     }
     if (n == 1) {
-      p.out[b * p.o_sb + (kvh * G + h) * p.o_sh + d] = f2h(o / L);
+      p.out[b * p.o_sb + (kvh * p.G + h0 + h) * p.o_sh + d] = f2h(o / L);
     } else {
-      const int64_t pi = (bkv * n + split) * 4 + h;
+      const int64_t pi = (slot * n + split) * 4 + h;
       store_agent(&p.ws_acc[pi * kD + d], o);
       if (d == 0) {
         store_agent(&p.ws_ml[2 * pi], Mh);
@@ -946,7 +951,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
   __syncthreads();
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&p.counters[bkv], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(&p.counters[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last_s = prev == static_cast<uint32_t>(n - 1);
   }
   __syncthreads();
@@ -955,7 +960,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     // thread tid merges items (head, channel) tid + e * kThreads; the loads of
     // a batch of 16 splits for all its items issue before any is used
     constexpr int kB = 16, kE = (kHeads * kD + kThreads - 1) / kThreads;
-    const int64_t p0 = bkv * n * 4;
+    const int64_t p0 = slot * n * 4;
     float Mh[kE], o[kE], L[kE];
 #pragma unroll
     for (int e = 0; e < kE; ++e) {
@@ -1001,10 +1006,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
     for (int e = 0; e < kE; ++e) {
       const int idx = tid + e * kThreads;
-      if (idx < G * kD) p.out[b * p.o_sb + (kvh * G + (idx >> 7)) * p.o_sh + (idx & (kD - 1))] = f2h(o[e] / L[e]);
+      if (idx < G * kD)
+        p.out[b * p.o_sb + (kvh * p.G + h0 + (idx >> 7)) * p.o_sh + (idx & (kD - 1))] = f2h(o[e] / L[e]);
     }
   }
-  if (tid == 0) __hip_atomic_store(&p.counters[bkv], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(&p.counters[slot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 bool aligned(const void* x, uintptr_t a) { return (reinterpret_cast<uintptr_t>(x) & (a - 1)) == 0; }
@@ -1018,7 +1024,9 @@ bool fp16_tier_ok(const Fp16Tier& t) {
 
 bool int4_supports(const Params& p) {
   const MidTier& m = p.mid;
-  if (m.len <= 0 || p.G > 4) return false;
+  // G = 5..8 runs as two head passes (the kv tiles are read once per pass):
+  // only for per-row lengths or pages, which the other kernels do not read
+  if (m.len <= 0 || p.G > 8 || (p.G > kHeads && p.lens == nullptr && m.pages == nullptr)) return false;
   const bool bits_ok = (m.k_bits == 4 || m.k_bits == 2) && (m.v_bits == 4 || m.v_bits == 2);
   if (m.fmt == FADE_MID_SYM) {
     if (!bits_ok) return false;
@@ -1093,7 +1101,8 @@ int int4_resident_wgs(const Params& p) {
 }
 
 int launch_int4(const Params& p, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv), static_cast<unsigned>(p.B));
+  const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv * p.passes),
+                  static_cast<unsigned>(p.B));
   const Choice c = packed_kernel(p);
   hipLaunchKernelGGL(c.k, grid, dim3(64 * c.waves), 0, st, p);
   return check_launch("fade_tiered_decode_attn(packed)");

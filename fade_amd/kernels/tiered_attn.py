@@ -237,7 +237,7 @@ class TieredDecodePlan:
         nb = ctypes.c_int64(0)
         _lib.check(lib.fade_tiered_decode_workspace_bytes(ctypes.byref(a), nb), "fade_tiered_decode_workspace_bytes")
         self.workspace = (_lib.workspace(nb.value, q.device) if stream is None
-                          else _lib.stream_workspace(nb.value, q.device, stream, B * Hkv))
+                          else _lib.stream_workspace(nb.value, q.device, stream, B * Hkv * -(-(Hq // Hkv) // 4)))
         a.workspace, a.workspace_bytes = self.workspace.data_ptr(), self.workspace.numel()
         self.args = a
         self.out = out

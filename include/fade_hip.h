@@ -258,18 +258,20 @@ typedef struct fade_decode_args {
   int32_t kernel;              /* 0 = auto, 1 = portable VALU kernel, 2 = matrix-core kernels
                                   only, 3 = the general matrix-core kernel (no INT4 fast path) */
   void* workspace;             /* zero-filled before its first use.  Its first
-                                  round256(4*B*Hkv) bytes hold per-(row, kv head) split
-                                  counters, which every call leaves at zero again; partial
-                                  results follow them.  Later calls with the same B*Hkv can
-                                  reuse it as it is, whatever their other sizes; before a call
-                                  with another B*Hkv, zero its first round256(4*B*Hkv) bytes
-                                  (an earlier call's partials may lie there). */
+                                  round256(4*B*Hkv*P) bytes (P = 1 for Hq/Hkv <= 4, else 2)
+                                  hold per-(row, kv head, head pass) split counters, which
+                                  every call leaves at zero again; partial results follow
+                                  them.  Later calls with the same B*Hkv*P can reuse it as it
+                                  is, whatever their other sizes; before a call with another
+                                  B*Hkv*P, zero its first round256(4*B*Hkv*P) bytes (an
+                                  earlier call's partials may lie there). */
   int64_t workspace_bytes;
   const int32_t* lens;         /* optional device [B][3]: sink, middle, recent tokens of each
                                   row (ragged batch; each at most the tier's len, which is then
                                   the padded capacity of its tensors; every row >= 1 token).
                                   NULL: every row has the tiers' full lengths.  Ragged rows
-                                  need the matrix-core INT4 kernel (SYM / ASYM formats). */
+                                  need the matrix-core INT4 kernel (SYM / ASYM formats; for
+                                  Hq/Hkv = 5..8 it runs two head passes). */
   int32_t deterministic;       /* nonzero: bitwise-reproducible results.  The matrix-core INT4
                                   kernel's waves then walk their split's tiles in a fixed
                                   round-robin order instead of claiming them as they finish

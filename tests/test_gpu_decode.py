@@ -322,6 +322,40 @@ def _row_slice_mid(omid, b, lm):
     return out
 
 
+@pytest.mark.parametrize("Hq,Hkv,fmt", [(28, 4, "int4"), (20, 4, "int4"), (16, 2, "asym"), (56, 8, "int4")])
+def test_tiered_decode_ragged_paged_gqa_5_to_8(dev, Hq, Hkv, fmt):
+    """GQA groups of 5-8 query heads (Qwen2.5-7B's 28/4, 20/4, 16/2, 56/8) with per-row
+    lengths and a paged middle tier: the INT4 kernel runs two head passes per kv head.
+    Each row against the oracle over its own tokens; paged == padded bit for bit in
+    deterministic mode; repeated plans on one stream share a workspace."""
+    from fade_amd.kernels.tiered_attn import paginate_middle
+
+    print(f"case decode ragged/paged GQA {Hq}/{Hkv} {fmt}", flush=True)
+    ns_c, mc, nr_c, B = 4, 700, 64, 3
+    S = ns_c + mc + nr_c
+    q, k, v, _, _ = _case(B, Hq, Hkv, S, ns_c, nr_c, seed=95 + Hq)
+    mid, omid = _int4_mid(dev, k, v, ns_c, nr_c) if fmt == "int4" else _asym_mid(dev, k, v, ns_c, nr_c, 4, 4)
+    lens = np.array([[4, 700, 64], [1, 129, 7], [4, 0, 33]], dtype=np.int32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    sink = (t(k[:, :, :ns_c]), t(v[:, :, :ns_c]))
+    rec = (t(k[:, :, S - nr_c :]), t(v[:, :, S - nr_c :]))
+    n_pages = int(sum(-(-int(x) // 64) for x in lens[:, 1]))
+    paged = paginate_middle(mid, lens[:, 1], order=np.random.default_rng(2).permutation(n_pages))
+    out_r = tiered_decode_attention(t(q), sink, mid, rec, lens=t(lens), deterministic=True)
+    out_p = tiered_decode_attention(t(q), sink, paged, rec, lens=t(lens), deterministic=True)
+    assert torch.equal(out_r, out_p)
+    out = out_r.float().cpu().numpy()
+    for b, (ls, lm, lr) in enumerate(lens):
+        ref = oatt.tiered_decode(
+            q[b : b + 1], k[b : b + 1, :, :ls], v[b : b + 1, :, :ls], _row_slice_mid(omid, b, lm),
+            k[b : b + 1, :, S - nr_c : S - nr_c + lr], v[b : b + 1, :, S - nr_c : S - nr_c + lr],
+        )
+        assert np.abs(out[b : b + 1] - ref).max() <= ATOL, b
+    for n_splits in (1, 5):  # other split counts, claims on: still within the oracle's tolerance
+        o = tiered_decode_attention(t(q), sink, paged, rec, lens=t(lens), n_splits=n_splits)
+        assert (o.float() - out_r.float()).abs().max().item() <= 1e-3
+
+
 @pytest.mark.parametrize("fmt", ["int4", "asym42"])
 @pytest.mark.parametrize("n_splits", [0, 1, 7])
 def test_tiered_decode_ragged_lens(dev, fmt, n_splits):
