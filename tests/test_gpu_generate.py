@@ -20,12 +20,12 @@ from fade_amd.cache import TIER_FP16, TIER_INT4
 pytestmark = pytest.mark.gpu
 
 
-def _tiny_model(dev, impl):
+def _tiny_model(dev, impl, heads=4, kv_heads=2):
     from transformers import AutoConfig, AutoModelForCausalLM
 
     cfg = AutoConfig.for_model(
-        "qwen2", vocab_size=128, hidden_size=512, intermediate_size=256, num_hidden_layers=2,
-        num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=256, rope_theta=10000.0,
+        "qwen2", vocab_size=128, hidden_size=128 * heads, intermediate_size=256, num_hidden_layers=2,
+        num_attention_heads=heads, num_key_value_heads=kv_heads, max_position_embeddings=256, rope_theta=10000.0,
         tie_word_embeddings=True,
     )
     torch.manual_seed(0)
@@ -99,6 +99,20 @@ def test_fused_logits_match_materialized(dev, middle):
     ref_cache = _cache(model)
     assert not ref_cache.fused
     ref = _steps(model, ref_cache, ids, 3, middle_after_prompt=middle)
+    for a, b in zip(fused, ref):
+        assert (a - b).abs().max().item() <= 2e-2
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(7, 1), (8, 1), (5, 1)])
+def test_fused_logits_match_materialized_gqa_5_to_8(dev, heads, kv_heads):
+    """Query-head groups of 5-8 (Qwen2.5-7B's 7): the prompt goes through the prefill
+    kernel's two head passes, the decode steps through the matrix-core kernel."""
+    print(f"case generate fused vs materialized GQA {heads}/{kv_heads}", flush=True)
+    model, cfg = _tiny_model(dev, "fade", heads, kv_heads)
+    ids = torch.randint(0, cfg.vocab_size, (2, 40), device=dev)
+    fused = _steps(model, _cache(model), ids, 3, middle_after_prompt=True)
+    model.set_attn_implementation("sdpa")
+    ref = _steps(model, _cache(model), ids, 3, middle_after_prompt=True)
     for a, b in zip(fused, ref):
         assert (a - b).abs().max().item() <= 2e-2
 
