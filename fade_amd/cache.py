@@ -105,6 +105,9 @@ class LayerState:
     mid_pages: list | None = None
     mid_pool: object | None = None
     mid_page_bytes: int = 0
+    # rows zero-padded by the reference's per-sequence assignment (row 0's positions,
+    # the earlier sink split kept): later per-sequence calls take the host path
+    _padded_rows: bool = False
 
     def total_seq_length(self) -> int:
         if self.lens_host is not None:
@@ -1116,6 +1119,69 @@ class TieredKVCache(DynamicCache):
         st.int4_k_deq = st.int4_v_deq = st.int2_k_deq = st.int2_v_deq = None
         st._compressed_bytes = self._layer_compressed_bytes(st)
         self._last_reassign_counts = cnt
+        return pos_new
+
+    def _apply_per_sequence_device(self, layer_idx: int, tiers_per_row: Tensor) -> bool:
+        """The reference's per-sequence mode (rows zero-padded to the longest,
+        fade/cache.py:1059-1230) through the device reassignment: one plan of every row
+        and one gather of their kept tokens (``_apply_per_sequence_ragged``), then the
+        per-row tiers laid out as the reference pads them: FP16 tier = each row's
+        FP16 tokens in position order, middle codes as quantized over the zero-padded
+        rows, positions of row 0, fields the reference leaves alone left alone.
+        Returns False, with the layer untouched, where it does not apply (another
+        middle format or backend, an INT2 tier, tiers other than FP16 / INT4 / EVICT)."""
+        st = self._layers[layer_idx]
+        if (not isinstance(self._quant_backend, SymmetricINT4Backend) or self.middle_v_bits != 4
+                or st.int2_kq is not None or st.backend_k is not None or st.lens is not None
+                or self.page_pool is not None or st._padded_rows):
+            return False
+        kept = {f: getattr(st, f) for f in ("sink_k", "sink_v", "sink_pos", "_fp16_buf_k", "_fp16_buf_v",
+                                            "_fp16_buf_pos", "_fp16_len", "_compressed_bytes")}
+        try:
+            pos_new = self._apply_per_sequence_ragged(layer_idx, tiers_per_row)
+        except NotImplementedError:
+            return False
+        lh = st.lens_host
+        B = len(lh)
+        sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
+        rec = (st.fp16_k, st.fp16_v)
+        H, D = int(rec[0].shape[1]), int(rec[0].shape[-1])
+        dev = rec[0].device
+        cs = 0 if sink is None else int(sink[0].shape[-2])
+        cr = int(rec[0].shape[-2])
+        nf = max(ls + lr for ls, _, lr in lh)
+        fk = fv = fpos = None
+        if nf:
+            # row b's FP16 tier: its sink tokens, then its recent ones, zero-padded
+            zero = torch.zeros(B, H, 1, D, dtype=rec[0].dtype, device=dev)
+            allk = torch.cat(([sink[0]] if sink else []) + [rec[0], zero], dim=2)
+            allv = torch.cat(([sink[1]] if sink else []) + [rec[1], zero], dim=2)
+            idx = torch.full((B, nf), cs + cr, dtype=torch.long)
+            for b, (ls, _, lr) in enumerate(lh):
+                idx[b, :ls] = torch.arange(ls)
+                idx[b, ls : ls + lr] = cs + torch.arange(lr)
+            idx = idx.pin_memory().to(dev, non_blocking=True)
+            rows = torch.arange(B, device=dev)[:, None]
+            fk = allk[rows, :, idx].permute(0, 2, 1, 3).contiguous()
+            fv = allv[rows, :, idx].permute(0, 2, 1, 3).contiguous()
+            ls0, _, lr0 = lh[0]
+            fpos = torch.cat([pos_new[0, 0, :ls0], pos_new[1, 0, :lr0]])
+        ls0, lm0, _ = lh[0]
+        ipos = pos_new[2, 0, :lm0] if st.int4_kq is not None else None
+        min_next = min(sum(r) for r in lh)
+        for f, val in kept.items():
+            setattr(st, f, val)
+        st.lens = st.lens_host = None
+        st.fp16_k, st.fp16_v, st.fp16_pos = fk, fv, fpos
+        self._reseed_fp16_buffer(st)
+        st.int4_pos = ipos
+        st.int2_kq = st.int2_vq = st.int2_ks = st.int2_vs = st.int2_pos = None
+        st.int2_actual_count = 0
+        st.int4_k_deq = st.int4_v_deq = st.int2_k_deq = st.int2_v_deq = None
+        st.next_position = min_next
+        st.sink_count = 0 if st.fp16_pos is None else min(self.n_sink, int(st.fp16_pos.shape[0]))
+        st._padded_rows = True
+        return True
 
     def apply_tier_assignment_per_sequence(self, layer_idx: int, tiers_per_row: Tensor, scores=None) -> None:
         """Per-row tiers ``[B, S]`` with zero-padding to the longest row (fade/cache.py:1059-1230).
@@ -1129,6 +1195,8 @@ class TieredKVCache(DynamicCache):
         st = self._layers[layer_idx]
         if st.lens is not None:
             raise NotImplementedError("this layer holds the ragged layout; set ragged_layout to reassign it")
+        if self.device_reassign and self._apply_per_sequence_device(layer_idx, tiers_per_row):
+            return
         k_full, v_full, pos_full = self._all_in_position_order(layer_idx)
         B, H, _, D = k_full.shape
         S = int(pos_full.shape[0])
@@ -1191,6 +1259,7 @@ class TieredKVCache(DynamicCache):
         st.int4_k_deq = st.int4_v_deq = st.int2_k_deq = st.int2_v_deq = None
         st.next_position = min_next
         st.sink_count = 0 if st.fp16_pos is None else min(self.n_sink, int(st.fp16_pos.shape[0]))
+        st._padded_rows = True
 
     # ----------------------------------------------------- fused attention
     def attend(self, q: Tensor, layer_idx: int, sm_scale: float | None = None) -> Tensor:

@@ -122,6 +122,36 @@ def test_reassign_int2_falls_back(dev):
     assert devc._layers[0].int2_actual_count == 5
 
 
+@pytest.mark.parametrize("tiers_on", ["cpu", "cuda"])
+@pytest.mark.parametrize("budgets", [(None, None, None), (30, None, 70), (20, 45, 90)])
+def test_per_sequence_device_matches_host(dev, tiers_on, budgets):
+    """The reference's per-sequence mode (rows zero-padded to the longest) on the device
+    path equals the host path (the reference's op sequence) field for field, bit for bit,
+    with eviction in some rows or all, and after later appends.  (One round: the padded
+    layout keeps row 0's positions, so rows of different lengths cannot be reassigned
+    per sequence again, on either path.)"""
+    print(f"case per-sequence device vs host tiers_on={tiers_on} budgets={budgets}", flush=True)
+    B, H = 3, 2
+    host, devc = _pair(n_sink=4, recent_window=16, int4_budget=None, int2_budget=0)
+    _append((host, devc), B, H, 150, 21, dev)
+    rng = np.random.default_rng(22)
+    S = host.get_seq_length(0)
+    tiers = torch.stack([_assign_one_layer(S, torch.from_numpy(rng.exponential(size=S).astype(np.float32)),
+                                           4, 16, budgets[b], 0) for b in range(B)])
+    if tiers_on == "cuda":
+        tiers = tiers.to(dev)
+    for c in (host, devc):
+        c.apply_tier_assignment_per_sequence(0, tiers.clone())
+    _same(host, devc, "reassignment")
+    assert devc._layers[0]._padded_rows
+    for rnd in range(2):
+        _append((host, devc), B, H, 5, 23 + rnd, dev)
+        _same(host, devc, f"append {rnd}")
+    kh, vh = host._materialize(0)
+    kd, vd = devc._materialize(0)
+    assert torch.equal(kh, kd) and torch.equal(vh, vd)
+
+
 RAGGED_FIELDS = (("sink_k", 0), ("sink_v", 0), ("int4_kq", 1), ("int4_vq", 1), ("int4_vs", 1), ("fp16_k", 2),
                  ("fp16_v", 2))
 
