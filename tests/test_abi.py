@@ -77,9 +77,9 @@ def test_prefill_struct_layout_matches_c(tmp_path):
 def test_prefill_argument_errors():
     lib = _lib.load()
     a = _lib.PrefillArgs()
-    a.B, a.Hq, a.Hkv, a.D, a.Sq = 2, 32, 4, 128, 16
+    a.B, a.Hq, a.Hkv, a.D, a.Sq = 2, 36, 4, 128, 16
     assert lib.fade_tiered_prefill_attn(ctypes.byref(a), None) == _lib.FADE_EINVAL
-    assert b"Hq/Hkv <= 4" in lib.fade_hip_last_error()
+    assert b"Hq/Hkv <= 8" in lib.fade_hip_last_error()
     a.Hkv = 8
     assert lib.fade_tiered_prefill_attn(ctypes.byref(a), None) == _lib.FADE_EINVAL
     assert b"null q, out or lens" in lib.fade_hip_last_error()
