@@ -80,7 +80,7 @@ def test_prefill_argument_errors():
     a.B, a.Hq, a.Hkv, a.D, a.Sq = 2, 36, 4, 128, 16
     assert lib.fade_tiered_prefill_attn(ctypes.byref(a), None) == _lib.FADE_EINVAL
     assert b"Hq/Hkv <= 8" in lib.fade_hip_last_error()
-    a.Hkv = 8
+    a.Hq, a.Hkv = 32, 8
     assert lib.fade_tiered_prefill_attn(ctypes.byref(a), None) == _lib.FADE_EINVAL
     assert b"null q, out or lens" in lib.fade_hip_last_error()
 
