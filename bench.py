@@ -302,6 +302,48 @@ def reassign_case(dev, n_inst: int = 8):
     return out
 
 
+def per_sequence_case(dev, n_inst: int = 4):
+    """The reference's per-sequence assignment (zero-padded rows) at config 3's cache
+    shape, wall-clock per call, device path vs host path (the reference's op
+    sequence): B=8 rows of 4096 tokens, Hkv=4, each row keeping 4 sink + its own 400
+    best-scoring middle + 128 recent tokens (per-row eviction, re-RoPE, middle quantized)."""
+    from fade_amd.cache import TieredKVCache
+    from fade_amd.policy import _assign_one_layer
+    from fade_amd.synthetic import exp_scores
+
+    B, H, S, D = 8, 4, 4096, 128
+    _, k, v = kv_tensors(B, H, S, D, seed=1003, Hq=28)
+    kd, vd = k.to(dev), v.to(dev)
+    tiers = torch.stack([_assign_one_layer(S, exp_scores(S, 1100 + b), 4, 128, 400, 0) for b in range(B)])
+    out = {}
+    for name, device_path in (("device", True), ("host", False)):
+        times = []
+        for i in range(n_inst + 1):
+            c = TieredKVCache(n_sink=4, recent_window=128, int4_budget=400, int2_budget=0, head_dim=D)
+            c.device_reassign = device_path
+            c.update(kd, vd, 0)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            c.apply_tier_assignment_per_sequence(0, tiers)
+            torch.cuda.synchronize()
+            if i:  # the first call warms up the RoPE table and the allocator
+                times.append((time.perf_counter() - t0) * 1e6)
+            del c
+        out[name] = round(float(np.median(times)), 1)
+    torch.cuda.empty_cache()
+    return out
+
+
+def gqa7_decode_case(dev):
+    """Decode at config 3's model shape (B=8, Hq=28, Hkv=4: 7 query heads per kv head,
+    S=4096, reference INT4 middle, sink 4, recent 128): the INT4 kernel's two head
+    passes (the default) against the general matrix-core kernel (kernel=3)."""
+    cfg = type("Cfg", (), dict(B=8, Hq=28, Hkv=4, S=4096, D=128, n_sink=4, recent=128, mid=4096 - 132))
+    plans = build_instances(cfg, "int4", dev, 1003, N_INSTANCES)
+    general = [TieredDecodePlan(*p._keep[:4], kernel=3) for p in plans]
+    return plans, general, decode_bytes(cfg, "int4")
+
+
 def copy_peak(dev, stream) -> float:
     """Device-to-device copy of 1 GiB (read + write), GB/s: the measured streaming ceiling."""
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -584,6 +626,18 @@ def main() -> int:
         ra = reassign_case(dev)
         extra["c3_reassign_layer_wall_us"] = {"device_path": ra["device"], "host_path": ra["host"],
                                               "speedup": round(ra["host"] / ra["device"], 2)}
+        ps = per_sequence_case(dev)
+        extra["c3_per_sequence_assignment_wall_us"] = {"device_path": ps["device"], "host_path": ps["host"],
+                                                       "speedup": round(ps["host"] / ps["device"], 2)}
+        g2, gg, gb = gqa7_decode_case(dev)
+        _, _, g2mean, _ = time_plans(g2, max(20, args.steps // 4), 20, stream)
+        _, _, ggmean, _ = time_plans(gg, max(20, args.steps // 4), 20, stream)
+        extra["c3_shape_decode_gqa7_int4"] = {
+            "us_two_head_passes": round(g2mean * 1e3, 2), "us_general_kernel": round(ggmean * 1e3, 2),
+            "bytes": gb, "GBps_two_head_passes": round(gb / (g2mean * 1e-3) / 1e9, 1),
+        }
+        del g2, gg
+        torch.cuda.empty_cache()
         extra["copy_peak_GBps"] = round(copy_peak(dev, stream), 1)
         torch.cuda.empty_cache()
         c2 = CONFIGS[2]
