@@ -1331,7 +1331,11 @@ class TieredKVCache(DynamicCache):
         sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
         midp = self._mid_padded(st)
         mid = None if midp is None else MiddleTier("int4", midp[0], midp[2], midp[1], midp[3])
-        return tiered_prefill_attention(q, chunk, sink, mid, (st.fp16_k, st.fp16_v), lens=lens, sm_scale=sm_scale)
+        # rows dispatched longest first, so the longest rows do not form the tail
+        order = sorted(range(B), key=lambda r: -sum(st.lens_host[r]))
+        order = torch.tensor(order, dtype=torch.int32).pin_memory().to(q.device, non_blocking=True)
+        return tiered_prefill_attention(q, chunk, sink, mid, (st.fp16_k, st.fp16_v), lens=lens, order=order,
+                                        sm_scale=sm_scale)
 
     def decode_attention(self, q: Tensor, layer_idx: int, sm_scale: float | None = None) -> Tensor:
         """Single-token attention of ``q`` [B, Hq, 1, D] straight from this layer's tiers.
