@@ -1329,8 +1329,13 @@ class TieredKVCache(DynamicCache):
         lens = st.lens.clone()
         lens[:, 2] -= Sq
         sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
-        midp = self._mid_padded(st)
-        mid = None if midp is None else MiddleTier("int4", midp[0], midp[2], midp[1], midp[3])
+        if st.mid_table is not None:  # paged: the kernel reads the pool through the block table
+            pool = st.mid_pool
+            mid = MiddleTier("int4", pool.k_codes, pool.v_codes, st.int4_ks, pool.v_scale,
+                             length=max(r[1] for r in st.lens_host), pages=st.mid_table)
+        else:
+            midp = self._mid_padded(st)
+            mid = None if midp is None else MiddleTier("int4", midp[0], midp[2], midp[1], midp[3])
         # rows dispatched longest first, so the longest rows do not form the tail
         order = sorted(range(B), key=lambda r: -sum(st.lens_host[r]))
         order = torch.tensor(order, dtype=torch.int32).pin_memory().to(q.device, non_blocking=True)

@@ -92,6 +92,8 @@ struct PParams {
   const uint16_t* ks;
   const uint8_t* vq;
   const uint16_t* vs;
+  const int32_t* pages;  // paged middle: block table [B][ppr] of 64-token pages (one middle tile each)
+  int64_t ppr;
 };
 
 // Eight two's-complement nibbles (one dword of packed codes, high nibble =
@@ -207,16 +209,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   auto fetch_mid = [&](const TileRef& tr) {
     const bool ok = r < tr.cnt;
     fok = ok;
-    const int key = tr.base + (ok ? r : tr.cnt - 1);  // rows past the tile: a valid row, zeroed in store_mid()
-    lds_dma16(kq + static_cast<int64_t>(key) * 64 + 16 * cp, stk);
+    // the tile's rows: from row tr.base of this (row, kv head)'s padded tensors,
+    // or from row 0 of its page's (page, kv head) block in the pools
+    const uint8_t* kq_t = kq;
+    const uint8_t* vq_t = vq;
+    const uint16_t* vs_t = vsr;
+    int row0 = tr.base;
+    if (p.pages != nullptr) {
+      const int64_t blk = static_cast<int64_t>(p.pages[b * p.ppr + (tr.base >> 6)]) * p.Hkv + kvh;
+      kq_t = p.kq + blk * kKT * 64;
+      vq_t = p.vq + blk * kKT * 64;
+      vs_t = p.vs + blk * kKT;
+      row0 = 0;
+    }
+    const int key = row0 + (ok ? r : tr.cnt - 1);  // rows past the tile: a valid row, zeroed in store_mid()
+    lds_dma16(kq_t + static_cast<int64_t>(key) * 64 + 16 * cp, stk);
     // V: lane l of wave w fills unit l of the wave's block: row rho = l >> 2,
     // source unit (l & 3) ^ ((rho >> 1) & 3).  Rows past the tile read the last
     // valid key (finite; their probabilities are zero).
     const int vr = lane >> 2;
     const int vk = 16 * wave + vr, sk2 = 16 * wave + (lane & 15);
-    lds_dma16(vq + static_cast<int64_t>(tr.base + (vk < tr.cnt ? vk : tr.cnt - 1)) * 64 + 16 * ((lane & 3) ^ ((vr >> 1) & 3)),
+    lds_dma16(vq_t + static_cast<int64_t>(row0 + (vk < tr.cnt ? vk : tr.cnt - 1)) * 64 + 16 * ((lane & 3) ^ ((vr >> 1) & 3)),
               stv);
-    lds_dma2(vsr + tr.base + (sk2 < tr.cnt ? sk2 : tr.cnt - 1), sts);
+    lds_dma2(vs_t + row0 + (sk2 < tr.cnt ? sk2 : tr.cnt - 1), sts);
   };
   // staged codes -> fp16(code * scale) rows of K and V in LDS buffer buf
   auto store_mid = [&](int buf) {
@@ -499,6 +514,8 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
     if (!m.k_codes || !m.v_codes || !m.k_scale || !m.v_scale || !aligned16(m.k_codes) || !aligned16(m.v_codes) ||
         (reinterpret_cast<uintptr_t>(m.k_scale) & 15))
       return einval("fade_tiered_prefill_attn: middle tier pointers missing or misaligned");
+    if (m.pages != nullptr && (m.page_stride != 0 || m.pages_per_row * kKT < m.len))
+      return einval("fade_tiered_prefill_attn: a paged middle tier needs separate pools and pages_per_row * 64 >= len");
   }
   PParams p{};
   p.B = a->B;
@@ -525,6 +542,8 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   p.ks = static_cast<const uint16_t*>(m.k_scale);
   p.vq = static_cast<const uint8_t*>(m.v_codes);
   p.vs = static_cast<const uint16_t*>(m.v_scale);
+  p.pages = has_mid ? m.pages : nullptr;
+  p.ppr = has_mid ? m.pages_per_row : 0;
   const dim3 grid(static_cast<unsigned>(cdiv(a->Sq, kQB) * p.passes), static_cast<unsigned>(a->Hkv),
                   static_cast<unsigned>(a->B));
   hipLaunchKernelGGL(prefill_kernel, grid, dim3(kThreads), 0, as_stream(stream), p);

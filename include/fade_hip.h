@@ -289,7 +289,8 @@ int fade_tiered_decode_attn(const fade_decode_args* args, void* stream);
  * [sink | middle | recent] followed by the chunk itself, bottom-right causal:
  * query j of row b sees cache tokens and chunk tokens 0..j.  Tier tensors are
  * padded along S (row b uses the first lens[3b+0..2] tokens of sink / middle /
- * recent); the middle tier is FADE_MID_SYM 4-bit or FADE_MID_NONE.  D = 128,
+ * recent); the middle tier is FADE_MID_SYM 4-bit (padded, or paged: mid.pages,
+ * separate pools, pages_per_row * 64 >= mid.len) or FADE_MID_NONE.  D = 128,
  * Hq/Hkv <= 8.  `order` (optional, device int32 [B]) lists batch rows in the
  * order their workgroups are dispatched (longest first balances the tail).
  * Replaces the reference's prefill path: update() returning the materialized

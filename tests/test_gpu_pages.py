@@ -91,7 +91,9 @@ def test_paged_middle_matches_unpaged(dev):
     _close(plain.decode_attention(q, 0), paged.decode_attention(q, 0), 1e-3, "decode")
     _append((plain, paged), 24, 4, dev)
     qc = torch.randn(B, HQ, 24, D, generator=g).half().to(dev)
-    _close(plain.prefill_attention(qc, 0), paged.prefill_attention(qc, 0), 1e-3, "chunk prefill")
+    # the prefill reads the pages in place; no tile claims, so bit for bit
+    assert torch.equal(plain.prefill_attention(qc, 0), paged.prefill_attention(qc, 0)), "chunk prefill"
+
     _reassign((plain, paged), [60, None, 130], 5)  # frees the old pages and takes new ones
     _same(plain, paged, "second reassignment")
     _close(plain.decode_attention(q, 0), paged.decode_attention(q, 0), 1e-3, "decode after the second")

@@ -87,6 +87,22 @@ def test_tiered_prefill_ragged(dev, B, Hq, Hkv, Sq, rows):
     assert np.abs(out.float().cpu().numpy() - ref).max() <= ATOL
 
 
+def test_tiered_prefill_paged_middle(dev):
+    """A paged middle tier (64-token pages of one pool, shuffled, per-row block table):
+    the kernel reads the pages in place and gives the padded layout's output bit for bit."""
+    from fade_amd.kernels.tiered_attn import paginate_middle
+
+    print("case prefill paged middle", flush=True)
+    rows = [(4, 700, 64), (4, 130, 20), (2, 0, 64), (1, 64, 5)]
+    q, chunk, sink, mid, rec, lens, ref = _ragged(dev, 4, 32, 8, 96, rows, seed=4500)
+    n_pages = sum(-(-r[1] // 64) for r in rows)
+    paged = paginate_middle(mid, [r[1] for r in rows], order=np.random.default_rng(3).permutation(n_pages))
+    out_r = tiered_prefill_attention(q, chunk, sink, mid, rec, lens=lens)
+    out_p = tiered_prefill_attention(q, chunk, sink, paged, rec, lens=lens)
+    assert torch.equal(out_r, out_p)
+    assert np.abs(out_p.float().cpu().numpy() - ref).max() <= ATOL
+
+
 def test_tiered_prefill_order_and_fp16_only(dev):
     """Dispatch order does not change results; a cache with no middle tier works."""
     print("case prefill order / fp16-only", flush=True)
