@@ -170,7 +170,7 @@ __device__ __forceinline__ int lit_swz(int r) { return ((r >> 1) & 3) | ((r >> 2
 // formats, 8 or 10 KB for the asymmetric ones, 12.25 KB for literal INT2 V).
 // NW waves per workgroup (4, 6 or 8; see packed_kernel); registers are sized
 // for two waves per SIMD.
-template <int KB, int VB, int FMT, int NW>
+template <int KB, int VB, int FMT, int NW, bool DET>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_packed_kernel(
     Params p) {
   constexpr int kWaves = NW, kThreads = 64 * NW;
@@ -213,11 +213,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   // Tiles of the split: the first two of each wave are t0 + wave and
   // t0 + NW + wave; after that waves claim tiles t0 + 2 NW + c in order
   // through an LDS counter, so that a wave that runs faster (e.g. the older
-  // wave of a SIMD, which wins issue arbitration) takes more of them.  With
-  // p.deterministic, wave w walks t0 + w, t0 + w + NW, ... instead, so the
-  // order of every fp32 sum is fixed.
+  // wave of a SIMD, which wins issue arbitration) takes more of them.  The
+  // DET instance (p.deterministic) has wave w walk t0 + w, t0 + w + NW, ...
+  // instead, so the order of every fp32 sum is fixed.
   const int n = p.n_splits;
-  const bool det = p.deterministic != 0;
   __shared__ int claim_s;
   if (tid == 0) claim_s = 0;
 
@@ -860,7 +859,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     __builtin_amdgcn_s_waitcnt(kLgkm0);  // every LDS read of this stage has returned
     __builtin_amdgcn_wave_barrier();
     int64_t nt;
-    if (det) {  // wave w walks tiles t0 + w, t0 + w + NW, ... : cur's successor's successor
+    if constexpr (DET) {  // wave w walks tiles t0 + w, t0 + w + NW, ... : cur's successor's successor
       nt = cur + 2 * kWaves;
     } else {
       int c = 0;
@@ -1069,17 +1068,24 @@ struct Choice {
 // measured best on MI355X): the reference INT4 format runs two 4-wave
 // workgroups per CU; the others one workgroup per CU, of eight waves where two
 // stages per wave fit the 160 KB of LDS, six for the 10 and 12.25 KB stages.
-Choice packed_kernel(const Params& p) {
+// The deterministic instances (fixed tile order) share their claiming twin's
+// occupancy, so `index` (the resident-workgroup cache slot) is the same.
+template <bool DET>
+Choice packed_kernel_t(const Params& p) {
   const int kb = p.mid.k_bits, vb = p.mid.v_bits;
-  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6>, 6, 6};
+  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6, DET>, 6, 6};
   if (p.mid.fmt == FADE_MID_SYM) {
-    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4>, 4, 0};  // two workgroups per CU
-    return {decode_packed_kernel<2, 2, kFmtSym, 8>, 8, 1};
+    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET>, 4, 0};  // two workgroups per CU
+    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET>, 8, 1};
   }
-  if (kb == 4 && vb == 4) return {decode_packed_kernel<4, 4, kFmtAsym, 6>, 6, 2};
-  if (kb == 4 && vb == 2) return {decode_packed_kernel<4, 2, kFmtAsym, 8>, 8, 3};
-  if (kb == 2 && vb == 2) return {decode_packed_kernel<2, 2, kFmtAsym, 8>, 8, 4};
-  return {decode_packed_kernel<2, 4, kFmtAsym, 6>, 6, 5};
+  if (kb == 4 && vb == 4) return {decode_packed_kernel<4, 4, kFmtAsym, 6, DET>, 6, 2};
+  if (kb == 4 && vb == 2) return {decode_packed_kernel<4, 2, kFmtAsym, 8, DET>, 8, 3};
+  if (kb == 2 && vb == 2) return {decode_packed_kernel<2, 2, kFmtAsym, 8, DET>, 8, 4};
+  return {decode_packed_kernel<2, 4, kFmtAsym, 6, DET>, 6, 5};
+}
+
+Choice packed_kernel(const Params& p) {
+  return p.deterministic ? packed_kernel_t<true>(p) : packed_kernel_t<false>(p);
 }
 
 }  // namespace
