@@ -170,7 +170,7 @@ __device__ __forceinline__ int lit_swz(int r) { return ((r >> 1) & 3) | ((r >> 2
 // formats, 8 or 10 KB for the asymmetric ones, 12.25 KB for literal INT2 V).
 // NW waves per workgroup (4, 6 or 8; see packed_kernel); registers are sized
 // for two waves per SIMD.
-template <int KB, int VB, int FMT, int NW, bool DET>
+template <int KB, int VB, int FMT, int NW, bool DET, bool TWO>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_packed_kernel(
     Params p) {
   constexpr int kWaves = NW, kThreads = 64 * NW;
@@ -182,16 +182,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   const int split = blockIdx.x;
   // blockIdx.y = (kv head, head pass): a pass serves up to 4 of the kv head's
   // G query heads, from head h0 of the group (G = 5..8 takes two passes)
-  const int pl2 = p.passes - 1;  // log2 of the pass count (1 or 2 passes)
-  const int64_t kvh = blockIdx.y >> pl2, b = blockIdx.z;
-  const int h0 = 4 * static_cast<int>(blockIdx.y & pl2);
+  // (TWO: the two-pass instance, for G = 5..8; one pass otherwise)
+  const int64_t kvh = TWO ? blockIdx.y >> 1 : blockIdx.y, b = blockIdx.z;
+  const int h0 = TWO ? 4 * static_cast<int>(blockIdx.y & 1) : 0;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, g = lane >> 4;
   const int hq = n16 >> 2, sq = n16 & 3;  // head / sub-tile of this lane's scores
-  const int G = p.G - h0 < kHeads ? p.G - h0 : kHeads;  // query heads of this pass
+  const int G = TWO ? (p.G - h0 < kHeads ? p.G - h0 : kHeads) : p.G;  // query heads of this pass
   const int64_t bkv = b * p.Hkv + kvh;                    // the kv pair: tier addressing
-  const int64_t slot = (bkv << pl2) + (h0 >> 2);          // split counter / partials of this pass
+  const int64_t slot = TWO ? 2 * bkv + (h0 >> 2) : bkv;   // split counter / partials of this pass
   // Mc: rows of the middle tensors per (batch row, kv head); M, ns, F: this
   // row's middle, sink and fp16 token counts (per-row lengths when given,
   // clamped to the capacities)
@@ -1070,22 +1070,23 @@ struct Choice {
 // stages per wave fit the 160 KB of LDS, six for the 10 and 12.25 KB stages.
 // The deterministic instances (fixed tile order) share their claiming twin's
 // occupancy, so `index` (the resident-workgroup cache slot) is the same.
-template <bool DET>
+template <bool DET, bool TWO>
 Choice packed_kernel_t(const Params& p) {
   const int kb = p.mid.k_bits, vb = p.mid.v_bits;
-  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6, DET>, 6, 6};
+  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6, DET, TWO>, 6, 6};
   if (p.mid.fmt == FADE_MID_SYM) {
-    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET>, 4, 0};  // two workgroups per CU
-    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET>, 8, 1};
+    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO>, 4, 0};  // two workgroups per CU
+    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO>, 8, 1};
   }
-  if (kb == 4 && vb == 4) return {decode_packed_kernel<4, 4, kFmtAsym, 6, DET>, 6, 2};
-  if (kb == 4 && vb == 2) return {decode_packed_kernel<4, 2, kFmtAsym, 8, DET>, 8, 3};
-  if (kb == 2 && vb == 2) return {decode_packed_kernel<2, 2, kFmtAsym, 8, DET>, 8, 4};
-  return {decode_packed_kernel<2, 4, kFmtAsym, 6, DET>, 6, 5};
+  if (kb == 4 && vb == 4) return {decode_packed_kernel<4, 4, kFmtAsym, 6, DET, TWO>, 6, 2};
+  if (kb == 4 && vb == 2) return {decode_packed_kernel<4, 2, kFmtAsym, 8, DET, TWO>, 8, 3};
+  if (kb == 2 && vb == 2) return {decode_packed_kernel<2, 2, kFmtAsym, 8, DET, TWO>, 8, 4};
+  return {decode_packed_kernel<2, 4, kFmtAsym, 6, DET, TWO>, 6, 5};
 }
 
 Choice packed_kernel(const Params& p) {
-  return p.deterministic ? packed_kernel_t<true>(p) : packed_kernel_t<false>(p);
+  if (p.passes > 1) return p.deterministic ? packed_kernel_t<true, true>(p) : packed_kernel_t<false, true>(p);
+  return p.deterministic ? packed_kernel_t<true, false>(p) : packed_kernel_t<false, false>(p);
 }
 
 }  // namespace
