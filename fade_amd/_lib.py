@@ -32,6 +32,10 @@ MID_SYM = 2
 MID_K4V2G = 3
 MID_ASYM = 4
 
+MASK_BOTTOM_RIGHT = 0
+MASK_TOP_LEFT = 1
+MASK_NONE = 2
+
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
 _p = ctypes.c_void_p
@@ -119,6 +123,7 @@ class PrefillArgs(ctypes.Structure):
         ("mid", MidTier),
         ("recent", Fp16Tier),
         ("chunk", Fp16Tier),
+        ("mask_mode", _i32),
     ]
 
 
@@ -274,16 +279,27 @@ def stream_workspace(nbytes: int, device: torch.device, stream: int, pairs: int)
     stream run in order; different streams get different buffers.  A buffer
     too small for a call is replaced by a zero-filled one of at least twice
     its size; the old one is kept for the life of the process, as every buffer
-    is (a graph that captured one keeps a valid address).
+    is (a graph that captured one keeps a valid address).  The zero fill runs on
+    ``stream`` itself, so the first kernel on that stream sees it done; a buffer
+    is never created or grown while a HIP graph is being captured (the fill
+    would only be recorded in the graph): run the same call once before
+    capturing.
     """
     idx = device.index if device.index is not None else torch.cuda.current_device()
     key = (idx, int(stream), int(pairs))
     need = max(int(nbytes), 1)
     ws = _STREAM_WS.get(key)
     if ws is None or ws.numel() < need:
-        if ws is not None:
-            _STREAM_WS_OUTGROWN.append(ws)
-            need = max(need, 2 * ws.numel())
-        ws = torch.zeros(need, dtype=torch.uint8, device=torch.device("cuda", idx))
+        target = torch.cuda.ExternalStream(int(stream), device=torch.device("cuda", idx))
+        with torch.cuda.stream(target):
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    "tiered decode: its shared workspace would be created or grown during HIP-graph capture; "
+                    "run the same call once on this stream before capturing"
+                )
+            if ws is not None:
+                _STREAM_WS_OUTGROWN.append(ws)
+                need = max(need, 2 * ws.numel())
+            ws = torch.zeros(need, dtype=torch.uint8, device=torch.device("cuda", idx))
         _STREAM_WS[key] = ws
     return ws

@@ -107,15 +107,30 @@ class RotatedINT4Backend:
 
 @dataclass
 class AsymGroupBackend:
-    """Per-token asymmetric groups along head_dim with fp16 scale/zero (build format)."""
+    """Per-token asymmetric groups along head_dim with fp16 scale/zero (build format).
+
+    ``bits`` is the K code width; ``v_bits`` (default: ``bits``) the V code
+    width, so the K 4-bit / V 2-bit tier of the benchmark's long-context
+    configuration is one backend."""
 
     head_dim: int = 128
     bits: int = 4
     group: int = 32
+    v_bits: int | None = None
+
+    @property
+    def k_bits(self) -> int:
+        return self.bits
+
+    @property
+    def value_bits(self) -> int:
+        return self.bits if self.v_bits is None else self.v_bits
 
     @property
     def name(self) -> str:
-        return f"int{self.bits}_asym_g{self.group}"
+        if self.value_bits == self.bits:
+            return f"int{self.bits}_asym_g{self.group}"
+        return f"k{self.bits}v{self.value_bits}_asym_g{self.group}"
 
     def compress_k(self, k: Tensor) -> dict[str, Tensor]:
         packed, scale, zero = quant_asym(k, self.bits, self.group)
@@ -125,8 +140,13 @@ class AsymGroupBackend:
         c = compressed
         return dequant_asym(c["packed"], c["scale"], c["zero"], self.bits, self.group).to(dtype)
 
-    compress_v = compress_k
-    decompress_v = decompress_k
+    def compress_v(self, v: Tensor) -> dict[str, Tensor]:
+        packed, scale, zero = quant_asym(v, self.value_bits, self.group)
+        return {"packed": packed, "scale": scale, "zero": zero}
+
+    def decompress_v(self, compressed: dict[str, Tensor], dtype: torch.dtype = torch.float16) -> Tensor:
+        c = compressed
+        return dequant_asym(c["packed"], c["scale"], c["zero"], self.value_bits, self.group).to(dtype)
 
 
 @dataclass

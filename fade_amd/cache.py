@@ -190,6 +190,8 @@ class TieredKVCache(DynamicCache):
         # ragged layout: a fade_amd.pages.MiddlePagePool to keep the middle tier in
         # 64-token pages (per-row memory instead of padding to the longest row)
         self.page_pool = None
+        # split count of the fused decode kernel (0: the kernel's planner fills the GPU)
+        self.decode_splits = 0
         self._last_reassign_counts = None
 
     # transformers 5.x defines a read-only ``Cache.batch_size``; the tiered cache
@@ -1367,7 +1369,7 @@ class TieredKVCache(DynamicCache):
                                  torch.zeros(B, H, 1, 1, dtype=torch.float16, device=q.device))
             sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
             recent = None if st.fp16_k is None or st.fp16_k.shape[-2] == 0 else (st.fp16_k, st.fp16_v)
-            return tiered_decode_attention(q, sink, mid, recent, sm_scale, lens=st.lens)
+            return tiered_decode_attention(q, sink, mid, recent, sm_scale, n_splits=self.decode_splits, lens=st.lens)
         if st.int2_kq is not None:
             raise RuntimeError("decode_attention: the INT2 tier is not read by the fused kernel; use update()")
         if st.sink_k is not None:
@@ -1405,7 +1407,7 @@ class TieredKVCache(DynamicCache):
             elif isinstance(be, AsymGroupBackend):
                 mid = MiddleTier(
                     "asym", bk["packed"], bv["packed"], bk["scale"], bv["scale"], bk["zero"], bv["zero"],
-                    k_bits=be.bits, v_bits=be.bits, group=be.group,
+                    k_bits=be.bits, v_bits=be.value_bits, group=be.group,
                 )
             else:
                 raise RuntimeError(f"decode_attention: backend {be.name} is not read by the fused kernel")
@@ -1413,7 +1415,7 @@ class TieredKVCache(DynamicCache):
             # Sink/recent are unrotated fp16; attend in the rotated basis for all tiers.
             sink = None if sink is None else tuple((t.float() @ post_rotate.T).to(torch.float16) for t in sink)
             recent = None if recent is None else tuple((t.float() @ post_rotate.T).to(torch.float16) for t in recent)
-        out = tiered_decode_attention(q, sink, mid, recent, sm_scale)
+        out = tiered_decode_attention(q, sink, mid, recent, sm_scale, n_splits=self.decode_splits)
         if post_rotate is not None:
             out = (out.float() @ post_rotate).to(torch.float16)
         return out

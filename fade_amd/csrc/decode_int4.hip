@@ -1061,27 +1061,28 @@ typedef void (*PackedKernel)(Params);
 struct Choice {
   PackedKernel k;
   int waves;  // wavefronts per workgroup (one workgroup per CU)
-  int index;
+  int index;  // the template instance: format slot * 4 + DET * 2 + TWO
 };
 
 // The kernel instance for a middle tier int4_supports accepted (wave counts
 // measured best on MI355X): the reference INT4 format runs two 4-wave
 // workgroups per CU; the others one workgroup per CU, of eight waves where two
 // stages per wave fit the 160 KB of LDS, six for the 10 and 12.25 KB stages.
-// The deterministic instances (fixed tile order) share their claiming twin's
-// occupancy, so `index` (the resident-workgroup cache slot) is the same.
+// `index` keys the resident-workgroup cache per template instance, so an
+// instance whose registers or LDS differ gets its own occupancy.
 template <bool DET, bool TWO>
 Choice packed_kernel_t(const Params& p) {
   const int kb = p.mid.k_bits, vb = p.mid.v_bits;
-  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6, DET, TWO>, 6, 6};
+  constexpr int v = (DET ? 2 : 0) + (TWO ? 1 : 0);
+  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6, DET, TWO>, 6, 4 * 6 + v};
   if (p.mid.fmt == FADE_MID_SYM) {
-    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO>, 4, 0};  // two workgroups per CU
-    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO>, 8, 1};
+    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO>, 4, 4 * 0 + v};  // two workgroups per CU
+    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO>, 8, 4 * 1 + v};
   }
-  if (kb == 4 && vb == 4) return {decode_packed_kernel<4, 4, kFmtAsym, 6, DET, TWO>, 6, 2};
-  if (kb == 4 && vb == 2) return {decode_packed_kernel<4, 2, kFmtAsym, 8, DET, TWO>, 8, 3};
-  if (kb == 2 && vb == 2) return {decode_packed_kernel<2, 2, kFmtAsym, 8, DET, TWO>, 8, 4};
-  return {decode_packed_kernel<2, 4, kFmtAsym, 6, DET, TWO>, 6, 5};
+  if (kb == 4 && vb == 4) return {decode_packed_kernel<4, 4, kFmtAsym, 6, DET, TWO>, 6, 4 * 2 + v};
+  if (kb == 4 && vb == 2) return {decode_packed_kernel<4, 2, kFmtAsym, 8, DET, TWO>, 8, 4 * 3 + v};
+  if (kb == 2 && vb == 2) return {decode_packed_kernel<2, 2, kFmtAsym, 8, DET, TWO>, 8, 4 * 4 + v};
+  return {decode_packed_kernel<2, 4, kFmtAsym, 6, DET, TWO>, 6, 4 * 5 + v};
 }
 
 Choice packed_kernel(const Params& p) {
@@ -1092,7 +1093,7 @@ Choice packed_kernel(const Params& p) {
 }  // namespace
 
 int int4_resident_wgs(const Params& p) {
-  static int cached[7] = {0, 0, 0, 0, 0, 0, 0};
+  static int cached[7 * 4] = {};
   const Choice c = packed_kernel(p);
   if (cached[c.index] > 0) return cached[c.index];
   int dev = 0, cus = 0, per_cu = 0;

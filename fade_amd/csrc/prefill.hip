@@ -94,6 +94,8 @@ struct PParams {
   const uint16_t* vs;
   const int32_t* pages;  // paged middle: block table [B][ppr] of 64-token pages (one middle tile each)
   int64_t ppr;
+  int mask_mode;          // FADE_MASK_*: bottom-right over the chunk, top-left over the row, none
+  int chunk_len;          // chunk keys (Sq under FADE_MASK_BOTTOM_RIGHT)
 };
 
 // Eight two's-complement nibbles (one dword of packed codes, high nibble =
@@ -137,24 +139,39 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int Sq = static_cast<int>(p.Sq);
   const int j0 = qb * kQB;
   const int jn = Sq - j0 < kQB ? Sq - j0 : kQB;  // queries of this block
-  const int cv = j0 + jn;                        // chunk keys any query of the block can see
+  const int mode = p.mask_mode;
+  // chunk keys any query of the block can see (bottom-right: chunk keys 0..j)
+  const int cv = mode == FADE_MASK_BOTTOM_RIGHT ? j0 + jn : p.chunk_len;
   // Key tiles never straddle a tier: sink, middle, recent, chunk tiles in turn.
   const int nts = (ns + kKT - 1) / kKT, ntm = (nm + kKT - 1) / kKT, ntr = (nr + kKT - 1) / kKT;
-  const int n_tiles = nts + ntm + ntr + (cv + kKT - 1) / kKT;
+  const int ntc = (cv + kKT - 1) / kKT;
+  int n_tiles = nts + ntm + ntr + ntc;
+  if (mode == FADE_MASK_TOP_LEFT) {
+    // query j sees keys 0..j of the row's sequence: only the tiles that start
+    // at or before the block's last query (a prefix of the tile order)
+    const int jmax = j0 + jn - 1;
+    auto upto = [&](int nt, int off) {
+      if (jmax < off) return 0;
+      const int c = (jmax - off) / kKT + 1;
+      return c < nt ? c : nt;
+    };
+    n_tiles = upto(nts, 0) + upto(ntm, ns) + upto(ntr, ns + nm) + upto(ntc, ns + nm + nr);
+  }
   struct TileRef {
-    int seg, base, cnt;  // segment (0 sink, 1 middle, 2 recent, 3 chunk), first key, keys
+    int seg, base, cnt, gbase;  // segment (0 sink, 1 middle, 2 recent, 3 chunk), first key, keys,
+                                // first key's index in the row's sequence
   };
   auto tile_of = [&](int t) {
     TileRef r;
     int len;
     if (t < nts) {
-      r.seg = 0; r.base = kKT * t; len = ns;
+      r.seg = 0; r.base = kKT * t; len = ns; r.gbase = r.base;
     } else if (t < nts + ntm) {
-      r.seg = 1; r.base = kKT * (t - nts); len = nm;
+      r.seg = 1; r.base = kKT * (t - nts); len = nm; r.gbase = ns + r.base;
     } else if (t < nts + ntm + ntr) {
-      r.seg = 2; r.base = kKT * (t - nts - ntm); len = nr;
+      r.seg = 2; r.base = kKT * (t - nts - ntm); len = nr; r.gbase = ns + nm + r.base;
     } else {
-      r.seg = 3; r.base = kKT * (t - nts - ntm - ntr); len = cv;
+      r.seg = 3; r.base = kKT * (t - nts - ntm - ntr); len = cv; r.gbase = ns + nm + nr + r.base;
     }
     r.cnt = len - r.base < kKT ? len - r.base : kKT;
     return r;
@@ -373,12 +390,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], s[kb], 0, 0, 0);
       }
     }
-    // every key of a full cache tile is visible to every query of the block
-    const bool full = tr.seg != 3 && tr.cnt == kKT;
+    // bottom-right: every key of a full cache tile is visible to every query of
+    // the block; top-left: a full tile that ends at or before the block's first query
+    const bool full = tr.cnt == kKT && (mode == FADE_MASK_NONE || (mode == FADE_MASK_BOTTOM_RIGHT && tr.seg != 3) ||
+                                        (mode == FADE_MASK_TOP_LEFT && tr.gbase + kKT - 1 <= j0));
     if (!full) {
       const int jq = j0 + n32;
-      // key kk of the tile is visible when kk < cnt and, in the chunk, base + kk <= jq
-      const int lim = tr.seg == 3 ? (jq - tr.base + 1 < tr.cnt ? jq - tr.base + 1 : tr.cnt) : tr.cnt;
+      // key kk of the tile is visible when kk < cnt and, bottom-right, in the chunk base + kk <= jq;
+      // top-left, gbase + kk <= jq
+      int lim = tr.cnt;
+      if (mode == FADE_MASK_BOTTOM_RIGHT && tr.seg == 3) lim = jq - tr.base + 1 < tr.cnt ? jq - tr.base + 1 : tr.cnt;
+      if (mode == FADE_MASK_TOP_LEFT) lim = jq - tr.gbase + 1 < tr.cnt ? jq - tr.gbase + 1 : tr.cnt;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -503,7 +525,11 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
     return einval("fade_tiered_prefill_attn: null q, out or lens");
   if (!aligned16(a->q) || (a->q_sb | a->q_sh | a->q_ss) % 8)
     return einval("fade_tiered_prefill_attn: q rows must be 16-byte aligned");
-  if (a->chunk.len != a->Sq) return einval("fade_tiered_prefill_attn: chunk tier must hold Sq tokens");
+  if (a->mask_mode != FADE_MASK_BOTTOM_RIGHT && a->mask_mode != FADE_MASK_TOP_LEFT && a->mask_mode != FADE_MASK_NONE)
+    return einval("fade_tiered_prefill_attn: unknown mask_mode %d", a->mask_mode);
+  if (a->mask_mode == FADE_MASK_BOTTOM_RIGHT && a->chunk.len != a->Sq)
+    return einval("fade_tiered_prefill_attn: chunk tier must hold Sq tokens");
+  if (a->chunk.len < 0 || a->chunk.len > (1 << 24)) return einval("fade_tiered_prefill_attn: bad chunk length");
   if (!tier_ok(a->sink) || !tier_ok(a->recent) || !tier_ok(a->chunk))
     return einval("fade_tiered_prefill_attn: fp16 tiers need 16-byte aligned rows");
   const fade_mid_tier& m = a->mid;
@@ -544,6 +570,8 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   p.vs = static_cast<const uint16_t*>(m.v_scale);
   p.pages = has_mid ? m.pages : nullptr;
   p.ppr = has_mid ? m.pages_per_row : 0;
+  p.mask_mode = a->mask_mode;
+  p.chunk_len = static_cast<int>(a->chunk.len);
   const dim3 grid(static_cast<unsigned>(cdiv(a->Sq, kQB) * p.passes), static_cast<unsigned>(a->Hkv),
                   static_cast<unsigned>(a->B));
   hipLaunchKernelGGL(prefill_kernel, grid, dim3(kThreads), 0, as_stream(stream), p);

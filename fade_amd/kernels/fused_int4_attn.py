@@ -2,8 +2,10 @@
 
 Same signature, shapes and GQA mapping as the reference's Triton op
 (fade/kernels/fused_int4_attn.py:277-342).  Single-token queries run the
-tiered decode kernel with the whole packed tensor as its middle tier; GQA
-is resolved inside the kernel (no ``repeat_interleave`` copies).
+tiered decode kernel with the whole packed tensor as its middle tier; several
+query rows (or a top-left causal mask) run the MFMA prefill kernel over it in
+one launch.  GQA is resolved inside the kernels (no ``repeat_interleave``
+copies).
 """
 
 from __future__ import annotations
@@ -13,6 +15,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from .. import _lib
+from .prefill import tiered_prefill_attention
 from .tiered_attn import MiddleTier, tiered_decode_attention
 
 
@@ -48,30 +51,14 @@ def fused_int4_sdpa(
         v_scale=v_scale.to(torch.float16).contiguous(),
     )
     q16 = q.to(torch.float16)
-    if Sq == 1 and (not is_causal or Sk >= 1):
-        # Top-left causal with one query row keeps key 0 only.
-        if is_causal:
-            mid = MiddleTier(
-                fmt="int4", k_codes=mid.k_codes[:, :, :1].contiguous(), v_codes=mid.v_codes[:, :, :1].contiguous(),
-                k_scale=mid.k_scale, v_scale=mid.v_scale[:, :, :1].contiguous(),
-            )
+    if Sq == 1 and not is_causal:
         return tiered_decode_attention(q16, None, mid, None)
-    outs = [
-        tiered_decode_attention(q16[:, :, i : i + 1].contiguous(), None, _prefix(mid, i + 1) if is_causal else mid, None)
-        for i in range(Sq)
-    ]
-    return torch.cat(outs, dim=2)
-
-
-def _prefix(mid: MiddleTier, n: int) -> MiddleTier:
-    n = min(n, int(mid.k_codes.shape[2]))
-    return MiddleTier(
-        fmt="int4",
-        k_codes=mid.k_codes[:, :, :n].contiguous(),
-        v_codes=mid.v_codes[:, :, :n].contiguous(),
-        k_scale=mid.k_scale,
-        v_scale=mid.v_scale[:, :, :n].contiguous(),
-    )
+    # several query rows, or top-left causal: one launch of the MFMA prefill kernel with the
+    # packed tensor as every row's middle tier and no keys of the queries' own
+    B = int(q.shape[0])
+    lens = torch.tensor([[0, Sk, 0]] * B, dtype=torch.int32).to(q.device, non_blocking=True)
+    return tiered_prefill_attention(q16, None, None, mid, None, lens=lens,
+                                    mask="top_left" if is_causal else "none")
 
 
 def fused_int4_sdpa_with_fallback(q, k_packed, k_scale, v_packed, v_scale, force_fused: bool = False) -> Tensor:

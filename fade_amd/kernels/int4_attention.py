@@ -2,9 +2,9 @@
 
 The reference dequantizes (torch or an uncoalesced Triton unpack) and calls
 SDPA without expanding GQA heads.  Here the packed tensors feed the fused
-decode kernel for single-token queries; longer queries dequantize on the
-HIP kernel and run SDPA on the GPU.  ``force_triton`` is accepted for
-signature compatibility and ignored (there is no Triton in this build).
+kernels (decode for single-token queries, the MFMA prefill kernel without a
+mask for longer ones), which also resolve GQA.  ``force_triton`` is accepted
+for signature compatibility and ignored (there is no Triton in this build).
 """
 
 from __future__ import annotations
@@ -21,11 +21,7 @@ USE_TRITON_KERNEL = False
 
 
 def _int4_sdpa_hip(q, k_packed, k_scale, v_packed, v_scale, dtype=torch.float16) -> Tensor:
-    if q.shape[2] == 1:
-        return fused_int4_sdpa(q, k_packed, k_scale, v_packed, v_scale).to(dtype)
-    k = dequant_int4(k_packed, k_scale)
-    v = dequant_int4(v_packed, v_scale)
-    return F.scaled_dot_product_attention(q.to(dtype), k.to(dtype), v.to(dtype))
+    return fused_int4_sdpa(q, k_packed, k_scale, v_packed, v_scale).to(dtype)
 
 
 def int4_sdpa(

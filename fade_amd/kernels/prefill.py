@@ -19,19 +19,26 @@ from torch import Tensor
 from .. import _lib
 from .tiered_attn import MiddleTier, _fp16_tier, _mid_tier
 
+_MASKS = {"bottom_right": _lib.MASK_BOTTOM_RIGHT, "top_left": _lib.MASK_TOP_LEFT, "none": _lib.MASK_NONE}
+
 
 class TieredPrefillPlan:
     """Validated launch for fixed tensors; ``run()`` enqueues one kernel.
 
     Args:
         q: [B, Hq, Sq, 128] fp16 queries of the chunk.
-        chunk: (K, V) [B, Hkv, Sq, 128] fp16, the chunk's own keys/values.
+        chunk: (K, V) [B, Hkv, Sq, 128] fp16, the chunk's own keys/values
+            (with ``mask`` ``"top_left"`` / ``"none"``: any length, or None).
         sink, recent: (K, V) [B, Hkv, cap, 128] fp16 padded along S, or None.
         mid: reference INT4 middle tier (``MiddleTier("int4", ...)``) with
             codes padded to a common row count, or None.
         lens: int32 [B, 3] (sink, middle, recent tokens used by each row);
             default: every row uses the full capacities.
         order: optional int32 [B] dispatch order of the batch rows (longest first).
+        mask: ``"bottom_right"`` (default: the cache fully visible, chunk key
+            i visible to chunk queries j >= i), ``"top_left"`` (query j sees
+            keys 0..j of the row's sequence [sink | middle | recent | chunk],
+            the reference fused kernel's ``is_causal``) or ``"none"``.
     """
 
     def __init__(
@@ -45,16 +52,27 @@ class TieredPrefillPlan:
         order: Tensor | None = None,
         sm_scale: float | None = None,
         out: Tensor | None = None,
+        mask: str = "bottom_right",
     ) -> None:
         if q.dim() != 4:
             raise ValueError(f"q must be [B, Hq, Sq, D], got {tuple(q.shape)}")
-        tensors = [q, *chunk] + ([*sink] if sink else []) + ([*recent] if recent else []) + (mid.tensors() if mid else [])
+        if mask not in _MASKS:
+            raise ValueError(f"mask must be one of {sorted(_MASKS)}, got {mask!r}")
+        if chunk is None and mask == "bottom_right":
+            raise ValueError("the bottom-right mask needs the chunk's own K/V")
+        tensors = [q] + ([*chunk] if chunk else []) + ([*sink] if sink else []) + ([*recent] if recent else []) \
+            + (mid.tensors() if mid else [])
         _lib.require_gpu(*tensors, op="tiered_prefill_attention")
         _lib.require_f16(q, "tiered_prefill_attention")
         B, Hq, Sq, D = q.shape
-        Hkv = int(chunk[0].shape[1])
-        if tuple(chunk[0].shape) != (B, Hkv, Sq, D) or chunk[1].shape != chunk[0].shape:
-            raise ValueError(f"chunk K/V must be [B, Hkv, Sq={Sq}, D]")
+        ref = chunk[0] if chunk else (sink[0] if sink else (recent[0] if recent else (mid.k_codes if mid else None)))
+        if ref is None:
+            raise ValueError("tiered_prefill_attention: no keys")
+        Hkv = int(ref.shape[1])
+        if chunk is not None:
+            n_c = Sq if mask == "bottom_right" else int(chunk[0].shape[2])
+            if tuple(chunk[0].shape) != (B, Hkv, n_c, D) or chunk[1].shape != chunk[0].shape:
+                raise ValueError(f"chunk K/V must be [B, Hkv, {'Sq=' if mask == 'bottom_right' else ''}{n_c}, D]")
         if mid is not None and mid.fmt not in ("int4", "sym"):
             raise ValueError("the prefill kernel reads the reference INT4 middle tier")
         if q.stride(-1) != 1:
@@ -78,6 +96,7 @@ class TieredPrefillPlan:
         a.lens = lens.data_ptr()
         a.order = order.data_ptr() if order is not None else None
         a.sink, a.mid, a.recent, a.chunk = _fp16_tier(sink), _mid_tier(mid), _fp16_tier(recent), _fp16_tier(chunk)
+        a.mask_mode = _MASKS[mask]
         self.args = a
         self.out = out
         self._fn = _lib.load().fade_tiered_prefill_attn
@@ -89,9 +108,10 @@ class TieredPrefillPlan:
         return self.out
 
 
-def tiered_prefill_attention(q, chunk, sink=None, mid=None, recent=None, lens=None, order=None, sm_scale=None) -> Tensor:
+def tiered_prefill_attention(q, chunk, sink=None, mid=None, recent=None, lens=None, order=None, sm_scale=None,
+                             mask: str = "bottom_right") -> Tensor:
     """Causal attention of a chunk over each row's tiered cache; returns fp16 [B, Hq, Sq, 128]."""
-    return TieredPrefillPlan(q, chunk, sink, mid, recent, lens, order, sm_scale).run()
+    return TieredPrefillPlan(q, chunk, sink, mid, recent, lens, order, sm_scale, mask=mask).run()
 
 
 __all__ = ["TieredPrefillPlan", "tiered_prefill_attention"]

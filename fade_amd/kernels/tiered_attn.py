@@ -239,14 +239,14 @@ class TieredDecodePlan:
         self.workspace = (_lib.workspace(nb.value, q.device) if stream is None
                           else _lib.stream_workspace(nb.value, q.device, stream, B * Hkv * -(-(Hq // Hkv) // 4)))
         a.workspace, a.workspace_bytes = self.workspace.data_ptr(), self.workspace.numel()
+        self._fn, self._name = lib.fade_tiered_decode_attn, "fade_tiered_decode_attn"
         self.args = a
         self.out = out
-        self._fn = lib.fade_tiered_decode_attn
         self._argp = ctypes.byref(a)
 
     def run(self, stream: int | None = None) -> Tensor:
         s = torch.cuda.current_stream(self.out.device).cuda_stream if stream is None else stream
-        _lib.check(self._fn(self._argp, s), "fade_tiered_decode_attn")
+        _lib.check(self._fn(self._argp, s), self._name)
         return self.out
 
 

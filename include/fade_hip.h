@@ -285,9 +285,19 @@ int fade_tiered_decode_workspace_bytes(const fade_decode_args* args, int64_t* by
 int fade_tiered_decode_attn(const fade_decode_args* args, void* stream);
 
 /* ---------------- ragged tiered prefill attention -------------------------- */
+/* Masks of fade_tiered_prefill_attn (fade_prefill_args.mask_mode). */
+#define FADE_MASK_BOTTOM_RIGHT 0 /* the cache fully visible, chunk causal: query j sees chunk keys 0..j */
+#define FADE_MASK_TOP_LEFT 1     /* query j sees keys 0..j of the row's whole key sequence
+                                    [sink | middle | recent | chunk], as the reference's fused
+                                    kernel applies is_causal (fade/kernels/fused_int4_attn.py:165-169) */
+#define FADE_MASK_NONE 2         /* every key visible to every query */
 /* A chunk of Sq new tokens per batch row attends to that row's cache
  * [sink | middle | recent] followed by the chunk itself, bottom-right causal:
- * query j of row b sees cache tokens and chunk tokens 0..j.  Tier tensors are
+ * query j of row b sees cache tokens and chunk tokens 0..j (mask_mode
+ * FADE_MASK_BOTTOM_RIGHT, chunk.len = Sq).  The two other masks take any chunk
+ * length, 0 included (queries without keys of their own, as the reference's
+ * fused_int4_sdpa over one packed tensor, fade/kernels/fused_int4_attn.py:277-342);
+ * every row must then see at least one key.  Tier tensors are
  * padded along S (row b uses the first lens[3b+0..2] tokens of sink / middle /
  * recent); the middle tier is FADE_MID_SYM 4-bit (padded, or paged: mid.pages,
  * separate pools, pages_per_row * 64 >= mid.len) or FADE_MID_NONE.  D = 128,
@@ -307,7 +317,8 @@ typedef struct fade_prefill_args {
   fade_fp16_tier sink;  /* len = padded capacity */
   fade_mid_tier mid;    /* len = padded capacity (rows of the code tensors) */
   fade_fp16_tier recent;
-  fade_fp16_tier chunk; /* the chunk's own K/V, len = Sq */
+  fade_fp16_tier chunk; /* the chunk's own K/V, len = Sq (other masks: any length) */
+  int32_t mask_mode;    /* FADE_MASK_*; 0 (zero-initialized arguments) = bottom-right */
 } fade_prefill_args;
 
 int fade_tiered_prefill_attn(const fade_prefill_args* args, void* stream);

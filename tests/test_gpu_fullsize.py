@@ -233,3 +233,96 @@ def test_config2_full_rotated_quant(dev):
     xs = x[b : b + 1, h : h + 1].numpy()
     _check_fused_rotated(xs, R, 2, "channel", kp[b : b + 1, h : h + 1].cpu().numpy(), ks[b : b + 1, h : h + 1].cpu().numpy())
     _check_fused_rotated(xs, R, 2, "token", vp[b : b + 1, h : h + 1].cpu().numpy(), vs[b : b + 1, h : h + 1].cpu().numpy())
+
+
+# ---- config 2's own middle formats at full size, through the cache's decode ----
+C2 = dict(B=4, Hkv=8, Hq=32, S=32768, ns=4, nr=256, seed=1002, row=3)
+
+
+def _c2_cache(dev, k, v, **kw):
+    """Config 2's cache: every token between the 4 sinks and the 256 recent ones in the middle tier."""
+    S = int(k.shape[2])
+    c = TieredKVCache(n_sink=C2["ns"], recent_window=C2["nr"], int4_budget=None, head_dim=128, **kw)
+    c.update(k.to(dev), v.to(dev), 0)
+    c.apply_tier_assignment(0, _assign_one_layer(S, torch.zeros(S), C2["ns"], C2["nr"], None, 0))
+    return c
+
+
+def _c2_decode_checks(dev, c, q, kn, vn, mid_ref, what):
+    """Decode of the whole batch through the cache: every row split-invariant (one split vs
+    the planner's), row C2['row'] within 2e-3 of the oracle's dequant + fp32 SDPA."""
+    qd = q.to(dev)
+    out = c.decode_attention(qd, 0)
+    c.decode_splits = 1
+    one = c.decode_attention(qd, 0)
+    c.decode_splits = 0
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out.float()).all()), f"{what}: non-finite output"
+    d = (out.float() - one.float()).abs().amax(dim=(1, 2, 3))
+    assert float(d.max()) <= ATOL, f"{what}: one split differs from the default splits by {d.tolist()}"
+    b, ns, nr = C2["row"], C2["ns"], C2["nr"]
+    ref = oatt.tiered_decode(q.numpy()[b : b + 1], kn[b : b + 1, :, :ns], vn[b : b + 1, :, :ns], mid_ref,
+                             kn[b : b + 1, :, -nr:], vn[b : b + 1, :, -nr:])
+    err = float(np.abs(out[b : b + 1].float().cpu().numpy() - ref).max())
+    assert err <= ATOL, f"{what}: row {b} decode max-abs error {err}"
+
+
+def test_config2_full_k4_literal_v2_decode(dev):
+    """Config 2 in the reference's INT4-K / INT2-V layout (fade/cache.py:983-988: V grouped 64
+    along S, int8 codes): row 3's codes and scales bit-exact with the oracle, decode within 2e-3."""
+    print("case full-size config 2 K4 + literal V2 decode", flush=True)
+    q, k, v = kv_tensors(C2["B"], C2["Hkv"], C2["S"], 128, seed=C2["seed"], Hq=C2["Hq"])
+    c = _c2_cache(dev, k, v, middle_v_bits=2)
+    st = c._layers[0]
+    b, ns, nr = C2["row"], C2["ns"], C2["nr"]
+    kn, vn = k.numpy(), v.numpy()
+    okq, oks = oq.quant_k_int4(kn[b : b + 1, :, ns:-nr])
+    vpad, _ = oq.pad_to_group(vn[b : b + 1, :, ns:-nr], 64)
+    ovq, ovs = oq.quant_int2_grouped(vpad, 64)
+    assert np.array_equal(st.int4_kq[b : b + 1].cpu().numpy(), okq), "K codes differ from the oracle"
+    assert np.array_equal(st.int4_ks[b : b + 1].cpu().numpy().view(np.uint16), oks.view(np.uint16)), "K scales"
+    assert np.array_equal(st.int4_vq[b : b + 1].cpu().numpy(), ovq), "INT2 V codes differ from the oracle"
+    assert np.array_equal(st.int4_vs[b : b + 1].cpu().numpy().view(np.uint16), ovs.view(np.uint16)), "INT2 V scales"
+    mid = {"fmt": "k4v2", "kq": okq, "ks": oks, "vq": ovq, "vs": ovs, "group": 64}
+    _c2_decode_checks(dev, c, q, kn, vn, mid, "K4 + literal V2")
+
+
+def test_config2_full_asym_k4v2_decode(dev):
+    """Config 2 in BASELINE's format (asymmetric group-32, K 4-bit / V 2-bit) through the cache:
+    row 3's codes, scales and zeros bit-exact with the oracle, decode within 2e-3."""
+    from fade_amd.backends import AsymGroupBackend
+
+    print("case full-size config 2 asym K4/V2 decode", flush=True)
+    q, k, v = kv_tensors(C2["B"], C2["Hkv"], C2["S"], 128, seed=C2["seed"], Hq=C2["Hq"])
+    c = _c2_cache(dev, k, v, quant_backend=AsymGroupBackend(head_dim=128, bits=4, group=32, v_bits=2))
+    st = c._layers[0]
+    b, ns, nr = C2["row"], C2["ns"], C2["nr"]
+    kn, vn = k.numpy(), v.numpy()
+    mid = {"fmt": "asym", "k_bits": 4, "v_bits": 2, "group": 32}
+    for name, x, comp, bits in (("K", kn, st.backend_k, 4), ("V", vn, st.backend_v, 2)):
+        op, os_, oz = oq.quant_asym_group(x[b : b + 1, :, ns:-nr], bits, 32)
+        assert np.array_equal(comp["packed"][b : b + 1].cpu().numpy(), op), f"{name} codes differ from the oracle"
+        assert np.array_equal(comp["scale"][b : b + 1].cpu().numpy().view(np.uint16), os_.view(np.uint16)), name
+        assert np.array_equal(comp["zero"][b : b + 1].cpu().numpy().view(np.uint16), oz.view(np.uint16)), name
+        p = name.lower()
+        mid.update({f"{p}q": op, f"{p}s": os_, f"{p}z": oz})
+    _c2_decode_checks(dev, c, q, kn, vn, mid, "asym K4/V2")
+
+
+def test_config2_full_rotated_k2v2_decode(dev):
+    """Config 2's rotated-2bit variant (seed-42 rotation, K and V 2-bit) through the cache: decode of
+    the cache's own codes within 2e-3 of the oracle's rotated dequant (fade/rotated_quant.py:134-187)
+    + fp32 SDPA.  The codes themselves are pinned by test_config2_full_rotated_quant."""
+    from fade_amd.backends import RotatedINT4Backend
+
+    print("case full-size config 2 rotated K2/V2 decode", flush=True)
+    q, k, v = kv_tensors(C2["B"], C2["Hkv"], C2["S"], 128, seed=C2["seed"], Hq=C2["Hq"])
+    c = _c2_cache(dev, k, v, quant_backend=RotatedINT4Backend(head_dim=128, bits=2))
+    st = c._layers[0]
+    b = C2["row"]
+    R = np.load(__file__.rsplit("/", 1)[0] + "/golden/rotation_d128_seed42.npy")
+    bk, bv = st.backend_k, st.backend_v
+    mid = {"fmt": "rot", "R": R, "k_bits": 2, "v_bits": 2,
+           "kq": bk["packed"][b : b + 1].cpu().numpy(), "ks": bk["scale"][b : b + 1].half().cpu().numpy(),
+           "vq": bv["packed"][b : b + 1].cpu().numpy(), "vs": bv["scale"][b : b + 1].half().cpu().numpy()}
+    _c2_decode_checks(dev, c, q, k.numpy(), v.numpy(), mid, "rotated K2/V2")
