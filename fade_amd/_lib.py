@@ -170,6 +170,7 @@ _SIGNATURES: dict[str, list] = {
     ],
     "fade_tiered_decode_workspace_bytes": [ctypes.POINTER(DecodeArgs), _pi64],
     "fade_tiered_decode_attn": [ctypes.POINTER(DecodeArgs), _p],
+    "fade_tiered_decode_attn_noalloc": [ctypes.POINTER(DecodeArgs), _p],
     "fade_reassign_plan": [_p, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p],
     "fade_reassign_gather": [ctypes.POINTER(ReassignArgs), _p],
     "fade_tiered_prefill_attn": [ctypes.POINTER(PrefillArgs), _p],

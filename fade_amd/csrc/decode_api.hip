@@ -1,9 +1,19 @@
 // Host side of the tiered decode attention: validation, split planning,
 // kernel choice and the combine launch.
+#include <mutex>
+
 #include "decode_common.h"
 
 using namespace fade;
 using namespace fade::decode;
+
+// The library's own decode scratch (fade_tiered_decode_attn_noalloc): 16 MiB on
+// every GPU the library runs on, held until the process ends.  Host code never
+// uses this name as an address: the per-device address comes from
+// hipGetSymbolAddress (scratch_for below).
+constexpr int64_t kScratchBytes = 16ll << 20;
+constexpr int64_t kScratchCounterBytes = 256ll << 10;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {
 
@@ -199,6 +209,115 @@ Plan make_plan(const fade_decode_args* a, const Params& p) {
   return pl;
 }
 
+
+// Partial-result bytes (ml + acc) of a plan with n splits, after the counters.
+int64_t partial_bytes(const fade_decode_args* a, int64_t n) {
+  const WsLayout w = ws_layout(a, n);
+  return w.total - w.ml;
+}
+
+// The kernels of a validated plan, with the split counters at `counters` and the
+// partial results at `partials` (ml, then acc, as ws_layout places them after
+// its counter region).
+int run_plan(const fade_decode_args* a, Params& p, const Plan& pl, uint32_t* counters, char* partials,
+             hipStream_t st) {
+  if ((a->kernel == 2 || a->kernel == 3) && pl.k == Kern::kValu)
+    return einval("fade_tiered_decode_attn: the matrix-core kernels do not handle this middle tier (format %d)",
+                  p.mid.fmt);
+  if ((a->lens != nullptr || a->mid.pages != nullptr) && pl.k != Kern::kInt4)
+    return einval("fade_tiered_decode_attn: per-row lengths and paged middle tiers need the matrix-core INT4 "
+                  "kernel (middle tier FADE_MID_SYM or FADE_MID_ASYM, GQA <= 8)");
+  if (pl.n > 65535) return einval("fade_tiered_decode_attn: too many splits");
+  const WsLayout ws = ws_layout(a, pl.n);
+  p.n_splits = static_cast<int>(pl.n);
+  p.tokens_per_split = pl.tps;
+  p.ws_ml = reinterpret_cast<float*>(partials);
+  p.ws_acc = reinterpret_cast<float*>(partials + (ws.acc - ws.ml));
+  if (pl.k == Kern::kInt4) {
+    p.out = static_cast<uint16_t*>(a->out);
+    p.o_sb = a->o_sb;
+    p.o_sh = a->o_sh;
+    p.n_f16_tiles = pl.n_f16_tiles;
+    p.tiles_per_split = pl.tiles_per_split;
+    p.counters = counters;
+    return launch_int4(p, st);
+  }
+  int rc = pl.k == Kern::kMfma ? launch_mfma(p, st) : launch_valu(p, st);
+  if (rc) return rc;
+  const int64_t rows = a->B * a->Hq;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(static_cast<unsigned>(rows)), dim3(kD), 0, st, p.ws_ml,
+                     p.ws_acc, p.n_splits, a->Hq, static_cast<uint16_t*>(a->out), a->o_sb, a->o_sh);
+  return check_launch("fade_tiered_decode_attn(combine)");
+}
+
+// ---- the library's own decode scratch (fade_tiered_decode_attn_noalloc) ----
+// One array per GPU the library runs on, held until the process ends:
+// [split counters: kScratchCounterBytes][partial results].  The counters sit
+// in a region of their own, so no call's partials ever land on them; every
+// decode call leaves the counters it used at zero, and the region is zeroed
+// once, by the first call on each device (stream-ordered before its kernels).
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch` on each device
+
+__global__ void zero_words_kernel(uint32_t* p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Device address of this device's `scratch` (looked up once per device, with
+// that device current); on the first call the counter region is zeroed on `st`.
+int scratch_for(hipStream_t st, char** out) {
+  int cur = 0;
+  if (hipGetDevice(&cur) != hipSuccess) {
+    (void)hipGetLastError();
+    set_error("fade_tiered_decode_attn_noalloc: hipGetDevice failed");
+    return FADE_ERUNTIME;
+  }
+  int dev = cur;
+  if (st != nullptr) {
+    hipDevice_t d = 0;
+    if (hipStreamGetDevice(st, &d) != hipSuccess) {
+      (void)hipGetLastError();
+      set_error("fade_tiered_decode_attn_noalloc: hipStreamGetDevice failed");
+      return FADE_ERUNTIME;
+    }
+    dev = static_cast<int>(d);
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("fade_tiered_decode_attn_noalloc: device %d beyond the %d the library tracks", dev, kMaxDevices);
+    return FADE_ERUNTIME;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur && hipSetDevice(dev) != hipSuccess) {
+      (void)hipGetLastError();
+      set_error("fade_tiered_decode_attn_noalloc: hipSetDevice(%d) failed", dev);
+      return FADE_ERUNTIME;
+    }
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    int rc = FADE_OK;
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("fade_tiered_decode_attn_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      (void)hipGetLastError();
+      rc = FADE_ERUNTIME;
+    } else {
+      const int64_t words = kScratchCounterBytes / 4;
+      hipLaunchKernelGGL(zero_words_kernel, dim3(static_cast<unsigned>(cdiv(words, 256))), dim3(256), 0, st,
+                         static_cast<uint32_t*>(ptr), words);
+      rc = check_launch("fade_tiered_decode_attn_noalloc(zero counters)");
+      if (rc == FADE_OK) g_scratch_ptr[dev] = ptr;
+    }
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (rc) return rc;
+  }
+  *out = static_cast<char*>(g_scratch_ptr[dev]);
+  return FADE_OK;
+}
+
 }  // namespace
 
 FADE_API int fade_tiered_decode_workspace_bytes(const fade_decode_args* a, int64_t* bytes) {
@@ -216,37 +335,40 @@ FADE_API int fade_tiered_decode_attn(const fade_decode_args* a, void* stream) {
   if (rc) return rc;
   Params p = to_params(a);
   const Plan pl = make_plan(a, p);
-  if ((a->kernel == 2 || a->kernel == 3) && pl.k == Kern::kValu)
-    return einval("fade_tiered_decode_attn: the matrix-core kernels do not handle this middle tier (format %d)",
-                  p.mid.fmt);
-  if ((a->lens != nullptr || a->mid.pages != nullptr) && pl.k != Kern::kInt4)
-    return einval("fade_tiered_decode_attn: per-row lengths and paged middle tiers need the matrix-core INT4 "
-                  "kernel (middle tier FADE_MID_SYM or FADE_MID_ASYM, GQA <= 8)");
   const WsLayout ws = ws_layout(a, pl.n);
   if (a->workspace == nullptr || a->workspace_bytes < ws.total)
     return einval("fade_tiered_decode_attn: workspace too small (%lld < %lld bytes)",
                   (long long)a->workspace_bytes, (long long)ws.total);
-  if (pl.n > 65535) return einval("fade_tiered_decode_attn: too many splits");
   char* wsb = static_cast<char*>(a->workspace);
-  p.n_splits = static_cast<int>(pl.n);
-  p.tokens_per_split = pl.tps;
-  p.ws_ml = reinterpret_cast<float*>(wsb + ws.ml);
-  p.ws_acc = reinterpret_cast<float*>(wsb + ws.acc);
-  hipStream_t st = as_stream(stream);
-  if (pl.k == Kern::kInt4) {
-    p.out = static_cast<uint16_t*>(a->out);
-    p.o_sb = a->o_sb;
-    p.o_sh = a->o_sh;
-    p.n_f16_tiles = pl.n_f16_tiles;
-    p.tiles_per_split = pl.tiles_per_split;
-    p.counters = reinterpret_cast<uint32_t*>(wsb + ws.counters);
-    return launch_int4(p, st);
-  }
-  rc = pl.k == Kern::kMfma ? launch_mfma(p, st) : launch_valu(p, st);
+  return run_plan(a, p, pl, reinterpret_cast<uint32_t*>(wsb + ws.counters), wsb + ws.ml, as_stream(stream));
+}
+
+FADE_API int fade_tiered_decode_attn_noalloc(const fade_decode_args* a, void* stream) {
+  int rc = validate(a);
   if (rc) return rc;
-  const int64_t rows = a->B * a->Hq;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(static_cast<unsigned>(rows)), dim3(kD), 0, st,
-                     p.ws_ml, p.ws_acc, p.n_splits, a->Hq, static_cast<uint16_t*>(a->out), a->o_sb,
-                     a->o_sh);
-  return check_launch("fade_tiered_decode_attn(combine)");
+  Params p = to_params(a);
+  const int64_t passes = (a->Hq / a->Hkv + 3) / 4;
+  if (a->B * a->Hkv * passes * 4 > kScratchCounterBytes)
+    return einval("fade_tiered_decode_attn_noalloc: B*Hkv*ceil(Hq/Hkv/4) = %lld split counters exceed the "
+                  "library scratch's %lld",
+                  (long long)(a->B * a->Hkv * passes), (long long)(kScratchCounterBytes / 4));
+  // the planner's split count, halved until the partial results fit the scratch
+  const int64_t cap = kScratchBytes - kScratchCounterBytes;
+  fade_decode_args b = *a;
+  Plan pl = make_plan(&b, p);
+  while (partial_bytes(&b, pl.n) > cap && pl.n > 1) {
+    b.n_splits = static_cast<int32_t>(pl.n / 2);
+    const Plan smaller = make_plan(&b, p);
+    if (smaller.n >= pl.n) break;  // e.g. a paged tier's minimum split count
+    pl = smaller;
+  }
+  if (partial_bytes(&b, pl.n) > cap)
+    return einval("fade_tiered_decode_attn_noalloc: %lld bytes of partial results exceed the library scratch's "
+                  "%lld (%lld splits)",
+                  (long long)partial_bytes(&b, pl.n), (long long)cap, (long long)pl.n);
+  hipStream_t st = as_stream(stream);
+  char* base = nullptr;
+  rc = scratch_for(st, &base);
+  if (rc) return rc;
+  return run_plan(&b, p, pl, reinterpret_cast<uint32_t*>(base), base + kScratchCounterBytes, st);
 }

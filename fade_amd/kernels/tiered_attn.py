@@ -188,7 +188,10 @@ class TieredDecodePlan:
     workspace; ``run()`` enqueues the kernels on the current stream.  With
     ``stream`` given, the plan uses the zero-filled workspace shared by the
     calls on that stream (``_lib.stream_workspace``) instead of its own, and
-    must then run on that stream.
+    must then run on that stream.  With ``no_alloc`` the plan allocates no
+    workspace: ``run()`` calls ``fade_tiered_decode_attn_noalloc``, whose
+    kernels use the library's own per-GPU scratch (shared by every such call
+    on that GPU, so such calls must not overlap on one GPU).
     """
 
     def __init__(
@@ -204,6 +207,7 @@ class TieredDecodePlan:
         lens: Tensor | None = None,
         stream: int | None = None,
         deterministic: bool | None = None,
+        no_alloc: bool = False,
     ) -> None:
         if q.dim() != 4 or q.shape[2] != 1:
             raise ValueError(f"q must be [B, Hq, 1, D], got {tuple(q.shape)}")
@@ -234,12 +238,18 @@ class TieredDecodePlan:
             deterministic = torch.are_deterministic_algorithms_enabled()
         a.deterministic = int(bool(deterministic))
         lib = _lib.load()
-        nb = ctypes.c_int64(0)
-        _lib.check(lib.fade_tiered_decode_workspace_bytes(ctypes.byref(a), nb), "fade_tiered_decode_workspace_bytes")
-        self.workspace = (_lib.workspace(nb.value, q.device) if stream is None
-                          else _lib.stream_workspace(nb.value, q.device, stream, B * Hkv * -(-(Hq // Hkv) // 4)))
-        a.workspace, a.workspace_bytes = self.workspace.data_ptr(), self.workspace.numel()
-        self._fn, self._name = lib.fade_tiered_decode_attn, "fade_tiered_decode_attn"
+        if no_alloc:
+            self.workspace = None
+            a.workspace, a.workspace_bytes = None, 0
+            self._fn, self._name = lib.fade_tiered_decode_attn_noalloc, "fade_tiered_decode_attn_noalloc"
+        else:
+            nb = ctypes.c_int64(0)
+            _lib.check(lib.fade_tiered_decode_workspace_bytes(ctypes.byref(a), nb),
+                       "fade_tiered_decode_workspace_bytes")
+            self.workspace = (_lib.workspace(nb.value, q.device) if stream is None
+                              else _lib.stream_workspace(nb.value, q.device, stream, B * Hkv * -(-(Hq // Hkv) // 4)))
+            a.workspace, a.workspace_bytes = self.workspace.data_ptr(), self.workspace.numel()
+            self._fn, self._name = lib.fade_tiered_decode_attn, "fade_tiered_decode_attn"
         self.args = a
         self.out = out
         self._argp = ctypes.byref(a)

@@ -284,6 +284,21 @@ typedef struct fade_decode_args {
 int fade_tiered_decode_workspace_bytes(const fade_decode_args* args, int64_t* bytes);
 int fade_tiered_decode_attn(const fade_decode_args* args, void* stream);
 
+/* fade_tiered_decode_attn without a workspace: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments, kernels
+ * and results as fade_tiered_decode_attn; args->workspace and workspace_bytes
+ * are ignored.  The split counters and partial results live in the library's
+ * own scratch: one 16 MiB array per GPU (256 KiB of counters, at most 65536
+ * (row, kv head, head pass) slots, then partial results), held until the
+ * process ends.  The split count is halved until the partial results fit;
+ * FADE_EINVAL when even one split does not.  Nothing is allocated or freed.
+ * Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU
+ * (other streams, other threads) race and must not be issued.  The first call
+ * on a device zeroes the counter region on its stream; every call leaves the
+ * counters at zero again. */
+int fade_tiered_decode_attn_noalloc(const fade_decode_args* args, void* stream);
+
 /* ---------------- ragged tiered prefill attention -------------------------- */
 /* Masks of fade_tiered_prefill_attn (fade_prefill_args.mask_mode). */
 #define FADE_MASK_BOTTOM_RIGHT 0 /* the cache fully visible, chunk causal: query j sees chunk keys 0..j */
