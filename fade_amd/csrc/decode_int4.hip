@@ -148,6 +148,34 @@ struct FpRow {
   const uint16_t* v;
 };
 
+// Tile loads: non-temporal (read once per launch) unless NT is false (the two
+// head passes of GQA 5-8 read every tile twice).
+template <bool NT>
+__device__ __forceinline__ void tile_dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+  if constexpr (NT) lds_dma16_nt(sbase, voff, lds);
+  else lds_dma16(sbase, voff, lds);
+}
+template <bool NT>
+__device__ __forceinline__ void tile_dma16(const void* g, uint32_t lds) {
+  if constexpr (NT) lds_dma16_nt(g, lds);
+  else lds_dma16(g, lds);
+}
+template <bool NT>
+__device__ __forceinline__ void tile_dma4(const void* sbase, uint32_t voff, uint32_t lds) {
+  if constexpr (NT) lds_dma4_nt(sbase, voff, lds);
+  else lds_dma4(sbase, voff, lds);
+}
+template <bool NT>
+__device__ __forceinline__ void tile_dma2(const void* sbase, uint32_t voff, uint32_t lds) {
+  if constexpr (NT) lds_dma2_nt(sbase, voff, lds);
+  else lds_dma2(sbase, voff, lds);
+}
+template <bool NT>
+__device__ __forceinline__ void tile_dma2(const void* g, uint32_t lds) {
+  if constexpr (NT) lds_dma2_nt(g, lds);
+  else lds_dma2(g, lds);
+}
+
 __device__ __forceinline__ void store_agent(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -155,6 +183,18 @@ __device__ __forceinline__ void store_agent(float* p, float v) {
 __device__ __forceinline__ float load_agent(const float* p) {
   return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT));
+}
+// (m, l) of one partial as one 8-byte device-coherent access
+__device__ __forceinline__ void store_agent2(float* p, float a, float b) {
+  const uint64_t v = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, a)) |
+                     (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, b)) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void load_agent2(const float* p, float& a, float& b) {
+  const uint64_t v =
+      __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  a = __builtin_bit_cast(float, static_cast<uint32_t>(v));
+  b = __builtin_bit_cast(float, static_cast<uint32_t>(v >> 32));
 }
 
 __device__ __forceinline__ float half_of(uint32_t dw, int hi) {
@@ -179,6 +219,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   using S = Stage<KB, VB, FMT>;
   constexpr int kOps = S::kOps, kOpsF16 = S::kOpsF16, kMeta = S::kMeta;
   constexpr int kRowK = 16 * KB, kRowV = 16 * VB;  // packed row bytes of one token
+  constexpr bool kNT = !TWO;                       // tiles are read once per launch
   const int split = blockIdx.x;
   // blockIdx.y = (kv head, head pass): a pass serves up to 4 of the kv head's
   // G query heads, from head h0 of the group (G = 5..8 takes two passes)
@@ -294,7 +335,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     voff[k] = (16 * k + (lane >> 2)) * 64 + 16 * ((lane & 3) ^ ((k ^ (lane >> 4)) & 3));
     koff[k] = (16 * k + (lane >> 2)) * 64 + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
   }
-  auto issue = [&](int64_t tt, uint32_t st) {
+  // kp / vp: the tile's K codes (K rows of an fp16 tile) / everything else;
+  // a stage's K part is refilled as soon as the tile in it has read its K codes
+  auto issue = [&](int64_t tt, uint32_t st, bool kp, bool vp) {
     if (tt >= nFt) {
       const int64_t m0 = (tt - nFt) * kTile;  // the tile's first token of the row's middle
       int64_t r0 = m0;                        // its first row in the tensors
@@ -308,7 +351,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
       const uint8_t* kb = ob >= 0 ? kc + ob : kc + r0 * kRowK;
       const uint8_t* vb = ob >= 0 ? vc + ob : vc + r0 * kRowV;
       const int lim = m0 + kTile > M ? static_cast<int>(M - 1 - m0) : kTile - 1;
-      if (KB == 4) {
+      if (kp && KB == 4) {
         uint32_t ko[4] = {koff[0], koff[1], koff[2], koff[3]};
         if (lim < kTile - 1) {
 #pragma unroll
@@ -319,22 +362,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
           }
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) lds_dma16(kb, ko[k], st + kStageK + 1024 * k);
-      } else {
+        for (int k = 0; k < 4; ++k) tile_dma16<kNT>(kb, ko[k], st + kStageK + 1024 * k);
+      } else if (kp) {
         // 32-byte K rows in natural order
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           const int r = 32 * k + (lane >> 1);
           const int rr = r < lim ? r : lim;
-          lds_dma16(kb, rr * 32 + 16 * (lane & 1), st + kStageK + 1024 * k);
+          tile_dma16<kNT>(kb, rr * 32 + 16 * (lane & 1), st + kStageK + 1024 * k);
         }
       }
+      if (!vp) return;
       if (VB == 8) {
         // 8 KB of int8 codes; the padded tier has all 64 rows of the tile
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           const int r = 8 * k + (lane >> 3);
-          lds_dma16(vb, r * 128 + 16 * ((lane & 7) ^ lit_swz(r)), st + kStageV + 1024 * k);
+          tile_dma16<kNT>(vb, r * 128 + 16 * ((lane & 7) ^ lit_swz(r)), st + kStageV + 1024 * k);
         }
       } else if (VB == 4) {
         uint32_t vo[4] = {voff[0], voff[1], voff[2], voff[3]};
@@ -347,14 +391,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
           }
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) lds_dma16(vb, vo[k], st + kStageV + 1024 * k);
+        for (int k = 0; k < 4; ++k) tile_dma16<kNT>(vb, vo[k], st + kStageV + 1024 * k);
       } else {
         // 32-byte V rows: row r unit u at 2r + (u ^ ((r >> 4) & 1)) (spreads the tr4 reads over more banks)
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           const int r = 32 * k + (lane >> 1);
           const int rr = r < lim ? r : lim;
-          lds_dma16(vb, rr * 32 + 16 * ((lane & 1) ^ ((r >> 4) & 1)), st + kStageV + 1024 * k);
+          tile_dma16<kNT>(vb, rr * 32 + 16 * ((lane & 1) ^ ((r >> 4) & 1)), st + kStageV + 1024 * k);
         }
       }
       if constexpr (ASYM) {
@@ -363,16 +407,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         for (int k = 0; k < 2; ++k) {
           const int r = 32 * k + (lane >> 1);
           const uint32_t o = 8u * (r < lim ? r : lim) + 4u * (lane & 1);
-          lds_dma4(ksg + 4 * r0, o, st + kMeta + 256 * k);
-          lds_dma4(kzg + 4 * r0, o, st + kMeta + 512 + 256 * k);
-          lds_dma4(vsg + 4 * r0, o, st + kMeta + 1024 + 256 * k);
-          lds_dma4(vzg + 4 * r0, o, st + kMeta + 1536 + 256 * k);
+          tile_dma4<kNT>(ksg + 4 * r0, o, st + kMeta + 256 * k);
+          tile_dma4<kNT>(kzg + 4 * r0, o, st + kMeta + 512 + 256 * k);
+          tile_dma4<kNT>(vsg + 4 * r0, o, st + kMeta + 1024 + 256 * k);
+          tile_dma4<kNT>(vzg + 4 * r0, o, st + kMeta + 1536 + 256 * k);
         }
       } else if constexpr (LIT) {
-        lds_dma4(vsg + (m0 / kTile) * kD, 4u * lane, st + kMeta);  // the tile's scale row
+        tile_dma4<kNT>(vsg + (m0 / kTile) * kD, 4u * lane, st + kMeta);  // the tile's scale row
       } else {
         const uint32_t so = 2u * (lane < lim ? lane : lim);
-        lds_dma2(ob >= 0 ? reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(vsg) + ob) : vsg + r0, so,
+        tile_dma2<kNT>(ob >= 0 ? reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(vsg) + ob) : vsg + r0, so,
                  st + kMeta);
       }
     } else {
@@ -384,11 +428,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
       for (int k = 0; k < 4; ++k) {
         const int row = 4 * k + (lane >> 4);
         const FpRow fr = fp16row(f0 + (row < vf ? row : vf - 1));
-        lds_dma16(fr.k + 8 * (u ^ row), st + kStageK + 1024 * k);
-        lds_dma16(fr.v + 8 * u, st + kStageV + 1024 * k);
+        if (kp) tile_dma16<kNT>(fr.k + 8 * (u ^ row), st + kStageK + 1024 * k);
         vr = fr.v;
       }
-      if constexpr (FMT == kFmtSym) lds_dma2(vr, st + kMeta);  // filler: as many loads as a packed tile
+      if (!vp) return;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int row = 4 * k + (lane >> 4);
+        const FpRow fr = fp16row(f0 + (row < vf ? row : vf - 1));
+        tile_dma16<kNT>(fr.v + 8 * u, st + kStageV + 1024 * k);
+      }
+      if constexpr (FMT == kFmtSym) tile_dma2<kNT>(vr, st + kMeta);  // filler: as many loads as a packed tile
     }
   };
 
@@ -414,8 +464,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * F));
   };
   int64_t ta = t0 + wave, tb = t0 + kWaves + wave;  // tiles in stages 0 and 1
-  if (ta < t1) issue(ta, st0);
-  if (tb < t1) issue(tb, st1);
+  if (ta < t1) issue(ta, st0, true, true);
+  if (tb < t1) issue(tb, st1, true, true);
   wait_vm(ops_t(ta) + ops_t(tb));  // the query (and K-scale) loads have landed
   __builtin_amdgcn_wave_barrier();
 
@@ -541,7 +591,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   };
 
   // ---- fp16 tile (16 tokens) from a ring stage ----
-  auto fp16_tile = [&](int64_t t, const lds_u8* sp) {
+  auto fp16_tile = [&](int64_t t, const lds_u8* sp, auto&& after_k) {
     const int64_t f0 = t * kMini;
     const int vf = static_cast<int>(F - f0 < kMini ? F - f0 : kMini);
     // QK^T in the plain layout: k = 32 channels (8 per lane group), columns
@@ -555,6 +605,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
       c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, bq), c4, 0,
                                                   0, 0);
     }
+    after_k();  // the stage's K rows have been read
     float x[4], pr[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = (sq == 0 && 4 * g + i < vf) ? c4[i] * scale_log2 : -INFINITY;
@@ -636,7 +687,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   // K codes -> int8 operand: two's complement (x & m) or offset binary ((x & m) ^ 0x80)
   constexpr uint32_t kFlip = ASYM ? 0x80808080u : 0u;
 
-  auto packed_tile = [&](int64_t t, const lds_u8* sp) {
+  auto packed_tile = [&](int64_t t, const lds_u8* sp, auto&& after_k) {
     float x[4], pr[4];
     if constexpr (!ASYM) {
       // QK^T: A = K codes of token `lane` as int8 (16*c or 64*c)
@@ -736,6 +787,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[i] = fmaf(xs[i], qsc, xz[i]);
     }
+    after_k();  // the stage's K codes have been read
     const int64_t m0 = (t - nFt) * kTile;
     if (m0 + kTile > M) {
       const int valid = static_cast<int>(M - m0);
@@ -852,12 +904,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   // it; afterwards the stage is refilled with a newly claimed tile, returned
   // (>= t1 when the split is exhausted; claims only grow).
   auto step = [&](int64_t cur, int64_t nxt, const lds_u8* sp, uint32_t st) -> int64_t {
-    wait_vm(ops_t(nxt));  // `cur` landed
-    __builtin_amdgcn_wave_barrier();
-    if (cur < nFt) fp16_tile(cur, sp);
-    else packed_tile(cur, sp);
-    __builtin_amdgcn_s_waitcnt(kLgkm0);  // every LDS read of this stage has returned
-    __builtin_amdgcn_wave_barrier();
+    // the tile that refills this stage, known before `cur` is computed
     int64_t nt;
     if constexpr (DET) {  // wave w walks tiles t0 + w, t0 + w + NW, ... : cur's successor's successor
       nt = cur + 2 * kWaves;
@@ -866,7 +913,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
       if (lane == 0) c = __hip_atomic_fetch_add(&claim_s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       nt = t0 + 2 * kWaves + __builtin_amdgcn_readfirstlane(c);
     }
-    if (nt < t1) issue(nt, st);
+    wait_vm(ops_t(nxt));  // `cur` landed
+    __builtin_amdgcn_wave_barrier();
+    // once cur's K codes have been read from the stage, nt's K codes are loaded
+    // into it: they fly during the rest of cur's compute
+    auto refill_k = [&]() {
+      if (nt < t1) {
+        __builtin_amdgcn_s_waitcnt(kLgkm0);
+        __builtin_amdgcn_wave_barrier();
+        issue(nt, st, true, false);
+      }
+    };
+    if (cur < nFt) fp16_tile(cur, sp, refill_k);
+    else packed_tile(cur, sp, refill_k);
+    __builtin_amdgcn_s_waitcnt(kLgkm0);  // every LDS read of this stage has returned
+    __builtin_amdgcn_wave_barrier();
+    if (nt < t1) issue(nt, st, false, true);
     return nt;
   };
   while (ta < t1) {
@@ -933,10 +995,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     } else {
       const int64_t pi = (slot * n + split) * 4 + h;
       store_agent(&p.ws_acc[pi * kD + d], o);
-      if (d == 0) {
-        store_agent(&p.ws_ml[2 * pi], Mh);
-        store_agent(&p.ws_ml[2 * pi + 1], L);
-      }
+      if (d == 0) store_agent2(&p.ws_ml[2 * pi], Mh, L);
     }
   }
   if (n == 1) return;
@@ -970,15 +1029,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     for (int s0 = 0; s0 < n; s0 += kB) {
       float mm[kE][kB], ll[kE][kB], aa[kE][kB];
 #pragma unroll
-      for (int e = 0; e < kE; ++e) {
-        const int idx = tid + e * kThreads;
-        const int h = idx < G * kD ? idx >> 7 : 0, d = idx & (kD - 1);
+      for (int j = 0; j < kB; ++j) {
+        if (s0 + j < n) {  // wave-uniform: only the splits that exist are loaded
 #pragma unroll
-        for (int j = 0; j < kB; ++j) {
-          const int64_t pi = p0 + 4 * (s0 + j < n ? s0 + j : s0) + h;
-          mm[e][j] = load_agent(&p.ws_ml[2 * pi]);
-          ll[e][j] = load_agent(&p.ws_ml[2 * pi + 1]);
-          aa[e][j] = load_agent(&p.ws_acc[pi * kD + d]);
+          for (int e = 0; e < kE; ++e) {
+            const int idx = tid + e * kThreads;
+            const int h = idx < G * kD ? idx >> 7 : 0, d = idx & (kD - 1);
+            const int64_t pi = p0 + 4 * (s0 + j) + h;
+            load_agent2(&p.ws_ml[2 * pi], mm[e][j], ll[e][j]);
+            aa[e][j] = load_agent(&p.ws_acc[pi * kD + d]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < kE; ++e) {
+            mm[e][j] = kNegBig;
+            ll[e][j] = 0.0f;
+            aa[e][j] = 0.0f;
+          }
         }
       }
 #pragma unroll

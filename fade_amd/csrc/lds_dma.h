@@ -38,4 +38,25 @@ __device__ __forceinline__ void lds_dma4(const void* sbase, uint32_t voff, uint3
                : "memory", "m0");
 }
 
+// Non-temporal forms (cache policy nt: the lines are streamed, not kept) for
+// data read once per launch, e.g. the decode's K/V tiles.
+__device__ __forceinline__ void lds_dma16_nt(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "s"(lds_base) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma16_nt(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma2_nt(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_ushort %0, off nt" ::"v"(g), "s"(lds_base) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma2_nt(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_ushort %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4_nt(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
+
 }  // namespace fade
