@@ -122,42 +122,98 @@ def time_plans(plans, steps: int, warmup: int, stream):
 
 
 def time_plans_graph(plans, calls: int, replays: int, warmup: int, stream):
-    """Decode calls as a serving loop issues them: ``calls`` launches (rotating over the
-    instances) captured once in a HIP graph, the graph replayed ``replays`` times with HIP
-    events around each replay on the launch stream.  Returns per-call ms (mean, median) and
-    the wall ms per call of the timed region (synchronized on both sides)."""
+    """Decode calls as a serving loop issues them: the instances' calls captured in HIP
+    graphs of ``calls`` back-to-back launches (several graphs when ``calls`` is shorter than
+    the instance rotation, replayed in turn so that consecutive calls still use different
+    instances), each replay bracketed by HIP events on the launch stream.  Returns per-call
+    ms (mean, median over the ``replays`` samples) and the wall ms per call of the timed
+    region (synchronized on both sides)."""
     for i in range(warmup):
         plans[i % len(plans)].run(stream.cuda_stream)
     torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=stream):
-        for i in range(calls):
-            plans[i % len(plans)].run(stream.cuda_stream)
+    n_graphs = max(1, len(plans) // calls) if calls < len(plans) else 1
+    graphs = []
+    for j in range(n_graphs):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(calls):
+                plans[(j * calls + i) % len(plans)].run(stream.cuda_stream)
+        graphs.append(g)
     with torch.cuda.stream(stream):
-        g.replay()  # first replay uploads the graph
+        for g in graphs:
+            g.replay()  # first replay uploads the graph
     torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     with torch.cuda.stream(stream):
-        for a, b in ev:
+        for r, (a, b) in enumerate(ev):
             a.record(stream)
-            g.replay()
+            graphs[r % n_graphs].replay()
             b.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     per_call = np.array([a.elapsed_time(b) for a, b in ev]) / calls
-    del g
+    del graphs
     return float(per_call.mean()), float(np.median(per_call)), wall_ms / (calls * replays)
 
 
 def graph_split(steps: int, most: int = 32, rotate: int = N_INSTANCES) -> tuple[int, int]:
     """(calls per graph, replays) with calls * replays == steps, calls <= most; a multiple
-    of ``rotate`` when one divides steps (no instance runs twice in a row across replays)."""
+    of ``rotate`` when one divides steps (no instance runs twice in a row across replays).
+    Long graphs keep the replay-launch overhead out of the per-call time; the median over
+    many replays comes from a separate statistics pass (``STATS_REPLAYS``)."""
     divs = [d for d in range(1, min(most, steps) + 1) if steps % d == 0]
     rot = [d for d in divs if d % rotate == 0]
     calls = max(rot) if rot else max(divs)
     return calls, steps // calls
+
+
+STATS_CALLS, STATS_REPLAYS = 20, 10
+
+
+def settle(plans, stream, ms: float = 200.0) -> int:
+    """Untimed decode calls for ``ms`` of wall time before any measurement: the GPU's clocks
+    ramp up over the first ~20 ms of work after idle (per-call times fall by ~8% over the
+    first few hundred calls).  Returns the number of calls made."""
+    n, t0 = 0, time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(20):
+            plans[n % len(plans)].run(stream.cuda_stream)
+            n += 1
+        torch.cuda.synchronize()
+    return n
+
+
+STREAM_WGS = 4096
+
+
+def stream_read_peak(dev, nbytes: int, stream, calls: int = 20, replays: int = 10) -> dict:
+    """Read-only HBM ceiling at the decode's size: ``nbytes`` streamed by one launch of the
+    16-byte non-temporal read kernel of libfade_bench.so, rotating over 4 buffers like the
+    decode instances, timed over HIP-graph replays like the headline."""
+    lib = ctypes.CDLL(os.path.join(ROOT, "fade_amd", "libfade_bench.so"))
+    fn = lib.fade_bench_stream_read
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    nb = nbytes // 16 * 16
+    bufs = [torch.empty(nb, dtype=torch.uint8, device=dev).fill_(i + 1) for i in range(N_INSTANCES)]
+    sink = torch.zeros(STREAM_WGS, dtype=torch.int32, device=dev)
+
+    class _P:
+        def __init__(self, b):
+            self.b = b
+
+        def run(self, s):
+            if fn(self.b.data_ptr(), nb, STREAM_WGS, sink.data_ptr(), s) != 0:
+                raise RuntimeError("fade_bench_stream_read failed")
+
+    plans = [_P(b) for b in bufs]
+    settle(plans, stream, 50.0)
+    mean, med, _ = time_plans_graph(plans, calls, replays, 10, stream)
+    del bufs
+    return {"bytes": nb, "us": round(med * 1e3, 2), "GBps": round(nb / (med * 1e-3) / 1e9, 1),
+            "frac_of_8TBps": round(nb / (med * 1e-3) / 1e9 / HBM_PEAK_GBPS, 3),
+            "kernel": f"16-byte non-temporal loads, {STREAM_WGS} workgroups of 256 threads, 8 loads in flight each"}
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0
@@ -418,38 +474,48 @@ def ragged_decode_case(dev, seed: int = 1004):
     return plans, nbytes, int(paged.k_codes.shape[0])
 
 
-def cpu_baseline(cfg, seed: int):
-    """The oracle's dequantize + concatenate + fp32 SDPA on a bounded sample (two batch rows)."""
-    from oracle import attention as oatt
-    from oracle import quant as oq
+def cpu_baseline(cfg, plans) -> dict:
+    """The reference's CPU decode step (oracle/torch_cpu.py: unpack + dequantize,
+    concatenate the tiers, GQA expansion, SDPA) over the whole config-1 batch (all 16
+    rows), in both working dtypes of the reference's CPU path: fp16 cache with fp32
+    SDPA, and fp32 throughout.  Codes come from the first GPU instance (bit-identical
+    to the oracle's quantizer); median of 5 calls after 2 warmups, per mode."""
+    from oracle import torch_cpu
 
     try:
-        from threadpoolctl import threadpool_info
+        import psutil
 
-        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+        phys = psutil.cpu_count(logical=False)
     except Exception:  # pragma: no cover
-        threads = 1
-    rows = 2
-    q, k, v = kv_tensors(rows, cfg.Hkv, cfg.S, cfg.D, seed=seed, Hq=cfg.Hq)
-    q, k, v = q.numpy(), k.numpy(), v.numpy()
-    ns, nr, S = cfg.n_sink, cfg.recent, cfg.S
-    kq, ks = oq.quant_k_int4(k[:, :, ns : S - nr])
-    vq, vs = oq.quant_v_int4(v[:, :, ns : S - nr])
-    mid = {"fmt": "int4", "kq": kq, "ks": ks, "vq": vq, "vs": vs}
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        K, V = oatt.materialize(k[:, :, :ns], v[:, :, :ns], mid, k[:, :, S - nr :], v[:, :, S - nr :])
-        oatt.sdpa_fp32(q, K.astype(np.float32), V.astype(np.float32))
-        times.append(time.perf_counter() - t0)
-    per_call_us = float(np.median(times)) * 1e6 * cfg.B / rows
+        phys = None
+    threads = torch.get_num_threads()
+    q, sink, mid, rec = plans[0]._keep[:4]
+    host = lambda t: t.detach().to("cpu")  # noqa: E731
+    qc = host(q)
+    sk = (host(sink[0]), host(sink[1]))
+    rc = (host(rec[0]), host(rec[1]))
+    md = (host(mid.k_codes), host(mid.k_scale), host(mid.v_codes), host(mid.v_scale))
+    out = {}
+    for mode in ("fp16", "fp32"):
+        times = []
+        for i in range(7):
+            t0 = time.perf_counter()
+            torch_cpu.decode_step(qc, sk, md, rc, mode=mode)
+            if i >= 2:
+                times.append(time.perf_counter() - t0)
+        out[mode] = round(float(np.median(times)) * 1e6, 1)
     return {
-        "value": round(per_call_us, 1),
-        "unit": "us per decode call (config 1, extrapolated from the sample)",
+        "value": out["fp16"],
+        "unit": "us per decode call (config 1, whole batch)",
         "cores": int(threads),
         "kind": "port",
-        "sample": f"{rows} of {cfg.B} batch rows of config 1, median of 3 runs of oracle dequant+cat+fp32 SDPA, "
-        f"scaled x{cfg.B // rows}; host has {os.cpu_count()} logical CPUs",
+        "sample": f"all {cfg.B} rows of config 1, one decode call = unpack + dequantize + cat + GQA expand + "
+        f"SDPA (torch CPU restatement of fade/quant.py:46-58,124-127, fade/cache.py:715-808, "
+        f"fade/kernels/int4_attention.py:179-202); median of 5 after 2 warmups per mode; value = fp16 cache "
+        f"with fp32 SDPA; fp32 throughout = {out['fp32']} us; {threads} torch threads on a host with "
+        f"{phys} physical cores / {os.cpu_count()} logical CPUs",
+        "fp32_us": out["fp32"],
+        "physical_cores": phys,
     }
 
 
@@ -563,28 +629,40 @@ def main() -> int:
     cfg = CONFIGS[1]
 
     plans = build_instances(cfg, "int4", dev, 1001, N_INSTANCES)
+    settled = settle(plans, stream)
     _, eager_med_ms, eager_mean_ms, _ = time_plans(plans, args.steps, args.warmup, stream)
     calls, replays = graph_split(args.steps)
-    mean_ms, med_ms, ms_step = time_plans_graph(plans, calls, replays, args.warmup, stream)
+    mean_ms, _, ms_step = time_plans_graph(plans, calls, replays, args.warmup, stream)
+    # statistics pass (not the timed K steps): the per-call median over STATS_REPLAYS replays
+    _, med_ms, _ = time_plans_graph(plans, STATS_CALLS, STATS_REPLAYS, 0, stream)
     nbytes = decode_bytes(cfg, "int4")
     achieved = nbytes / (mean_ms * 1e-3) / 1e9
+    cpu = None if args.no_cpu_baseline else cpu_baseline(cfg, plans)
     del plans
     torch.cuda.empty_cache()
+    peak = stream_read_peak(dev, nbytes, stream)
+    torch.cuda.empty_cache()
 
-    extra = {}
+    def graph_us(pl) -> float:
+        """Per-call µs of other decode workloads: settled, then the median of 10 replays of
+        a 20-call graph rotating over the instances."""
+        settle(pl, stream, 50.0)
+        return time_plans_graph(pl, 20, 10, 5, stream)[1] * 1e3
+
+    extra = {"stream_read_ceiling_c1_bytes": peak}
     if not args.no_extra:
         fp = build_instances(cfg, "fp16", dev, 1001, N_INSTANCES)
-        _, fmed, fmean, _ = time_plans(fp, args.steps, args.warmup, stream)
+        fus = graph_us(fp)
         fb = decode_bytes(cfg, "fp16")
         extra["c1_fp16_flash_decode"] = {
-            "us": round(fmean * 1e3, 2), "GBps": round(fb / (fmean * 1e-3) / 1e9, 1), "bytes": fb,
-            "int4_speedup": round(fmean / mean_ms, 2),
+            "us": round(fus, 2), "GBps": round(fb / (fus * 1e-6) / 1e9, 1), "bytes": fb,
+            "int4_speedup": round(fus / (med_ms * 1e3), 2),
         }
         del fp
         torch.cuda.empty_cache()
         # config 1 in the format BASELINE states (asymmetric group-32 INT4 K and V)
         pa = build_instances(cfg, "asym44", dev, 1001, N_INSTANCES)
-        _, _, amean, _ = time_plans(pa, args.steps, args.warmup, stream)
+        amean = graph_us(pa) * 1e-3
         ab = decode_bytes(cfg, "asym44")
         extra["c1_asym_g32_k4v4"] = {
             "us": round(amean * 1e3, 2), "GBps": round(ab / (amean * 1e-3) / 1e9, 1), "bytes": ab,
@@ -630,8 +708,7 @@ def main() -> int:
         extra["c3_per_sequence_assignment_wall_us"] = {"device_path": ps["device"], "host_path": ps["host"],
                                                        "speedup": round(ps["host"] / ps["device"], 2)}
         g2, gg, gb = gqa7_decode_case(dev)
-        _, _, g2mean, _ = time_plans(g2, max(20, args.steps // 4), 20, stream)
-        _, _, ggmean, _ = time_plans(gg, max(20, args.steps // 4), 20, stream)
+        g2mean, ggmean = graph_us(g2) * 1e-3, graph_us(gg) * 1e-3
         extra["c3_shape_decode_gqa7_int4"] = {
             "us_two_head_passes": round(g2mean * 1e3, 2), "us_general_kernel": round(ggmean * 1e3, 2),
             "bytes": gb, "GBps_two_head_passes": round(gb / (g2mean * 1e-3) / 1e9, 1),
@@ -643,7 +720,7 @@ def main() -> int:
         c2 = CONFIGS[2]
         for fmt in ("asym42", "k4v2", "int4", "rot2"):  # asym42: the format BASELINE states for config 2
             pl = build_instances(c2, fmt, dev, 1002, N_INSTANCES)
-            _, m2, mean2, _ = time_plans(pl, max(20, args.steps // 2), args.warmup, stream)
+            mean2 = graph_us(pl) * 1e-3
             b2 = decode_bytes(c2, fmt)
             extra[f"c2_32k_{fmt}"] = {
                 "us": round(mean2 * 1e3, 2), "GBps": round(b2 / (mean2 * 1e-3) / 1e9, 1), "bytes": b2,
@@ -668,12 +745,15 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4 codes / fp16 tiers, fp32 accumulate",
+        "dtype": "int4 K/V codes with fp16 scales and fp16 sink/recent tiers; QK^T of the codes on int8 "
+        "MFMAs against the query times the K scales as a 16-bit fixed-point number in two 8-bit digits "
+        "(exact int32 sums), PV on f16 MFMAs, fp32 softmax and accumulation, fp16 output",
         "data": "synthetic (seeded N(0,1) K*LogNormal(0,0.5) channel scales, V, Q)",
         "config": {
             "workload": "config 1: fused tiered decode, B=16, Hq=32, Hkv=8, D=128, S=8192 "
             "(4 fp16 sink + 8124 INT4 + 64 fp16 recent), reference INT4 format",
             "instances_rotated": N_INSTANCES,
+            "settle_calls_before_timing": settled,
         },
         "roofline": {
             "bound": "hbm",
@@ -683,17 +763,24 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
             "algorithmic_bytes_per_call": nbytes,
-            "timed": f"HIP events around {replays} replays of a HIP graph of {calls} back-to-back calls "
-            f"(rotating over the instances) on the launch stream, per call = replay / {calls} (one kernel: "
-            "decode_packed_kernel<4,4,kFmtSym,4>, split merge fused); eager_us_per_call: HIP events around "
-            "each separately launched call",
+            "timed": f"the K={args.steps} steps: HIP events around each of {replays} replay(s) of a HIP graph "
+            f"of {calls} back-to-back calls (rotating over the {N_INSTANCES} instances) on the launch stream, "
+            f"value = their total / K (one kernel: decode_packed_kernel<4,4,0,4,false,false>, split merge "
+            f"fused); median_us: a separate statistics pass, the median over {STATS_REPLAYS} replays of a "
+            f"{STATS_CALLS}-call graph (per call = replay / {STATS_CALLS}); eager_us_per_call: HIP events "
+            "around each separately launched call",
+            "replays": replays,
+            "calls_per_replay": calls,
             "median_us": round(med_ms * 1e3, 2),
+            "median_replays": STATS_REPLAYS,
             "eager_us_per_call": round(eager_mean_ms * 1e3, 2),
+            "measured_read_ceiling_GBps": peak["GBps"],
+            "frac_of_measured_read_ceiling": round(achieved / peak["GBps"], 3),
         },
         "extra": extra,
     }
-    if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(cfg, 1001)
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
     print(json.dumps(line))
     return 0
 

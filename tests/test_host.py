@@ -191,3 +191,5 @@ def test_host_tier_counts_and_graph_split():
         calls, reps = bench.graph_split(steps)
         assert calls * reps == steps and calls <= 32
     assert bench.graph_split(200) == (20, 10)
+    assert bench.graph_split(20) == (20, 1)
+    assert bench.STATS_REPLAYS >= 10
