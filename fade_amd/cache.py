@@ -108,6 +108,11 @@ class LayerState:
     # rows zero-padded by the reference's per-sequence assignment (row 0's positions,
     # the earlier sink split kept): later per-sequence calls take the host path
     _padded_rows: bool = False
+    # fused attention's ephemeral fp16 forms (never checkpointed): the sink followed by
+    # the dequantized INT2 tier, and the dequantized middle tier of formats the prefill
+    # kernel does not read in place; each with the tensors it was built from
+    _front_cache: tuple | None = None
+    _mid_f16_cache: tuple | None = None
 
     def total_seq_length(self) -> int:
         if self.lens_host is not None:
@@ -295,9 +300,14 @@ class TieredKVCache(DynamicCache):
     _LAYER_SCALAR_KEYS = ("int2_actual_count", "int2_group_size", "sink_count", "next_position")
 
     def cache_state_dict(self) -> dict:
-        """Essential compressed form, on the CPU, same keys as fade/cache.py:510-534."""
-        if any(st.lens is not None for st in self._layers):
-            raise NotImplementedError("cache_state_dict: the ragged layout has no reference checkpoint form")
+        """Essential compressed form, on the CPU, same keys as fade/cache.py:510-534.
+
+        Layers the reference has no form for add keys its loader ignores: a
+        backend-compressed middle tier (``layer.{i}.backend_k.<field>``,
+        ``backend_v.<field>``, ``backend_pos``) and the ragged layout
+        (``layer.{i}.lens``, int32 [B, 3] per-row sink / middle / recent
+        lengths; the tier tensors are then padded capacities, a paged middle
+        tier gathered back into them)."""
         sd: dict = {
             "n_layers": len(self._layers),
             "n_sink": self.n_sink,
@@ -309,27 +319,53 @@ class TieredKVCache(DynamicCache):
             "dtype": str(self.dtype),
         }
         for i, st in enumerate(self._layers):
-            for k in self._LAYER_TENSOR_KEYS:
-                v = getattr(st, k)
+            vals = {k: getattr(st, k) for k in self._LAYER_TENSOR_KEYS}
+            if st.mid_table is not None:  # paged: the padded tensors the pool stands for
+                vals["int4_kq"], vals["int4_ks"], vals["int4_vq"], vals["int4_vs"] = self._mid_padded(st)
+            for k, v in vals.items():
                 if v is not None:
                     sd[f"layer.{i}.{k}"] = v.cpu()
             for k in self._LAYER_SCALAR_KEYS:
                 sd[f"layer.{i}.{k}"] = getattr(st, k)
+            for name in ("backend_k", "backend_v"):
+                d = getattr(st, name)
+                if d is not None:
+                    for f, t in d.items():
+                        sd[f"layer.{i}.{name}.{f}"] = t.cpu()
+            if st.backend_pos is not None:
+                sd[f"layer.{i}.backend_pos"] = st.backend_pos.cpu()
+            if st.lens is not None:
+                sd[f"layer.{i}.lens"] = torch.tensor(st.lens_host, dtype=torch.int32)
         return sd
 
     def load_cache_state_dict(self, sd: dict, device: torch.device | str | None = None) -> None:
-        """Restore from ``cache_state_dict`` output (fade/cache.py:536-559)."""
+        """Restore from ``cache_state_dict`` output (fade/cache.py:536-559), including
+        the build's extra keys (backend-compressed middle tier, ragged layout)."""
+        mv = (lambda t: t.to(device)) if device is not None else (lambda t: t)
         self._layers = []
         for i in range(sd["n_layers"]):
             st = LayerState()
             for k in self._LAYER_TENSOR_KEYS:
                 v = sd.get(f"layer.{i}.{k}")
                 if v is not None:
-                    setattr(st, k, v.to(device) if device is not None else v)
+                    setattr(st, k, mv(v))
             for k in self._LAYER_SCALAR_KEYS:
                 v = sd.get(f"layer.{i}.{k}")
                 if v is not None:
                     setattr(st, k, v)
+            for name in ("backend_k", "backend_v"):
+                pre = f"layer.{i}.{name}."
+                d = {key[len(pre):]: mv(t) for key, t in sd.items() if key.startswith(pre)}
+                if d:
+                    setattr(st, name, d)
+            if sd.get(f"layer.{i}.backend_pos") is not None:
+                st.backend_pos = mv(sd[f"layer.{i}.backend_pos"])
+            lens = sd.get(f"layer.{i}.lens")
+            if lens is not None:
+                st.lens_host = [[int(x) for x in r] for r in lens.tolist()]
+                ref = next((t for t in (st.sink_k, st.fp16_k, st.int4_kq) if t is not None), None)
+                st.lens = lens.to(torch.int32).to(ref.device if ref is not None else (device or "cpu"))
+            st._compressed_bytes = self._layer_compressed_bytes(st)
             self._layers.append(st)
         if sd.get("batch_size") is not None:
             self.batch_size = sd["batch_size"]
@@ -371,6 +407,8 @@ class TieredKVCache(DynamicCache):
         n = int(k.shape[-2])
         B, H, _, D = k.shape
         have = max(r[2] for r in st.lens_host)
+        if st._fp16_buf_k is None and st.fp16_k is not None:  # restored from a checkpoint
+            st._fp16_buf_k, st._fp16_buf_v = st.fp16_k.contiguous(), st.fp16_v.contiguous()
         cap = 0 if st._fp16_buf_k is None else int(st._fp16_buf_k.shape[-2])
         if have + n > cap:
             cap2 = max(2 * cap, have + n, DEFAULT_FP16_PREALLOC)
@@ -1285,7 +1323,9 @@ class TieredKVCache(DynamicCache):
     def prefill_attention(self, q: Tensor, layer_idx: int, sm_scale: float | None = None) -> Tensor:
         """Causal attention of a chunk ``q`` [B, Hq, Sq, D] whose K/V are the last Sq
         tokens of this layer's fp16 tier (just appended by ``update``), over
-        ``[sink | INT4 middle | recent | chunk]`` with the ragged prefill kernel."""
+        ``[sink (+ INT2 tier) | middle | recent | chunk]`` with the ragged prefill kernel.
+        The reference INT4 middle tier is read in place; the other middle formats
+        through their fp16 dequantization, kept between chunks."""
         from .kernels.prefill import tiered_prefill_attention
         from .kernels.tiered_attn import MiddleTier
 
@@ -1296,16 +1336,16 @@ class TieredKVCache(DynamicCache):
         sink, rest = self._fp16_split(st)
         if rest is None or int(rest[0].shape[-2]) < Sq:
             raise RuntimeError("prefill_attention: the chunk's K/V must be the last Sq tokens of the fp16 tier")
-        if st.int2_kq is not None or st.backend_k is not None or (st.int4_kq is not None and self.middle_v_bits != 4):
-            raise NotImplementedError(
-                "prefill_attention: the fused prefill reads fp16 tiers and the reference INT4 middle tier only"
-            )
         n_rest = int(rest[0].shape[-2]) - Sq
         recent = None if n_rest == 0 else (rest[0][..., :n_rest, :], rest[1][..., :n_rest, :])
         chunk = (rest[0][..., n_rest:, :], rest[1][..., n_rest:, :])
+        sink = self._front_tier(st, sink)
         mid = None
-        if st.int4_kq is not None:
+        if st.int4_kq is not None and self.middle_v_bits == 4:
             mid = MiddleTier("int4", st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs)
+        elif st.int4_kq is not None or st.backend_k is not None:
+            mk, mv = self._mid_fp16(st)
+            mid = MiddleTier("fp16", mk, mv)
         return tiered_prefill_attention(q, chunk, sink, mid, recent, sm_scale=sm_scale)
 
     def _prefill_attention_ragged(self, q: Tensor, st: LayerState, sm_scale: float | None) -> Tensor:
@@ -1344,13 +1384,51 @@ class TieredKVCache(DynamicCache):
         return tiered_prefill_attention(q, chunk, sink, mid, (st.fp16_k, st.fp16_v), lens=lens, order=order,
                                         sm_scale=sm_scale)
 
+    def _front_tier(self, st: LayerState, sink):
+        """The fp16 tier the fused kernels read first: the sink, followed by the INT2
+        tier's fp16 dequantization (fade/cache.py:861-876) when the layer has one.
+        Attention over the cache is a softmax over a set of keys, so where the INT2
+        tokens sit among the cache tokens does not change it.  The joined tensors are
+        kept until the sink or the INT2 tier changes."""
+        if st.int2_kq is None:
+            return sink
+        k2, v2 = self._get_int2_dequant(st)
+        c = st._front_cache
+        sk = None if sink is None else sink[0]
+        if c is not None and c[0] is sk and c[1] is k2:
+            return c[2], c[3]
+        if sink is None:
+            fk, fv = k2.contiguous(), v2.contiguous()
+        else:
+            fk, fv = torch.cat([sink[0], k2], dim=-2), torch.cat([sink[1], v2], dim=-2)
+        st._front_cache = (sk, k2, fk, fv)
+        return fk, fv
+
+    def _mid_fp16(self, st: LayerState):
+        """The middle tier as fp16 rows for the chunk prefill of middle formats the
+        prefill kernel does not read in place (K4 + literal INT2 V, backend-compressed
+        tiers): the reference's own dequantization (fade/cache.py:758-763,810-842), kept
+        until the middle tier changes."""
+        if st.int4_kq is not None:
+            k, v = self._get_int4_dequant(st)
+            src = st.int4_kq
+        else:
+            src = st.backend_k["packed"]
+            c = st._mid_f16_cache
+            if c is not None and c[0] is src:
+                return c[1], c[2]
+            k = self._quant_backend.decompress_k(st.backend_k, dtype=self.dtype)
+            v = self._quant_backend.decompress_v(st.backend_v, dtype=self.dtype)
+            st._mid_f16_cache = (src, k, v)
+        return k.contiguous(), v.contiguous()
+
     def decode_attention(self, q: Tensor, layer_idx: int, sm_scale: float | None = None) -> Tensor:
         """Single-token attention of ``q`` [B, Hq, 1, D] straight from this layer's tiers.
 
         Covers the layouts the fused kernel reads in place: sink + recent fp16
         with an INT4 (reference format), INT4-K/INT2-V, rotated or
-        asymmetric middle tier.  An INT2 tier alongside the middle tier
-        interleaves positions and is not supported here.
+        asymmetric middle tier.  An INT2 tier (``int2_budget > 0``) is read as
+        its fp16 dequantization joined to the sink, kept between calls.
         """
         from .kernels.tiered_attn import MiddleTier, tiered_decode_attention
 
@@ -1370,8 +1448,6 @@ class TieredKVCache(DynamicCache):
             sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
             recent = None if st.fp16_k is None or st.fp16_k.shape[-2] == 0 else (st.fp16_k, st.fp16_v)
             return tiered_decode_attention(q, sink, mid, recent, sm_scale, n_splits=self.decode_splits, lens=st.lens)
-        if st.int2_kq is not None:
-            raise RuntimeError("decode_attention: the INT2 tier is not read by the fused kernel; use update()")
         if st.sink_k is not None:
             sink = (st.sink_k, st.sink_v)
             recent = None if st.fp16_k is None else (st.fp16_k, st.fp16_v)
@@ -1381,6 +1457,7 @@ class TieredKVCache(DynamicCache):
             recent = (st.fp16_k[..., ns:, :], st.fp16_v[..., ns:, :])
         else:
             sink = recent = None
+        sink = self._front_tier(st, sink)
         mid = None
         post_rotate = None
         if st.int4_kq is not None:

@@ -87,6 +87,7 @@ struct PParams {
   const int32_t* order;
   Tier sink, recent, chunk;
   int has_mid;
+  int mid_fp16;                           // the middle tier is fp16 rows [B,Hkv,cap,128] (kq / vq)
   int64_t mid_cap, sink_cap, recent_cap;  // padded tier capacities: per-row lengths are clamped to them
   const uint8_t* kq;
   const uint16_t* ks;
@@ -200,6 +201,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int64_t ck_ss = p.chunk.k_ss, cv_ss = p.chunk.v_ss;
   const uint8_t* kq = p.kq + bkv * p.mid_cap * 64;
   const uint8_t* vq = p.vq + bkv * p.mid_cap * 64;
+  // fp16 middle tier: rows of 128 halves, [B, Hkv, cap, 128] contiguous
+  const uint16_t* mk16 = reinterpret_cast<const uint16_t*>(p.kq) + bkv * p.mid_cap * kD;
+  const uint16_t* mv16 = reinterpret_cast<const uint16_t*>(p.vq) + bkv * p.mid_cap * kD;
   const uint16_t* vsr = p.vs + bkv * p.mid_cap;
 
   // K scales of this thread's 32 channels as fp16 pairs, in the stored order
@@ -207,7 +211,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint4 w = make_uint4(0, 0, 0, 0);
-    if (p.has_mid) w = *reinterpret_cast<const uint4*>(p.ks + bkv * kD + 32 * cp + 8 * i);
+    if (p.has_mid && !p.mid_fp16) w = *reinterpret_cast<const uint4*>(p.ks + bkv * kD + 32 * cp + 8 * i);
     const u32x4 st = to_stored(w.x, w.y, w.z, w.w);
 #pragma unroll
     for (int e = 0; e < 4; ++e) ksc[4 * i + e] = st[e];
@@ -308,13 +312,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
     }
   };
-  // fp16 tile (sink, recent or chunk: a few per row): loaded and stored at once
+  // fp16 tile (sink, recent or chunk: a few per row; an fp16 middle tier): loaded and stored at once
   auto load_store_f16 = [&](const TileRef& tr, int buf) {
     uint4 fk[4], fv[4];
     const int key = tr.base + r;
     if (r < tr.cnt) {
-      const uint16_t* kp = tr.seg == 0 ? sk + key * sk_ss : (tr.seg == 2 ? rk + key * rk_ss : ck + key * ck_ss);
-      const uint16_t* vp = tr.seg == 0 ? sv + key * sv_ss : (tr.seg == 2 ? rv + key * rv_ss : cvp + key * cv_ss);
+      const uint16_t* kp = tr.seg == 0 ? sk + key * sk_ss
+                           : (tr.seg == 1 ? mk16 + static_cast<int64_t>(key) * kD
+                                          : (tr.seg == 2 ? rk + key * rk_ss : ck + key * ck_ss));
+      const uint16_t* vp = tr.seg == 0 ? sv + key * sv_ss
+                           : (tr.seg == 1 ? mv16 + static_cast<int64_t>(key) * kD
+                                          : (tr.seg == 2 ? rv + key * rv_ss : cvp + key * cv_ss));
       const uint4* k4 = reinterpret_cast<const uint4*>(kp + 32 * cp);
       const uint4* v4 = reinterpret_cast<const uint4*>(vp + 32 * cp);
 #pragma unroll
@@ -340,7 +348,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // starts (returns true) and completes in store_mid().
   auto begin_tile = [&](int t, int buf) {
     const TileRef tr = tile_of(t);
-    if (tr.seg == 1) {
+    if (tr.seg == 1 && !p.mid_fp16) {
       fetch_mid(tr);
       return true;
     }
@@ -534,9 +542,14 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
     return einval("fade_tiered_prefill_attn: fp16 tiers need 16-byte aligned rows");
   const fade_mid_tier& m = a->mid;
   const bool has_mid = m.len > 0 && m.fmt != FADE_MID_NONE;
-  if (has_mid) {
+  const bool mid_fp16 = has_mid && m.fmt == FADE_MID_FP16;
+  if (has_mid && mid_fp16) {
+    if (!m.k_codes || !m.v_codes || !aligned16(m.k_codes) || !aligned16(m.v_codes))
+      return einval("fade_tiered_prefill_attn: fp16 middle tier pointers missing or misaligned");
+    if (m.pages != nullptr) return einval("fade_tiered_prefill_attn: an fp16 middle tier cannot be paged");
+  } else if (has_mid) {
     if (m.fmt != FADE_MID_SYM || m.k_bits != 4 || m.v_bits != 4)
-      return einval("fade_tiered_prefill_attn: the middle tier must be FADE_MID_SYM 4-bit");
+      return einval("fade_tiered_prefill_attn: the middle tier must be FADE_MID_SYM 4-bit or FADE_MID_FP16");
     if (!m.k_codes || !m.v_codes || !m.k_scale || !m.v_scale || !aligned16(m.k_codes) || !aligned16(m.v_codes) ||
         (reinterpret_cast<uintptr_t>(m.k_scale) & 15))
       return einval("fade_tiered_prefill_attn: middle tier pointers missing or misaligned");
@@ -561,6 +574,7 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   p.recent = tier_of(a->recent);
   p.chunk = tier_of(a->chunk);
   p.has_mid = has_mid ? 1 : 0;
+  p.mid_fp16 = mid_fp16 ? 1 : 0;
   p.mid_cap = has_mid ? m.len : 0;
   p.sink_cap = a->sink.len;
   p.recent_cap = a->recent.len;

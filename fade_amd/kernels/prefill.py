@@ -31,7 +31,8 @@ class TieredPrefillPlan:
             (with ``mask`` ``"top_left"`` / ``"none"``: any length, or None).
         sink, recent: (K, V) [B, Hkv, cap, 128] fp16 padded along S, or None.
         mid: reference INT4 middle tier (``MiddleTier("int4", ...)``) with
-            codes padded to a common row count, or None.
+            codes padded to a common row count, an fp16 one (``MiddleTier("fp16",
+            k, v)``, rows [B, Hkv, S, D]), or None.
         lens: int32 [B, 3] (sink, middle, recent tokens used by each row);
             default: every row uses the full capacities.
         order: optional int32 [B] dispatch order of the batch rows (longest first).
@@ -73,8 +74,10 @@ class TieredPrefillPlan:
             n_c = Sq if mask == "bottom_right" else int(chunk[0].shape[2])
             if tuple(chunk[0].shape) != (B, Hkv, n_c, D) or chunk[1].shape != chunk[0].shape:
                 raise ValueError(f"chunk K/V must be [B, Hkv, {'Sq=' if mask == 'bottom_right' else ''}{n_c}, D]")
-        if mid is not None and mid.fmt not in ("int4", "sym"):
-            raise ValueError("the prefill kernel reads the reference INT4 middle tier")
+        if mid is not None and mid.fmt not in ("int4", "sym", "fp16"):
+            raise ValueError("the prefill kernel reads the reference INT4 middle tier or an fp16 one")
+        if mid is not None and mid.fmt == "fp16" and (mid.k_codes.dtype != torch.float16 or mid.k_codes.shape[-1] != D):
+            raise ValueError("an fp16 middle tier holds float16 rows [B, Hkv, S, D]")
         if q.stride(-1) != 1:
             q = q.contiguous()
         caps = [int(sink[0].shape[2]) if sink else 0, mid.n_tokens if mid else 0, int(recent[0].shape[2]) if recent else 0]

@@ -281,7 +281,8 @@ def test_ragged_layout_chunk_prefill_matches_single_rows(dev):
 
 
 def test_ragged_layout_rejects_shared_calls(dev):
-    """A ragged layer refuses the shared-tier entry point and the checkpoint form."""
+    """A ragged layer refuses the shared-tier entry point; its checkpoint carries the
+    per-row lengths (layer.{i}.lens, a key the reference's loader ignores)."""
     rag = TieredKVCache(n_sink=2, recent_window=4, int4_budget=None, int2_budget=0, head_dim=128)
     rag.ragged_layout = True
     kv = torch.randn(2, 2, 20, 128).half().to(dev)
@@ -290,8 +291,8 @@ def test_ragged_layout_rejects_shared_calls(dev):
     rag.apply_tier_assignment_per_sequence(0, tiers.unsqueeze(0).expand(2, -1).contiguous())
     with pytest.raises(NotImplementedError):
         rag.apply_tier_assignment(0, tiers)
-    with pytest.raises(NotImplementedError):
-        rag.cache_state_dict()
+    sd = rag.cache_state_dict()
+    assert sd["layer.0.lens"].tolist() == rag._layers[0].lens_host
 
 
 @pytest.mark.parametrize("budget", [None, 50])
