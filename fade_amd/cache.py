@@ -195,6 +195,12 @@ class TieredKVCache(DynamicCache):
         # ragged layout: a fade_amd.pages.MiddlePagePool to keep the middle tier in
         # 64-token pages (per-row memory instead of padding to the longest row)
         self.page_pool = None
+        # The device reassignment's gather reports tokens it had to drop in a status
+        # word (a position outside the RoPE tables, a slot past a tier's capacity, a
+        # token a row does not have: a plan the cache did not make).  Reading it costs
+        # a host synchronization, so by default it is not read; True reads it after
+        # every device reassignment and raises RuntimeError when a bit is set.
+        self.check_reassign_status = False
         # split count of the fused decode kernel (0: the kernel's planner fills the GPU)
         self.decode_splits = 0
         self._last_reassign_counts = None
@@ -750,6 +756,21 @@ class TieredKVCache(DynamicCache):
             out[key] = o
         return out
 
+    _STATUS_BITS = {1: "INT2 tokens in the plan", 2: "an unknown tier value",
+                    4: "a position outside the RoPE tables", 8: "a slot past a tier's capacity",
+                    16: "a token the row does not have"}
+
+    def _check_status(self, cnt: Tensor, rows: int) -> None:
+        """With ``check_reassign_status``: raise if the gather dropped a token (see __init__)."""
+        if not self.check_reassign_status:
+            return
+        words = cnt.view(-1, 4)[:rows, 3].cpu().tolist()
+        bad = [(r, w) for r, w in enumerate(words) if w]
+        if bad:
+            r, w = bad[0]
+            what = ", ".join(t for b, t in self._STATUS_BITS.items() if w & b) or f"status {w:#x}"
+            raise RuntimeError(f"device reassignment dropped tokens (row {r}): {what}")
+
     def _apply_tier_assignment_device(self, layer_idx: int, tiers: Tensor, counts) -> bool:
         """``apply_tier_assignment`` on the device for the reference INT4 layout.
 
@@ -896,6 +917,7 @@ class TieredKVCache(DynamicCache):
         st._compressed_bytes = self._layer_compressed_bytes(st)
         st.sink_count = n_sink_new
         self._last_reassign_counts = cnt
+        self._check_status(cnt, 1)
         return True
 
     def apply_tier_assignment(
@@ -1159,6 +1181,7 @@ class TieredKVCache(DynamicCache):
         st.int4_k_deq = st.int4_v_deq = st.int2_k_deq = st.int2_v_deq = None
         st._compressed_bytes = self._layer_compressed_bytes(st)
         self._last_reassign_counts = cnt
+        self._check_status(cnt, B)
         return pos_new
 
     def _apply_per_sequence_device(self, layer_idx: int, tiers_per_row: Tensor) -> bool:

@@ -40,10 +40,11 @@ class MiddleTier:
     fmt ``"asym"``: codes [B,Hkv,S,D*bits/8], scale/zero [B,Hkv,S,D/group].
     fmt ``"fp16"``: ``k_codes``/``v_codes`` fp16 [B,Hkv,S,D].
 
-    Paged (``"int4"``/``"sym"``/``"asym"``, decode only): ``pages`` int32
-    [B, pages_per_row] holds the page of each 64-token tile of a row, and every
-    per-token tensor is a pool [n_pages, Hkv, 64, ...] (``paginate_middle``
-    builds one); ``length`` is the longest row's middle.
+    Paged (``"int4"``/``"sym"``/``"asym"``): ``pages`` int32 [B, pages_per_row]
+    holds the page of each 64-token tile of a row, and every per-token tensor is
+    a pool [n_pages, Hkv, 64, ...] (``paginate_middle`` builds one); ``length``
+    is the longest row's middle.  Decode reads every paged format; the chunk
+    prefill reads a paged reference INT4 tier (separate pools, no page_stride).
     """
 
     fmt: str

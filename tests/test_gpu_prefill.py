@@ -87,14 +87,16 @@ def test_tiered_prefill_ragged(dev, B, Hq, Hkv, Sq, rows):
     assert np.abs(out.float().cpu().numpy() - ref).max() <= ATOL
 
 
-def test_tiered_prefill_paged_middle(dev):
+@pytest.mark.parametrize("heads", [(32, 8), (28, 4), (20, 4)])
+def test_tiered_prefill_paged_middle(dev, heads):
     """A paged middle tier (64-token pages of one pool, shuffled, per-row block table):
-    the kernel reads the pages in place and gives the padded layout's output bit for bit."""
+    the kernel reads the pages in place and gives the padded layout's output bit for bit;
+    at 4 query heads per kv head (one head pass) and at 7 and 5 (two head passes)."""
     from fade_amd.kernels.tiered_attn import paginate_middle
 
-    print("case prefill paged middle", flush=True)
+    print(f"case prefill paged middle heads={heads}", flush=True)
     rows = [(4, 700, 64), (4, 130, 20), (2, 0, 64), (1, 64, 5)]
-    q, chunk, sink, mid, rec, lens, ref = _ragged(dev, 4, 32, 8, 96, rows, seed=4500)
+    q, chunk, sink, mid, rec, lens, ref = _ragged(dev, 4, heads[0], heads[1], 96, rows, seed=4500)
     n_pages = sum(-(-r[1] // 64) for r in rows)
     paged = paginate_middle(mid, [r[1] for r in rows], order=np.random.default_rng(3).permutation(n_pages))
     out_r = tiered_prefill_attention(q, chunk, sink, mid, rec, lens=lens)

@@ -193,3 +193,21 @@ def test_host_tier_counts_and_graph_split():
     assert bench.graph_split(200) == (20, 10)
     assert bench.graph_split(20) == (20, 1)
     assert bench.STATS_REPLAYS >= 10
+
+
+def test_reassign_status_check():
+    """check_reassign_status reads the gather's status word and names the dropped tokens
+    (a fabricated counts tensor: host logic only)."""
+    import pytest
+    import torch
+
+    from fade_amd.cache import TieredKVCache
+
+    c = TieredKVCache(head_dim=128)
+    ok = torch.tensor([3, 5, 8, 0], dtype=torch.int32)
+    bad = torch.tensor([[3, 5, 8, 0], [3, 5, 8, 8 | 16]], dtype=torch.int32)
+    c._check_status(bad, 2)  # off by default: nothing read
+    c.check_reassign_status = True
+    c._check_status(ok, 1)
+    with pytest.raises(RuntimeError, match="row 1.*slot past a tier's capacity.*token the row does not have"):
+        c._check_status(bad, 2)
