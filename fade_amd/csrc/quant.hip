@@ -345,15 +345,13 @@ __global__ __launch_bounds__(kBlock) void quant_asym_kernel(const uint16_t* __re
     mx = group_max<LPG>(mx);
     const uint16_t sc = f2h((mx - mn) / QMAXU);
     const float s = h2f(sc);
+    // one correctly rounded reciprocal per group, then a rounded product per element
+    const float inv = s == 0.0f ? 0.0f : 1.0f / s;
     int code[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      if (s == 0.0f) {
-        code[j] = 0;
-      } else {
-        const float t = rintf((v[j] - mn) / s);
-        code[j] = static_cast<int>(fminf(fmaxf(t, 0.0f), QMAXU));
-      }
+      const float t = rintf((v[j] - mn) * inv);
+      code[j] = static_cast<int>(fminf(fmaxf(t, 0.0f), QMAXU));
     }
     uint8_t* dst = packed + r * ROW_BYTES + c * BITS;
     if (BITS == 4) {

@@ -238,8 +238,12 @@ def quant_asym_group(x: np.ndarray, bits: int, group: int = 32):
       mn, mx  = min / max of the group (exact fp16)
       scale   = fp16( fp32(mx - mn) / (2^bits - 1) )
       zero    = mn
-      code    = 0 if scale == 0 else clamp(rne( fp32(x - mn) / fp32(scale) ), 0, 2^bits-1)
+      inv     = 0 if scale == 0 else fp32( 1 / fp32(scale) )   (one reciprocal per group)
+      code    = clamp(rne( fp32( fp32(x - mn) * inv ) ), 0, 2^bits-1)
       x_hat   = fp16( fp32(code * scale) + zero )
+    The product with the rounded reciprocal can differ from the correctly
+    rounded quotient by an ulp, so a code may differ from rne((x - mn) / scale)
+    only where that quotient lies within a few ulps of a half-integer.
     Packing: 4-bit unsigned nibbles, high nibble = even index; 2-bit
     unsigned, four per byte, first element in the top bits.
     """
@@ -254,9 +258,9 @@ def quant_asym_group(x: np.ndarray, bits: int, group: int = 32):
     scale16 = ((mx - mn).astype(F32) / F32(qmax)).astype(F16)
     s32 = scale16.astype(F32)
     with np.errstate(divide="ignore", invalid="ignore"):
-        t = ((xg - mn).astype(F32) / s32).astype(F32)
-        q = np.clip(np.rint(t), 0, qmax)
-    q = np.where(s32 == 0, 0, q).astype(np.uint8).reshape(*lead, D)
+        inv = np.where(s32 == 0, F32(0), F32(1) / s32).astype(F32)
+    t = ((xg - mn).astype(F32) * inv).astype(F32)
+    q = np.clip(np.rint(t), 0, qmax).astype(np.uint8).reshape(*lead, D)
     if bits == 4:
         packed = ((q[..., 0::2] << 4) | q[..., 1::2]).astype(np.uint8)
     elif bits == 2:

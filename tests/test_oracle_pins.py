@@ -185,6 +185,19 @@ def test_asym_group_invariants(bits):
     err = np.abs(deq - xg.astype(np.float32))
     bound = 0.5 * scale.astype(np.float32)[..., None] * 1.01 + 8e-3
     assert np.all(err <= bound)
+    # codes are the nearest integers to the exact quotient (x - min) / scale,
+    # clamped, wherever that quotient is not within 1e-5 of a half-integer
+    s64 = scale.astype(np.float64)[..., None]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        exact = (xg.astype(np.float64) - zero.astype(np.float64)[..., None]) / s64
+    want = np.clip(np.floor(exact + 0.5), 0, qmax)
+    clear = (s64 > 0) & (np.abs(exact - np.floor(exact) - 0.5) > 1e-5)
+    clear = np.broadcast_to(clear, codes.shape)
+    assert clear.mean() > 0.99
+    assert np.array_equal(codes[clear], want[clear].astype(codes.dtype))
+    # the group maximum lands on the top code or one below it (the fp16 scale rounds either way)
+    top = codes.max(axis=-1)[nz]
+    assert np.all(top >= qmax - 1)
 
 
 # ------------------------------------------------------------------- RoPE
