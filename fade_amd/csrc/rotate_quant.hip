@@ -2,12 +2,15 @@
 // (fade/rotated_quant.py:106-131,148-173) for fp16 K/V with head_dim 128.
 //
 // x_rot = x @ R^T runs on f16 matrix cores without leaving the chip.  x is
-// fp16, so it is exact as an MFMA operand; R is split into
-// R_hi = fp16(R) and R_lo = fp16((R - R_hi) * 2^12), and
-// x_rot = x R_hi^T + 2^-12 (x R_lo^T) with fp32 accumulation, which carries R
-// to about 2^-22 relative: the error of an fp32 GEMM, not of an fp16 one.
-// The quantizer then follows the reference's fp32 steps as quant.hip's
-// rotated path does: inv = fp32(fp32(1 / max(absmax, 1e-8)) * qmax),
+// fp16, so it is exact as an MFMA operand; R is carried at scale 2^10 as
+// R_hi = fp16(2^10 R) and R_lo = fp16(2^10 R - R_hi) (both normal for every
+// entry that matters), and both products accumulate into one fp32 register:
+// y = x R_hi^T + x R_lo^T = 2^10 x_rot to about 2^-22 relative, the error of
+// an fp32 GEMM, not of an fp16 one.  The power-of-two scale is exact in fp32,
+// so it is folded into the quantizer rather than divided out: absmax =
+// 2^-10 max|y|, and y * (2^-10 inv) is the same fp32 product as x_rot * inv.
+// The quantizer follows the reference's fp32 steps as quant.hip's rotated
+// path does: inv = fp32(fp32(1 / max(absmax, 1e-8)) * qmax),
 // code = clamp(rne(fp32(x_rot * inv))), scale = fp16(absmax / qmax).
 //
 // MFMA (32x32x16 f16): C^T[out channel][row] = R[out][in] x^T[in][row].
@@ -34,7 +37,8 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kRows = 32;     // rows per wave tile
 constexpr int kRPitch = 136;  // halves per R row in LDS: 16-byte reads of 8 rows hit distinct banks
-constexpr float kLoScale = 4096.0f;
+constexpr float kRScale = 1024.0f;         // R is carried as 2^10 R
+constexpr float kRUnscale = 1.0f / 1024.0f;
 
 template <int BITS>
 struct RQ;
@@ -80,8 +84,9 @@ __device__ __forceinline__ void load_r(const float* __restrict__ R, RTile& rt) {
     const float f[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const _Float16 h = static_cast<_Float16>(f[j]);
-      const _Float16 l = static_cast<_Float16>((f[j] - static_cast<float>(h)) * kLoScale);
+      const float fs = f[j] * kRScale;  // exact
+      const _Float16 h = static_cast<_Float16>(fs);
+      const _Float16 l = static_cast<_Float16>(fs - static_cast<float>(h));
       rt.hi[row][col + j] = __builtin_bit_cast(uint16_t, h);
       rt.lo[row][col + j] = __builtin_bit_cast(uint16_t, l);
     }
@@ -97,25 +102,25 @@ __device__ __forceinline__ void load_x(const uint16_t* __restrict__ x, int64_t o
     xb[ks] = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(x + off + 16 * ks + 8 * h));
 }
 
-// Output tile mt (channels 32 mt .. + 31) of x_rot for the wave's 32 rows.
+// Output tile mt (channels 32 mt .. + 31) of 2^10 x_rot for the wave's 32 rows.
 __device__ __forceinline__ f32x16 rotate_tile(const f16x8 (&xb)[8], const RTile& rt, int mt, int n, int h) {
-  f32x16 hi = {}, lo = {};
+  f32x16 acc = {};
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
     const f16x8 ah = *reinterpret_cast<const f16x8*>(&rt.hi[32 * mt + n][16 * ks + 8 * h]);
     const f16x8 al = *reinterpret_cast<const f16x8*>(&rt.lo[32 * mt + n][16 * ks + 8 * h]);
-    hi = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, xb[ks], hi, 0, 0, 0);
-    lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, xb[ks], lo, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, xb[ks], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, xb[ks], acc, 0, 0, 0);
   }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) hi[i] = fmaf(lo[i], 1.0f / kLoScale, hi[i]);
-  return hi;
+  return acc;
 }
 
-__device__ __forceinline__ float sym_inv(float absmax, float qmax, uint16_t* scale_h) {
-  const float a = fmaxf(absmax, 1e-8f);
+// From the scaled absmax (2^10 max|x_rot|): the scale, and the inverse scale
+// for the scaled values (2^-10 inv).
+__device__ __forceinline__ float sym_inv(float absmax_scaled, float qmax, uint16_t* scale_h) {
+  const float a = fmaxf(absmax_scaled * kRUnscale, 1e-8f);
   *scale_h = f2h(a / qmax);
-  return (1.0f / a) * qmax;
+  return ((1.0f / a) * qmax) * kRUnscale;
 }
 
 // Code of x * inv as the low bits of an fp32: clamp to [lo, hi] (integer
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(kThreads) void rotq_token_kernel(const uint16_t* __
   }
 }
 
-// Per-channel pass 1: column absmax of x_rot over S-block blockIdx.x of (b, h) = blockIdx.y.
+// Per-channel pass 1: column absmax of 2^10 x_rot over S-block blockIdx.x of (b, h) = blockIdx.y.
 __global__ __launch_bounds__(kThreads) void rotq_colmax_kernel(const uint16_t* __restrict__ x, Geom gm,
                                                                int64_t rows_per_block, const float* __restrict__ R,
                                                                float* __restrict__ partial) {
