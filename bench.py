@@ -67,7 +67,7 @@ def build_instances(cfg, fmt: str, dev, seed: int, n: int):
     km, vm = kd[:, :, ns : S - nr].contiguous(), vd[:, :, ns : S - nr].contiguous()
     sink = (kd[:, :, :ns].contiguous(), vd[:, :, :ns].contiguous())
     rec = (kd[:, :, S - nr :].contiguous(), vd[:, :, S - nr :].contiguous())
-    pre = None
+    rot = None
     if fmt == "int4":
         kq, ks = fq.quant_k_int4(km)
         vq, vs = fq.quant_v_int4(vm)
@@ -81,7 +81,7 @@ def build_instances(cfg, fmt: str, dev, seed: int, n: int):
         kq, ks = frq.rotated_quant_k(km, R, 2)
         vq, vs = frq.rotated_quant_v(vm, R, 2)
         mid = MiddleTier("sym", kq, vq, ks, vs, k_bits=2, v_bits=2)
-        pre = R
+        rot = R  # q, sink and recent stay in the model's basis: the kernel rotates
     elif fmt.startswith("asym"):
         kb, vb = int(fmt[4]), int(fmt[5])
         kq, ks, kz = fq.quant_asym(km, kb, 32)
@@ -95,10 +95,9 @@ def build_instances(cfg, fmt: str, dev, seed: int, n: int):
         m = MiddleTier(mid.fmt, *(t.clone() if t is not None else None for t in
                                   (mid.k_codes, mid.v_codes, mid.k_scale, mid.v_scale, mid.k_zero, mid.v_zero)),
                        k_bits=mid.k_bits, v_bits=mid.v_bits, group=mid.group, length=mid.length)
-        qq = qd if pre is None else (qd.float() @ pre.T).to(torch.float16)
-        s = tuple(t.clone() for t in sink) if pre is None else tuple((t.float() @ pre.T).half() for t in sink)
-        r = tuple(t.clone() for t in rec) if pre is None else tuple((t.float() @ pre.T).half() for t in rec)
-        plans.append(TieredDecodePlan(qq, s, m, r))
+        s = tuple(t.clone() for t in sink)
+        r = tuple(t.clone() for t in rec)
+        plans.append(TieredDecodePlan(qd, s, m, r, rotation=rot))
     return plans
 
 
@@ -726,6 +725,8 @@ def main() -> int:
                 "us": round(mean2 * 1e3, 2), "GBps": round(b2 / (mean2 * 1e-3) / 1e9, 1), "bytes": b2,
                 "frac_of_peak": round(b2 / (mean2 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 3),
             }
+            if fmt == "rot2":  # the product path: unrotated q / sink / recent, R applied in the kernel
+                extra[f"c2_32k_{fmt}"]["rotation"] = "in kernel (q R^T for the middle, middle output part times R)"
             del pl
             torch.cuda.empty_cache()
 

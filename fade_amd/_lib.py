@@ -98,6 +98,7 @@ class DecodeArgs(ctypes.Structure):
         ("workspace_bytes", _i64),
         ("lens", _p),
         ("deterministic", _i32),
+        ("rotation", _p),
     ]
 
 

@@ -1482,7 +1482,7 @@ class TieredKVCache(DynamicCache):
             sink = recent = None
         sink = self._front_tier(st, sink)
         mid = None
-        post_rotate = None
+        rotation = None
         if st.int4_kq is not None:
             if self.middle_v_bits == 4:
                 mid = MiddleTier("int4", st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs)
@@ -1497,13 +1497,12 @@ class TieredKVCache(DynamicCache):
             if isinstance(be, RotatedINT4Backend):
                 if be.bits == 3:
                     raise RuntimeError("decode_attention: 3-bit rotated codes are not read by the fused kernel")
-                R = be._get_R(q.device)
+                # the kernel scores the middle with q R^T and un-rotates its part of the output
+                rotation = be._get_R(q.device)
                 mid = MiddleTier(
                     "sym", bk["packed"], bv["packed"], bk["scale"].to(torch.float16),
                     bv["scale"].to(torch.float16), k_bits=be.bits, v_bits=be.bits,
                 )
-                q = (q.float() @ R.T).to(torch.float16)
-                post_rotate = R
             elif isinstance(be, AsymGroupBackend):
                 mid = MiddleTier(
                     "asym", bk["packed"], bv["packed"], bk["scale"], bv["scale"], bk["zero"], bv["zero"],
@@ -1511,14 +1510,8 @@ class TieredKVCache(DynamicCache):
                 )
             else:
                 raise RuntimeError(f"decode_attention: backend {be.name} is not read by the fused kernel")
-        if post_rotate is not None:
-            # Sink/recent are unrotated fp16; attend in the rotated basis for all tiers.
-            sink = None if sink is None else tuple((t.float() @ post_rotate.T).to(torch.float16) for t in sink)
-            recent = None if recent is None else tuple((t.float() @ post_rotate.T).to(torch.float16) for t in recent)
-        out = tiered_decode_attention(q, sink, mid, recent, sm_scale, n_splits=self.decode_splits)
-        if post_rotate is not None:
-            out = (out.float() @ post_rotate).to(torch.float16)
-        return out
+        return tiered_decode_attention(q, sink, mid, recent, sm_scale, n_splits=self.decode_splits,
+                                       rotation=rotation)
 
 
 __all__ = [

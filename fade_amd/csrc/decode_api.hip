@@ -121,6 +121,12 @@ int validate(const fade_decode_args* a) {
     }
   }
   if (a->kernel < 0 || a->kernel > 3) return einval("fade_tiered_decode_attn: kernel must be 0, 1, 2 or 3");
+  if (a->rotation != nullptr && a->mid.len > 0) {
+    if (a->mid.fmt != FADE_MID_SYM)
+      return einval("fade_tiered_decode_attn: a rotation applies to a FADE_MID_SYM middle tier");
+    if (reinterpret_cast<uintptr_t>(a->rotation) & 15)
+      return einval("fade_tiered_decode_attn: rotation must be 16-byte aligned");
+  }
   return FADE_OK;
 }
 
@@ -165,6 +171,7 @@ Params to_params(const fade_decode_args* a) {
   p.lens = a->lens;
   p.deterministic = a->deterministic;
   p.passes = static_cast<int>((p.G + 3) / 4);
+  p.rot = m.len > 0 ? a->rotation : nullptr;  // no middle tokens: nothing is rotated
   return p;
 }
 
@@ -193,14 +200,25 @@ Plan make_plan(const fade_decode_args* a, const Params& p) {
     const int64_t nT = int4_tiles(p);
     const int64_t pairs = a->B * a->Hkv * p.passes;  // workgroups per split
     int64_t want = a->n_splits > 0 ? a->n_splits : (int4_resident_wgs(p) + pairs / 2) / pairs;
+    pl.n_f16_tiles = int4_fp16_tiles(p);
+    pl.tps = 0;
+    if (p.rot != nullptr) {
+      // rotated middle tier: split 0 = the fp16 tiles, then middle splits of equal tile counts
+      const int64_t nMt = nT - pl.n_f16_tiles;
+      int64_t ms = want - 1;
+      if (ms > nMt) ms = nMt;
+      if (ms < 1) ms = 1;
+      if (p.mid.pages != nullptr && ms < cdiv(nMt, kPageSlots)) ms = cdiv(nMt, kPageSlots);
+      pl.tiles_per_split = cdiv(nMt, ms);
+      pl.n = 1 + cdiv(nMt, pl.tiles_per_split);
+      return pl;
+    }
     if (want > nT) want = nT;
     if (want < 1) want = 1;
     // paged middle tier: a split's page ids fit the workgroup's kPageSlots
     if (p.mid.pages != nullptr && want < cdiv(nT, kPageSlots)) want = cdiv(nT, kPageSlots);
     pl.tiles_per_split = cdiv(nT, want);
     pl.n = cdiv(nT, pl.tiles_per_split);
-    pl.n_f16_tiles = int4_fp16_tiles(p);
-    pl.tps = 0;
     return pl;
   }
   const bool mfma = pl.k == Kern::kMfma;
@@ -224,6 +242,9 @@ int run_plan(const fade_decode_args* a, Params& p, const Plan& pl, uint32_t* cou
   if ((a->kernel == 2 || a->kernel == 3) && pl.k == Kern::kValu)
     return einval("fade_tiered_decode_attn: the matrix-core kernels do not handle this middle tier (format %d)",
                   p.mid.fmt);
+  if (p.rot != nullptr && pl.k != Kern::kInt4)
+    return einval("fade_tiered_decode_attn: a rotated middle tier needs the matrix-core INT4 kernel "
+                  "(FADE_MID_SYM with 4- or 2-bit K and V, GQA <= 8)");
   if ((a->lens != nullptr || a->mid.pages != nullptr) && pl.k != Kern::kInt4)
     return einval("fade_tiered_decode_attn: per-row lengths and paged middle tiers need the matrix-core INT4 "
                   "kernel (middle tier FADE_MID_SYM or FADE_MID_ASYM, GQA <= 8)");

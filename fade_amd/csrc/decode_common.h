@@ -56,6 +56,11 @@ struct Params {
   const int32_t* lens;      // optional [B][3] per-row sink / middle / recent lengths
   int32_t deterministic;    // INT4 kernel: fixed round-robin tile order instead of claims
   int passes;               // INT4 kernel: head passes per kv head, ceil(G / 4): 1 or 2
+  // INT4 kernel, FADE_MID_SYM: the rotated backend's R (fp32 [kD][kD]); the
+  // middle tier then holds codes of x R^T.  Split 0 takes the fp16 tiles,
+  // splits 1.. the middle tiles (scored with q R^T); the merge returns
+  // fp16 part + (middle part) R.  nullptr: no rotation.
+  const float* rot;
 };
 
 // Signed symmetric code of channel d in a packed row (fade/quant.py:26-43,

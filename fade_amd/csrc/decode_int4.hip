@@ -210,7 +210,7 @@ __device__ __forceinline__ int lit_swz(int r) { return ((r >> 1) & 3) | ((r >> 2
 // formats, 8 or 10 KB for the asymmetric ones, 12.25 KB for literal INT2 V).
 // NW waves per workgroup (4, 6 or 8; see packed_kernel); registers are sized
 // for two waves per SIMD.
-template <int KB, int VB, int FMT, int NW, bool DET, bool TWO>
+template <int KB, int VB, int FMT, int NW, bool DET, bool TWO, bool ROT>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_packed_kernel(
     Params p) {
   constexpr int kWaves = NW, kThreads = 64 * NW;
@@ -249,8 +249,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     nFt = (F + kMini - 1) / kMini;
   }
   const int64_t nT = nFt + (M + kTile - 1) / kTile;
-  const int64_t t0 = static_cast<int64_t>(split) * p.tiles_per_split;
-  const int64_t t1 = t0 + p.tiles_per_split < nT ? t0 + p.tiles_per_split : nT;
+  // rotated middle tier: split 0 takes the fp16 tiles, splits 1.. the middle
+  // tiles, so that every split's partial lies in one basis
+  static_assert(!ROT || FMT == kFmtSym, "the rotated backend's middle tier is symmetric");
+  constexpr bool rot = ROT;  // the ROT instances serve p.rot != nullptr
+  const int64_t t0 = !rot ? static_cast<int64_t>(split) * p.tiles_per_split
+                          : (split == 0 ? 0 : nFt + static_cast<int64_t>(split - 1) * p.tiles_per_split);
+  const int64_t t1 = rot && split == 0 ? nFt : (t0 + p.tiles_per_split < nT ? t0 + p.tiles_per_split : nT);
   // Tiles of the split: the first two of each wave are t0 + wave and
   // t0 + NW + wave; after that waves claim tiles t0 + 2 NW + c in order
   // through an LDS counter, so that a wave that runs faster (e.g. the older
@@ -270,6 +275,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   __shared__ int qoff_s[4][kGroups];    // asymmetric: 128 * sum of the query digits of a group
   __shared__ float qg_s[4][kGroups];    // asymmetric: sum of the query of a group (log2 domain)
   __shared__ float red_m[kWaves][4], red_l[kWaves][4];
+  __shared__ float qrot_s[ROT ? kHeads : 1][ROT ? kD : 1];  // q R^T (rotated tier)
   __shared__ int last_s;
 
   // Paged middle tier: per-token tensors are pools [page][Hkv][64][...] and
@@ -463,17 +469,83 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     else if (c == A + F) __builtin_amdgcn_s_waitcnt(vmcnt_imm(A + F));
     else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * F));
   };
+  // ---- rotated middle tier: q R^T of the pass's heads, for the middle splits ----
+  // f16 MFMA 16x16x32: C[channel 16 mt + row][head] = sum_k R[16 mt + row][k] q[head][k],
+  // with R carried at scale 2^10 as hi = fp16(2^10 R) and lo = fp16(2^10 R - hi)
+  // (about 2^-22 relative: an fp32 product), accumulated in fp32.  This wave's
+  // R rows are loaded ahead of the first two tiles by loads the compiler does
+  // not track, so that nothing waits for the tiles: the wait below for the
+  // query covers them, and the registers are read only after it.
+  constexpr int kMt = ROT ? (kD / 16 + kWaves - 1) / kWaves : 1;  // 16-channel blocks per wave
+  const int ar = lane & 15, kq = lane >> 4;  // q R^T: A row / B column (head), and k group
+  f32x4 rr[kMt][4][2];
+  if constexpr (ROT) {
+    if (rot && split > 0) {
+#pragma unroll
+      for (int i = 0; i < kMt; ++i) {
+        const int mt = wave + i * kWaves < kD / 16 ? wave + i * kWaves : kD / 16 - 1;
+        const float* rrow = p.rot + (16 * mt + ar) * kD + 8 * kq;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(rr[i][ks][0]) : "v"(rrow + 32 * ks) : "memory");
+          asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(rr[i][ks][1]) : "v"(rrow + 32 * ks + 4) : "memory");
+        }
+      }
+    }
+  }
   int64_t ta = t0 + wave, tb = t0 + kWaves + wave;  // tiles in stages 0 and 1
   if (ta < t1) issue(ta, st0, true, true);
   if (tb < t1) issue(tb, st1, true, true);
-  wait_vm(ops_t(ta) + ops_t(tb));  // the query (and K-scale) loads have landed
+  wait_vm(ops_t(ta) + ops_t(tb));  // the query (and K-scale, and R) loads have landed
   __builtin_amdgcn_wave_barrier();
+  if constexpr (ROT) {
+    if (rot && split > 0) {
+#pragma unroll
+      for (int i = 0; i < kMt; ++i)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) asm volatile("" : "+v"(rr[i][ks][0]), "+v"(rr[i][ks][1]));
+      __syncthreads();  // every wave's query row has landed
+#pragma unroll
+      for (int i = 0; i < kMt; ++i) {
+        const int mt = wave + i * kWaves;
+        if (mt < kD / 16) {
+          f32x4 c = {0, 0, 0, 0};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            f16x8 hi, lo;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const float v = rr[i][ks][j >> 2][j & 3] * 1024.0f;  // exact
+              hi[j] = static_cast<_Float16>(v);
+              lo[j] = static_cast<_Float16>(v - static_cast<float>(hi[j]));
+            }
+            const uint4 bq = ar < kHeads ? *reinterpret_cast<const uint4*>(
+                                               reinterpret_cast<const uint16_t*>(&qraw_s[ar][0]) + 32 * ks + 8 * kq)
+                                         : make_uint4(0u, 0u, 0u, 0u);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, __builtin_bit_cast(f16x8, bq), c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, __builtin_bit_cast(f16x8, bq), c, 0, 0, 0);
+          }
+          if (ar < kHeads) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qrot_s[ar][16 * mt + 4 * kq + j] = c[j] * (1.0f / 1024.0f);
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
 
   // ---- query digits: wave h < 4 handles head h (channels 2*lane, 2*lane+1) ----
   if (wave < kHeads) {
     const int h = wave;
     const uint32_t qq = qraw_s[h][lane];
     float qf0 = h2f(static_cast<uint16_t>(qq & 0xFFFFu)), qf1 = h2f(static_cast<uint16_t>(qq >> 16));
+    if constexpr (ROT) {
+      if (rot && split > 0) {  // the middle tiles are scored with q R^T
+        qf0 = qrot_s[h][2 * lane];
+        qf1 = qrot_s[h][2 * lane + 1];
+      }
+    }
     if constexpr (!ASYM) {
       const uint32_t ks = ksraw_s[h][lane];
       qf0 *= h2f(static_cast<uint16_t>(ks & 0xFFFFu));
@@ -1019,12 +1091,30 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     // a batch of 16 splits for all its items issue before any is used
     constexpr int kB = 16, kE = (kHeads * kD + kThreads - 1) / kThreads;
     const int64_t p0 = slot * n * 4;
-    float Mh[kE], o[kE], L[kE];
+    // rotated tier: thread (channel c, quarter dq) of 4 kD virtual threads needs
+    // R[32 dq .. 32 dq + 31][c]; loaded first, so that they fly with the partials
+    constexpr int kV = (4 * kD + kThreads - 1) / kThreads;
+    float rr[ROT ? kV : 1][ROT ? 32 : 1];
+    if constexpr (ROT) {
+      {
+#pragma unroll
+        for (int iv = 0; iv < kV; ++iv) {
+          const int vt = tid + iv * kThreads;
+          if (vt < 4 * kD) {
+#pragma unroll
+            for (int d = 0; d < 32; ++d) rr[iv][d] = p.rot[(32 * (vt >> 7) + d) * kD + (vt & (kD - 1))];
+          }
+        }
+      }
+    }
+    // rotated tier: of = split 0 (fp16 tiers, plain basis), o = the middle splits (rotated basis)
+    float Mh[kE], o[kE], L[kE], of[kE];
 #pragma unroll
     for (int e = 0; e < kE; ++e) {
       Mh[e] = kNegBig;
       o[e] = 0.0f;
       L[e] = 0.0f;
+      of[e] = 0.0f;
     }
     for (int s0 = 0; s0 < n; s0 += kB) {
       float mm[kE][kB], ll[kE][kB], aa[kE][kB];
@@ -1058,22 +1148,62 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         const float r = exp2f(Mh[e] - Mn);
         o[e] *= r;
         L[e] *= r;
+        of[e] *= r;
 #pragma unroll
         for (int j = 0; j < kB; ++j) {
           if (s0 + j < n) {
             const float w = exp2f(mm[e][j] - Mn);
             L[e] += ll[e][j] * w;
-            o[e] += aa[e][j] * w;
+            if (rot && s0 + j == 0) of[e] += aa[e][j] * w;
+            else o[e] += aa[e][j] * w;
           }
         }
         Mh[e] = Mn;
       }
     }
+    if (rot) {
+      // out = (of + o R) / L: o [head][d] to LDS, then 512 virtual threads
+      // (channel c, quarter dq) sum d over [32 dq, 32 dq + 32) for every head
+      float* ro = reinterpret_cast<float*>(&ring0[0][0]);  // [4][kD] o, then [4 dq][4][kD] partial products
+      float* pp = ro + kHeads * kD;
 #pragma unroll
-    for (int e = 0; e < kE; ++e) {
-      const int idx = tid + e * kThreads;
-      if (idx < G * kD)
-        p.out[b * p.o_sb + (kvh * p.G + h0 + (idx >> 7)) * p.o_sh + (idx & (kD - 1))] = f2h(o[e] / L[e]);
+      for (int e = 0; e < kE; ++e) {
+        const int idx = tid + e * kThreads;
+        if (idx < kHeads * kD) ro[idx] = idx < G * kD ? o[e] : 0.0f;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int iv = 0; iv < kV; ++iv) {
+        const int vt = tid + iv * kThreads;
+        if (vt < 4 * kD) {
+          const int c = vt & (kD - 1), dq = vt >> 7;
+          float sh[kHeads] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int d = 0; d < 32; ++d)
+#pragma unroll
+            for (int h = 0; h < kHeads; ++h) sh[h] = fmaf(ro[h * kD + 32 * dq + d], rr[iv][d], sh[h]);
+#pragma unroll
+          for (int h = 0; h < kHeads; ++h) pp[(dq * kHeads + h) * kD + c] = sh[h];
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int e = 0; e < kE; ++e) {
+        const int idx = tid + e * kThreads;
+        if (idx < G * kD) {
+          const int h = idx >> 7, c = idx & (kD - 1);
+          const float v = of[e] + ((pp[h * kD + c] + pp[(kHeads + h) * kD + c]) +
+                                   (pp[(2 * kHeads + h) * kD + c] + pp[(3 * kHeads + h) * kD + c]));
+          p.out[b * p.o_sb + (kvh * p.G + h0 + h) * p.o_sh + c] = f2h(v / L[e]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kE; ++e) {
+        const int idx = tid + e * kThreads;
+        if (idx < G * kD)
+          p.out[b * p.o_sb + (kvh * p.G + h0 + (idx >> 7)) * p.o_sh + (idx & (kD - 1))] = f2h(o[e] / L[e]);
+      }
     }
   }
   if (tid == 0) __hip_atomic_store(&p.counters[slot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1141,15 +1271,19 @@ template <bool DET, bool TWO>
 Choice packed_kernel_t(const Params& p) {
   const int kb = p.mid.k_bits, vb = p.mid.v_bits;
   constexpr int v = (DET ? 2 : 0) + (TWO ? 1 : 0);
-  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6, DET, TWO>, 6, 4 * 6 + v};
+  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6, DET, TWO, false>, 6, 4 * 6 + v};
   if (p.mid.fmt == FADE_MID_SYM) {
-    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO>, 4, 4 * 0 + v};  // two workgroups per CU
-    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO>, 8, 4 * 1 + v};
+    if (p.rot != nullptr) {  // rotated backend: q R^T in the prologue, the middle part times R in the merge
+      if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO, true>, 4, 4 * 7 + v};
+      return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO, true>, 8, 4 * 8 + v};
+    }
+    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO, false>, 4, 4 * 0 + v};  // two workgroups per CU
+    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO, false>, 8, 4 * 1 + v};
   }
-  if (kb == 4 && vb == 4) return {decode_packed_kernel<4, 4, kFmtAsym, 6, DET, TWO>, 6, 4 * 2 + v};
-  if (kb == 4 && vb == 2) return {decode_packed_kernel<4, 2, kFmtAsym, 8, DET, TWO>, 8, 4 * 3 + v};
-  if (kb == 2 && vb == 2) return {decode_packed_kernel<2, 2, kFmtAsym, 8, DET, TWO>, 8, 4 * 4 + v};
-  return {decode_packed_kernel<2, 4, kFmtAsym, 6, DET, TWO>, 6, 4 * 5 + v};
+  if (kb == 4 && vb == 4) return {decode_packed_kernel<4, 4, kFmtAsym, 6, DET, TWO, false>, 6, 4 * 2 + v};
+  if (kb == 4 && vb == 2) return {decode_packed_kernel<4, 2, kFmtAsym, 8, DET, TWO, false>, 8, 4 * 3 + v};
+  if (kb == 2 && vb == 2) return {decode_packed_kernel<2, 2, kFmtAsym, 8, DET, TWO, false>, 8, 4 * 4 + v};
+  return {decode_packed_kernel<2, 4, kFmtAsym, 6, DET, TWO, false>, 6, 4 * 5 + v};
 }
 
 Choice packed_kernel(const Params& p) {
@@ -1160,7 +1294,7 @@ Choice packed_kernel(const Params& p) {
 }  // namespace
 
 int int4_resident_wgs(const Params& p) {
-  static int cached[7 * 4] = {};
+  static int cached[9 * 4] = {};
   const Choice c = packed_kernel(p);
   if (cached[c.index] > 0) return cached[c.index];
   int dev = 0, cus = 0, per_cu = 0;

@@ -192,7 +192,11 @@ class TieredDecodePlan:
     must then run on that stream.  With ``no_alloc`` the plan allocates no
     workspace: ``run()`` calls ``fade_tiered_decode_attn_noalloc``, whose
     kernels use the library's own per-GPU scratch (shared by every such call
-    on that GPU, so such calls must not overlap on one GPU).
+    on that GPU, so such calls must not overlap on one GPU).  ``rotation``
+    (fp32 [128, 128] on the device, the rotated backend's R) marks the middle
+    tier as codes of ``K R^T`` / ``V R^T`` while q, sink and recent stay in the
+    model's basis: the kernel scores middle tokens with ``q R^T`` and returns
+    the fp16 tiers' part plus the middle part times R (no torch op per call).
     """
 
     def __init__(
@@ -209,6 +213,7 @@ class TieredDecodePlan:
         stream: int | None = None,
         deterministic: bool | None = None,
         no_alloc: bool = False,
+        rotation: Tensor | None = None,
     ) -> None:
         if q.dim() != 4 or q.shape[2] != 1:
             raise ValueError(f"q must be [B, Hq, 1, D], got {tuple(q.shape)}")
@@ -224,9 +229,15 @@ class TieredDecodePlan:
         Hkv = int(ref.shape[1])
         if q.stride(-1) != 1:
             q = q.contiguous()
+        if rotation is not None:
+            if mid is None or mid.fmt not in ("int4", "sym"):
+                raise ValueError("a rotation applies to a symmetric ('sym') middle tier")
+            if tuple(rotation.shape) != (D, D) or rotation.dtype != torch.float32 or rotation.device != q.device:
+                raise ValueError(f"rotation must be float32 [{D}, {D}] on {q.device}")
+            rotation = rotation.contiguous()
         if out is None:
             out = torch.empty(B, Hq, 1, D, dtype=torch.float16, device=q.device)
-        self._keep = (q, sink, mid, recent, out, lens)
+        self._keep = (q, sink, mid, recent, out, lens, rotation)
         a = _lib.DecodeArgs()
         a.B, a.Hq, a.Hkv, a.D = B, Hq, Hkv, D
         a.q, a.q_sb, a.q_sh = q.data_ptr(), q.stride(0), q.stride(1)
@@ -238,6 +249,7 @@ class TieredDecodePlan:
         if deterministic is None:
             deterministic = torch.are_deterministic_algorithms_enabled()
         a.deterministic = int(bool(deterministic))
+        a.rotation = _lib.ptr(rotation)
         lib = _lib.load()
         if no_alloc:
             self.workspace = None
@@ -271,6 +283,7 @@ def tiered_decode_attention(
     kernel: int = 0,
     lens: Tensor | None = None,
     deterministic: bool | None = None,
+    rotation: Tensor | None = None,
 ) -> Tensor:
     """Decode attention of ``q`` [B,Hq,1,D] over the tiered cache; returns fp16 [B,Hq,1,D].
 
@@ -283,10 +296,13 @@ def tiered_decode_attention(
     makes repeated calls on the same inputs bitwise identical; otherwise the
     INT4 kernel's waves claim tiles as they finish, and results can differ in
     the last bits between calls.
+    ``rotation`` (fp32 [128, 128] R): the middle tier holds rotated codes
+    (fade/rotated_quant.py:134-187) while q, sink and recent are unrotated; the
+    kernel rotates q for the middle tokens and un-rotates their output part.
     """
     s = torch.cuda.current_stream(q.device).cuda_stream
     plan = TieredDecodePlan(q, sink, mid, recent, sm_scale, n_splits=n_splits, kernel=kernel, lens=lens, stream=s,
-                            deterministic=deterministic)
+                            deterministic=deterministic, rotation=rotation)
     return plan.run(s)
 
 

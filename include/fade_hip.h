@@ -277,6 +277,14 @@ typedef struct fade_decode_args {
                                   round-robin order instead of claiming them as they finish
                                   (the order of the fp32 sums then no longer depends on timing);
                                   the other kernels are deterministic either way. */
+  const float* rotation;       /* optional device fp32 [128][128] R, row-major, of the rotated
+                                  backend (fade/rotated_quant.py:41-45,134-187): the middle tier
+                                  (FADE_MID_SYM, 4- or 2-bit) holds codes of K R^T and V R^T,
+                                  while q, sink and recent are in the model's basis.  Middle
+                                  tokens are scored with q R^T (computed in the kernel) and their
+                                  values summed in the rotated basis; the result is the fp16
+                                  tiers' part + (middle part) R.  Needs the matrix-core INT4
+                                  kernel.  NULL: no rotation. */
 } fade_decode_args;
 
 /* Replaces dequantize + torch.cat (fade/cache.py:683-842) + SDPA and the

@@ -205,6 +205,65 @@ def test_tiered_decode_rotated(dev, bits):
 
 
 @pytest.mark.parametrize(
+    "B,Hq,Hkv,S,ns,nr,n_splits,bits,det",
+    [
+        (1, 32, 8, 1500, 4, 64, 0, 2, False),
+        (2, 8, 4, 777, 4, 64, 3, 2, False),  # G=2
+        (1, 4, 1, 300, 0, 37, 1, 2, False),  # one kv head, no sink; one split asked for: fp16 split + one middle split
+        (2, 12, 4, 2000, 4, 256, 0, 2, True),  # G=3, config-2 windows, deterministic order
+        (1, 28, 4, 1000, 4, 64, 0, 2, False),  # G=7: two head passes
+        (1, 32, 8, 600, 0, 0, 0, 2, False),  # no fp16 tokens: the fp16 split is empty
+        (2, 32, 8, 1300, 4, 64, 0, 4, False),  # rotated 4-bit
+        (1, 20, 4, 900, 4, 100, 5, 4, False),  # 4-bit, G=5
+    ],
+)
+def test_tiered_decode_rotation_in_kernel(dev, B, Hq, Hkv, S, ns, nr, n_splits, bits, det):
+    """Rotated middle tier with q, sink and recent in the model's basis (what the cache
+    holds): the kernel scores the middle with q R^T and un-rotates its output part.
+    Oracle: the reference's rotated dequant (codes -> x_rot_hat -> @ R, rounded to fp16,
+    fade/rotated_quant.py:134-187) concatenated with the fp16 tiers, then fp32 SDPA."""
+    print(f"case decode rotation in kernel B={B} Hq={Hq} Hkv={Hkv} S={S} ns={ns} nr={nr} splits={n_splits} "
+          f"bits={bits} det={det}", flush=True)
+    R = torch.from_numpy(np.load(__file__.rsplit("/", 1)[0] + "/golden/rotation_d128_seed42.npy")).to(dev)
+    q, k, v, ns, nr = _case(B, Hq, Hkv, S, ns, nr, seed=4100 + S + bits)
+    S = k.shape[2]
+    km = torch.from_numpy(np.ascontiguousarray(k[:, :, ns : S - nr])).to(dev)
+    vm = torch.from_numpy(np.ascontiguousarray(v[:, :, ns : S - nr])).to(dev)
+    kp, ks = frq.rotated_quant_k(km, R, bits)
+    vp, vs = frq.rotated_quant_v(vm, R, bits)
+    mid = MiddleTier("sym", kp, vp, ks.half(), vs.half(), k_bits=bits, v_bits=bits)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    sink = (t(k[:, :, :ns]), t(v[:, :, :ns])) if ns else None
+    rec = (t(k[:, :, S - nr :]), t(v[:, :, S - nr :])) if nr else None
+    out = tiered_decode_attention(t(q), sink, mid, rec, n_splits=n_splits, deterministic=det,
+                                  rotation=R).float().cpu().numpy()
+    omid = {"fmt": "rot", "kq": kp.cpu().numpy(), "ks": ks.half().cpu().numpy(), "vq": vp.cpu().numpy(),
+            "vs": vs.half().cpu().numpy(), "R": R.cpu().numpy(), "k_bits": bits, "v_bits": bits}
+    ref = oatt.tiered_decode(q, k[:, :, :ns], v[:, :, :ns], omid, k[:, :, S - nr :], v[:, :, S - nr :])
+    assert np.isfinite(out).all()
+    assert np.abs(out - ref).max() <= ATOL
+    if det:
+        again = tiered_decode_attention(t(q), sink, mid, rec, n_splits=n_splits, deterministic=True,
+                                        rotation=R).float().cpu().numpy()
+        assert np.array_equal(out, again)
+
+
+def test_tiered_decode_rotation_rejects(dev):
+    """A rotation needs the matrix-core INT4 kernel and a symmetric middle tier."""
+    R = torch.eye(128, dtype=torch.float32, device=dev)
+    q, k, v, ns, nr = _case(1, 8, 2, 300, 4, 16, seed=5)
+    km = torch.from_numpy(np.ascontiguousarray(k[:, :, 4:-16])).to(dev)
+    kp, ks = fq.quant_k_int4(km)
+    vp, vs = fq.quant_v_int4(torch.from_numpy(np.ascontiguousarray(v[:, :, 4:-16])).to(dev))
+    mid = MiddleTier("int4", kp, vp, ks, vs)
+    qt = torch.from_numpy(q).to(dev)
+    with pytest.raises(ValueError, match="rotated middle tier needs the matrix-core INT4 kernel"):
+        tiered_decode_attention(qt, None, mid, None, kernel=1, rotation=R)
+    with pytest.raises(ValueError, match="float32"):
+        tiered_decode_attention(qt, None, mid, None, rotation=R.half())
+
+
+@pytest.mark.parametrize(
     "B,Hq,Hkv,S,ns,nr,n_splits",
     [
         (1, 32, 8, 1500, 4, 64, 0),
