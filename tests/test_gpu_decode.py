@@ -270,6 +270,8 @@ def test_tiered_decode_rotation_rejects(dev):
         (2, 8, 4, 777, 4, 64, 3),  # G=2
         (1, 4, 1, 300, 0, 37, 1),  # one kv head, ragged recent window
         (2, 12, 4, 2000, 4, 256, 0),  # G=3, config-2 windows
+        (1, 16, 2, 900, 4, 64, 0),  # G=8: two head passes
+        (2, 24, 4, 700, 4, 64, 3),  # G=6
     ],
 )
 def test_tiered_decode_sym2_fast_path(dev, B, Hq, Hkv, S, ns, nr, n_splits):
