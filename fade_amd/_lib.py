@@ -144,6 +144,7 @@ class ReassignArgs(ctypes.Structure):
         ("out_rec_k", _p), ("out_rec_v", _p), ("out_rec_sb", _i64), ("out_rec_sh", _i64), ("out_rec_ss", _i64),
         ("cap_rec", _i64),
         ("out_mid_k", _p), ("out_mid_v", _p), ("cap_mid", _i64),
+        ("mid_colmax", _p), ("colmax_parts", _i64),
     ]
 
 
@@ -155,6 +156,7 @@ _SIGNATURES: dict[str, list] = {
     "fade_unpack_codes": [_p, _i64, _i64, _i32, _p, _p],
     "fade_quant_k_int4_workspace_bytes": [_i64, _i64, _i64, _i64, _pi64],
     "fade_quant_k_int4": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p],
+    "fade_quant_k_int4_from_colmax": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
     "fade_quant_v_int4": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p],
     "fade_dequant_sym": [_p, _p, _i32, _i32, _i64, _i64, _i64, _i64, _p, _p],
     "fade_quant_int2_grouped": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p],

@@ -33,6 +33,7 @@ from .quant import (
     dequant_int4,
     quant_int2_padded,
     quant_k_int4,
+    quant_k_int4_from_colmax,
     quant_v_int4,
 )
 from .pages import PAGE_TOKENS
@@ -44,6 +45,8 @@ DEFAULT_INT4_BUDGET: int | None = None
 DEFAULT_INT2_BUDGET: int = 0
 DEFAULT_ROPE_THETA: float = 10000.0
 DEFAULT_FP16_PREALLOC: int = 128
+# partial column maxima the device reassignment's gather leaves for the K quantizer
+_COLMAX_PARTS: int = 16
 DEFAULT_MAX_DEQUANT_AGE: int | None = None
 
 TIER_FP16: int = 0
@@ -880,8 +883,12 @@ class TieredKVCache(DynamicCache):
             a.out_rec_k, a.out_rec_v = buf[0].data_ptr(), buf[1].data_ptr()
             a.out_rec_sb, a.out_rec_sh, a.out_rec_ss = buf[0].stride()[:3]
             a.cap_rec = n_rec_new
+        colmax = None
         if mid is not None:
             a.out_mid_k, a.out_mid_v, a.cap_mid = mid[0].data_ptr(), mid[1].data_ptr(), n_int4
+            # the gather also leaves the middle K's column absmax: one quantizer pass instead of two
+            colmax = torch.zeros(B * H, _COLMAX_PARTS, D, dtype=torch.float32, device=dev)
+            a.mid_colmax, a.colmax_parts = colmax.data_ptr(), _COLMAX_PARTS
         _lib.check(_lib.load().fade_reassign_gather(ctypes.byref(a), stream), "fade_reassign_gather")
 
         # new state (the same fields as the host path)
@@ -900,7 +907,7 @@ class TieredKVCache(DynamicCache):
             st._fp16_buf_k = st._fp16_buf_v = st._fp16_buf_pos = None
             st._fp16_len = 0
         if mid is not None:
-            st.int4_kq, st.int4_ks = quant_k_int4(mid[0])
+            st.int4_kq, st.int4_ks = quant_k_int4_from_colmax(mid[0], colmax)
             if self.incremental_quant and old_v[0] is not None and tiers.device.type == "cpu":
                 st.int4_vq, st.int4_vs = self._incremental_v(tiers, ns_old, nm_old, old_v, mid[1])
             else:
@@ -1150,8 +1157,11 @@ class TieredKVCache(DynamicCache):
         a.out_rec_k, a.out_rec_v = buf[0].data_ptr(), buf[1].data_ptr()
         a.out_rec_sb, a.out_rec_sh, a.out_rec_ss = buf[0].stride()[:3]
         a.cap_rec = cap
+        colmax = None
         if mid is not None:
             a.out_mid_k, a.out_mid_v, a.cap_mid = mid[0].data_ptr(), mid[1].data_ptr(), cm
+            colmax = torch.zeros(B * H, _COLMAX_PARTS, D, dtype=torch.float32, device=dev)
+            a.mid_colmax, a.colmax_parts = colmax.data_ptr(), _COLMAX_PARTS
         _lib.check(_lib.load().fade_reassign_gather(ctypes.byref(a), stream), "fade_reassign_gather")
 
         st.sink_k, st.sink_v = (out_sink[0], out_sink[1]) if out_sink is not None else (None, None)
@@ -1159,7 +1169,7 @@ class TieredKVCache(DynamicCache):
         st._fp16_len = cr
         st.fp16_k, st.fp16_v = buf[0][:, :, :cr], buf[1][:, :, :cr]
         if mid is not None:
-            st.int4_kq, st.int4_ks = quant_k_int4(mid[0])
+            st.int4_kq, st.int4_ks = quant_k_int4_from_colmax(mid[0], colmax)
             st.int4_vq, st.int4_vs = quant_v_int4(mid[1])
         else:
             st.int4_kq = st.int4_vq = st.int4_ks = st.int4_vs = None

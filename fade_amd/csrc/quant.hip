@@ -202,21 +202,22 @@ __global__ __launch_bounds__(kBlock) void colmax_kernel(const InT* __restrict__ 
   }
 }
 
-// Pass 2: finish the column absmax, emit the scale, quantize this S-block.
+// Pass 2: finish the column absmax from nparts partial maxima per (b, h)
+// (partial[bh][k][d]; pass 1's S-blocks, or partials another kernel
+// gathered), emit the scale, quantize this S-block.
 template <typename InT, int MODE, int BITS, int LPR>
 __global__ __launch_bounds__(kBlock) void quant_channel_kernel(
     const InT* __restrict__ x, int64_t H, int64_t S, int64_t sb, int64_t sh, int64_t ss,
-    int64_t rows_per_block, const float* __restrict__ partial, uint8_t* __restrict__ packed,
+    int64_t rows_per_block, const float* __restrict__ partial, int nparts, uint8_t* __restrict__ packed,
     uint16_t* __restrict__ scale) {
   constexpr int RP = kBlock / LPR;
   constexpr int D = LPR * 8;
   constexpr int ROW_BYTES = LPR * lane_bytes<BITS>();
   const int64_t bh = blockIdx.y;
-  const int nsb = gridDim.x;
   __shared__ float inv_s[D];
   for (int d = threadIdx.x; d < D; d += kBlock) {
     float a = 0.0f;
-    for (int k = 0; k < nsb; ++k) a = fmaxf(a, partial[(bh * nsb + k) * D + d]);
+    for (int k = 0; k < nparts; ++k) a = fmaxf(a, partial[(bh * nparts + k) * D + d]);
     float inv;
     uint16_t sc;
     sym_params<MODE, QRange<BITS>::hi>(a, inv, sc);
@@ -510,7 +511,28 @@ int launch_channel(const char* fn, const InT* x, int64_t B, int64_t H, int64_t S
     hipLaunchKernelGGL((colmax_kernel<InT, LPR>), grid, dim3(kBlock), 0, st, x, H, S, sb, sh, ss,
                        rpb, static_cast<float*>(ws));
     hipLaunchKernelGGL((quant_channel_kernel<InT, MODE, BITS, LPR>), grid, dim3(kBlock), 0, st, x,
-                       H, S, sb, sh, ss, rpb, static_cast<const float*>(ws),
+                       H, S, sb, sh, ss, rpb, static_cast<const float*>(ws), static_cast<int>(nsb),
+                       static_cast<uint8_t*>(packed), static_cast<uint16_t*>(scale));
+  });
+  return check_launch(fn);
+}
+
+// Pass 2 alone, on column maxima another kernel produced: partial [B*H][nparts][D].
+template <typename InT, int MODE, int BITS>
+int launch_channel_given(const char* fn, const InT* x, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                         int64_t sh, int64_t ss, const float* partial, int64_t nparts, void* packed, void* scale,
+                         hipStream_t st) {
+  const int64_t BH = B * H;
+  if (BH == 0) return FADE_OK;
+  if (S == 0) return einval("%s: S must be > 0 for a per-channel scale", fn);
+  if (partial == nullptr || nparts < 1 || nparts > 65535) return einval("%s: need 1..65535 column-max partials", fn);
+  if (BH > 65535) return einval("%s: B*H=%lld exceeds 65535", fn, (long long)BH);
+  int64_t nsb, rpb;
+  channel_blocking(BH, S, &nsb, &rpb);
+  dim3 grid(static_cast<unsigned>(nsb), static_cast<unsigned>(BH));
+  FADE_DISPATCH_LPR(D, {
+    hipLaunchKernelGGL((quant_channel_kernel<InT, MODE, BITS, LPR>), grid, dim3(kBlock), 0, st, x,
+                       H, S, sb, sh, ss, rpb, partial, static_cast<int>(nparts),
                        static_cast<uint8_t*>(packed), static_cast<uint16_t*>(scale));
   });
   return check_launch(fn);
@@ -575,6 +597,18 @@ FADE_API int fade_quant_k_int4_workspace_bytes(int64_t B, int64_t H, int64_t S, 
   channel_blocking(B * H, S, &nsb, &rpb);
   *bytes = B * H * nsb * D * static_cast<int64_t>(sizeof(float));
   return FADE_OK;
+}
+
+FADE_API int fade_quant_k_int4_from_colmax(const void* k_f16, int64_t B, int64_t H, int64_t S, int64_t D,
+                                           int64_t sb, int64_t sh, int64_t ss, const float* colmax,
+                                           int64_t parts, void* packed_u8, void* scale_f16, void* stream) {
+  int rc = check_dims("fade_quant_k_int4_from_colmax", B, H, S, D);
+  if (rc) return rc;
+  if (!aligned(k_f16, 16) || (sb | sh | ss) % 8 != 0)
+    return einval("fade_quant_k_int4_from_colmax: input must be 16-byte aligned with strides a multiple of 8");
+  return launch_channel_given<uint16_t, MODE_F16, 4>("fade_quant_k_int4_from_colmax",
+                                                     static_cast<const uint16_t*>(k_f16), B, H, S, D, sb, sh, ss,
+                                                     colmax, parts, packed_u8, scale_f16, as_stream(stream));
 }
 
 FADE_API int fade_quant_k_int4(const void* k_f16, int64_t B, int64_t H, int64_t S, int64_t D,

@@ -145,6 +145,10 @@ __device__ __forceinline__ float nib(uint32_t byte, bool high) {
 
 // One thread per (kept token, channel pair i, i + D/2) of one (b, h); the
 // grid covers `rows` kept ranks (the host's count, or S when it has none).
+// With mid_colmax, the workgroup's middle rows also leave their per-channel
+// max |K| (after the RoPE rewrite, as fp16 values), reduced in LDS and
+// folded into part blockIdx.x % colmax_parts by an atomic max on the float's
+// bits (order-preserving for values >= 0).
 __global__ __launch_bounds__(256) void gather_kernel(FadeReassignArgs a) {
   const int D = static_cast<int>(a.D), half = D / 2;
   const int rows_per_block = blockDim.x / half;
@@ -158,95 +162,117 @@ __global__ __launch_bounds__(256) void gather_kernel(FadeReassignArgs a) {
   int32_t* status = a.counts + 4 * pr + 3;
   const int32_t* dst = a.dst + pr * a.S;
   const int32_t* newpos = a.newpos + pr * a.S;
-  if (rank >= counts[2] || rank >= a.S) return;
-  const int64_t j = a.src_of[pr * a.S + rank];
-  if (j < 0 || j >= a.S) return;
-  const int32_t d = dst[j];
-  if (d < 0) return;
-  const int cls = d >> kClsShift;
-  const int64_t slot = d & kSlotMask;
-  // this row's partition of the position order into sink | middle | recent,
-  // and its token count (tokens were evicted from it iff it keeps fewer)
-  int64_t nso = a.n_sink_old, nmo = a.n_mid_old, Sb = a.S;
-  if (a.src_lens != nullptr) {
-    nso = a.src_lens[3 * b];
-    nmo = a.src_lens[3 * b + 1];
-    const int64_t nro = a.src_lens[3 * b + 2];
-    Sb = nso + nmo + nro;
-    if (nso < 0 || nso > a.n_sink_old || nmo < 0 || nmo > a.n_mid_old || nro < 0 || nro > a.n_rec_cap || j >= Sb) {
-      atomicOr(status, 16);  // a kept token the row does not have
-      return;
+  float cm0 = 0.0f, cm1 = 0.0f;  // |K| of channels i and i + half if this thread wrote a middle row
+  do {  // `break` = this thread writes nothing (every thread still reaches the column-max reduction)
+    if (rank >= counts[2] || rank >= a.S) break;
+    const int64_t j = a.src_of[pr * a.S + rank];
+    if (j < 0 || j >= a.S) break;
+    const int32_t d = dst[j];
+    if (d < 0) break;
+    const int cls = d >> kClsShift;
+    const int64_t slot = d & kSlotMask;
+    // this row's partition of the position order into sink | middle | recent,
+    // and its token count (tokens were evicted from it iff it keeps fewer)
+    int64_t nso = a.n_sink_old, nmo = a.n_mid_old, Sb = a.S;
+    if (a.src_lens != nullptr) {
+      nso = a.src_lens[3 * b];
+      nmo = a.src_lens[3 * b + 1];
+      const int64_t nro = a.src_lens[3 * b + 2];
+      Sb = nso + nmo + nro;
+      if (nso < 0 || nso > a.n_sink_old || nmo < 0 || nmo > a.n_mid_old || nro < 0 || nro > a.n_rec_cap || j >= Sb) {
+        atomicOr(status, 16);  // a kept token the row does not have
+        break;
+      }
     }
-  }
-  // source pair
-  float k0, k1;
-  uint16_t v0, v1;
-  if (j < nso || j >= nso + nmo) {
-    const bool sink = j < nso;
-    const int64_t r = sink ? j : j - nso - nmo;
-    const uint16_t* kb = static_cast<const uint16_t*>(sink ? a.sink_k : a.rec_k);
-    const uint16_t* vb = static_cast<const uint16_t*>(sink ? a.sink_v : a.rec_v);
-    const int64_t off = sink ? b * a.sink_sb + h * a.sink_sh + r * a.sink_ss : b * a.rec_sb + h * a.rec_sh + r * a.rec_ss;
-    k0 = h2f(kb[off + i]);
-    k1 = h2f(kb[off + i + half]);
-    v0 = vb[off + i];
-    v1 = vb[off + i + half];
-  } else {
-    // reference INT4: K per-channel scale [B,H,1,D], V per-token scale [B,H,mid,1]
-    const int64_t r = j - nso;
-    const uint8_t* kq = static_cast<const uint8_t*>(a.mid_kq) + (bh * a.n_mid_old + r) * half;
-    const uint8_t* vq = static_cast<const uint8_t*>(a.mid_vq) + (bh * a.n_mid_old + r) * half;
-    const uint16_t* ks = static_cast<const uint16_t*>(a.mid_ks) + bh * D;
-    const float vs = h2f(static_cast<const uint16_t*>(a.mid_vs)[bh * a.n_mid_old + r]);
-    const bool hi0 = (i & 1) == 0, hi1 = ((i + half) & 1) == 0;  // even channel: high nibble
-    k0 = round_f16(nib(kq[i >> 1], hi0) * h2f(ks[i]));
-    k1 = round_f16(nib(kq[(i + half) >> 1], hi1) * h2f(ks[i + half]));
-    v0 = f2h(nib(vq[i >> 1], hi0) * vs);
-    v1 = f2h(nib(vq[(i + half) >> 1], hi1) * vs);
-  }
-  uint16_t ko0, ko1;
-  if (counts[2] < Sb) {
-    // un-RoPE at the old position (k*cos - rotate_half(k)*sin), fp16, then
-    // RoPE at the new one (k*cos + rotate_half(k)*sin), fp16
-    const int64_t po = a.pos_old[a.pos_old_rs * b + j], pn = newpos[j];
-    if (po < 0 || po >= a.table_rows || pn < 0 || pn >= a.table_rows) {
-      atomicOr(status, 4);
-      return;
+    // source pair
+    float k0, k1;
+    uint16_t v0, v1;
+    if (j < nso || j >= nso + nmo) {
+      const bool sink = j < nso;
+      const int64_t r = sink ? j : j - nso - nmo;
+      const uint16_t* kb = static_cast<const uint16_t*>(sink ? a.sink_k : a.rec_k);
+      const uint16_t* vb = static_cast<const uint16_t*>(sink ? a.sink_v : a.rec_v);
+      const int64_t off = sink ? b * a.sink_sb + h * a.sink_sh + r * a.sink_ss : b * a.rec_sb + h * a.rec_sh + r * a.rec_ss;
+      k0 = h2f(kb[off + i]);
+      k1 = h2f(kb[off + i + half]);
+      v0 = vb[off + i];
+      v1 = vb[off + i + half];
+    } else {
+      // reference INT4: K per-channel scale [B,H,1,D], V per-token scale [B,H,mid,1]
+      const int64_t r = j - nso;
+      const uint8_t* kq = static_cast<const uint8_t*>(a.mid_kq) + (bh * a.n_mid_old + r) * half;
+      const uint8_t* vq = static_cast<const uint8_t*>(a.mid_vq) + (bh * a.n_mid_old + r) * half;
+      const uint16_t* ks = static_cast<const uint16_t*>(a.mid_ks) + bh * D;
+      const float vs = h2f(static_cast<const uint16_t*>(a.mid_vs)[bh * a.n_mid_old + r]);
+      const bool hi0 = (i & 1) == 0, hi1 = ((i + half) & 1) == 0;  // even channel: high nibble
+      k0 = round_f16(nib(kq[i >> 1], hi0) * h2f(ks[i]));
+      k1 = round_f16(nib(kq[(i + half) >> 1], hi1) * h2f(ks[i + half]));
+      v0 = f2h(nib(vq[i >> 1], hi0) * vs);
+      v1 = f2h(nib(vq[(i + half) >> 1], hi1) * vs);
     }
-    const float* co = a.cos_tab + po * D;
-    const float* so = a.sin_tab + po * D;
-    const float u0 = round_f16(k0 * co[i] - (-k1) * so[i]);
-    const float u1 = round_f16(k1 * co[i + half] - k0 * so[i + half]);
-    const float* cn = a.cos_tab + pn * D;
-    const float* sn = a.sin_tab + pn * D;
-    ko0 = f2h(u0 * cn[i] + (-u1) * sn[i]);
-    ko1 = f2h(u1 * cn[i + half] + u0 * sn[i + half]);
-  } else {
-    ko0 = f2h(k0);
-    ko1 = f2h(k1);
+    uint16_t ko0, ko1;
+    if (counts[2] < Sb) {
+      // un-RoPE at the old position (k*cos - rotate_half(k)*sin), fp16, then
+      // RoPE at the new one (k*cos + rotate_half(k)*sin), fp16
+      const int64_t po = a.pos_old[a.pos_old_rs * b + j], pn = newpos[j];
+      if (po < 0 || po >= a.table_rows || pn < 0 || pn >= a.table_rows) {
+        atomicOr(status, 4);
+        break;
+      }
+      const float* co = a.cos_tab + po * D;
+      const float* so = a.sin_tab + po * D;
+      const float u0 = round_f16(k0 * co[i] - (-k1) * so[i]);
+      const float u1 = round_f16(k1 * co[i + half] - k0 * so[i + half]);
+      const float* cn = a.cos_tab + pn * D;
+      const float* sn = a.sin_tab + pn * D;
+      ko0 = f2h(u0 * cn[i] + (-u1) * sn[i]);
+      ko1 = f2h(u1 * cn[i + half] + u0 * sn[i + half]);
+    } else {
+      ko0 = f2h(k0);
+      ko1 = f2h(k1);
+    }
+    uint16_t *kd, *vd;
+    int64_t off;
+    if (cls == 0) {
+      if (slot >= a.cap_sink) { atomicOr(status, 8); break; }
+      kd = static_cast<uint16_t*>(a.out_sink_k);
+      vd = static_cast<uint16_t*>(a.out_sink_v);
+      off = (bh * a.cap_sink + slot) * D;
+    } else if (cls == 1) {
+      if (slot >= a.cap_rec) { atomicOr(status, 8); break; }
+      kd = static_cast<uint16_t*>(a.out_rec_k);
+      vd = static_cast<uint16_t*>(a.out_rec_v);
+      off = b * a.out_rec_sb + h * a.out_rec_sh + slot * a.out_rec_ss;
+    } else {
+      if (slot >= a.cap_mid) { atomicOr(status, 8); break; }
+      kd = static_cast<uint16_t*>(a.out_mid_k);
+      vd = static_cast<uint16_t*>(a.out_mid_v);
+      off = (bh * a.cap_mid + slot) * D;
+    }
+    kd[off + i] = ko0;
+    kd[off + i + half] = ko1;
+    vd[off + i] = v0;
+    vd[off + i + half] = v1;
+    if (cls == 2) {
+      cm0 = fabsf(h2f(ko0));
+      cm1 = fabsf(h2f(ko1));
+    }
+  } while (false);
+  if (a.mid_colmax == nullptr) return;
+  __shared__ float red[2][256];
+  red[0][threadIdx.x] = cm0;
+  red[1][threadIdx.x] = cm1;
+  __syncthreads();
+  if (static_cast<int>(threadIdx.x) < half) {
+    float m0 = 0.0f, m1 = 0.0f;
+    for (int t = i; t < static_cast<int>(blockDim.x); t += half) {
+      m0 = fmaxf(m0, red[0][t]);
+      m1 = fmaxf(m1, red[1][t]);
+    }
+    unsigned int* cp = reinterpret_cast<unsigned int*>(a.mid_colmax + (bh * a.colmax_parts + blockIdx.x % a.colmax_parts) * D);
+    if (m0 > 0.0f || m0 != m0) atomicMax(cp + i, __float_as_uint(m0));
+    if (m1 > 0.0f || m1 != m1) atomicMax(cp + i + half, __float_as_uint(m1));
   }
-  uint16_t *kd, *vd;
-  int64_t off;
-  if (cls == 0) {
-    if (slot >= a.cap_sink) { atomicOr(status, 8); return; }
-    kd = static_cast<uint16_t*>(a.out_sink_k);
-    vd = static_cast<uint16_t*>(a.out_sink_v);
-    off = (bh * a.cap_sink + slot) * D;
-  } else if (cls == 1) {
-    if (slot >= a.cap_rec) { atomicOr(status, 8); return; }
-    kd = static_cast<uint16_t*>(a.out_rec_k);
-    vd = static_cast<uint16_t*>(a.out_rec_v);
-    off = b * a.out_rec_sb + h * a.out_rec_sh + slot * a.out_rec_ss;
-  } else {
-    if (slot >= a.cap_mid) { atomicOr(status, 8); return; }
-    kd = static_cast<uint16_t*>(a.out_mid_k);
-    vd = static_cast<uint16_t*>(a.out_mid_v);
-    off = (bh * a.cap_mid + slot) * D;
-  }
-  kd[off + i] = ko0;
-  kd[off + i + half] = ko1;
-  vd[off + i] = v0;
-  vd[off + i + half] = v1;
 }
 
 }  // namespace
@@ -294,6 +320,8 @@ FADE_API int fade_reassign_gather(const FadeReassignArgs* args, void* stream) {
       (a.cap_mid > 0 && (a.out_mid_k == nullptr || a.out_mid_v == nullptr)))
     return einval("%s: null output", fn);
   if (a.table_rows > 0 && (a.cos_tab == nullptr || a.sin_tab == nullptr)) return einval("%s: null RoPE table", fn);
+  if (a.mid_colmax != nullptr && (a.colmax_parts < 1 || a.colmax_parts > 65535))
+    return einval("%s: colmax_parts must be 1..65535 with mid_colmax", fn);
   const int64_t BH = a.B * a.H;
   if (BH == 0 || a.S == 0) return FADE_OK;
   if (BH > 65535) return einval("%s: B*H=%lld exceeds 65535", fn, (long long)BH);

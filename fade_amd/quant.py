@@ -110,6 +110,32 @@ def quant_k_int4(k: Tensor) -> tuple[Tensor, Tensor]:
     return packed, scale
 
 
+def quant_k_int4_from_colmax(k: Tensor, colmax: Tensor) -> tuple[Tensor, Tensor]:
+    """``quant_k_int4`` for K whose per-channel absmax is already gathered
+    (fade/quant.py:61-75, second pass only).
+
+    ``colmax``: fp32 [B*H, parts, D] partial maxima of |K| (e.g. from
+    ``fade_reassign_gather``); channel d's absmax is their max over the parts.
+    Codes and scales equal ``quant_k_int4(k)``'s when the parts cover every row.
+    """
+    k = _prep_f16(k, "quant_k_int4_from_colmax")
+    B, H, S, D = k.shape
+    if colmax.dtype != torch.float32 or colmax.dim() != 3 or colmax.shape[0] != B * H or colmax.shape[2] != D:
+        raise ValueError(f"colmax must be float32 [B*H={B * H}, parts, D={D}], got {tuple(colmax.shape)}")
+    _lib.require_gpu(k, colmax, op="quant_k_int4_from_colmax")
+    colmax = colmax.contiguous()
+    packed = torch.empty(B, H, S, D // 2, dtype=torch.uint8, device=k.device)
+    scale = torch.empty(B, H, 1, D, dtype=torch.float16, device=k.device)
+    if k.numel() == 0:
+        return packed, scale
+    sb, sh, ss = _strides_bhs(k)
+    _lib.call(
+        "fade_quant_k_int4_from_colmax", k.data_ptr(), B, H, S, D, sb, sh, ss, colmax.data_ptr(),
+        int(colmax.shape[1]), packed.data_ptr(), scale.data_ptr(), _lib.stream_of(k),
+    )
+    return packed, scale
+
+
 def quant_v_int4(v: Tensor) -> tuple[Tensor, Tensor]:
     """Per-token symmetric INT4 for V, bit-packed (fade/quant.py:78-92).
 
@@ -308,6 +334,7 @@ __all__ = [
     "quant_asym",
     "quant_k_int2",
     "quant_k_int4",
+    "quant_k_int4_from_colmax",
     "quant_v_int2",
     "quant_v_int4",
 ]

@@ -69,6 +69,14 @@ int fade_quant_k_int4_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D
 int fade_quant_k_int4(const void* k_f16, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
                       int64_t sh, int64_t ss, void* packed_u8, void* scale_f16, void* workspace,
                       int64_t workspace_bytes, void* stream);
+/* fade_quant_k_int4's second pass alone (fade/quant.py:61-75), for K whose
+ * column absmax another kernel already gathered (fade_reassign_gather's
+ * mid_colmax): colmax fp32 [B*H][parts][D], each part a max of |K| over some
+ * of the rows; the absmax of channel d is the max over the parts.  Codes and
+ * scales equal fade_quant_k_int4's when the parts cover every row. */
+int fade_quant_k_int4_from_colmax(const void* k_f16, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                                  int64_t sh, int64_t ss, const float* colmax, int64_t parts, void* packed_u8,
+                                  void* scale_f16, void* stream);
 /* V [B,H,S,D] fp16 -> packed [B,H,S,D/2] u8 and scale [B,H,S,1] fp16. */
 int fade_quant_v_int4(const void* v_f16, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
                       int64_t sh, int64_t ss, void* packed_u8, void* scale_f16, void* stream);
@@ -202,6 +210,11 @@ typedef struct FadeReassignArgs {
   void* out_mid_k;
   void* out_mid_v;
   int64_t cap_mid;
+  float* mid_colmax;     /* optional device fp32 [B*H][colmax_parts][D], zero-filled by the
+                            caller: per-channel max of |K| over the middle rows written (as
+                            their fp16 values), spread over the parts; with it
+                            fade_quant_k_int4_from_colmax quantizes the middle in one pass */
+  int64_t colmax_parts;  /* parts of mid_colmax (>= 1 when it is given) */
 } FadeReassignArgs;
 int fade_reassign_gather(const FadeReassignArgs* args, void* stream);
 

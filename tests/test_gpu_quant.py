@@ -41,6 +41,26 @@ def test_quant_k_int4_bit_exact(dev, shape):
 
 
 @pytest.mark.parametrize("shape", [(1, 8, 1980, 128), (2, 3, 67, 128), (1, 2, 5, 64), (1, 1, 300, 256)])
+@pytest.mark.parametrize("parts", [1, 16])
+def test_quant_k_int4_from_colmax_bit_exact(dev, shape, parts):
+    """The second pass alone, on column maxima spread over `parts` partials (rows
+    dealt round-robin, as the gather's workgroups fold into them): equal to the
+    oracle's quant_k_int4, bit for bit."""
+    print(f"case quant_k_int4_from_colmax {shape} parts={parts}", flush=True)
+    x = _edge_tensor(shape, 2)
+    B, H, S, D = shape
+    a = np.abs(x.astype(np.float32)).reshape(B * H, S, D)
+    colmax = np.zeros((B * H, parts, D), dtype=np.float32)
+    for p in range(parts):
+        if p < S:
+            colmax[:, p] = a[:, p::parts].max(axis=1)
+    packed, scale = fq.quant_k_int4_from_colmax(torch.from_numpy(x).to(dev), torch.from_numpy(colmax).to(dev))
+    op, osc = oq.quant_k_int4(x)
+    assert np.array_equal(packed.cpu().numpy(), op)
+    assert np.array_equal(_u16(scale.cpu().numpy()), _u16(osc))
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 1980, 128), (2, 3, 67, 128), (1, 2, 5, 64), (1, 1, 300, 256)])
 def test_quant_v_int4_bit_exact(dev, shape):
     print(f"case quant_v_int4 {shape}", flush=True)
     x = _edge_tensor(shape, 1)
