@@ -234,6 +234,16 @@ def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def current_stream_handle(device: torch.device) -> int:
+    """The current stream of ``device`` as a raw handle (the fast accessor when torch has it)."""
+    if _RAW_STREAM is not None:
+        return int(_RAW_STREAM(device.index if device.index is not None else torch.cuda.current_device()))
+    return torch.cuda.current_stream(device).cuda_stream
+
+
 def require_gpu(*tensors: torch.Tensor | None, op: str = "fade_amd") -> None:
     """Reject CPU tensors: the hot path has no CPU implementation."""
     dev = None

@@ -116,6 +116,7 @@ class LayerState:
     # kernel does not read in place; each with the tensors it was built from
     _front_cache: tuple | None = None
     _mid_f16_cache: tuple | None = None
+    _decode_plan: tuple | None = None  # (key, TieredDecodePlan) reused while the tiers are the same objects
 
     def total_seq_length(self) -> int:
         if self.lens_host is not None:
@@ -1463,7 +1464,7 @@ class TieredKVCache(DynamicCache):
         asymmetric middle tier.  An INT2 tier (``int2_budget > 0``) is read as
         its fp16 dequantization joined to the sink, kept between calls.
         """
-        from .kernels.tiered_attn import MiddleTier, tiered_decode_attention
+        from .kernels.tiered_attn import MiddleTier, TieredDecodePlan, tiered_decode_attention
 
         st = self._layers[layer_idx]
         if st.lens is not None:
@@ -1481,6 +1482,13 @@ class TieredKVCache(DynamicCache):
             sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
             recent = None if st.fp16_k is None or st.fp16_k.shape[-2] == 0 else (st.fp16_k, st.fp16_v)
             return tiered_decode_attention(q, sink, mid, recent, sm_scale, n_splits=self.decode_splits, lens=st.lens)
+        # the recent tier's current length (the one field that moves from step to step)
+        n_rec = 0 if st.fp16_k is None else int(st.fp16_k.shape[-2]) - (0 if st.sink_k is not None else st.sink_count)
+        stream = _lib.current_stream_handle(q.device)
+        key = self._decode_key(st, q, sm_scale, n_rec > 0, stream)
+        cached = st._decode_plan
+        if cached is not None and _same_key(cached[0], key):
+            return cached[1].rerun(q, n_rec, stream)
         if st.sink_k is not None:
             sink = (st.sink_k, st.sink_v)
             recent = None if st.fp16_k is None else (st.fp16_k, st.fp16_v)
@@ -1520,8 +1528,36 @@ class TieredKVCache(DynamicCache):
                 )
             else:
                 raise RuntimeError(f"decode_attention: backend {be.name} is not read by the fused kernel")
-        return tiered_decode_attention(q, sink, mid, recent, sm_scale, n_splits=self.decode_splits,
-                                       rotation=rotation)
+        plan = TieredDecodePlan(q, sink, mid, recent if n_rec > 0 else None, sm_scale, n_splits=self.decode_splits,
+                                stream=stream, rotation=rotation)
+        st._decode_plan = (key, plan)
+        return plan.run(stream)
+
+    def _decode_key(self, st: LayerState, q: Tensor, sm_scale, has_recent: bool, stream: int) -> tuple:
+        """What a decode plan of this layer depends on: the tier tensors (as
+        objects: a reassignment or a grown fp16 buffer replaces them), the query's
+        layout and the call's settings; the recent tier's length is set per call."""
+        return (st.sink_k, st.sink_v, st._fp16_buf_k, st._fp16_buf_v,
+                st.fp16_k if st._fp16_buf_k is None else None, st.sink_count, has_recent,
+                st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs, st.backend_k, st.backend_v,
+                st.int2_kq, st.int2_vq, st.int2_ks, st.int2_vs,
+                tuple(q.shape), q.stride(), q.device, q.dtype, sm_scale, self.decode_splits, self.middle_v_bits,
+                self._quant_backend, torch.are_deterministic_algorithms_enabled(), stream)
+
+
+def _same_key(a: tuple, b: tuple) -> bool:
+    """Tensors, dicts and backends compare by identity; plain values by equality."""
+    if len(a) != len(b):
+        return False
+    for x, y in zip(a, b):
+        if x is y:
+            continue
+        if type(x) is not type(y) or type(x) not in _KEY_VALUE_TYPES or x != y:
+            return False
+    return True
+
+
+_KEY_VALUE_TYPES = (int, float, bool, str, tuple, torch.device, torch.dtype)
 
 
 __all__ = [

@@ -251,6 +251,7 @@ class TieredDecodePlan:
         a.deterministic = int(bool(deterministic))
         a.rotation = _lib.ptr(rotation)
         lib = _lib.load()
+        self._lib = lib
         if no_alloc:
             self.workspace = None
             a.workspace, a.workspace_bytes = None, 0
@@ -266,11 +267,36 @@ class TieredDecodePlan:
         self.args = a
         self.out = out
         self._argp = ctypes.byref(a)
+        self._ws_tiles = (int(a.sink.len) + int(a.recent.len) + 15) // 16
 
     def run(self, stream: int | None = None) -> Tensor:
         s = torch.cuda.current_stream(self.out.device).cuda_stream if stream is None else stream
         _lib.check(self._fn(self._argp, s), self._name)
         return self.out
+
+    def rerun(self, q: Tensor, recent_len: int, stream: int) -> Tensor:
+        """Launch again for a new query of the same shape and strides, into a new
+        output, with the recent tier (same tensors) now ``recent_len`` tokens long:
+        the decode loop's step, without re-validating the tiers.  The workspace
+        grows if the longer row needs more splits."""
+        a = self.args
+        if q.stride(-1) != 1:
+            q = q.contiguous()
+        a.q = q.data_ptr()
+        out = torch.empty_like(self.out)
+        a.out = out.data_ptr()
+        a.recent.len = int(recent_len)
+        tiles = (int(a.sink.len) + int(a.recent.len) + 15) // 16  # the split plan moves with the fp16 tile count
+        if self.workspace is not None and tiles != self._ws_tiles:
+            self._ws_tiles = tiles
+            nb = ctypes.c_int64(0)
+            _lib.check(self._lib.fade_tiered_decode_workspace_bytes(self._argp, nb), "fade_tiered_decode_workspace_bytes")
+            if nb.value > self.workspace.numel():
+                B, Hq, Hkv = int(a.B), int(a.Hq), int(a.Hkv)
+                self.workspace = _lib.stream_workspace(nb.value, out.device, stream, B * Hkv * -(-(Hq // Hkv) // 4))
+                a.workspace, a.workspace_bytes = self.workspace.data_ptr(), self.workspace.numel()
+        _lib.check(self._fn(self._argp, stream), self._name)
+        return out
 
 
 def tiered_decode_attention(

@@ -155,3 +155,52 @@ def test_create_tiered_cache_from_hf_config(dev):
     out = c.decode_attention(q.to(dev), 0)
     ref = F.scaled_dot_product_attention(q.float(), k.float().repeat_interleave(2, 1), v.float().repeat_interleave(2, 1))
     assert (out.float().cpu() - ref).abs().max() <= 2e-3
+
+
+@pytest.mark.parametrize("split_sink", [False, True])
+def test_decode_plan_reuse_matches_fresh_plans(dev, split_sink):
+    """decode_attention keeps one plan per layer and relaunches it while the tiers are
+    the same tensors (only q, the output and the recent tier's length change).  Across
+    appends, a grown fp16 buffer and a reassignment, every step equals a plan built
+    afresh for that step, bit for bit (deterministic mode), and the SDPA reference."""
+    print(f"case decode plan reuse split_sink={split_sink}", flush=True)
+    B, H, Hq, D = 2, 4, 16, 128
+    g = torch.Generator().manual_seed(7)
+    c = TieredKVCache(n_sink=4, recent_window=16, int4_budget=None, int2_budget=0, head_dim=D)
+    k = torch.randn(B, H, 300, D, generator=g).half().to(dev)
+    v = torch.randn(B, H, 300, D, generator=g).half().to(dev)
+    c.update(k, v, 0)
+    t = torch.full((300,), TIER_INT4, dtype=torch.long)
+    t[:4] = TIER_FP16
+    t[-16:] = TIER_FP16
+    c.apply_tier_assignment(0, t)
+    st = c._layers[0]
+    if not split_sink:  # the sink as the head of the fp16 tier
+        st.fp16_k = torch.cat([st.sink_k, st.fp16_k], dim=2)
+        st.fp16_v = torch.cat([st.sink_v, st.fp16_v], dim=2)
+        st.fp16_pos = torch.cat([st.sink_pos, st.fp16_pos])
+        st._fp16_buf_k = st._fp16_buf_v = st._fp16_buf_pos = None
+        st.sink_k = st.sink_v = st.sink_pos = None
+        st.sink_count = 4
+    torch.use_deterministic_algorithms(True)
+    try:
+        plans = set()
+        for step in range(140):  # crosses the fp16 buffer's first growth
+            kt = torch.randn(B, H, 1, D, generator=g).half().to(dev)
+            vt = torch.randn(B, H, 1, D, generator=g).half().to(dev)
+            c.update(kt, vt, 0)
+            q = torch.randn(B, Hq, 1, D, generator=g).half().to(dev)
+            out = c.decode_attention(q, 0)
+            plans.add(id(st._decode_plan[1]))
+            st_plan, st._decode_plan = st._decode_plan, None
+            fresh = c.decode_attention(q, 0)  # built afresh for this step
+            st._decode_plan = st_plan
+            assert torch.equal(out, fresh), step
+            if step % 35 == 0:
+                kf, vf = c._materialize(0)
+                ref = F.scaled_dot_product_attention(q.float(), kf.float().repeat_interleave(Hq // H, 1),
+                                                     vf.float().repeat_interleave(Hq // H, 1))
+                assert (out.float() - ref).abs().max().item() <= 2e-3, step
+        assert len(plans) < 10  # reused, not rebuilt per step
+    finally:
+        torch.use_deterministic_algorithms(False)

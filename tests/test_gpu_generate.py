@@ -70,17 +70,22 @@ def test_fused_cache_mode_and_kernels_run(dev, monkeypatch):
     import fade_amd.kernels.prefill as kp
     import fade_amd.kernels.tiered_attn as kt
 
-    real_d, real_p = kt.tiered_decode_attention, kp.tiered_prefill_attention
+    real_run, real_rerun, real_p = kt.TieredDecodePlan.run, kt.TieredDecodePlan.rerun, kp.tiered_prefill_attention
 
-    def d(*a, **k):
+    def run(self, *a, **k):  # decode launches: a plan's first launch, then its relaunches
         calls["decode"] += 1
-        return real_d(*a, **k)
+        return real_run(self, *a, **k)
+
+    def rerun(self, *a, **k):
+        calls["decode"] += 1
+        return real_rerun(self, *a, **k)
 
     def p(*a, **k):
         calls["prefill"] += 1
         return real_p(*a, **k)
 
-    monkeypatch.setattr(kt, "tiered_decode_attention", d)
+    monkeypatch.setattr(kt.TieredDecodePlan, "run", run)
+    monkeypatch.setattr(kt.TieredDecodePlan, "rerun", rerun)
     monkeypatch.setattr(kp, "tiered_prefill_attention", p)
     ids = torch.randint(0, cfg.vocab_size, (1, 12), device=dev)
     _steps(model, cache, ids, 2)
