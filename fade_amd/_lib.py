@@ -159,6 +159,9 @@ _SIGNATURES: dict[str, list] = {
     "fade_quant_k_int4_from_colmax": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
     "fade_quant_v_int4": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p],
     "fade_dequant_sym": [_p, _p, _i32, _i32, _i64, _i64, _i64, _i64, _p, _p],
+    "fade_quant_k_int4_dtype": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p],
+    "fade_quant_v_int4_dtype": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p],
+    "fade_dequant_sym_dtype": [_p, _p, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _p, _p],
     "fade_quant_int2_grouped": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p],
     "fade_dequant_int2_grouped": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
     "fade_quant_rotated_workspace_bytes": [_i64, _i64, _i64, _i64, _i32, _pi64],
@@ -259,6 +262,10 @@ def require_gpu(*tensors: torch.Tensor | None, op: str = "fade_amd") -> None:
             dev = t.device
         elif t.device != dev:
             raise ValueError(f"{op}: tensors are on different devices ({dev} vs {t.device})")
+
+
+# FADE_DTYPE_* of the dtype-tagged quantizer entry points
+DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
 
 def require_f16(t: torch.Tensor, op: str) -> None:

@@ -32,12 +32,35 @@ __device__ __forceinline__ float round_f16(float x) {
   return static_cast<float>(static_cast<_Float16>(x));
 }
 
+// bf16 helpers: fp32 -> bf16 rounds to nearest even; NaN becomes the
+// canonical quiet NaN 0x7FC0 (torch's c10::BFloat16 conversion).
+__device__ __forceinline__ float bf2f(uint16_t bits) { return __uint_as_float(static_cast<uint32_t>(bits) << 16); }
+__device__ __forceinline__ uint16_t f2bf(float x) {
+  const uint32_t u = __float_as_uint(x);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  return static_cast<uint16_t>((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ float round_bf16(float x) { return bf2f(f2bf(x)); }
+
 // Reduction across `width` consecutive lanes (width a power of two <= 64).
 template <int WIDTH>
 __device__ __forceinline__ float group_max(float v) {
 #pragma unroll
   for (int o = WIDTH / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
+}
+// max(m, |v|) for m >= 0 that keeps NaN, as torch's amax does: on the bit
+// patterns of non-negative floats every NaN orders above +inf.
+__device__ __forceinline__ float absmax_nan(float m, float v) {
+  return __uint_as_float(max(__float_as_uint(m), __float_as_uint(fabsf(v))));
+}
+// group_max over non-negative values, NaN-propagating like absmax_nan.
+template <int WIDTH>
+__device__ __forceinline__ float group_max_abs(float v) {
+  uint32_t u = __float_as_uint(v);
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) u = max(u, static_cast<uint32_t>(__shfl_xor(static_cast<int>(u), o, 64)));
+  return __uint_as_float(u);
 }
 template <int WIDTH>
 __device__ __forceinline__ float group_min(float v) {

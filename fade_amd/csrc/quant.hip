@@ -17,7 +17,22 @@ namespace fade {
 namespace {
 
 constexpr int kBlock = 256;
-enum { MODE_F16 = 0, MODE_F32 = 1 };
+// Element arithmetic of the input tensor, as torch rounds it per op: fp16,
+// fp32 with an fp16 scale (the rotated path's x_rot), bf16, or plain fp32
+// K/V (fp32 scale).
+enum { MODE_F16 = 0, MODE_F32 = 1, MODE_BF16 = 2, MODE_F32S = 3 };
+struct Bf16 {  // bf16 elements (raw bits)
+  uint16_t bits;
+};
+// Storage of the emitted scale: 16-bit (fp16 or bf16 bits) or fp32.
+template <int MODE>
+struct ScaleOf {
+  using T = uint16_t;
+};
+template <>
+struct ScaleOf<MODE_F32S> {
+  using T = float;
+};
 
 template <int BITS>
 struct QRange;
@@ -46,6 +61,15 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* v) {
     v[2 * i + 1] = h2f(static_cast<uint16_t>(u[i] >> 16));
   }
 }
+__device__ __forceinline__ void load8(const Bf16* p, float* v) {
+  const uint4 w = *reinterpret_cast<const uint4*>(p);
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(u[i] << 16);
+    v[2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
+  }
+}
 __device__ __forceinline__ void load8(const float* p, float* v) {
   const float4 a = *reinterpret_cast<const float4*>(p);
   const float4 b = *reinterpret_cast<const float4*>(p + 4);
@@ -55,17 +79,26 @@ __device__ __forceinline__ void load8(const float* p, float* v) {
 
 // inv = qmax / absmax, scale = absmax / qmax in the reference's rounding.
 template <int MODE, int QMAX>
-__device__ __forceinline__ void sym_params(float absmax, float& inv, uint16_t& scale_h) {
-  if (MODE == MODE_F16) {
+__device__ __forceinline__ void sym_params(float absmax, float& inv, typename ScaleOf<MODE>::T& scale_h) {
+  if constexpr (MODE == MODE_F16) {
     // clamp(min=1e-8) is a no-op on fp16 (1e-8 rounds to zero).
     const float r = round_f16(1.0f / absmax);
     inv = round_f16(r * static_cast<float>(QMAX));
     scale_h = f2h(absmax / static_cast<float>(QMAX));
+  } else if constexpr (MODE == MODE_BF16) {
+    // bf16 holds 1e-8: the clamp bites, then every op rounds to bf16
+    const float a = round_bf16(absmax != absmax ? absmax : fmaxf(absmax, 1e-8f));
+    const float r = round_bf16(1.0f / a);
+    inv = round_bf16(r * static_cast<float>(QMAX));
+    scale_h = f2bf(a / static_cast<float>(QMAX));
   } else {
-    const float a = fmaxf(absmax, 1e-8f);
+    const float a = absmax != absmax ? absmax : fmaxf(absmax, 1e-8f);  // clamp keeps NaN
     const float r = 1.0f / a;
     inv = r * static_cast<float>(QMAX);
-    scale_h = f2h(a / static_cast<float>(QMAX));
+    if constexpr (MODE == MODE_F32S)
+      scale_h = a / static_cast<float>(QMAX);
+    else
+      scale_h = f2h(a / static_cast<float>(QMAX));
   }
 }
 
@@ -74,6 +107,7 @@ template <int MODE, int QLO, int QHI>
 __device__ __forceinline__ int sym_code(float x, float inv) {
   float p = x * inv;
   if (MODE == MODE_F16) p = round_f16(p);
+  if (MODE == MODE_BF16) p = round_bf16(p);
   float q = rintf(p);
   if (q != q) return 0;
   q = fminf(fmaxf(q, static_cast<float>(QLO)), static_cast<float>(QHI));
@@ -147,7 +181,7 @@ __global__ __launch_bounds__(kBlock) void quant_token_kernel(const InT* __restri
                                                              int64_t H, int64_t S, int64_t sb,
                                                              int64_t sh, int64_t ss, int64_t fs,
                                                              uint8_t* __restrict__ packed,
-                                                             uint16_t* __restrict__ scale) {
+                                                             typename ScaleOf<MODE>::T* __restrict__ scale) {
   constexpr int RP = kBlock / LPR;
   constexpr int ROW_BYTES = LPR * lane_bytes<BITS>();
   const int c = threadIdx.x % LPR;
@@ -157,10 +191,10 @@ __global__ __launch_bounds__(kBlock) void quant_token_kernel(const InT* __restri
     load8(x + (fs ? r * fs : row_offset(r, H, S, sb, sh, ss)) + c * 8, v);
     float a = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(v[j]));
-    a = group_max<LPR>(a);
+    for (int j = 0; j < 8; ++j) a = absmax_nan(a, v[j]);
+    a = group_max_abs<LPR>(a);
     float inv;
-    uint16_t sc;
+    typename ScaleOf<MODE>::T sc;
     sym_params<MODE, QRange<BITS>::hi>(a, inv, sc);
     int code[8];
 #pragma unroll
@@ -189,7 +223,7 @@ __global__ __launch_bounds__(kBlock) void colmax_kernel(const InT* __restrict__ 
     float v[8];
     load8(base + s * ss, v);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) m[j] = fmaxf(m[j], fabsf(v[j]));
+    for (int j = 0; j < 8; ++j) m[j] = absmax_nan(m[j], v[j]);
   }
   __shared__ float red[RP * D];
 #pragma unroll
@@ -197,7 +231,7 @@ __global__ __launch_bounds__(kBlock) void colmax_kernel(const InT* __restrict__ 
   __syncthreads();
   for (int d = threadIdx.x; d < D; d += kBlock) {
     float mm = 0.0f;
-    for (int r = 0; r < RP; ++r) mm = fmaxf(mm, red[r * D + d]);
+    for (int r = 0; r < RP; ++r) mm = absmax_nan(mm, red[r * D + d]);
     partial[(bh * gridDim.x + blockIdx.x) * D + d] = mm;
   }
 }
@@ -209,7 +243,7 @@ template <typename InT, int MODE, int BITS, int LPR>
 __global__ __launch_bounds__(kBlock) void quant_channel_kernel(
     const InT* __restrict__ x, int64_t H, int64_t S, int64_t sb, int64_t sh, int64_t ss,
     int64_t rows_per_block, const float* __restrict__ partial, int nparts, uint8_t* __restrict__ packed,
-    uint16_t* __restrict__ scale) {
+    typename ScaleOf<MODE>::T* __restrict__ scale) {
   constexpr int RP = kBlock / LPR;
   constexpr int D = LPR * 8;
   constexpr int ROW_BYTES = LPR * lane_bytes<BITS>();
@@ -217,9 +251,9 @@ __global__ __launch_bounds__(kBlock) void quant_channel_kernel(
   __shared__ float inv_s[D];
   for (int d = threadIdx.x; d < D; d += kBlock) {
     float a = 0.0f;
-    for (int k = 0; k < nparts; ++k) a = fmaxf(a, partial[(bh * nparts + k) * D + d]);
+    for (int k = 0; k < nparts; ++k) a = absmax_nan(a, partial[(bh * nparts + k) * D + d]);
     float inv;
-    uint16_t sc;
+    typename ScaleOf<MODE>::T sc;
     sym_params<MODE, QRange<BITS>::hi>(a, inv, sc);
     inv_s[d] = inv;
     if (blockIdx.x == 0) scale[bh * D + d] = sc;
@@ -243,11 +277,32 @@ __global__ __launch_bounds__(kBlock) void quant_channel_kernel(
 }
 
 // ---------------------------------------------------------- dequant (sym)
-template <int BITS, int LPR>
+// out = code * scale rounded to the output type; scale and out share it:
+// fp16 (uint16_t), bf16 (Bf16) or fp32.
+__device__ __forceinline__ float scale_ld(uint16_t u) { return h2f(u); }
+__device__ __forceinline__ float scale_ld(Bf16 u) { return bf2f(u.bits); }
+__device__ __forceinline__ float scale_ld(float u) { return u; }
+__device__ __forceinline__ void store8(uint16_t* p, const float* y) {
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) w[j] = static_cast<uint32_t>(f2h(y[2 * j])) | (static_cast<uint32_t>(f2h(y[2 * j + 1])) << 16);
+  *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+__device__ __forceinline__ void store8(Bf16* p, const float* y) {
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) w[j] = static_cast<uint32_t>(f2bf(y[2 * j])) | (static_cast<uint32_t>(f2bf(y[2 * j + 1])) << 16);
+  *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+__device__ __forceinline__ void store8(float* p, const float* y) {
+  reinterpret_cast<float4*>(p)[0] = make_float4(y[0], y[1], y[2], y[3]);
+  reinterpret_cast<float4*>(p)[1] = make_float4(y[4], y[5], y[6], y[7]);
+}
+
+template <int BITS, int LPR, typename T>
 __global__ __launch_bounds__(kBlock) void dequant_sym_kernel(const uint8_t* __restrict__ packed,
-                                                             const uint16_t* __restrict__ scale,
-                                                             int axis, int64_t rows, int64_t S,
-                                                             uint16_t* __restrict__ out) {
+                                                             const T* __restrict__ scale, int axis,
+                                                             int64_t rows, int64_t S, T* __restrict__ out) {
   constexpr int RP = kBlock / LPR;
   constexpr int D = LPR * 8;
   constexpr int ROW_BYTES = LPR * lane_bytes<BITS>();
@@ -256,21 +311,17 @@ __global__ __launch_bounds__(kBlock) void dequant_sym_kernel(const uint8_t* __re
        r += static_cast<int64_t>(gridDim.x) * RP) {
     int code[8];
     load_codes<BITS>(packed + r * ROW_BYTES + c * lane_bytes<BITS>(), code);
-    uint32_t w[4];
+    float y[8];
+    if (axis == FADE_AXIS_TOKEN) {
+      const float sc = scale_ld(scale[r]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float s0, s1;
-      if (axis == FADE_AXIS_TOKEN) {
-        s0 = s1 = h2f(scale[r]);
-      } else {
-        const int64_t bh = r / S;
-        s0 = h2f(scale[bh * D + c * 8 + 2 * j]);
-        s1 = h2f(scale[bh * D + c * 8 + 2 * j + 1]);
-      }
-      w[j] = static_cast<uint32_t>(f2h(static_cast<float>(code[2 * j]) * s0)) |
-             (static_cast<uint32_t>(f2h(static_cast<float>(code[2 * j + 1]) * s1)) << 16);
+      for (int j = 0; j < 8; ++j) y[j] = static_cast<float>(code[j]) * sc;
+    } else {
+      const T* sp = scale + (r / S) * D + c * 8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = static_cast<float>(code[j]) * scale_ld(sp[j]);
     }
-    *reinterpret_cast<uint4*>(out + r * D + c * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+    store8(out + r * D + c * 8, y);
   }
 }
 
@@ -289,7 +340,7 @@ __global__ void quant_int2_grouped_kernel(const uint16_t* __restrict__ x, int64_
   for (int i = 0; i < group; ++i) {
     const int64_t s = g * group + i;
     const float v = s < S ? h2f(base[s * ss]) : 0.0f;
-    a = fmaxf(a, fabsf(v));
+    a = absmax_nan(a, v);
   }
   float inv;
   uint16_t sc;
@@ -512,7 +563,7 @@ int launch_channel(const char* fn, const InT* x, int64_t B, int64_t H, int64_t S
                        rpb, static_cast<float*>(ws));
     hipLaunchKernelGGL((quant_channel_kernel<InT, MODE, BITS, LPR>), grid, dim3(kBlock), 0, st, x,
                        H, S, sb, sh, ss, rpb, static_cast<const float*>(ws), static_cast<int>(nsb),
-                       static_cast<uint8_t*>(packed), static_cast<uint16_t*>(scale));
+                       static_cast<uint8_t*>(packed), static_cast<typename ScaleOf<MODE>::T*>(scale));
   });
   return check_launch(fn);
 }
@@ -533,7 +584,7 @@ int launch_channel_given(const char* fn, const InT* x, int64_t B, int64_t H, int
   FADE_DISPATCH_LPR(D, {
     hipLaunchKernelGGL((quant_channel_kernel<InT, MODE, BITS, LPR>), grid, dim3(kBlock), 0, st, x,
                        H, S, sb, sh, ss, rpb, partial, static_cast<int>(nparts),
-                       static_cast<uint8_t*>(packed), static_cast<uint16_t*>(scale));
+                       static_cast<uint8_t*>(packed), static_cast<typename ScaleOf<MODE>::T*>(scale));
   });
   return check_launch(fn);
 }
@@ -546,7 +597,7 @@ int launch_token(const char* fn, const InT* x, int64_t B, int64_t H, int64_t S, 
   FADE_DISPATCH_LPR(D, {
     hipLaunchKernelGGL((quant_token_kernel<InT, MODE, BITS, LPR>), dim3(grid_for_rows(rows, LPR)),
                        dim3(kBlock), 0, st, x, rows, H, S, sb, sh, ss, flat_row_stride(H, S, sb, sh, ss),
-                       static_cast<uint8_t*>(packed), static_cast<uint16_t*>(scale));
+                       static_cast<uint8_t*>(packed), static_cast<typename ScaleOf<MODE>::T*>(scale));
   });
   return check_launch(fn);
 }
@@ -635,35 +686,97 @@ FADE_API int fade_quant_v_int4(const void* v_f16, int64_t B, int64_t H, int64_t 
                                              as_stream(stream));
 }
 
+FADE_API int fade_quant_k_int4_dtype(const void* k, int32_t dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                                     int64_t sb, int64_t sh, int64_t ss, void* packed_u8, void* scale,
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* fn = "fade_quant_k_int4_dtype";
+  int rc = check_dims(fn, B, H, S, D);
+  if (rc) return rc;
+  if (!aligned(k, 16) || (sb | sh | ss) % 8 != 0)
+    return einval("%s: input must be 16-byte aligned with strides a multiple of 8", fn);
+  switch (dtype) {
+    case FADE_DTYPE_F16:
+      return launch_channel<uint16_t, MODE_F16, 4>(fn, static_cast<const uint16_t*>(k), B, H, S, D, sb, sh, ss,
+                                                   packed_u8, scale, workspace, workspace_bytes, as_stream(stream));
+    case FADE_DTYPE_BF16:
+      return launch_channel<Bf16, MODE_BF16, 4>(fn, static_cast<const Bf16*>(k), B, H, S, D, sb, sh, ss, packed_u8,
+                                                scale, workspace, workspace_bytes, as_stream(stream));
+    case FADE_DTYPE_F32:
+      return launch_channel<float, MODE_F32S, 4>(fn, static_cast<const float*>(k), B, H, S, D, sb, sh, ss,
+                                                 packed_u8, scale, workspace, workspace_bytes, as_stream(stream));
+    default: return einval("%s: unknown dtype %d", fn, dtype);
+  }
+}
+
+FADE_API int fade_quant_v_int4_dtype(const void* v, int32_t dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                                     int64_t sb, int64_t sh, int64_t ss, void* packed_u8, void* scale,
+                                     void* stream) {
+  const char* fn = "fade_quant_v_int4_dtype";
+  int rc = check_dims(fn, B, H, S, D);
+  if (rc) return rc;
+  if (!aligned(v, 16) || (sb | sh | ss) % 8 != 0)
+    return einval("%s: input must be 16-byte aligned with strides a multiple of 8", fn);
+  switch (dtype) {
+    case FADE_DTYPE_F16:
+      return launch_token<uint16_t, MODE_F16, 4>(fn, static_cast<const uint16_t*>(v), B, H, S, D, sb, sh, ss,
+                                                 packed_u8, scale, as_stream(stream));
+    case FADE_DTYPE_BF16:
+      return launch_token<Bf16, MODE_BF16, 4>(fn, static_cast<const Bf16*>(v), B, H, S, D, sb, sh, ss, packed_u8,
+                                              scale, as_stream(stream));
+    case FADE_DTYPE_F32:
+      return launch_token<float, MODE_F32S, 4>(fn, static_cast<const float*>(v), B, H, S, D, sb, sh, ss, packed_u8,
+                                               scale, as_stream(stream));
+    default: return einval("%s: unknown dtype %d", fn, dtype);
+  }
+}
+
+namespace fade {
+namespace {
+template <typename T>
+int dequant_sym(const char* fn, const void* packed_u8, const void* scale, int32_t bits, int32_t axis, int64_t B,
+                int64_t H, int64_t S, int64_t D, void* out, void* stream) {
+  int rc = check_dims(fn, B, H, S, D);
+  if (rc) return rc;
+  if (bits != 4 && bits != 3 && bits != 2) return einval("%s: bits must be 4, 3 or 2, got %d", fn, bits);
+  if (axis != FADE_AXIS_CHANNEL && axis != FADE_AXIS_TOKEN) return einval("%s: bad axis %d", fn, axis);
+  const int64_t rows = B * H * S;
+  if (rows == 0) return FADE_OK;
+  const uint8_t* pk = static_cast<const uint8_t*>(packed_u8);
+  const T* sc = static_cast<const T*>(scale);
+  T* o = static_cast<T*>(out);
+  FADE_DISPATCH_LPR(D, {
+    const dim3 grid(grid_for_rows(rows, LPR));
+    if (bits == 4)
+      hipLaunchKernelGGL((dequant_sym_kernel<4, LPR, T>), grid, dim3(kBlock), 0, as_stream(stream), pk, sc, axis,
+                         rows, S, o);
+    else if (bits == 3)
+      hipLaunchKernelGGL((dequant_sym_kernel<3, LPR, T>), grid, dim3(kBlock), 0, as_stream(stream), pk, sc, axis,
+                         rows, S, o);
+    else
+      hipLaunchKernelGGL((dequant_sym_kernel<2, LPR, T>), grid, dim3(kBlock), 0, as_stream(stream), pk, sc, axis,
+                         rows, S, o);
+  });
+  return check_launch(fn);
+}
+}  // namespace
+}  // namespace fade
+
 FADE_API int fade_dequant_sym(const void* packed_u8, const void* scale_f16, int32_t bits,
                               int32_t axis, int64_t B, int64_t H, int64_t S, int64_t D,
                               void* out_f16, void* stream) {
-  int rc = check_dims("fade_dequant_sym", B, H, S, D);
-  if (rc) return rc;
-  if (bits != 4 && bits != 3 && bits != 2)
-    return einval("fade_dequant_sym: bits must be 4, 3 or 2, got %d", bits);
-  if (axis != FADE_AXIS_CHANNEL && axis != FADE_AXIS_TOKEN)
-    return einval("fade_dequant_sym: bad axis %d", axis);
-  const int64_t rows = B * H * S;
-  if (rows == 0) return FADE_OK;
-  FADE_DISPATCH_LPR(D, {
-    if (bits == 4)
-      hipLaunchKernelGGL((dequant_sym_kernel<4, LPR>), dim3(grid_for_rows(rows, LPR)), dim3(kBlock), 0,
-                         as_stream(stream), static_cast<const uint8_t*>(packed_u8),
-                         static_cast<const uint16_t*>(scale_f16), axis, rows, S,
-                         static_cast<uint16_t*>(out_f16));
-    else if (bits == 3)
-      hipLaunchKernelGGL((dequant_sym_kernel<3, LPR>), dim3(grid_for_rows(rows, LPR)), dim3(kBlock), 0,
-                         as_stream(stream), static_cast<const uint8_t*>(packed_u8),
-                         static_cast<const uint16_t*>(scale_f16), axis, rows, S,
-                         static_cast<uint16_t*>(out_f16));
-    else
-      hipLaunchKernelGGL((dequant_sym_kernel<2, LPR>), dim3(grid_for_rows(rows, LPR)), dim3(kBlock), 0,
-                         as_stream(stream), static_cast<const uint8_t*>(packed_u8),
-                         static_cast<const uint16_t*>(scale_f16), axis, rows, S,
-                         static_cast<uint16_t*>(out_f16));
-  });
-  return check_launch("fade_dequant_sym");
+  return dequant_sym<uint16_t>("fade_dequant_sym", packed_u8, scale_f16, bits, axis, B, H, S, D, out_f16, stream);
+}
+
+FADE_API int fade_dequant_sym_dtype(const void* packed_u8, const void* scale, int32_t dtype, int32_t bits,
+                                    int32_t axis, int64_t B, int64_t H, int64_t S, int64_t D, void* out,
+                                    void* stream) {
+  const char* fn = "fade_dequant_sym_dtype";
+  switch (dtype) {
+    case FADE_DTYPE_F16: return dequant_sym<uint16_t>(fn, packed_u8, scale, bits, axis, B, H, S, D, out, stream);
+    case FADE_DTYPE_BF16: return dequant_sym<Bf16>(fn, packed_u8, scale, bits, axis, B, H, S, D, out, stream);
+    case FADE_DTYPE_F32: return dequant_sym<float>(fn, packed_u8, scale, bits, axis, B, H, S, D, out, stream);
+    default: return einval("%s: unknown dtype %d", fn, dtype);
+  }
 }
 
 FADE_API int fade_quant_int2_grouped(const void* x_f16, int64_t B, int64_t H, int64_t S,

@@ -45,6 +45,20 @@ def _prep_f16(x: Tensor, op: str) -> Tensor:
     _check_4d(x, op)
     _lib.require_gpu(x, op=op)
     _lib.require_f16(x, op)
+    return _aligned(x)
+
+
+def _prep_kv(x: Tensor, op: str) -> Tensor:
+    """K/V input of the INT4 quantizers: float16, bfloat16 or float32 (the
+    reference's quantizers take any float dtype and return the scale in it)."""
+    _check_4d(x, op)
+    _lib.require_gpu(x, op=op)
+    if x.dtype not in _lib.DTYPE_CODES:
+        raise ValueError(f"{op}: expected a float16, bfloat16 or float32 tensor, got {x.dtype}")
+    return _aligned(x)
+
+
+def _aligned(x: Tensor) -> Tensor:
     if x.stride(-1) != 1 or x.data_ptr() % 16 or any(s % 8 for s in x.stride()[:3]):
         x = x.contiguous()
     return x
@@ -90,12 +104,13 @@ def _unpack_codes(packed: Tensor, bits: int) -> Tensor:
 def quant_k_int4(k: Tensor) -> tuple[Tensor, Tensor]:
     """Per-channel symmetric INT4 for K, bit-packed (fade/quant.py:61-75).
 
-    Returns ``(packed [B,H,S,D//2] uint8, scale [B,H,1,D] fp16)``.
+    Returns ``(packed [B,H,S,D//2] uint8, scale [B,H,1,D] k.dtype)``; ``k`` is
+    float16, bfloat16 or float32.
     """
-    k = _prep_f16(k, "quant_k_int4")
+    k = _prep_kv(k, "quant_k_int4")
     B, H, S, D = k.shape
     packed = torch.empty(B, H, S, D // 2, dtype=torch.uint8, device=k.device)
-    scale = torch.empty(B, H, 1, D, dtype=torch.float16, device=k.device)
+    scale = torch.empty(B, H, 1, D, dtype=k.dtype, device=k.device)
     if k.numel() == 0:
         return packed, scale
     lib = _lib.load()
@@ -103,10 +118,16 @@ def quant_k_int4(k: Tensor) -> tuple[Tensor, Tensor]:
     _lib.check(lib.fade_quant_k_int4_workspace_bytes(B, H, S, D, nb), "fade_quant_k_int4_workspace_bytes")
     ws = _lib.scratch(nb.value, k.device)  # column partials: written in full before they are read
     sb, sh, ss = _strides_bhs(k)
-    _lib.call(
-        "fade_quant_k_int4", k.data_ptr(), B, H, S, D, sb, sh, ss, packed.data_ptr(),
-        scale.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(k),
-    )
+    if k.dtype == torch.float16:
+        _lib.call(
+            "fade_quant_k_int4", k.data_ptr(), B, H, S, D, sb, sh, ss, packed.data_ptr(),
+            scale.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(k),
+        )
+    else:
+        _lib.call(
+            "fade_quant_k_int4_dtype", k.data_ptr(), _lib.DTYPE_CODES[k.dtype], B, H, S, D, sb, sh, ss,
+            packed.data_ptr(), scale.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(k),
+        )
     return packed, scale
 
 
@@ -139,19 +160,26 @@ def quant_k_int4_from_colmax(k: Tensor, colmax: Tensor) -> tuple[Tensor, Tensor]
 def quant_v_int4(v: Tensor) -> tuple[Tensor, Tensor]:
     """Per-token symmetric INT4 for V, bit-packed (fade/quant.py:78-92).
 
-    Returns ``(packed [B,H,S,D//2] uint8, scale [B,H,S,1] fp16)``.
+    Returns ``(packed [B,H,S,D//2] uint8, scale [B,H,S,1] v.dtype)``; ``v`` is
+    float16, bfloat16 or float32.
     """
-    v = _prep_f16(v, "quant_v_int4")
+    v = _prep_kv(v, "quant_v_int4")
     B, H, S, D = v.shape
     packed = torch.empty(B, H, S, D // 2, dtype=torch.uint8, device=v.device)
-    scale = torch.empty(B, H, S, 1, dtype=torch.float16, device=v.device)
+    scale = torch.empty(B, H, S, 1, dtype=v.dtype, device=v.device)
     if v.numel() == 0:
         return packed, scale
     sb, sh, ss = _strides_bhs(v)
-    _lib.call(
-        "fade_quant_v_int4", v.data_ptr(), B, H, S, D, sb, sh, ss, packed.data_ptr(),
-        scale.data_ptr(), _lib.stream_of(v),
-    )
+    if v.dtype == torch.float16:
+        _lib.call(
+            "fade_quant_v_int4", v.data_ptr(), B, H, S, D, sb, sh, ss, packed.data_ptr(),
+            scale.data_ptr(), _lib.stream_of(v),
+        )
+    else:
+        _lib.call(
+            "fade_quant_v_int4_dtype", v.data_ptr(), _lib.DTYPE_CODES[v.dtype], B, H, S, D, sb, sh, ss,
+            packed.data_ptr(), scale.data_ptr(), _lib.stream_of(v),
+        )
     return packed, scale
 
 
@@ -210,23 +238,30 @@ def _scale_axis(packed: Tensor, scale: Tensor) -> int:
 
 
 def dequant_sym(packed: Tensor, scale: Tensor, bits: int, dtype: torch.dtype = torch.float16) -> Tensor:
-    """Unpack symmetric codes and return ``fp16(code * scale)``."""
+    """Unpack symmetric codes and return ``dtype(code * scale.to(dtype))``
+    (float16, bfloat16 or float32, as ``q.to(dtype) * scale.to(dtype)``)."""
     _check_4d(packed, "dequant")
     _lib.require_gpu(packed, scale, op="dequant")
-    if dtype != torch.float16:
-        raise ValueError(f"fade_amd dequantizes to float16 only, got {dtype}")
+    if dtype not in _lib.DTYPE_CODES:
+        raise ValueError(f"fade_amd dequantizes to float16, bfloat16 or float32, got {dtype}")
     axis = _scale_axis(packed, scale)
     B, H, S, nb = packed.shape
     D = nb if bits == 3 else nb * 8 // bits
-    out = torch.empty(B, H, S, D, dtype=torch.float16, device=packed.device)
+    out = torch.empty(B, H, S, D, dtype=dtype, device=packed.device)
     if out.numel() == 0:
         return out
     packed = packed.contiguous()
-    scale = scale.to(torch.float16).contiguous()
-    _lib.call(
-        "fade_dequant_sym", packed.data_ptr(), scale.data_ptr(), bits, axis, B, H, S, D,
-        out.data_ptr(), _lib.stream_of(packed),
-    )
+    scale = scale.to(dtype).contiguous()
+    if dtype == torch.float16:
+        _lib.call(
+            "fade_dequant_sym", packed.data_ptr(), scale.data_ptr(), bits, axis, B, H, S, D,
+            out.data_ptr(), _lib.stream_of(packed),
+        )
+    else:
+        _lib.call(
+            "fade_dequant_sym_dtype", packed.data_ptr(), scale.data_ptr(), _lib.DTYPE_CODES[dtype], bits, axis,
+            B, H, S, D, out.data_ptr(), _lib.stream_of(packed),
+        )
     return out
 
 

@@ -39,6 +39,11 @@ extern "C" {
 #define FADE_AXIS_CHANNEL 0 /* one scale per (b, h, d): reduce over S (K)  */
 #define FADE_AXIS_TOKEN 1   /* one scale per (b, h, s): reduce over D (V)  */
 
+/* element type of the *_dtype quantizer entry points (input, scale, output) */
+#define FADE_DTYPE_F16 0
+#define FADE_DTYPE_BF16 1
+#define FADE_DTYPE_F32 2
+
 /* Middle-tier formats understood by the attention kernels. */
 #define FADE_MID_NONE 0 /* no middle tier                                      */
 #define FADE_MID_FP16 1 /* fp16 K/V (flash-decode comparator)                  */
@@ -86,6 +91,22 @@ int fade_quant_v_int4(const void* v_f16, int64_t B, int64_t H, int64_t S, int64_
  * scale layout ([B,H,1,D] for CHANNEL, [B,H,S,1] for TOKEN); bits 4|2. */
 int fade_dequant_sym(const void* packed_u8, const void* scale_f16, int32_t bits, int32_t axis,
                      int64_t B, int64_t H, int64_t S, int64_t D, void* out_f16, void* stream);
+
+/* fade_quant_k_int4 / fade_quant_v_int4 / fade_dequant_sym for any of the
+ * dtypes the reference's quantizers take (fade/quant.py:61-92, 124-127;
+ * tests/test_quant.py:110-141 run them on bfloat16 and float32): the scale
+ * is emitted in the input's dtype, and each op rounds to that dtype as
+ * torch's per-op arithmetic does (bf16: clamp(min=1e-8), reciprocal, *qmax,
+ * x*inv each rounded to bf16; fp32: one IEEE rounding per op).  dtype is a
+ * FADE_DTYPE_*; FADE_DTYPE_F16 gives the fp16 entry points' results. */
+int fade_quant_k_int4_dtype(const void* k, int32_t dtype, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                            int64_t sh, int64_t ss, void* packed_u8, void* scale, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+int fade_quant_v_int4_dtype(const void* v, int32_t dtype, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                            int64_t sh, int64_t ss, void* packed_u8, void* scale, void* stream);
+/* out = dtype(code * scale), scale and out both of `dtype`. */
+int fade_dequant_sym_dtype(const void* packed_u8, const void* scale, int32_t dtype, int32_t bits, int32_t axis,
+                           int64_t B, int64_t H, int64_t S, int64_t D, void* out, void* stream);
 
 /* ---------------- grouped INT2, reference literal (fade/quant.py:95-176) --- */
 /* x [B,H,S,D] fp16 (rows >= S read as zero, i.e. pad_to_group fused) ->

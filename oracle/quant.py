@@ -1,8 +1,8 @@
 """Numpy restatement of the reference quantizers (test infrastructure only).
 
 Reference: ``fade/quant.py`` and ``fade/rotated_quant.py`` of FADE.  Every
-fp16 op is modelled as "compute in fp32, round to fp16" (torch CPU
-semantics); every fp32 op as one IEEE fp32 rounding.
+fp16 (bf16) op is modelled as "compute in fp32, round to fp16 (bf16)" (torch
+CPU semantics); every fp32 op as one IEEE fp32 rounding.
 """
 
 from __future__ import annotations
@@ -183,6 +183,82 @@ def dequant_int2_grouped(q: np.ndarray, scale: np.ndarray, group_size: int = 64)
     G = S // group_size
     full = np.broadcast_to(scale[:, :, :, None, :], (B, H, G, group_size, D)).reshape(B, H, S, D)
     return dequant(q, full)
+
+
+# --------------------------------------------------------------------------- #
+# the INT4 K/V quantizers on any float dtype (fade/quant.py:61-92, 124-127):
+# tests/test_quant.py:110-141 run them on bfloat16 and float32.  numpy has no
+# bfloat16, so bf16 tensors are carried as their uint16 bit patterns.
+# --------------------------------------------------------------------------- #
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(F32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits, round to nearest even; every NaN -> 0x7FC0 (c10::BFloat16)."""
+    x = np.ascontiguousarray(x, dtype=F32)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[np.isnan(x)] = 0x7FC0
+    return r
+
+
+def to_f32(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Values of a tensor of ``dtype`` ("f16" | "bf16" | "f32") as fp32."""
+    if dtype == "bf16":
+        return bf16_to_f32(x)
+    return np.asarray(x).astype(F32)
+
+
+def from_f32(x32: np.ndarray, dtype: str) -> np.ndarray:
+    """Round fp32 values to ``dtype``'s storage (nearest even)."""
+    if dtype == "bf16":
+        return f32_to_bf16(x32)
+    if dtype == "f16":
+        return np.asarray(x32, dtype=F32).astype(F16)
+    return np.asarray(x32, dtype=F32)
+
+
+def _rnd(x32: np.ndarray, dtype: str) -> np.ndarray:
+    """One torch op on ``dtype``: computed in fp32, rounded to ``dtype``."""
+    return to_f32(from_f32(x32, dtype), dtype)
+
+
+def _sym_params_typed(absmax32: np.ndarray, qmax: int, dtype: str):
+    """``absmax.clamp(min=EPS)``, ``qmax / absmax`` (= reciprocal * qmax, two
+    roundings) and ``absmax / qmax``, each op rounded to ``dtype``.  The clamp
+    keeps NaN (torch.clamp propagates it); on fp16 it is a no-op."""
+    with np.errstate(divide="ignore", over="ignore", invalid="ignore"):
+        a = _rnd(np.where(np.isnan(absmax32), absmax32, np.maximum(absmax32, F32(EPS))), dtype)
+        r = _rnd(F32(1.0) / a, dtype)
+        inv = _rnd(r * F32(qmax), dtype)
+        scale = from_f32(a / F32(qmax), dtype)
+    return inv, scale
+
+
+def _sym_quant_typed(x, dtype: str, axis: int):
+    x32 = to_f32(x, dtype)
+    absmax = np.abs(x32).max(axis=axis, keepdims=True)  # NaN-propagating, as torch's amax
+    inv, scale = _sym_params_typed(absmax, INT4_MAX, dtype)
+    with np.errstate(invalid="ignore", over="ignore"):
+        prod = _rnd(x32 * inv, dtype)
+    return pack_int4_last_dim(_rne_clamp(prod, INT4_MIN, INT4_MAX)), scale
+
+
+def quant_k_int4_typed(k, dtype: str):
+    """fade/quant.py:61-75 on a ``dtype`` tensor: (packed, scale [B,H,1,D] of ``dtype``)."""
+    return _sym_quant_typed(k, dtype, -2)
+
+
+def quant_v_int4_typed(v, dtype: str):
+    """fade/quant.py:78-92 on a ``dtype`` tensor: (packed, scale [B,H,S,1] of ``dtype``)."""
+    return _sym_quant_typed(v, dtype, -1)
+
+
+def dequant_int4_typed(packed: np.ndarray, scale, dtype: str) -> np.ndarray:
+    """fade/quant.py:124-127: ``q.to(dtype) * scale.to(dtype)``, in ``dtype``'s storage."""
+    q = unpack_int4_last_dim(packed).astype(F32)
+    return from_f32(q * to_f32(scale, dtype), dtype)
 
 
 # --------------------------------------------------------------------------- #

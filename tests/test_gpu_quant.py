@@ -109,6 +109,81 @@ def test_dequant_int4_bit_exact(dev):
     assert np.array_equal(_u16(out.cpu().numpy()), _u16(oq.dequant_int4(op, osc)))
 
 
+# -------------------------------------------- bfloat16 / float32 K/V input
+_TDT = {"bf16": torch.bfloat16, "f32": torch.float32, "f16": torch.float16}
+
+
+def _typed_edge(shape, seed, dtype):
+    """``_edge_tensor``'s cases in ``dtype`` storage (bf16 as uint16 bits), plus
+    a channel under the 1e-8 clamp and one NaN (its channel's and token's
+    scales go NaN, their codes 0, as torch's amax/clamp/int8 cast give)."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(shape) * rng.lognormal(0, 0.5, size=shape[-1])).astype(np.float32)
+    x.reshape(-1)[::89] = 0.5
+    x.reshape(-1)[1::101] = -2.5
+    x[..., 0, :] = 0
+    x[..., 3] = 0
+    x[..., 5] = 3e-9
+    x[..., 7] = -3e-5
+    x[0, 0, 2, 9] = np.nan
+    return oq.from_f32(x, dtype)
+
+
+def _dev_typed(x, dtype, dev):
+    if dtype == "bf16":
+        return torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).view(torch.bfloat16).to(dev)
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def _host_typed(t, dtype):
+    t = t.cpu().contiguous()
+    return t.view(torch.int16).numpy().view(np.uint16) if dtype == "bf16" else t.numpy()
+
+
+def _same(got, ref, dtype):
+    """Bit-exact, except that a NaN matches any NaN pattern."""
+    g, r = oq.to_f32(got, dtype), oq.to_f32(ref, dtype)
+    nan = np.isnan(r)
+    assert np.array_equal(np.isnan(g), nan)
+    assert np.array_equal(g[~nan].view(np.uint32), r[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("shape", [(1, 8, 1980, 128), (2, 3, 67, 128), (1, 2, 5, 64), (1, 1, 300, 256)])
+def test_quant_int4_typed_bit_exact(dev, dtype, shape):
+    print(f"case quant_int4 {dtype} {shape}", flush=True)
+    x = _typed_edge(shape, 4, dtype)
+    xd = _dev_typed(x, dtype, dev)
+    for quant, oquant in ((fq.quant_k_int4, oq.quant_k_int4_typed), (fq.quant_v_int4, oq.quant_v_int4_typed)):
+        packed, scale = quant(xd)
+        assert scale.dtype == _TDT[dtype]
+        op, osc = oquant(x, dtype)
+        assert np.array_equal(packed.cpu().numpy(), op)
+        _same(_host_typed(scale, dtype), osc, dtype)
+        assert np.isnan(oq.to_f32(osc, dtype)).sum() == 1
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_dequant_int4_typed_bit_exact(dev, dtype):
+    print(f"case dequant_int4 {dtype}", flush=True)
+    x = _typed_edge((2, 2, 40, 128), 5, dtype)
+    for oquant in (oq.quant_k_int4_typed, oq.quant_v_int4_typed):
+        op, osc = oquant(x, dtype)
+        out = fq.dequant_int4(torch.from_numpy(op).to(dev), _dev_typed(osc, dtype, dev), dtype=_TDT[dtype])
+        assert out.dtype == _TDT[dtype]
+        _same(_host_typed(out, dtype), oq.dequant_int4_typed(op, osc, dtype), dtype)
+
+
+def test_dequant_int4_fp16_scale_to_bf16(dev):
+    """``dequant_int4(packed, fp16 scale, dtype=bf16)``: the scale is cast to
+    bf16 first (``scale.to(dtype)``), then the product rounds to bf16."""
+    x = _edge_tensor((1, 2, 33, 64), 6)
+    op, osc = oq.quant_v_int4(x)
+    out = fq.dequant_int4(torch.from_numpy(op).to(dev), torch.from_numpy(osc).to(dev), dtype=torch.bfloat16)
+    ref = oq.dequant_int4_typed(op, oq.from_f32(osc.astype(np.float32), "bf16"), "bf16")
+    _same(_host_typed(out, "bf16"), ref, "bf16")
+
+
 @pytest.mark.parametrize("bits", [4, 2])
 def test_pack_unpack_roundtrip_exhaustive(dev, bits):
     print(f"case pack bits={bits}", flush=True)
@@ -262,7 +337,7 @@ def test_empty_and_error_inputs(dev):
     e = torch.zeros(1, 2, 0, 128, dtype=torch.float16, device=dev)
     p, s = fq.quant_v_int4(e)
     assert p.shape == (1, 2, 0, 64) and s.shape == (1, 2, 0, 1)
-    with pytest.raises(ValueError, match="float16"):
-        fq.quant_k_int4(torch.zeros(1, 1, 4, 128, device=dev))
+    with pytest.raises(ValueError, match="float16, bfloat16 or float32"):
+        fq.quant_k_int4(torch.zeros(1, 1, 4, 128, dtype=torch.float64, device=dev))
     with pytest.raises(ValueError, match="head_dim must be"):
         fq.quant_v_int4(torch.zeros(1, 1, 4, 96, dtype=torch.float16, device=dev))

@@ -3,7 +3,8 @@ fade tests/test_quant.py, tests/test_cache.py, tests/test_cache_batched.py,
 tests/test_attn_impl.py and tests/test_perf.py (file:line on each test).  Same
 calls, shapes and bounds, with one difference: the build's caches and kernels are
 float16 on the GPU (the reference tests use float32 on the CPU), so every tensor
-here is fp16 on cuda:0 and bf16 input is refused with ValueError.  The one
+here is fp16 on cuda:0, except in the INT4 quantizer tests that the reference
+runs on bfloat16 and float32 (those dtypes are quantized natively).  The one
 fp32-precision bar (K of fp16 survivors within 1e-4) holds as it is: without an
 eviction nothing is re-RoPE'd.  Bit-level parity is pinned elsewhere against the
 oracle; these pin the contracts."""
@@ -80,16 +81,37 @@ def test_quant_int2_requires_divisible_group(dev, which):  # :83-89, :103-108
         quant(_randn(B, H, 100, D, dev=dev), group_size=64)
 
 
-def test_bf16_input_refused(dev):  # :110-132 (the reference round-trips bf16; the build is fp16-only)
-    x = torch.randn(B, H, S, D).to(torch.bfloat16).to(dev)
-    for fn in (quant_k_int4, quant_v_int4):
-        with pytest.raises(ValueError):
-            fn(x)
+def test_quant_k_int4_bf16_roundtrip(dev):  # :110-124
+    k = torch.randn(B, H, S, D, generator=torch.Generator().manual_seed(110)).to(torch.bfloat16).to(dev)
+    q, scale = quant_k_int4(k)
+    assert q.dtype == torch.uint8
+    assert scale.dtype == torch.bfloat16
+    k_hat = dequant_int4(q, scale, dtype=torch.bfloat16)
+    assert k_hat.dtype == torch.bfloat16
+    assert torch.isfinite(k_hat).all()
+    assert _rel(k.float(), k_hat.float()) < 0.2
+
+
+def test_quant_v_int4_bf16_roundtrip(dev):  # :127-132
+    v = torch.randn(B, H, S, D, generator=torch.Generator().manual_seed(127)).to(torch.bfloat16).to(dev)
+    q, scale = quant_v_int4(v)
+    v_hat = dequant_int4(q, scale, dtype=torch.bfloat16)
+    assert torch.isfinite(v_hat).all()
+    assert _rel(v.float(), v_hat.float()) < 0.2
 
 
 def test_quant_handles_tiny_absmax_without_nan(dev):  # :135-141
-    q, scale = quant_k_int4(torch.zeros(B, H, S, D, dtype=F16, device=dev))
-    assert torch.isfinite(dequant_int4(q, scale, dtype=F16)).all()
+    for dtype in (torch.float32, torch.float16, torch.bfloat16):
+        k = torch.zeros(B, H, S, D, dtype=dtype, device=dev)
+        q, scale = quant_k_int4(k)
+        k_hat = dequant_int4(q, scale, dtype=dtype)
+        assert torch.isfinite(k_hat).all(), f"NaN in {dtype} zero round-trip"
+
+
+def test_quant_rejects_non_float_kv_dtypes(dev):  # no reference counterpart: dtypes outside fp16/bf16/fp32
+    for dtype in (torch.float64, torch.int8):
+        with pytest.raises(ValueError):
+            quant_k_int4(torch.zeros(B, H, S, D, dtype=dtype, device=dev))
 
 
 def test_pad_to_group(dev):  # :144-154

@@ -132,6 +132,99 @@ def test_quant_int2_grouped_matches_torch_ops():
         oq.quant_int2_grouped(x[:, :, :100], 64)
 
 
+# ---------------------------------------- bfloat16 / float32 INT4 quantizers
+ALL_POS_BF16 = np.arange(1, 0x7F80, dtype=np.uint16)  # every positive finite bf16
+
+
+def _t_bf16(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16)
+
+
+def _bits_bf16(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_bf16_conversion_matches_torch():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(20000) * np.exp(rng.uniform(-40, 40, 20000))).astype(np.float32)
+    u = x.view(np.uint32)
+    u[:2000] = (u[:2000] & 0xFFFF0000) | 0x8000  # exact ties, both parities
+    x[2000:2004] = [np.inf, -np.inf, np.nan, -np.nan]
+    x[2004:2010] = [1e-40, -1e-42, 3.3895314e38, 3.4028235e38, 0.0, -0.0]  # subnormal, overflow to inf
+    ref = _bits_bf16(torch.from_numpy(x).to(torch.bfloat16))
+    got = oq.f32_to_bf16(x)
+    # NaN: any NaN pattern (torch's scalar conversion gives 0x7FC0, its
+    # vectorized CPU one 0xFFFF); every other value bit-exact
+    nan = np.isnan(x)
+    assert np.array_equal(got[~nan], ref[~nan])
+    assert np.all(np.isnan(oq.bf16_to_f32(got[nan]))) and np.all(np.isnan(oq.bf16_to_f32(ref[nan])))
+    assert np.array_equal(oq.bf16_to_f32(ref[~nan]), torch.from_numpy(x[~nan]).to(torch.bfloat16).float().numpy())
+
+
+@pytest.mark.parametrize("qmax", [7, 1])
+def test_sym_params_match_torch_bf16_for_every_positive_bf16(qmax):
+    """``absmax.clamp(min=1e-8)``, ``qmax / absmax``, ``absmax / qmax`` on bf16
+    tensors, exhaustively -- the clamp is live on bf16 (1e-8 is representable)."""
+    t = _t_bf16(np.concatenate([[0], ALL_POS_BF16]).astype(np.uint16)).clamp(min=1e-8)
+    inv, scale = oq._sym_params_typed(oq.bf16_to_f32(np.concatenate([[0], ALL_POS_BF16])), qmax, "bf16")
+    assert np.array_equal(oq.f32_to_bf16(inv), _bits_bf16(qmax / t))
+    assert np.array_equal(scale, _bits_bf16(t / qmax))
+
+
+def _hard_typed(shape, seed, dtype):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(shape) * rng.lognormal(0, 0.5, size=shape[-1])).astype(np.float32)
+    x.reshape(-1)[::97] = 0.5  # lands on .5 code boundaries after scaling
+    x[..., 0, :] = 0  # a zero token row
+    x[..., 3] = 0  # a zero channel
+    x[..., 5] = 3e-9  # a channel below the 1e-8 clamp (bf16/fp32 hold it)
+    x[..., 6] = rng.standard_normal(shape[:-1]) * 1e-9
+    x[0, 1, 7, 9] = np.nan  # a NaN: its channel's and token's scale go NaN, their codes 0
+    return oq.from_f32(x, dtype)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32", "f16"])
+def test_quant_int4_typed_matches_torch_ops(dtype):
+    x = _hard_typed((2, 3, 67, 64), 7, dtype)
+    t = _t_bf16(x) if dtype == "bf16" else torch.from_numpy(x)
+    bits = _bits_bf16 if dtype == "bf16" else (lambda a: a.numpy().view(np.uint16 if dtype == "f16" else np.uint32))
+    raw = (lambda a: a) if dtype == "bf16" else (lambda a: a.view(np.uint16 if dtype == "f16" else np.uint32))
+    for quant, tq in ((oq.quant_k_int4_typed, _torch_quant_k), (oq.quant_v_int4_typed, _torch_quant_v)):
+        qt, st = tq(t)
+        packed, scale = quant(x, dtype)
+        assert np.array_equal(oq.unpack_int4_last_dim(packed), qt.numpy())
+        nan = np.isnan(oq.to_f32(scale, dtype))
+        assert nan.sum() == 1 and np.array_equal(nan, torch.isnan(st).numpy())
+        assert np.array_equal(raw(scale)[~nan], bits(st)[~nan])
+    if dtype == "f16":  # the fp16 path is the same function
+        assert np.array_equal(oq.quant_k_int4_typed(x, "f16")[0], oq.quant_k_int4(x)[0])
+        assert np.array_equal(oq.quant_v_int4_typed(x, "f16")[1].view(np.uint16), oq.quant_v_int4(x)[1].view(np.uint16))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_dequant_int4_typed_matches_torch(dtype):
+    rng = np.random.default_rng(11)
+    q = rng.integers(-8, 8, size=(2, 2, 9, 16)).astype(np.int8)
+    s = oq.from_f32(rng.standard_normal((2, 2, 1, 16)).astype(np.float32), dtype)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    st = _t_bf16(s) if dtype == "bf16" else torch.from_numpy(s)
+    ref = torch.from_numpy(q).to(tdt) * st
+    got = oq.dequant_int4_typed(oq.pack_int4_last_dim(q), s, dtype)
+    assert np.array_equal(got, _bits_bf16(ref) if dtype == "bf16" else ref.numpy())
+
+
+def test_typed_quant_would_fail_without_the_bf16_clamp():
+    """A model without the clamp (fp16's no-op) disagrees with torch on bf16."""
+    x = _hard_typed((1, 2, 16, 16), 3, "bf16")
+    qt, _ = _torch_quant_k(_t_bf16(x))
+    x32 = oq.bf16_to_f32(x)
+    absmax = np.abs(x32).max(axis=-2, keepdims=True)
+    with np.errstate(divide="ignore", over="ignore", invalid="ignore"):
+        inv = oq._rnd(oq._rnd(np.float32(1) / absmax, "bf16") * np.float32(7), "bf16")
+        wrong = oq._rne_clamp(oq._rnd(x32 * inv, "bf16"), -8, 7)
+    assert not np.array_equal(wrong, qt.numpy())
+
+
 def test_dequant_matches_torch():
     rng = np.random.default_rng(3)
     q = rng.integers(-8, 8, size=(2, 2, 9, 16)).astype(np.int8)
