@@ -159,6 +159,7 @@ _SIGNATURES: dict[str, list] = {
     "fade_quant_k_int4_from_colmax": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
     "fade_quant_v_int4": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p],
     "fade_dequant_sym": [_p, _p, _i32, _i32, _i64, _i64, _i64, _i64, _p, _p],
+    "fade_quant_rotated_dtype": [_p, _i64, _i64, _i64, _i64, _i32, _i32, _p, _p, _i32, _p, _i64, _p],
     "fade_quant_k_int4_dtype": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p],
     "fade_quant_v_int4_dtype": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p],
     "fade_dequant_sym_dtype": [_p, _p, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _p, _p],

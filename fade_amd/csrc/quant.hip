@@ -18,9 +18,10 @@ namespace {
 
 constexpr int kBlock = 256;
 // Element arithmetic of the input tensor, as torch rounds it per op: fp16,
-// fp32 with an fp16 scale (the rotated path's x_rot), bf16, or plain fp32
-// K/V (fp32 scale).
-enum { MODE_F16 = 0, MODE_F32 = 1, MODE_BF16 = 2, MODE_F32S = 3 };
+// bf16, or fp32 (the rotated path's x_rot, plain fp32 K/V) with the fp32
+// scale stored as fp16 (MODE_F32), as fp32 (MODE_F32S) or as bf16
+// (MODE_F32B): one rounding of absmax / qmax to the stored type.
+enum { MODE_F16 = 0, MODE_F32 = 1, MODE_BF16 = 2, MODE_F32S = 3, MODE_F32B = 4 };
 struct Bf16 {  // bf16 elements (raw bits)
   uint16_t bits;
 };
@@ -97,6 +98,8 @@ __device__ __forceinline__ void sym_params(float absmax, float& inv, typename Sc
     inv = r * static_cast<float>(QMAX);
     if constexpr (MODE == MODE_F32S)
       scale_h = a / static_cast<float>(QMAX);
+    else if constexpr (MODE == MODE_F32B)
+      scale_h = f2bf(a / static_cast<float>(QMAX));
     else
       scale_h = f2h(a / static_cast<float>(QMAX));
   }
@@ -822,29 +825,58 @@ FADE_API int fade_quant_rotated_workspace_bytes(int64_t B, int64_t H, int64_t S,
   return fade_quant_k_int4_workspace_bytes(B, H, S, D, bytes);
 }
 
+namespace fade {
+namespace {
+template <int MODE>
+int quant_rotated(const char* fn, const float* x_rot, int64_t B, int64_t H, int64_t S, int64_t D, int32_t bits,
+                  int32_t axis, void* packed, void* scale, void* workspace, int64_t workspace_bytes,
+                  hipStream_t st) {
+  const int64_t sb = H * S * D, sh = S * D, ss = D;
+  if (axis == FADE_AXIS_TOKEN) {
+    switch (bits) {
+      case 4: return launch_token<float, MODE, 4>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale, st);
+      case 3: return launch_token<float, MODE, 3>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale, st);
+      case 2: return launch_token<float, MODE, 2>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale, st);
+      default: return einval("%s: bits must be 2, 3 or 4, got %d", fn, bits);
+    }
+  }
+  if (axis != FADE_AXIS_CHANNEL) return einval("%s: bad axis %d", fn, axis);
+  switch (bits) {
+    case 4: return launch_channel<float, MODE, 4>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale, workspace, workspace_bytes, st);
+    case 3: return launch_channel<float, MODE, 3>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale, workspace, workspace_bytes, st);
+    case 2: return launch_channel<float, MODE, 2>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale, workspace, workspace_bytes, st);
+    default: return einval("%s: bits must be 2, 3 or 4, got %d", fn, bits);
+  }
+}
+}  // namespace
+}  // namespace fade
+
 FADE_API int fade_quant_rotated(const float* x_rot, int64_t B, int64_t H, int64_t S, int64_t D,
                                 int32_t bits, int32_t axis, void* packed, void* scale_f16,
                                 void* workspace, int64_t workspace_bytes, void* stream) {
   int rc = check_dims("fade_quant_rotated", B, H, S, D);
   if (rc) return rc;
   if (!aligned(x_rot, 16)) return einval("fade_quant_rotated: input must be 16-byte aligned");
-  const int64_t sb = H * S * D, sh = S * D, ss = D;
+  return quant_rotated<MODE_F32>("fade_quant_rotated", x_rot, B, H, S, D, bits, axis, packed, scale_f16, workspace,
+                                 workspace_bytes, as_stream(stream));
+}
+
+FADE_API int fade_quant_rotated_dtype(const float* x_rot, int64_t B, int64_t H, int64_t S, int64_t D, int32_t bits,
+                                      int32_t axis, void* packed, void* scale, int32_t scale_dtype, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
+  const char* fn = "fade_quant_rotated_dtype";
+  int rc = check_dims(fn, B, H, S, D);
+  if (rc) return rc;
+  if (!aligned(x_rot, 16)) return einval("%s: input must be 16-byte aligned", fn);
   hipStream_t st = as_stream(stream);
-  const char* fn = "fade_quant_rotated";
-  if (axis == FADE_AXIS_TOKEN) {
-    switch (bits) {
-      case 4: return launch_token<float, MODE_F32, 4>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale_f16, st);
-      case 3: return launch_token<float, MODE_F32, 3>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale_f16, st);
-      case 2: return launch_token<float, MODE_F32, 2>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale_f16, st);
-      default: return einval("fade_quant_rotated: bits must be 2, 3 or 4, got %d", bits);
-    }
-  }
-  if (axis != FADE_AXIS_CHANNEL) return einval("fade_quant_rotated: bad axis %d", axis);
-  switch (bits) {
-    case 4: return launch_channel<float, MODE_F32, 4>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale_f16, workspace, workspace_bytes, st);
-    case 3: return launch_channel<float, MODE_F32, 3>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale_f16, workspace, workspace_bytes, st);
-    case 2: return launch_channel<float, MODE_F32, 2>(fn, x_rot, B, H, S, D, sb, sh, ss, packed, scale_f16, workspace, workspace_bytes, st);
-    default: return einval("fade_quant_rotated: bits must be 2, 3 or 4, got %d", bits);
+  switch (scale_dtype) {
+    case FADE_DTYPE_F16:
+      return quant_rotated<MODE_F32>(fn, x_rot, B, H, S, D, bits, axis, packed, scale, workspace, workspace_bytes, st);
+    case FADE_DTYPE_BF16:
+      return quant_rotated<MODE_F32B>(fn, x_rot, B, H, S, D, bits, axis, packed, scale, workspace, workspace_bytes, st);
+    case FADE_DTYPE_F32:
+      return quant_rotated<MODE_F32S>(fn, x_rot, B, H, S, D, bits, axis, packed, scale, workspace, workspace_bytes, st);
+    default: return einval("%s: unknown scale dtype %d", fn, scale_dtype);
   }
 }
 

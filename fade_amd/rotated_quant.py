@@ -6,8 +6,10 @@ R split into fp16 hi/lo parts (fp32-GEMM accuracy) and quantizes it in place
 (fp32 absmax, ``inv = reciprocal(absmax) * qmax``, round-half-even, clamp,
 bit-pack); x_rot never reaches HBM.  Other shapes and dtypes take the two-step
 path: an fp32 GEMM through torch, then ``fade_quant_rotated``, which is
-bit-exact given ``x_rot`` (``quant_rotated_given``).  Dequantize is
-``fp16(code * scale)`` in ``fade_dequant_sym`` followed by the fp32 ``@ R``
+bit-exact given ``x_rot`` (``quant_rotated_given``); bfloat16 and float32
+inputs get their scale in their own dtype (one rounding of the fp32
+``absmax / qmax``, as the reference's ``scale.to(k.dtype)``).  Dequantize is
+``dtype(code * scale)`` in ``fade_dequant_sym`` followed by the fp32 ``@ R``
 GEMM.
 """
 
@@ -49,12 +51,12 @@ def _rotate(x: Tensor, R: Tensor) -> Tensor:
     return (x.float() @ R.to(x.device, dtype=torch.float32).T).contiguous()
 
 
-def _alloc_out(shape, bits: int, axis: int, device):
+def _alloc_out(shape, bits: int, axis: int, device, scale_dtype=torch.float16):
     B, H, S, D = shape
     row = D if bits == 3 else D * bits // 8
     packed = torch.empty(B, H, S, row, dtype=torch.int8 if bits == 3 else torch.uint8, device=device)
     scale_shape = (B, H, 1, D) if axis == _lib.AXIS_CHANNEL else (B, H, S, 1)
-    scale = torch.empty(scale_shape, dtype=torch.float16, device=device)
+    scale = torch.empty(scale_shape, dtype=scale_dtype, device=device)
     return packed, scale
 
 
@@ -66,23 +68,33 @@ def _check(x: Tensor, bits: int, op: str) -> None:
     _lib.require_gpu(x, op=op)
 
 
-def quant_rotated_given(x_rot: Tensor, bits: int, axis: int, op: str = "quant_rotated_given"):
+def quant_rotated_given(
+    x_rot: Tensor, bits: int, axis: int, op: str = "quant_rotated_given", scale_dtype: torch.dtype = torch.float16
+):
     """Quantize an already-rotated fp32 tensor [B, H, S, D] (fade/rotated_quant.py:121-131 with
     ``axis=AXIS_CHANNEL``, 163-173 with ``AXIS_TOKEN``); bit-exact with the reference given x_rot.
-    Returns (packed, fp16 scale)."""
+    Returns (packed, scale of ``scale_dtype``: float16, bfloat16 or float32)."""
     _check(x_rot, bits, op)
+    if scale_dtype not in _lib.DTYPE_CODES:
+        raise ValueError(f"{op}: scale dtype must be float16, bfloat16 or float32, got {scale_dtype}")
     x_rot = x_rot.float().contiguous()
     B, H, S, D = x_rot.shape
-    packed, scale = _alloc_out(x_rot.shape, bits, axis, x_rot.device)
+    packed, scale = _alloc_out(x_rot.shape, bits, axis, x_rot.device, scale_dtype)
     if x_rot.numel() == 0:
         return packed, scale
     nb = ctypes.c_int64(0)
     _lib.check(_lib.load().fade_quant_rotated_workspace_bytes(B, H, S, D, axis, nb), op)
     ws = _lib.scratch(nb.value, x_rot.device)  # column partials: written in full before they are read
-    _lib.call(
-        "fade_quant_rotated", x_rot.data_ptr(), B, H, S, D, bits, axis, packed.data_ptr(),
-        scale.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(x_rot),
-    )
+    if scale_dtype == torch.float16:
+        _lib.call(
+            "fade_quant_rotated", x_rot.data_ptr(), B, H, S, D, bits, axis, packed.data_ptr(),
+            scale.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(x_rot),
+        )
+    else:
+        _lib.call(
+            "fade_quant_rotated_dtype", x_rot.data_ptr(), B, H, S, D, bits, axis, packed.data_ptr(),
+            scale.data_ptr(), _lib.DTYPE_CODES[scale_dtype], ws.data_ptr(), ws.numel(), _lib.stream_of(x_rot),
+        )
     return packed, scale
 
 
@@ -118,9 +130,9 @@ def _quant_rotated(x: Tensor, R: Tensor, bits: int, axis: int, op: str):
     if tuple(R.shape) != (x.shape[-1], x.shape[-1]):
         raise ValueError(f"{op}: R must be [{x.shape[-1]}, {x.shape[-1]}], got {tuple(R.shape)}")
     if _fused_ok(x):
-        packed, scale = _rotate_quant_fused(x, R, bits, axis, op)
-    else:
-        packed, scale = quant_rotated_given(_rotate(x, R), bits, axis, op)
+        return _rotate_quant_fused(x, R, bits, axis, op)
+    sdt = x.dtype if x.dtype in _lib.DTYPE_CODES else torch.float32
+    packed, scale = quant_rotated_given(_rotate(x, R), bits, axis, op, scale_dtype=sdt)
     return packed, scale.to(x.dtype)
 
 
@@ -134,13 +146,15 @@ def rotated_quant_v(v: Tensor, R: Tensor, bits: int = 4) -> tuple[Tensor, Tensor
     return _quant_rotated(v, R, bits, _lib.AXIS_TOKEN, "rotated_quant_v")
 
 
-def rotated_dequant_rot(packed: Tensor, scale: Tensor, bits: int) -> Tensor:
-    """fp16(code * scale) in the rotated basis (fade/rotated_quant.py:142-143)."""
-    return dequant_sym(packed, scale.to(torch.float16), bits)
+def rotated_dequant_rot(packed: Tensor, scale: Tensor, bits: int, dtype: torch.dtype = torch.float16) -> Tensor:
+    """``code.to(dtype) * scale.to(dtype)`` in the rotated basis (fade/rotated_quant.py:142-143)."""
+    return dequant_sym(packed, scale, bits, dtype)
 
 
 def _rotated_dequant(packed, scale, R, bits, dtype):
-    x_rot = rotated_dequant_rot(packed, scale, bits)
+    # the rotation back runs as an fp32 GEMM for every dtype (the reference's
+    # CPU path; on CUDA it multiplies bf16 in bf16)
+    x_rot = rotated_dequant_rot(packed, scale, bits, dtype if dtype in _lib.DTYPE_CODES else torch.float32)
     return (x_rot.float() @ R.to(x_rot.device, dtype=torch.float32)).to(dtype)
 
 

@@ -127,6 +127,13 @@ int fade_quant_rotated_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t 
 int fade_quant_rotated(const float* x_rot, int64_t B, int64_t H, int64_t S, int64_t D,
                        int32_t bits, int32_t axis, void* packed, void* scale_f16, void* workspace,
                        int64_t workspace_bytes, void* stream);
+/* fade_quant_rotated with the scale stored as scale_dtype (FADE_DTYPE_*): the
+ * reference computes absmax / qmax in fp32 and casts it to the input's dtype
+ * (fade/rotated_quant.py:129-131, 171-173), one rounding; for bfloat16 and
+ * float32 K/V. */
+int fade_quant_rotated_dtype(const float* x_rot, int64_t B, int64_t H, int64_t S, int64_t D, int32_t bits,
+                             int32_t axis, void* packed, void* scale, int32_t scale_dtype, void* workspace,
+                             int64_t workspace_bytes, void* stream);
 
 /* Fused rotate + quantize (fade/rotated_quant.py:106-131 K, 148-173 V) for
  * fp16 x [B,H,S,128] (element strides sb/sh/ss, rows 16-byte aligned) and

@@ -275,12 +275,14 @@ def random_orthogonal_from_gaussian(m: np.ndarray) -> np.ndarray:
     return q.astype(F32)
 
 
-def rotated_quant_codes(x_rot: np.ndarray, bits: int, axis: str):
+def rotated_quant_codes(x_rot: np.ndarray, bits: int, axis: str, scale_dtype: str = "f16"):
     """fade/rotated_quant.py:121-131 (K, ``axis='channel'``) / 163-173 (V, ``axis='token'``).
 
     Input is the already-rotated fp32 tensor ``x.float() @ R.T``.  Returns
-    (packed, scale_fp16).  ``qmax / absmax`` is ``reciprocal * qmax`` (two
-    fp32 roundings); ``absmax / qmax`` is an IEEE fp32 division.
+    (packed, scale) with the scale cast to the input's dtype ``scale_dtype``
+    ("f16" | "bf16" | "f32"; ``scale.to(k.dtype)``).  ``qmax / absmax`` is
+    ``reciprocal * qmax`` (two fp32 roundings); ``absmax / qmax`` is an IEEE
+    fp32 division.
     """
     qmin, qmax = BIT_PARAMS[bits]
     x_rot = np.asarray(x_rot, dtype=F32)
@@ -289,12 +291,14 @@ def rotated_quant_codes(x_rot: np.ndarray, bits: int, axis: str):
     inv = ((F32(1.0) / absmax).astype(F32) * F32(qmax)).astype(F32)
     scale = (absmax / F32(qmax)).astype(F32)
     q = _rne_clamp((x_rot * inv).astype(F32), qmin, qmax)
-    return pack_bits(q, bits), scale.astype(F16)
+    return pack_bits(q, bits), from_f32(scale, scale_dtype)
 
 
-def rotated_dequant_rot(packed: np.ndarray, scale: np.ndarray, bits: int) -> np.ndarray:
-    """fade/rotated_quant.py:142-143 / 184-185: fp16(q * scale) in the rotated basis."""
-    return dequant(unpack_bits(packed, bits), scale)
+def rotated_dequant_rot(packed: np.ndarray, scale: np.ndarray, bits: int, dtype: str = "f16") -> np.ndarray:
+    """fade/rotated_quant.py:142-143 / 184-185: ``q.to(dtype) * scale.to(dtype)`` in the rotated basis."""
+    if dtype == "f16":
+        return dequant(unpack_bits(packed, bits), scale)
+    return from_f32(unpack_bits(packed, bits).astype(F32) * to_f32(scale, dtype), dtype)
 
 
 def rotated_dequant(packed, scale, R, bits):

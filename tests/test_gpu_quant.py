@@ -235,6 +235,16 @@ def test_rotated_quant_bit_exact_given_rotation(dev, bits):
     assert np.array_equal(_u16(vs.cpu().numpy()), _u16(ovs))
     deq = frq.rotated_dequant_rot(kp, ks, bits).cpu().numpy()
     assert np.array_equal(_u16(deq), _u16(oq.rotated_dequant_rot(okp, oks, bits)))
+    # bfloat16 / float32 K/V: scales emitted in their dtype, dequantized in it
+    for dt in ("bf16", "f32"):
+        for axis, ax in ((_lib.AXIS_CHANNEL, "channel"), (_lib.AXIS_TOKEN, "token")):
+            p_, s_ = frq.quant_rotated_given(x_rot, bits, axis, scale_dtype=_TDT[dt])
+            op_, os_ = oq.rotated_quant_codes(xr, bits, ax, dt)
+            assert s_.dtype == _TDT[dt]
+            assert np.array_equal(p_.cpu().numpy().view(np.uint8), op_.view(np.uint8))
+            _same(_host_typed(s_, dt), os_, dt)
+            d_ = frq.rotated_dequant_rot(p_, s_, bits, _TDT[dt])
+            _same(_host_typed(d_, dt), oq.rotated_dequant_rot(op_, os_, bits, dt), dt)
 
 
 def _check_fused_rotated(x16, R, bits, axis, packed, scale):

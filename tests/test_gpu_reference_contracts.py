@@ -1,5 +1,5 @@
 """The reference's own contract tests for this path, run against the HIP build:
-fade tests/test_quant.py, tests/test_cache.py, tests/test_cache_batched.py,
+fade tests/test_quant.py, tests/test_backends.py, tests/test_cache.py, tests/test_cache_batched.py,
 tests/test_attn_impl.py and tests/test_perf.py (file:line on each test).  Same
 calls, shapes and bounds, with one difference: the build's caches and kernels are
 float16 on the GPU (the reference tests use float32 on the CPU), so every tensor
@@ -121,6 +121,51 @@ def test_pad_to_group(dev):  # :144-154
     y = _randn(B, H, 128, D, dev=dev)
     padded2, actual2 = pad_to_group(y, 64)
     assert actual2 == 128 and padded2.shape[-2] == 128
+
+
+# ------------------------------------------------------------- tests/test_backends.py
+def test_int4_backend_round_trip(dev):  # :19-38 (float32 K/V, as the reference's DTYPE)
+    from fade_amd.backends import SymmetricINT4Backend
+
+    backend = SymmetricINT4Backend()
+    gen = torch.Generator().manual_seed(19)
+    k = torch.randn(1, 2, 16, 64, generator=gen).to(dev)
+    v = torch.randn(1, 2, 16, 64, generator=gen).to(dev)
+    ck, cv = backend.compress_k(k), backend.compress_v(v)
+    assert "packed" in ck and "scale" in ck and "packed" in cv and "scale" in cv
+    k_hat = backend.decompress_k(ck, dtype=torch.float32)
+    v_hat = backend.decompress_v(cv, dtype=torch.float32)
+    assert k_hat.shape == k.shape and v_hat.shape == v.shape
+    assert ((k - k_hat).abs().mean() / k.abs().mean()).item() < 0.15
+    assert ((v - v_hat).abs().mean() / v.abs().mean()).item() < 0.15
+
+
+def test_rotated_backend_round_trip_float32_and_bf16(dev):  # no reference test: the same bar for the rotated backend
+    from fade_amd.backends import get_backend
+
+    be = get_backend("rotated", head_dim=64, bits=4)
+    for dtype in (torch.float32, torch.bfloat16):
+        k = torch.randn(1, 2, 16, 64, generator=torch.Generator().manual_seed(7)).to(dtype).to(dev)
+        ck = be.compress_k(k)
+        assert ck["scale"].dtype == dtype
+        k_hat = be.decompress_k(ck, dtype=dtype)
+        assert k_hat.dtype == dtype and torch.isfinite(k_hat).all()
+        assert ((k.float() - k_hat.float()).abs().mean() / k.float().abs().mean()).item() < 0.15
+
+
+def test_backend_registry_and_cache_field(dev):  # :41-52, :55-63, :87-100
+    from fade_amd.backends import SymmetricINT4Backend, get_backend
+    from fade_amd.config import FadeConfig
+
+    assert SymmetricINT4Backend().name == "symmetric_int4"
+    assert isinstance(get_backend("int4"), SymmetricINT4Backend)
+    with pytest.raises(ValueError, match="Unknown"):
+        get_backend("nonexistent")
+    with pytest.raises(ImportError):  # turboquant-kv is not installed: the reference's test skips
+        get_backend("turbo", head_dim=64, bits=4).compress_k(torch.zeros(1, 2, 16, 64, device=dev))
+    c = FadeConfig.safe()
+    assert c.quant_backend == "int4" and "quant_backend" in c.to_cache_kwargs()
+    assert TieredKVCache(head_dim=64, quant_backend="int4")._quant_backend.name == "symmetric_int4"
 
 
 # ---------------------------------------------------------------- tests/test_cache.py

@@ -248,6 +248,17 @@ def test_rotated_quantizer_matches_torch_fp32_ops(bits, axis):
     packed, scale = oq.rotated_quant_codes(xr, bits, axis)
     assert np.array_equal(oq.unpack_bits(packed, bits), qt.numpy())
     assert np.array_equal(scale.view(np.uint16), (absmax / qmax).to(torch.float16).numpy().view(np.uint16))
+    # bfloat16 / float32 K and V: the same fp32 scale cast to their dtype
+    _, sb = oq.rotated_quant_codes(xr, bits, axis, "bf16")
+    assert np.array_equal(sb, _bits_bf16((absmax / qmax).to(torch.bfloat16)))
+    _, sf = oq.rotated_quant_codes(xr, bits, axis, "f32")
+    assert np.array_equal(sf.view(np.uint32), (absmax / qmax).numpy().view(np.uint32))
+    for dt, tdt in (("bf16", torch.bfloat16), ("f32", torch.float32)):
+        s_dt = sb if dt == "bf16" else sf
+        st = _t_bf16(s_dt) if dt == "bf16" else torch.from_numpy(s_dt)
+        ref = qt.to(tdt) * st
+        got = oq.rotated_dequant_rot(packed, s_dt, bits, dt)
+        assert np.array_equal(got, _bits_bf16(ref) if dt == "bf16" else ref.numpy())
 
 
 def test_rotation_fixture_is_orthogonal_and_matches_torch_qr():
