@@ -1476,8 +1476,9 @@ class TieredKVCache(DynamicCache):
                 mid = MiddleTier("int4", st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs)
             else:  # the ragged kernel needs a middle format: one zero row no row reads (lens 0)
                 B, H = int(q.shape[0]), int((st.fp16_k if st.fp16_k is not None else st.sink_k).shape[1])
-                z8 = torch.zeros(B, H, 1, 64, dtype=torch.uint8, device=q.device)
-                mid = MiddleTier("int4", z8, z8.clone(), torch.zeros(B, H, 1, 128, dtype=torch.float16, device=q.device),
+                D = int(q.shape[-1])
+                z8 = torch.zeros(B, H, 1, D // 2, dtype=torch.uint8, device=q.device)
+                mid = MiddleTier("int4", z8, z8.clone(), torch.zeros(B, H, 1, D, dtype=torch.float16, device=q.device),
                                  torch.zeros(B, H, 1, 1, dtype=torch.float16, device=q.device))
             sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
             recent = None if st.fp16_k is None or st.fp16_k.shape[-2] == 0 else (st.fp16_k, st.fp16_v)
@@ -1512,9 +1513,12 @@ class TieredKVCache(DynamicCache):
         elif st.backend_k is not None:
             be = self._quant_backend
             bk, bv = st.backend_k, st.backend_v
-            if isinstance(be, RotatedINT4Backend):
-                if be.bits == 3:
-                    raise RuntimeError("decode_attention: 3-bit rotated codes are not read by the fused kernel")
+            if isinstance(be, RotatedINT4Backend) and (be.bits == 3 or int(q.shape[-1]) != 128):
+                # the in-kernel rotation is the INT4 kernel's (4- and 2-bit codes, head_dim 128);
+                # otherwise the middle is read through its fp16 dequantization, kept between calls
+                mk, mv = self._mid_fp16(st)
+                mid = MiddleTier("fp16", mk, mv)
+            elif isinstance(be, RotatedINT4Backend):
                 # the kernel scores the middle with q R^T and un-rotates its part of the output
                 rotation = be._get_R(q.device)
                 mid = MiddleTier(

@@ -7,6 +7,7 @@
 // kv head, batch row) serves the whole GQA group of Hq/Hkv query heads, so
 // each KV byte is read once.  Each workgroup writes an unnormalized partial
 // (m, l, acc[D]) in the log2 domain; decode_combine_kernel merges the splits.
+// Head dims 32, 64, 128 and 256 (the matrix-core kernels take 128 only).
 //
 // This file holds the portable VALU kernel (any middle format) and the
 // combine pass.  decode_mfma.hip holds the matrix-core kernel for the
@@ -22,28 +23,31 @@ namespace {
 constexpr int kTile = 64;
 constexpr int kThreads = 256;
 
-// 32 dequantized K values of token t, channels [32*quarter, 32*quarter+32).
-__device__ void load_k32(const Params& p, int64_t b, int64_t kvh, int64_t t, int quarter,
-                         const float* ks_s, float* out) {
-  const int d0 = 32 * quarter;
+// D/4 dequantized K values of token t of a row whose sink and middle tiers
+// hold ns and nm tokens, channels [D/4*quarter, D/4*(quarter+1)).
+template <int D>
+__device__ void load_kq(const Params& p, int64_t b, int64_t kvh, int64_t t, int64_t ns, int64_t nm, int quarter,
+                        const float* ks_s, float* out) {
+  constexpr int CQ = D / 4;
+  const int d0 = CQ * quarter;
   const Fp16Tier* seg = nullptr;
   int64_t r = t;
-  if (t < p.sink.len) {
+  if (t < ns) {
     seg = &p.sink;
-  } else if (t < p.sink.len + p.mid.len) {
-    const int64_t m = t - p.sink.len;
+  } else if (t < ns + nm) {
+    const int64_t m = t - ns;
     const int64_t row = (b * p.Hkv + kvh) * p.mid.len + m;
     switch (p.mid.fmt) {
       case FADE_MID_FP16: {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(p.mid.k_codes) + row * kD + d0;
-        for (int j = 0; j < 32; ++j) out[j] = h2f(src[j]);
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(p.mid.k_codes) + row * D + d0;
+        for (int j = 0; j < CQ; ++j) out[j] = h2f(src[j]);
         return;
       }
       case FADE_MID_SYM:
       case FADE_MID_K4V2G: {
         const int bits = p.mid.fmt == FADE_MID_SYM ? p.mid.k_bits : 4;
-        const uint8_t* src = p.mid.k_codes + row * (kD * bits / 8);
-        for (int j = 0; j < 32; ++j) {
+        const uint8_t* src = p.mid.k_codes + row * (D * bits / 8);
+        for (int j = 0; j < CQ; ++j) {
           const int d = d0 + j;
           out[j] = round_f16(static_cast<float>(sym_code_at(src, d, bits)) * ks_s[d]);
         }
@@ -51,11 +55,11 @@ __device__ void load_k32(const Params& p, int64_t b, int64_t kvh, int64_t t, int
       }
       default: {  // FADE_MID_ASYM
         const int bits = p.mid.k_bits, g = p.mid.group;
-        const uint8_t* src = p.mid.k_codes + row * (kD * bits / 8);
-        for (int j = 0; j < 32; ++j) {
+        const uint8_t* src = p.mid.k_codes + row * (D * bits / 8);
+        for (int j = 0; j < CQ; ++j) {
           const int d = d0 + j;
-          const float s = h2f(p.mid.k_scale[row * (kD / g) + d / g]);
-          const float z = h2f(p.mid.k_zero[row * (kD / g) + d / g]);
+          const float s = h2f(p.mid.k_scale[row * (D / g) + d / g]);
+          const float z = h2f(p.mid.k_zero[row * (D / g) + d / g]);
           out[j] = round_f16(static_cast<float>(asym_code_at(src, d, bits)) * s + z);
         }
         return;
@@ -63,96 +67,116 @@ __device__ void load_k32(const Params& p, int64_t b, int64_t kvh, int64_t t, int
     }
   } else {
     seg = &p.recent;
-    r = t - p.sink.len - p.mid.len;
+    r = t - ns - nm;
   }
   const uint16_t* src = seg->k + b * seg->k_sb + kvh * seg->k_sh + r * seg->k_ss + d0;
-  for (int j = 0; j < 32; ++j) out[j] = h2f(src[j]);
+  for (int j = 0; j < CQ; ++j) out[j] = h2f(src[j]);
 }
 
-// Dequantized V channels (2*dp, 2*dp+1) of token t.
-__device__ void load_v2(const Params& p, int64_t b, int64_t kvh, int64_t t, int dp, float& v0,
-                        float& v1) {
-  const int d = 2 * dp;
+// Dequantized V channels d0 .. d0 + N - 1 of token t (tiers as in load_kq).
+template <int D, int N>
+__device__ void load_vn(const Params& p, int64_t b, int64_t kvh, int64_t t, int64_t ns, int64_t nm, int d0,
+                        float* v) {
   const Fp16Tier* seg = nullptr;
   int64_t r = t;
-  if (t < p.sink.len) {
+  if (t < ns) {
     seg = &p.sink;
-  } else if (t < p.sink.len + p.mid.len) {
-    const int64_t m = t - p.sink.len;
+  } else if (t < ns + nm) {
+    const int64_t m = t - ns;
     const int64_t bkv = b * p.Hkv + kvh;
     const int64_t row = bkv * p.mid.len + m;
     switch (p.mid.fmt) {
       case FADE_MID_FP16: {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(p.mid.v_codes) + row * kD + d;
-        v0 = h2f(src[0]);
-        v1 = h2f(src[1]);
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(p.mid.v_codes) + row * D + d0;
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = h2f(src[j]);
         return;
       }
       case FADE_MID_SYM: {
         const int bits = p.mid.v_bits;
-        const uint8_t* src = p.mid.v_codes + row * (kD * bits / 8);
+        const uint8_t* src = p.mid.v_codes + row * (D * bits / 8);
         const float s = h2f(p.mid.v_scale[row]);
-        v0 = round_f16(static_cast<float>(sym_code_at(src, d, bits)) * s);
-        v1 = round_f16(static_cast<float>(sym_code_at(src, d + 1, bits)) * s);
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = round_f16(static_cast<float>(sym_code_at(src, d0 + j, bits)) * s);
         return;
       }
       case FADE_MID_K4V2G: {
-        const int8_t* src = reinterpret_cast<const int8_t*>(p.mid.v_codes) + (bkv * p.mid.v_rows + m) * kD + d;
+        const int8_t* src = reinterpret_cast<const int8_t*>(p.mid.v_codes) + (bkv * p.mid.v_rows + m) * D + d0;
         const int64_t G = p.mid.v_rows / p.mid.group;
-        const uint16_t* sc = p.mid.v_scale + (bkv * G + m / p.mid.group) * kD + d;
-        v0 = round_f16(static_cast<float>(src[0]) * h2f(sc[0]));
-        v1 = round_f16(static_cast<float>(src[1]) * h2f(sc[1]));
+        const uint16_t* sc = p.mid.v_scale + (bkv * G + m / p.mid.group) * D + d0;
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = round_f16(static_cast<float>(src[j]) * h2f(sc[j]));
         return;
       }
       default: {  // FADE_MID_ASYM
         const int bits = p.mid.v_bits, g = p.mid.group;
-        const uint8_t* src = p.mid.v_codes + row * (kD * bits / 8);
-        const float s = h2f(p.mid.v_scale[row * (kD / g) + d / g]);
-        const float z = h2f(p.mid.v_zero[row * (kD / g) + d / g]);
-        v0 = round_f16(static_cast<float>(asym_code_at(src, d, bits)) * s + z);
-        v1 = round_f16(static_cast<float>(asym_code_at(src, d + 1, bits)) * s + z);
+        const uint8_t* src = p.mid.v_codes + row * (D * bits / 8);
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+          const int d = d0 + j;
+          const float s = h2f(p.mid.v_scale[row * (D / g) + d / g]);
+          const float z = h2f(p.mid.v_zero[row * (D / g) + d / g]);
+          v[j] = round_f16(static_cast<float>(asym_code_at(src, d, bits)) * s + z);
+        }
         return;
       }
     }
   } else {
     seg = &p.recent;
-    r = t - p.sink.len - p.mid.len;
+    r = t - ns - nm;
   }
-  const uint16_t* src = seg->v + b * seg->v_sb + kvh * seg->v_sh + r * seg->v_ss + d;
-  v0 = h2f(src[0]);
-  v1 = h2f(src[1]);
+  const uint16_t* src = seg->v + b * seg->v_sb + kvh * seg->v_sh + r * seg->v_ss + d0;
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] = h2f(src[j]);
 }
 
-// Portable kernel.  Tile of 64 tokens:
-//   A) thread (quarter = wave, token = lane) dots its 32 channels with all heads;
+// Portable kernel, head_dim D (32, 64, 128 or 256).  Tile of 64 tokens:
+//   A) thread (quarter = wave, token = lane) dots its D/4 channels with all heads;
 //   B) wave h finishes head h's scores for the 64 tokens, online softmax;
-//   C) thread (heads wave / wave+4, channels 2*lane..+1) accumulates P*V.
+//   C) thread (heads wave / wave+4, channels CPL*lane .. + CPL-1) accumulates P*V.
+template <int D>
 __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
+  constexpr int CQ = D / 4;                   // channels per wave in A
+  constexpr int CPL = D >= 64 ? D / 64 : 1;   // channels per lane in C
+  constexpr int LANES = D / CPL;              // lanes holding channels in C
   const int split = blockIdx.x;
   const int64_t kvh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = p.G;
 
-  __shared__ float q_s[kMaxG][kD];
-  __shared__ float ks_s[kD];
+  __shared__ float q_s[kMaxG][D];
+  __shared__ float ks_s[D];
   __shared__ float sc_s[4][kMaxG][kTile];
   __shared__ float p_s[kMaxG][kTile];
   __shared__ float alpha_s[kMaxG];
 
-  for (int i = tid; i < G * kD; i += kThreads) {
-    const int h = i / kD, d = i % kD;
+  for (int i = tid; i < G * D; i += kThreads) {
+    const int h = i / D, d = i % D;
     q_s[h][d] = h2f(p.q[b * p.q_sb + (kvh * G + h) * p.q_sh + d]);
   }
   if (p.mid.fmt == FADE_MID_SYM || p.mid.fmt == FADE_MID_K4V2G)
-    for (int d = tid; d < kD; d += kThreads) ks_s[d] = h2f(p.mid.k_scale[(b * p.Hkv + kvh) * kD + d]);
+    for (int d = tid; d < D; d += kThreads) ks_s[d] = h2f(p.mid.k_scale[(b * p.Hkv + kvh) * D + d]);
   __syncthreads();
 
+  // the row's tier lengths: the tiers' own, or per row (lens, clamped to the padded tiers)
+  int64_t ns = p.sink.len, nm = p.mid.len, nr = p.recent.len;
+  if (p.lens != nullptr) {
+    auto clampl = [](int64_t x, int64_t cap) { return x < 0 ? 0 : (x > cap ? cap : x); };
+    ns = clampl(p.lens[3 * b], p.sink.len);
+    nm = clampl(p.lens[3 * b + 1], p.mid.len);
+    nr = clampl(p.lens[3 * b + 2], p.recent.len);
+  }
+  const int64_t total = ns + nm + nr;
   const int64_t t_begin = static_cast<int64_t>(split) * p.tokens_per_split;
-  const int64_t t_end = t_begin + p.tokens_per_split < p.total ? t_begin + p.tokens_per_split : p.total;
+  const int64_t t_end = t_begin + p.tokens_per_split < total ? t_begin + p.tokens_per_split : total;
 
   float m_run[2] = {-INFINITY, -INFINITY};
   float l_lane[2] = {0.0f, 0.0f};
-  float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+  float acc[2][CPL];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) acc[hh][c] = 0.0f;
 
   for (int64_t ts = t_begin; ts < t_end; ts += kTile) {
     {  // A
@@ -161,12 +185,12 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
 #pragma unroll
       for (int h = 0; h < kMaxG; ++h) part[h] = 0.0f;
       if (t < t_end) {
-        float kv[32];
-        load_k32(p, b, kvh, t, wave, ks_s, kv);
+        float kv[CQ];
+        load_kq<D>(p, b, kvh, t, ns, nm, wave, ks_s, kv);
         for (int h = 0; h < G; ++h) {
           float s = 0.0f;
 #pragma unroll
-          for (int j = 0; j < 32; ++j) s += q_s[h][32 * wave + j] * kv[j];
+          for (int j = 0; j < CQ; ++j) s += q_s[h][CQ * wave + j] * kv[j];
           part[h] = s;
         }
       }
@@ -194,26 +218,25 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
       }
     }
     __syncthreads();
-    {  // C
+    if (lane < LANES) {  // C
       const int nv = static_cast<int>(t_end - ts < kTile ? t_end - ts : kTile);
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int h = wave + 4 * hh;
-        if (h < G) {
-          acc[hh][0] *= alpha_s[h];
-          acc[hh][1] *= alpha_s[h];
-        }
+        if (h < G)
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) acc[hh][c] *= alpha_s[h];
       }
       for (int lt = 0; lt < nv; ++lt) {
-        float v0, v1;
-        load_v2(p, b, kvh, ts + lt, lane, v0, v1);
+        float v[CPL];
+        load_vn<D, CPL>(p, b, kvh, ts + lt, ns, nm, CPL * lane, v);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           const int h = wave + 4 * hh;
           if (h < G) {
             const float pp = p_s[h][lt];
-            acc[hh][0] += pp * v0;
-            acc[hh][1] += pp * v1;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) acc[hh][c] += pp * v[c];
           }
         }
       }
@@ -231,22 +254,24 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
         p.ws_ml[2 * idx] = m_run[hh];
         p.ws_ml[2 * idx + 1] = l;
       }
-      p.ws_acc[idx * kD + 2 * lane] = acc[hh][0];
-      p.ws_acc[idx * kD + 2 * lane + 1] = acc[hh][1];
+      if (lane < LANES)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) p.ws_acc[idx * D + CPL * lane + c] = acc[hh][c];
     }
   }
 }
 
 }  // namespace
 
-// Merge the n_splits partials of each (b, hq) into the fp16 output.
-__global__ __launch_bounds__(kD) void decode_combine_kernel(const float* __restrict__ ws_ml,
-                                                            const float* __restrict__ ws_acc,
-                                                            int n_splits, int64_t Hq,
-                                                            uint16_t* __restrict__ out,
-                                                            int64_t o_sb, int64_t o_sh) {
+// Merge the n_splits partials of each (b, hq) into the fp16 output; one
+// thread per channel (blockDim.x = head_dim D).
+__global__ __launch_bounds__(256) void decode_combine_kernel(const float* __restrict__ ws_ml,
+                                                             const float* __restrict__ ws_acc,
+                                                             int n_splits, int64_t Hq,
+                                                             uint16_t* __restrict__ out,
+                                                             int64_t o_sb, int64_t o_sh) {
   const int64_t bh = blockIdx.x;
-  const int d = threadIdx.x;
+  const int d = threadIdx.x, D = blockDim.x;
   const float* ml = ws_ml + bh * n_splits * 2;
   float M = -INFINITY;
   for (int s = 0; s < n_splits; ++s) M = fmaxf(M, ml[2 * s]);
@@ -257,7 +282,7 @@ __global__ __launch_bounds__(kD) void decode_combine_kernel(const float* __restr
       if (m == -INFINITY) continue;
       const float w = exp2f(m - M);
       L += ml[2 * s + 1] * w;
-      o += ws_acc[(bh * n_splits + s) * kD + d] * w;
+      o += ws_acc[(bh * n_splits + s) * D + d] * w;
     }
   }
   out[(bh / Hq) * o_sb + (bh % Hq) * o_sh + d] = f2h(o / L);
@@ -266,7 +291,13 @@ __global__ __launch_bounds__(kD) void decode_combine_kernel(const float* __restr
 int launch_valu(const Params& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv),
                   static_cast<unsigned>(p.B));
-  hipLaunchKernelGGL(decode_valu_kernel, grid, dim3(kThreads), 0, st, p);
+  switch (p.D) {
+    case 32: hipLaunchKernelGGL(decode_valu_kernel<32>, grid, dim3(kThreads), 0, st, p); break;
+    case 64: hipLaunchKernelGGL(decode_valu_kernel<64>, grid, dim3(kThreads), 0, st, p); break;
+    case 128: hipLaunchKernelGGL(decode_valu_kernel<128>, grid, dim3(kThreads), 0, st, p); break;
+    case 256: hipLaunchKernelGGL(decode_valu_kernel<256>, grid, dim3(kThreads), 0, st, p); break;
+    default: return einval("fade_tiered_decode_attn: head_dim must be 32, 64, 128 or 256, got %d", p.D);
+  }
   return check_launch("fade_tiered_decode_attn(valu)");
 }
 

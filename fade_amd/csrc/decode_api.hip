@@ -40,7 +40,7 @@ void plan_splits(const fade_decode_args* a, int tile, int64_t* n_splits, int64_t
 
 int64_t round256(int64_t x) { return ((x + 255) / 256) * 256; }
 
-// Workspace: [counters: B*Hkv*P u32][ml: rows*n*2 f32][acc: rows*n*kD f32], rows
+// Workspace: [counters: B*Hkv*P u32][ml: rows*n*2 f32][acc: rows*n*D f32], rows
 // covering both partial layouts (B*Hq per query head, or B*Hkv*4*P); P =
 // ceil((Hq/Hkv) / 4) head passes of the INT4 kernel.
 struct WsLayout {
@@ -53,13 +53,14 @@ WsLayout ws_layout(const fade_decode_args* a, int64_t n) {
   w.counters = 0;
   w.ml = round256(a->B * a->Hkv * P * 4);
   w.acc = w.ml + round256(rows * n * 2 * 4);
-  w.total = w.acc + rows * n * kD * 4;
+  w.total = w.acc + rows * n * a->D * 4;
   return w;
 }
 
 int validate(const fade_decode_args* a) {
   if (a == nullptr) return einval("fade_tiered_decode_attn: null args");
-  if (a->D != kD) return einval("fade_tiered_decode_attn: head_dim must be %d, got %lld", kD, (long long)a->D);
+  if (a->D != 32 && a->D != 64 && a->D != 128 && a->D != 256)
+    return einval("fade_tiered_decode_attn: head_dim must be 32, 64, 128 or 256, got %lld", (long long)a->D);
   if (a->B <= 0 || a->Hq <= 0 || a->Hkv <= 0)
     return einval("fade_tiered_decode_attn: B, Hq, Hkv must be positive");
   if (a->Hq % a->Hkv != 0)
@@ -136,6 +137,7 @@ Params to_params(const fade_decode_args* a) {
   p.Hq = a->Hq;
   p.Hkv = a->Hkv;
   p.G = static_cast<int>(a->Hq / a->Hkv);
+  p.D = static_cast<int>(a->D);
   p.q = static_cast<const uint16_t*>(a->q);
   p.q_sb = a->q_sb;
   p.q_sh = a->q_sh;
@@ -245,9 +247,11 @@ int run_plan(const fade_decode_args* a, Params& p, const Plan& pl, uint32_t* cou
   if (p.rot != nullptr && pl.k != Kern::kInt4)
     return einval("fade_tiered_decode_attn: a rotated middle tier needs the matrix-core INT4 kernel "
                   "(FADE_MID_SYM with 4- or 2-bit K and V, GQA <= 8)");
-  if ((a->lens != nullptr || a->mid.pages != nullptr) && pl.k != Kern::kInt4)
-    return einval("fade_tiered_decode_attn: per-row lengths and paged middle tiers need the matrix-core INT4 "
+  if (a->mid.pages != nullptr && pl.k != Kern::kInt4)
+    return einval("fade_tiered_decode_attn: paged middle tiers need the matrix-core INT4 "
                   "kernel (middle tier FADE_MID_SYM or FADE_MID_ASYM, GQA <= 8)");
+  if (a->lens != nullptr && pl.k == Kern::kMfma)
+    return einval("fade_tiered_decode_attn: per-row lengths need the INT4 kernel or the portable one (kernel 1)");
   if (pl.n > 65535) return einval("fade_tiered_decode_attn: too many splits");
   const WsLayout ws = ws_layout(a, pl.n);
   p.n_splits = static_cast<int>(pl.n);
@@ -266,7 +270,7 @@ int run_plan(const fade_decode_args* a, Params& p, const Plan& pl, uint32_t* cou
   int rc = pl.k == Kern::kMfma ? launch_mfma(p, st) : launch_valu(p, st);
   if (rc) return rc;
   const int64_t rows = a->B * a->Hq;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(static_cast<unsigned>(rows)), dim3(kD), 0, st, p.ws_ml,
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(static_cast<unsigned>(rows)), dim3(static_cast<unsigned>(p.D)), 0, st, p.ws_ml,
                      p.ws_acc, p.n_splits, a->Hq, static_cast<uint16_t*>(a->out), a->o_sb, a->o_sh);
   return check_launch("fade_tiered_decode_attn(combine)");
 }

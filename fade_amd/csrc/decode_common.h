@@ -6,7 +6,7 @@
 namespace fade {
 namespace decode {
 
-constexpr int kD = 128;   // head_dim of every attention kernel
+constexpr int kD = 128;   // head_dim of the matrix-core attention kernels (the portable one: 32..256)
 constexpr int kMaxG = 8;  // max query heads per kv head
 
 struct Fp16Tier {
@@ -37,6 +37,7 @@ constexpr int kPageSlots = 256;
 struct Params {
   int64_t B, Hq, Hkv;
   int G;
+  int D;  // head_dim: kD for the matrix-core kernels; 32, 64, 128 or 256 for the portable one
   const uint16_t* q;
   int64_t q_sb, q_sh;
   float scale_log2;  // sm_scale * log2(e): softmax runs in the exp2 domain
@@ -46,7 +47,7 @@ struct Params {
   int64_t tokens_per_split;  // multiple of the kernel tile
   int n_splits;
   float* ws_ml;   // [B][Hq][n_splits][2]  (m, l); INT4 kernel: [B*Hkv][n_splits][4][2]
-  float* ws_acc;  // [B][Hq][n_splits][kD] unnormalized output; INT4 kernel: [B*Hkv][n_splits][4][kD]
+  float* ws_acc;  // [B][Hq][n_splits][D] unnormalized output; INT4 kernel: [B*Hkv][n_splits][4][kD]
   // INT4 kernel only
   uint16_t* out;
   int64_t o_sb, o_sh;

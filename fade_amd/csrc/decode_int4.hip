@@ -1222,7 +1222,7 @@ bool int4_supports(const Params& p) {
   const MidTier& m = p.mid;
   // G = 5..8 runs as two head passes (the kv tiles are read once per pass);
   // measured faster than the general matrix-core kernel at most shapes
-  if (m.len <= 0 || p.G > 8) return false;
+  if (m.len <= 0 || p.G > 8 || p.D != kD) return false;
   const bool bits_ok = (m.k_bits == 4 || m.k_bits == 2) && (m.v_bits == 4 || m.v_bits == 2);
   if (m.fmt == FADE_MID_SYM) {
     if (!bits_ok) return false;

@@ -507,6 +507,7 @@ bool fp16_tier_ok(const Fp16Tier& t) {
 }  // namespace
 
 bool mfma_supports(const Params& p) {
+  if (p.D != kD) return false;
   if (!fp16_tier_ok(p.sink) || !fp16_tier_ok(p.recent)) return false;
   if (p.G > kMaxG) return false;
   if (reinterpret_cast<uintptr_t>(p.q) % 16 || p.q_sb % 8 || p.q_sh % 8) return false;

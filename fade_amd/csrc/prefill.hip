@@ -59,11 +59,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
-constexpr int kD = 128;
 constexpr int kThreads = 256;
 constexpr int kQB = 32;       // queries per workgroup
 constexpr int kKT = 64;       // keys per tile
-constexpr int kKPitch = 136;  // halves per K row in LDS (16-byte reads of 16 rows: distinct banks)
+// halves per K row in LDS: D + 8 (16-byte reads of 16 rows: distinct banks at D = 128)
+template <int D>
+constexpr int kKPitch = D + 8;
 constexpr int kVtPitch = 72;  // halves per V^T row in LDS (16-byte accesses of 8 consecutive rows: distinct banks)
 constexpr float kNegBig = -1.0e30f;
 constexpr float kTau = 8.0f;  // the running max moves only when a score exceeds it by kTau (log2)
@@ -118,7 +119,18 @@ __device__ __forceinline__ u32x4 to_stored(uint32_t d0, uint32_t d1, uint32_t d2
 // Position of key k (0..63) of a tile in a V^T row: bits 2 and 3 exchanged.
 __host__ __device__ constexpr int swap23(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
+// Head dims 32, 64 and 128: QK^T takes D/16 k-steps, PV D/32 column blocks;
+// a fetch thread covers D/4 channels of a token (fp16 tiles), and D/32
+// threads stage a middle token's D/2 code bytes, 16 each.
+template <int D>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PParams p) {
+  constexpr int KROW = D / 2;     // bytes of one token's packed 4-bit codes
+  constexpr int CPT = D / 4;      // channels per fetch thread (fp16 tiles)
+  constexpr int KTHR = D / 32;    // threads (16 code bytes each) per middle token
+  constexpr int UPR = D / 32;     // 16-byte units per staged V code row
+  constexpr int NKS = D / 16;     // QK^T k-steps
+  constexpr int NCB = D / 32;     // PV column blocks
+  constexpr int KP = kKPitch<D>;
   const int qb = blockIdx.x / p.passes;
   const int h0 = 4 * (blockIdx.x - qb * p.passes);  // first query head (within the group) of this workgroup
   const int64_t kvh = blockIdx.y;
@@ -178,19 +190,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     return r;
   };
 
-  __shared__ __attribute__((aligned(16))) uint16_t kt[2][kKT][kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t vtt[2][kD][kVtPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t kt[2][kKT][KP];
+  __shared__ __attribute__((aligned(16))) uint16_t vtt[2][D][kVtPitch];
   __shared__ __attribute__((aligned(16))) float rowf[4][32];  // per-wave factors of the 32 query rows
-  // middle-tile staging: thread tid's 16 bytes of K codes at 16 tid; keys
-  // 16 w + rho (rho < 16) in stg_v[1024 w ..], 16-byte unit u of row rho at
-  // unit 4 rho + (u ^ ((rho >> 1) & 3)); their V scales in dwords 64 w + l,
-  // key 16 w + (l & 15) (a 2-byte direct load fills one dword per lane)
+  // middle-tile staging: thread tid's 16 bytes of K codes at 16 tid (token
+  // tid / KTHR, channels 32 (tid % KTHR) ..); keys 16 w + rho (rho < 16) in
+  // stg_v[1024 w ..], 16-byte unit u of row rho at unit
+  // UPR rho + (u ^ ((rho >> 1) & (UPR - 1))); their V scales in dwords
+  // 64 w + l, key 16 w + (l & 15) (a 2-byte direct load fills one dword per lane)
   __shared__ __attribute__((aligned(16))) uint8_t stg_k[kThreads * 16];
   __shared__ __attribute__((aligned(16))) uint8_t stg_v[kThreads * 16];
   __shared__ __attribute__((aligned(16))) uint32_t stg_s[kThreads];
 
-  // ---- tile fetch: thread = token r of the tile, channels 32*cp .. 32*cp+31 ----
+  // ---- tile fetch: thread = token r of the tile, channels CPT*cp .. CPT*cp+CPT-1 ----
   const int r = tid >> 2, cp = tid & 3;
+  // middle K staging: thread = token mr, channels 32*mc .. 32*mc+31 (threads tid < 64 KTHR)
+  const int mr = tid / KTHR, mc = tid % KTHR;
+  const bool kstage = kKT * KTHR == kThreads || tid < kKT * KTHR;
   const uint16_t* sk = p.sink.k + b * p.sink.k_sb + kvh * p.sink.k_sh;
   const uint16_t* sv = p.sink.v + b * p.sink.v_sb + kvh * p.sink.v_sh;
   const uint16_t* rk = p.recent.k + b * p.recent.k_sb + kvh * p.recent.k_sh;
@@ -199,19 +215,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const uint16_t* cvp = p.chunk.v + b * p.chunk.v_sb + kvh * p.chunk.v_sh;
   const int64_t sk_ss = p.sink.k_ss, sv_ss = p.sink.v_ss, rk_ss = p.recent.k_ss, rv_ss = p.recent.v_ss;
   const int64_t ck_ss = p.chunk.k_ss, cv_ss = p.chunk.v_ss;
-  const uint8_t* kq = p.kq + bkv * p.mid_cap * 64;
-  const uint8_t* vq = p.vq + bkv * p.mid_cap * 64;
-  // fp16 middle tier: rows of 128 halves, [B, Hkv, cap, 128] contiguous
-  const uint16_t* mk16 = reinterpret_cast<const uint16_t*>(p.kq) + bkv * p.mid_cap * kD;
-  const uint16_t* mv16 = reinterpret_cast<const uint16_t*>(p.vq) + bkv * p.mid_cap * kD;
+  const uint8_t* kq = p.kq + bkv * p.mid_cap * KROW;
+  const uint8_t* vq = p.vq + bkv * p.mid_cap * KROW;
+  // fp16 middle tier: rows of D halves, [B, Hkv, cap, D] contiguous
+  const uint16_t* mk16 = reinterpret_cast<const uint16_t*>(p.kq) + bkv * p.mid_cap * D;
+  const uint16_t* mv16 = reinterpret_cast<const uint16_t*>(p.vq) + bkv * p.mid_cap * D;
   const uint16_t* vsr = p.vs + bkv * p.mid_cap;
 
-  // K scales of this thread's 32 channels as fp16 pairs, in the stored order
+  // K scales of this thread's 32 staged channels as fp16 pairs, in the stored order
   uint32_t ksc[16];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint4 w = make_uint4(0, 0, 0, 0);
-    if (p.has_mid && !p.mid_fp16) w = *reinterpret_cast<const uint4*>(p.ks + bkv * kD + 32 * cp + 8 * i);
+    if (p.has_mid && !p.mid_fp16 && kstage) w = *reinterpret_cast<const uint4*>(p.ks + bkv * D + 32 * mc + 8 * i);
     const u32x4 st = to_stored(w.x, w.y, w.z, w.w);
 #pragma unroll
     for (int e = 0; e < 4; ++e) ksc[4 * i + e] = st[e];
@@ -228,7 +244,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // Middle tile: codes and V scale to the staging area.  Nothing waits for
   // these loads before store_mid(), so they fly during the current tile's compute.
   auto fetch_mid = [&](const TileRef& tr) {
-    const bool ok = r < tr.cnt;
+    const bool ok = mr < tr.cnt;
     fok = ok;
     // the tile's rows: from row tr.base of this (row, kv head)'s padded tensors,
     // or from row 0 of its page's (page, kv head) block in the pools
@@ -238,28 +254,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     int row0 = tr.base;
     if (p.pages != nullptr) {
       const int64_t blk = static_cast<int64_t>(p.pages[b * p.ppr + (tr.base >> 6)]) * p.Hkv + kvh;
-      kq_t = p.kq + blk * kKT * 64;
-      vq_t = p.vq + blk * kKT * 64;
+      kq_t = p.kq + blk * kKT * KROW;
+      vq_t = p.vq + blk * kKT * KROW;
       vs_t = p.vs + blk * kKT;
       row0 = 0;
     }
-    const int key = row0 + (ok ? r : tr.cnt - 1);  // rows past the tile: a valid row, zeroed in store_mid()
-    lds_dma16(kq_t + static_cast<int64_t>(key) * 64 + 16 * cp, stk);
-    // V: lane l of wave w fills unit l of the wave's block: row rho = l >> 2,
-    // source unit (l & 3) ^ ((rho >> 1) & 3).  Rows past the tile read the last
-    // valid key (finite; their probabilities are zero).
-    const int vr = lane >> 2;
+    const int key = row0 + (ok ? mr : tr.cnt - 1);  // rows past the tile: a valid row, zeroed in store_mid()
+    if (kstage) lds_dma16(kq_t + static_cast<int64_t>(key) * KROW + 16 * mc, stk);
+    // V: lane l < 16 UPR of wave w fills unit l of the wave's block: row
+    // rho = l / UPR, source unit (l % UPR) ^ ((rho >> 1) & (UPR - 1)).  Rows
+    // past the tile read the last valid key (finite; their probabilities are zero).
+    const int vr = lane / UPR;
     const int vk = 16 * wave + vr, sk2 = 16 * wave + (lane & 15);
-    lds_dma16(vq_t + static_cast<int64_t>(row0 + (vk < tr.cnt ? vk : tr.cnt - 1)) * 64 + 16 * ((lane & 3) ^ ((vr >> 1) & 3)),
-              stv);
+    if (UPR == 4 || lane < 16 * UPR)
+      lds_dma16(vq_t + static_cast<int64_t>(row0 + (vk < tr.cnt ? vk : tr.cnt - 1)) * KROW +
+                    16 * ((lane % UPR) ^ ((vr >> 1) & (UPR - 1))),
+                stv);
     lds_dma2(vs_t + row0 + (sk2 < tr.cnt ? sk2 : tr.cnt - 1), sts);
   };
   // staged codes -> fp16(code * scale) rows of K and V in LDS buffer buf
   auto store_mid = [&](int buf) {
     // the staging loads are the only vector-memory operations in flight here
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    uint4 kraw = *reinterpret_cast<const uint4*>(&stg_k[16 * tid]);
-    if (!fok) kraw = make_uint4(0, 0, 0, 0);
+    uint4 kraw = make_uint4(0, 0, 0, 0);
+    if (kstage && fok) kraw = *reinterpret_cast<const uint4*>(&stg_k[16 * tid]);
     // codes -> fp16 72 + c -> c -> fp16(c * scale), already in the stored channel order
     const uint32_t kw[4] = {kraw.x, kraw.y, kraw.z, kraw.w};
     const f16x2 m72 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
@@ -272,7 +290,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int e = 0; e < 4; ++e)
         kd[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[e]) + m72) *
                                                  __builtin_bit_cast(f16x2, ksc[4 * i + e]));
-      *reinterpret_cast<u32x4*>(&kt[buf][r][32 * cp + 8 * i]) = kd;
+      if (kstage) *reinterpret_cast<u32x4*>(&kt[buf][mr][32 * mc + 8 * i]) = kd;
     }
     // V.  Scales of the wave's keys by row rho (low 16 bits of dword 64 w + rho).
     uint32_t sc[16];
@@ -290,12 +308,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // of those rows, nibble s' <-> position offset o(s'), so the fp16 pairs
     // come out as position pairs (2 j, 2 j + 1), rows (swap23(2 j), + 1).
     const int so = swap23(2 * (n16 & 3) + ((n16 >> 2) & 1) + 8 * (n16 >> 3));
-    const uint8_t* vrow = &stg_v[1024 * wave + 64 * so];
+    const uint8_t* vrow = &stg_v[1024 * wave + KROW * so];
+    // channel units of 16: D/16 of them, four per pass of the lane groups
+    // (D = 32: groups 2 and 3 repeat units 0 and 1 and store nothing)
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int cu = 4 * q + g;
+    for (int q = 0; q < (D / 16 + 3) / 4; ++q) {
+      const int cu = (4 * q + g) % (D / 16);
+      const bool cu_ok = 4 * q + g < D / 16;
       const i32x2 xv = __builtin_amdgcn_ds_read_tr4_b64_v2i32(reinterpret_cast<lds_i32x2*>(
-          const_cast<lds_u8*>((const lds_u8*)(vrow + 16 * ((cu >> 1) ^ ((so >> 1) & 3)) + 8 * (cu & 1)))));
+          const_cast<lds_u8*>((const lds_u8*)(vrow + 16 * ((cu >> 1) ^ ((so >> 1) & (UPR - 1))) + 8 * (cu & 1)))));
       const int ch = 16 * cu + (n16 ^ 1);
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
@@ -308,40 +329,41 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
           const uint32_t s2 = __builtin_amdgcn_perm(sc[ra + 1], sc[ra], 0x05040100u);
           vd[j] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[j]) + m72) * __builtin_bit_cast(f16x2, s2));
         }
-        *reinterpret_cast<u32x4*>(&vtt[buf][ch][16 * wave + 8 * half]) = vd;
+        if (cu_ok) *reinterpret_cast<u32x4*>(&vtt[buf][ch][16 * wave + 8 * half]) = vd;
       }
     }
   };
   // fp16 tile (sink, recent or chunk: a few per row; an fp16 middle tier): loaded and stored at once
   auto load_store_f16 = [&](const TileRef& tr, int buf) {
-    uint4 fk[4], fv[4];
+    constexpr int NU = CPT / 8;  // 16-byte units per thread
+    uint4 fk[NU], fv[NU];
     const int key = tr.base + r;
     if (r < tr.cnt) {
       const uint16_t* kp = tr.seg == 0 ? sk + key * sk_ss
-                           : (tr.seg == 1 ? mk16 + static_cast<int64_t>(key) * kD
+                           : (tr.seg == 1 ? mk16 + static_cast<int64_t>(key) * D
                                           : (tr.seg == 2 ? rk + key * rk_ss : ck + key * ck_ss));
       const uint16_t* vp = tr.seg == 0 ? sv + key * sv_ss
-                           : (tr.seg == 1 ? mv16 + static_cast<int64_t>(key) * kD
+                           : (tr.seg == 1 ? mv16 + static_cast<int64_t>(key) * D
                                           : (tr.seg == 2 ? rv + key * rv_ss : cvp + key * cv_ss));
-      const uint4* k4 = reinterpret_cast<const uint4*>(kp + 32 * cp);
-      const uint4* v4 = reinterpret_cast<const uint4*>(vp + 32 * cp);
+      const uint4* k4 = reinterpret_cast<const uint4*>(kp + CPT * cp);
+      const uint4* v4 = reinterpret_cast<const uint4*>(vp + CPT * cp);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < NU; ++i) {
         fk[i] = k4[i];
         fv[i] = v4[i];
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fk[i] = fv[i] = make_uint4(0, 0, 0, 0);
+      for (int i = 0; i < NU; ++i) fk[i] = fv[i] = make_uint4(0, 0, 0, 0);
     }
     const int pr = swap23(r);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<u32x4*>(&kt[buf][r][32 * cp + 8 * i]) = to_stored(fk[i].x, fk[i].y, fk[i].z, fk[i].w);
+    for (int i = 0; i < NU; ++i) {
+      *reinterpret_cast<u32x4*>(&kt[buf][r][CPT * cp + 8 * i]) = to_stored(fk[i].x, fk[i].y, fk[i].z, fk[i].w);
       const uint32_t vw[4] = {fv[i].x, fv[i].y, fv[i].z, fv[i].w};
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        vtt[buf][32 * cp + 8 * i + e][pr] = static_cast<uint16_t>(vw[e >> 1] >> (16 * (e & 1)));
+        vtt[buf][CPT * cp + 8 * i + e][pr] = static_cast<uint16_t>(vw[e >> 1] >> (16 * (e & 1)));
     }
   };
   // Tile t into LDS buffer buf: fp16 tiles complete here; a middle tile only
@@ -361,12 +383,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int n32 = lane & 31, h = lane >> 5;
   const bool active = wave < G;
   const int64_t hq = kvh * p.G + h0 + (active ? wave : 0);
-  f16x8 qf[8];
+  f16x8 qf[NKS];
   {
     const int j = j0 + n32;
     const uint16_t* qr = p.q + b * p.q_sb + hq * p.q_sh + static_cast<int64_t>(j < Sq ? j : Sq - 1) * p.q_ss;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < NKS; ++ks) {
       const uint4 w = (active && j < Sq) ? *reinterpret_cast<const uint4*>(qr + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
       qf[ks] = __builtin_bit_cast(f16x8, to_stored(w.x, w.y, w.z, w.w));
     }
@@ -374,9 +396,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   // O accumulators: acc[cb] lane (n32, h), register i <-> query row 8 (i / 4) + 4 h + i % 4,
   // channel 32 cb + n32
-  f32x16 acc[4];
+  f32x16 acc[NCB];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb)
+  for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[cb][i] = 0.0f;
   float m_run = kNegBig, l_run = 0.0f;  // of query row n32 (the same in both halves; l_run over this half's keys)
@@ -393,7 +415,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
+      for (int ks = 0; ks < NKS; ++ks) {
         const f16x8 a = *reinterpret_cast<const f16x8*>(&kt[buf][32 * kb + n32][16 * ks + 8 * h]);
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], s[kb], 0, 0, 0);
       }
@@ -434,7 +456,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int q = 0; q < 4; ++q) {
         const f32x4 a4 = *reinterpret_cast<const f32x4*>(&rf[8 * q + 4 * h]);
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
+        for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[cb][4 * q + i] *= a4[i];
       }
@@ -458,7 +480,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int ks2 = 0; ks2 < 4; ++ks2)
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
+      for (int cb = 0; cb < NCB; ++cb) {
         const f16x8 bv = *reinterpret_cast<const f16x8*>(&vtt[buf][32 * cb + n32][16 * ks2 + 8 * h]);
         acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[ks2], bv, acc[cb], 0, 0, 0);
       }
@@ -490,7 +512,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         if (j < Sq) {
           uint16_t* orow = p.out + b * p.o_sb + hq * p.o_sh + static_cast<int64_t>(j) * p.o_ss;
 #pragma unroll
-          for (int cb = 0; cb < 4; ++cb) orow[32 * cb + n32] = f2h(acc[cb][4 * q + i] * inv4[i]);
+          for (int cb = 0; cb < NCB; ++cb) orow[32 * cb + n32] = f2h(acc[cb][4 * q + i] * inv4[i]);
         }
       }
     }
@@ -522,7 +544,8 @@ using namespace fade::prefill;
 
 FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) {
   if (a == nullptr) return einval("fade_tiered_prefill_attn: null args");
-  if (a->D != kD) return einval("fade_tiered_prefill_attn: head_dim must be %d, got %lld", kD, (long long)a->D);
+  if (a->D != 32 && a->D != 64 && a->D != 128)
+    return einval("fade_tiered_prefill_attn: head_dim must be 32, 64 or 128, got %lld", (long long)a->D);
   if (a->B <= 0 || a->Hq <= 0 || a->Hkv <= 0 || a->Sq <= 0)
     return einval("fade_tiered_prefill_attn: B, Hq, Hkv and Sq must be positive");
   if (a->Hq % a->Hkv != 0 || a->Hq / a->Hkv > 8)
@@ -588,6 +611,10 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   p.chunk_len = static_cast<int>(a->chunk.len);
   const dim3 grid(static_cast<unsigned>(cdiv(a->Sq, kQB) * p.passes), static_cast<unsigned>(a->Hkv),
                   static_cast<unsigned>(a->B));
-  hipLaunchKernelGGL(prefill_kernel, grid, dim3(kThreads), 0, as_stream(stream), p);
+  switch (a->D) {
+    case 32: hipLaunchKernelGGL(prefill_kernel<32>, grid, dim3(kThreads), 0, as_stream(stream), p); break;
+    case 64: hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(kThreads), 0, as_stream(stream), p); break;
+    default: hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(kThreads), 0, as_stream(stream), p); break;
+  }
   return check_launch("fade_tiered_prefill_attn");
 }

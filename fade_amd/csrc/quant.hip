@@ -508,8 +508,8 @@ __global__ void unpack_kernel(const uint8_t* __restrict__ packed, int64_t n8, in
 // ---------------------------------------------------------------- host side
 int check_dims(const char* fn, int64_t B, int64_t H, int64_t S, int64_t D) {
   if (B < 0 || H < 0 || S < 0) return einval("%s: negative size (B=%lld H=%lld S=%lld)", fn, (long long)B, (long long)H, (long long)S);
-  if (D != 64 && D != 128 && D != 256)
-    return einval("%s: head_dim must be 64, 128 or 256, got %lld", fn, (long long)D);
+  if (D != 32 && D != 64 && D != 128 && D != 256)
+    return einval("%s: head_dim must be 32, 64, 128 or 256, got %lld", fn, (long long)D);
   return FADE_OK;
 }
 
@@ -542,6 +542,7 @@ void channel_blocking(int64_t BH, int64_t S, int64_t* nsb, int64_t* rows_per_blo
 
 #define FADE_DISPATCH_LPR(D, ...)           \
   switch (D) {                              \
+    case 32: { constexpr int LPR = 4; __VA_ARGS__; } break;   \
     case 64: { constexpr int LPR = 8; __VA_ARGS__; } break;   \
     case 128: { constexpr int LPR = 16; __VA_ARGS__; } break; \
     default: { constexpr int LPR = 32; __VA_ARGS__; } break;  \

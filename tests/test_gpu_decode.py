@@ -419,10 +419,12 @@ def test_tiered_decode_ragged_paged_gqa_5_to_8(dev, Hq, Hkv, fmt):
 
 @pytest.mark.parametrize("fmt", ["int4", "asym42"])
 @pytest.mark.parametrize("n_splits", [0, 1, 7])
-def test_tiered_decode_ragged_lens(dev, fmt, n_splits):
+@pytest.mark.parametrize("kernel", [0, 1])
+def test_tiered_decode_ragged_lens(dev, fmt, n_splits, kernel):
     """Per-row tier lengths (ragged batch): row b attends to the first lens[b] rows of
-    each padded tier; each row is checked against the oracle over its own tokens."""
-    print(f"case decode ragged {fmt} n_splits={n_splits}", flush=True)
+    each padded tier; each row is checked against the oracle over its own tokens.
+    Matrix-core INT4 kernel (0) and portable kernel (1)."""
+    print(f"case decode ragged {fmt} n_splits={n_splits} kernel={kernel}", flush=True)
     ns_c, mc, nr_c = 4, 600, 64
     S = ns_c + mc + nr_c
     B = 5
@@ -435,7 +437,8 @@ def test_tiered_decode_ragged_lens(dev, fmt, n_splits):
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     sink = (t(k[:, :, :ns_c]), t(v[:, :, :ns_c]))
     rec = (t(k[:, :, S - nr_c :]), t(v[:, :, S - nr_c :]))
-    out = tiered_decode_attention(t(q), sink, mid, rec, lens=t(lens), n_splits=n_splits).float().cpu().numpy()
+    out = tiered_decode_attention(t(q), sink, mid, rec, lens=t(lens), n_splits=n_splits,
+                                  kernel=kernel).float().cpu().numpy()
     for b, (ls, lm, lr) in enumerate(lens):
         ref = oatt.tiered_decode(
             q[b : b + 1], k[b : b + 1, :, :ls], v[b : b + 1, :, :ls], _row_slice_mid(omid, b, lm),
@@ -446,14 +449,14 @@ def test_tiered_decode_ragged_lens(dev, fmt, n_splits):
 
 
 def test_tiered_decode_ragged_lens_rejected_on_other_kernels(dev):
-    """Per-row lengths are a matrix-core INT4 kernel feature; the portable kernel refuses them."""
+    """Per-row lengths are read by the INT4 and portable kernels; the general matrix-core kernel refuses them."""
     q, k, v, ns, nr = _case(1, 8, 4, 200, 4, 16, seed=3)
     mid, _ = _int4_mid(dev, k, v, ns, nr)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     lens = torch.tensor([[4, 100, 16]], dtype=torch.int32, device=dev)
     with pytest.raises(ValueError, match="per-row lengths"):
         tiered_decode_attention(t(q), (t(k[:, :, :4]), t(v[:, :, :4])), mid, (t(k[:, :, 184:]), t(v[:, :, 184:])),
-                                lens=lens, kernel=1)
+                                lens=lens, kernel=3)
 
 
 @pytest.mark.parametrize("fmt", ["int4", "asym42"])

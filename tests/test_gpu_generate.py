@@ -1,7 +1,7 @@
 """HF generate() on the fused tiered kernels (attn_implementation="fade").
 
 Pins from the reference's own tests, on a tiny random-init Qwen2 (no
-downloads; head_dim 128 as the kernels require, fp16 on the GPU):
+downloads; head_dim 128, and 64 in one test, fp16 on the GPU):
   * greedy generate == a manual greedy loop (tests/test_generate.py:88-117);
   * with no eviction the first token equals a plain DynamicCache's
     (tests/test_eval_gate.py:104-138);
@@ -20,11 +20,11 @@ from fade_amd.cache import TIER_FP16, TIER_INT4
 pytestmark = pytest.mark.gpu
 
 
-def _tiny_model(dev, impl, heads=4, kv_heads=2):
+def _tiny_model(dev, impl, heads=4, kv_heads=2, head_dim=128):
     from transformers import AutoConfig, AutoModelForCausalLM
 
     cfg = AutoConfig.for_model(
-        "qwen2", vocab_size=128, hidden_size=128 * heads, intermediate_size=256, num_hidden_layers=2,
+        "qwen2", vocab_size=128, hidden_size=head_dim * heads, intermediate_size=256, num_hidden_layers=2,
         num_attention_heads=heads, num_key_value_heads=kv_heads, max_position_embeddings=256, rope_theta=10000.0,
         tie_word_embeddings=True,
     )
@@ -114,6 +114,20 @@ def test_fused_logits_match_materialized_gqa_5_to_8(dev, heads, kv_heads):
     kernel's two head passes, the decode steps through the matrix-core kernel."""
     print(f"case generate fused vs materialized GQA {heads}/{kv_heads}", flush=True)
     model, cfg = _tiny_model(dev, "fade", heads, kv_heads)
+    ids = torch.randint(0, cfg.vocab_size, (2, 40), device=dev)
+    fused = _steps(model, _cache(model), ids, 3, middle_after_prompt=True)
+    model.set_attn_implementation("sdpa")
+    ref = _steps(model, _cache(model), ids, 3, middle_after_prompt=True)
+    for a, b in zip(fused, ref):
+        assert (a - b).abs().max().item() <= 2e-2
+
+
+def test_fused_logits_match_materialized_head_dim_64(dev):
+    """Qwen2.5-0.5B's attention shape (14 query heads / 2 kv heads, head_dim 64): the
+    prompt through the prefill kernel's D = 64 instance (two head passes), the decode
+    steps through the portable kernel."""
+    print("case generate fused vs materialized head_dim 64", flush=True)
+    model, cfg = _tiny_model(dev, "fade", 14, 2, head_dim=64)
     ids = torch.randint(0, cfg.vocab_size, (2, 40), device=dev)
     fused = _steps(model, _cache(model), ids, 3, middle_after_prompt=True)
     model.set_attn_implementation("sdpa")

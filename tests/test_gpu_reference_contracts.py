@@ -169,7 +169,7 @@ def test_backend_registry_and_cache_field(dev):  # :41-52, :55-63, :87-100
 
 
 # ---------------------------------------------------------------- tests/test_cache.py
-CH, CD = 2, 64  # tests/test_cache.py:22 uses head_dim 32; the HIP quantizers take 64, 128 or 256
+CH, CD = 2, 32  # tests/test_cache.py:22
 
 
 def _cache(**kw):  # tests/test_cache.py:27-36
