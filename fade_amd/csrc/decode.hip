@@ -22,141 +22,211 @@ namespace {
 
 constexpr int kTile = 64;
 constexpr int kThreads = 256;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-// D/4 dequantized K values of token t of a row whose sink and middle tiers
-// hold ns and nm tokens, channels [D/4*quarter, D/4*(quarter+1)).
-template <int D>
-__device__ void load_kq(const Params& p, int64_t b, int64_t kvh, int64_t t, int64_t ns, int64_t nm, int quarter,
-                        const float* ks_s, float* out) {
-  constexpr int CQ = D / 4;
-  const int d0 = CQ * quarter;
-  const Fp16Tier* seg = nullptr;
-  int64_t r = t;
-  if (t < ns) {
-    seg = &p.sink;
-  } else if (t < ns + nm) {
-    const int64_t m = t - ns;
-    const int64_t row = (b * p.Hkv + kvh) * p.mid.len + m;
-    switch (p.mid.fmt) {
-      case FADE_MID_FP16: {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(p.mid.k_codes) + row * D + d0;
-        for (int j = 0; j < CQ; ++j) out[j] = h2f(src[j]);
-        return;
-      }
-      case FADE_MID_SYM:
-      case FADE_MID_K4V2G: {
-        const int bits = p.mid.fmt == FADE_MID_SYM ? p.mid.k_bits : 4;
-        const uint8_t* src = p.mid.k_codes + row * (D * bits / 8);
-        for (int j = 0; j < CQ; ++j) {
-          const int d = d0 + j;
-          out[j] = round_f16(static_cast<float>(sym_code_at(src, d, bits)) * ks_s[d]);
-        }
-        return;
-      }
-      default: {  // FADE_MID_ASYM
-        const int bits = p.mid.k_bits, g = p.mid.group;
-        const uint8_t* src = p.mid.k_codes + row * (D * bits / 8);
-        for (int j = 0; j < CQ; ++j) {
-          const int d = d0 + j;
-          const float s = h2f(p.mid.k_scale[row * (D / g) + d / g]);
-          const float z = h2f(p.mid.k_zero[row * (D / g) + d / g]);
-          out[j] = round_f16(static_cast<float>(asym_code_at(src, d, bits)) * s + z);
-        }
-        return;
-      }
-    }
-  } else {
-    seg = &p.recent;
-    r = t - ns - nm;
-  }
-  const uint16_t* src = seg->k + b * seg->k_sb + kvh * seg->k_sh + r * seg->k_ss + d0;
-  for (int j = 0; j < CQ; ++j) out[j] = h2f(src[j]);
+// Eight consecutive fp16 values (channels 8 cg .. 8 cg + 7) of a row, with a
+// 16-byte load where the address allows it.
+__device__ __forceinline__ uint4 load8h(const uint16_t* src) {
+  if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) return *reinterpret_cast<const uint4*>(src);
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) w[j] = static_cast<uint32_t>(src[2 * j]) | (static_cast<uint32_t>(src[2 * j + 1]) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// Dequantized V channels d0 .. d0 + N - 1 of token t (tiers as in load_kq).
-template <int D, int N>
-__device__ void load_vn(const Params& p, int64_t b, int64_t kvh, int64_t t, int64_t ns, int64_t nm, int d0,
-                        float* v) {
-  const Fp16Tier* seg = nullptr;
-  int64_t r = t;
-  if (t < ns) {
-    seg = &p.sink;
-  } else if (t < ns + nm) {
-    const int64_t m = t - ns;
+__device__ __forceinline__ uint4 pack8h(const float* x) {
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) w[j] = static_cast<uint32_t>(f2h(x[2 * j])) | (static_cast<uint32_t>(f2h(x[2 * j + 1])) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// One staging unit (channels 8 cg .. 8 cg + 7 of one token's K or V) as loaded
+// from HBM, before dequantization: fp16 tiers: the eight values; packed
+// middle tiers: x = codes (first code in the high bits), y = per-token scale
+// (low half) and zero (high half) where the format has them; literal INT2 V:
+// x, y = the eight int8 codes.
+struct RawUnit {
+  uint4 w;
+};
+
+// Where unit (token t, group cg) lives: seg 0 sink, 1 middle, 2 recent; r = row in the tier.
+struct UnitRef {
+  int seg;
+  int64_t r;
+};
+__device__ __forceinline__ UnitRef unit_ref(int64_t t, int64_t ns, int64_t nm) {
+  if (t < ns) return {0, t};
+  if (t < ns + nm) return {1, t - ns};
+  return {2, t - ns - nm};
+}
+
+// SYM44: the middle tier is the reference INT4 format (FADE_MID_SYM, 4-bit K
+// and V), known at compile time.
+template <int D, bool IS_V, bool SYM44>
+__device__ __forceinline__ RawUnit load_unit(const Params& p, int64_t b, int64_t kvh, UnitRef u, int cg) {
+  const int d0 = 8 * cg;
+  RawUnit ru;
+  if (u.seg != 1) {
+    const Fp16Tier& seg = u.seg == 0 ? p.sink : p.recent;
+    const uint16_t* src = IS_V ? seg.v + b * seg.v_sb + kvh * seg.v_sh + u.r * seg.v_ss
+                               : seg.k + b * seg.k_sb + kvh * seg.k_sh + u.r * seg.k_ss;
+    ru.w = load8h(src + d0);
+    return ru;
+  }
+  const int64_t m = u.r;
+  const int64_t bkv = b * p.Hkv + kvh;
+  const int64_t row = bkv * p.mid.len + m;
+  const int fmt = SYM44 ? FADE_MID_SYM : p.mid.fmt;
+  if (fmt == FADE_MID_FP16) {
+    const uint8_t* base = IS_V ? p.mid.v_codes : p.mid.k_codes;
+    ru.w = load8h(reinterpret_cast<const uint16_t*>(base) + row * D + d0);
+    return ru;
+  }
+  ru.w = make_uint4(0, 0, 0, 0);
+  if (IS_V && fmt == FADE_MID_K4V2G) {  // eight int8 codes
+    const uint8_t* src = p.mid.v_codes + (bkv * p.mid.v_rows + m) * D + d0;
+    if ((reinterpret_cast<uintptr_t>(src) & 7) == 0) {
+      const uint2 c8 = *reinterpret_cast<const uint2*>(src);
+      ru.w.x = c8.x;
+      ru.w.y = c8.y;
+    } else {
+      for (int j = 0; j < 4; ++j) {
+        ru.w.x |= static_cast<uint32_t>(src[j]) << (8 * j);
+        ru.w.y |= static_cast<uint32_t>(src[4 + j]) << (8 * j);
+      }
+    }
+    return ru;
+  }
+  const int bits = SYM44 || fmt == FADE_MID_K4V2G ? 4 : (IS_V ? p.mid.v_bits : p.mid.k_bits);
+  const uint8_t* src = (IS_V ? p.mid.v_codes : p.mid.k_codes) + row * (D * bits / 8);
+  if (bits == 4) {
+    const uint8_t* c = src + 4 * cg;
+    if ((reinterpret_cast<uintptr_t>(c) & 3) == 0)
+      ru.w.x = __builtin_bswap32(*reinterpret_cast<const uint32_t*>(c));
+    else
+      ru.w.x = (static_cast<uint32_t>(c[0]) << 24) | (static_cast<uint32_t>(c[1]) << 16) |
+               (static_cast<uint32_t>(c[2]) << 8) | static_cast<uint32_t>(c[3]);
+  } else {
+    const uint8_t* c = src + 2 * cg;
+    if ((reinterpret_cast<uintptr_t>(c) & 1) == 0)
+      ru.w.x = static_cast<uint32_t>(__builtin_bswap16(*reinterpret_cast<const uint16_t*>(c))) << 16;
+    else
+      ru.w.x = (static_cast<uint32_t>(c[0]) << 24) | (static_cast<uint32_t>(c[1]) << 16);
+  }
+  if (fmt == FADE_MID_ASYM) {
+    const int g = p.mid.group;  // >= 16: one group holds the unit's eight channels
+    const uint16_t* sc = IS_V ? p.mid.v_scale : p.mid.k_scale;
+    const uint16_t* zp = IS_V ? p.mid.v_zero : p.mid.k_zero;
+    ru.w.y = static_cast<uint32_t>(sc[row * (D / g) + d0 / g]) | (static_cast<uint32_t>(zp[row * (D / g) + d0 / g]) << 16);
+  } else if (IS_V) {
+    ru.w.y = p.mid.v_scale[row];
+  }
+  return ru;
+}
+
+// A loaded unit dequantized as the reference does (fp16(code * scale),
+// fp16(code * scale + zero) for the asymmetric format): eight fp16 values.
+// ks_s: the row's per-channel K scales (fp32).
+template <int D, bool IS_V, bool SYM44>
+__device__ __forceinline__ uint4 convert_unit(const Params& p, int64_t b, int64_t kvh, UnitRef u, int cg,
+                                              const RawUnit& ru, const float* ks_s) {
+  const int fmt = SYM44 ? FADE_MID_SYM : p.mid.fmt;
+  if (u.seg != 1 || fmt == FADE_MID_FP16) return ru.w;
+  const int d0 = 8 * cg;
+  float x[8];
+  if (IS_V && fmt == FADE_MID_K4V2G) {  // literal grouped INT2 V: per-(group, channel) scales
     const int64_t bkv = b * p.Hkv + kvh;
-    const int64_t row = bkv * p.mid.len + m;
-    switch (p.mid.fmt) {
-      case FADE_MID_FP16: {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(p.mid.v_codes) + row * D + d0;
+    const int64_t Gr = p.mid.v_rows / p.mid.group;
+    const uint4 sc = load8h(p.mid.v_scale + (bkv * Gr + u.r / p.mid.group) * D + d0);
+    const uint32_t sw[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
-        for (int j = 0; j < N; ++j) v[j] = h2f(src[j]);
-        return;
-      }
-      case FADE_MID_SYM: {
-        const int bits = p.mid.v_bits;
-        const uint8_t* src = p.mid.v_codes + row * (D * bits / 8);
-        const float s = h2f(p.mid.v_scale[row]);
-#pragma unroll
-        for (int j = 0; j < N; ++j) v[j] = round_f16(static_cast<float>(sym_code_at(src, d0 + j, bits)) * s);
-        return;
-      }
-      case FADE_MID_K4V2G: {
-        const int8_t* src = reinterpret_cast<const int8_t*>(p.mid.v_codes) + (bkv * p.mid.v_rows + m) * D + d0;
-        const int64_t G = p.mid.v_rows / p.mid.group;
-        const uint16_t* sc = p.mid.v_scale + (bkv * G + m / p.mid.group) * D + d0;
-#pragma unroll
-        for (int j = 0; j < N; ++j) v[j] = round_f16(static_cast<float>(src[j]) * h2f(sc[j]));
-        return;
-      }
-      default: {  // FADE_MID_ASYM
-        const int bits = p.mid.v_bits, g = p.mid.group;
-        const uint8_t* src = p.mid.v_codes + row * (D * bits / 8);
-#pragma unroll
-        for (int j = 0; j < N; ++j) {
-          const int d = d0 + j;
-          const float s = h2f(p.mid.v_scale[row * (D / g) + d / g]);
-          const float z = h2f(p.mid.v_zero[row * (D / g) + d / g]);
-          v[j] = round_f16(static_cast<float>(asym_code_at(src, d, bits)) * s + z);
-        }
-        return;
-      }
+    for (int j = 0; j < 8; ++j) {
+      const int8_t c = static_cast<int8_t>(((j < 4 ? ru.w.x : ru.w.y) >> (8 * (j & 3))) & 0xFF);
+      x[j] = static_cast<float>(c) * h2f(static_cast<uint16_t>(sw[j >> 1] >> (16 * (j & 1))));
     }
-  } else {
-    seg = &p.recent;
-    r = t - ns - nm;
+    return pack8h(x);
   }
-  const uint16_t* src = seg->v + b * seg->v_sb + kvh * seg->v_sh + r * seg->v_ss + d0;
+  const int bits = SYM44 || fmt == FADE_MID_K4V2G ? 4 : (IS_V ? p.mid.v_bits : p.mid.k_bits);
+  int c[8];
 #pragma unroll
-  for (int j = 0; j < N; ++j) v[j] = h2f(src[j]);
+  for (int j = 0; j < 8; ++j) {
+    if (bits == 4)
+      c[j] = static_cast<int>((ru.w.x >> (28 - 4 * j)) & 0xF);
+    else
+      c[j] = static_cast<int>((ru.w.x >> (30 - 2 * j)) & 0x3);
+  }
+  if (fmt == FADE_MID_ASYM) {
+    const float s = h2f(static_cast<uint16_t>(ru.w.y & 0xFFFFu));
+    const float z = h2f(static_cast<uint16_t>(ru.w.y >> 16));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = static_cast<float>(c[j]) * s + z;
+    return pack8h(x);
+  }
+  // symmetric: two's complement codes
+  const int sgn = bits == 4 ? 8 : 2;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c[j] -= (c[j] & sgn) << 1;
+  if (IS_V) {
+    const float s = h2f(static_cast<uint16_t>(ru.w.y & 0xFFFFu));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = static_cast<float>(c[j]) * s;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = static_cast<float>(c[j]) * ks_s[d0 + j];
+  }
+  return pack8h(x);
 }
 
-// Portable kernel, head_dim D (32, 64, 128 or 256).  Tile of 64 tokens:
-//   A) thread (quarter = wave, token = lane) dots its D/4 channels with all heads;
-//   B) wave h finishes head h's scores for the 64 tokens, online softmax;
-//   C) thread (heads wave / wave+4, channels CPL*lane .. + CPL-1) accumulates P*V.
-template <int D>
+__device__ __forceinline__ void unpack8h(const uint4& w, float* x) {
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[2 * j] = h2f(static_cast<uint16_t>(u[j] & 0xFFFFu));
+    x[2 * j + 1] = h2f(static_cast<uint16_t>(u[j] >> 16));
+  }
+}
+
+// Portable kernel, head_dim D (32, 64, 128 or 256), up to HP query heads per kv
+// head (4 or 8), any middle format.  Per tile of 64 tokens:
+//   stage: all threads dequantize the tile's K and V into LDS (fp16, the
+//          reference's rounding), one 8-channel unit per thread and step,
+//          coalesced global loads;
+//   QK:    thread (token = lane, heads wave and wave + 4) dots the K row with
+//          the fp16 query (v_dot2_f32_f16: fp16 pairs, fp32 sums), then the
+//          wave's online softmax in the log2 domain;
+//   PV:    thread (head, 8-channel group, token slice) accumulates P V over its
+//          slice of the tile's tokens; the slices are summed once per split.
+template <int D, int HP, bool SYM44>
 __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
-  constexpr int CQ = D / 4;                   // channels per wave in A
-  constexpr int CPL = D >= 64 ? D / 64 : 1;   // channels per lane in C
-  constexpr int LANES = D / CPL;              // lanes holding channels in C
+  constexpr int CG = D / 8;                 // 8-channel units per row
+  constexpr int KP = D + 8;                 // LDS row pitch (halves)
+  constexpr int NU = HP * CG;               // (head, unit) outputs
+  constexpr int TQ = kThreads / NU;         // token slices per output
+  constexpr int TPS = kTile / TQ;           // tokens per slice
+  constexpr int HPW = HP / 4;               // heads per wave in QK
+  static_assert(TQ >= 1 && kThreads % NU == 0, "PV decomposition");
   const int split = blockIdx.x;
   const int64_t kvh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = p.G;
 
-  __shared__ float q_s[kMaxG][D];
+  __shared__ __attribute__((aligned(16))) uint32_t q2_s[HP][D / 2];  // fp16 query pairs
   __shared__ float ks_s[D];
-  __shared__ float sc_s[4][kMaxG][kTile];
-  __shared__ float p_s[kMaxG][kTile];
-  __shared__ float alpha_s[kMaxG];
+  __shared__ __attribute__((aligned(16))) uint16_t kt[kTile][KP];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[kTile][KP];
+  __shared__ float p_s[HP][kTile];
+  __shared__ float alpha_s[HP];
+  __shared__ __attribute__((aligned(16))) float red[TQ > 1 ? TQ : 1][NU][8];
 
-  for (int i = tid; i < G * D; i += kThreads) {
-    const int h = i / D, d = i % D;
-    q_s[h][d] = h2f(p.q[b * p.q_sb + (kvh * G + h) * p.q_sh + d]);
+  for (int i = tid; i < HP * D / 2; i += kThreads) {
+    const int h = i / (D / 2), d = 2 * (i % (D / 2));
+    const uint16_t* qr = p.q + b * p.q_sb + (kvh * G + h) * p.q_sh + d;
+    q2_s[h][d / 2] = h < G ? static_cast<uint32_t>(qr[0]) | (static_cast<uint32_t>(qr[1]) << 16) : 0u;
   }
   if (p.mid.fmt == FADE_MID_SYM || p.mid.fmt == FADE_MID_K4V2G)
     for (int d = tid; d < D; d += kThreads) ks_s[d] = h2f(p.mid.k_scale[(b * p.Hkv + kvh) * D + d]);
-  __syncthreads();
+  if (tid < HP) alpha_s[tid] = 1.0f;
 
   // the row's tier lengths: the tiers' own, or per row (lens, clamped to the padded tiers)
   int64_t ns = p.sink.len, nm = p.mid.len, nr = p.recent.len;
@@ -170,94 +240,149 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
   const int64_t t_begin = static_cast<int64_t>(split) * p.tokens_per_split;
   const int64_t t_end = t_begin + p.tokens_per_split < total ? t_begin + p.tokens_per_split : total;
 
-  float m_run[2] = {-INFINITY, -INFINITY};
-  float l_lane[2] = {0.0f, 0.0f};
-  float acc[2][CPL];
+  float m_run[HPW], l_lane[HPW];
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh)
+  for (int i = 0; i < HPW; ++i) {
+    m_run[i] = -INFINITY;
+    l_lane[i] = 0.0f;
+  }
+  // PV: output (head ph, unit pc), token slice pq
+  const int po = tid % NU, pq = tid / NU;
+  const int ph = po / CG, pc = po % CG;
+  float acc[8];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) acc[hh][c] = 0.0f;
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+
+  // Staging: thread tid owns units tid + kThreads * i (token u / CG, group u % CG)
+  // of every tile: all loads of the tile are issued, then dequantized into LDS.
+  // (Loading the next tile's units during this tile's compute measured no faster.)
+  constexpr int UPT = kTile * CG / kThreads > 0 ? kTile * CG / kThreads : 1;
+  RawUnit rk[UPT], rv[UPT];
+  auto load_tile = [&](int64_t ts, int nv) {
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      const int uidx = tid + kThreads * i;
+      const int r = uidx / CG, cg = uidx % CG;
+      if (uidx < kTile * CG && r < nv) {
+        const UnitRef ur = unit_ref(ts + r, ns, nm);
+        rk[i] = load_unit<D, false, SYM44>(p, b, kvh, ur, cg);
+        rv[i] = load_unit<D, true, SYM44>(p, b, kvh, ur, cg);
+      }
+    }
+  };
+  auto store_tile = [&](int64_t ts, int nv) {  // tokens past nv as zeros
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      const int uidx = tid + kThreads * i;
+      const int r = uidx / CG, cg = uidx % CG;
+      if (uidx < kTile * CG) {
+        uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
+        if (r < nv) {
+          const UnitRef ur = unit_ref(ts + r, ns, nm);
+          kw = convert_unit<D, false, SYM44>(p, b, kvh, ur, cg, rk[i], ks_s);
+          vw = convert_unit<D, true, SYM44>(p, b, kvh, ur, cg, rv[i], ks_s);
+        }
+        *reinterpret_cast<uint4*>(&kt[r][8 * cg]) = kw;
+        *reinterpret_cast<uint4*>(&vt[r][8 * cg]) = vw;
+      }
+    }
+  };
+  auto tile_len = [&](int64_t ts) { return static_cast<int>(t_end - ts < kTile ? t_end - ts : kTile); };
+  __syncthreads();  // q_s, ks_s
 
   for (int64_t ts = t_begin; ts < t_end; ts += kTile) {
-    {  // A
-      const int64_t t = ts + lane;
-      float part[kMaxG];
+    const int nv = tile_len(ts);
+    load_tile(ts, nv);
+    store_tile(ts, nv);
+    __syncthreads();
+    // ---- QK and the online softmax: heads wave (+ 4) of token lane ----
+    {
+      float s[HPW];
 #pragma unroll
-      for (int h = 0; h < kMaxG; ++h) part[h] = 0.0f;
-      if (t < t_end) {
-        float kv[CQ];
-        load_kq<D>(p, b, kvh, t, ns, nm, wave, ks_s, kv);
-        for (int h = 0; h < G; ++h) {
-          float s = 0.0f;
+      for (int i = 0; i < HPW; ++i) s[i] = 0.0f;
+#pragma unroll 4
+      for (int cg = 0; cg < CG; ++cg) {
+        const uint4 kw = *reinterpret_cast<const uint4*>(&kt[lane][8 * cg]);
+        const uint32_t k2[4] = {kw.x, kw.y, kw.z, kw.w};
 #pragma unroll
-          for (int j = 0; j < CQ; ++j) s += q_s[h][CQ * wave + j] * kv[j];
-          part[h] = s;
+        for (int i = 0; i < HPW; ++i) {
+          const uint4 qw = *reinterpret_cast<const uint4*>(&q2_s[wave + 4 * i][4 * cg]);
+          const uint32_t q2[4] = {qw.x, qw.y, qw.z, qw.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            s[i] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, k2[j]), __builtin_bit_cast(f16x2, q2[j]), s[i],
+                                          false);
         }
       }
-      for (int h = 0; h < G; ++h) sc_s[wave][h][lane] = part[h];
-    }
-    __syncthreads();
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {  // B
-      const int h = wave + 4 * hh;
-      if (h < G) {
-        const int64_t t = ts + lane;
-        float s = -INFINITY;
-        if (t < t_end)
-          s = (sc_s[0][h][lane] + sc_s[1][h][lane] + sc_s[2][h][lane] + sc_s[3][h][lane]) * p.scale_log2;
-        const float m_new = fmaxf(m_run[hh], group_max<64>(s));
-        float alpha = 1.0f, pv = 0.0f;
-        if (m_new != -INFINITY) {
-          alpha = exp2f(m_run[hh] - m_new);
-          pv = exp2f(s - m_new);
-        }
-        l_lane[hh] = l_lane[hh] * alpha + pv;
-        p_s[h][lane] = pv;
-        if (lane == 0) alpha_s[h] = alpha;
-        m_run[hh] = m_new;
-      }
-    }
-    __syncthreads();
-    if (lane < LANES) {  // C
-      const int nv = static_cast<int>(t_end - ts < kTile ? t_end - ts : kTile);
+      for (int i = 0; i < HPW; ++i) s[i] *= p.scale_log2;  // log2 domain
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int h = wave + 4 * hh;
-        if (h < G)
-#pragma unroll
-          for (int c = 0; c < CPL; ++c) acc[hh][c] *= alpha_s[h];
-      }
-      for (int lt = 0; lt < nv; ++lt) {
-        float v[CPL];
-        load_vn<D, CPL>(p, b, kvh, ts + lt, ns, nm, CPL * lane, v);
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int h = wave + 4 * hh;
-          if (h < G) {
-            const float pp = p_s[h][lt];
-#pragma unroll
-            for (int c = 0; c < CPL; ++c) acc[hh][c] += pp * v[c];
+      for (int i = 0; i < HPW; ++i) {
+        const int h = wave + 4 * i;
+        if (h < G) {
+          const float sc = lane < nv ? s[i] : -INFINITY;
+          const float m_new = fmaxf(m_run[i], group_max<64>(sc));
+          float alpha = 1.0f, pv = 0.0f;
+          if (m_new != -INFINITY) {
+            alpha = exp2f(m_run[i] - m_new);
+            pv = exp2f(sc - m_new);
           }
+          l_lane[i] = l_lane[i] * alpha + pv;
+          p_s[h][lane] = pv;
+          if (lane == 0) alpha_s[h] = alpha;
+          m_run[i] = m_new;
         }
+      }
+    }
+    __syncthreads();
+    // ---- PV over this thread's token slice ----
+    if (ph < G) {
+      const float al = alpha_s[ph];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] *= al;
+      const int r0 = pq * TPS;
+      const int r1 = r0 + TPS < nv ? r0 + TPS : nv;
+      for (int r = r0; r < r1; ++r) {
+        const float pp = p_s[ph][r];
+        float v8[8];
+        unpack8h(*reinterpret_cast<const uint4*>(&vt[r][8 * pc]), v8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = fmaf(pp, v8[j], acc[j]);
       }
     }
     __syncthreads();
   }
 
+  // ---- partial (m, l, acc) of each head ----
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const int h = wave + 4 * hh;
+  for (int i = 0; i < HPW; ++i) {
+    const int h = wave + 4 * i;
     if (h < G) {
-      const float l = group_sum<64>(l_lane[hh]);
-      const int64_t idx = (b * p.Hq + kvh * G + h) * p.n_splits + split;
+      const float l = group_sum<64>(l_lane[i]);
       if (lane == 0) {
-        p.ws_ml[2 * idx] = m_run[hh];
+        const int64_t idx = (b * p.Hq + kvh * G + h) * p.n_splits + split;
+        p.ws_ml[2 * idx] = m_run[i];
         p.ws_ml[2 * idx + 1] = l;
       }
-      if (lane < LANES)
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) p.ws_acc[idx * D + CPL * lane + c] = acc[hh][c];
     }
+  }
+  if (TQ > 1) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) red[TQ > 1 ? pq : 0][po][j] = acc[j];
+    __syncthreads();
+    for (int o = tid; o < NU * 8; o += kThreads) {
+      const int oo = o / 8, j = o % 8, h = oo / CG, cg = oo % CG;
+      if (h < G) {
+        float sum = 0.0f;
+        for (int q = 0; q < TQ; ++q) sum += red[q][oo][j];
+        const int64_t idx = (b * p.Hq + kvh * G + h) * p.n_splits + split;
+        p.ws_acc[idx * D + 8 * cg + j] = sum;
+      }
+    }
+  } else if (ph < G) {
+    const int64_t idx = (b * p.Hq + kvh * G + ph) * p.n_splits + split;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) p.ws_acc[idx * D + 8 * pc + j] = acc[j];
   }
 }
 
@@ -291,13 +416,21 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const float* __rest
 int launch_valu(const Params& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv),
                   static_cast<unsigned>(p.B));
+  const bool h8 = p.G > 4;
+  const bool s44 = p.mid.fmt == FADE_MID_SYM && p.mid.k_bits == 4 && p.mid.v_bits == 4;
+#define FADE_VALU_LAUNCH(DD)                                                                          \
+  if (h8 && s44) hipLaunchKernelGGL((decode_valu_kernel<DD, 8, true>), grid, dim3(kThreads), 0, st, p);  \
+  else if (h8) hipLaunchKernelGGL((decode_valu_kernel<DD, 8, false>), grid, dim3(kThreads), 0, st, p);   \
+  else if (s44) hipLaunchKernelGGL((decode_valu_kernel<DD, 4, true>), grid, dim3(kThreads), 0, st, p);   \
+  else hipLaunchKernelGGL((decode_valu_kernel<DD, 4, false>), grid, dim3(kThreads), 0, st, p);
   switch (p.D) {
-    case 32: hipLaunchKernelGGL(decode_valu_kernel<32>, grid, dim3(kThreads), 0, st, p); break;
-    case 64: hipLaunchKernelGGL(decode_valu_kernel<64>, grid, dim3(kThreads), 0, st, p); break;
-    case 128: hipLaunchKernelGGL(decode_valu_kernel<128>, grid, dim3(kThreads), 0, st, p); break;
-    case 256: hipLaunchKernelGGL(decode_valu_kernel<256>, grid, dim3(kThreads), 0, st, p); break;
+    case 32: FADE_VALU_LAUNCH(32) break;
+    case 64: FADE_VALU_LAUNCH(64) break;
+    case 128: FADE_VALU_LAUNCH(128) break;
+    case 256: FADE_VALU_LAUNCH(256) break;
     default: return einval("fade_tiered_decode_attn: head_dim must be 32, 64, 128 or 256, got %d", p.D);
   }
+#undef FADE_VALU_LAUNCH
   return check_launch("fade_tiered_decode_attn(valu)");
 }
 
