@@ -165,6 +165,8 @@ _SIGNATURES: dict[str, list] = {
     "fade_dequant_sym_dtype": [_p, _p, _i32, _i32, _i32, _i64, _i64, _i64, _i64, _p, _p],
     "fade_quant_int2_grouped": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p],
     "fade_dequant_int2_grouped": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
+    "fade_quant_int2_grouped_dtype": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p],
+    "fade_dequant_int2_grouped_dtype": [_p, _p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
     "fade_quant_rotated_workspace_bytes": [_i64, _i64, _i64, _i64, _i32, _pi64],
     "fade_quant_rotated": [_p, _i64, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _i64, _p],
     "fade_rotate_quant_workspace_bytes": [_i64, _i64, _i64, _i64, _i32, _pi64],
@@ -174,6 +176,10 @@ _SIGNATURES: dict[str, list] = {
     "fade_rerope_gather": [
         _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
         _p, _i64, _p, _p, _p, _p, _p, _p, _p,
+    ],
+    "fade_rerope_gather_dtype": [
+        _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+        _p, _i64, _p, _p, _p, _p, _p, _p, _i32, _p,
     ],
     "fade_tiered_decode_workspace_bytes": [ctypes.POINTER(DecodeArgs), _pi64],
     "fade_tiered_decode_attn": [ctypes.POINTER(DecodeArgs), _p],

@@ -141,7 +141,11 @@ class TieredKVCache(DynamicCache):
 
     Shared-tier mode (``tiers`` is ``[S]`` for all rows and heads) and
     per-sequence mode (``apply_tier_assignment_per_sequence``) as in the
-    reference.  Only float16 caches are supported by the kernels.
+    reference.  ``dtype`` float16, bfloat16 or float32, as the reference's:
+    every tier, scale and dequantized copy is of it.  The fused attention
+    kernels (``fused`` mode), the device reassignment and the ragged layout
+    read float16 caches; the others use the host reassignment (the HIP
+    quantizers and re-RoPE kernel at their dtype).
     """
 
     def __init__(
@@ -161,8 +165,8 @@ class TieredKVCache(DynamicCache):
         quant_backend: str | QuantBackend = "int4",
     ) -> None:
         super().__init__()
-        if dtype != torch.float16:
-            raise ValueError(f"fade_amd TieredKVCache supports dtype=torch.float16 only, got {dtype}")
+        if dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise ValueError(f"fade_amd TieredKVCache supports float16, bfloat16 and float32, got {dtype}")
         self.n_sink = n_sink
         self.recent_window = recent_window
         self.int4_budget = int4_budget
@@ -258,6 +262,10 @@ class TieredKVCache(DynamicCache):
         if self.fused:
             from .hf_attention import set_active_cache
 
+            if self.dtype != torch.float16:
+                raise NotImplementedError(
+                    f"fused attention reads float16 caches; this one is {self.dtype} (use the model's own attention)"
+                )
             set_active_cache(self)
             return key_states, value_states
         return self._materialize(layer_idx)
@@ -580,9 +588,9 @@ class TieredKVCache(DynamicCache):
         if self.cache_dequant and st.int4_k_deq is not None:
             return st.int4_k_deq, st.int4_v_deq
         kq, ks, vq, vs = self._mid_padded(st)
-        k = dequant_int4(kq, ks)
+        k = dequant_int4(kq, ks, dtype=self.dtype)
         if self.middle_v_bits == 4:
-            v = dequant_int4(vq, vs)
+            v = dequant_int4(vq, vs, dtype=self.dtype)
         else:
             n = int(st.int4_pos.shape[0])
             v = dequant_int2_trimmed(st.int4_vq, st.int4_vs, n, DEFAULT_INT2_GROUP_SIZE)
@@ -695,6 +703,7 @@ class TieredKVCache(DynamicCache):
         dev = (k if k is not None else st.int4_kq).device
         return (
             self.device_reassign
+            and self.dtype == torch.float16  # the device gather writes fp16 tiers
             and dev.type == "cuda"
             and isinstance(self._quant_backend, SymmetricINT4Backend)
             and self.middle_k_bits == 4
@@ -733,7 +742,7 @@ class TieredKVCache(DynamicCache):
         B, H, n, D = v_new_f16.shape
         dev = v_new_f16.device
         vq = torch.empty(B, H, n, D // 2, dtype=torch.uint8, device=dev)
-        vs = torch.empty(B, H, n, 1, dtype=torch.float16, device=dev)
+        vs = torch.empty(B, H, n, 1, dtype=v_new_f16.dtype, device=dev)
         if slots.numel():
             si, ri = slots.to(dev), rows.to(dev)
             vq.index_copy_(2, si, old_v[0].index_select(2, ri))
@@ -1039,6 +1048,8 @@ class TieredKVCache(DynamicCache):
         if not isinstance(self._quant_backend, SymmetricINT4Backend) or self.middle_v_bits != 4 \
                 or st.int2_kq is not None or st.backend_k is not None:
             raise NotImplementedError("ragged_layout: the reference INT4 middle tier only (no INT2 tier / backend)")
+        if self.dtype != torch.float16:
+            raise NotImplementedError(f"ragged_layout: float16 caches only, this one is {self.dtype}")
         midp = self._mid_padded(st)  # a paged middle is read back as the padded tensors
         if st.lens is None:
             if st.sink_k is not None:
@@ -1205,7 +1216,7 @@ class TieredKVCache(DynamicCache):
         Returns False, with the layer untouched, where it does not apply (another
         middle format or backend, an INT2 tier, tiers other than FP16 / INT4 / EVICT)."""
         st = self._layers[layer_idx]
-        if (not isinstance(self._quant_backend, SymmetricINT4Backend) or self.middle_v_bits != 4
+        if (self.dtype != torch.float16 or not isinstance(self._quant_backend, SymmetricINT4Backend) or self.middle_v_bits != 4
                 or st.int2_kq is not None or st.backend_k is not None or st.lens is not None
                 or self.page_pool is not None or st._padded_rows):
             return False
@@ -1354,6 +1365,13 @@ class TieredKVCache(DynamicCache):
         sink = (st.fp16_k[..., :ns, :], st.fp16_v[..., :ns, :]) if ns > 0 else None
         return sink, (st.fp16_k[..., ns:, :], st.fp16_v[..., ns:, :])
 
+    def _require_f16_tiers(self, op: str) -> None:
+        if self.dtype != torch.float16:
+            raise NotImplementedError(
+                f"{op}: the tiered attention kernels read float16 tiers; this cache is {self.dtype} "
+                "(attend over the materialized K/V instead)"
+            )
+
     def prefill_attention(self, q: Tensor, layer_idx: int, sm_scale: float | None = None) -> Tensor:
         """Causal attention of a chunk ``q`` [B, Hq, Sq, D] whose K/V are the last Sq
         tokens of this layer's fp16 tier (just appended by ``update``), over
@@ -1363,6 +1381,7 @@ class TieredKVCache(DynamicCache):
         from .kernels.prefill import tiered_prefill_attention
         from .kernels.tiered_attn import MiddleTier
 
+        self._require_f16_tiers("prefill_attention")
         st = self._layers[layer_idx]
         if st.lens is not None:
             return self._prefill_attention_ragged(q, st, sm_scale)
@@ -1466,6 +1485,7 @@ class TieredKVCache(DynamicCache):
         """
         from .kernels.tiered_attn import MiddleTier, TieredDecodePlan, tiered_decode_attention
 
+        self._require_f16_tiers("decode_attention")
         st = self._layers[layer_idx]
         if st.lens is not None:
             if st.mid_table is not None:  # paged: the kernel reads the pool through the block table

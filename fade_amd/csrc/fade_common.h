@@ -42,6 +42,26 @@ __device__ __forceinline__ uint16_t f2bf(float x) {
 }
 __device__ __forceinline__ float round_bf16(float x) { return bf2f(f2bf(x)); }
 
+// Float elements of a cache dtype: fp16 as raw uint16_t bits, bf16 as the
+// Bf16 tag, fp32 as float.
+struct Bf16 {
+  uint16_t bits;
+};
+__device__ __forceinline__ float to_f32(uint16_t h) { return h2f(h); }
+__device__ __forceinline__ float to_f32(Bf16 b) { return bf2f(b.bits); }
+__device__ __forceinline__ float to_f32(float x) { return x; }
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);  // round to nearest even
+template <>
+__device__ __forceinline__ uint16_t from_f32<uint16_t>(float x) { return f2h(x); }
+template <>
+__device__ __forceinline__ Bf16 from_f32<Bf16>(float x) { return Bf16{f2bf(x)}; }
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+// one rounding of an fp32 value to T and back
+template <typename T>
+__device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<T>(x)); }
+
 // Reduction across `width` consecutive lanes (width a power of two <= 64).
 template <int WIDTH>
 __device__ __forceinline__ float group_max(float v) {

@@ -11,6 +11,8 @@
 //     qmax / absmax is reciprocal-then-multiply (two roundings);
 //   fp32 (rotated) inputs: each op one fp32 rounding.
 // This file is compiled with -ffp-contract=off and IEEE fp32 division.
+#include <type_traits>
+
 #include "fade_common.h"
 
 namespace fade {
@@ -22,9 +24,6 @@ constexpr int kBlock = 256;
 // scale stored as fp16 (MODE_F32), as fp32 (MODE_F32S) or as bf16
 // (MODE_F32B): one rounding of absmax / qmax to the stored type.
 enum { MODE_F16 = 0, MODE_F32 = 1, MODE_BF16 = 2, MODE_F32S = 3, MODE_F32B = 4 };
-struct Bf16 {  // bf16 elements (raw bits)
-  uint16_t bits;
-};
 // Storage of the emitted scale: 16-bit (fp16 or bf16 bits) or fp32.
 template <int MODE>
 struct ScaleOf {
@@ -330,36 +329,47 @@ __global__ __launch_bounds__(kBlock) void dequant_sym_kernel(const uint8_t* __re
 
 // ------------------------------------------------ grouped INT2 (reference)
 // One block per (group, b*h); one thread per channel.  Rows >= S are zero.
-__global__ void quant_int2_grouped_kernel(const uint16_t* __restrict__ x, int64_t H, int64_t S,
+// T: uint16_t (fp16 bits), Bf16 or float; the scale is stored in the same format
+// (MODE = Int2Mode<T>::value).  MODE is a plain int template argument: an
+// expression over the unnamed mode enum in the signature would be mangled
+// differently by the host and device passes.
+template <typename T>
+struct Int2Mode {
+  static constexpr int value = std::is_same<T, Bf16>::value ? MODE_BF16
+                               : std::is_same<T, float>::value ? MODE_F32S : MODE_F16;
+};
+template <typename T, int MODE>
+__global__ void quant_int2_grouped_kernel(const T* __restrict__ x, int64_t H, int64_t S,
                                           int64_t S_pad, int64_t sb, int64_t sh, int64_t ss,
                                           int group, int8_t* __restrict__ codes,
-                                          uint16_t* __restrict__ scale) {
+                                          typename ScaleOf<MODE>::T* __restrict__ scale) {
   const int d = threadIdx.x;
   const int D = blockDim.x;
   const int64_t g = blockIdx.x, bh = blockIdx.y;
   const int64_t G = gridDim.x;
-  const uint16_t* base = x + (bh / H) * sb + (bh % H) * sh + d;
+  const T* base = x + (bh / H) * sb + (bh % H) * sh + d;
   float a = 0.0f;
   for (int i = 0; i < group; ++i) {
     const int64_t s = g * group + i;
-    const float v = s < S ? h2f(base[s * ss]) : 0.0f;
+    const float v = s < S ? to_f32(base[s * ss]) : 0.0f;
     a = absmax_nan(a, v);
   }
   float inv;
-  uint16_t sc;
-  sym_params<MODE_F16, 1>(a, inv, sc);
+  typename ScaleOf<MODE>::T sc;
+  sym_params<MODE, 1>(a, inv, sc);
   scale[(bh * G + g) * D + d] = sc;
   for (int i = 0; i < group; ++i) {
     const int64_t s = g * group + i;
-    const float v = s < S ? h2f(base[s * ss]) : 0.0f;
-    codes[(bh * S_pad + s) * D + d] = static_cast<int8_t>(sym_code<MODE_F16, -2, 1>(v, inv));
+    const float v = s < S ? to_f32(base[s * ss]) : 0.0f;
+    codes[(bh * S_pad + s) * D + d] = static_cast<int8_t>(sym_code<MODE, -2, 1>(v, inv));
   }
 }
 
+template <typename T>
 __global__ void dequant_int2_grouped_kernel(const int8_t* __restrict__ codes,
-                                            const uint16_t* __restrict__ scale, int64_t BH,
+                                            const T* __restrict__ scale, int64_t BH,
                                             int64_t S_pad, int64_t D, int64_t group, int64_t S_out,
-                                            uint16_t* __restrict__ out) {
+                                            T* __restrict__ out) {
   const int64_t n = BH * S_out * D;
   const int64_t G = S_pad / group;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
@@ -368,7 +378,7 @@ __global__ void dequant_int2_grouped_kernel(const int8_t* __restrict__ codes,
     const int64_t s = (i / D) % S_out;
     const int64_t bh = i / (D * S_out);
     const float q = static_cast<float>(codes[(bh * S_pad + s) * D + d]);
-    out[i] = f2h(q * h2f(scale[(bh * G + s / group) * D + d]));
+    out[i] = from_f32<T>(q * to_f32(scale[(bh * G + s / group) * D + d]));
   }
 }
 
@@ -783,37 +793,81 @@ FADE_API int fade_dequant_sym_dtype(const void* packed_u8, const void* scale, in
   }
 }
 
-FADE_API int fade_quant_int2_grouped(const void* x_f16, int64_t B, int64_t H, int64_t S,
-                                     int64_t S_pad, int64_t D, int64_t sb, int64_t sh, int64_t ss,
-                                     int64_t group, void* codes_i8, void* scale_f16, void* stream) {
-  int rc = check_dims("fade_quant_int2_grouped", B, H, S, D);
+namespace fade {
+namespace {
+template <typename T>
+int quant_int2_grouped(const char* fn, const void* x, int64_t B, int64_t H, int64_t S, int64_t S_pad, int64_t D,
+                       int64_t sb, int64_t sh, int64_t ss, int64_t group, void* codes_i8, void* scale, void* stream) {
+  int rc = check_dims(fn, B, H, S, D);
   if (rc) return rc;
   if (group < 1 || S_pad % group != 0 || S_pad < S)
     return einval("S=%lld must be divisible by group_size=%lld", (long long)S_pad, (long long)group);
   const int64_t BH = B * H, G = S_pad / group;
   if (BH == 0 || G == 0) return FADE_OK;
-  if (BH > 65535) return einval("fade_quant_int2_grouped: B*H=%lld exceeds 65535", (long long)BH);
-  hipLaunchKernelGGL(quant_int2_grouped_kernel, dim3(static_cast<unsigned>(G), static_cast<unsigned>(BH)),
-                     dim3(static_cast<unsigned>(D)), 0, as_stream(stream),
-                     static_cast<const uint16_t*>(x_f16), H, S, S_pad, sb, sh, ss,
-                     static_cast<int>(group), static_cast<int8_t*>(codes_i8),
-                     static_cast<uint16_t*>(scale_f16));
-  return check_launch("fade_quant_int2_grouped");
+  if (BH > 65535) return einval("%s: B*H=%lld exceeds 65535", fn, (long long)BH);
+  constexpr int MODE = Int2Mode<T>::value;
+  hipLaunchKernelGGL((quant_int2_grouped_kernel<T, MODE>), dim3(static_cast<unsigned>(G), static_cast<unsigned>(BH)),
+                     dim3(static_cast<unsigned>(D)), 0, as_stream(stream), static_cast<const T*>(x), H, S, S_pad,
+                     sb, sh, ss, static_cast<int>(group), static_cast<int8_t*>(codes_i8),
+                     static_cast<typename ScaleOf<MODE>::T*>(scale));
+  return check_launch(fn);
 }
-
-FADE_API int fade_dequant_int2_grouped(const void* codes_i8, const void* scale_f16, int64_t B,
-                                       int64_t H, int64_t S_pad, int64_t D, int64_t group,
-                                       int64_t S_out, void* out_f16, void* stream) {
+template <typename T>
+int dequant_int2_grouped(const char* fn, const void* codes_i8, const void* scale, int64_t B, int64_t H,
+                         int64_t S_pad, int64_t D, int64_t group, int64_t S_out, void* out, void* stream) {
   if (group < 1 || S_pad % group != 0 || S_out > S_pad || S_out < 0)
-    return einval("fade_dequant_int2_grouped: bad sizes (S_pad=%lld group=%lld S_out=%lld)",
-                  (long long)S_pad, (long long)group, (long long)S_out);
+    return einval("%s: bad sizes (S_pad=%lld group=%lld S_out=%lld)", fn, (long long)S_pad, (long long)group,
+                  (long long)S_out);
   const int64_t n = B * H * S_out * D;
   if (n == 0) return FADE_OK;
   const int grid = static_cast<int>(cdiv(n, 256) < 16384 ? cdiv(n, 256) : 16384);
-  hipLaunchKernelGGL(dequant_int2_grouped_kernel, dim3(grid), dim3(256), 0, as_stream(stream),
-                     static_cast<const int8_t*>(codes_i8), static_cast<const uint16_t*>(scale_f16),
-                     B * H, S_pad, D, group, S_out, static_cast<uint16_t*>(out_f16));
-  return check_launch("fade_dequant_int2_grouped");
+  hipLaunchKernelGGL(dequant_int2_grouped_kernel<T>, dim3(grid), dim3(256), 0, as_stream(stream),
+                     static_cast<const int8_t*>(codes_i8), static_cast<const T*>(scale), B * H, S_pad, D, group,
+                     S_out, static_cast<T*>(out));
+  return check_launch(fn);
+}
+}  // namespace
+}  // namespace fade
+
+FADE_API int fade_quant_int2_grouped(const void* x_f16, int64_t B, int64_t H, int64_t S,
+                                     int64_t S_pad, int64_t D, int64_t sb, int64_t sh, int64_t ss,
+                                     int64_t group, void* codes_i8, void* scale_f16, void* stream) {
+  return quant_int2_grouped<uint16_t>("fade_quant_int2_grouped", x_f16, B, H, S, S_pad, D, sb, sh, ss, group,
+                                      codes_i8, scale_f16, stream);
+}
+FADE_API int fade_quant_int2_grouped_dtype(const void* x, int32_t dtype, int64_t B, int64_t H, int64_t S,
+                                           int64_t S_pad, int64_t D, int64_t sb, int64_t sh, int64_t ss,
+                                           int64_t group, void* codes_i8, void* scale, void* stream) {
+  const char* fn = "fade_quant_int2_grouped_dtype";
+  switch (dtype) {
+    case FADE_DTYPE_F16:
+      return quant_int2_grouped<uint16_t>(fn, x, B, H, S, S_pad, D, sb, sh, ss, group, codes_i8, scale, stream);
+    case FADE_DTYPE_BF16:
+      return quant_int2_grouped<Bf16>(fn, x, B, H, S, S_pad, D, sb, sh, ss, group, codes_i8, scale, stream);
+    case FADE_DTYPE_F32:
+      return quant_int2_grouped<float>(fn, x, B, H, S, S_pad, D, sb, sh, ss, group, codes_i8, scale, stream);
+    default: return einval("%s: unknown dtype %d", fn, dtype);
+  }
+}
+FADE_API int fade_dequant_int2_grouped(const void* codes_i8, const void* scale_f16, int64_t B,
+                                       int64_t H, int64_t S_pad, int64_t D, int64_t group,
+                                       int64_t S_out, void* out_f16, void* stream) {
+  return dequant_int2_grouped<uint16_t>("fade_dequant_int2_grouped", codes_i8, scale_f16, B, H, S_pad, D, group,
+                                        S_out, out_f16, stream);
+}
+FADE_API int fade_dequant_int2_grouped_dtype(const void* codes_i8, const void* scale, int32_t dtype, int64_t B,
+                                             int64_t H, int64_t S_pad, int64_t D, int64_t group, int64_t S_out,
+                                             void* out, void* stream) {
+  const char* fn = "fade_dequant_int2_grouped_dtype";
+  switch (dtype) {
+    case FADE_DTYPE_F16:
+      return dequant_int2_grouped<uint16_t>(fn, codes_i8, scale, B, H, S_pad, D, group, S_out, out, stream);
+    case FADE_DTYPE_BF16:
+      return dequant_int2_grouped<Bf16>(fn, codes_i8, scale, B, H, S_pad, D, group, S_out, out, stream);
+    case FADE_DTYPE_F32:
+      return dequant_int2_grouped<float>(fn, codes_i8, scale, B, H, S_pad, D, group, S_out, out, stream);
+    default: return einval("%s: unknown dtype %d", fn, dtype);
+  }
 }
 
 FADE_API int fade_quant_rotated_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D,

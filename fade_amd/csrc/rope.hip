@@ -7,22 +7,23 @@
 // each thread owns the pair (i, i + D/2) of one kept row, which is exactly
 // the pair that rotate_half mixes, and performs both rotations in registers
 // with the reference's rounding (three separately rounded fp32 ops per
-// rotation, fp16 rounding in between; compiled with -ffp-contract=off).
-// V rows are gathered in the same launch.
+// rotation, a rounding to the cache dtype -- fp16, bf16 or none for fp32 -- in between;
+// compiled with -ffp-contract=off).  V rows are gathered in the same launch.
 #include "fade_common.h"
 
 namespace fade {
 namespace {
 
-__global__ void rerope_gather_kernel(const uint16_t* __restrict__ k, int64_t ksb, int64_t ksh,
-                                     int64_t kss, const uint16_t* __restrict__ v, int64_t vsb,
+template <typename T>
+__global__ void rerope_gather_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh,
+                                     int64_t kss, const T* __restrict__ v, int64_t vsb,
                                      int64_t vsh, int64_t vss, int64_t H, int64_t S, int D,
                                      const int64_t* __restrict__ keep, int64_t n_kept,
                                      const float* __restrict__ cos_old,
                                      const float* __restrict__ sin_old,
                                      const float* __restrict__ cos_new,
-                                     const float* __restrict__ sin_new, uint16_t* __restrict__ k_out,
-                                     uint16_t* __restrict__ v_out) {
+                                     const float* __restrict__ sin_new, T* __restrict__ k_out,
+                                     T* __restrict__ v_out) {
   const int half = D / 2;
   const int rows_per_block = blockDim.x / half;
   const int i = threadIdx.x % half;
@@ -30,28 +31,28 @@ __global__ void rerope_gather_kernel(const uint16_t* __restrict__ k, int64_t ksb
   const int64_t bh = blockIdx.y;
   if (j >= n_kept) return;
   const int64_t src = keep[j];
-  uint16_t* ko = k_out + (bh * n_kept + j) * D;
-  uint16_t* vo = v_out ? v_out + (bh * n_kept + j) * D : nullptr;
+  T* ko = k_out + (bh * n_kept + j) * D;
+  T* vo = v_out ? v_out + (bh * n_kept + j) * D : nullptr;
   if (src < 0 || src >= S) {  // never produced by the host; keep the access in bounds
-    ko[i] = ko[i + half] = 0;
-    if (vo) vo[i] = vo[i + half] = 0;
+    ko[i] = ko[i + half] = from_f32<T>(0.0f);
+    if (vo) vo[i] = vo[i + half] = from_f32<T>(0.0f);
     return;
   }
-  const uint16_t* kr = k + (bh / H) * ksb + (bh % H) * ksh + src * kss;
-  const float a = h2f(kr[i]);         // k[i]
-  const float b = h2f(kr[i + half]);  // k[i + D/2]
+  const T* kr = k + (bh / H) * ksb + (bh % H) * ksh + src * kss;
+  const float a = to_f32(kr[i]);         // k[i]
+  const float b = to_f32(kr[i + half]);  // k[i + D/2]
   // inverse: k*cos - rotate_half(k)*sin, rotate_half(k) = [-k2, k1]
   const float* co = cos_old + src * D;
   const float* so = sin_old + src * D;
-  const float u_lo = round_f16(a * co[i] - (-b) * so[i]);
-  const float u_hi = round_f16(b * co[i + half] - a * so[i + half]);
+  const float u_lo = round_to<T>(a * co[i] - (-b) * so[i]);
+  const float u_hi = round_to<T>(b * co[i + half] - a * so[i + half]);
   // apply: k*cos + rotate_half(k)*sin at the new position
   const float* cn = cos_new + j * D;
   const float* sn = sin_new + j * D;
-  ko[i] = f2h(u_lo * cn[i] + (-u_hi) * sn[i]);
-  ko[i + half] = f2h(u_hi * cn[i + half] + u_lo * sn[i + half]);
+  ko[i] = from_f32<T>(u_lo * cn[i] + (-u_hi) * sn[i]);
+  ko[i + half] = from_f32<T>(u_hi * cn[i + half] + u_lo * sn[i + half]);
   if (vo) {
-    const uint16_t* vr = v + (bh / H) * vsb + (bh % H) * vsh + src * vss;
+    const T* vr = v + (bh / H) * vsb + (bh % H) * vsh + src * vss;
     vo[i] = vr[i];
     vo[i + half] = vr[i + half];
   }
@@ -62,28 +63,57 @@ __global__ void rerope_gather_kernel(const uint16_t* __restrict__ k, int64_t ksb
 
 using namespace fade;
 
+namespace fade {
+namespace {
+template <typename T>
+int rerope_gather(const char* fn, const void* k, int64_t ksb, int64_t ksh, int64_t kss, const void* v, int64_t vsb,
+                  int64_t vsh, int64_t vss, int64_t B, int64_t H, int64_t S, int64_t D, const int64_t* keep_idx,
+                  int64_t n_kept, const float* cos_old, const float* sin_old, const float* cos_new,
+                  const float* sin_new, void* k_out, void* v_out, void* stream) {
+  if (D <= 0 || D % 2 != 0 || D > 512) return einval("%s: head_dim must be even and <= 512, got %lld", fn, (long long)D);
+  if (n_kept < 0 || n_kept > S)
+    return einval("%s: n_kept=%lld out of range for S=%lld", fn, (long long)n_kept, (long long)S);
+  if ((v == nullptr) != (v_out == nullptr)) return einval("%s: v and v_out must both be given or both be NULL", fn);
+  const int64_t BH = B * H;
+  if (BH == 0 || n_kept == 0) return FADE_OK;
+  if (BH > 65535) return einval("%s: B*H=%lld exceeds 65535", fn, (long long)BH);
+  const int half = static_cast<int>(D / 2);
+  const int rpb = half >= 256 ? 1 : 256 / half;
+  const dim3 grid(static_cast<unsigned>(cdiv(n_kept, rpb)), static_cast<unsigned>(BH));
+  hipLaunchKernelGGL(rerope_gather_kernel<T>, grid, dim3(rpb * half), 0, as_stream(stream), static_cast<const T*>(k),
+                     ksb, ksh, kss, static_cast<const T*>(v), vsb, vsh, vss, H, S, static_cast<int>(D), keep_idx,
+                     n_kept, cos_old, sin_old, cos_new, sin_new, static_cast<T*>(k_out), static_cast<T*>(v_out));
+  return check_launch(fn);
+}
+}  // namespace
+}  // namespace fade
+
 FADE_API int fade_rerope_gather(const void* k_f16, int64_t ksb, int64_t ksh, int64_t kss,
                                 const void* v_f16, int64_t vsb, int64_t vsh, int64_t vss, int64_t B,
                                 int64_t H, int64_t S, int64_t D, const int64_t* keep_idx,
                                 int64_t n_kept, const float* cos_old, const float* sin_old,
                                 const float* cos_new, const float* sin_new, void* k_out_f16,
                                 void* v_out_f16, void* stream) {
-  if (D <= 0 || D % 2 != 0 || D > 512)
-    return einval("fade_rerope_gather: head_dim must be even and <= 512, got %lld", (long long)D);
-  if (n_kept < 0 || n_kept > S)
-    return einval("fade_rerope_gather: n_kept=%lld out of range for S=%lld", (long long)n_kept, (long long)S);
-  if ((v_f16 == nullptr) != (v_out_f16 == nullptr))
-    return einval("fade_rerope_gather: v and v_out must both be given or both be NULL");
-  const int64_t BH = B * H;
-  if (BH == 0 || n_kept == 0) return FADE_OK;
-  if (BH > 65535) return einval("fade_rerope_gather: B*H=%lld exceeds 65535", (long long)BH);
-  const int half = static_cast<int>(D / 2);
-  const int rpb = half >= 256 ? 1 : 256 / half;
-  const dim3 grid(static_cast<unsigned>(cdiv(n_kept, rpb)), static_cast<unsigned>(BH));
-  hipLaunchKernelGGL(rerope_gather_kernel, grid, dim3(rpb * half), 0, as_stream(stream),
-                     static_cast<const uint16_t*>(k_f16), ksb, ksh, kss,
-                     static_cast<const uint16_t*>(v_f16), vsb, vsh, vss, H, S, static_cast<int>(D),
-                     keep_idx, n_kept, cos_old, sin_old, cos_new, sin_new,
-                     static_cast<uint16_t*>(k_out_f16), static_cast<uint16_t*>(v_out_f16));
-  return check_launch("fade_rerope_gather");
+  return rerope_gather<uint16_t>("fade_rerope_gather", k_f16, ksb, ksh, kss, v_f16, vsb, vsh, vss, B, H, S, D,
+                                 keep_idx, n_kept, cos_old, sin_old, cos_new, sin_new, k_out_f16, v_out_f16, stream);
+}
+
+FADE_API int fade_rerope_gather_dtype(const void* k, int64_t ksb, int64_t ksh, int64_t kss, const void* v,
+                                      int64_t vsb, int64_t vsh, int64_t vss, int64_t B, int64_t H, int64_t S,
+                                      int64_t D, const int64_t* keep_idx, int64_t n_kept, const float* cos_old,
+                                      const float* sin_old, const float* cos_new, const float* sin_new,
+                                      void* k_out, void* v_out, int32_t dtype, void* stream) {
+  const char* fn = "fade_rerope_gather_dtype";
+  switch (dtype) {
+    case FADE_DTYPE_F16:
+      return rerope_gather<uint16_t>(fn, k, ksb, ksh, kss, v, vsb, vsh, vss, B, H, S, D, keep_idx, n_kept, cos_old,
+                                     sin_old, cos_new, sin_new, k_out, v_out, stream);
+    case FADE_DTYPE_BF16:
+      return rerope_gather<Bf16>(fn, k, ksb, ksh, kss, v, vsb, vsh, vss, B, H, S, D, keep_idx, n_kept, cos_old,
+                                 sin_old, cos_new, sin_new, k_out, v_out, stream);
+    case FADE_DTYPE_F32:
+      return rerope_gather<float>(fn, k, ksb, ksh, kss, v, vsb, vsh, vss, B, H, S, D, keep_idx, n_kept, cos_old,
+                                  sin_old, cos_new, sin_new, k_out, v_out, stream);
+    default: return einval("%s: unknown dtype %d", fn, dtype);
+  }
 }

@@ -184,7 +184,7 @@ def quant_v_int4(v: Tensor) -> tuple[Tensor, Tensor]:
 
 
 def _quant_int2_grouped(x: Tensor, group_size: int, op: str, s_actual: int | None = None):
-    x = _prep_f16(x, op)
+    x = _prep_kv(x, op)
     B, H, S, D = x.shape
     s_pad = S
     if s_actual is None:
@@ -194,14 +194,20 @@ def _quant_int2_grouped(x: Tensor, group_size: int, op: str, s_actual: int | Non
         s_pad = S + (-S) % group_size
     G = s_pad // group_size
     codes = torch.empty(B, H, s_pad, D, dtype=torch.int8, device=x.device)
-    scale = torch.empty(B, H, G, D, dtype=torch.float16, device=x.device)
+    scale = torch.empty(B, H, G, D, dtype=x.dtype, device=x.device)
     if codes.numel() == 0:
         return codes, scale
     sb, sh, ss = _strides_bhs(x)
-    _lib.call(
-        "fade_quant_int2_grouped", x.data_ptr(), B, H, S, s_pad, D, sb, sh, ss, group_size,
-        codes.data_ptr(), scale.data_ptr(), _lib.stream_of(x),
-    )
+    if x.dtype == torch.float16:
+        _lib.call(
+            "fade_quant_int2_grouped", x.data_ptr(), B, H, S, s_pad, D, sb, sh, ss, group_size,
+            codes.data_ptr(), scale.data_ptr(), _lib.stream_of(x),
+        )
+    else:
+        _lib.call(
+            "fade_quant_int2_grouped_dtype", x.data_ptr(), _lib.DTYPE_CODES[x.dtype], B, H, S, s_pad, D, sb, sh,
+            ss, group_size, codes.data_ptr(), scale.data_ptr(), _lib.stream_of(x),
+        )
     return codes, scale
 
 
@@ -273,19 +279,25 @@ def dequant_int4(packed: Tensor, scale: Tensor, dtype: torch.dtype = torch.float
 def _dequant_int2(q: Tensor, scale: Tensor, group_size: int, dtype, s_out: int | None = None) -> Tensor:
     _check_4d(q, "dequant_int2")
     _lib.require_gpu(q, scale, op="dequant_int2")
-    if dtype != torch.float16:
-        raise ValueError(f"fade_amd dequantizes to float16 only, got {dtype}")
+    if dtype not in _lib.DTYPE_CODES:
+        raise ValueError(f"fade_amd dequantizes to float16, bfloat16 or float32, got {dtype}")
     B, H, S, D = q.shape
     s_out = S if s_out is None else s_out
-    out = torch.empty(B, H, s_out, D, dtype=torch.float16, device=q.device)
+    out = torch.empty(B, H, s_out, D, dtype=dtype, device=q.device)
     if out.numel() == 0:
         return out
     q = q.contiguous()
-    scale = scale.contiguous()
-    _lib.call(
-        "fade_dequant_int2_grouped", q.data_ptr(), scale.data_ptr(), B, H, S, D, group_size, s_out,
-        out.data_ptr(), _lib.stream_of(q),
-    )
+    scale = scale.to(dtype).contiguous()  # q.to(dtype) * scale.to(dtype)
+    if dtype == torch.float16:
+        _lib.call(
+            "fade_dequant_int2_grouped", q.data_ptr(), scale.data_ptr(), B, H, S, D, group_size, s_out,
+            out.data_ptr(), _lib.stream_of(q),
+        )
+    else:
+        _lib.call(
+            "fade_dequant_int2_grouped_dtype", q.data_ptr(), scale.data_ptr(), _lib.DTYPE_CODES[dtype], B, H, S, D,
+            group_size, s_out, out.data_ptr(), _lib.stream_of(q),
+        )
     return out
 
 
@@ -301,7 +313,7 @@ def dequant_v_int2(q, scale, group_size: int = DEFAULT_INT2_GROUP_SIZE, dtype=to
 
 def dequant_int2_trimmed(q, scale, n: int, group_size: int = DEFAULT_INT2_GROUP_SIZE) -> Tensor:
     """Dequantize and drop the ``pad_to_group`` rows in one pass (fade/cache.py:834-837, 868-872)."""
-    return _dequant_int2(q, scale, group_size, torch.float16, s_out=n)
+    return _dequant_int2(q, scale, group_size, scale.dtype, s_out=n)
 
 
 def pad_to_group(x: Tensor, group_size: int) -> tuple[Tensor, int]:

@@ -317,12 +317,13 @@ def rerope_gather(
 ) -> tuple[Tensor, Tensor | None]:
     """Fused eviction re-RoPE of the kept rows (fade/cache.py:911-935).
 
-    ``k``/``v``: [B, H, S, D] fp16 on the GPU (K post-RoPE at its old
+    ``k``/``v``: [B, H, S, D] fp16, bf16 or fp32 on the GPU (K post-RoPE at its old
     positions); ``keep_idx``: ascending int64 indices of kept rows;
     ``cos_old``/``sin_old``: [S, D] fp32 tables of the old positions;
     ``cos_new``/``sin_new``: [n_kept, D] tables of the new positions.
     Returns K re-RoPE'd at the new positions and the gathered V, both
-    [B, H, n_kept, D] fp16.
+    [B, H, n_kept, D] in K's dtype (the rounding between the two rotations
+    is to that dtype, as the reference's casts to k.dtype).
     """
     from . import _lib
 
@@ -331,7 +332,10 @@ def rerope_gather(
         raise ValueError(f"key_states must be [B, H, S, D]; got shape {tuple(k.shape)}")
     if v is not None and v.shape != k.shape:
         raise ValueError(f"K/V shape mismatch: {tuple(k.shape)} vs {tuple(v.shape)}")
-    _lib.require_f16(k, "rerope_gather")
+    if k.dtype not in _lib.DTYPE_CODES:
+        raise ValueError(f"rerope_gather: expected a float16, bfloat16 or float32 tensor, got {k.dtype}")
+    if v is not None and v.dtype != k.dtype:
+        raise ValueError(f"rerope_gather: K and V dtypes differ ({k.dtype}, {v.dtype})")
     B, H, S, D = k.shape
     n = int(keep_idx.shape[0])
     dev = k.device
@@ -349,12 +353,20 @@ def rerope_gather(
             v = v.contiguous()
         v_out = torch.empty(B, H, n, D, dtype=v.dtype, device=dev)
         vs = (v.stride(0), v.stride(1), v.stride(2))
-    _lib.call(
-        "fade_rerope_gather", k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
-        _lib.ptr(v), *vs, B, H, S, D, keep_idx.data_ptr(), n,
-        tabs[0].data_ptr(), tabs[1].data_ptr(), tabs[2].data_ptr(), tabs[3].data_ptr(),
-        k_out.data_ptr(), _lib.ptr(v_out), _lib.stream_of(k),
-    )
+    if k.dtype == torch.float16:
+        _lib.call(
+            "fade_rerope_gather", k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+            _lib.ptr(v), *vs, B, H, S, D, keep_idx.data_ptr(), n,
+            tabs[0].data_ptr(), tabs[1].data_ptr(), tabs[2].data_ptr(), tabs[3].data_ptr(),
+            k_out.data_ptr(), _lib.ptr(v_out), _lib.stream_of(k),
+        )
+    else:
+        _lib.call(
+            "fade_rerope_gather_dtype", k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+            _lib.ptr(v), *vs, B, H, S, D, keep_idx.data_ptr(), n,
+            tabs[0].data_ptr(), tabs[1].data_ptr(), tabs[2].data_ptr(), tabs[3].data_ptr(),
+            k_out.data_ptr(), _lib.ptr(v_out), _lib.DTYPE_CODES[k.dtype], _lib.stream_of(k),
+        )
     return k_out, v_out
 
 

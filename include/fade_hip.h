@@ -118,6 +118,15 @@ int fade_quant_int2_grouped(const void* x_f16, int64_t B, int64_t H, int64_t S, 
 int fade_dequant_int2_grouped(const void* codes_i8, const void* scale_f16, int64_t B, int64_t H,
                               int64_t S_pad, int64_t D, int64_t group, int64_t S_out,
                               void* out_f16, void* stream);
+/* The same two for a bfloat16 or float32 cache (fade/quant.py:95-176 on a
+ * tensor of that dtype): each op rounds to the dtype, the scale and the
+ * dequantized output are of it.  dtype is a FADE_DTYPE_*. */
+int fade_quant_int2_grouped_dtype(const void* x, int32_t dtype, int64_t B, int64_t H, int64_t S, int64_t S_pad,
+                                  int64_t D, int64_t sb, int64_t sh, int64_t ss, int64_t group, void* codes_i8,
+                                  void* scale, void* stream);
+int fade_dequant_int2_grouped_dtype(const void* codes_i8, const void* scale, int32_t dtype, int64_t B, int64_t H,
+                                    int64_t S_pad, int64_t D, int64_t group, int64_t S_out, void* out,
+                                    void* stream);
 
 /* ---------------- rotated symmetric on fp32 (fade/rotated_quant.py:106-173) */
 /* x_rot [B,H,S,D] fp32 contiguous (x.float() @ R.T) -> packed codes at
@@ -169,6 +178,14 @@ int fade_rerope_gather(const void* k_f16, int64_t ksb, int64_t ksh, int64_t kss,
                        int64_t D, const int64_t* keep_idx, int64_t n_kept, const float* cos_old,
                        const float* sin_old, const float* cos_new, const float* sin_new,
                        void* k_out_f16, void* v_out_f16, void* stream);
+/* fade_rerope_gather for a bfloat16 or float32 cache: the same fp32 ops,
+ * rounded to the cache dtype where the reference casts to k.dtype
+ * (fade/cache.py:311, 935; no rounding for float32).  dtype is a FADE_DTYPE_*. */
+int fade_rerope_gather_dtype(const void* k, int64_t ksb, int64_t ksh, int64_t kss, const void* v, int64_t vsb,
+                             int64_t vsh, int64_t vss, int64_t B, int64_t H, int64_t S, int64_t D,
+                             const int64_t* keep_idx, int64_t n_kept, const float* cos_old, const float* sin_old,
+                             const float* cos_new, const float* sin_new, void* k_out, void* v_out, int32_t dtype,
+                             void* stream);
 
 /* ---------------- device-side tier reassignment --------------------------- */
 /* fade/cache.py:881-1057 (apply_tier_assignment, shared tiers) for the

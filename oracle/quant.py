@@ -255,6 +255,32 @@ def quant_v_int4_typed(v, dtype: str):
     return _sym_quant_typed(v, dtype, -1)
 
 
+def quant_int2_grouped_typed(x, dtype: str, group_size: int = DEFAULT_INT2_GROUP_SIZE):
+    """fade/quant.py:95-112 / 130-150 on a ``dtype`` tensor: codes [B,H,S,D] int8 and
+    scale [B,H,S/group,D] of ``dtype`` (each op rounded to it, the clamp live on bf16)."""
+    x32 = to_f32(x, dtype)
+    B, H, S, D = x32.shape
+    if S % group_size != 0:
+        raise ValueError(f"S={S} must be divisible by group_size={group_size}")
+    G = S // group_size
+    xg = x32.reshape(B, H, G, group_size, D)
+    absmax = np.abs(xg).max(axis=-2, keepdims=True)
+    inv, scale = _sym_params_typed(absmax, INT2_MAX, dtype)
+    with np.errstate(invalid="ignore", over="ignore"):
+        prod = _rnd(xg * inv, dtype)
+    q = _rne_clamp(prod, INT2_MIN, INT2_MAX)
+    return q.reshape(B, H, S, D), scale.reshape(B, H, G, D)
+
+
+def dequant_int2_typed(q: np.ndarray, scale, dtype: str, group_size: int = DEFAULT_INT2_GROUP_SIZE) -> np.ndarray:
+    """fade/quant.py:153-176 at ``dtype``: ``q.to(dtype) * scale.to(dtype)`` per group."""
+    B, H, S, D = q.shape
+    G = S // group_size
+    s32 = to_f32(scale, dtype)
+    full = np.broadcast_to(s32[:, :, :, None, :], (B, H, G, group_size, D)).reshape(B, H, S, D)
+    return from_f32(q.astype(F32) * full, dtype)
+
+
 def dequant_int4_typed(packed: np.ndarray, scale, dtype: str) -> np.ndarray:
     """fade/quant.py:124-127: ``q.to(dtype) * scale.to(dtype)``, in ``dtype``'s storage."""
     q = unpack_int4_last_dim(packed).astype(F32)

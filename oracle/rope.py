@@ -73,3 +73,35 @@ def rerope_gather(k, v, keep_idx, cos_old, sin_old, cos_new, sin_new):
     out_k = apply_rope(pre, cos_new, sin_new)
     out_v = np.asarray(v)[:, :, keep_idx, :]
     return out_k, out_v
+
+
+# --------------------------------------------------------------------------- #
+# the same on a bfloat16 / float32 cache: fp32 ops, each result cast to the
+# cache dtype (fade/cache.py:290-311 cast to k.dtype); bf16 as uint16 bits
+# --------------------------------------------------------------------------- #
+def _rope_typed(k, cos, sin, dtype: str, sign: float):
+    from oracle import quant as oq
+
+    kf = oq.to_f32(k, dtype)
+    a = (kf * cos).astype(F32)
+    b = (_rotate_half(kf) * sin).astype(F32)
+    return oq.from_f32((a + F32(sign) * b).astype(F32), dtype)
+
+
+def apply_rope_typed(k, cos, sin, dtype: str):
+    """fade/cache.py:290-299 on a ``dtype`` cache."""
+    return _rope_typed(k, cos, sin, dtype, 1.0)
+
+
+def inverse_rope_typed(k, cos, sin, dtype: str):
+    """fade/cache.py:301-311 on a ``dtype`` cache."""
+    return _rope_typed(k, cos, sin, dtype, -1.0)
+
+
+def rerope_gather_typed(k, v, keep_idx, cos_old, sin_old, cos_new, sin_new, dtype: str):
+    """``rerope_gather`` on a ``dtype`` cache (K and V in that dtype's storage)."""
+    keep_idx = np.asarray(keep_idx, dtype=np.int64)
+    k_kept = np.asarray(k)[:, :, keep_idx, :]
+    pre = inverse_rope_typed(k_kept, cos_old[keep_idx], sin_old[keep_idx], dtype)
+    out_k = apply_rope_typed(pre, cos_new, sin_new, dtype)
+    return out_k, np.asarray(v)[:, :, keep_idx, :]

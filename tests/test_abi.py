@@ -3,6 +3,7 @@
 import ctypes
 import os
 import re
+import struct
 import subprocess
 
 import pytest
@@ -32,6 +33,73 @@ def test_library_exports_every_declared_symbol():
     for name in _declared_functions():
         assert hasattr(lib, name), name
     assert lib.fade_hip_abi_version() == 1
+
+
+def _elf_sections(data: bytes):
+    """{name: (offset, size, link)} of an ELF64 little-endian image."""
+    shoff = struct.unpack_from("<Q", data, 0x28)[0]
+    shentsize, shnum, shstrndx = struct.unpack_from("<HHH", data, 0x3A)
+    hdrs = [struct.unpack_from("<IIQQQQIIQQ", data, shoff + i * shentsize) for i in range(shnum)]
+    stro = hdrs[shstrndx][4]
+    out = {}
+    for h in hdrs:
+        name = data[stro + h[0] : data.index(b"\0", stro + h[0])].decode()
+        out[name] = (h[4], h[5], h[6], hdrs)
+    return out
+
+
+def _elf_symbols(data: bytes) -> set[str]:
+    secs = _elf_sections(data)
+    off, size, link, hdrs = secs[".symtab"]
+    stroff = hdrs[link][4]
+    names = set()
+    for i in range(size // 24):
+        st_name = struct.unpack_from("<I", data, off + 24 * i)[0]
+        if st_name:
+            names.add(data[stroff + st_name : data.index(b"\0", stroff + st_name)].decode())
+    return names
+
+
+def _device_symbols(lib: bytes) -> set[str]:
+    """Symbols of every gfx950 code object in the library's offload bundles."""
+    off, size, _, _ = _elf_sections(lib)[".hip_fatbin"]
+    fat = lib[off : off + size]
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    names: set[str] = set()
+    starts = [m.start() for m in re.finditer(re.escape(magic), fat)]
+    assert starts, "no offload bundle in .hip_fatbin"
+    for b in starts:
+        (n,) = struct.unpack_from("<Q", fat, b + len(magic))
+        p = b + len(magic) + 8
+        for _ in range(n):
+            eoff, esize, tlen = struct.unpack_from("<QQQ", fat, p)
+            triple = fat[p + 24 : p + 24 + tlen].decode()
+            p += 24 + tlen
+            if "gfx950" in triple:
+                names |= _elf_symbols(fat[b + eoff : b + eoff + esize])
+    return names
+
+
+def test_every_launched_kernel_is_in_the_code_object():
+    """Each kernel the host side launches (one ``__device_stub__`` per kernel)
+    names a symbol of the gfx950 code object.  A kernel whose signature the
+    host and device passes mangle differently (e.g. an expression over an
+    unnamed enum) builds and links, then aborts at its first launch."""
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} missing: run __graft_entry__.build()")
+    lib = open(_lib.LIB_PATH, "rb").read()
+    host = _elf_symbols(lib)
+    stub = re.compile(r"(\d+)__device_stub__")
+    kernels = set()
+    for name in host:
+        m = stub.search(name)
+        if m:  # mangled: <len>__device_stub__<id> -> <len-15><id>
+            kernels.add(name[: m.start()] + str(int(m.group(1)) - 15) + name[m.end() :])
+        elif name.startswith("__device_stub__"):
+            kernels.add(name[len("__device_stub__") :])
+    assert len(kernels) > 50
+    missing = sorted(kernels - _device_symbols(lib))
+    assert not missing, f"{len(missing)} launched kernels absent from the code object: {missing[:3]}"
 
 
 def test_ctypes_struct_layout_matches_c(tmp_path):

@@ -18,19 +18,32 @@ from oracle import rope as orope
 pytestmark = pytest.mark.gpu
 
 
-def _oracle_reassign(k, v, pos, tiers, scheme, n_sink):
-    """The composed state change of apply_tier_assignment, restated with the oracle."""
+_TDT = {"bf16": torch.bfloat16, "f32": torch.float32}
+
+
+def _oracle_reassign(k, v, pos, tiers, scheme, n_sink, dtype="f16"):
+    """The composed state change of apply_tier_assignment, restated with the oracle
+    (``dtype`` "bf16" / "f32": a cache of that dtype, bf16 as uint16 bits)."""
     keep = np.nonzero(tiers != TIER_EVICT)[0]
     n = keep.size
     if n < k.shape[2]:
-        co, so = scheme.host_cos_sin(torch.from_numpy(pos))
-        cn, sn = scheme.host_cos_sin(torch.arange(n))
-        k, v = orope.rerope_gather(k, v, keep, co.numpy(), so.numpy(), cn.numpy(), sn.numpy())
+        tdt = _TDT.get(dtype, torch.float16)
+        co, so = scheme.host_cos_sin(torch.from_numpy(pos), tdt)
+        cn, sn = scheme.host_cos_sin(torch.arange(n), tdt)
+        tabs = (co.numpy(), so.numpy(), cn.numpy(), sn.numpy())
+        if dtype == "f16":
+            k, v = orope.rerope_gather(k, v, keep, *tabs)
+        else:
+            k, v = orope.rerope_gather_typed(k, v, keep, *tabs, dtype)
         tiers, pos = tiers[keep], np.arange(n)
     f = np.nonzero(tiers == TIER_FP16)[0]
     i4 = np.nonzero(tiers == TIER_INT4)[0]
-    kq, ks = oq.quant_k_int4(k[:, :, i4])
-    vq, vs = oq.quant_v_int4(v[:, :, i4])
+    if dtype == "f16":
+        kq, ks = oq.quant_k_int4(k[:, :, i4])
+        vq, vs = oq.quant_v_int4(v[:, :, i4])
+    else:
+        kq, ks = oq.quant_k_int4_typed(k[:, :, i4], dtype)
+        vq, vs = oq.quant_v_int4_typed(v[:, :, i4], dtype)
     return {"fp16_k": k[:, :, f], "fp16_v": v[:, :, f], "kq": kq, "ks": ks, "vq": vq, "vs": vs,
             "int4_pos": pos[i4], "fp16_pos": pos[f], "n_sink": min(n_sink, f.size)}
 
@@ -90,6 +103,79 @@ def test_apply_tier_assignment_matches_oracle_composition(dev, budget):
     o2 = _oracle_reassign(Kp, Vp, pos2, tiers2.numpy(), scheme, 4)
     st = c._layers[0]
     assert np.array_equal(st.int4_kq.cpu().numpy(), o2["kq"]) and np.array_equal(st.int4_vq.cpu().numpy(), o2["vq"])
+
+
+def _dev_t(a, dtype, dev):
+    if dtype == "bf16":
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(dev)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _host_t(t, dtype):
+    t = t.cpu().contiguous()
+    return t.view(torch.int16).numpy().view(np.uint16) if dtype == "bf16" else t.numpy()
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_typed_cache_reassign_matches_oracle_composition(dev, dtype):
+    """A bfloat16 / float32 cache (create_tiered_cache(dtype=...)): eviction, re-RoPE
+    and INT4 requant at the cache dtype bit-exact, the materialized K/V the
+    dequantized tiers in position order, a second reassignment from them, and
+    an INT2 tier's grouped codes."""
+    print(f"case typed cache {dtype}", flush=True)
+    tdt = _TDT[dtype]
+    B, Hkv, S, D = 2, 4, 700, 128
+    _, k16, v16 = kv_tensors(B, Hkv, S, D, seed=31)
+    scheme = Vanilla(theta=1e6, head_dim=D)
+    cos, sin = scheme.host_cos_sin(torch.arange(S), tdt)
+    k = orope.apply_rope_typed(oq.from_f32(k16.float().numpy() * 1.7, dtype), cos.numpy(), sin.numpy(), dtype)
+    v = oq.from_f32(v16.float().numpy(), dtype)
+    c = TieredKVCache(n_sink=4, recent_window=64, int4_budget=300, rope_scheme=scheme, head_dim=D, dtype=tdt)
+    K0, _ = c.update(_dev_t(k, dtype, dev), _dev_t(v, dtype, dev), 0)
+    assert K0.dtype == tdt
+    tiers = _assign_one_layer(S, exp_scores(S, seed=32), 4, 64, 300, 0)
+    c.apply_tier_assignment(0, tiers)
+    o = _oracle_reassign(k, v, np.arange(S), tiers.numpy(), scheme, 4, dtype)
+    st = c._layers[0]
+    assert st.int4_ks.dtype == tdt and st.int4_vs.dtype == tdt and st.fp16_k.dtype == tdt
+    assert np.array_equal(st.int4_kq.cpu().numpy(), o["kq"]) and np.array_equal(st.int4_vq.cpu().numpy(), o["vq"])
+    assert np.array_equal(_host_t(st.int4_ks, dtype), o["ks"]) and np.array_equal(_host_t(st.int4_vs, dtype), o["vs"])
+    ns = o["n_sink"]
+    assert np.array_equal(_host_t(st.sink_k, dtype), o["fp16_k"][:, :, :ns])
+    assert np.array_equal(_host_t(st.fp16_k, dtype), o["fp16_k"][:, :, ns:])
+    assert np.array_equal(_host_t(st.fp16_v, dtype), o["fp16_v"][:, :, ns:])
+    assert np.array_equal(st.int4_pos.cpu().numpy(), o["int4_pos"])
+
+    # materialized K/V: sink | dequantized middle | recent (the middle sits between them here)
+    K, V = c._materialize(0)
+    assert K.dtype == tdt
+    kd = oq.dequant_int4_typed(o["kq"], o["ks"], dtype)
+    vd = oq.dequant_int4_typed(o["vq"], o["vs"], dtype)
+    fk, fv = o["fp16_k"], o["fp16_v"]
+    assert np.array_equal(_host_t(K, dtype), np.concatenate([fk[:, :, :ns], kd, fk[:, :, ns:]], 2))
+    assert np.array_equal(_host_t(V, dtype), np.concatenate([fv[:, :, :ns], vd, fv[:, :, ns:]], 2))
+    with pytest.raises(NotImplementedError, match="float16 tiers"):
+        c.decode_attention(torch.zeros(B, 8, 1, D, dtype=torch.float16, device=dev), 0)
+
+    # a second reassignment requantizes from the dequantized values
+    S2 = c.get_seq_length(0)
+    tiers2 = _assign_one_layer(S2, torch.arange(S2, dtype=torch.float32), 4, 64, 150, 0)
+    pos2 = np.concatenate([st.sink_pos.cpu().numpy(), st.int4_pos.cpu().numpy(), st.fp16_pos.cpu().numpy()])
+    c.apply_tier_assignment(0, tiers2)
+    o2 = _oracle_reassign(_host_t(K, dtype), _host_t(V, dtype), pos2, tiers2.numpy(), scheme, 4, dtype)
+    st = c._layers[0]
+    assert np.array_equal(st.int4_kq.cpu().numpy(), o2["kq"]) and np.array_equal(st.int4_vq.cpu().numpy(), o2["vq"])
+    assert np.array_equal(_host_t(st.int4_ks, dtype), o2["ks"])
+
+    # an INT2 tier (three-tier policy): grouped codes at the cache dtype
+    c3 = TieredKVCache(n_sink=4, recent_window=64, int4_budget=200, int2_budget=128, rope_scheme=scheme,
+                       head_dim=D, dtype=tdt)
+    c3.update(_dev_t(k, dtype, dev), _dev_t(v, dtype, dev), 0)
+    c3.apply_tier_assignment(0, _assign_one_layer(S, exp_scores(S, seed=33), 4, 64, 200, 128))
+    st3 = c3._layers[0]
+    assert st3.int2_kq is not None and st3.int2_ks.dtype == tdt
+    K3, _ = c3._materialize(0)
+    assert K3.dtype == tdt and K3.shape[2] == c3.get_seq_length(0)
 
 
 def test_k4v2_cache_decode(dev):

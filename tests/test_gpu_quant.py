@@ -215,6 +215,29 @@ def test_quant_int2_grouped_bit_exact(dev, S):
             fq.quant_k_int2(torch.from_numpy(np.ascontiguousarray(x)).to(dev))
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("S", [128, 100, 1])
+def test_quant_int2_grouped_typed_bit_exact(dev, dtype, S):
+    print(f"case int2 grouped {dtype} S={S}", flush=True)
+    x = _typed_edge((2, 3, 128, 128), 8, dtype)[:, :, :S]
+    xp, _ = oq.pad_to_group(x, 64)
+    oqv, osc = oq.quant_int2_grouped_typed(xp, dtype, 64)
+    q, sc = fq.quant_int2_padded(_dev_typed(x, dtype, dev), 64)
+    assert sc.dtype == _TDT[dtype]
+    assert np.array_equal(q.cpu().numpy(), oqv)
+    _same(_host_typed(sc, dtype), osc, dtype)
+    deq = fq.dequant_int2_trimmed(q, sc, S, 64)
+    assert deq.dtype == _TDT[dtype]
+    _same(_host_typed(deq, dtype), oq.dequant_int2_typed(oqv, osc, dtype, 64)[:, :, :S], dtype)
+    if S % 64 == 0:
+        q2, sc2 = fq.quant_k_int2(_dev_typed(x, dtype, dev))
+        assert torch.equal(q2, q) and torch.equal(sc2.nan_to_num(), sc.nan_to_num())
+        # the reference's default: dequantize to float16 (scale.to(fp16) first)
+        d16 = fq.dequant_k_int2(q2, sc2, 64).cpu().numpy()
+        s16 = oq.to_f32(osc, dtype).astype(np.float16)
+        _same(d16, oq.dequant_int2_grouped(oqv, s16, 64), "f16")
+
+
 @pytest.mark.parametrize("bits", [4, 3, 2])
 def test_rotated_quant_bit_exact_given_rotation(dev, bits):
     """Codes and scales are bit-exact given x_rot; x_rot itself is an fp32 GEMM (tolerance)."""

@@ -8,6 +8,7 @@ from fade_amd import rope as frope
 from fade_amd.policy import _assign_one_layer
 from fade_amd.synthetic import ReropeConfig, exp_scores, kv_tensors
 from oracle import policy as opol
+from oracle import quant as oq
 from oracle import rope as orope
 
 pytestmark = pytest.mark.gpu
@@ -73,3 +74,37 @@ def test_rerope_llama3_scheme_tables(dev):
     ko, _ = frope.rerope_gather(k.to(dev), v.to(dev), keep.to(dev), co, so, cn, sn)
     rk, _ = orope.rerope_gather(k.numpy(), v.numpy(), keep.numpy(), co.numpy(), so.numpy(), cn.numpy(), sn.numpy())
     assert np.array_equal(ko.cpu().numpy().view(np.uint16), rk.view(np.uint16))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("D", [128, 64])
+def test_rerope_typed_bit_exact(dev, dtype, D):
+    """A bfloat16 / float32 cache: fp32 math, un-RoPE and re-RoPE each rounded
+    to the cache dtype; bf16 tables are not rounded (fade/rope.py:83-93)."""
+    print(f"case rerope {dtype} D={D}", flush=True)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    rng = np.random.default_rng(21)
+    S = 300
+    k = oq.from_f32((rng.standard_normal((2, 4, S, D)) * 3).astype(np.float32), dtype)
+    v = oq.from_f32(rng.standard_normal((2, 4, S, D)).astype(np.float32), dtype)
+    scheme = frope.Vanilla(theta=1e6, head_dim=D)
+    keep = torch.tensor(sorted(rng.choice(S, 120, replace=False)))
+    co, so = scheme.host_cos_sin(torch.arange(S) + 500, tdt)
+    cn, sn = scheme.host_cos_sin(torch.arange(120), tdt)
+
+    def dev_t(a):
+        if dtype == "bf16":
+            return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(dev)
+        return torch.from_numpy(a).to(dev)
+
+    def host(t):
+        t = t.cpu().contiguous()
+        return t.view(torch.int16).numpy().view(np.uint16) if dtype == "bf16" else t.numpy()
+
+    ko, vo = frope.rerope_gather(dev_t(k), dev_t(v), keep.to(dev), co, so, cn, sn)
+    assert ko.dtype == tdt and vo.dtype == tdt
+    rk, rv = orope.rerope_gather_typed(k, v, keep.numpy(), co.numpy(), so.numpy(), cn.numpy(), sn.numpy(), dtype)
+    assert np.array_equal(host(vo), rv)
+    assert np.array_equal(host(ko), rk)
+    with pytest.raises(ValueError, match="dtypes differ"):
+        frope.rerope_gather(dev_t(k), dev_t(v).half(), keep.to(dev), co, so, cn, sn)

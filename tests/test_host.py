@@ -105,8 +105,9 @@ def test_cache_contracts_without_gpu():
         c.update(torch.zeros(2, 3, 4), torch.zeros(2, 3, 4), 0)
     with pytest.raises(ValueError, match="K/V shape mismatch"):
         c.update(torch.zeros(1, 2, 3, 8), torch.zeros(1, 2, 4, 8), 0)
-    with pytest.raises(ValueError, match="float16 only"):
-        TieredKVCache(dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="float16, bfloat16 and float32"):
+        TieredKVCache(dtype=torch.float64)
+    assert TieredKVCache(dtype=torch.bfloat16).dtype == torch.bfloat16
     assert c.get_mask_sizes(5, 0) == (5, 0)
 
 
@@ -147,6 +148,22 @@ def test_fade_attention_registration_and_fused_update():
     assert rk is k and rv is v
     assert cache.get_seq_length(0) == 5
     assert active_cache() is cache
+    # the fused kernels read float16 tiers: a bf16 cache refuses fused mode
+    from transformers import AutoConfig
+
+    from fade_amd import create_tiered_cache
+
+    cfg = AutoConfig.for_model("qwen2", hidden_size=256, num_attention_heads=2, num_key_value_heads=1,
+                               num_hidden_layers=2, intermediate_size=512, vocab_size=100)
+    cfg._attn_implementation = "fade"
+    model = types.SimpleNamespace(config=cfg)
+    with pytest.raises(ValueError, match="reads float16 caches"):
+        create_tiered_cache(model, dtype=torch.bfloat16)
+    assert create_tiered_cache(model).fused
+    c16 = TieredKVCache(dtype=torch.bfloat16)
+    c16.fused = True
+    with pytest.raises(NotImplementedError, match="float16"):
+        c16.update(k.bfloat16(), v.bfloat16(), 0)
 
 
 def test_paginate_middle_pools_pages_on_host():

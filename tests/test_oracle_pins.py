@@ -213,6 +213,36 @@ def test_dequant_int4_typed_matches_torch(dtype):
     assert np.array_equal(got, _bits_bf16(ref) if dtype == "bf16" else ref.numpy())
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32", "f16"])
+def test_quant_int2_typed_matches_torch_ops(dtype):
+    """fade/quant.py:95-112 run by torch on a bf16 / fp32 / fp16 tensor."""
+    x = _hard_typed((2, 2, 128, 32), 11, dtype)
+    t = (_t_bf16(x) if dtype == "bf16" else torch.from_numpy(x)).view(2, 2, 2, 64, 32)
+    absmax = t.abs().amax(dim=-2, keepdim=True).clamp(min=1e-8)
+    qt = (t * (1 / absmax)).round().clamp(-2, 1).to(torch.int8).view(2, 2, 128, 32)
+    st = (absmax / 1).squeeze(-2)
+    q, s = oq.quant_int2_grouped_typed(x, dtype, 64)
+    assert np.array_equal(q, qt.numpy())
+    if dtype == "bf16":
+        same = np.isnan(oq.bf16_to_f32(s)) == torch.isnan(st.float()).numpy()
+        fin = ~np.isnan(oq.bf16_to_f32(s))
+        assert same.all() and np.array_equal(s[fin], _bits_bf16(st)[fin])
+    else:
+        assert np.array_equal(s, st.numpy(), equal_nan=True)
+    if dtype == "f16":
+        qf, sf = oq.quant_int2_grouped(x, 64)
+        assert np.array_equal(q, qf) and np.array_equal(s.view(np.uint16), sf.view(np.uint16))
+    # dequant: q.to(dtype) * scale.to(dtype), the scale repeated over the group
+    tdt = {"bf16": torch.bfloat16, "f32": torch.float32, "f16": torch.float16}[dtype]
+    sfull = st.unsqueeze(-2).expand(2, 2, 2, 64, 32).reshape(2, 2, 128, 32)
+    ref = qt.to(tdt) * sfull.to(tdt)
+    got = oq.dequant_int2_typed(q, s, dtype, 64)
+    rb = _bits_bf16(ref) if dtype == "bf16" else ref.numpy()
+    nan = np.isnan(oq.to_f32(got, dtype))
+    assert np.array_equal(nan, torch.isnan(ref.float()).numpy())
+    assert np.array_equal(got[~nan], rb[~nan])
+
+
 def test_typed_quant_would_fail_without_the_bf16_clamp():
     """A model without the clamp (fp16's no-op) disagrees with torch on bf16."""
     x = _hard_typed((1, 2, 16, 16), 3, "bf16")
@@ -355,6 +385,37 @@ def test_rerope_identity_when_positions_do_not_move():
     # the rotated pair's magnitude, plus two fp16 roundings of the result.
     pair = np.abs(k4) + np.abs(np.concatenate([k4[..., 16:], k4[..., :16]], -1))
     assert np.all(d <= pair * 2.0 ** -9 + 2 * np.spacing(np.abs(k[:, :, :4])).astype(np.float32))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_rerope_typed_matches_torch_ops(dtype):
+    """fade/cache.py:290-311 on a bf16 / fp32 cache, evaluated by torch: fp32
+    math, each of un-RoPE and re-RoPE cast to the cache dtype."""
+    rng = np.random.default_rng(12)
+    D, S = 64, 40
+    k = oq.from_f32((rng.standard_normal((2, 3, S, D)) * 4).astype(np.float32), dtype)
+    v = oq.from_f32(rng.standard_normal((2, 3, S, D)).astype(np.float32), dtype)
+    inv = orope.vanilla_inv_freq(D, 1e4)
+    cos_o, sin_o = orope.cos_sin_tables(np.arange(S) + 100, inv, round_fp16=False)
+    keep = np.array([0, 3, 4, 9, 17, 30, 39])
+    cos_n, sin_n = orope.cos_sin_tables(np.arange(len(keep)), inv, round_fp16=False)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    kt = (_t_bf16(k) if dtype == "bf16" else torch.from_numpy(k))[:, :, keep]
+
+    def rot(x):
+        return torch.cat((-x[..., D // 2:], x[..., : D // 2]), -1)
+
+    co, so = torch.from_numpy(cos_o[keep]), torch.from_numpy(sin_o[keep])
+    pre = (kt.float() * co - rot(kt.float()) * so).to(tdt)
+    post = (pre.float() * torch.from_numpy(cos_n) + rot(pre.float()) * torch.from_numpy(sin_n)).to(tdt)
+    ko, vo = orope.rerope_gather_typed(k, v, keep, cos_o, sin_o, cos_n, sin_n, dtype)
+    assert np.array_equal(ko, _bits_bf16(post) if dtype == "bf16" else post.numpy())
+    assert np.array_equal(vo, v[:, :, keep])
+    # a single rounding (no cast between un-RoPE and re-RoPE) differs on bf16
+    if dtype == "bf16":
+        once = (kt.float() * co - rot(kt.float()) * so)
+        once = (once * torch.from_numpy(cos_n) + rot(once) * torch.from_numpy(sin_n)).to(tdt)
+        assert not np.array_equal(ko, _bits_bf16(once))
 
 
 # ----------------------------------------------------------------- policy
