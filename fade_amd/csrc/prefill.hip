@@ -68,6 +68,7 @@ constexpr int kKPitch = D + 8;
 constexpr int kVtPitch = 72;  // halves per V^T row in LDS (16-byte accesses of 8 consecutive rows: distinct banks)
 constexpr float kNegBig = -1.0e30f;
 constexpr float kTau = 8.0f;  // the running max moves only when a score exceeds it by kTau (log2)
+constexpr float kTauP = 256.0f;  // 2^kTau
 
 struct Tier {
   const uint16_t* k;
@@ -207,19 +208,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // middle K staging: thread = token mr, channels 32*mc .. 32*mc+31 (threads tid < 64 KTHR)
   const int mr = tid / KTHR, mc = tid % KTHR;
   const bool kstage = kKT * KTHR == kThreads || tid < kKT * KTHR;
-  const uint16_t* sk = p.sink.k + b * p.sink.k_sb + kvh * p.sink.k_sh;
-  const uint16_t* sv = p.sink.v + b * p.sink.v_sb + kvh * p.sink.v_sh;
-  const uint16_t* rk = p.recent.k + b * p.recent.k_sb + kvh * p.recent.k_sh;
-  const uint16_t* rv = p.recent.v + b * p.recent.v_sb + kvh * p.recent.v_sh;
-  const uint16_t* ck = p.chunk.k + b * p.chunk.k_sb + kvh * p.chunk.k_sh;
-  const uint16_t* cvp = p.chunk.v + b * p.chunk.v_sb + kvh * p.chunk.v_sh;
-  const int64_t sk_ss = p.sink.k_ss, sv_ss = p.sink.v_ss, rk_ss = p.recent.k_ss, rv_ss = p.recent.v_ss;
-  const int64_t ck_ss = p.chunk.k_ss, cv_ss = p.chunk.v_ss;
+  // fp16 rows of each segment (0 sink, 1 fp16 middle tier, 2 recent, 3 chunk)
+  // of this (row, kv head): K and V row pointers and row strides in halves.
+  // They sit in LDS, read (one broadcast per tile) by the few fp16 tiles of a
+  // row, so the tile loop keeps no scalar registers for them.
+  __shared__ __attribute__((aligned(16))) int64_t segd[4][4];
+  if (tid == 0) {
+    auto put = [&](int sg, const Tier t) {
+      segd[sg][0] = reinterpret_cast<int64_t>(t.k + b * t.k_sb + kvh * t.k_sh);
+      segd[sg][1] = reinterpret_cast<int64_t>(t.v + b * t.v_sb + kvh * t.v_sh);
+      segd[sg][2] = t.k_ss;
+      segd[sg][3] = t.v_ss;
+    };
+    put(0, p.sink);
+    put(2, p.recent);
+    put(3, p.chunk);
+    // fp16 middle tier: [B, Hkv, cap, D] contiguous
+    segd[1][0] = reinterpret_cast<int64_t>(reinterpret_cast<const uint16_t*>(p.kq) + bkv * p.mid_cap * D);
+    segd[1][1] = reinterpret_cast<int64_t>(reinterpret_cast<const uint16_t*>(p.vq) + bkv * p.mid_cap * D);
+    segd[1][2] = D;
+    segd[1][3] = D;
+  }
   const uint8_t* kq = p.kq + bkv * p.mid_cap * KROW;
   const uint8_t* vq = p.vq + bkv * p.mid_cap * KROW;
-  // fp16 middle tier: rows of D halves, [B, Hkv, cap, D] contiguous
-  const uint16_t* mk16 = reinterpret_cast<const uint16_t*>(p.kq) + bkv * p.mid_cap * D;
-  const uint16_t* mv16 = reinterpret_cast<const uint16_t*>(p.vq) + bkv * p.mid_cap * D;
   const uint16_t* vsr = p.vs + bkv * p.mid_cap;
 
   // K scales of this thread's 32 staged channels as fp16 pairs, in the stored order
@@ -339,12 +350,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     uint4 fk[NU], fv[NU];
     const int key = tr.base + r;
     if (r < tr.cnt) {
-      const uint16_t* kp = tr.seg == 0 ? sk + key * sk_ss
-                           : (tr.seg == 1 ? mk16 + static_cast<int64_t>(key) * D
-                                          : (tr.seg == 2 ? rk + key * rk_ss : ck + key * ck_ss));
-      const uint16_t* vp = tr.seg == 0 ? sv + key * sv_ss
-                           : (tr.seg == 1 ? mv16 + static_cast<int64_t>(key) * D
-                                          : (tr.seg == 2 ? rv + key * rv_ss : cvp + key * cv_ss));
+      typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
+      const i64x2 ptr = *reinterpret_cast<const i64x2*>(&segd[tr.seg][0]);
+      const i64x2 ss = *reinterpret_cast<const i64x2*>(&segd[tr.seg][2]);
+      const uint16_t* kp = reinterpret_cast<const uint16_t*>(ptr.x) + key * ss.x;
+      const uint16_t* vp = reinterpret_cast<const uint16_t*>(ptr.y) + key * ss.y;
       const uint4* k4 = reinterpret_cast<const uint4*>(kp + CPT * cp);
       const uint4* v4 = reinterpret_cast<const uint4*>(vp + CPT * cp);
 #pragma unroll
@@ -403,7 +413,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int i = 0; i < 16; ++i) acc[cb][i] = 0.0f;
   float m_run = kNegBig, l_run = 0.0f;  // of query row n32 (the same in both halves; l_run over this half's keys)
   const float sl2 = p.scale_log2;
-  const float tau_raw = kTau / sl2;  // the lazy-rescale margin in raw score units
   float* const rf = &rowf[wave][0];
 
   auto compute = [&](int t, int buf) {
@@ -437,14 +446,34 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         for (int i = 0; i < 16; ++i)
           if (32 * kb + 8 * (i >> 2) + 4 * h + (i & 3) >= lim) s[kb][i] = -INFINITY;
     }
-    float lmax = kNegBig;
+    // probabilities exp2((x - m) * scale) against the running max m (raw score
+    // units), as fp16: PV A operands, k-step s = registers 8 (s & 1) .. + 7 of
+    // key block s >> 1
+    f16x8 pa[4];
+    auto probs = [&]() {
+      const float nm = -m_run * sl2;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; i += 2) lmax = fmaxf(lmax, fmaxf(s[kb][i], s[kb][i + 1]));
-    lmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
-    // running max in raw score units; probabilities exp2((x - m) * scale)
-    if (__builtin_amdgcn_ballot_w64(lmax - m_run > tau_raw) != 0) {
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            pa[2 * kb + hf][j] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + j], sl2, nm)));
+    };
+    probs();
+    // The running max moves only when a score exceeds it by more than kTau
+    // (log2 units), i.e. when a probability exceeds 2^kTau (inf included): a
+    // packed fp16 max over the probabilities finds those tiles; the exact fp32
+    // max is taken on them alone.
+    f16x8 pm = __builtin_elementwise_max(__builtin_elementwise_max(pa[0], pa[1]), __builtin_elementwise_max(pa[2], pa[3]));
+    f16x2 pm2 = __builtin_elementwise_max(__builtin_elementwise_max(pm.s01, pm.s23), __builtin_elementwise_max(pm.s45, pm.s67));
+    if (__builtin_amdgcn_ballot_w64(static_cast<float>(pm2.x) > kTauP || static_cast<float>(pm2.y) > kTauP) != 0) {
+      float lmax = kNegBig;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) lmax = fmaxf(lmax, fmaxf(s[kb][i], s[kb][i + 1]));
+      lmax = fmaxf(lmax, __shfl_xor(lmax, 32, 64));
       const float m_new = fmaxf(m_run, lmax);
       const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * sl2);
       m_run = m_new;
@@ -460,21 +489,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[cb][4 * q + i] *= a4[i];
       }
+      probs();
     }
-    const float nm = -m_run * sl2;
-    float ps = 0.0f;
-    f16x8 pa[4];  // PV A operands: k-step s = registers 8 (s & 1) .. + 7 of key block s >> 1
+    // the row sum of the same fp16 probabilities PV multiplies: fp32 dot products with 1
+    {
+      const f16x2 one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+      float ps = 0.0f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int k = 0; k < 4; ++k) {
+        const u32x4 w = __builtin_bit_cast(u32x4, pa[k]);
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + j], sl2, nm));
-          ps += pv;
-          pa[2 * kb + hf][j] = static_cast<_Float16>(pv);
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t we = w[e];
+          ps = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, we), one, ps, false);
         }
-    l_run += ps;
+      }
+      l_run += ps;
+    }
     // O += P V.  B operand: lane (n32, h) reads channel 32 cb + n32 at V^T
     // positions 16 s + 8 h .. + 7 (keys 16 s + 8 (j >> 2) + 4 h + (j & 3)).
 #pragma unroll
@@ -486,6 +517,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
   };
 
+  __syncthreads();  // segd
   if (begin_tile(0, 0)) store_mid(0);
   __syncthreads();
   for (int t = 0; t < n_tiles; ++t) {
