@@ -5,12 +5,15 @@
 // and to chunk tokens 0..j (bottom-right causal, as the model's SDPA over
 // the reference's materialized tiers, fade/cache.py:347-379,683-842).
 //
-// Workgroup = (32-query block and head pass, kv head, batch row); wave w
-// serves query head kvh*G + 4*pass + w (G = Hq/Hkv <= 8: one pass of up to 4
-// heads for G <= 4, two passes for G = 5..8), its 32 query rows as one 32-row
-// M tile.  The row's key
+// Workgroup = (query blocks and head pass, kv head, batch row): one or two
+// groups of 4 waves, group q serving the q-th 32-query block; wave w of a
+// group serves query head kvh*G + 4*pass + w (G = Hq/Hkv <= 8: one pass of up
+// to 4 heads for G <= 4, two passes for G = 5..8), its 32 query rows as one
+// 32-row M tile.  With two groups, the first stages and dequantizes each
+// tile's K and the second its V, so one dequantization serves 64 queries per
+// head.  The row's key
 // sequence is walked in 64-token tiles that never straddle a tier (sink,
-// middle, recent, then the chunk).  All 256 threads fetch a tile (thread =
+// middle, recent, then the chunk).  The threads fetch a tile (thread =
 // one token x 32 channels) into double-buffered LDS (the next tile's global
 // loads fly while the current one is computed): fp16 K and V rows as they
 // are, through registers; middle-tier codes and V scales by direct
@@ -123,8 +126,11 @@ __host__ __device__ constexpr int swap23(int k) { return (k & ~12) | ((k & 4) <<
 // Head dims 32, 64 and 128: QK^T takes D/16 k-steps, PV D/32 column blocks;
 // a fetch thread covers D/4 channels of a token (fp16 tiles), and D/32
 // threads stage a middle token's D/2 code bytes, 16 each.
-template <int D>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PParams p) {
+// NQB query blocks of 32 per workgroup (4 waves each).  With NQB = 2 the two
+// groups of 4 waves split the tile staging: waves 0-3 stage and dequantize K,
+// waves 4-7 V, so each middle tile's dequantization serves 64 queries per head.
+template <int D, int NQB>
+__global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PParams p) {
   constexpr int KROW = D / 2;     // bytes of one token's packed 4-bit codes
   constexpr int CPT = D / 4;      // channels per fetch thread (fp16 tiles)
   constexpr int KTHR = D / 32;    // threads (16 code bytes each) per middle token
@@ -142,6 +148,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wq = wave & 3, qblk = wave >> 2;  // wave within its group, the group's query block
+  const int gtid = tid & (kThreads - 1);      // thread within its group of 4 waves
+  // staging roles: K (codes, scales) and V (codes, scales) of every tile
+  const bool do_k = NQB == 1 || qblk == 0, do_v = NQB == 1 || qblk == NQB - 1;
   const int n16 = lane & 15, g = lane >> 4;
   const int G = p.G - h0 < 4 ? p.G - h0 : 4;  // query heads this workgroup serves
   const int64_t bkv = b * p.Hkv + kvh;
@@ -151,11 +161,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int nm = clampi(__builtin_amdgcn_readfirstlane(p.lens[3 * b + 1]), p.mid_cap);
   const int nr = clampi(__builtin_amdgcn_readfirstlane(p.lens[3 * b + 2]), p.recent_cap);
   const int Sq = static_cast<int>(p.Sq);
-  const int j0 = qb * kQB;
-  const int jn = Sq - j0 < kQB ? Sq - j0 : kQB;  // queries of this block
+  const int jw = qb * kQB * NQB;                       // the workgroup's first query
+  const int jwn = Sq - jw < kQB * NQB ? Sq - jw : kQB * NQB;  // its queries
+  const int j0 = jw + kQB * qblk;                      // this wave's query block
   const int mode = p.mask_mode;
-  // chunk keys any query of the block can see (bottom-right: chunk keys 0..j)
-  const int cv = mode == FADE_MASK_BOTTOM_RIGHT ? j0 + jn : p.chunk_len;
+  // chunk keys any query of the workgroup can see (bottom-right: chunk keys 0..j)
+  const int cv = mode == FADE_MASK_BOTTOM_RIGHT ? jw + jwn : p.chunk_len;
   // Key tiles never straddle a tier: sink, middle, recent, chunk tiles in turn.
   const int nts = (ns + kKT - 1) / kKT, ntm = (nm + kKT - 1) / kKT, ntr = (nr + kKT - 1) / kKT;
   const int ntc = (cv + kKT - 1) / kKT;
@@ -163,7 +174,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   if (mode == FADE_MASK_TOP_LEFT) {
     // query j sees keys 0..j of the row's sequence: only the tiles that start
     // at or before the block's last query (a prefix of the tile order)
-    const int jmax = j0 + jn - 1;
+    const int jmax = jw + jwn - 1;
     auto upto = [&](int nt, int off) {
       if (jmax < off) return 0;
       const int c = (jmax - off) / kKT + 1;
@@ -193,7 +204,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   __shared__ __attribute__((aligned(16))) uint16_t kt[2][kKT][KP];
   __shared__ __attribute__((aligned(16))) uint16_t vtt[2][D][kVtPitch];
-  __shared__ __attribute__((aligned(16))) float rowf[4][32];  // per-wave factors of the 32 query rows
+  __shared__ __attribute__((aligned(16))) float rowf[4 * NQB][32];  // per-wave factors of the 32 query rows
   // middle-tile staging: thread tid's 16 bytes of K codes at 16 tid (token
   // tid / KTHR, channels 32 (tid % KTHR) ..); keys 16 w + rho (rho < 16) in
   // stg_v[1024 w ..], 16-byte unit u of row rho at unit
@@ -204,10 +215,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   __shared__ __attribute__((aligned(16))) uint32_t stg_s[kThreads];
 
   // ---- tile fetch: thread = token r of the tile, channels CPT*cp .. CPT*cp+CPT-1 ----
-  const int r = tid >> 2, cp = tid & 3;
-  // middle K staging: thread = token mr, channels 32*mc .. 32*mc+31 (threads tid < 64 KTHR)
-  const int mr = tid / KTHR, mc = tid % KTHR;
-  const bool kstage = kKT * KTHR == kThreads || tid < kKT * KTHR;
+  const int r = gtid >> 2, cp = gtid & 3;
+  // middle K staging: thread = token mr, channels 32*mc .. 32*mc+31 (threads gtid < 64 KTHR)
+  const int mr = gtid / KTHR, mc = gtid % KTHR;
+  const bool kstage = do_k && (kKT * KTHR == kThreads || gtid < kKT * KTHR);
   // fp16 rows of each segment (0 sink, 1 fp16 middle tier, 2 recent, 3 chunk)
   // of this (row, kv head): K and V row pointers and row strides in halves.
   // They sit in LDS, read (one broadcast per tile) by the few fp16 tiles of a
@@ -247,11 +258,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // staging slots of this wave's lanes (a direct load writes lane l's bytes at base + l * size)
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   const uint32_t stk = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_k[16 * 64 * wave])));
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_k[16 * 64 * wq])));
   const uint32_t stv = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_v[16 * 64 * wave])));
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_v[16 * 64 * wq])));
   const uint32_t sts = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_s[64 * wave])));
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_s[64 * wq])));
   // Middle tile: codes and V scale to the staging area.  Nothing waits for
   // these loads before store_mid(), so they fly during the current tile's compute.
   auto fetch_mid = [&](const TileRef& tr) {
@@ -275,23 +286,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // V: lane l < 16 UPR of wave w fills unit l of the wave's block: row
     // rho = l / UPR, source unit (l % UPR) ^ ((rho >> 1) & (UPR - 1)).  Rows
     // past the tile read the last valid key (finite; their probabilities are zero).
-    const int vr = lane / UPR;
-    const int vk = 16 * wave + vr, sk2 = 16 * wave + (lane & 15);
-    if (UPR == 4 || lane < 16 * UPR)
-      lds_dma16(vq_t + static_cast<int64_t>(row0 + (vk < tr.cnt ? vk : tr.cnt - 1)) * KROW +
-                    16 * ((lane % UPR) ^ ((vr >> 1) & (UPR - 1))),
-                stv);
-    lds_dma2(vs_t + row0 + (sk2 < tr.cnt ? sk2 : tr.cnt - 1), sts);
+    if (do_v) {
+      const int vr = lane / UPR;
+      const int vk = 16 * wq + vr, sk2 = 16 * wq + (lane & 15);
+      if (UPR == 4 || lane < 16 * UPR)
+        lds_dma16(vq_t + static_cast<int64_t>(row0 + (vk < tr.cnt ? vk : tr.cnt - 1)) * KROW +
+                      16 * ((lane % UPR) ^ ((vr >> 1) & (UPR - 1))),
+                  stv);
+      lds_dma2(vs_t + row0 + (sk2 < tr.cnt ? sk2 : tr.cnt - 1), sts);
+    }
   };
   // staged codes -> fp16(code * scale) rows of K and V in LDS buffer buf
   auto store_mid = [&](int buf) {
     // the staging loads are the only vector-memory operations in flight here
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const f16x2 m72 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+    if (do_k) {
     uint4 kraw = make_uint4(0, 0, 0, 0);
-    if (kstage && fok) kraw = *reinterpret_cast<const uint4*>(&stg_k[16 * tid]);
+    if (kstage && fok) kraw = *reinterpret_cast<const uint4*>(&stg_k[16 * gtid]);
     // codes -> fp16 72 + c -> c -> fp16(c * scale), already in the stored channel order
     const uint32_t kw[4] = {kraw.x, kraw.y, kraw.z, kraw.w};
-    const f16x2 m72 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t o[4];
@@ -303,11 +317,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                                                  __builtin_bit_cast(f16x2, ksc[4 * i + e]));
       if (kstage) *reinterpret_cast<u32x4*>(&kt[buf][mr][32 * mc + 8 * i]) = kd;
     }
+    }
+    if (!do_v) return;
     // V.  Scales of the wave's keys by row rho (low 16 bits of dword 64 w + rho).
     uint32_t sc[16];
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
-      const uint4 d = *reinterpret_cast<const uint4*>(&stg_s[64 * wave + 4 * q4]);
+      const uint4 d = *reinterpret_cast<const uint4*>(&stg_s[64 * wq + 4 * q4]);
       sc[4 * q4] = d.x;
       sc[4 * q4 + 1] = d.y;
       sc[4 * q4 + 2] = d.z;
@@ -319,7 +335,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // of those rows, nibble s' <-> position offset o(s'), so the fp16 pairs
     // come out as position pairs (2 j, 2 j + 1), rows (swap23(2 j), + 1).
     const int so = swap23(2 * (n16 & 3) + ((n16 >> 2) & 1) + 8 * (n16 >> 3));
-    const uint8_t* vrow = &stg_v[1024 * wave + KROW * so];
+    const uint8_t* vrow = &stg_v[1024 * wq + KROW * so];
     // channel units of 16: D/16 of them, four per pass of the lane groups
     // (D = 32: groups 2 and 3 repeat units 0 and 1 and store nothing)
 #pragma unroll
@@ -340,7 +356,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
           const uint32_t s2 = __builtin_amdgcn_perm(sc[ra + 1], sc[ra], 0x05040100u);
           vd[j] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[j]) + m72) * __builtin_bit_cast(f16x2, s2));
         }
-        if (cu_ok) *reinterpret_cast<u32x4*>(&vtt[buf][ch][16 * wave + 8 * half]) = vd;
+        if (cu_ok) *reinterpret_cast<u32x4*>(&vtt[buf][ch][16 * wq + 8 * half]) = vd;
       }
     }
   };
@@ -359,8 +375,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       const uint4* v4 = reinterpret_cast<const uint4*>(vp + CPT * cp);
 #pragma unroll
       for (int i = 0; i < NU; ++i) {
-        fk[i] = k4[i];
-        fv[i] = v4[i];
+        if (do_k) fk[i] = k4[i];
+        if (do_v) fv[i] = v4[i];
       }
     } else {
 #pragma unroll
@@ -369,11 +385,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int pr = swap23(r);
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
-      *reinterpret_cast<u32x4*>(&kt[buf][r][CPT * cp + 8 * i]) = to_stored(fk[i].x, fk[i].y, fk[i].z, fk[i].w);
-      const uint32_t vw[4] = {fv[i].x, fv[i].y, fv[i].z, fv[i].w};
+      if (do_k)
+        *reinterpret_cast<u32x4*>(&kt[buf][r][CPT * cp + 8 * i]) = to_stored(fk[i].x, fk[i].y, fk[i].z, fk[i].w);
+      if (do_v) {
+        const uint32_t vw[4] = {fv[i].x, fv[i].y, fv[i].z, fv[i].w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        vtt[buf][CPT * cp + 8 * i + e][pr] = static_cast<uint16_t>(vw[e >> 1] >> (16 * (e & 1)));
+        for (int e = 0; e < 8; ++e)
+          vtt[buf][CPT * cp + 8 * i + e][pr] = static_cast<uint16_t>(vw[e >> 1] >> (16 * (e & 1)));
+      }
     }
   };
   // Tile t into LDS buffer buf: fp16 tiles complete here; a middle tile only
@@ -391,8 +410,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // ---- query fragments: B operand of S^T = K Q^T; lane (n32, h) holds query
   // row j0 + n32, channels 16 ks + 8 h .. + 7 in the stored order ----
   const int n32 = lane & 31, h = lane >> 5;
-  const bool active = wave < G;
-  const int64_t hq = kvh * p.G + h0 + (active ? wave : 0);
+  const bool active = wq < G && j0 < Sq;
+  const int64_t hq = kvh * p.G + h0 + (active ? wq : 0);
   f16x8 qf[NKS];
   {
     const int j = j0 + n32;
@@ -641,12 +660,18 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   p.ppr = has_mid ? m.pages_per_row : 0;
   p.mask_mode = a->mask_mode;
   p.chunk_len = static_cast<int>(a->chunk.len);
-  const dim3 grid(static_cast<unsigned>(cdiv(a->Sq, kQB) * p.passes), static_cast<unsigned>(a->Hkv),
+  // two query blocks per workgroup once there are more than 32 queries
+  const int nqb = a->Sq > kQB ? 2 : 1;
+  const dim3 grid(static_cast<unsigned>(cdiv(a->Sq, kQB * nqb) * p.passes), static_cast<unsigned>(a->Hkv),
                   static_cast<unsigned>(a->B));
+#define FADE_PREFILL_LAUNCH(DD)                                                                               \
+  if (nqb == 2) hipLaunchKernelGGL((prefill_kernel<DD, 2>), grid, dim3(2 * kThreads), 0, as_stream(stream), p); \
+  else hipLaunchKernelGGL((prefill_kernel<DD, 1>), grid, dim3(kThreads), 0, as_stream(stream), p);
   switch (a->D) {
-    case 32: hipLaunchKernelGGL(prefill_kernel<32>, grid, dim3(kThreads), 0, as_stream(stream), p); break;
-    case 64: hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(kThreads), 0, as_stream(stream), p); break;
-    default: hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(kThreads), 0, as_stream(stream), p); break;
+    case 32: FADE_PREFILL_LAUNCH(32) break;
+    case 64: FADE_PREFILL_LAUNCH(64) break;
+    default: FADE_PREFILL_LAUNCH(128) break;
   }
+#undef FADE_PREFILL_LAUNCH
   return check_launch("fade_tiered_prefill_attn");
 }
