@@ -24,6 +24,18 @@ def _case(B, Hq, Hkv, S, ns, nr, seed):
     return q.numpy(), k.numpy(), v.numpy(), ns, nr
 
 
+class _Err(float):
+    """A max-abs error that carries a diagnosis for the assertion message."""
+
+    def __new__(cls, value, note=""):
+        o = super().__new__(cls, value)
+        o.note = note
+        return o
+
+    def __repr__(self):
+        return f"{float(self)!r} ({self.note})" if self.note else repr(float(self))
+
+
 def _run(dev, q, k, v, ns, nr, mid_gpu, mid_oracle, kernel=0, n_splits=0):
     S = k.shape[2]
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
@@ -31,7 +43,20 @@ def _run(dev, q, k, v, ns, nr, mid_gpu, mid_oracle, kernel=0, n_splits=0):
     rec = (t(k[:, :, S - nr :]), t(v[:, :, S - nr :])) if nr else None
     out = tiered_decode_attention(t(q), sink, mid_gpu, rec, kernel=kernel, n_splits=n_splits)
     ref = oatt.tiered_decode(q, k[:, :, :ns], v[:, :, :ns], mid_oracle, k[:, :, S - nr :], v[:, :, S - nr :])
-    return np.abs(out.float().cpu().numpy() - ref).max()
+    err = np.abs(out.float().cpu().numpy() - ref).max()
+    if err <= ATOL:
+        return err
+    # a failure says whether the same call, run again, agrees, and whether the
+    # GPU-quantized middle tier equals the oracle's codes and scales
+    again = tiered_decode_attention(t(q), sink, mid_gpu, rec, kernel=kernel, n_splits=n_splits)
+    err2 = np.abs(again.float().cpu().numpy() - ref).max()
+    same_mid = None
+    if mid_oracle.get("fmt") == "int4" and mid_gpu.fmt == "int4":
+        same_mid = all(
+            np.array_equal(getattr(mid_gpu, a).cpu().numpy().view(np.uint8), np.asarray(mid_oracle[b]).view(np.uint8))
+            for a, b in (("k_codes", "kq"), ("v_codes", "vq"), ("k_scale", "ks"), ("v_scale", "vs"))
+        )
+    return _Err(err, f"re-run error {err2:.3g}, middle tier equal to the oracle's: {same_mid}")
 
 
 def _int4_mid(dev, k, v, ns, nr):

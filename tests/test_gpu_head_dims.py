@@ -316,4 +316,17 @@ def test_cache_per_sequence_head_dim_64(dev):
         cb.update(k[b : b + 1].to(dev), v[b : b + 1].to(dev), 0)
         cb.apply_tier_assignment(0, t[b].to(dev))
         ob = cb.decode_attention(q[b : b + 1], 0)
-        assert (out[b : b + 1].float() - ob.float()).abs().max().item() <= 1e-3, b
+        e = (out[b : b + 1].float() - ob.float()).abs().max().item()
+        if e > 1e-3:  # say which tier differs and whether the decodes repeat
+            st, sb = c._layers[0], cb._layers[0]
+            ls, lm, lr = st.lens_host[b]
+            tiers = {
+                "sink": torch.equal(st.sink_k[b : b + 1, :, :ls], sb.sink_k),
+                "int4_kq": torch.equal(st.int4_kq[b : b + 1, :, :lm], sb.int4_kq),
+                "int4_ks": torch.equal(st.int4_ks[b : b + 1], sb.int4_ks),
+                "int4_vq": torch.equal(st.int4_vq[b : b + 1, :, :lm], sb.int4_vq),
+                "int4_vs": torch.equal(st.int4_vs[b : b + 1, :, :lm], sb.int4_vs),
+                "recent": torch.equal(st.fp16_k[b : b + 1, :, :lr], sb.fp16_k),
+            }
+            again = (c.decode_attention(q, 0)[b : b + 1].float() - cb.decode_attention(q[b : b + 1], 0).float())
+            pytest.fail(f"row {b}: error {e:.3g}; tiers equal {tiers}; re-run error {again.abs().max().item():.3g}")
