@@ -179,3 +179,34 @@ def test_batched_equals_unbatched(dev):
         one = _steps(model, _cache(model), ids[r : r + 1], 2, middle_after_prompt=True)
         for a, b in zip(both, one):
             assert (a[r] - b[0]).abs().max().item() <= 2e-3
+
+
+def test_bf16_model_on_bf16_tiered_cache(dev):
+    """A bfloat16 model on TieredKVCache(dtype=bfloat16), attending over the
+    materialized K/V (attn_implementation="sdpa", as the reference runs bf16
+    models): before any compression its logits equal a DynamicCache's bit for
+    bit; after an INT4 middle tier the tiers and scales are bf16, the decode
+    steps stay close to the uncompressed cache, and generate() runs."""
+    print("case generate bf16 cache", flush=True)
+    from transformers import DynamicCache
+
+    model, cfg = _tiny_model(dev, "sdpa")
+    model.to(torch.bfloat16)
+    ids = torch.randint(0, cfg.vocab_size, (1, 24), device=dev)
+    kw = {"n_sink": 2, "recent_window": 8, "int4_budget": None, "int2_budget": 0}
+    with torch.no_grad():
+        a = model(ids, past_key_values=create_tiered_cache(model, dtype=torch.bfloat16, **kw), use_cache=True).logits
+        b = model(ids, past_key_values=DynamicCache(), use_cache=True).logits
+    assert torch.equal(a, b)
+    cache = create_tiered_cache(model, dtype=torch.bfloat16, **kw)
+    tiered = _steps(model, cache, ids, 3, middle_after_prompt=True)
+    st = cache._layers[0]
+    assert st.int4_kq is not None and st.int4_ks.dtype == torch.bfloat16 and st.fp16_k.dtype == torch.bfloat16
+    plain = _steps(model, DynamicCache(), ids, 3)
+    assert tiered[0].tolist() == plain[0].tolist()  # the prompt's logits precede the tiering
+    assert all(torch.isfinite(t).all() for t in tiered)
+    # the first decode step feeds both caches the same token
+    assert (tiered[1] - plain[1]).abs().max().item() <= 0.1 * plain[1].abs().max().item()
+    gen = model.generate(ids, past_key_values=create_tiered_cache(model, dtype=torch.bfloat16, **kw), max_new_tokens=4,
+                         do_sample=False)
+    assert gen.shape[0] == 1 and 24 < gen.shape[1] <= 28
