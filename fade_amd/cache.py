@@ -250,6 +250,10 @@ class TieredKVCache(DynamicCache):
             raise ValueError(f"key_states must be [B, H, S, D]; got shape {tuple(key_states.shape)}")
         if key_states.shape != value_states.shape:
             raise ValueError(f"K/V shape mismatch: {tuple(key_states.shape)} vs {tuple(value_states.shape)}")
+        if self.fused and self.dtype != torch.float16:  # refused before any state changes
+            raise NotImplementedError(
+                f"fused attention reads float16 caches; this one is {self.dtype} (use the model's own attention)"
+            )
         batch = int(key_states.shape[0])
         if self.batch_size is None:
             self.batch_size = batch
@@ -262,10 +266,6 @@ class TieredKVCache(DynamicCache):
         if self.fused:
             from .hf_attention import set_active_cache
 
-            if self.dtype != torch.float16:
-                raise NotImplementedError(
-                    f"fused attention reads float16 caches; this one is {self.dtype} (use the model's own attention)"
-                )
             set_active_cache(self)
             return key_states, value_states
         return self._materialize(layer_idx)

@@ -58,6 +58,29 @@ def test_round_trip_with_int4(dev):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_round_trip_typed_cache_with_int4_and_int2(dev, dtype):
+    """tests/test_checkpoint.py:52-86 on a bfloat16 / float32 cache (the reference's
+    own tests run fp32): tiers, scales and the materialized cache keep the dtype
+    and come back bit-identical, after eviction and with an INT2 tier."""
+    print(f"case checkpoint {dtype}", flush=True)
+    kw = dict(dtype=dtype, int4_budget=4, int2_budget=64)
+    cache = _make_cache(**kw)
+    k, v = _kv(dev, 200, seed=5)
+    cache.update(k.to(dtype), v.to(dtype), layer_idx=0)
+    g = torch.Generator().manual_seed(6)
+    cache.apply_tier_assignment(0, _assign_one_layer(200, torch.rand(200, generator=g), 2, 3, 4, 64))
+    st = cache._layers[0]
+    assert st.int2_kq is not None and st.int2_ks.dtype == dtype and st.int4_ks.dtype == dtype
+    sd = cache.cache_state_dict()
+    assert sd["dtype"] == str(dtype)
+    cache2 = _make_cache(**kw)
+    cache2.load_cache_state_dict(sd, device=dev)
+    assert cache2.get_seq_length(0) == cache.get_seq_length(0)
+    for a, b in zip(cache._materialize(0), cache2._materialize(0)):
+        assert a.dtype == dtype and torch.equal(a, b)
+
+
 def test_excludes_dequant_caches(dev):
     """tests/test_checkpoint.py:89-106."""
     cache = _make_cache()

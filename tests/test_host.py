@@ -164,6 +164,7 @@ def test_fade_attention_registration_and_fused_update():
     c16.fused = True
     with pytest.raises(NotImplementedError, match="float16"):
         c16.update(k.bfloat16(), v.bfloat16(), 0)
+    assert c16.get_seq_length(0) == 0 and c16.batch_size is None  # refused before any state changes
 
 
 def test_paginate_middle_pools_pages_on_host():
