@@ -74,7 +74,7 @@ def test_int4_sdpa_query_rows(dev):
 
 @pytest.mark.parametrize("S_q", [1, 16])
 def test_check_parity_helper(dev, S_q):
-    """fade/kernels/int4_attention.py:228-269: the helper's keys and its verdict."""
+    """fade/kernels/int4_attention.py:228-269: the helper's keys and its pass/fail result."""
     print(f"case check_parity S_q={S_q}", flush=True)
     res = check_parity(S_q=S_q)
     assert set(res) == {"passed", "max_abs_error", "mean_abs_error", "atol", "rtol"}
