@@ -389,11 +389,12 @@ def per_sequence_case(dev, n_inst: int = 4):
     return out
 
 
-def gqa7_decode_case(dev):
-    """Decode at config 3's model shape (B=8, Hq=28, Hkv=4: 7 query heads per kv head,
-    S=4096, reference INT4 middle, sink 4, recent 128): the INT4 kernel's two head
-    passes (the default) against the general matrix-core kernel (kernel=3)."""
-    cfg = type("Cfg", (), dict(B=8, Hq=28, Hkv=4, S=4096, D=128, n_sink=4, recent=128, mid=4096 - 132))
+def gqa7_decode_case(dev, B: int = 8, S: int = 4096):
+    """Decode at config 3's model shape (Hq=28, Hkv=4: 7 query heads per kv head,
+    reference INT4 middle, sink 4, recent 128; B=8, S=4096 by default): the INT4
+    kernel's two head passes (the default) against the general matrix-core kernel
+    (kernel=3)."""
+    cfg = type("Cfg", (), dict(B=B, Hq=28, Hkv=4, S=S, D=128, n_sink=4, recent=128, mid=S - 132))
     plans = build_instances(cfg, "int4", dev, 1003, N_INSTANCES)
     general = [TieredDecodePlan(*p._keep[:4], kernel=3) for p in plans]
     return plans, general, decode_bytes(cfg, "int4")
@@ -711,6 +712,16 @@ def main() -> int:
         extra["c3_shape_decode_gqa7_int4"] = {
             "us_two_head_passes": round(g2mean * 1e3, 2), "us_general_kernel": round(ggmean * 1e3, 2),
             "bytes": gb, "GBps_two_head_passes": round(gb / (g2mean * 1e-3) / 1e9, 1),
+        }
+        del g2, gg
+        torch.cuda.empty_cache()
+        # the same model shape at a size that is not launch-bound
+        g2, gg, gb = gqa7_decode_case(dev, B=16, S=8192)
+        g2mean, ggmean = graph_us(g2) * 1e-3, graph_us(gg) * 1e-3
+        extra["c3_shape_b16_s8192_decode_gqa7_int4"] = {
+            "us_two_head_passes": round(g2mean * 1e3, 2), "us_general_kernel": round(ggmean * 1e3, 2),
+            "bytes": gb, "GBps_two_head_passes": round(gb / (g2mean * 1e-3) / 1e9, 1),
+            "frac_of_peak": round(gb / (g2mean * 1e-3) / 1e9 / HBM_PEAK_GBPS, 3),
         }
         del g2, gg
         torch.cuda.empty_cache()
