@@ -216,10 +216,10 @@ def test_quant_int2_grouped_bit_exact(dev, S):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("S", [128, 100, 1])
-def test_quant_int2_grouped_typed_bit_exact(dev, dtype, S):
-    print(f"case int2 grouped {dtype} S={S}", flush=True)
-    x = _typed_edge((2, 3, 128, 128), 8, dtype)[:, :, :S]
+@pytest.mark.parametrize("S,D", [(128, 128), (100, 128), (1, 128), (70, 64), (64, 256), (65, 32)])
+def test_quant_int2_grouped_typed_bit_exact(dev, dtype, S, D):
+    print(f"case int2 grouped {dtype} S={S} D={D}", flush=True)
+    x = _typed_edge((2, 3, 128, D), 8, dtype)[:, :, :S]
     xp, _ = oq.pad_to_group(x, 64)
     oqv, osc = oq.quant_int2_grouped_typed(xp, dtype, 64)
     q, sc = fq.quant_int2_padded(_dev_typed(x, dtype, dev), 64)
