@@ -6,8 +6,8 @@
 // the reference's materialized tiers, fade/cache.py:347-379,683-842).
 //
 // Workgroup = (query blocks and head pass, kv head, batch row): one or two
-// groups of 4 waves, group q serving the q-th 32-query block; wave w of a
-// group serves query head kvh*G + 4*pass + w (G = Hq/Hkv <= 8: one pass of up
+// groups of 4 waves (interleaved: wave w belongs to group w % NQB), group q
+// serving the q-th 32-query block; wave w of a group serves query head kvh*G + 4*pass + w (G = Hq/Hkv <= 8: one pass of up
 // to 4 heads for G <= 4, two passes for G = 5..8), its 32 query rows as one
 // 32-row M tile.  With two groups, the first stages and dequantizes each
 // tile's K and the second its V, so one dequantization serves 64 queries per
@@ -148,8 +148,10 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
   }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wq = wave & 3, qblk = wave >> 2;  // wave within its group, the group's query block
-  const int gtid = tid & (kThreads - 1);      // thread within its group of 4 waves
+  // groups interleaved: wave w is wave w / NQB of group w % NQB (1% faster
+  // than groups of consecutive waves)
+  const int wq = wave / NQB, qblk = wave % NQB;  // wave within its group, the group's query block
+  const int gtid = (wq << 6) | lane;             // thread within its group of 4 waves
   // staging roles: K (codes, scales) and V (codes, scales) of every tile
   const bool do_k = NQB == 1 || qblk == 0, do_v = NQB == 1 || qblk == NQB - 1;
   const int n16 = lane & 15, g = lane >> 4;
