@@ -777,7 +777,7 @@ def main() -> int:
             "algorithmic_bytes_per_call": nbytes,
             "timed": f"the K={args.steps} steps: HIP events around each of {replays} replay(s) of a HIP graph "
             f"of {calls} back-to-back calls (rotating over the {N_INSTANCES} instances) on the launch stream, "
-            f"value = their total / K (one kernel: decode_packed_kernel<4,4,0,4,false,false>, split merge "
+            f"value = their total / K (one kernel: decode_packed_kernel<4,4,0,4,false,false,false>, split merge "
             f"fused); median_us: a separate statistics pass, the median over {STATS_REPLAYS} replays of a "
             f"{STATS_CALLS}-call graph (per call = replay / {STATS_CALLS}); eager_us_per_call: HIP events "
             "around each separately launched call",
