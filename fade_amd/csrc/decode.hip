@@ -43,7 +43,8 @@ __device__ __forceinline__ uint4 pack8h(const float* x) {
 
 // One staging unit (channels 8 cg .. 8 cg + 7 of one token's K or V) as loaded
 // from HBM, before dequantization: fp16 tiers: the eight values; packed
-// middle tiers: x = codes (first code in the high bits), y = per-token scale
+// middle tiers: x = codes (first code in the high bits; the reference INT4
+// format: the dword as stored, first code in bits 4..7), y = per-token scale
 // (low half) and zero (high half) where the format has them; literal INT2 V:
 // x, y = the eight int8 codes.
 struct RawUnit {
@@ -100,7 +101,14 @@ __device__ __forceinline__ RawUnit load_unit(const Params& p, int64_t b, int64_t
   }
   const int bits = SYM44 || fmt == FADE_MID_K4V2G ? 4 : (IS_V ? p.mid.v_bits : p.mid.k_bits);
   const uint8_t* src = (IS_V ? p.mid.v_codes : p.mid.k_codes) + row * (D * bits / 8);
-  if (bits == 4) {
+  if (SYM44) {  // the dword as stored (sym4_to_f16 takes it so)
+    const uint8_t* c = src + 4 * cg;
+    if ((reinterpret_cast<uintptr_t>(c) & 3) == 0)
+      ru.w.x = *reinterpret_cast<const uint32_t*>(c);
+    else
+      ru.w.x = static_cast<uint32_t>(c[0]) | (static_cast<uint32_t>(c[1]) << 8) |
+               (static_cast<uint32_t>(c[2]) << 16) | (static_cast<uint32_t>(c[3]) << 24);
+  } else if (bits == 4) {
     const uint8_t* c = src + 4 * cg;
     if ((reinterpret_cast<uintptr_t>(c) & 3) == 0)
       ru.w.x = __builtin_bswap32(*reinterpret_cast<const uint32_t*>(c));
@@ -125,15 +133,49 @@ __device__ __forceinline__ RawUnit load_unit(const Params& p, int64_t b, int64_t
   return ru;
 }
 
+// Eight two's-complement nibbles (one dword as stored: byte k holds channel
+// 2k in its high and 2k + 1 in its low nibble) -> fp16(c * scale) of the
+// eight channels in order, dword k = channels (2k, 2k + 1).  Each nibble goes
+// to mantissa bits 4..7 of 64.0 (one code step = 1.0) with its top bit
+// flipped, i.e. the fp16 value 72 + c, exact; then - 72 and one packed fp16
+// multiply, whose single rounding equals the reference's fp16(code * scale).
+// s2: the scales of the four channel pairs (for V one scale twice).
+__device__ __forceinline__ uint4 sym4_to_f16(uint32_t w, const uint32_t (&s2)[4]) {
+  const uint32_t o0 = ((w << 4) & 0x00F000F0u) ^ 0x54805480u;  // channels (1, 5)
+  const uint32_t o1 = (w & 0x00F000F0u) ^ 0x54805480u;         // (0, 4)
+  const uint32_t o2 = ((w >> 4) & 0x00F000F0u) ^ 0x54805480u;  // (3, 7)
+  const uint32_t o3 = ((w >> 8) & 0x00F000F0u) ^ 0x54805480u;  // (2, 6)
+  const uint32_t n[4] = {__builtin_amdgcn_perm(o0, o1, 0x05040100u), __builtin_amdgcn_perm(o2, o3, 0x05040100u),
+                         __builtin_amdgcn_perm(o0, o1, 0x07060302u), __builtin_amdgcn_perm(o2, o3, 0x07060302u)};
+  const f16x2 m72 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+  uint32_t x[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    x[k] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, n[k]) + m72) * __builtin_bit_cast(f16x2, s2[k]));
+  return make_uint4(x[0], x[1], x[2], x[3]);
+}
+
 // A loaded unit dequantized as the reference does (fp16(code * scale),
 // fp16(code * scale + zero) for the asymmetric format): eight fp16 values.
-// ks_s: the row's per-channel K scales (fp32).
+// ks_s: the row's per-channel K scales (fp32); ks2_s: the same as fp16 pairs.
 template <int D, bool IS_V, bool SYM44>
 __device__ __forceinline__ uint4 convert_unit(const Params& p, int64_t b, int64_t kvh, UnitRef u, int cg,
-                                              const RawUnit& ru, const float* ks_s) {
+                                              const RawUnit& ru, const float* ks_s, const uint32_t* ks2_s) {
   const int fmt = SYM44 ? FADE_MID_SYM : p.mid.fmt;
   if (u.seg != 1 || fmt == FADE_MID_FP16) return ru.w;
   const int d0 = 8 * cg;
+  if (SYM44) {
+    uint32_t s2[4];
+    if (IS_V) {
+      const uint32_t sv = ru.w.y & 0xFFFFu;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) s2[k] = sv | (sv << 16);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) s2[k] = ks2_s[d0 / 2 + k];
+    }
+    return sym4_to_f16(ru.w.x, s2);
+  }
   float x[8];
   if (IS_V && fmt == FADE_MID_K4V2G) {  // literal grouped INT2 V: per-(group, channel) scales
     const int64_t bkv = b * p.Hkv + kvh;
@@ -178,34 +220,54 @@ __device__ __forceinline__ uint4 convert_unit(const Params& p, int64_t b, int64_
   return pack8h(x);
 }
 
-__device__ __forceinline__ void unpack8h(const uint4& w, float* x) {
-  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    x[2 * j] = h2f(static_cast<uint16_t>(u[j] & 0xFFFFu));
-    x[2 * j + 1] = h2f(static_cast<uint16_t>(u[j] >> 16));
-  }
+// Max over the 64 lanes of a wave (all lanes active): DPP exchanges within
+// each row of 16 lanes (lane ^ 1, lane ^ 2, rotations by 4 and 8), then the
+// four row maxima read as scalars.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_max64(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = fmaxf(v, dpp_f<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp_f<0x128>(v));  // row_ror:8
+  const int iv = __builtin_bit_cast(int, v);
+  return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16))),
+               fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48))));
 }
 
 // Portable kernel, head_dim D (32, 64, 128 or 256), up to HP query heads per kv
 // head (4 or 8), any middle format.  Per tile of 64 tokens:
 //   stage: all threads dequantize the tile's K and V into LDS (fp16, the
-//          reference's rounding), one 8-channel unit per thread and step,
-//          coalesced global loads;
+//          reference's rounding), one (token pair, 8-channel group) unit per
+//          thread and step, coalesced global loads; K rows as they are, V as
+//          dwords of one channel of two consecutive tokens;
 //   QK:    thread (token = lane, heads wave and wave + 4) dots the K row with
 //          the fp16 query (v_dot2_f32_f16: fp16 pairs, fp32 sums), then the
-//          wave's online softmax in the log2 domain;
+//          wave's online softmax in the log2 domain; the probabilities are
+//          kept in fp16 for PV (as the matrix-core kernels do), the row sums
+//          in fp32;
 //   PV:    thread (head, 8-channel group, token slice) accumulates P V over its
-//          slice of the tile's tokens; the slices are summed once per split.
+//          slice of the tile's tokens, one v_dot2_f32_f16 per channel and
+//          token pair; the slices are summed once per split.
+// The split's partial (m, l, acc) goes to the workspace and
+// decode_combine_kernel merges the splits; with one split the kernel writes
+// the output directly.  (Merging in the last workgroup to finish, as the
+// matrix-core kernel does, measured slower here: these workgroups are short,
+// and each then waits for its partial stores and a counter round trip.)
 template <int D, int HP, bool SYM44>
 __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
   constexpr int CG = D / 8;                 // 8-channel units per row
-  constexpr int KP = D + 8;                 // LDS row pitch (halves)
+  constexpr int KP = D + 8;                 // K row pitch in LDS (halves)
+  constexpr int VPP = D + 4;                // V token-pair row pitch in LDS (dwords)
   constexpr int NU = HP * CG;               // (head, unit) outputs
   constexpr int TQ = kThreads / NU;         // token slices per output
   constexpr int TPS = kTile / TQ;           // tokens per slice
   constexpr int HPW = HP / 4;               // heads per wave in QK
-  static_assert(TQ >= 1 && kThreads % NU == 0, "PV decomposition");
+  static_assert(TQ >= 1 && kThreads % NU == 0 && TPS % 2 == 0, "PV decomposition");
   const int split = blockIdx.x;
   const int64_t kvh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -213,9 +275,10 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
 
   __shared__ __attribute__((aligned(16))) uint32_t q2_s[HP][D / 2];  // fp16 query pairs
   __shared__ float ks_s[D];
+  __shared__ uint32_t ks2_s[SYM44 ? D / 2 : 1];
   __shared__ __attribute__((aligned(16))) uint16_t kt[kTile][KP];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[kTile][KP];
-  __shared__ float p_s[HP][kTile];
+  __shared__ __attribute__((aligned(16))) uint32_t vp[kTile / 2][VPP];  // (token 2i, 2i + 1) of one channel
+  __shared__ __attribute__((aligned(4))) uint16_t ph_s[HP][kTile];     // fp16 probabilities
   __shared__ float alpha_s[HP];
   __shared__ __attribute__((aligned(16))) float red[TQ > 1 ? TQ : 1][NU][8];
 
@@ -226,6 +289,11 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
   }
   if (p.mid.fmt == FADE_MID_SYM || p.mid.fmt == FADE_MID_K4V2G)
     for (int d = tid; d < D; d += kThreads) ks_s[d] = h2f(p.mid.k_scale[(b * p.Hkv + kvh) * D + d]);
+  if (SYM44)
+    for (int d = tid; d < D / 2; d += kThreads) {
+      const uint16_t* ks = p.mid.k_scale + (b * p.Hkv + kvh) * D + 2 * d;
+      ks2_s[d] = static_cast<uint32_t>(ks[0]) | (static_cast<uint32_t>(ks[1]) << 16);
+    }
   if (tid < HP) alpha_s[tid] = 1.0f;
 
   // the row's tier lengths: the tiers' own, or per row (lens, clamped to the padded tiers)
@@ -253,37 +321,58 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
 
-  // Staging: thread tid owns units tid + kThreads * i (token u / CG, group u % CG)
-  // of every tile: all loads of the tile are issued, then dequantized into LDS.
-  // (Loading the next tile's units during this tile's compute measured no faster.)
-  constexpr int UPT = kTile * CG / kThreads > 0 ? kTile * CG / kThreads : 1;
-  RawUnit rk[UPT], rv[UPT];
+  // Staging: thread tid owns units tid + kThreads * i (tokens 2 (u / CG) and
+  // 2 (u / CG) + 1, group u % CG) of every tile: all loads of the tile are
+  // issued, then dequantized into LDS.  (Loading the next tile's units during
+  // this tile's compute measured no faster.)
+  constexpr int NPU = kTile / 2 * CG;
+  constexpr int PPT = (NPU + kThreads - 1) / kThreads;
+  RawUnit rk[PPT][2], rv[PPT][2];
   auto load_tile = [&](int64_t ts, int nv) {
 #pragma unroll
-    for (int i = 0; i < UPT; ++i) {
+    for (int i = 0; i < PPT; ++i) {
       const int uidx = tid + kThreads * i;
-      const int r = uidx / CG, cg = uidx % CG;
-      if (uidx < kTile * CG && r < nv) {
-        const UnitRef ur = unit_ref(ts + r, ns, nm);
-        rk[i] = load_unit<D, false, SYM44>(p, b, kvh, ur, cg);
-        rv[i] = load_unit<D, true, SYM44>(p, b, kvh, ur, cg);
-      }
+      const int rp = uidx / CG, cg = uidx % CG;
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        if (uidx < NPU && 2 * rp + e < nv) {
+          const UnitRef ur = unit_ref(ts + 2 * rp + e, ns, nm);
+          rk[i][e] = load_unit<D, false, SYM44>(p, b, kvh, ur, cg);
+          rv[i][e] = load_unit<D, true, SYM44>(p, b, kvh, ur, cg);
+        }
     }
   };
   auto store_tile = [&](int64_t ts, int nv) {  // tokens past nv as zeros
 #pragma unroll
-    for (int i = 0; i < UPT; ++i) {
+    for (int i = 0; i < PPT; ++i) {
       const int uidx = tid + kThreads * i;
-      const int r = uidx / CG, cg = uidx % CG;
-      if (uidx < kTile * CG) {
-        uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
-        if (r < nv) {
-          const UnitRef ur = unit_ref(ts + r, ns, nm);
-          kw = convert_unit<D, false, SYM44>(p, b, kvh, ur, cg, rk[i], ks_s);
-          vw = convert_unit<D, true, SYM44>(p, b, kvh, ur, cg, rv[i], ks_s);
+      const int rp = uidx / CG, cg = uidx % CG;
+      if (uidx < NPU) {
+        uint32_t vw[2][4];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int r = 2 * rp + e;
+          uint4 kw = make_uint4(0, 0, 0, 0), v = make_uint4(0, 0, 0, 0);
+          if (r < nv) {
+            const UnitRef ur = unit_ref(ts + r, ns, nm);
+            kw = convert_unit<D, false, SYM44>(p, b, kvh, ur, cg, rk[i][e], ks_s, ks2_s);
+            v = convert_unit<D, true, SYM44>(p, b, kvh, ur, cg, rv[i][e], ks_s, ks2_s);
+          }
+          *reinterpret_cast<uint4*>(&kt[r][8 * cg]) = kw;
+          vw[e][0] = v.x;
+          vw[e][1] = v.y;
+          vw[e][2] = v.z;
+          vw[e][3] = v.w;
         }
-        *reinterpret_cast<uint4*>(&kt[r][8 * cg]) = kw;
-        *reinterpret_cast<uint4*>(&vt[r][8 * cg]) = vw;
+        // channel 2k: the low halves of dword k of both tokens; 2k + 1: the high halves
+        uint32_t pr[8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          pr[2 * k] = __builtin_amdgcn_perm(vw[1][k], vw[0][k], 0x05040100u);
+          pr[2 * k + 1] = __builtin_amdgcn_perm(vw[1][k], vw[0][k], 0x07060302u);
+        }
+        *reinterpret_cast<uint4*>(&vp[rp][8 * cg]) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+        *reinterpret_cast<uint4*>(&vp[rp][8 * cg + 4]) = make_uint4(pr[4], pr[5], pr[6], pr[7]);
       }
     }
   };
@@ -321,14 +410,14 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
         const int h = wave + 4 * i;
         if (h < G) {
           const float sc = lane < nv ? s[i] : -INFINITY;
-          const float m_new = fmaxf(m_run[i], group_max<64>(sc));
+          const float m_new = fmaxf(m_run[i], wave_max64(sc));
           float alpha = 1.0f, pv = 0.0f;
           if (m_new != -INFINITY) {
-            alpha = exp2f(m_run[i] - m_new);
-            pv = exp2f(sc - m_new);
+            alpha = __builtin_amdgcn_exp2f(m_run[i] - m_new);
+            pv = __builtin_amdgcn_exp2f(sc - m_new);
           }
           l_lane[i] = l_lane[i] * alpha + pv;
-          p_s[h][lane] = pv;
+          ph_s[h][lane] = f2h(pv);
           if (lane == 0) alpha_s[h] = alpha;
           m_run[i] = m_new;
         }
@@ -340,32 +429,46 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
       const float al = alpha_s[ph];
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] *= al;
+      // token pairs; past nv the probabilities and V are zeros
       const int r0 = pq * TPS;
-      const int r1 = r0 + TPS < nv ? r0 + TPS : nv;
-      for (int r = r0; r < r1; ++r) {
-        const float pp = p_s[ph][r];
-        float v8[8];
-        unpack8h(*reinterpret_cast<const uint4*>(&vt[r][8 * pc]), v8);
+      const int nv2 = (nv + 1) & ~1;
+      const int r1 = r0 + TPS < nv2 ? r0 + TPS : nv2;
+      for (int r = r0; r < r1; r += 2) {
+        const f16x2 p2 = __builtin_bit_cast(f16x2, *reinterpret_cast<const uint32_t*>(&ph_s[ph][r]));
+        const uint4 va = *reinterpret_cast<const uint4*>(&vp[r / 2][8 * pc]);
+        const uint4 vb = *reinterpret_cast<const uint4*>(&vp[r / 2][8 * pc + 4]);
+        const uint32_t v8[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = fmaf(pp, v8[j], acc[j]);
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, v8[j]), p2, acc[j], false);
       }
     }
     __syncthreads();
   }
 
-  // ---- partial (m, l, acc) of each head ----
+  // ---- partial (m, l, acc) of each head, or the output with one split ----
+  __shared__ float l_s[HP];
+  const int n = p.n_splits;
+  const int64_t row0 = b * p.Hq + kvh * G;  // partial rows: query head (b, kvh G + h)
 #pragma unroll
   for (int i = 0; i < HPW; ++i) {
     const int h = wave + 4 * i;
     if (h < G) {
       const float l = group_sum<64>(l_lane[i]);
       if (lane == 0) {
-        const int64_t idx = (b * p.Hq + kvh * G + h) * p.n_splits + split;
-        p.ws_ml[2 * idx] = m_run[i];
-        p.ws_ml[2 * idx + 1] = l;
+        l_s[h] = l;
+        if (n > 1) {
+          p.ws_ml[2 * ((row0 + h) * n + split)] = m_run[i];
+          p.ws_ml[2 * ((row0 + h) * n + split) + 1] = l;
+        }
       }
     }
   }
+  auto emit = [&](int h, int d, float v) {  // the split's P V sum of (head h, channel d)
+    if (n == 1)
+      p.out[b * p.o_sb + (kvh * G + h) * p.o_sh + d] = f2h(v / l_s[h]);
+    else
+      p.ws_acc[((row0 + h) * n + split) * D + d] = v;
+  };
   if (TQ > 1) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) red[TQ > 1 ? pq : 0][po][j] = acc[j];
@@ -375,14 +478,15 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
       if (h < G) {
         float sum = 0.0f;
         for (int q = 0; q < TQ; ++q) sum += red[q][oo][j];
-        const int64_t idx = (b * p.Hq + kvh * G + h) * p.n_splits + split;
-        p.ws_acc[idx * D + 8 * cg + j] = sum;
+        emit(h, 8 * cg + j, sum);
       }
     }
-  } else if (ph < G) {
-    const int64_t idx = (b * p.Hq + kvh * G + ph) * p.n_splits + split;
+  } else {
+    __syncthreads();  // l_s
+    if (ph < G) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) p.ws_acc[idx * D + 8 * pc + j] = acc[j];
+      for (int j = 0; j < 8; ++j) emit(ph, 8 * pc + j, acc[j]);
+    }
   }
 }
 

@@ -258,17 +258,18 @@ int run_plan(const fade_decode_args* a, Params& p, const Plan& pl, uint32_t* cou
   p.tokens_per_split = pl.tps;
   p.ws_ml = reinterpret_cast<float*>(partials);
   p.ws_acc = reinterpret_cast<float*>(partials + (ws.acc - ws.ml));
+  p.out = static_cast<uint16_t*>(a->out);
+  p.o_sb = a->o_sb;
+  p.o_sh = a->o_sh;
+  p.counters = counters;
   if (pl.k == Kern::kInt4) {
-    p.out = static_cast<uint16_t*>(a->out);
-    p.o_sb = a->o_sb;
-    p.o_sh = a->o_sh;
     p.n_f16_tiles = pl.n_f16_tiles;
     p.tiles_per_split = pl.tiles_per_split;
-    p.counters = counters;
     return launch_int4(p, st);
   }
-  int rc = pl.k == Kern::kMfma ? launch_mfma(p, st) : launch_valu(p, st);
+  const int rc = pl.k == Kern::kMfma ? launch_mfma(p, st) : launch_valu(p, st);
   if (rc) return rc;
+  if (pl.k == Kern::kValu && p.n_splits == 1) return 0;  // the portable kernel wrote the output
   const int64_t rows = a->B * a->Hq;
   hipLaunchKernelGGL(decode_combine_kernel, dim3(static_cast<unsigned>(rows)), dim3(static_cast<unsigned>(p.D)), 0, st, p.ws_ml,
                      p.ws_acc, p.n_splits, a->Hq, static_cast<uint16_t*>(a->out), a->o_sb, a->o_sh);

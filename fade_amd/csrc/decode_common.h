@@ -48,12 +48,14 @@ struct Params {
   int n_splits;
   float* ws_ml;   // [B][Hq][n_splits][2]  (m, l); INT4 kernel: [B*Hkv][n_splits][4][2]
   float* ws_acc;  // [B][Hq][n_splits][D] unnormalized output; INT4 kernel: [B*Hkv][n_splits][4][kD]
-  // INT4 kernel only
+  // output (the INT4 kernel; the portable kernel with one split) and split
+  // counters (INT4 kernel)
   uint16_t* out;
   int64_t o_sb, o_sh;
+  uint32_t* counters;       // [B*Hkv*passes] finished splits; zero between calls
+  // INT4 kernel only
   int64_t n_f16_tiles;      // 16-token fp16 tiles ahead of the packed 64-token tiles
   int64_t tiles_per_split;  // tiles (either kind) per split
-  uint32_t* counters;       // [B*Hkv] finished splits; zero between calls
   const int32_t* lens;      // optional [B][3] per-row sink / middle / recent lengths
   int32_t deterministic;    // INT4 kernel: fixed round-robin tile order instead of claims
   int passes;               // INT4 kernel: head passes per kv head, ceil(G / 4): 1 or 2
@@ -106,6 +108,29 @@ int launch_int4(const Params& p, hipStream_t st);
 int mfma_tile();
 // Number of 64-token tiles the matrix-core kernel walks (fp16 tokens, then packed).
 int64_t mfma_tiles(const Params& p);
+
+// Split partials and their merge reads: device-coherent (agent-scope) accesses,
+// per instruction, with no whole-cache write-back or invalidate.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT));
+}
+// (m, l) of one partial as one 8-byte device-coherent access
+__device__ __forceinline__ void store_agent2(float* p, float a, float b) {
+  const uint64_t v = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, a)) |
+                     (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, b)) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void load_agent2(const float* p, float& a, float& b) {
+  const uint64_t v =
+      __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  a = __builtin_bit_cast(float, static_cast<uint32_t>(v));
+  b = __builtin_bit_cast(float, static_cast<uint32_t>(v >> 32));
+}
 
 }  // namespace decode
 }  // namespace fade

@@ -176,27 +176,6 @@ __device__ __forceinline__ void tile_dma2(const void* g, uint32_t lds) {
   else lds_dma2(g, lds);
 }
 
-__device__ __forceinline__ void store_agent(float* p, float v) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_agent(const float* p) {
-  return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT));
-}
-// (m, l) of one partial as one 8-byte device-coherent access
-__device__ __forceinline__ void store_agent2(float* p, float a, float b) {
-  const uint64_t v = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, a)) |
-                     (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, b)) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void load_agent2(const float* p, float& a, float& b) {
-  const uint64_t v =
-      __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  a = __builtin_bit_cast(float, static_cast<uint32_t>(v));
-  b = __builtin_bit_cast(float, static_cast<uint32_t>(v >> 32));
-}
-
 __device__ __forceinline__ float half_of(uint32_t dw, int hi) {
   return h2f(static_cast<uint16_t>(hi ? dw >> 16 : dw & 0xFFFFu));
 }

@@ -70,8 +70,9 @@ template <int D>
 constexpr int kKPitch = D + 8;
 constexpr int kVtPitch = 72;  // halves per V^T row in LDS (16-byte accesses of 8 consecutive rows: distinct banks)
 constexpr float kNegBig = -1.0e30f;
-constexpr float kTau = 8.0f;  // the running max moves only when a score exceeds it by kTau (log2)
-constexpr float kTauP = 256.0f;  // 2^kTau
+// The running max moves only when a score exceeds it by kTau = 8 (log2 units),
+// i.e. when a probability exceeds kTauP = 2^kTau.
+constexpr float kTauP = 256.0f;
 
 struct Tier {
   const uint16_t* k;

@@ -63,7 +63,7 @@ def test_decode_head_dims(dev, D, fmt, B, Hq, Hkv, S, ns, nr):
     sink = (_t(dev, k[:, :, :ns]), _t(dev, v[:, :, :ns])) if ns else None
     rec = (_t(dev, k[:, :, S - nr :]), _t(dev, v[:, :, S - nr :])) if nr else None
     ref = oatt.tiered_decode(q, k[:, :, :ns], v[:, :, :ns], omid, k[:, :, S - nr :], v[:, :, S - nr :])
-    for n_splits in (0, 3):
+    for n_splits in (0, 1, 3):  # 1: the portable kernel writes the output itself
         out = tiered_decode_attention(_t(dev, q), sink, mid, rec, n_splits=n_splits)
         assert out.shape == (B, Hq, 1, D)
         assert np.abs(out.float().cpu().numpy() - ref).max() <= ATOL, n_splits
@@ -243,7 +243,7 @@ def test_decode_head_dims_ragged_lens(dev, D):
     lens = np.array([[4, 600, 64], [2, 130, 17], [4, 1, 0], [0, 333, 64], [1, 0, 5]], dtype=np.int32)
     sink = (_t(dev, k[:, :, :ns_c]), _t(dev, v[:, :, :ns_c]))
     rec = (_t(dev, k[:, :, S - nr_c :]), _t(dev, v[:, :, S - nr_c :]))
-    for n_splits in (0, 7):
+    for n_splits in (0, 1, 7):
         out = tiered_decode_attention(_t(dev, q), sink, mid, rec, lens=_t(dev, lens), n_splits=n_splits)
         out = out.float().cpu().numpy()
         for b, (ls, lm, lr) in enumerate(lens):
