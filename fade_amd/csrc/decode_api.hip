@@ -25,11 +25,13 @@ int64_t total_tokens(const fade_decode_args* a) { return a->sink.len + a->mid.le
 // wave of the machine (measured best for configs 1 and 2); the portable
 // kernel wants more, smaller workgroups.
 void plan_splits(const fade_decode_args* a, int tile, int64_t* n_splits, int64_t* tps,
-                 int64_t total_override = -1, int64_t target_wgs = 2048) {
+                 int64_t total_override = -1, int64_t target_wgs = 2048, int64_t min_tiles = 1) {
   const int64_t total = total_override >= 0 ? total_override : total_tokens(a);
   const int64_t pairs = a->B * a->Hkv;
   int64_t want = a->n_splits > 0 ? a->n_splits : (target_wgs + pairs / 2) / (pairs > 0 ? pairs : 1);
   const int64_t max_splits = cdiv(total, tile) > 0 ? cdiv(total, tile) : 1;
+  // automatic split counts keep at least min_tiles tiles per split
+  if (a->n_splits <= 0 && want > cdiv(total, tile * min_tiles)) want = cdiv(total, tile * min_tiles);
   if (want > max_splits) want = max_splits;
   if (want < 1) want = 1;
   int64_t t = cdiv(cdiv(total, want), tile) * tile;
@@ -223,9 +225,15 @@ Plan make_plan(const fade_decode_args* a, const Params& p) {
     pl.n = cdiv(nT, pl.tiles_per_split);
     return pl;
   }
-  const bool mfma = pl.k == Kern::kMfma;
-  plan_splits(a, mfma ? mfma_tile() : 64, &pl.n, &pl.tps, mfma ? mfma_tiles(p) * mfma_tile() : -1,
-              mfma ? 512 : 2048);
+  if (pl.k == Kern::kMfma) {
+    plan_splits(a, mfma_tile(), &pl.n, &pl.tps, mfma_tiles(p) * mfma_tile(), 512);
+    return pl;
+  }
+  // Portable kernel: at least four 64-token tiles per split, about 1024
+  // workgroups (2048 at head_dim 128).  Measured at head dims 32, 64, 128 and
+  // 256, 14/2 and 32/8 heads, B = 4 and 16: below that the per-split set-up
+  // and partials outweigh the added parallelism.
+  plan_splits(a, 64, &pl.n, &pl.tps, -1, p.D == 128 ? 2048 : 1024, 4);
   return pl;
 }
 
