@@ -551,6 +551,34 @@ def prefill_pass(calls: int) -> int:
     return 0
 
 
+def portable_pass(calls: int, head_dim: int) -> int:
+    """``calls`` launches of the portable decode kernel at another head dim (B=16,
+    32/8 heads, S=8192, reference INT4 middle), for ``rocprofv3`` runs; prints the
+    mean call time (HIP events) of 200 more."""
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, S, D, ns, nr = 16, 32, 8, 8192, head_dim, 4, 64
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, Hq, 1, D, device=dev, generator=g).half()
+    k = torch.randn(B, Hkv, S, D, device=dev, generator=g).half()
+    v = torch.randn(B, Hkv, S, D, device=dev, generator=g).half()
+    kq, ks = fq.quant_k_int4(k[:, :, ns:S - nr].contiguous())
+    vq, vs = fq.quant_v_int4(v[:, :, ns:S - nr].contiguous())
+    plan = TieredDecodePlan(q, (k[:, :, :ns].contiguous(), v[:, :, :ns].contiguous()), MiddleTier("int4", kq, vq, ks, vs),
+                            (k[:, :, S - nr:].contiguous(), v[:, :, S - nr:].contiguous()), kernel=1)
+    for _ in range(calls):
+        plan.run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(200):
+        plan.run()
+    e1.record()
+    torch.cuda.synchronize()
+    print(json.dumps({"portable_pass": True, "head_dim": D, "calls": calls + 200,
+                      "us_per_call": round(e0.elapsed_time(e1) / 200 * 1e3, 2)}))
+    return 0
+
+
 def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
     """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the decode kernel, scaled by
     what the same counters read for the copy kernel (which moves COPY_MIB each way)."""
@@ -607,6 +635,8 @@ def main() -> int:
                     help="copy calibration + --steps decode calls, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--prefill-pass", action="store_true",
                     help="--steps config-4 prefill calls only, for rocprofv3 --pmc SQ counters")
+    ap.add_argument("--portable-pass", type=int, metavar="HEAD_DIM",
+                    help="--steps calls of the portable decode kernel at HEAD_DIM (32, 64, 256), for rocprofv3")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc output folders into " + os.path.relpath(TRAFFIC_FILE, ROOT))
     args = ap.parse_args()
@@ -623,6 +653,8 @@ def main() -> int:
         return pmc_pass(args.steps)
     if args.prefill_pass:
         return prefill_pass(args.steps)
+    if args.portable_pass:
+        return portable_pass(args.steps, args.portable_pass)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(dev)
