@@ -1052,16 +1052,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   if (n == 1) return;
 
   // ---- the last workgroup of this (batch row, kv head) merges the splits ----
-  // Partials, counter and the merge reads are device-coherent accesses
-  // (agent-scope atomics: per-instruction coherence, no whole-L2 write-back or
-  // invalidate).  Order: each thread's partial stores complete (vmcnt(0))
-  // before the barrier, the barrier before the counter increment, and the
-  // merge loads issue only after the increment has returned.
+  // Release/acquire on the split counter at agent scope (the L2s of the XCDs
+  // are separate caches):
+  // - writers: every wave waits for its own partial stores (vmcnt(0); the
+  //   workgroup barrier alone does not wait for other waves' stores), then
+  //   thread 0 releases (L2 write-back) and increments the counter;
+  // - the workgroup whose increment returns n - 1 acquires (invalidates its
+  //   L1 and its L2's lines of other XCDs' memory) before the barrier that
+  //   lets its waves load the partials.
+  // The partial stores and loads are agent-scope accesses as well.
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
   __syncthreads();
   if (tid == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     const uint32_t prev = __hip_atomic_fetch_add(&p.counters[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last_s = prev == static_cast<uint32_t>(n - 1);
+    const bool last = prev == static_cast<uint32_t>(n - 1);
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    last_s = last;
   }
   __syncthreads();
   if (!last_s) return;
