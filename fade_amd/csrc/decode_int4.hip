@@ -1052,19 +1052,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   if (n == 1) return;
 
   // ---- the last workgroup of this (batch row, kv head) merges the splits ----
-  // Release/acquire on the split counter at agent scope (the L2s of the XCDs
-  // are separate caches):
-  // - writers: every wave waits for its own partial stores (vmcnt(0); the
-  //   workgroup barrier alone does not wait for other waves' stores), then
-  //   thread 0 releases (L2 write-back) and increments the counter;
-  // - the workgroup whose increment returns n - 1 acquires (invalidates its
-  //   L1 and its L2's lines of other XCDs' memory) before the barrier that
-  //   lets its waves load the partials.
-  // The partial stores and loads are agent-scope accesses as well.
+  // Cross-workgroup protocol at agent scope (the XCDs' L2s are separate caches):
+  // - writers: every (m, l, acc) partial is an agent-scope atomic store
+  //   (global_store ... sc1: written through the L2 to the agent's coherence
+  //   point, so no line of it stays dirty in an L2); every wave waits for the
+  //   completion of its own stores (vmcnt(0); the workgroup barrier alone does
+  //   not wait for other waves' stores), then thread 0 increments the counter.
+  //   No release fence: its buffer_wbl2 sc1 writes back an XCD's whole L2 for
+  //   the sake of non-atomic stores, which this merge has none of (it cost
+  //   12 us per call at config 1);
+  // - the workgroup whose increment returns n - 1 has seen every other
+  //   increment, each issued after its partials completed; it acquires
+  //   (buffer_inv sc1: no L1 or L2 line of an earlier call's partials
+  //   survives) before the barrier that lets its waves issue the partial
+  //   loads, which are agent-scope atomic loads as well.
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
   __syncthreads();
   if (tid == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     const uint32_t prev = __hip_atomic_fetch_add(&p.counters[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = prev == static_cast<uint32_t>(n - 1);
     if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
