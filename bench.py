@@ -521,22 +521,24 @@ def cpu_baseline(cfg, plans) -> dict:
 
 COPY_MIB = 256
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_int4_c1_traffic.json")
+TRAFFIC_FILE_C2 = os.path.join(ROOT, "profiles", "decode_c2_32k_traffic.json")
 
 
-def pmc_pass(steps: int) -> int:
+def pmc_pass(steps: int, config: int = 1, fmt: str = "int4") -> int:
     """Short run for ``rocprofv3 --pmc``: a plain copy of known size (the counter
-    calibration), then ``steps`` config-1 INT4 decode calls."""
+    calibration), then ``steps`` decode calls of config ``config`` (1 or 2) in
+    middle format ``fmt`` (int4, k4v2, rot2, asym42, ...)."""
     dev = torch.device("cuda:0")
     src = torch.ones(COPY_MIB << 18, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    plans = build_instances(CONFIGS[1], "int4", dev, 1001, N_INSTANCES)
+    plans = build_instances(CONFIGS[config], fmt, dev, 1000 + config, N_INSTANCES)
     for i in range(steps):
         plans[i % len(plans)].run()
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_pass": True, "copy_MiB": COPY_MIB, "decode_calls": steps}))
+    print(json.dumps({"pmc_pass": True, "copy_MiB": COPY_MIB, "config": config, "fmt": fmt, "decode_calls": steps}))
     return 0
 
 
@@ -579,9 +581,11 @@ def portable_pass(calls: int, head_dim: int) -> int:
     return 0
 
 
-def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
+def summarize_pmc(fetch_dir: str, write_dir: str, config: int = 1, fmt: str = "int4") -> int:
     """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the decode kernel, scaled by
-    what the same counters read for the copy kernel (which moves COPY_MIB each way)."""
+    what the same counters read for the copy kernel (which moves COPY_MIB each way).
+    Config 1 INT4 goes to TRAFFIC_FILE (the headline line's ``traffic``); config-2
+    formats go to one entry each of TRAFFIC_FILE_C2."""
     import csv
 
     def per_kernel(d: str, counter: str):
@@ -615,11 +619,22 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
         out[f"{key}_scale"] = round(factor, 4)
         out[f"{key}_bytes"] = int(dec_kib * 1024 * factor)
     out["hbm_bytes_per_call"] = out["fetch_bytes"] + out["write_bytes"]
-    out["algorithmic_bytes_per_call"] = decode_bytes(CONFIGS[1], "int4")
+    out["algorithmic_bytes_per_call"] = decode_bytes(CONFIGS[config], fmt)
+    out["traffic_ratio"] = round(out["hbm_bytes_per_call"] / out["algorithmic_bytes_per_call"], 4)
     os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
-    with open(TRAFFIC_FILE, "w") as f:
-        json.dump(out, f, indent=1)
-        f.write("\n")
+    if config == 1 and fmt == "int4":
+        with open(TRAFFIC_FILE, "w") as f:
+            json.dump(out, f, indent=1)
+            f.write("\n")
+    else:
+        allf = {}
+        if os.path.exists(TRAFFIC_FILE_C2):
+            with open(TRAFFIC_FILE_C2) as f:
+                allf = json.load(f)
+        allf[f"c{config}_{fmt}"] = out
+        with open(TRAFFIC_FILE_C2, "w") as f:
+            json.dump(allf, f, indent=1, sort_keys=True)
+            f.write("\n")
     print(json.dumps(out))
     return 0
 
@@ -637,11 +652,14 @@ def main() -> int:
                     help="--steps config-4 prefill calls only, for rocprofv3 --pmc SQ counters")
     ap.add_argument("--portable-pass", type=int, metavar="HEAD_DIM",
                     help="--steps calls of the portable decode kernel at HEAD_DIM (32, 64, 256), for rocprofv3")
+    ap.add_argument("--pmc-config", type=int, default=1, choices=(1, 2),
+                    help="config of --pmc-pass / --summarize-pmc (default 1)")
+    ap.add_argument("--pmc-fmt", default="int4", help="middle format of --pmc-pass / --summarize-pmc (default int4)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc output folders into " + os.path.relpath(TRAFFIC_FILE, ROOT))
     args = ap.parse_args()
     if args.summarize_pmc:
-        return summarize_pmc(*args.summarize_pmc)
+        return summarize_pmc(*args.summarize_pmc, config=args.pmc_config, fmt=args.pmc_fmt)
     if args.gpus != 1:
         print(
             "bench.py: this build measures one GPU; the decode path shards by batch / kv head "
@@ -650,7 +668,7 @@ def main() -> int:
         )
         return 2
     if args.pmc_pass:
-        return pmc_pass(args.steps)
+        return pmc_pass(args.steps, args.pmc_config, args.pmc_fmt)
     if args.prefill_pass:
         return prefill_pass(args.steps)
     if args.portable_pass:
@@ -760,6 +778,10 @@ def main() -> int:
         extra["copy_peak_GBps"] = round(copy_peak(dev, stream), 1)
         torch.cuda.empty_cache()
         c2 = CONFIGS[2]
+        c2_traffic = {}
+        if os.path.exists(TRAFFIC_FILE_C2):
+            with open(TRAFFIC_FILE_C2) as f:
+                c2_traffic = json.load(f)
         for fmt in ("asym42", "k4v2", "int4", "rot2"):  # asym42: the format BASELINE states for config 2
             pl = build_instances(c2, fmt, dev, 1002, N_INSTANCES)
             mean2 = graph_us(pl) * 1e-3
@@ -768,6 +790,9 @@ def main() -> int:
                 "us": round(mean2 * 1e3, 2), "GBps": round(b2 / (mean2 * 1e-3) / 1e9, 1), "bytes": b2,
                 "frac_of_peak": round(b2 / (mean2 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 3),
             }
+            tr = c2_traffic.get(f"c2_{fmt}")
+            if tr is not None:  # rocprofv3 FETCH_SIZE + WRITE_SIZE of this format (profiles/decode_c2_32k.md)
+                extra[f"c2_32k_{fmt}"]["traffic_ratio"] = tr["traffic_ratio"]
             if fmt == "rot2":  # the product path: unrotated q / sink / recent, R applied in the kernel
                 extra[f"c2_32k_{fmt}"]["rotation"] = "in kernel (q R^T for the middle, middle output part times R)"
             del pl
