@@ -1394,9 +1394,9 @@ class TieredKVCache(DynamicCache):
         chunk = (rest[0][..., n_rest:, :], rest[1][..., n_rest:, :])
         sink = self._front_tier(st, sink)
         mid = None
-        if st.int4_kq is not None and self.middle_v_bits == 4:
+        if st.int4_kq is not None and self.middle_v_bits == 4 and int(q.shape[-1]) % 32 == 0:
             mid = MiddleTier("int4", st.int4_kq, st.int4_vq, st.int4_ks, st.int4_vs)
-        elif st.int4_kq is not None or st.backend_k is not None:
+        elif st.int4_kq is not None or st.backend_k is not None:  # (packed rows in place need head_dim % 32)
             mk, mv = self._mid_fp16(st)
             mid = MiddleTier("fp16", mk, mv)
         return tiered_prefill_attention(q, chunk, sink, mid, recent, sm_scale=sm_scale)

@@ -7,7 +7,7 @@
 // kv head, batch row) serves the whole GQA group of Hq/Hkv query heads, so
 // each KV byte is read once.  Each workgroup writes an unnormalized partial
 // (m, l, acc[D]) in the log2 domain; decode_combine_kernel merges the splits.
-// Head dims 32, 64, 128 and 256 (the matrix-core kernels take 128 only).
+// Head dims: any multiple of 8 up to 256 (the matrix-core kernels take 128 only).
 //
 // This file holds the portable VALU kernel (any middle format) and the
 // combine pass.  decode_mfma.hip holds the matrix-core kernel for the
@@ -63,10 +63,11 @@ __device__ __forceinline__ UnitRef unit_ref(int64_t t, int64_t ns, int64_t nm) {
 }
 
 // SYM44: the middle tier is the reference INT4 format (FADE_MID_SYM, 4-bit K
-// and V), known at compile time.
-template <int D, bool IS_V, bool SYM44>
+// and V), known at compile time.  Rows are p.D channels long.
+template <bool IS_V, bool SYM44>
 __device__ __forceinline__ RawUnit load_unit(const Params& p, int64_t b, int64_t kvh, UnitRef u, int cg) {
   const int d0 = 8 * cg;
+  const int D = p.D;
   RawUnit ru;
   if (u.seg != 1) {
     const Fp16Tier& seg = u.seg == 0 ? p.sink : p.recent;
@@ -158,12 +159,13 @@ __device__ __forceinline__ uint4 sym4_to_f16(uint32_t w, const uint32_t (&s2)[4]
 // A loaded unit dequantized as the reference does (fp16(code * scale),
 // fp16(code * scale + zero) for the asymmetric format): eight fp16 values.
 // ks_s: the row's per-channel K scales (fp32); ks2_s: the same as fp16 pairs.
-template <int D, bool IS_V, bool SYM44>
+template <bool IS_V, bool SYM44>
 __device__ __forceinline__ uint4 convert_unit(const Params& p, int64_t b, int64_t kvh, UnitRef u, int cg,
                                               const RawUnit& ru, const float* ks_s, const uint32_t* ks2_s) {
   const int fmt = SYM44 ? FADE_MID_SYM : p.mid.fmt;
   if (u.seg != 1 || fmt == FADE_MID_FP16) return ru.w;
   const int d0 = 8 * cg;
+  const int D = p.D;
   if (SYM44) {
     uint32_t s2[4];
     if (IS_V) {
@@ -239,8 +241,10 @@ __device__ __forceinline__ float wave_max64(float v) {
                      __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48))));
 }
 
-// Portable kernel, head_dim D (32, 64, 128 or 256), up to HP query heads per kv
-// head (4 or 8), any middle format.  Per tile of 64 tokens:
+// Portable kernel, head_dim p.D (a multiple of 8 up to the instance's capacity
+// DP = 32, 64, 128 or 256; the 8-channel units past p.D stage zeros and emit
+// nothing), up to HP query heads per kv head (4 or 8), any middle format.
+// Per tile of 64 tokens:
 //   stage: all threads dequantize the tile's K and V into LDS (fp16, the
 //          reference's rounding), one (token pair, 8-channel group) unit per
 //          thread and step, coalesced global loads; K rows as they are, V as
@@ -258,11 +262,11 @@ __device__ __forceinline__ float wave_max64(float v) {
 // the output directly.  (Merging in the last workgroup to finish, as the
 // matrix-core kernel does, measured slower here: these workgroups are short,
 // and each then waits for its partial stores and a counter round trip.)
-template <int D, int HP, bool SYM44>
+template <int DP, int HP, bool SYM44>
 __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
-  constexpr int CG = D / 8;                 // 8-channel units per row
-  constexpr int KP = D + 8;                 // K row pitch in LDS (halves)
-  constexpr int VPP = D + 4;                // V token-pair row pitch in LDS (dwords)
+  constexpr int CG = DP / 8;                // 8-channel units per row (capacity)
+  constexpr int KP = DP + 8;                // K row pitch in LDS (halves)
+  constexpr int VPP = DP + 4;               // V token-pair row pitch in LDS (dwords)
   constexpr int NU = HP * CG;               // (head, unit) outputs
   constexpr int TQ = kThreads / NU;         // token slices per output
   constexpr int TPS = kTile / TQ;           // tokens per slice
@@ -272,27 +276,28 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
   const int64_t kvh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = p.G;
+  const int D = p.D;  // the row's channels (<= DP)
 
-  __shared__ __attribute__((aligned(16))) uint32_t q2_s[HP][D / 2];  // fp16 query pairs
-  __shared__ float ks_s[D];
-  __shared__ uint32_t ks2_s[SYM44 ? D / 2 : 1];
+  __shared__ __attribute__((aligned(16))) uint32_t q2_s[HP][DP / 2];  // fp16 query pairs (0 past D)
+  __shared__ float ks_s[DP];
+  __shared__ uint32_t ks2_s[SYM44 ? DP / 2 : 1];
   __shared__ __attribute__((aligned(16))) uint16_t kt[kTile][KP];
   __shared__ __attribute__((aligned(16))) uint32_t vp[kTile / 2][VPP];  // (token 2i, 2i + 1) of one channel
   __shared__ __attribute__((aligned(4))) uint16_t ph_s[HP][kTile];     // fp16 probabilities
   __shared__ float alpha_s[HP];
   __shared__ __attribute__((aligned(16))) float red[TQ > 1 ? TQ : 1][NU][8];
 
-  for (int i = tid; i < HP * D / 2; i += kThreads) {
-    const int h = i / (D / 2), d = 2 * (i % (D / 2));
+  for (int i = tid; i < HP * DP / 2; i += kThreads) {
+    const int h = i / (DP / 2), d = 2 * (i % (DP / 2));
     const uint16_t* qr = p.q + b * p.q_sb + (kvh * G + h) * p.q_sh + d;
-    q2_s[h][d / 2] = h < G ? static_cast<uint32_t>(qr[0]) | (static_cast<uint32_t>(qr[1]) << 16) : 0u;
+    q2_s[h][d / 2] = h < G && d < D ? static_cast<uint32_t>(qr[0]) | (static_cast<uint32_t>(qr[1]) << 16) : 0u;
   }
   if (p.mid.fmt == FADE_MID_SYM || p.mid.fmt == FADE_MID_K4V2G)
-    for (int d = tid; d < D; d += kThreads) ks_s[d] = h2f(p.mid.k_scale[(b * p.Hkv + kvh) * D + d]);
+    for (int d = tid; d < DP; d += kThreads) ks_s[d] = d < D ? h2f(p.mid.k_scale[(b * p.Hkv + kvh) * D + d]) : 0.0f;
   if (SYM44)
-    for (int d = tid; d < D / 2; d += kThreads) {
+    for (int d = tid; d < DP / 2; d += kThreads) {
       const uint16_t* ks = p.mid.k_scale + (b * p.Hkv + kvh) * D + 2 * d;
-      ks2_s[d] = static_cast<uint32_t>(ks[0]) | (static_cast<uint32_t>(ks[1]) << 16);
+      ks2_s[d] = 2 * d < D ? static_cast<uint32_t>(ks[0]) | (static_cast<uint32_t>(ks[1]) << 16) : 0u;
     }
   if (tid < HP) alpha_s[tid] = 1.0f;
 
@@ -335,10 +340,10 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
       const int rp = uidx / CG, cg = uidx % CG;
 #pragma unroll
       for (int e = 0; e < 2; ++e)
-        if (uidx < NPU && 2 * rp + e < nv) {
+        if (uidx < NPU && 2 * rp + e < nv && 8 * cg < D) {
           const UnitRef ur = unit_ref(ts + 2 * rp + e, ns, nm);
-          rk[i][e] = load_unit<D, false, SYM44>(p, b, kvh, ur, cg);
-          rv[i][e] = load_unit<D, true, SYM44>(p, b, kvh, ur, cg);
+          rk[i][e] = load_unit<false, SYM44>(p, b, kvh, ur, cg);
+          rv[i][e] = load_unit<true, SYM44>(p, b, kvh, ur, cg);
         }
     }
   };
@@ -353,10 +358,10 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
         for (int e = 0; e < 2; ++e) {
           const int r = 2 * rp + e;
           uint4 kw = make_uint4(0, 0, 0, 0), v = make_uint4(0, 0, 0, 0);
-          if (r < nv) {
+          if (r < nv && 8 * cg < D) {
             const UnitRef ur = unit_ref(ts + r, ns, nm);
-            kw = convert_unit<D, false, SYM44>(p, b, kvh, ur, cg, rk[i][e], ks_s, ks2_s);
-            v = convert_unit<D, true, SYM44>(p, b, kvh, ur, cg, rv[i][e], ks_s, ks2_s);
+            kw = convert_unit<false, SYM44>(p, b, kvh, ur, cg, rk[i][e], ks_s, ks2_s);
+            v = convert_unit<true, SYM44>(p, b, kvh, ur, cg, rv[i][e], ks_s, ks2_s);
           }
           *reinterpret_cast<uint4*>(&kt[r][8 * cg]) = kw;
           vw[e][0] = v.x;
@@ -463,7 +468,8 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
       }
     }
   }
-  auto emit = [&](int h, int d, float v) {  // the split's P V sum of (head h, channel d)
+  auto emit = [&](int h, int d, float v) {  // the split's P V sum of (head h, channel d < D)
+    if (d >= D) return;
     if (n == 1)
       p.out[b * p.o_sb + (kvh * G + h) * p.o_sh + d] = f2h(v / l_s[h]);
     else
@@ -527,13 +533,13 @@ int launch_valu(const Params& p, hipStream_t st) {
   else if (h8) hipLaunchKernelGGL((decode_valu_kernel<DD, 8, false>), grid, dim3(kThreads), 0, st, p);   \
   else if (s44) hipLaunchKernelGGL((decode_valu_kernel<DD, 4, true>), grid, dim3(kThreads), 0, st, p);   \
   else hipLaunchKernelGGL((decode_valu_kernel<DD, 4, false>), grid, dim3(kThreads), 0, st, p);
-  switch (p.D) {
-    case 32: FADE_VALU_LAUNCH(32) break;
-    case 64: FADE_VALU_LAUNCH(64) break;
-    case 128: FADE_VALU_LAUNCH(128) break;
-    case 256: FADE_VALU_LAUNCH(256) break;
-    default: return einval("fade_tiered_decode_attn: head_dim must be 32, 64, 128 or 256, got %d", p.D);
-  }
+  // the smallest instance whose capacity covers the head_dim
+  if (p.D < 8 || p.D > 256 || p.D % 8 != 0)
+    return einval("fade_tiered_decode_attn: head_dim must be a multiple of 8 in [8, 256], got %d", p.D);
+  if (p.D <= 32) { FADE_VALU_LAUNCH(32) }
+  else if (p.D <= 64) { FADE_VALU_LAUNCH(64) }
+  else if (p.D <= 128) { FADE_VALU_LAUNCH(128) }
+  else { FADE_VALU_LAUNCH(256) }
 #undef FADE_VALU_LAUNCH
   return check_launch("fade_tiered_decode_attn(valu)");
 }

@@ -61,8 +61,8 @@ WsLayout ws_layout(const fade_decode_args* a, int64_t n) {
 
 int validate(const fade_decode_args* a) {
   if (a == nullptr) return einval("fade_tiered_decode_attn: null args");
-  if (a->D != 32 && a->D != 64 && a->D != 128 && a->D != 256)
-    return einval("fade_tiered_decode_attn: head_dim must be 32, 64, 128 or 256, got %lld", (long long)a->D);
+  if (a->D < 8 || a->D > 256 || a->D % 8 != 0)
+    return einval("fade_tiered_decode_attn: head_dim must be a multiple of 8 in [8, 256], got %lld", (long long)a->D);
   if (a->B <= 0 || a->Hq <= 0 || a->Hkv <= 0)
     return einval("fade_tiered_decode_attn: B, Hq, Hkv must be positive");
   if (a->Hq % a->Hkv != 0)

@@ -103,6 +103,7 @@ struct PParams {
   int64_t ppr;
   int mask_mode;          // FADE_MASK_*: bottom-right over the chunk, top-left over the row, none
   int chunk_len;          // chunk keys (Sq under FADE_MASK_BOTTOM_RIGHT)
+  int D;                  // head_dim: a multiple of 8 up to the instance's capacity (packed middle: of 32)
 };
 
 // Eight two's-complement nibbles (one dword of packed codes, high nibble =
@@ -124,21 +125,28 @@ __device__ __forceinline__ u32x4 to_stored(uint32_t d0, uint32_t d1, uint32_t d2
 // Position of key k (0..63) of a tile in a V^T row: bits 2 and 3 exchanged.
 __host__ __device__ constexpr int swap23(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
-// Head dims 32, 64 and 128: QK^T takes D/16 k-steps, PV D/32 column blocks;
-// a fetch thread covers D/4 channels of a token (fp16 tiles), and D/32
-// threads stage a middle token's D/2 code bytes, 16 each.
+// Head dims up to the capacity DP = 32, 64 or 128: QK^T takes DP/16 k-steps,
+// PV DP/32 column blocks; a fetch thread covers DP/4 channels of a token (fp16
+// tiles), and DP/32 threads stage a middle token's code bytes, 16 (32
+// channels) each.  A head_dim D < DP (p.D) leaves the channels past D as
+// zeros in the K rows and the query (so they add nothing to the scores) and
+// never stores them; V channels past D feed only output columns that are not
+// stored.  fp16 rows move in 8-channel units, packed rows in 32-channel ones.
 // NQB query blocks of 32 per workgroup (4 waves each).  With NQB = 2 the two
 // groups of 4 waves split the tile staging: waves 0-3 stage and dequantize K,
 // waves 4-7 V, so each middle tile's dequantization serves 64 queries per head.
-template <int D, int NQB>
+template <int DP, int NQB>
 __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PParams p) {
-  constexpr int KROW = D / 2;     // bytes of one token's packed 4-bit codes
+  constexpr int D = DP;           // channel capacity of the LDS rows and MFMA tiles
+  constexpr int KROW = D / 2;     // staged bytes of one token's packed 4-bit codes
   constexpr int CPT = D / 4;      // channels per fetch thread (fp16 tiles)
   constexpr int KTHR = D / 32;    // threads (16 code bytes each) per middle token
   constexpr int UPR = D / 32;     // 16-byte units per staged V code row
   constexpr int NKS = D / 16;     // QK^T k-steps
   constexpr int NCB = D / 32;     // PV column blocks
   constexpr int KP = kKPitch<D>;
+  const int Dr = p.D;             // the rows' channels (<= D)
+  const int krow = Dr / 2;        // bytes of one token's packed codes in HBM
   const int qb = blockIdx.x / p.passes;
   const int h0 = 4 * (blockIdx.x - qb * p.passes);  // first query head (within the group) of this workgroup
   const int64_t kvh = blockIdx.y;
@@ -238,13 +246,13 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
     put(2, p.recent);
     put(3, p.chunk);
     // fp16 middle tier: [B, Hkv, cap, D] contiguous
-    segd[1][0] = reinterpret_cast<int64_t>(reinterpret_cast<const uint16_t*>(p.kq) + bkv * p.mid_cap * D);
-    segd[1][1] = reinterpret_cast<int64_t>(reinterpret_cast<const uint16_t*>(p.vq) + bkv * p.mid_cap * D);
-    segd[1][2] = D;
-    segd[1][3] = D;
+    segd[1][0] = reinterpret_cast<int64_t>(reinterpret_cast<const uint16_t*>(p.kq) + bkv * p.mid_cap * Dr);
+    segd[1][1] = reinterpret_cast<int64_t>(reinterpret_cast<const uint16_t*>(p.vq) + bkv * p.mid_cap * Dr);
+    segd[1][2] = Dr;
+    segd[1][3] = Dr;
   }
-  const uint8_t* kq = p.kq + bkv * p.mid_cap * KROW;
-  const uint8_t* vq = p.vq + bkv * p.mid_cap * KROW;
+  const uint8_t* kq = p.kq + bkv * p.mid_cap * krow;
+  const uint8_t* vq = p.vq + bkv * p.mid_cap * krow;
   const uint16_t* vsr = p.vs + bkv * p.mid_cap;
 
   // K scales of this thread's 32 staged channels as fp16 pairs, in the stored order
@@ -252,7 +260,7 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint4 w = make_uint4(0, 0, 0, 0);
-    if (p.has_mid && !p.mid_fp16 && kstage) w = *reinterpret_cast<const uint4*>(p.ks + bkv * D + 32 * mc + 8 * i);
+    if (p.has_mid && !p.mid_fp16 && kstage && 32 * mc < Dr) w = *reinterpret_cast<const uint4*>(p.ks + bkv * Dr + 32 * mc + 8 * i);
     const u32x4 st = to_stored(w.x, w.y, w.z, w.w);
 #pragma unroll
     for (int e = 0; e < 4; ++e) ksc[4 * i + e] = st[e];
@@ -279,23 +287,22 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
     int row0 = tr.base;
     if (p.pages != nullptr) {
       const int64_t blk = static_cast<int64_t>(p.pages[b * p.ppr + (tr.base >> 6)]) * p.Hkv + kvh;
-      kq_t = p.kq + blk * kKT * KROW;
-      vq_t = p.vq + blk * kKT * KROW;
+      kq_t = p.kq + blk * kKT * krow;
+      vq_t = p.vq + blk * kKT * krow;
       vs_t = p.vs + blk * kKT;
       row0 = 0;
     }
     const int key = row0 + (ok ? mr : tr.cnt - 1);  // rows past the tile: a valid row, zeroed in store_mid()
-    if (kstage) lds_dma16(kq_t + static_cast<int64_t>(key) * KROW + 16 * mc, stk);
+    if (kstage && 32 * mc < Dr) lds_dma16(kq_t + static_cast<int64_t>(key) * krow + 16 * mc, stk);
     // V: lane l < 16 UPR of wave w fills unit l of the wave's block: row
     // rho = l / UPR, source unit (l % UPR) ^ ((rho >> 1) & (UPR - 1)).  Rows
     // past the tile read the last valid key (finite; their probabilities are zero).
     if (do_v) {
       const int vr = lane / UPR;
       const int vk = 16 * wq + vr, sk2 = 16 * wq + (lane & 15);
-      if (UPR == 4 || lane < 16 * UPR)
-        lds_dma16(vq_t + static_cast<int64_t>(row0 + (vk < tr.cnt ? vk : tr.cnt - 1)) * KROW +
-                      16 * ((lane % UPR) ^ ((vr >> 1) & (UPR - 1))),
-                  stv);
+      const int vu = (lane % UPR) ^ ((vr >> 1) & (UPR - 1));  // the unit's 32 channels in the row
+      if ((UPR == 4 || lane < 16 * UPR) && 32 * vu < Dr)
+        lds_dma16(vq_t + static_cast<int64_t>(row0 + (vk < tr.cnt ? vk : tr.cnt - 1)) * krow + 16 * vu, stv);
       lds_dma2(vs_t + row0 + (sk2 < tr.cnt ? sk2 : tr.cnt - 1), sts);
     }
   };
@@ -306,7 +313,7 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
     const f16x2 m72 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
     if (do_k) {
     uint4 kraw = make_uint4(0, 0, 0, 0);
-    if (kstage && fok) kraw = *reinterpret_cast<const uint4*>(&stg_k[16 * gtid]);
+    if (kstage && fok && 32 * mc < Dr) kraw = *reinterpret_cast<const uint4*>(&stg_k[16 * gtid]);
     // codes -> fp16 72 + c -> c -> fp16(c * scale), already in the stored channel order
     const uint32_t kw[4] = {kraw.x, kraw.y, kraw.z, kraw.w};
 #pragma unroll
@@ -378,8 +385,10 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
       const uint4* v4 = reinterpret_cast<const uint4*>(vp + CPT * cp);
 #pragma unroll
       for (int i = 0; i < NU; ++i) {
-        if (do_k) fk[i] = k4[i];
-        if (do_v) fv[i] = v4[i];
+        const bool in = CPT * cp + 8 * i < Dr;  // units past the head_dim stay zero
+        fk[i] = fv[i] = make_uint4(0, 0, 0, 0);
+        if (do_k && in) fk[i] = k4[i];
+        if (do_v && in) fv[i] = v4[i];
       }
     } else {
 #pragma unroll
@@ -421,7 +430,8 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
     const uint16_t* qr = p.q + b * p.q_sb + hq * p.q_sh + static_cast<int64_t>(j < Sq ? j : Sq - 1) * p.q_ss;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      const uint4 w = (active && j < Sq) ? *reinterpret_cast<const uint4*>(qr + 16 * ks + 8 * h) : make_uint4(0, 0, 0, 0);
+      const uint4 w = (active && j < Sq && 16 * ks + 8 * h < Dr) ? *reinterpret_cast<const uint4*>(qr + 16 * ks + 8 * h)
+                                                                : make_uint4(0, 0, 0, 0);
       qf[ks] = __builtin_bit_cast(f16x8, to_stored(w.x, w.y, w.z, w.w));
     }
   }
@@ -566,7 +576,8 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
         if (j < Sq) {
           uint16_t* orow = p.out + b * p.o_sb + hq * p.o_sh + static_cast<int64_t>(j) * p.o_ss;
 #pragma unroll
-          for (int cb = 0; cb < NCB; ++cb) orow[32 * cb + n32] = f2h(acc[cb][4 * q + i] * inv4[i]);
+          for (int cb = 0; cb < NCB; ++cb)
+            if (32 * cb + n32 < Dr) orow[32 * cb + n32] = f2h(acc[cb][4 * q + i] * inv4[i]);
         }
       }
     }
@@ -598,8 +609,8 @@ using namespace fade::prefill;
 
 FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) {
   if (a == nullptr) return einval("fade_tiered_prefill_attn: null args");
-  if (a->D != 32 && a->D != 64 && a->D != 128)
-    return einval("fade_tiered_prefill_attn: head_dim must be 32, 64 or 128, got %lld", (long long)a->D);
+  if (a->D < 8 || a->D > 128 || a->D % 8 != 0)
+    return einval("fade_tiered_prefill_attn: head_dim must be a multiple of 8 in [8, 128], got %lld", (long long)a->D);
   if (a->B <= 0 || a->Hq <= 0 || a->Hkv <= 0 || a->Sq <= 0)
     return einval("fade_tiered_prefill_attn: B, Hq, Hkv and Sq must be positive");
   if (a->Hq % a->Hkv != 0 || a->Hq / a->Hkv > 8)
@@ -627,6 +638,9 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   } else if (has_mid) {
     if (m.fmt != FADE_MID_SYM || m.k_bits != 4 || m.v_bits != 4)
       return einval("fade_tiered_prefill_attn: the middle tier must be FADE_MID_SYM 4-bit or FADE_MID_FP16");
+    if (a->D % 32 != 0)
+      return einval("fade_tiered_prefill_attn: a packed middle tier needs head_dim %% 32 == 0 (got %lld); "
+                    "pass it as an fp16 middle tier", (long long)a->D);
     if (!m.k_codes || !m.v_codes || !m.k_scale || !m.v_scale || !aligned16(m.k_codes) || !aligned16(m.v_codes) ||
         (reinterpret_cast<uintptr_t>(m.k_scale) & 15))
       return einval("fade_tiered_prefill_attn: middle tier pointers missing or misaligned");
@@ -663,6 +677,7 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   p.ppr = has_mid ? m.pages_per_row : 0;
   p.mask_mode = a->mask_mode;
   p.chunk_len = static_cast<int>(a->chunk.len);
+  p.D = static_cast<int>(a->D);
   // two query blocks per workgroup once there are more than 32 queries
   const int nqb = a->Sq > kQB ? 2 : 1;
   const dim3 grid(static_cast<unsigned>(cdiv(a->Sq, kQB * nqb) * p.passes), static_cast<unsigned>(a->Hkv),
@@ -670,11 +685,10 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
 #define FADE_PREFILL_LAUNCH(DD)                                                                               \
   if (nqb == 2) hipLaunchKernelGGL((prefill_kernel<DD, 2>), grid, dim3(2 * kThreads), 0, as_stream(stream), p); \
   else hipLaunchKernelGGL((prefill_kernel<DD, 1>), grid, dim3(kThreads), 0, as_stream(stream), p);
-  switch (a->D) {
-    case 32: FADE_PREFILL_LAUNCH(32) break;
-    case 64: FADE_PREFILL_LAUNCH(64) break;
-    default: FADE_PREFILL_LAUNCH(128) break;
-  }
+  // the smallest instance whose capacity covers the head_dim
+  if (a->D <= 32) { FADE_PREFILL_LAUNCH(32) }
+  else if (a->D <= 64) { FADE_PREFILL_LAUNCH(64) }
+  else { FADE_PREFILL_LAUNCH(128) }
 #undef FADE_PREFILL_LAUNCH
   return check_launch("fade_tiered_prefill_attn");
 }

@@ -179,18 +179,19 @@ __device__ __forceinline__ void load_codes(const uint8_t* src, int* c) {
 
 // ---------------------------------------------------------------- per token
 template <typename InT, int MODE, int BITS, int LPR>
-__global__ __launch_bounds__(kBlock) void quant_token_kernel(const InT* __restrict__ x, int64_t rows,
+__global__ __launch_bounds__(kBlock) void quant_token_kernel(const InT* __restrict__ x, int D, int64_t rows,
                                                              int64_t H, int64_t S, int64_t sb,
                                                              int64_t sh, int64_t ss, int64_t fs,
                                                              uint8_t* __restrict__ packed,
                                                              typename ScaleOf<MODE>::T* __restrict__ scale) {
   constexpr int RP = kBlock / LPR;
-  constexpr int ROW_BYTES = LPR * lane_bytes<BITS>();
+  const int row_bytes = (D / 8) * lane_bytes<BITS>();
   const int c = threadIdx.x % LPR;
+  const bool on = c * 8 < D;  // lanes past the row's D / 8 groups of 8 channels idle
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; r < rows;
        r += static_cast<int64_t>(gridDim.x) * RP) {
-    float v[8];
-    load8(x + (fs ? r * fs : row_offset(r, H, S, sb, sh, ss)) + c * 8, v);
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (on) load8(x + (fs ? r * fs : row_offset(r, H, S, sb, sh, ss)) + c * 8, v);
     float a = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) a = absmax_nan(a, v[j]);
@@ -201,7 +202,7 @@ __global__ __launch_bounds__(kBlock) void quant_token_kernel(const InT* __restri
     int code[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) code[j] = sym_code<MODE, QRange<BITS>::lo, QRange<BITS>::hi>(v[j], inv);
-    store_codes<BITS>(packed + r * ROW_BYTES + c * lane_bytes<BITS>(), code);
+    if (on) store_codes<BITS>(packed + r * row_bytes + c * lane_bytes<BITS>(), code);
     if (c == 0) scale[r] = sc;
   }
 }
@@ -209,31 +210,31 @@ __global__ __launch_bounds__(kBlock) void quant_token_kernel(const InT* __restri
 // -------------------------------------------------------------- per channel
 // Pass 1: column absmax of each S-block -> partial[bh][block][d] (fp32).
 template <typename InT, int LPR>
-__global__ __launch_bounds__(kBlock) void colmax_kernel(const InT* __restrict__ x, int64_t H,
+__global__ __launch_bounds__(kBlock) void colmax_kernel(const InT* __restrict__ x, int D, int64_t H,
                                                         int64_t S, int64_t sb, int64_t sh,
                                                         int64_t ss, int64_t rows_per_block,
                                                         float* __restrict__ partial) {
   constexpr int RP = kBlock / LPR;
-  constexpr int D = LPR * 8;
+  constexpr int DP = LPR * 8;  // the instance's channel capacity (>= D)
   const int64_t bh = blockIdx.y;
   const int c = threadIdx.x % LPR, rs = threadIdx.x / LPR;
   const int64_t s0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
   const int64_t s1 = s0 + rows_per_block < S ? s0 + rows_per_block : S;
   const InT* base = x + (bh / H) * sb + (bh % H) * sh + c * 8;
   float m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int64_t s = s0 + rs; s < s1; s += RP) {
+  for (int64_t s = s0 + rs; c * 8 < D && s < s1; s += RP) {
     float v[8];
     load8(base + s * ss, v);
 #pragma unroll
     for (int j = 0; j < 8; ++j) m[j] = absmax_nan(m[j], v[j]);
   }
-  __shared__ float red[RP * D];
+  __shared__ float red[RP * DP];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) red[rs * D + c * 8 + j] = m[j];
+  for (int j = 0; j < 8; ++j) red[rs * DP + c * 8 + j] = m[j];
   __syncthreads();
   for (int d = threadIdx.x; d < D; d += kBlock) {
     float mm = 0.0f;
-    for (int r = 0; r < RP; ++r) mm = absmax_nan(mm, red[r * D + d]);
+    for (int r = 0; r < RP; ++r) mm = absmax_nan(mm, red[r * DP + d]);
     partial[(bh * gridDim.x + blockIdx.x) * D + d] = mm;
   }
 }
@@ -243,14 +244,14 @@ __global__ __launch_bounds__(kBlock) void colmax_kernel(const InT* __restrict__ 
 // gathered), emit the scale, quantize this S-block.
 template <typename InT, int MODE, int BITS, int LPR>
 __global__ __launch_bounds__(kBlock) void quant_channel_kernel(
-    const InT* __restrict__ x, int64_t H, int64_t S, int64_t sb, int64_t sh, int64_t ss,
+    const InT* __restrict__ x, int D, int64_t H, int64_t S, int64_t sb, int64_t sh, int64_t ss,
     int64_t rows_per_block, const float* __restrict__ partial, int nparts, uint8_t* __restrict__ packed,
     typename ScaleOf<MODE>::T* __restrict__ scale) {
   constexpr int RP = kBlock / LPR;
-  constexpr int D = LPR * 8;
-  constexpr int ROW_BYTES = LPR * lane_bytes<BITS>();
+  constexpr int DP = LPR * 8;  // the instance's channel capacity (>= D)
+  const int row_bytes = (D / 8) * lane_bytes<BITS>();
   const int64_t bh = blockIdx.y;
-  __shared__ float inv_s[D];
+  __shared__ float inv_s[DP];
   for (int d = threadIdx.x; d < D; d += kBlock) {
     float a = 0.0f;
     for (int k = 0; k < nparts; ++k) a = absmax_nan(a, partial[(bh * nparts + k) * D + d]);
@@ -262,6 +263,7 @@ __global__ __launch_bounds__(kBlock) void quant_channel_kernel(
   }
   __syncthreads();
   const int c = threadIdx.x % LPR, rs = threadIdx.x / LPR;
+  if (c * 8 >= D) return;  // past the row's channels (no barrier follows)
   float iv[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) iv[j] = inv_s[c * 8 + j];
@@ -274,7 +276,7 @@ __global__ __launch_bounds__(kBlock) void quant_channel_kernel(
     int code[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) code[j] = sym_code<MODE, QRange<BITS>::lo, QRange<BITS>::hi>(v[j], iv[j]);
-    store_codes<BITS>(packed + (bh * S + s) * ROW_BYTES + c * lane_bytes<BITS>(), code);
+    store_codes<BITS>(packed + (bh * S + s) * row_bytes + c * lane_bytes<BITS>(), code);
   }
 }
 
@@ -303,16 +305,16 @@ __device__ __forceinline__ void store8(float* p, const float* y) {
 
 template <int BITS, int LPR, typename T>
 __global__ __launch_bounds__(kBlock) void dequant_sym_kernel(const uint8_t* __restrict__ packed,
-                                                             const T* __restrict__ scale, int axis,
+                                                             const T* __restrict__ scale, int D, int axis,
                                                              int64_t rows, int64_t S, T* __restrict__ out) {
   constexpr int RP = kBlock / LPR;
-  constexpr int D = LPR * 8;
-  constexpr int ROW_BYTES = LPR * lane_bytes<BITS>();
+  const int row_bytes = (D / 8) * lane_bytes<BITS>();
   const int c = threadIdx.x % LPR;
+  if (c * 8 >= D) return;  // past the row's channels
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; r < rows;
        r += static_cast<int64_t>(gridDim.x) * RP) {
     int code[8];
-    load_codes<BITS>(packed + r * ROW_BYTES + c * lane_bytes<BITS>(), code);
+    load_codes<BITS>(packed + r * row_bytes + c * lane_bytes<BITS>(), code);
     float y[8];
     if (axis == FADE_AXIS_TOKEN) {
       const float sc = scale_ld(scale[r]);
@@ -384,22 +386,22 @@ __global__ void dequant_int2_grouped_kernel(const int8_t* __restrict__ codes,
 
 // ------------------------------------------------------ asymmetric groups
 template <int BITS, int LPG, int LPR>
-__global__ __launch_bounds__(kBlock) void quant_asym_kernel(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(kBlock) void quant_asym_kernel(const uint16_t* __restrict__ x, int D,
                                                             int64_t rows, int64_t H, int64_t S,
                                                             int64_t sb, int64_t sh, int64_t ss, int64_t fs,
                                                             uint8_t* __restrict__ packed,
                                                             uint16_t* __restrict__ scale,
                                                             uint16_t* __restrict__ zero) {
   constexpr int RP = kBlock / LPR;
-  constexpr int D = LPR * 8;
-  constexpr int NG = LPR / LPG;  // groups per row
-  constexpr int ROW_BYTES = D * BITS / 8;
+  const int NG = D / (8 * LPG);  // groups per row (D is a multiple of the group)
+  const int row_bytes = D * BITS / 8;
   constexpr float QMAXU = static_cast<float>((1 << BITS) - 1);
   const int c = threadIdx.x % LPR;
+  const bool on = c * 8 < D;  // whole groups of lanes idle past the row's channels
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; r < rows;
        r += static_cast<int64_t>(gridDim.x) * RP) {
-    float v[8];
-    load8(x + (fs ? r * fs : row_offset(r, H, S, sb, sh, ss)) + c * 8, v);
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (on) load8(x + (fs ? r * fs : row_offset(r, H, S, sb, sh, ss)) + c * 8, v);
     float mn = v[0], mx = v[0];
 #pragma unroll
     for (int j = 1; j < 8; ++j) {
@@ -418,7 +420,8 @@ __global__ __launch_bounds__(kBlock) void quant_asym_kernel(const uint16_t* __re
       const float t = rintf((v[j] - mn) * inv);
       code[j] = static_cast<int>(fminf(fmaxf(t, 0.0f), QMAXU));
     }
-    uint8_t* dst = packed + r * ROW_BYTES + c * BITS;
+    if (!on) continue;
+    uint8_t* dst = packed + r * row_bytes + c * BITS;
     if (BITS == 4) {
       uint32_t w = 0;
 #pragma unroll
@@ -444,19 +447,19 @@ __global__ __launch_bounds__(kBlock) void quant_asym_kernel(const uint16_t* __re
 template <int BITS, int LPG, int LPR>
 __global__ __launch_bounds__(kBlock) void dequant_asym_kernel(const uint8_t* __restrict__ packed,
                                                               const uint16_t* __restrict__ scale,
-                                                              const uint16_t* __restrict__ zero,
+                                                              const uint16_t* __restrict__ zero, int D,
                                                               int64_t rows,
                                                               uint16_t* __restrict__ out) {
   constexpr int RP = kBlock / LPR;
-  constexpr int D = LPR * 8;
-  constexpr int NG = LPR / LPG;
-  constexpr int ROW_BYTES = D * BITS / 8;
+  const int NG = D / (8 * LPG);
+  const int row_bytes = D * BITS / 8;
   const int c = threadIdx.x % LPR;
+  if (c * 8 >= D) return;  // past the row's channels
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; r < rows;
        r += static_cast<int64_t>(gridDim.x) * RP) {
     const float s = h2f(scale[r * NG + c / LPG]);
     const float z = h2f(zero[r * NG + c / LPG]);
-    const uint8_t* src = packed + r * ROW_BYTES + c * BITS;
+    const uint8_t* src = packed + r * row_bytes + c * BITS;
     int code[8];
     if (BITS == 4) {
       const uint32_t w = *reinterpret_cast<const uint32_t*>(src);
@@ -518,8 +521,8 @@ __global__ void unpack_kernel(const uint8_t* __restrict__ packed, int64_t n8, in
 // ---------------------------------------------------------------- host side
 int check_dims(const char* fn, int64_t B, int64_t H, int64_t S, int64_t D) {
   if (B < 0 || H < 0 || S < 0) return einval("%s: negative size (B=%lld H=%lld S=%lld)", fn, (long long)B, (long long)H, (long long)S);
-  if (D != 32 && D != 64 && D != 128 && D != 256)
-    return einval("%s: head_dim must be 32, 64, 128 or 256, got %lld", fn, (long long)D);
+  if (D < 8 || D > 256 || D % 8 != 0)
+    return einval("%s: head_dim must be a multiple of 8 in [8, 256], got %lld", fn, (long long)D);
   return FADE_OK;
 }
 
@@ -550,13 +553,13 @@ void channel_blocking(int64_t BH, int64_t S, int64_t* nsb, int64_t* rows_per_blo
   *nsb = cdiv(S, rpb) > 0 ? cdiv(S, rpb) : 1;
 }
 
-#define FADE_DISPATCH_LPR(D, ...)           \
-  switch (D) {                              \
-    case 32: { constexpr int LPR = 4; __VA_ARGS__; } break;   \
-    case 64: { constexpr int LPR = 8; __VA_ARGS__; } break;   \
-    case 128: { constexpr int LPR = 16; __VA_ARGS__; } break; \
-    default: { constexpr int LPR = 32; __VA_ARGS__; } break;  \
-  }
+// Lanes per row: the power of two that covers D / 8 lanes (8 channels each);
+// the lanes past D / 8 idle.
+#define FADE_DISPATCH_LPR(D, ...)                                        \
+  if ((D) <= 32) { constexpr int LPR = 4; __VA_ARGS__; }                 \
+  else if ((D) <= 64) { constexpr int LPR = 8; __VA_ARGS__; }            \
+  else if ((D) <= 128) { constexpr int LPR = 16; __VA_ARGS__; }          \
+  else { constexpr int LPR = 32; __VA_ARGS__; }
 
 template <typename InT, int MODE, int BITS>
 int launch_channel(const char* fn, const InT* x, int64_t B, int64_t H, int64_t S, int64_t D,
@@ -573,10 +576,10 @@ int launch_channel(const char* fn, const InT* x, int64_t B, int64_t H, int64_t S
   if (BH > 65535) return einval("%s: B*H=%lld exceeds 65535", fn, (long long)BH);
   dim3 grid(static_cast<unsigned>(nsb), static_cast<unsigned>(BH));
   FADE_DISPATCH_LPR(D, {
-    hipLaunchKernelGGL((colmax_kernel<InT, LPR>), grid, dim3(kBlock), 0, st, x, H, S, sb, sh, ss,
+    hipLaunchKernelGGL((colmax_kernel<InT, LPR>), grid, dim3(kBlock), 0, st, x, static_cast<int>(D), H, S, sb, sh, ss,
                        rpb, static_cast<float*>(ws));
     hipLaunchKernelGGL((quant_channel_kernel<InT, MODE, BITS, LPR>), grid, dim3(kBlock), 0, st, x,
-                       H, S, sb, sh, ss, rpb, static_cast<const float*>(ws), static_cast<int>(nsb),
+                       static_cast<int>(D), H, S, sb, sh, ss, rpb, static_cast<const float*>(ws), static_cast<int>(nsb),
                        static_cast<uint8_t*>(packed), static_cast<typename ScaleOf<MODE>::T*>(scale));
   });
   return check_launch(fn);
@@ -597,7 +600,7 @@ int launch_channel_given(const char* fn, const InT* x, int64_t B, int64_t H, int
   dim3 grid(static_cast<unsigned>(nsb), static_cast<unsigned>(BH));
   FADE_DISPATCH_LPR(D, {
     hipLaunchKernelGGL((quant_channel_kernel<InT, MODE, BITS, LPR>), grid, dim3(kBlock), 0, st, x,
-                       H, S, sb, sh, ss, rpb, partial, static_cast<int>(nparts),
+                       static_cast<int>(D), H, S, sb, sh, ss, rpb, partial, static_cast<int>(nparts),
                        static_cast<uint8_t*>(packed), static_cast<typename ScaleOf<MODE>::T*>(scale));
   });
   return check_launch(fn);
@@ -610,7 +613,7 @@ int launch_token(const char* fn, const InT* x, int64_t B, int64_t H, int64_t S, 
   if (rows == 0) return FADE_OK;
   FADE_DISPATCH_LPR(D, {
     hipLaunchKernelGGL((quant_token_kernel<InT, MODE, BITS, LPR>), dim3(grid_for_rows(rows, LPR)),
-                       dim3(kBlock), 0, st, x, rows, H, S, sb, sh, ss, flat_row_stride(H, S, sb, sh, ss),
+                       dim3(kBlock), 0, st, x, static_cast<int>(D), rows, H, S, sb, sh, ss, flat_row_stride(H, S, sb, sh, ss),
                        static_cast<uint8_t*>(packed), static_cast<typename ScaleOf<MODE>::T*>(scale));
   });
   return check_launch(fn);
@@ -761,13 +764,16 @@ int dequant_sym(const char* fn, const void* packed_u8, const void* scale, int32_
   FADE_DISPATCH_LPR(D, {
     const dim3 grid(grid_for_rows(rows, LPR));
     if (bits == 4)
-      hipLaunchKernelGGL((dequant_sym_kernel<4, LPR, T>), grid, dim3(kBlock), 0, as_stream(stream), pk, sc, axis,
+      hipLaunchKernelGGL((dequant_sym_kernel<4, LPR, T>), grid, dim3(kBlock), 0, as_stream(stream), pk, sc,
+                         static_cast<int>(D), axis,
                          rows, S, o);
     else if (bits == 3)
-      hipLaunchKernelGGL((dequant_sym_kernel<3, LPR, T>), grid, dim3(kBlock), 0, as_stream(stream), pk, sc, axis,
+      hipLaunchKernelGGL((dequant_sym_kernel<3, LPR, T>), grid, dim3(kBlock), 0, as_stream(stream), pk, sc,
+                         static_cast<int>(D), axis,
                          rows, S, o);
     else
-      hipLaunchKernelGGL((dequant_sym_kernel<2, LPR, T>), grid, dim3(kBlock), 0, as_stream(stream), pk, sc, axis,
+      hipLaunchKernelGGL((dequant_sym_kernel<2, LPR, T>), grid, dim3(kBlock), 0, as_stream(stream), pk, sc,
+                         static_cast<int>(D), axis,
                          rows, S, o);
   });
   return check_launch(fn);
@@ -969,7 +975,8 @@ FADE_API int fade_quant_asym(const void* x_f16, int64_t B, int64_t H, int64_t S,
                      hipLaunchKernelGGL((quant_asym_kernel<BITS, LPG, LPR>),
                                          dim3(grid_for_rows(rows, LPR)), dim3(kBlock), 0,
                                          as_stream(stream), static_cast<const uint16_t*>(x_f16),
-                                         rows, H, S, sb, sh, ss, flat_row_stride(H, S, sb, sh, ss),
+                                         static_cast<int>(D), rows, H, S, sb, sh, ss,
+                                         flat_row_stride(H, S, sb, sh, ss),
                                          static_cast<uint8_t*>(packed_u8),
                                          static_cast<uint16_t*>(scale_f16),
                                          static_cast<uint16_t*>(zero_f16)));
@@ -988,7 +995,7 @@ FADE_API int fade_dequant_asym(const void* packed_u8, const void* scale_f16, con
                                          dim3(grid_for_rows(rows, LPR)), dim3(kBlock), 0,
                                          as_stream(stream), static_cast<const uint8_t*>(packed_u8),
                                          static_cast<const uint16_t*>(scale_f16),
-                                         static_cast<const uint16_t*>(zero_f16), rows,
+                                         static_cast<const uint16_t*>(zero_f16), static_cast<int>(D), rows,
                                          static_cast<uint16_t*>(out_f16)));
   return check_launch("fade_dequant_asym");
 }

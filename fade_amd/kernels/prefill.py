@@ -26,10 +26,10 @@ class TieredPrefillPlan:
     """Validated launch for fixed tensors; ``run()`` enqueues one kernel.
 
     Args:
-        q: [B, Hq, Sq, 128] fp16 queries of the chunk.
-        chunk: (K, V) [B, Hkv, Sq, 128] fp16, the chunk's own keys/values
+        q: [B, Hq, Sq, D] fp16 queries of the chunk; D a multiple of 8 up to 128.
+        chunk: (K, V) [B, Hkv, Sq, D] fp16, the chunk's own keys/values
             (with ``mask`` ``"top_left"`` / ``"none"``: any length, or None).
-        sink, recent: (K, V) [B, Hkv, cap, 128] fp16 padded along S, or None.
+        sink, recent: (K, V) [B, Hkv, cap, D] fp16 padded along S, or None.
         mid: reference INT4 middle tier (``MiddleTier("int4", ...)``) with
             codes padded to a common row count, an fp16 one (``MiddleTier("fp16",
             k, v)``, rows [B, Hkv, S, D]), or None.
@@ -76,6 +76,16 @@ class TieredPrefillPlan:
                 raise ValueError(f"chunk K/V must be [B, Hkv, {'Sq=' if mask == 'bottom_right' else ''}{n_c}, D]")
         if mid is not None and mid.fmt not in ("int4", "sym", "fp16"):
             raise ValueError("the prefill kernel reads the reference INT4 middle tier or an fp16 one")
+        if mid is not None and mid.fmt in ("int4", "sym") and D % 32:
+            # the kernel stages packed rows in 32-channel units: at other head dims it
+            # reads the middle tier as its fp16 dequantization (the reference's
+            # rounding, fade/quant.py:124-127)
+            if mid.pages is not None:
+                raise ValueError("a paged INT4 middle tier needs head_dim % 32 == 0 in the prefill kernel")
+            from ..quant import dequant_int4
+
+            mid = MiddleTier("fp16", dequant_int4(mid.k_codes, mid.k_scale), dequant_int4(mid.v_codes, mid.v_scale),
+                             length=mid.length)
         if mid is not None and mid.fmt == "fp16" and (mid.k_codes.dtype != torch.float16 or mid.k_codes.shape[-1] != D):
             raise ValueError("an fp16 middle tier holds float16 rows [B, Hkv, S, D]")
         if q.stride(-1) != 1:
@@ -113,7 +123,7 @@ class TieredPrefillPlan:
 
 def tiered_prefill_attention(q, chunk, sink=None, mid=None, recent=None, lens=None, order=None, sm_scale=None,
                              mask: str = "bottom_right") -> Tensor:
-    """Causal attention of a chunk over each row's tiered cache; returns fp16 [B, Hq, Sq, 128]."""
+    """Causal attention of a chunk over each row's tiered cache; returns fp16 [B, Hq, Sq, D]."""
     return TieredPrefillPlan(q, chunk, sink, mid, recent, lens, order, sm_scale, mask=mask).run()
 
 

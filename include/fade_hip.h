@@ -303,9 +303,9 @@ typedef struct fade_mid_tier {
 } fade_mid_tier;
 
 typedef struct fade_decode_args {
-  int64_t B, Hq, Hkv, D;       /* D 32, 64, 128 or 256 (the matrix-core kernels take 128; other
-                                  head dims run the portable kernel, which reads every middle
-                                  format and per-row lens, not pages or a rotation);
+  int64_t B, Hq, Hkv, D;       /* D a multiple of 8 in [8, 256] (the matrix-core kernels take
+                                  128; other head dims run the portable kernel, which reads
+                                  every middle format and per-row lens, not pages or a rotation);
                                   Hq % Hkv == 0; Hq/Hkv <= 8 */
   const void* q;               /* [B,Hq,1,D] fp16 */
   int64_t q_sb, q_sh;
@@ -384,8 +384,8 @@ int fade_tiered_decode_attn_noalloc(const fade_decode_args* args, void* stream);
  * every row must then see at least one key.  Tier tensors are
  * padded along S (row b uses the first lens[3b+0..2] tokens of sink / middle /
  * recent); the middle tier is FADE_MID_SYM 4-bit (padded, or paged: mid.pages,
- * separate pools, pages_per_row * 64 >= mid.len) or FADE_MID_NONE.  D = 32, 64
- * or 128, Hq/Hkv <= 8.  `order` (optional, device int32 [B]) lists batch rows in the
+ * separate pools, pages_per_row * 64 >= mid.len; D % 32 == 0), FADE_MID_FP16
+ * or FADE_MID_NONE.  D a multiple of 8 in [8, 128], Hq/Hkv <= 8.  `order` (optional, device int32 [B]) lists batch rows in the
  * order their workgroups are dispatched (longest first balances the tail).
  * Replaces the reference's prefill path: update() returning the materialized
  * tiers (fade/cache.py:347-379,683-842) followed by causal SDPA in the model. */

@@ -157,10 +157,10 @@ def test_argument_errors_come_back_as_value_errors():
     """Validation runs before any GPU work, so it is testable without a device."""
     lib = _lib.load()
     a = _lib.DecodeArgs()
-    a.B, a.Hq, a.Hkv, a.D = 1, 32, 8, 96
+    a.B, a.Hq, a.Hkv, a.D = 1, 32, 8, 100
     rc = lib.fade_tiered_decode_attn(ctypes.byref(a), None)
     assert rc == _lib.FADE_EINVAL
-    assert b"head_dim must be 32, 64, 128 or 256" in lib.fade_hip_last_error()
+    assert b"head_dim must be a multiple of 8 in [8, 256]" in lib.fade_hip_last_error()
     with pytest.raises(ValueError, match="head_dim"):
         _lib.check(rc, "fade_tiered_decode_attn")
     a.D, a.Hq = 128, 30

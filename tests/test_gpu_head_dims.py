@@ -2,10 +2,12 @@
 
 The reference's quantizers and kernels take any even head_dim
 (fade/quant.py:36-37; its fused-kernel tests run D = 64,
-tests/test_fused_blackwell.py:50-109, and its INT4 SDPA tests D = 32,
-tests/test_perf.py:17).  Here decode at D = 32, 64 and 256 runs the portable
-kernel (every middle format); the MFMA prefill kernel takes D = 32, 64 and
-128.  Tolerance: max-abs 2e-3 against fp32 attention over the oracle's
+tests/test_fused_blackwell.py:50-109, its INT4 SDPA tests D = 32,
+tests/test_perf.py:17, its model tests D = 16, tests/test_models.py:43-49).
+Here every multiple of 8 up to 256 is taken: decode at D != 128 runs the
+portable kernel (every middle format; instances of capacity 32/64/128/256,
+channels past D idle), the MFMA prefill kernel takes D up to 128 (a packed
+middle tier in place at multiples of 32, its fp16 dequantization otherwise).  Tolerance: max-abs 2e-3 against fp32 attention over the oracle's
 dequantized tiers, as for D = 128.
 """
 
@@ -53,10 +55,12 @@ def _mid(dev, fmt, km, vm):
              "k_bits": 4, "v_bits": 2, "group": 32})
 
 
-@pytest.mark.parametrize("D", [32, 64, 256])
+@pytest.mark.parametrize("D", [32, 64, 256, 16, 80, 96, 160])
 @pytest.mark.parametrize("fmt", ["int4", "fp16", "k4v2", "asym"])
 @pytest.mark.parametrize("B,Hq,Hkv,S,ns,nr", [(2, 8, 2, 700, 4, 64), (1, 16, 2, 130, 0, 7), (3, 4, 4, 70, 2, 0)])
 def test_decode_head_dims(dev, D, fmt, B, Hq, Hkv, S, ns, nr):
+    if fmt == "asym" and D % 32:
+        pytest.skip("the asymmetric format's 32-channel groups need D % 32 == 0")
     print(f"case decode D={D} {fmt} B={B} Hq={Hq} Hkv={Hkv} S={S} ns={ns} nr={nr}", flush=True)
     q, k, v = (x.numpy() for x in kv_tensors(B, Hkv, S, D, seed=300 + D + S, Hq=Hq))
     mid, omid = _mid(dev, fmt, k[:, :, ns : S - nr], v[:, :, ns : S - nr])
@@ -124,7 +128,7 @@ def _ragged(dev, D, B, Hq, Hkv, Sq, rows, seed, fmt="int4"):
     return _t(dev, qs), (_t(dev, chunk_k), _t(dev, chunk_v)), sink, mid, rec, lens, ref
 
 
-@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("D", [32, 64, 16, 48, 80, 96])
 @pytest.mark.parametrize("fmt", ["int4", "fp16"])
 @pytest.mark.parametrize(
     "B,Hq,Hkv,Sq,rows",

@@ -11,6 +11,9 @@ from fade_amd.synthetic import kv_tensors
 from oracle import quant as oq
 
 pytestmark = pytest.mark.gpu
+# head dims 128 / 64 / 256 and others that are multiples of 8 (the reference takes any even D)
+SHAPES = [(1, 8, 1980, 128), (2, 3, 67, 128), (1, 2, 5, 64), (1, 1, 300, 256), (2, 3, 67, 96),
+          (1, 2, 40, 80), (1, 3, 33, 16), (1, 1, 50, 160), (1, 2, 21, 48)]
 F16 = np.float16
 
 
@@ -30,7 +33,7 @@ def _edge_tensor(shape, seed):
     return x
 
 
-@pytest.mark.parametrize("shape", [(1, 8, 1980, 128), (2, 3, 67, 128), (1, 2, 5, 64), (1, 1, 300, 256)])
+@pytest.mark.parametrize("shape", SHAPES)
 def test_quant_k_int4_bit_exact(dev, shape):
     print(f"case quant_k_int4 {shape}", flush=True)
     x = _edge_tensor(shape, 0)
@@ -40,7 +43,7 @@ def test_quant_k_int4_bit_exact(dev, shape):
     assert np.array_equal(_u16(scale.cpu().numpy()), _u16(osc))
 
 
-@pytest.mark.parametrize("shape", [(1, 8, 1980, 128), (2, 3, 67, 128), (1, 2, 5, 64), (1, 1, 300, 256)])
+@pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("parts", [1, 16])
 def test_quant_k_int4_from_colmax_bit_exact(dev, shape, parts):
     """The second pass alone, on column maxima spread over `parts` partials (rows
@@ -60,7 +63,7 @@ def test_quant_k_int4_from_colmax_bit_exact(dev, shape, parts):
     assert np.array_equal(_u16(scale.cpu().numpy()), _u16(osc))
 
 
-@pytest.mark.parametrize("shape", [(1, 8, 1980, 128), (2, 3, 67, 128), (1, 2, 5, 64), (1, 1, 300, 256)])
+@pytest.mark.parametrize("shape", SHAPES)
 def test_quant_v_int4_bit_exact(dev, shape):
     print(f"case quant_v_int4 {shape}", flush=True)
     x = _edge_tensor(shape, 1)
@@ -98,9 +101,10 @@ def test_quant_strided_views(dev):
     assert torch.equal(c[0], d[0]) and torch.equal(c[1], d[1])
 
 
-def test_dequant_int4_bit_exact(dev):
-    print("case dequant_int4", flush=True)
-    x = _edge_tensor((2, 2, 40, 128), 3)
+@pytest.mark.parametrize("D", [128, 96, 16])
+def test_dequant_int4_bit_exact(dev, D):
+    print(f"case dequant_int4 D={D}", flush=True)
+    x = _edge_tensor((2, 2, 40, D), 3)
     op, osc = oq.quant_k_int4(x)
     out = fq.dequant_int4(torch.from_numpy(op).to(dev), torch.from_numpy(osc).to(dev))
     assert np.array_equal(_u16(out.cpu().numpy()), _u16(oq.dequant_int4(op, osc)))
@@ -149,7 +153,7 @@ def _same(got, ref, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("shape", [(1, 8, 1980, 128), (2, 3, 67, 128), (1, 2, 5, 64), (1, 1, 300, 256)])
+@pytest.mark.parametrize("shape", SHAPES)
 def test_quant_int4_typed_bit_exact(dev, dtype, shape):
     print(f"case quant_int4 {dtype} {shape}", flush=True)
     x = _typed_edge(shape, 4, dtype)
@@ -216,7 +220,7 @@ def test_quant_int2_grouped_bit_exact(dev, S):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("S,D", [(128, 128), (100, 128), (1, 128), (70, 64), (64, 256), (65, 32)])
+@pytest.mark.parametrize("S,D", [(128, 128), (100, 128), (1, 128), (70, 64), (64, 256), (65, 32), (90, 96), (64, 16)])
 def test_quant_int2_grouped_typed_bit_exact(dev, dtype, S, D):
     print(f"case int2 grouped {dtype} S={S} D={D}", flush=True)
     x = _typed_edge((2, 3, 128, D), 8, dtype)[:, :, :S]
@@ -352,9 +356,10 @@ def test_rotate_quant_fused_rejects(dev):
 
 @pytest.mark.parametrize("bits", [4, 2])
 @pytest.mark.parametrize("group", [32, 16])
-def test_asym_group_quant_bit_exact(dev, bits, group):
-    print(f"case asym bits={bits} group={group}", flush=True)
-    x = _edge_tensor((2, 3, 50, 128), 7)
+@pytest.mark.parametrize("D", [128, 96])
+def test_asym_group_quant_bit_exact(dev, bits, group, D):
+    print(f"case asym bits={bits} group={group} D={D}", flush=True)
+    x = _edge_tensor((2, 3, 50, D), 7)
     x[0, 0, 1, :32] = F16(1.25)
     p, s, z = fq.quant_asym(torch.from_numpy(x).to(dev), bits, group)
     op, os_, oz = oq.quant_asym_group(x, bits, group)
@@ -372,5 +377,7 @@ def test_empty_and_error_inputs(dev):
     assert p.shape == (1, 2, 0, 64) and s.shape == (1, 2, 0, 1)
     with pytest.raises(ValueError, match="float16, bfloat16 or float32"):
         fq.quant_k_int4(torch.zeros(1, 1, 4, 128, dtype=torch.float64, device=dev))
+    with pytest.raises(ValueError, match="head_dim must be"):  # even, but not a multiple of 8
+        fq.quant_v_int4(torch.zeros(1, 1, 4, 100, dtype=torch.float16, device=dev))
     with pytest.raises(ValueError, match="head_dim must be"):
-        fq.quant_v_int4(torch.zeros(1, 1, 4, 96, dtype=torch.float16, device=dev))
+        fq.quant_v_int4(torch.zeros(1, 1, 4, 264, dtype=torch.float16, device=dev))
