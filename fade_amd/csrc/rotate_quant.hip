@@ -115,6 +115,24 @@ __device__ __forceinline__ f32x16 rotate_tile(const f16x8 (&xb)[8], const RTile&
   return acc;
 }
 
+// The same tile for two 32-row x tiles at once: each R fragment read from LDS
+// feeds two MFMAs (the per-channel passes, whose registers have room for it;
+// LDS reads of R then cost half the MFMA time instead of all of it).
+__device__ __forceinline__ void rotate_tile2(const f16x8 (&xa)[8], const f16x8 (&xb)[8], const RTile& rt, int mt,
+                                             int n, int h, f32x16& ya, f32x16& yb) {
+  ya = f32x16{};
+  yb = f32x16{};
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    const f16x8 ah = *reinterpret_cast<const f16x8*>(&rt.hi[32 * mt + n][16 * ks + 8 * h]);
+    const f16x8 al = *reinterpret_cast<const f16x8*>(&rt.lo[32 * mt + n][16 * ks + 8 * h]);
+    ya = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, xa[ks], ya, 0, 0, 0);
+    yb = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, xb[ks], yb, 0, 0, 0);
+    ya = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, xa[ks], ya, 0, 0, 0);
+    yb = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, xb[ks], yb, 0, 0, 0);
+  }
+}
+
 // From the scaled absmax (2^10 max|x_rot|): the scale, and the inverse scale
 // for the scaled values (2^-10 inv).
 __device__ __forceinline__ float sym_inv(float absmax_scaled, float qmax, uint16_t* scale_h) {
@@ -256,21 +274,30 @@ __global__ __launch_bounds__(kThreads) void rotq_colmax_kernel(const uint16_t* _
   const int64_t s1 = s0 + rows_per_block < gm.S ? s0 + rows_per_block : gm.S;
   const uint16_t* base = x + (bh / gm.H) * gm.sb + (bh % gm.H) * gm.sh;
   f32x16 m[4] = {};
-  int64_t t0 = s0 + kRows * wave;
-  f16x8 xb[8];
-  load_x(base, (t0 + n < s1 ? t0 + n : s1 - 1) * gm.ss, h, xb);
-  for (; t0 < s1; t0 += kRows * kWaves) {
+  // each wave takes two 32-row tiles per step (rows past the block: its last
+  // row again, which changes no column's absmax)
+  constexpr int64_t kStep = 2 * kRows * kWaves;
+  int64_t t0 = s0 + 2 * kRows * wave;
+  auto rowc = [&](int64_t r) { return (r < s1 ? r : s1 - 1) * gm.ss; };
+  f16x8 xa[8], xb[8];
+  load_x(base, rowc(t0 + n), h, xa);
+  load_x(base, rowc(t0 + kRows + n), h, xb);
+  for (; t0 < s1; t0 += kStep) {
     __asm__ volatile("" ::: "memory");  // keep the R fragment reads inside the loop
-    f16x8 cur[8];
+    f16x8 ca[8], cb[8];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) cur[ks] = xb[ks];
-    const int64_t nx = t0 + kRows * kWaves + n;
-    load_x(base, (nx < s1 ? nx : s1 - 1) * gm.ss, h, xb);
+    for (int ks = 0; ks < 8; ++ks) {
+      ca[ks] = xa[ks];
+      cb[ks] = xb[ks];
+    }
+    load_x(base, rowc(t0 + kStep + n), h, xa);
+    load_x(base, rowc(t0 + kStep + kRows + n), h, xb);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      const f32x16 xr = rotate_tile(cur, rt, mt, n, h);
+      f32x16 ya, yb;
+      rotate_tile2(ca, cb, rt, mt, n, h, ya, yb);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) m[mt][i] = fmaxf(m[mt][i], fabsf(xr[i]));
+      for (int i = 0; i < 16; ++i) m[mt][i] = fmaxf(m[mt][i], fmaxf(fabsf(ya[i]), fabsf(yb[i])));
     }
   }
   // over the wave's 32 rows (lanes n), then over the waves
@@ -300,7 +327,7 @@ __global__ __launch_bounds__(kThreads) void rotq_channel_kernel(const uint16_t* 
   constexpr float QMAX = static_cast<float>(RQ<BITS>::hi);
   constexpr int RB = RQ<BITS>::row_bytes;
   __shared__ __attribute__((aligned(16))) RTile rt;
-  __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][kRows * StagePitch<BITS>::value];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][2 * kRows * StagePitch<BITS>::value];
   __shared__ float inv_s[kD];
   load_r(R, rt);
   const int64_t bh = blockIdx.y;
@@ -323,22 +350,34 @@ __global__ __launch_bounds__(kThreads) void rotq_channel_kernel(const uint16_t* 
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) inv[mt][i] = inv_s[32 * mt + 8 * (i / 4) + 4 * h + i % 4];
-  int64_t t0 = s0 + kRows * wave;
-  f16x8 xb[8];
-  load_x(base, (t0 + n < s1 ? t0 + n : s1 - 1) * gm.ss, h, xb);
-  for (; t0 < s1; t0 += kRows * kWaves) {
+  // two 32-row tiles per step, as in pass 1 (rows past the block are computed
+  // from its last row and never stored)
+  constexpr int64_t kStep = 2 * kRows * kWaves;
+  constexpr int kHalf = kRows * StagePitch<BITS>::value;  // stage bytes of one 32-row tile
+  int64_t t0 = s0 + 2 * kRows * wave;
+  auto rowc = [&](int64_t r) { return (r < s1 ? r : s1 - 1) * gm.ss; };
+  f16x8 xa[8], xb[8];
+  load_x(base, rowc(t0 + n), h, xa);
+  load_x(base, rowc(t0 + kRows + n), h, xb);
+  for (; t0 < s1; t0 += kStep) {
     __asm__ volatile("" ::: "memory");  // keep the R fragment reads inside the loop
-    f16x8 cur[8];
+    f16x8 ca[8], cb[8];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) cur[ks] = xb[ks];
-    const int64_t nx = t0 + kRows * kWaves + n;
-    load_x(base, (nx < s1 ? nx : s1 - 1) * gm.ss, h, xb);
+    for (int ks = 0; ks < 8; ++ks) {
+      ca[ks] = xa[ks];
+      cb[ks] = xb[ks];
+    }
+    load_x(base, rowc(t0 + kStep + n), h, xa);
+    load_x(base, rowc(t0 + kStep + kRows + n), h, xb);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      const f32x16 xr = rotate_tile(cur, rt, mt, n, h);
-      stage_codes<BITS>(xr, mt, n, h, inv[mt], 1, &stage[wave][0]);
+      f32x16 ya, yb;
+      rotate_tile2(ca, cb, rt, mt, n, h, ya, yb);
+      stage_codes<BITS>(ya, mt, n, h, inv[mt], 1, &stage[wave][0]);
+      stage_codes<BITS>(yb, mt, n, h, inv[mt], 1, &stage[wave][kHalf]);
     }
     flush_stage<BITS>(&stage[wave][0], out, t0, s1, lane);
+    flush_stage<BITS>(&stage[wave][kHalf], out, t0 + kRows, s1, lane);
   }
 }
 
