@@ -189,7 +189,27 @@ __device__ __forceinline__ int lit_swz(int r) { return ((r >> 1) & 3) | ((r >> 2
 // formats, 8 or 10 KB for the asymmetric ones, 12.25 KB for literal INT2 V).
 // NW waves per workgroup (4, 6 or 8; see packed_kernel); registers are sized
 // for two waves per SIMD.
-template <int KB, int VB, int FMT, int NW, bool DET, bool TWO, bool ROT>
+// s_waitcnt vmcnt(c) for a run-time c = i A + j F (i + j <= NS: loads of
+// i packed and j fp16 tiles): s_waitcnt takes an immediate, so every count
+// the ring can reach has its own instruction.
+template <int A, int F, int NS, int I = 0, int J = 0>
+__device__ __forceinline__ void wait_vm_dispatch(int c) {
+  if constexpr (I > NS) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // not reached: every count is listed
+  } else if constexpr (I + J > NS) {
+    wait_vm_dispatch<A, F, NS, I + 1, 0>(c);
+  } else {
+    static_assert(I * A + J * F <= 63, "more loads in flight than vmcnt counts");
+    if (c == I * A + J * F) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(I * A + J * F));
+      return;
+    }
+    wait_vm_dispatch<A, F, NS, I, J + 1>(c);
+  }
+}
+
+// NS: ring stages per wave (tiles in flight while one is computed: NS - 1).
+template <int KB, int VB, int FMT, int NW, bool DET, bool TWO, bool ROT, int NS>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_packed_kernel(
     Params p) {
   constexpr int kWaves = NW, kThreads = 64 * NW;
@@ -245,8 +265,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   __shared__ int claim_s;
   if (tid == 0) claim_s = 0;
 
-  __shared__ __attribute__((aligned(16))) uint8_t ring0[kWaves][S::kBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t ring1[kWaves][S::kBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t ring[NS][kWaves][S::kBytes];
   __shared__ __attribute__((aligned(16))) uint32_t qraw_s[kHeads][kD / 2];  // fp16 query rows
   __shared__ __attribute__((aligned(16))) uint32_t ksraw_s[ASYM ? 1 : kHeads][kD / 2];  // K scales (waves 0..3)
   __shared__ __attribute__((aligned(16))) uint8_t qd_s[kQdZero + 16];
@@ -304,10 +323,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
     return r;
   };
-  lds_u8* const sp0 = (lds_u8*)&ring0[wave][0];
-  lds_u8* const sp1 = (lds_u8*)&ring1[wave][0];
-  const uint32_t st0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sp0)));
-  const uint32_t st1 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sp1)));
+  lds_u8* spr[NS];   // this wave's ring stages
+  uint32_t str[NS];  // their LDS addresses (wave-uniform)
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    spr[s] = (lds_u8*)&ring[s][wave][0];
+    str[s] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(spr[s])));
+  }
 
   // ---- loads of one tile into a ring stage (kOps per packed tile, kOpsF16 per fp16 tile) ----
   // Packed tile, 4-bit codes: 16-byte unit q of K row r at LDS unit 4r + (q ^ ((r >> 2) & 3)),
@@ -439,15 +461,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   }
   auto ops_t = [&](int64_t t) { return t < t1 ? (t < nFt ? kOpsF16 : kOps) : 0; };
   // s_waitcnt needs an immediate: the outstanding-op counts that can occur
-  auto wait_vm = [&](int c) {
-    constexpr int A = kOps, F = kOpsF16;
-    if (c == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    else if (c == A) __builtin_amdgcn_s_waitcnt(vmcnt_imm(A));
-    else if (c == F) __builtin_amdgcn_s_waitcnt(vmcnt_imm(F));
-    else if (c == 2 * A) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * A));
-    else if (c == A + F) __builtin_amdgcn_s_waitcnt(vmcnt_imm(A + F));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * F));
-  };
+  auto wait_vm = [&](int c) { wait_vm_dispatch<kOps, kOpsF16, NS>(c); };
   // ---- rotated middle tier: q R^T of the pass's heads, for the middle splits ----
   // f16 MFMA 16x16x32: C[channel 16 mt + row][head] = sum_k R[16 mt + row][k] q[head][k],
   // with R carried at scale 2^10 as hi = fp16(2^10 R) and lo = fp16(2^10 R - hi)
@@ -472,10 +486,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
       }
     }
   }
-  int64_t ta = t0 + wave, tb = t0 + kWaves + wave;  // tiles in stages 0 and 1
-  if (ta < t1) issue(ta, st0, true, true);
-  if (tb < t1) issue(tb, st1, true, true);
-  wait_vm(ops_t(ta) + ops_t(tb));  // the query (and K-scale, and R) loads have landed
+  // the ring's tiles, oldest first from stage 0: the wave's first NS tiles
+  int64_t tq[NS];
+  int c_first = 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    tq[s] = t0 + s * kWaves + wave;
+    if (tq[s] < t1) issue(tq[s], str[s], true, true);
+    c_first += ops_t(tq[s]);
+  }
+  wait_vm(c_first);  // the query (and K-scale, and R) loads have landed
   __builtin_amdgcn_wave_barrier();
   if constexpr (ROT) {
     if (rot && split > 0) {
@@ -950,21 +970,29 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
   };
 
-  // ---- main loop: two stages, two tiles in flight ----
-  // step: tile `cur` sits in stage (sp, st), `nxt` (if any) is in flight behind
-  // it; afterwards the stage is refilled with a newly claimed tile, returned
-  // (>= t1 when the split is exhausted; claims only grow).
-  auto step = [&](int64_t cur, int64_t nxt, const lds_u8* sp, uint32_t st) -> int64_t {
+  // ---- main loop: NS stages, NS - 1 tiles in flight behind the one computed ----
+  // step s: tile tq[s] (the oldest) sits in stage s, the tiles of the other
+  // stages are in flight behind it; afterwards stage s is refilled with a
+  // newly claimed tile.  Claims only grow, so once the oldest tile is past the
+  // split (>= t1) so is every tile behind it, and nothing is in flight.
+  auto step = [&](int s) -> bool {
+    const int64_t cur = tq[s];
+    if (cur >= t1) return false;
+    lds_u8* const sp = spr[s];
+    const uint32_t st = str[s];
     // the tile that refills this stage, known before `cur` is computed
     int64_t nt;
-    if constexpr (DET) {  // wave w walks tiles t0 + w, t0 + w + NW, ... : cur's successor's successor
-      nt = cur + 2 * kWaves;
+    if constexpr (DET) {  // wave w walks tiles t0 + w, t0 + w + NW, ... : cur's NS-th successor
+      nt = cur + NS * kWaves;
     } else {
       int c = 0;
       if (lane == 0) c = __hip_atomic_fetch_add(&claim_s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      nt = t0 + 2 * kWaves + __builtin_amdgcn_readfirstlane(c);
+      nt = t0 + NS * kWaves + __builtin_amdgcn_readfirstlane(c);
     }
-    wait_vm(ops_t(nxt));  // `cur` landed
+    int behind = 0;  // loads issued after cur's
+#pragma unroll
+    for (int j = 1; j < NS; ++j) behind += ops_t(tq[(s + j) % NS]);
+    wait_vm(behind);  // `cur` landed
     __builtin_amdgcn_wave_barrier();
     // once cur's K codes have been read from the stage, nt's K codes are loaded
     // into it: they fly during the rest of cur's compute
@@ -980,13 +1008,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     __builtin_amdgcn_s_waitcnt(kLgkm0);  // every LDS read of this stage has returned
     __builtin_amdgcn_wave_barrier();
     if (nt < t1) issue(nt, st, false, true);
-    return nt;
+    tq[s] = nt;
+    return true;
   };
-  while (ta < t1) {
-    const int64_t na = step(ta, tb, sp0, st0);
-    if (tb >= t1) break;
-    tb = step(tb, na, sp1, st1);
-    ta = na;
+  for (bool more = true; more;) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      if (more) more = step(s);
   }
 
   // ---- merge the wavefronts of the workgroup ----
@@ -1013,7 +1041,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     red_l[wave][hq] = lsum;
   }
   __syncthreads();
-  float* red_o = reinterpret_cast<float*>(&ring0[0][0]);  // [wave][4 heads][128] (NW * 2 KB)
+  float* red_o = reinterpret_cast<float*>(&ring[0][0][0]);  // [wave][4 heads][128] (NW * 2 KB)
   {
     float Mg = red_m[0][g];
 #pragma unroll
@@ -1154,7 +1182,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     if (rot) {
       // out = (of + o R) / L: o [head][d] to LDS, then 512 virtual threads
       // (channel c, quarter dq) sum d over [32 dq, 32 dq + 32) for every head
-      float* ro = reinterpret_cast<float*>(&ring0[0][0]);  // [4][kD] o, then [4 dq][4][kD] partial products
+      float* ro = reinterpret_cast<float*>(&ring[0][0][0]);  // [4][kD] o, then [4 dq][4][kD] partial products
       float* pp = ro + kHeads * kD;
 #pragma unroll
       for (int e = 0; e < kE; ++e) {
@@ -1261,19 +1289,19 @@ template <bool DET, bool TWO>
 Choice packed_kernel_t(const Params& p) {
   const int kb = p.mid.k_bits, vb = p.mid.v_bits;
   constexpr int v = (DET ? 2 : 0) + (TWO ? 1 : 0);
-  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6, DET, TWO, false>, 6, 4 * 6 + v};
+  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6, DET, TWO, false, 2>, 6, 4 * 6 + v};
   if (p.mid.fmt == FADE_MID_SYM) {
     if (p.rot != nullptr) {  // rotated backend: q R^T in the prologue, the middle part times R in the merge
-      if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO, true>, 4, 4 * 7 + v};
-      return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO, true>, 8, 4 * 8 + v};
+      if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO, true, 2>, 4, 4 * 7 + v};
+      return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO, true, 2>, 8, 4 * 8 + v};
     }
-    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO, false>, 4, 4 * 0 + v};  // two workgroups per CU
-    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO, false>, 8, 4 * 1 + v};
+    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO, false, 2>, 4, 4 * 0 + v};  // two workgroups per CU
+    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO, false, 2>, 8, 4 * 1 + v};
   }
-  if (kb == 4 && vb == 4) return {decode_packed_kernel<4, 4, kFmtAsym, 6, DET, TWO, false>, 6, 4 * 2 + v};
-  if (kb == 4 && vb == 2) return {decode_packed_kernel<4, 2, kFmtAsym, 8, DET, TWO, false>, 8, 4 * 3 + v};
-  if (kb == 2 && vb == 2) return {decode_packed_kernel<2, 2, kFmtAsym, 8, DET, TWO, false>, 8, 4 * 4 + v};
-  return {decode_packed_kernel<2, 4, kFmtAsym, 6, DET, TWO, false>, 6, 4 * 5 + v};
+  if (kb == 4 && vb == 4) return {decode_packed_kernel<4, 4, kFmtAsym, 6, DET, TWO, false, 2>, 6, 4 * 2 + v};
+  if (kb == 4 && vb == 2) return {decode_packed_kernel<4, 2, kFmtAsym, 8, DET, TWO, false, 2>, 8, 4 * 3 + v};
+  if (kb == 2 && vb == 2) return {decode_packed_kernel<2, 2, kFmtAsym, 8, DET, TWO, false, 2>, 8, 4 * 4 + v};
+  return {decode_packed_kernel<2, 4, kFmtAsym, 6, DET, TWO, false, 2>, 6, 4 * 5 + v};
 }
 
 Choice packed_kernel(const Params& p) {

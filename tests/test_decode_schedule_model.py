@@ -1,6 +1,6 @@
 """Host-side model of the packed decode kernel's tile pipeline (CPU only).
 
-``decode_packed_kernel`` (fade_amd/csrc/decode_int4.hip) streams tiles into two
+``decode_packed_kernel`` (fade_amd/csrc/decode_int4.hip) streams tiles into NS
 LDS ring stages per wave with direct-to-LDS loads that the compiler does not
 track, and waits for them with its own ``s_waitcnt vmcnt(c)``: c is the number
 of loads issued after the ones the next stage read needs.  The counts are
@@ -75,9 +75,10 @@ class Wave:
         self.q.extend([(tile, stage, part)] * n)
         self.loaded[(stage, part)] = tile
 
-    def wait(self, c, fmt: Fmt):
-        allowed = {0, fmt.A, fmt.F, 2 * fmt.A, fmt.A + fmt.F, 2 * fmt.F}
-        assert c in allowed, f"wait count {c} has no immediate (kernel falls through to 2F)"
+    def wait(self, c, fmt: Fmt, ns: int = 2):
+        allowed = {i * fmt.A + j * fmt.F for i in range(ns + 1) for j in range(ns + 1 - i)}
+        assert c in allowed, f"wait count {c} has no immediate (kernel falls through to vmcnt(0))"
+        assert c <= 63, "more loads in flight than vmcnt counts"
         while len(self.q) > c:  # adversarial: retire only the oldest
             self.q.pop(0)
 
@@ -87,8 +88,9 @@ class Wave:
         assert not pending, f"read of tile {tile} stage {stage} {part} with loads in flight: {pending[:2]}"
 
 
-def run_workgroup(fmt: Fmt, NW: int, t0: int, t1: int, nFt: int, det: bool, rng: random.Random, q_loads=2):
-    """Replays one workgroup; returns the tiles each wave processed."""
+def run_workgroup(fmt: Fmt, NW: int, t0: int, t1: int, nFt: int, det: bool, rng: random.Random, q_loads=2,
+                  NS: int = 2):
+    """Replays one workgroup (NS ring stages per wave); returns the tiles each wave processed."""
     claim = [0]
     taken = [[] for _ in range(NW)]
 
@@ -110,36 +112,39 @@ def run_workgroup(fmt: Fmt, NW: int, t0: int, t1: int, nFt: int, det: bool, rng:
             if v:
                 wv.issue(t, st, "V", vp)
 
-        if ta < t1:
-            issue(ta, 0, True, True)
-        if tb < t1:
-            issue(tb, 1, True, True)
-        wv.wait(ops(ta) + ops(tb), fmt)
+        tq = [t0 + s * NW + w for s in range(NS)]  # the ring, oldest first from stage 0
+        for s in range(NS):
+            if tq[s] < t1:
+                issue(tq[s], s, True, True)
+        wv.wait(sum(ops(t) for t in tq), fmt, NS)
         assert not [x for x in wv.q if x[0] == "query"], "query loads still in flight after the prologue wait"
 
-        def step(cur, nxt, st):
+        def step(s):
+            cur = tq[s]
+            if cur >= t1:
+                return False
             if det:
-                nt = cur + 2 * NW
+                nt = cur + NS * NW
             else:
                 yield "claim"  # the only point where other waves can interleave meaningfully
-                nt = t0 + 2 * NW + claim[0]
+                nt = t0 + NS * NW + claim[0]
                 claim[0] += 1
-            wv.wait(ops(nxt), fmt)
-            wv.read(cur, st, "K")
+            wv.wait(sum(ops(tq[(s + j) % NS]) for j in range(1, NS)), fmt, NS)
+            wv.read(cur, s, "K")
             if nt < t1:
-                issue(nt, st, True, False)  # refill_k: after the K reads (lgkmcnt(0))
-            wv.read(cur, st, "V")
+                issue(nt, s, True, False)  # refill_k: after the K reads (lgkmcnt(0))
+            wv.read(cur, s, "V")
             taken[w].append(cur)
             if nt < t1:
-                issue(nt, st, False, True)
-            return nt
+                issue(nt, s, False, True)
+            tq[s] = nt
+            return True
 
-        while ta < t1:
-            na = yield from step(ta, tb, 0)
-            if tb >= t1:
-                break
-            tb = yield from step(tb, na, 1)
-            ta = na
+        more = True
+        while more:
+            for s in range(NS):
+                if more:
+                    more = yield from step(s)
         assert not wv.q, f"wave {w} leaves the loop with loads in flight: {wv.q[:2]}"
 
     progs = [wave_prog(w) for w in range(NW)]
@@ -159,11 +164,14 @@ def split_bounds(split, tps, nT, nFt, rot):
     return t0, t1
 
 
+@pytest.mark.parametrize("NS", [2, 3, 4])
 @pytest.mark.parametrize("fmt_name", sorted(FORMATS))
-def test_schedule_model(fmt_name):
+def test_schedule_model(fmt_name, NS):
     fmt = fmt_ops(fmt_name)
-    rng = random.Random(hash(fmt_name) & 0xFFFF)
-    for trial in range(400):
+    if NS * max(fmt.A, fmt.F) > 63:
+        pytest.skip("more loads in flight than vmcnt counts: the kernel does not build this stage count")
+    rng = random.Random((hash(fmt_name) & 0xFFFF) + NS)
+    for trial in range(300):
         NW = rng.choice([4, 6, 8])
         nFt = rng.randrange(0, 7)
         nMt = rng.randrange(1 if nFt == 0 else 0, 40)
@@ -187,7 +195,7 @@ def test_schedule_model(fmt_name):
             if not rot:
                 t1 = min(t1, row_nT)
             taken = run_workgroup(fmt, NW, t0, t1, row_nFt if rot else nFt, det, rng,
-                                  q_loads=2 + (8 if rot and split > 0 else 0))
+                                  q_loads=2 + (8 if rot and split > 0 else 0), NS=NS)
             flat = sorted(t for ts in taken for t in ts)
             assert flat == list(range(t0, max(t0, t1))), (fmt_name, trial, split, flat, t0, t1)
             seen += flat

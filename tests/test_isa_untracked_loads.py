@@ -41,7 +41,7 @@ def test_rotated_prologue_registers_untouched_until_the_wait(tmp_path):
     subprocess.run(cmd, check=True, capture_output=True, timeout=600)
     lines = out.read_text().split("\n")
     starts = [i for i, l in enumerate(lines)
-              if re.match(r"^_ZN4fade6decode12_GLOBAL__N_120decode_packed_kernelIL.*Lb1EEEvNS0_6ParamsE:", l)
+              if re.match(r"^_ZN4fade6decode12_GLOBAL__N_120decode_packed_kernelIL.*Lb1ELi\d+EEEvNS0_6ParamsE:", l)
               and "ELi0ELi" in l]
     assert len(starts) == 8, "expected the 8 rotated instances (4/2-bit x DET x two passes)"
     for s in starts:
