@@ -58,10 +58,11 @@ def decode_bytes(cfg, fmt: str) -> int:
     return cfg.B * cfg.Hkv * per_head + 2 * cfg.B * cfg.Hq * D * 2
 
 
-def build_instances(cfg, fmt: str, dev, seed: int, n: int):
-    """Quantize the middle tier once on the GPU, then clone it into n distinct allocations."""
+def build_instances(cfg, fmt: str, dev, seed: int, n: int, dtype=torch.float16):
+    """Quantize the middle tier once on the GPU, then clone it into n distinct allocations.
+    ``dtype``: the cache's (and model's) float type, float16 or bfloat16."""
     q, k, v = kv_tensors(cfg.B, cfg.Hkv, cfg.S, cfg.D, seed=seed, Hq=cfg.Hq)
-    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    qd, kd, vd = q.to(dev, dtype), k.to(dev, dtype), v.to(dev, dtype)
     del k, v
     ns, nr, S = cfg.n_sink, cfg.recent, cfg.S
     km, vm = kd[:, :, ns : S - nr].contiguous(), vd[:, :, ns : S - nr].contiguous()
@@ -719,6 +720,16 @@ def main() -> int:
             "frac_of_peak": round(ab / (amean * 1e-3) / 1e9 / HBM_PEAK_GBPS, 3),
         }
         del pa
+        torch.cuda.empty_cache()
+        # config 1 on a bfloat16 cache (bf16 models: q, fp16-layout tiers, scales and output
+        # in bf16; bf16 MFMAs for P V)
+        pb = build_instances(cfg, "int4", dev, 1001, N_INSTANCES, dtype=torch.bfloat16)
+        bmean = graph_us(pb) * 1e-3
+        extra["c1_bf16_int4"] = {
+            "us": round(bmean * 1e3, 2), "GBps": round(nbytes / (bmean * 1e-3) / 1e9, 1), "bytes": nbytes,
+            "frac_of_peak": round(nbytes / (bmean * 1e-3) / 1e9 / HBM_PEAK_GBPS, 3),
+        }
+        del pb
         torch.cuda.empty_cache()
         pf, pflops, pbytes = prefill_case(dev)
         # 40 warmup calls: this MFMA-bound kernel's per-call time keeps falling

@@ -76,6 +76,10 @@ class MidTier(ctypes.Structure):
     ]
 
 
+# FADE_ABI_VERSION of include/fade_hip.h that DecodeArgs / PrefillArgs mirror
+ABI_VERSION = 2
+
+
 class DecodeArgs(ctypes.Structure):
     _fields_ = [
         ("B", _i64),
@@ -99,6 +103,7 @@ class DecodeArgs(ctypes.Structure):
         ("lens", _p),
         ("deterministic", _i32),
         ("rotation", _p),
+        ("dtype", _i32),
     ]
 
 
@@ -125,6 +130,7 @@ class PrefillArgs(ctypes.Structure):
         ("recent", Fp16Tier),
         ("chunk", Fp16Tier),
         ("mask_mode", _i32),
+        ("dtype", _i32),
     ]
 
 
@@ -218,6 +224,11 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes
                 fn.restype = _RESTYPES.get(name, ctypes.c_int)
+            if lib.fade_hip_abi_version() != ABI_VERSION:  # the argument structs below match this version only
+                raise RuntimeError(
+                    f"fade_amd: {LIB_PATH} has ABI version {lib.fade_hip_abi_version()}, this package needs "
+                    f"{ABI_VERSION}; rebuild it (`make -C fade_amd/csrc`)"
+                )
             _lib = lib
     return _lib
 

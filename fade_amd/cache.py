@@ -143,9 +143,10 @@ class TieredKVCache(DynamicCache):
     per-sequence mode (``apply_tier_assignment_per_sequence``) as in the
     reference.  ``dtype`` float16, bfloat16 or float32, as the reference's:
     every tier, scale and dequantized copy is of it.  The fused attention
-    kernels (``fused`` mode), the device reassignment and the ragged layout
-    read float16 caches; the others use the host reassignment (the HIP
-    quantizers and re-RoPE kernel at their dtype).
+    kernels (``fused`` mode) read float16 and bfloat16 caches; the device
+    reassignment and the ragged layout read float16 caches, the others use
+    the host reassignment (the HIP quantizers and re-RoPE kernel at their
+    dtype).
     """
 
     def __init__(
@@ -250,9 +251,10 @@ class TieredKVCache(DynamicCache):
             raise ValueError(f"key_states must be [B, H, S, D]; got shape {tuple(key_states.shape)}")
         if key_states.shape != value_states.shape:
             raise ValueError(f"K/V shape mismatch: {tuple(key_states.shape)} vs {tuple(value_states.shape)}")
-        if self.fused and self.dtype != torch.float16:  # refused before any state changes
+        if self.fused and self.dtype not in _FUSED_DTYPES:  # refused before any state changes
             raise NotImplementedError(
-                f"fused attention reads float16 caches; this one is {self.dtype} (use the model's own attention)"
+                f"fused attention reads float16 and bfloat16 caches; this one is {self.dtype} "
+                "(use the model's own attention)"
             )
         batch = int(key_states.shape[0])
         if self.batch_size is None:
@@ -1366,9 +1368,9 @@ class TieredKVCache(DynamicCache):
         return sink, (st.fp16_k[..., ns:, :], st.fp16_v[..., ns:, :])
 
     def _require_f16_tiers(self, op: str) -> None:
-        if self.dtype != torch.float16:
+        if self.dtype not in _FUSED_DTYPES:
             raise NotImplementedError(
-                f"{op}: the tiered attention kernels read float16 tiers; this cache is {self.dtype} "
+                f"{op}: the tiered attention kernels read float16 and bfloat16 tiers; this cache is {self.dtype} "
                 "(attend over the materialized K/V instead)"
             )
 
@@ -1498,8 +1500,8 @@ class TieredKVCache(DynamicCache):
                 B, H = int(q.shape[0]), int((st.fp16_k if st.fp16_k is not None else st.sink_k).shape[1])
                 D = int(q.shape[-1])
                 z8 = torch.zeros(B, H, 1, D // 2, dtype=torch.uint8, device=q.device)
-                mid = MiddleTier("int4", z8, z8.clone(), torch.zeros(B, H, 1, D, dtype=torch.float16, device=q.device),
-                                 torch.zeros(B, H, 1, 1, dtype=torch.float16, device=q.device))
+                mid = MiddleTier("int4", z8, z8.clone(), torch.zeros(B, H, 1, D, dtype=self.dtype, device=q.device),
+                                 torch.zeros(B, H, 1, 1, dtype=self.dtype, device=q.device))
             sink = None if st.sink_k is None else (st.sink_k, st.sink_v)
             recent = None if st.fp16_k is None or st.fp16_k.shape[-2] == 0 else (st.fp16_k, st.fp16_v)
             return tiered_decode_attention(q, sink, mid, recent, sm_scale, n_splits=self.decode_splits, lens=st.lens)
@@ -1542,8 +1544,8 @@ class TieredKVCache(DynamicCache):
                 # the kernel scores the middle with q R^T and un-rotates its part of the output
                 rotation = be._get_R(q.device)
                 mid = MiddleTier(
-                    "sym", bk["packed"], bv["packed"], bk["scale"].to(torch.float16),
-                    bv["scale"].to(torch.float16), k_bits=be.bits, v_bits=be.bits,
+                    "sym", bk["packed"], bv["packed"], bk["scale"].to(self.dtype),
+                    bv["scale"].to(self.dtype), k_bits=be.bits, v_bits=be.bits,
                 )
             elif isinstance(be, AsymGroupBackend):
                 mid = MiddleTier(
@@ -1567,6 +1569,10 @@ class TieredKVCache(DynamicCache):
                 st.int2_kq, st.int2_vq, st.int2_ks, st.int2_vs,
                 tuple(q.shape), q.stride(), q.device, q.dtype, sm_scale, self.decode_splits, self.middle_v_bits,
                 self._quant_backend, torch.are_deterministic_algorithms_enabled(), stream)
+
+
+# cache dtypes the fused attention kernels read
+_FUSED_DTYPES = (torch.float16, torch.bfloat16)
 
 
 def _same_key(a: tuple, b: tuple) -> bool:

@@ -23,6 +23,15 @@ namespace {
 constexpr int kTile = 64;
 constexpr int kThreads = 256;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// fp32 += a.x * b.x + a.y * b.y over 16-bit pairs of the instance's dtype
+// (BF: bfloat16, else fp16), products and sum in fp32.
+template <bool BF>
+__device__ __forceinline__ float dot2w(uint32_t a, uint32_t b, float c) {
+  if constexpr (BF) return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+  else return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+}
 
 // Eight consecutive fp16 values (channels 8 cg .. 8 cg + 7) of a row, with a
 // 16-byte load where the address allows it.
@@ -34,10 +43,13 @@ __device__ __forceinline__ uint4 load8h(const uint16_t* src) {
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Eight fp32 values rounded to the instance's 16-bit dtype (nearest even).
+template <bool BF>
 __device__ __forceinline__ uint4 pack8h(const float* x) {
   uint32_t w[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) w[j] = static_cast<uint32_t>(f2h(x[2 * j])) | (static_cast<uint32_t>(f2h(x[2 * j + 1])) << 16);
+  for (int j = 0; j < 4; ++j)
+    w[j] = static_cast<uint32_t>(f2w<BF>(x[2 * j])) | (static_cast<uint32_t>(f2w<BF>(x[2 * j + 1])) << 16);
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
@@ -157,9 +169,10 @@ __device__ __forceinline__ uint4 sym4_to_f16(uint32_t w, const uint32_t (&s2)[4]
 }
 
 // A loaded unit dequantized as the reference does (fp16(code * scale),
-// fp16(code * scale + zero) for the asymmetric format): eight fp16 values.
+// fp16(code * scale + zero) for the asymmetric format; bf16(code * scale) in
+// a bfloat16 instance): eight values of the instance's dtype.
 // ks_s: the row's per-channel K scales (fp32); ks2_s: the same as fp16 pairs.
-template <bool IS_V, bool SYM44>
+template <bool IS_V, bool SYM44, bool BF>
 __device__ __forceinline__ uint4 convert_unit(const Params& p, int64_t b, int64_t kvh, UnitRef u, int cg,
                                               const RawUnit& ru, const float* ks_s, const uint32_t* ks2_s) {
   const int fmt = SYM44 ? FADE_MID_SYM : p.mid.fmt;
@@ -187,9 +200,9 @@ __device__ __forceinline__ uint4 convert_unit(const Params& p, int64_t b, int64_
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int8_t c = static_cast<int8_t>(((j < 4 ? ru.w.x : ru.w.y) >> (8 * (j & 3))) & 0xFF);
-      x[j] = static_cast<float>(c) * h2f(static_cast<uint16_t>(sw[j >> 1] >> (16 * (j & 1))));
+      x[j] = static_cast<float>(c) * w2f<BF>(static_cast<uint16_t>(sw[j >> 1] >> (16 * (j & 1))));
     }
-    return pack8h(x);
+    return pack8h<BF>(x);
   }
   const int bits = SYM44 || fmt == FADE_MID_K4V2G ? 4 : (IS_V ? p.mid.v_bits : p.mid.k_bits);
   int c[8];
@@ -205,21 +218,21 @@ __device__ __forceinline__ uint4 convert_unit(const Params& p, int64_t b, int64_
     const float z = h2f(static_cast<uint16_t>(ru.w.y >> 16));
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = static_cast<float>(c[j]) * s + z;
-    return pack8h(x);
+    return pack8h<BF>(x);
   }
   // symmetric: two's complement codes
   const int sgn = bits == 4 ? 8 : 2;
 #pragma unroll
   for (int j = 0; j < 8; ++j) c[j] -= (c[j] & sgn) << 1;
   if (IS_V) {
-    const float s = h2f(static_cast<uint16_t>(ru.w.y & 0xFFFFu));
+    const float s = w2f<BF>(static_cast<uint16_t>(ru.w.y & 0xFFFFu));
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = static_cast<float>(c[j]) * s;
   } else {
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = static_cast<float>(c[j]) * ks_s[d0 + j];
   }
-  return pack8h(x);
+  return pack8h<BF>(x);
 }
 
 // Max over the 64 lanes of a wave (all lanes active): DPP exchanges within
@@ -262,8 +275,11 @@ __device__ __forceinline__ float wave_max64(float v) {
 // the output directly.  (Merging in the last workgroup to finish, as the
 // matrix-core kernel does, measured slower here: these workgroups are short,
 // and each then waits for its partial stores and a counter round trip.)
-template <int DP, int HP, bool SYM44>
+// BF: every 16-bit float of the call is bfloat16 (SYM44, a packed fp16
+// dequantization, has no bfloat16 instance).
+template <int DP, int HP, bool SYM44, bool BF>
 __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
+  static_assert(!(SYM44 && BF), "the SYM44 fast path dequantizes in fp16");
   constexpr int CG = DP / 8;                // 8-channel units per row (capacity)
   constexpr int KP = DP + 8;                // K row pitch in LDS (halves)
   constexpr int VPP = DP + 4;               // V token-pair row pitch in LDS (dwords)
@@ -293,7 +309,7 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
     q2_s[h][d / 2] = h < G && d < D ? static_cast<uint32_t>(qr[0]) | (static_cast<uint32_t>(qr[1]) << 16) : 0u;
   }
   if (p.mid.fmt == FADE_MID_SYM || p.mid.fmt == FADE_MID_K4V2G)
-    for (int d = tid; d < DP; d += kThreads) ks_s[d] = d < D ? h2f(p.mid.k_scale[(b * p.Hkv + kvh) * D + d]) : 0.0f;
+    for (int d = tid; d < DP; d += kThreads) ks_s[d] = d < D ? w2f<BF>(p.mid.k_scale[(b * p.Hkv + kvh) * D + d]) : 0.0f;
   if (SYM44)
     for (int d = tid; d < DP / 2; d += kThreads) {
       const uint16_t* ks = p.mid.k_scale + (b * p.Hkv + kvh) * D + 2 * d;
@@ -360,8 +376,8 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
           uint4 kw = make_uint4(0, 0, 0, 0), v = make_uint4(0, 0, 0, 0);
           if (r < nv && 8 * cg < D) {
             const UnitRef ur = unit_ref(ts + r, ns, nm);
-            kw = convert_unit<false, SYM44>(p, b, kvh, ur, cg, rk[i][e], ks_s, ks2_s);
-            v = convert_unit<true, SYM44>(p, b, kvh, ur, cg, rv[i][e], ks_s, ks2_s);
+            kw = convert_unit<false, SYM44, BF>(p, b, kvh, ur, cg, rk[i][e], ks_s, ks2_s);
+            v = convert_unit<true, SYM44, BF>(p, b, kvh, ur, cg, rv[i][e], ks_s, ks2_s);
           }
           *reinterpret_cast<uint4*>(&kt[r][8 * cg]) = kw;
           vw[e][0] = v.x;
@@ -403,9 +419,7 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
           const uint4 qw = *reinterpret_cast<const uint4*>(&q2_s[wave + 4 * i][4 * cg]);
           const uint32_t q2[4] = {qw.x, qw.y, qw.z, qw.w};
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            s[i] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, k2[j]), __builtin_bit_cast(f16x2, q2[j]), s[i],
-                                          false);
+          for (int j = 0; j < 4; ++j) s[i] = dot2w<BF>(k2[j], q2[j], s[i]);
         }
       }
 #pragma unroll
@@ -422,7 +436,7 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
             pv = __builtin_amdgcn_exp2f(sc - m_new);
           }
           l_lane[i] = l_lane[i] * alpha + pv;
-          ph_s[h][lane] = f2h(pv);
+          ph_s[h][lane] = f2w<BF>(pv);
           if (lane == 0) alpha_s[h] = alpha;
           m_run[i] = m_new;
         }
@@ -439,12 +453,12 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
       const int nv2 = (nv + 1) & ~1;
       const int r1 = r0 + TPS < nv2 ? r0 + TPS : nv2;
       for (int r = r0; r < r1; r += 2) {
-        const f16x2 p2 = __builtin_bit_cast(f16x2, *reinterpret_cast<const uint32_t*>(&ph_s[ph][r]));
+        const uint32_t p2 = *reinterpret_cast<const uint32_t*>(&ph_s[ph][r]);
         const uint4 va = *reinterpret_cast<const uint4*>(&vp[r / 2][8 * pc]);
         const uint4 vb = *reinterpret_cast<const uint4*>(&vp[r / 2][8 * pc + 4]);
         const uint32_t v8[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, v8[j]), p2, acc[j], false);
+        for (int j = 0; j < 8; ++j) acc[j] = dot2w<BF>(v8[j], p2, acc[j]);
       }
     }
     __syncthreads();
@@ -471,7 +485,7 @@ __global__ __launch_bounds__(kThreads) void decode_valu_kernel(Params p) {
   auto emit = [&](int h, int d, float v) {  // the split's P V sum of (head h, channel d < D)
     if (d >= D) return;
     if (n == 1)
-      p.out[b * p.o_sb + (kvh * G + h) * p.o_sh + d] = f2h(v / l_s[h]);
+      p.out[b * p.o_sb + (kvh * G + h) * p.o_sh + d] = f2w<BF>(v / l_s[h]);
     else
       p.ws_acc[((row0 + h) * n + split) * D + d] = v;
   };
@@ -504,7 +518,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const float* __rest
                                                              const float* __restrict__ ws_acc,
                                                              int n_splits, int64_t Hq,
                                                              uint16_t* __restrict__ out,
-                                                             int64_t o_sb, int64_t o_sh) {
+                                                             int64_t o_sb, int64_t o_sh, int bf16) {
   const int64_t bh = blockIdx.x;
   const int d = threadIdx.x, D = blockDim.x;
   const float* ml = ws_ml + bh * n_splits * 2;
@@ -520,19 +534,22 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const float* __rest
       o += ws_acc[(bh * n_splits + s) * D + d] * w;
     }
   }
-  out[(bh / Hq) * o_sb + (bh % Hq) * o_sh + d] = f2h(o / L);
+  out[(bh / Hq) * o_sb + (bh % Hq) * o_sh + d] = bf16 ? f2bf(o / L) : f2h(o / L);
 }
 
 int launch_valu(const Params& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv),
                   static_cast<unsigned>(p.B));
   const bool h8 = p.G > 4;
-  const bool s44 = p.mid.fmt == FADE_MID_SYM && p.mid.k_bits == 4 && p.mid.v_bits == 4;
-#define FADE_VALU_LAUNCH(DD)                                                                          \
-  if (h8 && s44) hipLaunchKernelGGL((decode_valu_kernel<DD, 8, true>), grid, dim3(kThreads), 0, st, p);  \
-  else if (h8) hipLaunchKernelGGL((decode_valu_kernel<DD, 8, false>), grid, dim3(kThreads), 0, st, p);   \
-  else if (s44) hipLaunchKernelGGL((decode_valu_kernel<DD, 4, true>), grid, dim3(kThreads), 0, st, p);   \
-  else hipLaunchKernelGGL((decode_valu_kernel<DD, 4, false>), grid, dim3(kThreads), 0, st, p);
+  const bool bf = p.bf16 != 0;
+  const bool s44 = !bf && p.mid.fmt == FADE_MID_SYM && p.mid.k_bits == 4 && p.mid.v_bits == 4;
+#define FADE_VALU_LAUNCH(DD)                                                                                 \
+  if (bf && h8) hipLaunchKernelGGL((decode_valu_kernel<DD, 8, false, true>), grid, dim3(kThreads), 0, st, p);   \
+  else if (bf) hipLaunchKernelGGL((decode_valu_kernel<DD, 4, false, true>), grid, dim3(kThreads), 0, st, p);    \
+  else if (h8 && s44) hipLaunchKernelGGL((decode_valu_kernel<DD, 8, true, false>), grid, dim3(kThreads), 0, st, p); \
+  else if (h8) hipLaunchKernelGGL((decode_valu_kernel<DD, 8, false, false>), grid, dim3(kThreads), 0, st, p);   \
+  else if (s44) hipLaunchKernelGGL((decode_valu_kernel<DD, 4, true, false>), grid, dim3(kThreads), 0, st, p);   \
+  else hipLaunchKernelGGL((decode_valu_kernel<DD, 4, false, false>), grid, dim3(kThreads), 0, st, p);
   // the smallest instance whose capacity covers the head_dim
   if (p.D < 8 || p.D > 256 || p.D % 8 != 0)
     return einval("fade_tiered_decode_attn: head_dim must be a multiple of 8 in [8, 256], got %d", p.D);

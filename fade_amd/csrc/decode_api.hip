@@ -124,6 +124,16 @@ int validate(const fade_decode_args* a) {
     }
   }
   if (a->kernel < 0 || a->kernel > 3) return einval("fade_tiered_decode_attn: kernel must be 0, 1, 2 or 3");
+  if (a->dtype != FADE_DTYPE_F16 && a->dtype != FADE_DTYPE_BF16)
+    return einval("fade_tiered_decode_attn: dtype must be FADE_DTYPE_F16 or FADE_DTYPE_BF16, got %d", a->dtype);
+  if (a->dtype == FADE_DTYPE_BF16) {
+    if (a->kernel == 3)
+      return einval("fade_tiered_decode_attn: bfloat16 runs the INT4 matrix-core kernel or the portable one "
+                    "(kernel 0, 1 or 2), not kernel 3");
+    if (a->mid.len > 0 && a->mid.fmt == FADE_MID_ASYM)
+      return einval("fade_tiered_decode_attn: the asymmetric middle format holds fp16 tensors; bfloat16 calls "
+                    "take FADE_MID_SYM, FADE_MID_K4V2G or FADE_MID_FP16");
+  }
   if (a->rotation != nullptr && a->mid.len > 0) {
     if (a->mid.fmt != FADE_MID_SYM)
       return einval("fade_tiered_decode_attn: a rotation applies to a FADE_MID_SYM middle tier");
@@ -176,6 +186,7 @@ Params to_params(const fade_decode_args* a) {
   p.deterministic = a->deterministic;
   p.passes = static_cast<int>((p.G + 3) / 4);
   p.rot = m.len > 0 ? a->rotation : nullptr;  // no middle tokens: nothing is rotated
+  p.bf16 = a->dtype == FADE_DTYPE_BF16 ? 1 : 0;
   return p;
 }
 
@@ -186,7 +197,7 @@ enum class Kern { kValu, kMfma, kInt4 };
 Kern choose(const fade_decode_args* a, const Params& p) {
   if (a->kernel == 1) return Kern::kValu;
   if (a->kernel != 3 && int4_supports(p)) return Kern::kInt4;
-  if (mfma_supports(p)) return Kern::kMfma;
+  if (!p.bf16 && mfma_supports(p)) return Kern::kMfma;  // the general kernel reads fp16 only
   return Kern::kValu;
 }
 
@@ -280,7 +291,7 @@ int run_plan(const fade_decode_args* a, Params& p, const Plan& pl, uint32_t* cou
   if (pl.k == Kern::kValu && p.n_splits == 1) return 0;  // the portable kernel wrote the output
   const int64_t rows = a->B * a->Hq;
   hipLaunchKernelGGL(decode_combine_kernel, dim3(static_cast<unsigned>(rows)), dim3(static_cast<unsigned>(p.D)), 0, st, p.ws_ml,
-                     p.ws_acc, p.n_splits, a->Hq, static_cast<uint16_t*>(a->out), a->o_sb, a->o_sh);
+                     p.ws_acc, p.n_splits, a->Hq, static_cast<uint16_t*>(a->out), a->o_sb, a->o_sh, p.bf16);
   return check_launch("fade_tiered_decode_attn(combine)");
 }
 

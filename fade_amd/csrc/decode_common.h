@@ -64,6 +64,10 @@ struct Params {
   // splits 1.. the middle tiles (scored with q R^T); the merge returns
   // fp16 part + (middle part) R.  nullptr: no rotation.
   const float* rot;
+  // dtype of every 16-bit float of the call (query, output, fp16-tier K/V, the
+  // symmetric and literal-INT2 formats' scales, an fp16-format middle tier):
+  // 0 fp16, 1 bfloat16.  The asymmetric format's scale and zero are fp16.
+  int bf16;
 };
 
 // Signed symmetric code of channel d in a packed row (fade/quant.py:26-43,
@@ -91,7 +95,7 @@ __device__ __forceinline__ int asym_code_at(const uint8_t* row, int d, int bits)
 
 __global__ void decode_combine_kernel(const float* __restrict__ ws_ml,
                                       const float* __restrict__ ws_acc, int n_splits, int64_t Hq,
-                                      uint16_t* __restrict__ out, int64_t o_sb, int64_t o_sh);
+                                      uint16_t* __restrict__ out, int64_t o_sb, int64_t o_sh, int bf16);
 
 int launch_valu(const Params& p, hipStream_t st);
 // Matrix-core kernel; returns FADE_EINVAL when the middle format is not handled.
@@ -105,6 +109,17 @@ int int4_fp16_tiles(const Params& p);
 int64_t int4_tiles(const Params& p);
 int int4_resident_wgs(const Params& p);  // resident workgroups of the kernel instance for p
 int launch_int4(const Params& p, hipStream_t st);
+// A packed-kernel instance: the kernel, its wavefronts per workgroup, and its
+// slot in the resident-workgroup cache (fp16 instances 0..35, bf16 36..71).
+struct PackedChoice {
+  void (*k)(Params);
+  int waves;
+  int index;
+};
+constexpr int kPackedSlots = 72;
+// The bfloat16 instance for a middle tier int4_supports accepted (reference
+// INT4, rotated 4- or 2-bit, K4 + literal INT2 V; decode_int4_bf16.hip).
+PackedChoice packed_kernel_bf16(const Params& p);
 int mfma_tile();
 // Number of 64-token tiles the matrix-core kernel walks (fp16 tokens, then packed).
 int64_t mfma_tiles(const Params& p);

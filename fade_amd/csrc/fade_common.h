@@ -41,6 +41,24 @@ __device__ __forceinline__ uint16_t f2bf(float x) {
   return static_cast<uint16_t>((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 __device__ __forceinline__ float round_bf16(float x) { return bf2f(f2bf(x)); }
+// Two fp32 values -> a bf16 pair (low half = a), each rounded to nearest even
+// (v_cvt_pk_bf16_f32; for the kernels' internal operands, not stored results).
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+// 16-bit floats of a kernel instance's dtype: bfloat16 when BF, else fp16.
+template <bool BF>
+__device__ __forceinline__ float w2f(uint16_t bits) {
+  if constexpr (BF) return bf2f(bits);
+  else return h2f(bits);
+}
+template <bool BF>
+__device__ __forceinline__ uint16_t f2w(float x) {
+  if constexpr (BF) return f2bf(x);
+  else return f2h(x);
+}
 
 // Float elements of a cache dtype: fp16 as raw uint16_t bits, bf16 as the
 // Bf16 tag, fp32 as float.

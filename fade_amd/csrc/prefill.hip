@@ -56,6 +56,9 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -122,6 +125,26 @@ __device__ __forceinline__ u32x4 to_stored(uint32_t d0, uint32_t d1, uint32_t d2
   return u32x4{__builtin_amdgcn_perm(d2, d0, 0x07060302u), __builtin_amdgcn_perm(d2, d0, 0x05040100u),
                __builtin_amdgcn_perm(d3, d1, 0x07060302u), __builtin_amdgcn_perm(d3, d1, 0x05040100u)};
 }
+// 32x32x16 MFMA on eight 16-bit values per lane of the instance's dtype
+// (BF: bfloat16, else fp16), as bit patterns.
+template <bool BF>
+__device__ __forceinline__ f32x16 mfma32x32(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (BF)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+// Codes of a pair as fp16 72 + c (one dword of nib_to_f16) times two scales
+// (bfloat16 bit patterns, low half first) -> the bf16 pair
+// (bf16(c_lo * s_lo), bf16(c_hi * s_hi)): c * s is exact in fp32 (4-bit code,
+// 8-bit significand), so one rounding, as the reference's bf16 dequantization.
+__device__ __forceinline__ uint32_t dequant_pair_bf16(uint32_t o72, uint32_t s2) {
+  const f16x2 m72 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+  const f16x2 c = __builtin_bit_cast(f16x2, o72) + m72;  // exact
+  return pack_bf16(static_cast<float>(c.x) * __uint_as_float(s2 << 16),
+                   static_cast<float>(c.y) * __uint_as_float(s2 & 0xFFFF0000u));
+}
+
 // Position of key k (0..63) of a tile in a V^T row: bits 2 and 3 exchanged.
 __host__ __device__ constexpr int swap23(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
@@ -135,7 +158,10 @@ __host__ __device__ constexpr int swap23(int k) { return (k & ~12) | ((k & 4) <<
 // NQB query blocks of 32 per workgroup (4 waves each).  With NQB = 2 the two
 // groups of 4 waves split the tile staging: waves 0-3 stage and dequantize K,
 // waves 4-7 V, so each middle tile's dequantization serves 64 queries per head.
-template <int DP, int NQB>
+// BF: q, out, the fp16-layout tiers and the middle tier's scales are bfloat16;
+// middle codes dequantize to bf16(code * scale), the MFMAs take bfloat16
+// operands (the probabilities too), accumulating in fp32.
+template <int DP, int NQB, bool BF>
 __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PParams p) {
   constexpr int D = DP;           // channel capacity of the LDS rows and MFMA tiles
   constexpr int KROW = D / 2;     // staged bytes of one token's packed 4-bit codes
@@ -323,8 +349,9 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
       nib_to_f16(kw[i], o);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        kd[e] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[e]) + m72) *
-                                                 __builtin_bit_cast(f16x2, ksc[4 * i + e]));
+        kd[e] = BF ? dequant_pair_bf16(o[e], ksc[4 * i + e])
+                   : __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[e]) + m72) *
+                                                      __builtin_bit_cast(f16x2, ksc[4 * i + e]));
       if (kstage) *reinterpret_cast<u32x4*>(&kt[buf][mr][32 * mc + 8 * i]) = kd;
     }
     }
@@ -364,7 +391,8 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
         for (int j = 0; j < 4; ++j) {
           const int ra = swap23(8 * half + 2 * j);
           const uint32_t s2 = __builtin_amdgcn_perm(sc[ra + 1], sc[ra], 0x05040100u);
-          vd[j] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[j]) + m72) * __builtin_bit_cast(f16x2, s2));
+          vd[j] = BF ? dequant_pair_bf16(o[j], s2)
+                     : __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[j]) + m72) * __builtin_bit_cast(f16x2, s2));
         }
         if (cu_ok) *reinterpret_cast<u32x4*>(&vtt[buf][ch][16 * wq + 8 * half]) = vd;
       }
@@ -424,7 +452,7 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
   const int n32 = lane & 31, h = lane >> 5;
   const bool active = wq < G && j0 < Sq;
   const int64_t hq = kvh * p.G + h0 + (active ? wq : 0);
-  f16x8 qf[NKS];
+  u32x4 qf[NKS];
   {
     const int j = j0 + n32;
     const uint16_t* qr = p.q + b * p.q_sb + hq * p.q_sh + static_cast<int64_t>(j < Sq ? j : Sq - 1) * p.q_ss;
@@ -432,7 +460,7 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
     for (int ks = 0; ks < NKS; ++ks) {
       const uint4 w = (active && j < Sq && 16 * ks + 8 * h < Dr) ? *reinterpret_cast<const uint4*>(qr + 16 * ks + 8 * h)
                                                                 : make_uint4(0, 0, 0, 0);
-      qf[ks] = __builtin_bit_cast(f16x8, to_stored(w.x, w.y, w.z, w.w));
+      qf[ks] = to_stored(w.x, w.y, w.z, w.w);
     }
   }
 
@@ -457,8 +485,8 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
       for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(&kt[buf][32 * kb + n32][16 * ks + 8 * h]);
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], s[kb], 0, 0, 0);
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&kt[buf][32 * kb + n32][16 * ks + 8 * h]);
+        s[kb] = mfma32x32<BF>(a, qf[ks], s[kb]);
       }
     }
     // bottom-right: every key of a full cache tile is visible to every query of
@@ -479,27 +507,52 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
           if (32 * kb + 8 * (i >> 2) + 4 * h + (i & 3) >= lim) s[kb][i] = -INFINITY;
     }
     // probabilities exp2((x - m) * scale) against the running max m (raw score
-    // units), as fp16: PV A operands, k-step s = registers 8 (s & 1) .. + 7 of
-    // key block s >> 1
-    f16x8 pa[4];
+    // units), as fp16 (bfloat16 in a BF instance): PV A operands, k-step s =
+    // registers 8 (s & 1) .. + 7 of key block s >> 1
+    u32x4 pa[4];
     auto probs = [&]() {
       const float nm = -m_run * sl2;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
+        for (int hf = 0; hf < 2; ++hf) {
+          if constexpr (BF) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-            pa[2 * kb + hf][j] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + j], sl2, nm)));
+            for (int j = 0; j < 4; ++j)
+              pa[2 * kb + hf][j] = pack_bf16(__builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + 2 * j], sl2, nm)),
+                                             __builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + 2 * j + 1], sl2, nm)));
+          } else {
+            f16x8 ph;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ph[j] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + j], sl2, nm)));
+            pa[2 * kb + hf] = __builtin_bit_cast(u32x4, ph);
+          }
+        }
     };
     probs();
     // The running max moves only when a score exceeds it by more than kTau
     // (log2 units), i.e. when a probability exceeds 2^kTau (inf included): a
-    // packed fp16 max over the probabilities finds those tiles; the exact fp32
-    // max is taken on them alone.
-    f16x8 pm = __builtin_elementwise_max(__builtin_elementwise_max(pa[0], pa[1]), __builtin_elementwise_max(pa[2], pa[3]));
-    f16x2 pm2 = __builtin_elementwise_max(__builtin_elementwise_max(pm.s01, pm.s23), __builtin_elementwise_max(pm.s45, pm.s67));
-    if (__builtin_amdgcn_ballot_w64(static_cast<float>(pm2.x) > kTauP || static_cast<float>(pm2.y) > kTauP) != 0) {
+    // packed max over the probabilities finds those tiles (fp16; bfloat16 as
+    // unsigned 16-bit patterns, which order like the non-negative values);
+    // the exact fp32 max is taken on them alone.
+    bool over;
+    if constexpr (BF) {
+      const u16x8 pm = __builtin_elementwise_max(
+          __builtin_elementwise_max(__builtin_bit_cast(u16x8, pa[0]), __builtin_bit_cast(u16x8, pa[1])),
+          __builtin_elementwise_max(__builtin_bit_cast(u16x8, pa[2]), __builtin_bit_cast(u16x8, pa[3])));
+      uint16_t mx = pm[0];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) mx = mx > pm[j] ? mx : pm[j];
+      over = mx > 0x4380u;  // bfloat16 2^8
+    } else {
+      const f16x8 pm = __builtin_elementwise_max(
+          __builtin_elementwise_max(__builtin_bit_cast(f16x8, pa[0]), __builtin_bit_cast(f16x8, pa[1])),
+          __builtin_elementwise_max(__builtin_bit_cast(f16x8, pa[2]), __builtin_bit_cast(f16x8, pa[3])));
+      const f16x2 pm2 =
+          __builtin_elementwise_max(__builtin_elementwise_max(pm.s01, pm.s23), __builtin_elementwise_max(pm.s45, pm.s67));
+      over = static_cast<float>(pm2.x) > kTauP || static_cast<float>(pm2.y) > kTauP;
+    }
+    if (__builtin_amdgcn_ballot_w64(over) != 0) {
       float lmax = kNegBig;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -523,17 +576,22 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
       }
       probs();
     }
-    // the row sum of the same fp16 probabilities PV multiplies: fp32 dot products with 1
+    // the row sum of the same 16-bit probabilities PV multiplies: fp32 dot products with 1
     {
-      const f16x2 one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
       float ps = 0.0f;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const u32x4 w = __builtin_bit_cast(u32x4, pa[k]);
+        const u32x4 w = pa[k];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const uint32_t we = w[e];
-          ps = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, we), one, ps, false);
+          if constexpr (BF) {
+            const bf16x2 one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+            ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, we), one, ps, false);
+          } else {
+            const f16x2 one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+            ps = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, we), one, ps, false);
+          }
         }
       }
       l_run += ps;
@@ -544,8 +602,8 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
     for (int ks2 = 0; ks2 < 4; ++ks2)
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb) {
-        const f16x8 bv = *reinterpret_cast<const f16x8*>(&vtt[buf][32 * cb + n32][16 * ks2 + 8 * h]);
-        acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[ks2], bv, acc[cb], 0, 0, 0);
+        const u32x4 bv = *reinterpret_cast<const u32x4*>(&vtt[buf][32 * cb + n32][16 * ks2 + 8 * h]);
+        acc[cb] = mfma32x32<BF>(pa[ks2], bv, acc[cb]);
       }
   };
 
@@ -577,7 +635,7 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
           uint16_t* orow = p.out + b * p.o_sb + hq * p.o_sh + static_cast<int64_t>(j) * p.o_ss;
 #pragma unroll
           for (int cb = 0; cb < NCB; ++cb)
-            if (32 * cb + n32 < Dr) orow[32 * cb + n32] = f2h(acc[cb][4 * q + i] * inv4[i]);
+            if (32 * cb + n32 < Dr) orow[32 * cb + n32] = f2w<BF>(acc[cb][4 * q + i] * inv4[i]);
         }
       }
     }
@@ -621,6 +679,8 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
     return einval("fade_tiered_prefill_attn: null q, out or lens");
   if (!aligned16(a->q) || (a->q_sb | a->q_sh | a->q_ss) % 8)
     return einval("fade_tiered_prefill_attn: q rows must be 16-byte aligned");
+  if (a->dtype != FADE_DTYPE_F16 && a->dtype != FADE_DTYPE_BF16)
+    return einval("fade_tiered_prefill_attn: dtype must be FADE_DTYPE_F16 or FADE_DTYPE_BF16, got %d", a->dtype);
   if (a->mask_mode != FADE_MASK_BOTTOM_RIGHT && a->mask_mode != FADE_MASK_TOP_LEFT && a->mask_mode != FADE_MASK_NONE)
     return einval("fade_tiered_prefill_attn: unknown mask_mode %d", a->mask_mode);
   if (a->mask_mode == FADE_MASK_BOTTOM_RIGHT && a->chunk.len != a->Sq)
@@ -682,9 +742,12 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   const int nqb = a->Sq > kQB ? 2 : 1;
   const dim3 grid(static_cast<unsigned>(cdiv(a->Sq, kQB * nqb) * p.passes), static_cast<unsigned>(a->Hkv),
                   static_cast<unsigned>(a->B));
-#define FADE_PREFILL_LAUNCH(DD)                                                                               \
-  if (nqb == 2) hipLaunchKernelGGL((prefill_kernel<DD, 2>), grid, dim3(2 * kThreads), 0, as_stream(stream), p); \
-  else hipLaunchKernelGGL((prefill_kernel<DD, 1>), grid, dim3(kThreads), 0, as_stream(stream), p);
+  const bool bf = a->dtype == FADE_DTYPE_BF16;
+#define FADE_PREFILL_LAUNCH(DD)                                                                                        \
+  if (bf && nqb == 2) hipLaunchKernelGGL((prefill_kernel<DD, 2, true>), grid, dim3(2 * kThreads), 0, as_stream(stream), p); \
+  else if (bf) hipLaunchKernelGGL((prefill_kernel<DD, 1, true>), grid, dim3(kThreads), 0, as_stream(stream), p);           \
+  else if (nqb == 2) hipLaunchKernelGGL((prefill_kernel<DD, 2, false>), grid, dim3(2 * kThreads), 0, as_stream(stream), p); \
+  else hipLaunchKernelGGL((prefill_kernel<DD, 1, false>), grid, dim3(kThreads), 0, as_stream(stream), p);
   // the smallest instance whose capacity covers the head_dim
   if (a->D <= 32) { FADE_PREFILL_LAUNCH(32) }
   else if (a->D <= 64) { FADE_PREFILL_LAUNCH(64) }

@@ -17,7 +17,7 @@ import torch
 from torch import Tensor
 
 from .. import _lib
-from .tiered_attn import MiddleTier, _fp16_tier, _mid_tier
+from .tiered_attn import MiddleTier, _attn_dtype, _fp16_tier, _mid_tier
 
 _MASKS = {"bottom_right": _lib.MASK_BOTTOM_RIGHT, "top_left": _lib.MASK_TOP_LEFT, "none": _lib.MASK_NONE}
 
@@ -26,7 +26,8 @@ class TieredPrefillPlan:
     """Validated launch for fixed tensors; ``run()`` enqueues one kernel.
 
     Args:
-        q: [B, Hq, Sq, D] fp16 queries of the chunk; D a multiple of 8 up to 128.
+        q: [B, Hq, Sq, D] fp16 or bf16 queries of the chunk; D a multiple of 8 up to 128.
+            Every other 16-bit tensor (tiers, scales, the output) is of q's dtype.
         chunk: (K, V) [B, Hkv, Sq, D] fp16, the chunk's own keys/values
             (with ``mask`` ``"top_left"`` / ``"none"``: any length, or None).
         sink, recent: (K, V) [B, Hkv, cap, D] fp16 padded along S, or None.
@@ -64,7 +65,7 @@ class TieredPrefillPlan:
         tensors = [q] + ([*chunk] if chunk else []) + ([*sink] if sink else []) + ([*recent] if recent else []) \
             + (mid.tensors() if mid else [])
         _lib.require_gpu(*tensors, op="tiered_prefill_attention")
-        _lib.require_f16(q, "tiered_prefill_attention")
+        dtc = _attn_dtype(q, "tiered_prefill_attention")
         B, Hq, Sq, D = q.shape
         ref = chunk[0] if chunk else (sink[0] if sink else (recent[0] if recent else (mid.k_codes if mid else None)))
         if ref is None:
@@ -84,10 +85,10 @@ class TieredPrefillPlan:
                 raise ValueError("a paged INT4 middle tier needs head_dim % 32 == 0 in the prefill kernel")
             from ..quant import dequant_int4
 
-            mid = MiddleTier("fp16", dequant_int4(mid.k_codes, mid.k_scale), dequant_int4(mid.v_codes, mid.v_scale),
-                             length=mid.length)
-        if mid is not None and mid.fmt == "fp16" and (mid.k_codes.dtype != torch.float16 or mid.k_codes.shape[-1] != D):
-            raise ValueError("an fp16 middle tier holds float16 rows [B, Hkv, S, D]")
+            mid = MiddleTier("fp16", dequant_int4(mid.k_codes, mid.k_scale, dtype=q.dtype),
+                             dequant_int4(mid.v_codes, mid.v_scale, dtype=q.dtype), length=mid.length)
+        if mid is not None and mid.fmt == "fp16" and (mid.k_codes.dtype != q.dtype or mid.k_codes.shape[-1] != D):
+            raise ValueError(f"an fp16-layout middle tier holds {q.dtype} rows [B, Hkv, S, D] (the query's dtype)")
         if q.stride(-1) != 1:
             q = q.contiguous()
         caps = [int(sink[0].shape[2]) if sink else 0, mid.n_tokens if mid else 0, int(recent[0].shape[2]) if recent else 0]
@@ -99,7 +100,9 @@ class TieredPrefillPlan:
         if order is not None:
             order = order.to(device=q.device, dtype=torch.int32).contiguous()
         if out is None:
-            out = torch.empty(B, Hq, Sq, D, dtype=torch.float16, device=q.device)
+            out = torch.empty(B, Hq, Sq, D, dtype=q.dtype, device=q.device)
+        if out.dtype != q.dtype:
+            raise ValueError(f"out must be {q.dtype} (the query's dtype), got {out.dtype}")
         self._keep = (q, chunk, sink, mid, recent, lens, order, out)
         a = _lib.PrefillArgs()
         a.B, a.Hq, a.Hkv, a.D, a.Sq = B, Hq, Hkv, D, Sq
@@ -108,8 +111,11 @@ class TieredPrefillPlan:
         a.sm_scale = float(1.0 / math.sqrt(D) if sm_scale is None else sm_scale)
         a.lens = lens.data_ptr()
         a.order = order.data_ptr() if order is not None else None
-        a.sink, a.mid, a.recent, a.chunk = _fp16_tier(sink), _mid_tier(mid), _fp16_tier(recent), _fp16_tier(chunk)
+        dt = q.dtype
+        a.sink, a.mid = _fp16_tier(sink, dt), _mid_tier(mid, dt)
+        a.recent, a.chunk = _fp16_tier(recent, dt), _fp16_tier(chunk, dt)
         a.mask_mode = _MASKS[mask]
+        a.dtype = dtc
         self.args = a
         self.out = out
         self._fn = _lib.load().fade_tiered_prefill_attn
@@ -123,7 +129,7 @@ class TieredPrefillPlan:
 
 def tiered_prefill_attention(q, chunk, sink=None, mid=None, recent=None, lens=None, order=None, sm_scale=None,
                              mask: str = "bottom_right") -> Tensor:
-    """Causal attention of a chunk over each row's tiered cache; returns fp16 [B, Hq, Sq, D]."""
+    """Causal attention of a chunk over each row's tiered cache; returns [B, Hq, Sq, D] of q's dtype."""
     return TieredPrefillPlan(q, chunk, sink, mid, recent, lens, order, sm_scale, mask=mask).run()
 
 

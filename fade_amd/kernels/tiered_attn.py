@@ -70,13 +70,26 @@ class MiddleTier:
                             self.pages) if t is not None]
 
 
-def _fp16_tier(kv: tuple[Tensor, Tensor] | None) -> _lib.Fp16Tier:
+# dtype codes of the attention kernels (FADE_DTYPE_F16 / FADE_DTYPE_BF16): every
+# 16-bit float of a call (query, output, fp16-layout tiers, the symmetric and
+# literal-INT2 scales) is of the query's dtype, as the reference's cache keeps
+# every tier and scale in the model's dtype (fade/cache.py:124-160).
+_ATTN_DTYPES = {torch.float16: 0, torch.bfloat16: 1}
+
+
+def _attn_dtype(q: Tensor, op: str) -> int:
+    if q.dtype not in _ATTN_DTYPES:
+        raise ValueError(f"{op}: expected a float16 or bfloat16 query, got {q.dtype}")
+    return _ATTN_DTYPES[q.dtype]
+
+
+def _fp16_tier(kv: tuple[Tensor, Tensor] | None, dtype: torch.dtype = torch.float16) -> _lib.Fp16Tier:
     t = _lib.Fp16Tier()
     if kv is None or kv[0] is None or kv[0].shape[2] == 0:
         return t
     k, v = kv
-    if k.dtype != torch.float16 or v.dtype != torch.float16:
-        raise ValueError("sink/recent tiers must be float16")
+    if k.dtype != dtype or v.dtype != dtype:
+        raise ValueError(f"sink/recent tiers must be {dtype} (the query's dtype), got {k.dtype}/{v.dtype}")
     if k.stride(-1) != 1 or v.stride(-1) != 1:
         raise ValueError("sink/recent tiers need a contiguous head_dim axis")
     t.k, t.v, t.len = k.data_ptr(), v.data_ptr(), int(k.shape[2])
@@ -85,13 +98,25 @@ def _fp16_tier(kv: tuple[Tensor, Tensor] | None) -> _lib.Fp16Tier:
     return t
 
 
-def _mid_tier(mid: MiddleTier | None) -> _lib.MidTier:
+def _mid_tier(mid: MiddleTier | None, dtype: torch.dtype = torch.float16) -> _lib.MidTier:
     m = _lib.MidTier()
     if mid is None or mid.n_tokens == 0:
         m.fmt = _lib.MID_NONE
         return m
     if mid.fmt not in _FMT:
         raise ValueError(f"unknown middle format {mid.fmt!r}")
+    if mid.fmt == "asym":
+        if dtype != torch.float16:
+            raise ValueError("the asymmetric middle format holds fp16 tensors; it pairs with float16 queries")
+        want = [mid.k_scale, mid.v_scale, mid.k_zero, mid.v_zero]
+    elif mid.fmt == "fp16":
+        want = [mid.k_codes, mid.v_codes]
+    else:
+        want = [mid.k_scale, mid.v_scale]
+    for t in want:
+        if t is not None and t.dtype != (torch.float16 if mid.fmt == "asym" else dtype):
+            raise ValueError(f"middle tier ({mid.fmt}): scales / rows must be "
+                             f"{torch.float16 if mid.fmt == 'asym' else dtype}, got {t.dtype}")
     for t in mid.tensors():
         if not t.is_contiguous() and not mid.page_stride:
             raise ValueError("middle-tier tensors must be contiguous")
@@ -223,7 +248,7 @@ class TieredDecodePlan:
             lens = lens.to(device=q.device, dtype=torch.int32).contiguous()
         tensors = [q] + ([*sink] if sink else []) + ([*recent] if recent else []) + (mid.tensors() if mid else [])
         _lib.require_gpu(*tensors, op="tiered_decode_attention")
-        _lib.require_f16(q, "tiered_decode_attention")
+        dtc = _attn_dtype(q, "tiered_decode_attention")
         B, Hq, _, D = q.shape
         ref = sink[0] if sink else (recent[0] if recent else mid.k_codes)
         Hkv = int(ref.shape[1])
@@ -236,14 +261,17 @@ class TieredDecodePlan:
                 raise ValueError(f"rotation must be float32 [{D}, {D}] on {q.device}")
             rotation = rotation.contiguous()
         if out is None:
-            out = torch.empty(B, Hq, 1, D, dtype=torch.float16, device=q.device)
+            out = torch.empty(B, Hq, 1, D, dtype=q.dtype, device=q.device)
+        if out.dtype != q.dtype:
+            raise ValueError(f"out must be {q.dtype} (the query's dtype), got {out.dtype}")
         self._keep = (q, sink, mid, recent, out, lens, rotation)
         a = _lib.DecodeArgs()
         a.B, a.Hq, a.Hkv, a.D = B, Hq, Hkv, D
         a.q, a.q_sb, a.q_sh = q.data_ptr(), q.stride(0), q.stride(1)
         a.out, a.o_sb, a.o_sh = out.data_ptr(), out.stride(0), out.stride(1)
         a.sm_scale = float(1.0 / math.sqrt(D) if sm_scale is None else sm_scale)
-        a.sink, a.mid, a.recent = _fp16_tier(sink), _mid_tier(mid), _fp16_tier(recent)
+        a.sink, a.mid, a.recent = _fp16_tier(sink, q.dtype), _mid_tier(mid, q.dtype), _fp16_tier(recent, q.dtype)
+        a.dtype = dtc
         a.n_splits, a.kernel = int(n_splits), int(kernel)
         a.lens = _lib.ptr(lens)
         if deterministic is None:
@@ -311,7 +339,11 @@ def tiered_decode_attention(
     deterministic: bool | None = None,
     rotation: Tensor | None = None,
 ) -> Tensor:
-    """Decode attention of ``q`` [B,Hq,1,D] over the tiered cache; returns fp16 [B,Hq,1,D].
+    """Decode attention of ``q`` [B,Hq,1,D] over the tiered cache; returns [B,Hq,1,D] of q's dtype.
+
+    ``q`` is float16 or bfloat16, and so are the sink / recent tiers and the
+    symmetric formats' scales (the reference's cache keeps everything in the
+    model's dtype); the asymmetric format's scale / zero are float16.
 
     Query head ``h`` attends to KV head ``h // (Hq // Hkv)`` (the reference's
     ``repeat_interleave`` GQA mapping, fade/kernels/fused_int4_attn.py:306-312).

@@ -43,8 +43,8 @@ def create_tiered_cache(model, dtype: torch.dtype = torch.float16, config: FadeC
     cache = TieredKVCache(dtype=dtype, rope_theta=scheme.theta, head_dim=head_dim, rope_scheme=scheme, **kw)
     # attn_implementation="fade": attention reads the tiers in place (no materialized K/V)
     cache.fused = uses_fade_attention(model)
-    if cache.fused and dtype != torch.float16:
-        raise ValueError(f'attn_implementation="fade" reads float16 caches; got dtype={dtype}')
+    if cache.fused and dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f'attn_implementation="fade" reads float16 and bfloat16 caches; got dtype={dtype}')
     layer_types = getattr(text_cfg, "layer_types", None)
     if layer_types is not None:
         skip = {i for i, t in enumerate(layer_types) if t not in ("full_attention", "sliding_attention")}

@@ -33,7 +33,7 @@ extern "C" {
 #define FADE_ERUNTIME (-1)
 #define FADE_EINVAL (-22)
 
-#define FADE_ABI_VERSION 1
+#define FADE_ABI_VERSION 2  /* 2: fade_decode_args and fade_prefill_args end with dtype */
 
 /* Quantization axes. */
 #define FADE_AXIS_CHANNEL 0 /* one scale per (b, h, d): reduce over S (K)  */
@@ -346,6 +346,13 @@ typedef struct fade_decode_args {
                                   values summed in the rotated basis; the result is the fp16
                                   tiers' part + (middle part) R.  Needs the matrix-core INT4
                                   kernel.  NULL: no rotation. */
+  int32_t dtype;               /* FADE_DTYPE_F16 (0, zero-initialized arguments) or
+                                  FADE_DTYPE_BF16: the type of q, out, the sink / recent K/V,
+                                  an fp16-format middle tier and the FADE_MID_SYM /
+                                  FADE_MID_K4V2G scales (the reference's cache keeps every
+                                  tier and scale in the model's dtype).  FADE_MID_ASYM (fp16
+                                  scale / zero by format) takes FADE_DTYPE_F16 only;
+                                  bfloat16 runs kernel 0, 1 or 2. */
 } fade_decode_args;
 
 /* Replaces dequantize + torch.cat (fade/cache.py:683-842) + SDPA and the
@@ -403,6 +410,9 @@ typedef struct fade_prefill_args {
   fade_fp16_tier recent;
   fade_fp16_tier chunk; /* the chunk's own K/V, len = Sq (other masks: any length) */
   int32_t mask_mode;    /* FADE_MASK_*; 0 (zero-initialized arguments) = bottom-right */
+  int32_t dtype;        /* FADE_DTYPE_F16 (0) or FADE_DTYPE_BF16: q, out, the fp16-layout tiers
+                           (sink, recent, chunk, an fp16-format middle) and the packed middle
+                           tier's scales; middle codes dequantize to dtype(code * scale) */
 } fade_prefill_args;
 
 int fade_tiered_prefill_attn(const fade_prefill_args* args, void* stream);

@@ -52,8 +52,20 @@ def bottom_right_causal_mask(sq: int, sk: int) -> np.ndarray:
     return t <= (sk - sq + j)
 
 
+def _vals(x, dtype: str) -> np.ndarray:
+    """Values of an fp16 / fp32 array, or of bf16 bit patterns (uint16) when ``dtype`` is "bf16"."""
+    return oq.to_f32(x, "bf16") if dtype == "bf16" else np.asarray(x)
+
+
 def dequant_middle(mid: dict) -> tuple[np.ndarray, np.ndarray]:
     """Dequantize a middle tier described by a dict (format key ``fmt``).
+
+    ``mid["dtype"]`` ("f16", default, or "bf16") is the cache dtype: scales and
+    fp16-layout rows are then bf16 bit patterns, and the dequantization rounds
+    to bf16 as the reference does at that dtype (``q.to(dtype) *
+    scale.to(dtype)``, fade/quant.py:124-127,170-176; the rotated formats'
+    ``(x_rot.float() @ R).to(dtype)`` of its CPU path, fade/rotated_quant.py:142-145,184-187).
+    The result is fp32 values (or fp16 for "f16").
 
     Formats:
       ``int4``      reference INT4: per-channel K scale, per-token V scale
@@ -66,6 +78,9 @@ def dequant_middle(mid: dict) -> tuple[np.ndarray, np.ndarray]:
       ``fp16``      plain fp16 middle (the flash-decode comparator)
     """
     fmt = mid["fmt"]
+    dt = mid.get("dtype", "f16")
+    if dt == "bf16":
+        return _dequant_middle_bf16(mid)
     if fmt == "fp16":
         return np.asarray(mid["k"]), np.asarray(mid["v"])
     if fmt == "int4":
@@ -87,27 +102,54 @@ def dequant_middle(mid: dict) -> tuple[np.ndarray, np.ndarray]:
     raise ValueError(f"unknown middle format {fmt!r}")
 
 
-def materialize(sink_k, sink_v, mid: dict | None, recent_k, recent_v):
-    """fade/cache.py:693-699: cat(sink, middle, recent) along S."""
+def _dequant_middle_bf16(mid: dict) -> tuple[np.ndarray, np.ndarray]:
+    """``dequant_middle`` of a bfloat16 cache (scales and rows as bf16 bit patterns)."""
+    fmt = mid["fmt"]
+    b = lambda x: oq.to_f32(x, "bf16")  # noqa: E731
+    if fmt == "fp16":
+        return b(mid["k"]), b(mid["v"])
+    if fmt == "int4":
+        return b(oq.dequant_int4_typed(mid["kq"], mid["ks"], "bf16")), b(oq.dequant_int4_typed(mid["vq"], mid["vs"], "bf16"))
+    if fmt == "k4v2":
+        k = b(oq.dequant_int4_typed(mid["kq"], mid["ks"], "bf16"))
+        v = b(oq.dequant_int2_typed(mid["vq"], mid["vs"], "bf16", mid.get("group", 64)))
+        return k, v[..., : k.shape[-2], :]
+    if fmt == "rot":
+        R = np.asarray(mid["R"], dtype=F32)
+        out = []
+        for qk, sk, bits in ((mid["kq"], mid["ks"], mid["k_bits"]), (mid["vq"], mid["vs"], mid["v_bits"])):
+            xr = b(oq.rotated_dequant_rot(qk, sk, bits, "bf16"))
+            out.append(b(oq.from_f32((xr.astype(np.float64) @ R.astype(np.float64)).astype(F32), "bf16")))
+        return out[0], out[1]
+    raise ValueError(f"middle format {fmt!r} has no bfloat16 form")
+
+
+def materialize(sink_k, sink_v, mid: dict | None, recent_k, recent_v, dtype: str = "f16"):
+    """fade/cache.py:693-699: cat(sink, middle, recent) along S.  ``dtype`` "bf16":
+    the sink / recent arrays are bf16 bit patterns (and ``mid["dtype"]`` should be "bf16")."""
     ks, vs = [], []
     if sink_k is not None and sink_k.shape[-2] > 0:
-        ks.append(np.asarray(sink_k))
-        vs.append(np.asarray(sink_v))
+        ks.append(_vals(sink_k, dtype))
+        vs.append(_vals(sink_v, dtype))
     if mid is not None:
         mk, mv = dequant_middle(mid)
         if mk.shape[-2] > 0:
             ks.append(mk)
             vs.append(mv)
     if recent_k is not None and recent_k.shape[-2] > 0:
-        ks.append(np.asarray(recent_k))
-        vs.append(np.asarray(recent_v))
+        ks.append(_vals(recent_k, dtype))
+        vs.append(_vals(recent_v, dtype))
+    if dtype == "bf16":
+        ks = [np.asarray(x, dtype=F32) for x in ks]
+        vs = [np.asarray(x, dtype=F32) for x in vs]
     return np.concatenate(ks, axis=-2), np.concatenate(vs, axis=-2)
 
 
-def tiered_decode(q, sink_k, sink_v, mid, recent_k, recent_v):
-    """Single-token decode over the tiered cache: fp32 SDPA of the materialized K/V."""
-    k, v = materialize(sink_k, sink_v, mid, recent_k, recent_v)
-    return sdpa_fp32(q, k, v)
+def tiered_decode(q, sink_k, sink_v, mid, recent_k, recent_v, dtype: str = "f16"):
+    """Single-token decode over the tiered cache: fp32 SDPA of the materialized K/V.
+    ``dtype`` "bf16": q, sink and recent are bf16 bit patterns (the cache's dtype)."""
+    k, v = materialize(sink_k, sink_v, mid, recent_k, recent_v, dtype)
+    return sdpa_fp32(_vals(q, dtype), k, v)
 
 
 def ragged_prefill(q_chunks, k_full_list, v_full_list):

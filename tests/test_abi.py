@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(_lib.LIB_PATH)
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.fade_hip_abi_version() == 1
+    assert lib.fade_hip_abi_version() == 2
 
 
 def _elf_sections(data: bytes):

@@ -1,6 +1,6 @@
 """Host-side model of the packed decode kernel's tile pipeline (CPU only).
 
-``decode_packed_kernel`` (fade_amd/csrc/decode_int4.hip) streams tiles into NS
+``decode_packed_kernel`` (fade_amd/csrc/decode_packed.h) streams tiles into NS
 LDS ring stages per wave with direct-to-LDS loads that the compiler does not
 track, and waits for them with its own ``s_waitcnt vmcnt(c)``: c is the number
 of loads issued after the ones the next stage read needs.  The counts are

@@ -148,7 +148,7 @@ def test_fade_attention_registration_and_fused_update():
     assert rk is k and rv is v
     assert cache.get_seq_length(0) == 5
     assert active_cache() is cache
-    # the fused kernels read float16 tiers: a bf16 cache refuses fused mode
+    # the fused kernels read float16 and bfloat16 tiers: a float32 cache refuses fused mode
     from transformers import AutoConfig
 
     from fade_amd import create_tiered_cache
@@ -157,14 +157,19 @@ def test_fade_attention_registration_and_fused_update():
                                num_hidden_layers=2, intermediate_size=512, vocab_size=100)
     cfg._attn_implementation = "fade"
     model = types.SimpleNamespace(config=cfg)
-    with pytest.raises(ValueError, match="reads float16 caches"):
-        create_tiered_cache(model, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="reads float16 and bfloat16 caches"):
+        create_tiered_cache(model, dtype=torch.float32)
     assert create_tiered_cache(model).fused
-    c16 = TieredKVCache(dtype=torch.bfloat16)
-    c16.fused = True
-    with pytest.raises(NotImplementedError, match="float16"):
-        c16.update(k.bfloat16(), v.bfloat16(), 0)
-    assert c16.get_seq_length(0) == 0 and c16.batch_size is None  # refused before any state changes
+    assert create_tiered_cache(model, dtype=torch.bfloat16).fused
+    c32 = TieredKVCache(dtype=torch.float32)
+    c32.fused = True
+    with pytest.raises(NotImplementedError, match="bfloat16"):
+        c32.update(k.float(), v.float(), 0)
+    assert c32.get_seq_length(0) == 0 and c32.batch_size is None  # refused before any state changes
+    cb = TieredKVCache(dtype=torch.bfloat16)
+    cb.fused = True
+    rk, _ = cb.update(k.bfloat16(), v.bfloat16(), 0)
+    assert rk.dtype == torch.bfloat16 and cb.get_seq_length(0) == 5
 
 
 def test_paginate_middle_pools_pages_on_host():

@@ -22,7 +22,7 @@ import pytest
 
 HIPCC = "/opt/rocm/bin/hipcc"
 CSRC = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "fade_amd", "csrc")
-SOURCES = ("decode_int4.hip", "decode_mfma.hip", "prefill.hip")
+SOURCES = ("decode_int4.hip", "decode_int4_bf16.hip", "decode_mfma.hip", "prefill.hip")
 FLAGS = ["--offload-arch=gfx950", "--cuda-device-only", "-S", "-O3", "-std=c++17", "-Xclang", "-target-feature",
          "-Xclang", "-packed-fp32-ops", "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-fast-math",
          "-Wno-inline-asm", "-I", CSRC]

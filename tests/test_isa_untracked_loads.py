@@ -32,12 +32,13 @@ def _regs(line: str) -> set[int]:
     return out
 
 
-def test_rotated_prologue_registers_untouched_until_the_wait(tmp_path):
-    out = tmp_path / "decode_int4.s"
+@pytest.mark.parametrize("source", ["decode_int4.hip", "decode_int4_bf16.hip"])  # fp16 and bf16 instances
+def test_rotated_prologue_registers_untouched_until_the_wait(tmp_path, source):
+    out = tmp_path / (source[:-4] + ".s")
     cmd = [HIPCC, "--offload-arch=gfx950", "--cuda-device-only", "-S", "-O3", "-std=c++17",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
            "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-fast-math", "-Wno-inline-asm",
-           "-I", CSRC, os.path.join(CSRC, "decode_int4.hip"), "-o", str(out)]
+           "-I", CSRC, os.path.join(CSRC, source), "-o", str(out)]
     subprocess.run(cmd, check=True, capture_output=True, timeout=600)
     lines = out.read_text().split("\n")
     starts = [i for i, l in enumerate(lines)

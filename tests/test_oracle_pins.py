@@ -472,3 +472,52 @@ def test_sdpa_uniform_keys_average_values_and_causal_mask():
     q2 = rng.standard_normal((1, 1, 2, 4))
     out = oatt.sdpa_fp32(q2, k, v, mask=m)
     assert np.allclose(out[0, 0, 0], v[0, 0, :5].mean(0), atol=1e-6)
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_bf16_rotated_middle_matches_torch_cpu_sequence(bits):
+    """The oracle's bfloat16 rotated middle tier against torch running the
+    reference's CPU sequence on bf16 tensors (fade/rotated_quant.py:134-145):
+    ``(q.to(bf16) * scale.to(bf16)).to(float32) @ R.float()``, then ``.to(bf16)``.
+    The fp32 product's summation order is torch's own, so results agree to one
+    bf16 rounding step: equal bits, or neighbours where the fp32 value sits on
+    a rounding boundary."""
+    rng = np.random.default_rng(21 + bits)
+    B, H, S, D = 2, 2, 9, 128
+    qmin, qmax = oq.BIT_PARAMS[bits]
+    q = rng.integers(qmin, qmax + 1, size=(B, H, S, D)).astype(np.int8)
+    s = oq.f32_to_bf16(rng.uniform(0.05, 2.0, (B, H, S, 1)).astype(np.float32))
+    R = np.load(f"{__import__('os').path.dirname(__file__)}/golden/rotation_d128_seed42.npy")
+    packed = oq.pack_bits(q, bits)
+    mid = {"fmt": "rot", "dtype": "bf16", "R": R, "k_bits": bits, "v_bits": bits,
+           "kq": packed, "ks": s, "vq": packed, "vs": s}
+    k, v = oatt.dequant_middle(mid)
+    ref = ((torch.from_numpy(q).to(torch.bfloat16) * _t_bf16(s)).to(torch.float32) @ torch.from_numpy(R)).to(torch.bfloat16)
+    rb = _bits_bf16(ref).astype(np.int32)
+    gb = oq.f32_to_bf16(k).astype(np.int32)
+    assert np.array_equal(k, v)
+    assert np.abs(rb - gb).max() <= 1 and (rb != gb).mean() < 0.01
+
+
+def test_bf16_tiered_decode_matches_torch_materialized_sdpa():
+    """oatt.tiered_decode with dtype "bf16" (q, sink, recent and the INT4 middle's
+    scales as bf16 bits) against torch: the reference INT4 dequantization on bf16
+    tensors, torch.cat of the tiers, GQA repeat_interleave and float64 softmax
+    attention (fade/cache.py:693-699, fade/kernels/fused_int4_attn.py:306-312)."""
+    rng = np.random.default_rng(31)
+    B, Hq, Hkv, D, ns, nm, nr = 2, 8, 2, 32, 3, 40, 5
+    bf = lambda *shape: oq.f32_to_bf16(rng.standard_normal(shape).astype(np.float32))  # noqa: E731
+    q, sk, sv, rk, rv = bf(B, Hq, 1, D), bf(B, Hkv, ns, D), bf(B, Hkv, ns, D), bf(B, Hkv, nr, D), bf(B, Hkv, nr, D)
+    kq = rng.integers(0, 256, (B, Hkv, nm, D // 2), dtype=np.uint8)
+    vq = rng.integers(0, 256, (B, Hkv, nm, D // 2), dtype=np.uint8)
+    ks = oq.f32_to_bf16(rng.uniform(0.01, 1.0, (B, Hkv, 1, D)).astype(np.float32))
+    vs = oq.f32_to_bf16(rng.uniform(0.01, 1.0, (B, Hkv, nm, 1)).astype(np.float32))
+    mid = {"fmt": "int4", "dtype": "bf16", "kq": kq, "ks": ks, "vq": vq, "vs": vs}
+    got = oatt.tiered_decode(q, sk, sv, mid, rk, rv, dtype="bf16")
+    unpack = lambda p: torch.from_numpy(oq.unpack_int4_last_dim(p).astype(np.int8))  # noqa: E731
+    km = unpack(kq).to(torch.bfloat16) * _t_bf16(ks)
+    vm = unpack(vq).to(torch.bfloat16) * _t_bf16(vs)
+    k = torch.cat([_t_bf16(sk), km, _t_bf16(rk)], dim=-2).double().repeat_interleave(Hq // Hkv, dim=1)
+    v = torch.cat([_t_bf16(sv), vm, _t_bf16(rv)], dim=-2).double().repeat_interleave(Hq // Hkv, dim=1)
+    p = torch.softmax(_t_bf16(q).double() @ k.transpose(-1, -2) / math.sqrt(D), dim=-1)
+    assert np.abs(got - (p @ v).float().numpy()).max() < 1e-6
