@@ -123,7 +123,7 @@ int validate(const fade_decode_args* a) {
       }
     }
   }
-  if (a->kernel < 0 || a->kernel > 3) return einval("fade_tiered_decode_attn: kernel must be 0, 1, 2 or 3");
+  if (a->kernel < 0 || a->kernel > 4) return einval("fade_tiered_decode_attn: kernel must be 0, 1, 2, 3 or 4");
   if (a->dtype != FADE_DTYPE_F16 && a->dtype != FADE_DTYPE_BF16)
     return einval("fade_tiered_decode_attn: dtype must be FADE_DTYPE_F16 or FADE_DTYPE_BF16, got %d", a->dtype);
   if (a->dtype == FADE_DTYPE_BF16) {
@@ -187,6 +187,7 @@ Params to_params(const fade_decode_args* a) {
   p.passes = static_cast<int>((p.G + 3) / 4);
   p.rot = m.len > 0 ? a->rotation : nullptr;  // no middle tokens: nothing is rotated
   p.bf16 = a->dtype == FADE_DTYPE_BF16 ? 1 : 0;
+  p.force_h8 = a->kernel == 4 ? 1 : 0;
   return p;
 }
 
@@ -213,7 +214,7 @@ Plan make_plan(const fade_decode_args* a, const Params& p) {
     // One machine-wide wave of resident workgroups; tiles of either kind cost
     // about the same bytes (8 KB), so splits take equal tile counts.
     const int64_t nT = int4_tiles(p);
-    const int64_t pairs = a->B * a->Hkv * p.passes;  // workgroups per split
+    const int64_t pairs = a->B * a->Hkv * int4_grid_passes(p);  // workgroups per split
     int64_t want = a->n_splits > 0 ? a->n_splits : (int4_resident_wgs(p) + pairs / 2) / pairs;
     pl.n_f16_tiles = int4_fp16_tiles(p);
     pl.tps = 0;
@@ -260,7 +261,7 @@ int64_t partial_bytes(const fade_decode_args* a, int64_t n) {
 // its counter region).
 int run_plan(const fade_decode_args* a, Params& p, const Plan& pl, uint32_t* counters, char* partials,
              hipStream_t st) {
-  if ((a->kernel == 2 || a->kernel == 3) && pl.k == Kern::kValu)
+  if ((a->kernel == 2 || a->kernel == 3 || a->kernel == 4) && pl.k == Kern::kValu)
     return einval("fade_tiered_decode_attn: the matrix-core kernels do not handle this middle tier (format %d)",
                   p.mid.fmt);
   if (p.rot != nullptr && pl.k != Kern::kInt4)

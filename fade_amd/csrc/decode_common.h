@@ -68,6 +68,9 @@ struct Params {
   // symmetric and literal-INT2 formats' scales, an fp16-format middle tier):
   // 0 fp16, 1 bfloat16.  The asymmetric format's scale and zero are fp16.
   int bf16;
+  // GQA 5..8 on an unrotated symmetric tier: eight heads per pass whatever the
+  // size (else only where every resident workgroup gets at least 8 tiles)
+  int force_h8;
 };
 
 // Signed symmetric code of channel d in a packed row (fade/quant.py:26-43,
@@ -108,15 +111,19 @@ bool int4_supports(const Params& p);
 int int4_fp16_tiles(const Params& p);
 int64_t int4_tiles(const Params& p);
 int int4_resident_wgs(const Params& p);  // resident workgroups of the kernel instance for p
+int int4_grid_passes(const Params& p);   // head passes the instance's grid carries per kv head
+bool eight_heads_pay(const Params& p);   // GQA 5..8, symmetric tier: one eight-head pass rather than two
 int launch_int4(const Params& p, hipStream_t st);
 // A packed-kernel instance: the kernel, its wavefronts per workgroup, and its
-// slot in the resident-workgroup cache (fp16 instances 0..35, bf16 36..71).
+// slot in the resident-workgroup cache (fp16 instances 0..35, bf16 36..71,
+// the two-pass symmetric instances of small GQA 5..8 caches 72..79).
 struct PackedChoice {
   void (*k)(Params);
   int waves;
   int index;
+  int grid_passes;  // head passes in the grid's y dimension (2: the two-pass instance; 1 otherwise)
 };
-constexpr int kPackedSlots = 72;
+constexpr int kPackedSlots = 80;
 // The bfloat16 instance for a middle tier int4_supports accepted (reference
 // INT4, rotated 4- or 2-bit, K4 + literal INT2 V; decode_int4_bf16.hip).
 PackedChoice packed_kernel_bf16(const Params& p);

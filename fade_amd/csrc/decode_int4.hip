@@ -51,32 +51,74 @@ int64_t int4_tiles(const Params& p) { return int4_fp16_tiles(p) + cdiv(p.mid.len
 
 namespace {
 
-// index: the template instance, format slot * 4 + DET * 2 + TWO (bf16: + 36)
+// index: the template instance, format slot * 4 + DET * 2 + MANY (bf16: + 36);
+// 72..79: the two-pass symmetric instances of small GQA 5..8 caches
 typedef PackedChoice Choice;
+
+int cu_count() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        n > 0)
+      cus = n;
+    else
+      (void)hipGetLastError();
+  }
+  return cus > 0 ? cus : 256;
+}
+
+}  // namespace
+
+// GQA 5..8 on a symmetric tier: at least 8 tiles per resident workgroup of the
+// eight-head instance (two 4-wave workgroups per CU for 4-bit codes, one
+// 8-wave workgroup for 2-bit).
+bool eight_heads_pay(const Params& p) {
+  const int64_t resident = static_cast<int64_t>(cu_count()) * (p.mid.k_bits == 4 ? 2 : 1);
+  return int4_tiles(p) * p.B * p.Hkv >= 8 * resident;
+}
+
+namespace {
 
 // The kernel instance for a middle tier int4_supports accepted (wave counts
 // measured best on MI355X): the reference INT4 format runs two 4-wave
 // workgroups per CU; the others one workgroup per CU, of eight waves where two
 // stages per wave fit the 160 KB of LDS, six for the 10 and 12.25 KB stages.
+// GQA 5..8 (MANY): the unrotated symmetric formats serve all eight heads in
+// one pass (H8, each kv tile read once) when that gives every resident
+// workgroup at least 8 tiles; below that (small caches) two head passes keep
+// twice the workgroups busy and measured faster (B=8, 28/4 heads, S=4096:
+// 16.4 against 19.3 us; B=16, S=8192: 31.4 against 25.4 us).  The other
+// formats run two head passes (the rotated 4-bit instance with eight heads
+// spills registers in its R merge).
 // `index` keys the resident-workgroup cache per template instance, so an
 // instance whose registers or LDS differ gets its own occupancy.
-template <bool DET, bool TWO>
+template <bool DET, bool MANY>
 Choice packed_kernel_t(const Params& p) {
   const int kb = p.mid.k_bits, vb = p.mid.v_bits;
-  constexpr int v = (DET ? 2 : 0) + (TWO ? 1 : 0);
-  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6, DET, TWO, false, false, 2>, 6, 4 * 6 + v};
+  constexpr int v = (DET ? 2 : 0) + (MANY ? 1 : 0);
+  constexpr int gp = MANY ? 2 : 1;
+  if (MANY && p.mid.fmt == FADE_MID_SYM && p.rot == nullptr && !p.force_h8 && !eight_heads_pay(p))
+    return kb == 4 ? Choice{decode_packed_kernel<4, 4, kFmtSym, 4, DET, true, false, false, false, 2>, 4, 72 + (DET ? 1 : 0), 2}
+                   : Choice{decode_packed_kernel<2, 2, kFmtSym, 8, DET, true, false, false, false, 2>, 8, 74 + (DET ? 1 : 0), 2};
+  if (p.mid.fmt == FADE_MID_K4V2G)
+    return {decode_packed_kernel<4, 8, kFmtLit, 6, DET, MANY, false, false, false, 2>, 6, 4 * 6 + v, gp};
   if (p.mid.fmt == FADE_MID_SYM) {
     if (p.rot != nullptr) {  // rotated backend: q R^T in the prologue, the middle part times R in the merge
-      if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO, false, true, 2>, 4, 4 * 7 + v};
-      return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO, false, true, 2>, 8, 4 * 8 + v};
+      if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, MANY, false, false, true, 2>, 4, 4 * 7 + v, gp};
+      return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, MANY, false, false, true, 2>, 8, 4 * 8 + v, gp};
     }
-    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO, false, false, 2>, 4, 4 * 0 + v};  // two workgroups per CU
-    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO, false, false, 2>, 8, 4 * 1 + v};
+    if (kb == 4)  // two workgroups per CU
+      return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, false, MANY, false, false, 2>, 4, 4 * 0 + v, 1};
+    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, false, MANY, false, false, 2>, 8, 4 * 1 + v, 1};
   }
-  if (kb == 4 && vb == 4) return {decode_packed_kernel<4, 4, kFmtAsym, 6, DET, TWO, false, false, 2>, 6, 4 * 2 + v};
-  if (kb == 4 && vb == 2) return {decode_packed_kernel<4, 2, kFmtAsym, 8, DET, TWO, false, false, 2>, 8, 4 * 3 + v};
-  if (kb == 2 && vb == 2) return {decode_packed_kernel<2, 2, kFmtAsym, 8, DET, TWO, false, false, 2>, 8, 4 * 4 + v};
-  return {decode_packed_kernel<2, 4, kFmtAsym, 6, DET, TWO, false, false, 2>, 6, 4 * 5 + v};
+  if (kb == 4 && vb == 4)
+    return {decode_packed_kernel<4, 4, kFmtAsym, 6, DET, MANY, false, false, false, 2>, 6, 4 * 2 + v, gp};
+  if (kb == 4 && vb == 2)
+    return {decode_packed_kernel<4, 2, kFmtAsym, 8, DET, MANY, false, false, false, 2>, 8, 4 * 3 + v, gp};
+  if (kb == 2 && vb == 2)
+    return {decode_packed_kernel<2, 2, kFmtAsym, 8, DET, MANY, false, false, false, 2>, 8, 4 * 4 + v, gp};
+  return {decode_packed_kernel<2, 4, kFmtAsym, 6, DET, MANY, false, false, false, 2>, 6, 4 * 5 + v, gp};
 }
 
 Choice packed_kernel(const Params& p) {
@@ -103,10 +145,12 @@ int int4_resident_wgs(const Params& p) {
   return cached[c.index];
 }
 
+int int4_grid_passes(const Params& p) { return packed_kernel(p).grid_passes; }
+
 int launch_int4(const Params& p, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv * p.passes),
-                  static_cast<unsigned>(p.B));
   const Choice c = packed_kernel(p);
+  const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv * c.grid_passes),
+                  static_cast<unsigned>(p.B));
   hipLaunchKernelGGL(c.k, grid, dim3(64 * c.waves), 0, st, p);
   return check_launch("fade_tiered_decode_attn(packed)");
 }

@@ -9,19 +9,23 @@ namespace fade {
 namespace decode {
 namespace {
 
-// Same wave counts as the fp16 instances (decode_int4.hip); slots 36.. of the
-// resident-workgroup cache.
-template <bool DET, bool TWO>
+// Same wave counts and head-pass choices as the fp16 instances
+// (decode_int4.hip); slots 36.. of the resident-workgroup cache.
+template <bool DET, bool MANY>
 PackedChoice packed_bf16_t(const Params& p) {
-  constexpr int v = 36 + (DET ? 2 : 0) + (TWO ? 1 : 0);
+  constexpr int v = 36 + (DET ? 2 : 0) + (MANY ? 1 : 0);
   const int kb = p.mid.k_bits;
-  if (p.mid.fmt == FADE_MID_K4V2G) return {decode_packed_kernel<4, 8, kFmtLit, 6, DET, TWO, true, false, 2>, 6, 4 * 6 + v};
+  if (MANY && p.mid.fmt == FADE_MID_SYM && p.rot == nullptr && !p.force_h8 && !eight_heads_pay(p))
+    return kb == 4 ? PackedChoice{decode_packed_kernel<4, 4, kFmtSym, 4, DET, true, false, true, false, 2>, 4, 76 + (DET ? 1 : 0), 2}
+                   : PackedChoice{decode_packed_kernel<2, 2, kFmtSym, 8, DET, true, false, true, false, 2>, 8, 78 + (DET ? 1 : 0), 2};
+  if (p.mid.fmt == FADE_MID_K4V2G)
+    return {decode_packed_kernel<4, 8, kFmtLit, 6, DET, MANY, false, true, false, 2>, 6, 4 * 6 + v, MANY ? 2 : 1};
   if (p.rot != nullptr) {
-    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO, true, true, 2>, 4, 4 * 7 + v};
-    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO, true, true, 2>, 8, 4 * 8 + v};
+    if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, MANY, false, true, true, 2>, 4, 4 * 7 + v, MANY ? 2 : 1};
+    return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, MANY, false, true, true, 2>, 8, 4 * 8 + v, MANY ? 2 : 1};
   }
-  if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, TWO, true, false, 2>, 4, 4 * 0 + v};
-  return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, TWO, true, false, 2>, 8, 4 * 1 + v};
+  if (kb == 4) return {decode_packed_kernel<4, 4, kFmtSym, 4, DET, false, MANY, true, false, 2>, 4, 4 * 0 + v, 1};
+  return {decode_packed_kernel<2, 2, kFmtSym, 8, DET, false, MANY, true, false, 2>, 8, 4 * 1 + v, 1};
 }
 
 }  // namespace

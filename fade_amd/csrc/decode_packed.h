@@ -59,6 +59,20 @@
 //
 // fp16 tokens (sink + recent) form 16-token tiles handled with f16 MFMAs in
 // the same fragment layout (sub-tile 0 only).
+//
+// Eight heads per pass (H8, GQA 5-8, symmetric formats).  A 64-token tile is
+// two 32-token groups of two 16-token sub-tiles; QK^T's 16 columns are
+// (head h, sub-tile s) = 2h + s and its k dimension carries 32 channels of
+// each of the two sub-tiles (lane half g & 1 takes channel half 64 (g & 1),
+// k-step ks its channels 16 ks .. 16 ks + 15), so a lane owns eight scores:
+//
+//   lane = 16g + 2h + s, register i of group q   <->   head h, token 32q + 16s + 4g + i
+//
+// The PV operand and MFMAs are those of four heads (rows 2h + s instead of
+// 4h + s; groups 0 and 1 are the a0 / a1 token halves), and the accumulator
+// register i of lane (n, g) holds head 2g + i / 2: the sum over sub-tiles is
+// still lane-local.  Each kv tile is read once for up to eight heads, at the
+// MFMA and V-conversion cost of four and twice the softmax work.
 #include <math.h>
 
 #include "decode_common.h"
@@ -265,10 +279,18 @@ __device__ __forceinline__ void wait_vm_dispatch(int c) {
 // BF: the query, the fp16-tier K/V, the symmetric formats' scales and the
 // output are bfloat16 (else fp16); probabilities and V codes then enter the
 // PV MFMAs as bfloat16 too.
-template <int KB, int VB, int FMT, int NW, bool DET, bool TWO, bool BF, bool ROT, int NS>
+// H8: eight query heads per pass (GQA 5-8, symmetric formats; partials and
+// split counter laid out as the two-pass instance's, heads 4..7 in the second
+// pass's slot).
+template <int KB, int VB, int FMT, int NW, bool DET, bool TWO, bool H8, bool BF, bool ROT, int NS>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_packed_kernel(
     Params p) {
   constexpr int kWaves = NW, kThreads = 64 * NW;
+  static_assert(!H8 || (FMT == kFmtSym && !TWO), "eight heads per pass: symmetric formats, one pass");
+  constexpr int kHP = H8 ? 8 : kHeads;  // query heads a workgroup serves
+  constexpr int kNX = H8 ? 8 : 4;       // scores per lane and packed tile
+  constexpr int kQdBytes = H8 ? 4 * 2 * 8 * 2 * 16 : 8 * 2 * 4 * 16;  // query digits, then 16 zero bytes
+  constexpr int kNKs = H8 ? 4 : 8;      // query-digit k-steps held in registers
   constexpr bool ASYM = FMT == kFmtAsym;  // asymmetric group-32 formats
   constexpr bool LIT = FMT == kFmtLit;    // K4 + literal grouped INT2 V (int8 codes)
   using S = Stage<KB, VB, FMT>;
@@ -284,10 +306,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, g = lane >> 4;
-  const int hq = n16 >> 2, sq = n16 & 3;  // head / sub-tile of this lane's scores
+  // head / sub-tile of this lane's scores
+  const int hq = H8 ? n16 >> 1 : n16 >> 2, sq = H8 ? n16 & 1 : n16 & 3;
   const int G = TWO ? (p.G - h0 < kHeads ? p.G - h0 : kHeads) : p.G;  // query heads of this pass
   const int64_t bkv = b * p.Hkv + kvh;                    // the kv pair: tier addressing
-  const int64_t slot = TWO ? 2 * bkv + (h0 >> 2) : bkv;   // split counter / partials of this pass
+  // split counter / partials of this pass (H8: the first of the two-pass slots)
+  const int64_t slot = TWO ? 2 * bkv + (h0 >> 2) : (H8 ? 2 * bkv : bkv);
   // Mc: rows of the middle tensors per (batch row, kv head); M, ns, F: this
   // row's middle, sink and fp16 token counts (per-row lengths when given,
   // clamped to the capacities)
@@ -323,14 +347,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   if (tid == 0) claim_s = 0;
 
   __shared__ __attribute__((aligned(16))) uint8_t ring[NS][kWaves][S::kBytes];
-  __shared__ __attribute__((aligned(16))) uint32_t qraw_s[kHeads][kD / 2];  // fp16 query rows
+  __shared__ __attribute__((aligned(16))) uint32_t qraw_s[kHP][kD / 2];  // fp16 query rows
   __shared__ __attribute__((aligned(16))) uint32_t ksraw_s[ASYM ? 1 : kHeads][kD / 2];  // K scales (waves 0..3)
-  __shared__ __attribute__((aligned(16))) uint8_t qd_s[kQdZero + 16];
-  __shared__ float qsc_s[4];
+  __shared__ __attribute__((aligned(16))) uint8_t qd_s[kQdBytes + 16];
+  __shared__ float qsc_s[kHP];
   __shared__ int qoff_s[4][kGroups];    // asymmetric: 128 * sum of the query digits of a group
   __shared__ float qg_s[4][kGroups];    // asymmetric: sum of the query of a group (log2 domain)
-  __shared__ float red_m[kWaves][4], red_l[kWaves][4];
-  __shared__ float qrot_s[ROT ? kHeads : 1][ROT ? kD : 1];  // q R^T (rotated tier)
+  __shared__ float red_m[kWaves][kHP], red_l[kWaves][kHP];
+  __shared__ float qrot_s[ROT ? kHP : 1][ROT ? kD : 1];  // q R^T (rotated tier)
   __shared__ int last_s;
 
   // Paged middle tier: per-token tensors are pools [page][Hkv][64][...] and
@@ -508,9 +532,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 
   // ---- prologue: query rows (and K scales) first, then the first two tiles ----
   {
-    const uint32_t qa = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&qraw_s[wave][0])));
-    if (wave < G) lds_dma4(p.q + b * p.q_sb + (kvh * p.G + h0 + wave) * p.q_sh + 2 * lane, qa);
-    else if (wave < kHeads) qraw_s[wave][lane] = 0u;
+#pragma unroll
+    for (int h = wave; h < kHP; h += kWaves) {
+      const uint32_t qa = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&qraw_s[h][0])));
+      if (h < G) lds_dma4(p.q + b * p.q_sb + (kvh * p.G + h0 + h) * p.q_sh + 2 * lane, qa);
+      else qraw_s[h][lane] = 0u;
+    }
     if (!ASYM && wave < kHeads) {
       const uint32_t ka = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&ksraw_s[wave][0])));
       lds_dma4(p.mid.k_scale + bkv * kD + 2 * lane, ka);
@@ -568,7 +595,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
           f32x4 c = {0, 0, 0, 0};
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks) {
-            const uint4 bq = ar < kHeads ? *reinterpret_cast<const uint4*>(
+            const uint4 bq = ar < kHP ? *reinterpret_cast<const uint4*>(
                                                reinterpret_cast<const uint16_t*>(&qraw_s[ar][0]) + 32 * ks + 8 * kq)
                                          : make_uint4(0u, 0u, 0u, 0u);
             const u32x4 bqv = {bq.x, bq.y, bq.z, bq.w};
@@ -603,7 +630,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
               c = mfma32<false>(__builtin_bit_cast(u32x4, lo), bqv, c);
             }
           }
-          if (ar < kHeads) {
+          if (ar < kHP) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) qrot_s[ar][16 * mt + 4 * kq + j] = c[j] * (1.0f / 1024.0f);
           }
@@ -613,9 +640,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
   }
 
-  // ---- query digits: wave h < 4 handles head h (channels 2*lane, 2*lane+1) ----
-  if (wave < kHeads) {
-    const int h = wave;
+  // ---- query digits: wave w handles heads w, w + NW, ... (channels 2*lane, 2*lane+1) ----
+  if (tid < 4) reinterpret_cast<uint32_t*>(&qd_s[kQdBytes])[tid] = 0u;
+#pragma unroll
+  for (int h = wave; h < kHP; h += kWaves) {
     const uint32_t qq = qraw_s[h][lane];
     float qf0 = w2f<BF>(static_cast<uint16_t>(qq & 0xFFFFu)), qf1 = w2f<BF>(static_cast<uint16_t>(qq >> 16));
     if constexpr (ROT) {
@@ -625,7 +653,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
       }
     }
     if constexpr (!ASYM) {
-      const uint32_t ks = ksraw_s[h][lane];
+      const uint32_t ks = ksraw_s[h & 3][lane];  // every row holds the kv head's K scales
       qf0 *= w2f<BF>(static_cast<uint16_t>(ks & 0xFFFFu));
       qf1 *= w2f<BF>(static_cast<uint16_t>(ks >> 16));
     }
@@ -640,8 +668,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
       const int j = KB == 4 ? 4 * (2 * (r >> 3) + (r & 1)) + ((r & 7) >> 1) : 4 * (r & 3) + (r >> 2);
       const int hi = (qi[e] + 128) >> 8;
       const int lo = qi[e] - 256 * hi;
-      qd_s[(2 * ksd + 0) * 64 + h * 16 + j] = static_cast<uint8_t>(hi & 0xFF);
-      qd_s[(2 * ksd + 1) * 64 + h * 16 + j] = static_cast<uint8_t>(lo & 0xFF);
+      if constexpr (H8) {
+        // [k-step (16 ks .. of channel half d >> 6)][digit][head][half][16 B]
+        const int ks8 = (d >> 4) & 3, half = d >> 6;
+        qd_s[(((2 * ks8 + 0) * 8 + h) * 2 + half) * 16 + j] = static_cast<uint8_t>(hi & 0xFF);
+        qd_s[(((2 * ks8 + 1) * 8 + h) * 2 + half) * 16 + j] = static_cast<uint8_t>(lo & 0xFF);
+      } else {
+        qd_s[(2 * ksd + 0) * 64 + h * 16 + j] = static_cast<uint8_t>(hi & 0xFF);
+        qd_s[(2 * ksd + 1) * 64 + h * 16 + j] = static_cast<uint8_t>(lo & 0xFF);
+      }
     }
     if constexpr (ASYM) {
       // per 32-channel group (16 lanes): the digit sum restores the offset-binary
@@ -661,7 +696,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
     // the K operand carries 16*c (4-bit) or 64*c (2-bit)
     if (lane == 0) qsc_s[h] = mx > 0.0f ? (mx / kQMax) * p.scale_log2 * (KB == 4 ? 0.0625f : 0.015625f) : 0.0f;
-    if (tid < 4) reinterpret_cast<uint32_t*>(&qd_s[kQdZero])[tid] = 0u;
   }
   __syncthreads();
 
@@ -669,13 +703,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   // query operands of the QK^T MFMAs (zero unless this lane's column block
   // matches its k group): registers for the reference formats, LDS reads per
   // tile for the asymmetric ones
-  const bool qlane = (sq == g) && (hq < G);
-  const lds_u8* const qd_l = (const lds_u8*)&qd_s[0] + (qlane ? hq * 16 : kQdZero);
-  const int qstride = qlane ? 64 : 0;
-  i32x4 qdh[ASYM ? 1 : 8], qdl[ASYM ? 1 : 8];
+  // (H8: column block 2h + s takes k groups 2s, 2s + 1, the two channel halves)
+  const bool qlane = (H8 ? (g >> 1) == sq : sq == g) && (hq < G);
+  const lds_u8* const qd_l =
+      (const lds_u8*)&qd_s[0] + (qlane ? (H8 ? (2 * hq + (g & 1)) * 16 : hq * 16) : kQdBytes);
+  const int qstride = qlane ? (H8 ? 256 : 64) : 0;
+  i32x4 qdh[ASYM ? 1 : kNKs], qdl[ASYM ? 1 : kNKs];
   if constexpr (!ASYM) {
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < kNKs; ++ks) {
       qdh[ks] = *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(qd_l + (2 * ks) * qstride);
       qdl[ks] = *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(qd_l + (2 * ks + 1) * qstride);
     }
@@ -711,33 +747,46 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
   for (int gi = 0; gi < kGroups; ++gi) zacc[gi] = 0.0f;
 
-  // Online-softmax step for this lane's four log2-domain scores x (absolute);
+  // Online-softmax step for this lane's kNX log2-domain scores x (absolute);
   // pr = the unnormalized probabilities relative to the running max.
-  auto softmax4 = [&](float (&x)[4], float (&pr)[4]) {
-    const float lmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  auto softmax = [&](float (&x)[kNX], float (&pr)[kNX]) {
+    float lmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    if constexpr (H8) lmax = fmaxf(lmax, fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
     if (__builtin_amdgcn_ballot_w64(lmax - m_run > kTau) != 0) {
+      // the max over the lanes of this lane's head
       float tmax = lmax;
       tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
+      if constexpr (!H8) tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
       const float m_new = fmaxf(m_run, tmax);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
       l_run *= alpha;
-      const float ag = __shfl(alpha, 4 * g, 64);  // accumulator rows of lane (n, g) belong to head g
+      if constexpr (H8) {
+        // accumulator registers 0, 1 of lane (n, g) belong to head 2g, 2 and 3 to 2g + 1
+        const float a0s = __shfl(alpha, 4 * g, 64), a1s = __shfl(alpha, 4 * g + 2, 64);
 #pragma unroll
-      for (int c = 0; c < 8; ++c) acc[c] *= ag;
+        for (int c = 0; c < 8; ++c) acc[c] *= f32x4{a0s, a0s, a1s, a1s};
 #pragma unroll
-      for (int gi = 0; gi < kOffs; ++gi) acc_off[gi] *= ag;
+        for (int gi = 0; gi < kOffs; ++gi) acc_off[gi] *= f32x4{a0s, a0s, a1s, a1s};
+      } else {
+        const float ag = __shfl(alpha, 4 * g, 64);  // accumulator rows of lane (n, g) belong to head g
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] *= ag;
+#pragma unroll
+        for (int gi = 0; gi < kOffs; ++gi) acc_off[gi] *= ag;
+      }
       if constexpr (ASYM) {
 #pragma unroll
         for (int gi = 0; gi < kGroups; ++gi) zacc[gi] *= alpha;
       }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_exp2f(x[i] - m_run);
-    l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    for (int i = 0; i < kNX; ++i) pr[i] = __builtin_amdgcn_exp2f(x[i] - m_run);
+    float ps = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    if constexpr (H8) ps += (pr[4] + pr[5]) + (pr[6] + pr[7]);
+    l_run += ps;
   };
 
   // ---- fp16 tile (16 tokens) from a ring stage ----
@@ -745,7 +794,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const int64_t f0 = t * kMini;
     const int vf = static_cast<int>(F - f0 < kMini ? F - f0 : kMini);
     // QK^T in the plain layout: k = 32 channels (8 per lane group), columns
-    // 4h + s repeat head h for every s; the s != 0 copies are masked below.
+    // 4h + s (H8: 2h + s) repeat head h for every s; the s != 0 copies are masked below.
     f32x4 c4 = {0, 0, 0, 0};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -755,10 +804,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
       c4 = mfma32<BF>(a, u32x4{bq.x, bq.y, bq.z, bq.w}, c4);
     }
     after_k();  // the stage's K rows have been read
-    float x[4], pr[4];
+    float x[kNX], pr[kNX];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = (sq == 0 && 4 * g + i < vf) ? c4[i] * scale_log2 : -INFINITY;
-    softmax4(x, pr);
+    for (int i = 0; i < kNX; ++i) x[i] = (i < 4 && sq == 0 && 4 * g + i < vf) ? c4[i & 3] * scale_log2 : -INFINITY;
+    softmax(x, pr);
     const uint32_t pk0 = sq == 0 ? pack_w<BF>(pr[0], pr[1]) : 0u;
     const uint32_t pk1 = sq == 0 ? pack_w<BF>(pr[2], pr[3]) : 0u;
     const i32x2 a4 = {static_cast<int>(pk0), static_cast<int>(pk1)};
@@ -804,10 +853,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
       for (int c4 = 0; c4 < 4; ++c4) vrd[c4] = kStageV + 32 * r + 16 * ((c4 >> 1) ^ (sigma & 1)) + 8 * (c4 & 1);
     }
   }
-  uint32_t krd[4];  // K row `lane`, 16-byte unit q
+  uint32_t krd[4];  // K row `lane`, 16-byte unit q (H8: [group][u], row 32q + 16(g >> 1) + n16, unit 2(g & 1) + u)
 #pragma unroll
-  for (int qq = 0; qq < 4; ++qq)
-    krd[qq] = KB == 4 ? kStageK + 16 * (4 * lane + (qq ^ ((lane >> 2) & 3))) : kStageK + 32 * lane + 16 * (qq & 1);
+  for (int qq = 0; qq < 4; ++qq) {
+    if constexpr (H8) {
+      const int r = 32 * (qq >> 1) + 16 * (g >> 1) + n16, u = 2 * (g & 1) + (qq & 1);
+      krd[qq] = KB == 4 ? kStageK + 16 * (4 * r + (u ^ ((r >> 2) & 3))) : kStageK + 32 * r + 16 * (g & 1);
+    } else {
+      krd[qq] = KB == 4 ? kStageK + 16 * (4 * lane + (qq ^ ((lane >> 2) & 3))) : kStageK + 32 * lane + 16 * (qq & 1);
+    }
+  }
   // this lane's tokens 16*sq + 4g + i: V scales (reference) or the four
   // [token][group] metadata arrays (asymmetric), 8 bytes per token
   const uint32_t vs_rd = ASYM ? kMeta + 8 * (16 * sq + 4 * g) : kMeta + 4 * (16 * sq + 4 * g);
@@ -844,8 +899,42 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   constexpr uint32_t kFlip = ASYM ? 0x80808080u : 0u;
 
   auto packed_tile = [&](int64_t t, const lds_u8* sp, auto&& after_k) {
-    float x[4], pr[4];
-    if constexpr (!ASYM) {
+    float x[kNX], pr[kNX];
+    if constexpr (H8) {
+      // QK^T of the two 32-token groups: A = K codes of token 32q + 16(g >> 1) + n16,
+      // channel half g & 1; k-step ks = channels 64 (g & 1) + 16 ks .. + 15
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        i32x4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
+        if (KB == 4) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const u32x4 kv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + krd[2 * q + u]);
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int ks = 2 * u + h2;
+              const uint32_t w0 = kv[2 * h2], w1 = kv[2 * h2 + 1];
+              const i32x4 a = {static_cast<int>(w0 & 0xF0F0F0F0u), static_cast<int>((w0 << 4) & 0xF0F0F0F0u),
+                               static_cast<int>(w1 & 0xF0F0F0F0u), static_cast<int>((w1 << 4) & 0xF0F0F0F0u)};
+              chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig(ks, 0), chi, 0, 0, 0);
+              clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig(ks, 1), clo, 0, 0, 0);
+            }
+          }
+        } else {
+          const u32x4 kv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + krd[2 * q]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t w = kv[e];
+            const i32x4 a = {static_cast<int>(w & 0xC0C0C0C0u), static_cast<int>((w << 2) & 0xC0C0C0C0u),
+                             static_cast<int>((w << 4) & 0xC0C0C0C0u), static_cast<int>((w << 6) & 0xC0C0C0C0u)};
+            chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig(e, 0), chi, 0, 0, 0);
+            clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig(e, 1), clo, 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[4 * q + i] = static_cast<float>(chi[i] * 256 + clo[i]) * qsc;
+      }
+    } else if constexpr (!ASYM) {
       // QK^T: A = K codes of token `lane` as int8 (16*c or 64*c)
       i32x4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
       if (KB == 4) {
@@ -948,10 +1037,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     if (m0 + kTile > M) {
       const int valid = static_cast<int>(M - m0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (16 * sq + 4 * g + i >= valid) x[i] = -INFINITY;
+      for (int i = 0; i < kNX; ++i)
+        if (32 * (i >> 2) * (H8 ? 1 : 0) + 16 * sq + 4 * g + (i & 3) >= valid) x[i] = -INFINITY;
     }
-    softmax4(x, pr);
+    softmax(x, pr);
     // P' = P * v_scale: one operand pair (a0, a1) per V scale group
     constexpr int kPs = ASYM ? kGroups : 1;
     u32x4 a0[kPs], a1[kPs];
@@ -960,6 +1049,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
       const uint32_t pk0 = pack_w<BF>(pr[0], pr[1]), pk1 = pack_w<BF>(pr[2], pr[3]);
       a0[0] = u32x4{sq == 0 ? pk0 : z, sq == 0 ? pk1 : z, sq == 1 ? pk0 : z, sq == 1 ? pk1 : z};
       a1[0] = u32x4{sq == 2 ? pk0 : z, sq == 2 ? pk1 : z, sq == 3 ? pk0 : z, sq == 3 ? pk1 : z};
+    } else if constexpr (H8) {
+      // group q's probabilities times their tokens' V scales: the a0 / a1 token halves
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const u32x4 sv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd + 128 * q);
+        const uint32_t pk0 = pack_w<BF>(pr[4 * q] * w2f<BF>(static_cast<uint16_t>(sv[0])),
+                                        pr[4 * q + 1] * w2f<BF>(static_cast<uint16_t>(sv[1])));
+        const uint32_t pk1 = pack_w<BF>(pr[4 * q + 2] * w2f<BF>(static_cast<uint16_t>(sv[2])),
+                                        pr[4 * q + 3] * w2f<BF>(static_cast<uint16_t>(sv[3])));
+        const u32x4 aq = {sq == 0 ? pk0 : z, sq == 0 ? pk1 : z, sq == 1 ? pk0 : z, sq == 1 ? pk1 : z};
+        if (q == 0) a0[0] = aq;
+        else a1[0] = aq;
+      }
     } else if constexpr (!ASYM) {
       // scales sit in the low halves of the stage's scale dwords
       const u32x4 sv = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(sp + vs_rd);
@@ -1105,9 +1207,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   }
 
   // ---- merge the wavefronts of the workgroup ----
-  float lsum = l_run;
+  float lsum = l_run;  // summed over the lanes of this lane's head
   lsum += __shfl_xor(lsum, 1, 64);
-  lsum += __shfl_xor(lsum, 2, 64);
+  if constexpr (!H8) lsum += __shfl_xor(lsum, 2, 64);
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
   // zero-point sums of head hq (score lanes), then of head g (accumulator lanes)
@@ -1128,8 +1230,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     red_l[wave][hq] = lsum;
   }
   __syncthreads();
-  float* red_o = reinterpret_cast<float*>(&ring[0][0][0]);  // [wave][4 heads][128] (NW * 2 KB)
-  {
+  float* red_o = reinterpret_cast<float*>(&ring[0][0][0]);  // [wave][kHP heads][128] (NW * 2 or 4 KB)
+  if constexpr (H8) {
+    // accumulator registers 0, 1 of lane (n, g): head 2g; 2, 3: head 2g + 1
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int h = 2 * g + e;
+      float Mg = red_m[0][h];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) Mg = fmaxf(Mg, red_m[w][h]);
+      const float wsc = exp2f(red_m[wave][h] - Mg);
+      const float off = acc_off[0][2 * e] + acc_off[0][2 * e + 1];
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        red_o[(wave * kHP + h) * kD + out_channel<VB>(c, n16)] = ((acc[c][2 * e] + acc[c][2 * e + 1]) - off) * wsc;
+    }
+  } else {
     float Mg = red_m[0][g];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) Mg = fmaxf(Mg, red_m[w][g]);
@@ -1153,13 +1269,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     float o = 0.0f, L = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      o += red_o[(w * 4 + h) * kD + d];
+      o += red_o[(w * kHP + h) * kD + d];
       L += red_l[w][h] * exp2f(red_m[w][h] - Mh);
     }
     if (n == 1) {
       p.out[b * p.o_sb + (kvh * p.G + h0 + h) * p.o_sh + d] = f2w<BF>(o / L);
     } else {
-      const int64_t pi = (slot * n + split) * 4 + h;
+      // H8: heads 4..7 in the second pass's slot (the two-pass layout)
+      const int64_t pi = ((slot + (h >> 2)) * n + split) * 4 + (h & 3);
       store_agent(&p.ws_acc[pi * kD + d], o);
       if (d == 0) store_agent2(&p.ws_ml[2 * pi], Mh, L);
     }
@@ -1194,8 +1311,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
   {
     // thread tid merges items (head, channel) tid + e * kThreads; the loads of
     // a batch of 16 splits for all its items issue before any is used
-    constexpr int kB = 16, kE = (kHeads * kD + kThreads - 1) / kThreads;
-    const int64_t p0 = slot * n * 4;
+    constexpr int kB = 16, kE = (kHP * kD + kThreads - 1) / kThreads;
     // rotated tier: thread (channel c, quarter dq) of 4 kD virtual threads needs
     // R[32 dq .. 32 dq + 31][c]; loaded first, so that they fly with the partials
     constexpr int kV = (4 * kD + kThreads - 1) / kThreads;
@@ -1230,7 +1346,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
           for (int e = 0; e < kE; ++e) {
             const int idx = tid + e * kThreads;
             const int h = idx < G * kD ? idx >> 7 : 0, d = idx & (kD - 1);
-            const int64_t pi = p0 + 4 * (s0 + j) + h;
+            const int64_t pi = ((slot + (h >> 2)) * n + s0 + j) * 4 + (h & 3);
             load_agent2(&p.ws_ml[2 * pi], mm[e][j], ll[e][j]);
             aa[e][j] = load_agent(&p.ws_acc[pi * kD + d]);
           }
@@ -1269,12 +1385,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     if (rot) {
       // out = (of + o R) / L: o [head][d] to LDS, then 512 virtual threads
       // (channel c, quarter dq) sum d over [32 dq, 32 dq + 32) for every head
-      float* ro = reinterpret_cast<float*>(&ring[0][0][0]);  // [4][kD] o, then [4 dq][4][kD] partial products
-      float* pp = ro + kHeads * kD;
+      float* ro = reinterpret_cast<float*>(&ring[0][0][0]);  // [kHP][kD] o, then [4 dq][kHP][kD] partial products
+      float* pp = ro + kHP * kD;
 #pragma unroll
       for (int e = 0; e < kE; ++e) {
         const int idx = tid + e * kThreads;
-        if (idx < kHeads * kD) ro[idx] = idx < G * kD ? o[e] : 0.0f;
+        if (idx < kHP * kD) ro[idx] = idx < G * kD ? o[e] : 0.0f;
       }
       __syncthreads();
 #pragma unroll
@@ -1282,13 +1398,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         const int vt = tid + iv * kThreads;
         if (vt < 4 * kD) {
           const int c = vt & (kD - 1), dq = vt >> 7;
-          float sh[kHeads] = {0.0f, 0.0f, 0.0f, 0.0f};
+          float sh[kHP];
+#pragma unroll
+          for (int h = 0; h < kHP; ++h) sh[h] = 0.0f;
 #pragma unroll
           for (int d = 0; d < 32; ++d)
 #pragma unroll
-            for (int h = 0; h < kHeads; ++h) sh[h] = fmaf(ro[h * kD + 32 * dq + d], rr[iv][d], sh[h]);
+            for (int h = 0; h < kHP; ++h) sh[h] = fmaf(ro[h * kD + 32 * dq + d], rr[iv][d], sh[h]);
 #pragma unroll
-          for (int h = 0; h < kHeads; ++h) pp[(dq * kHeads + h) * kD + c] = sh[h];
+          for (int h = 0; h < kHP; ++h) pp[(dq * kHP + h) * kD + c] = sh[h];
         }
       }
       __syncthreads();
@@ -1297,8 +1415,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         const int idx = tid + e * kThreads;
         if (idx < G * kD) {
           const int h = idx >> 7, c = idx & (kD - 1);
-          const float v = of[e] + ((pp[h * kD + c] + pp[(kHeads + h) * kD + c]) +
-                                   (pp[(2 * kHeads + h) * kD + c] + pp[(3 * kHeads + h) * kD + c]));
+          const float v = of[e] + ((pp[h * kD + c] + pp[(kHP + h) * kD + c]) +
+                                   (pp[(2 * kHP + h) * kD + c] + pp[(3 * kHP + h) * kD + c]));
           p.out[b * p.o_sb + (kvh * p.G + h0 + h) * p.o_sh + c] = f2w<BF>(v / L[e]);
         }
       }

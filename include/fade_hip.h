@@ -317,7 +317,11 @@ typedef struct fade_decode_args {
   fade_fp16_tier recent;       /* last recent.len tokens */
   int32_t n_splits;            /* 0 = choose automatically */
   int32_t kernel;              /* 0 = auto, 1 = portable VALU kernel, 2 = matrix-core kernels
-                                  only, 3 = the general matrix-core kernel (no INT4 fast path) */
+                                  only, 3 = the general matrix-core kernel (no INT4 fast path),
+                                  4 = as 2, with Hq/Hkv = 5..8 on an unrotated FADE_MID_SYM tier
+                                  served eight heads per pass whatever the size (0 and 2 take
+                                  that instance where every resident workgroup gets at least 8
+                                  tiles, two head passes below) */
   void* workspace;             /* zero-filled before its first use.  Its first
                                   round256(4*B*Hkv*P) bytes (P = 1 for Hq/Hkv <= 4, else 2)
                                   hold per-(row, kv head, head pass) split counters, which

@@ -74,13 +74,14 @@ def _middle(fmt, km, vm, R=None):
 
 SHAPES = [
     (2, 32, 8, 700, 4, 64),  # GQA 4 (Llama-3 heads)
-    (2, 28, 4, 700, 4, 64),  # GQA 7: two head passes
+    (2, 28, 4, 700, 4, 64),  # GQA 7: two head passes at this size; kernel 4: eight heads per pass
     (1, 8, 8, 130, 0, 0),  # MHA, middle only, ragged tile
 ]
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,S,ns,nr", SHAPES)
-@pytest.mark.parametrize("fmt,kernel", [("int4", 0), ("int4", 1), ("k4v2", 0), ("k4v2", 1), ("rot4", 0), ("rot2", 0)])
+@pytest.mark.parametrize("fmt,kernel", [("int4", 0), ("int4", 1), ("int4", 4), ("k4v2", 0), ("k4v2", 1), ("rot4", 0),
+                                        ("rot2", 0)])
 def test_decode_bf16_formats(dev, B, Hq, Hkv, S, ns, nr, fmt, kernel):
     print(f"case bf16 decode {fmt} kernel={kernel} B={B} Hq={Hq} Hkv={Hkv} S={S}", flush=True)
     q, k, v = _kv(dev, B, Hq, Hkv, S, 128, seed=700 + S + Hq)

@@ -154,8 +154,19 @@ def test_typed_cache_reassign_matches_oracle_composition(dev, dtype):
     fk, fv = o["fp16_k"], o["fp16_v"]
     assert np.array_equal(_host_t(K, dtype), np.concatenate([fk[:, :, :ns], kd, fk[:, :, ns:]], 2))
     assert np.array_equal(_host_t(V, dtype), np.concatenate([fv[:, :, :ns], vd, fv[:, :, ns:]], 2))
-    with pytest.raises(NotImplementedError, match="float16 tiers"):
-        c.decode_attention(torch.zeros(B, 8, 1, D, dtype=torch.float16, device=dev), 0)
+    if dtype == "f32":
+        with pytest.raises(NotImplementedError, match="bfloat16 tiers"):
+            c.decode_attention(torch.zeros(B, 8, 1, D, dtype=torch.float32, device=dev), 0)
+    else:
+        # a bf16 cache decodes on the kernels: fp32 attention over the materialized
+        # bf16 K/V (the reference's path), bf16 tolerance 4e-3 + 2^-7 |ref|
+        qd = torch.randn(B, 8, 1, D, generator=torch.Generator().manual_seed(34)).to(dev, tdt)
+        out = c.decode_attention(qd, 0)
+        assert out.dtype == tdt
+        ref = oatt.sdpa_fp32(qd.float().cpu().numpy(), K.float().cpu().numpy(), V.float().cpu().numpy())
+        assert (np.abs(out.float().cpu().numpy() - ref) - 2.0**-7 * np.abs(ref)).max() <= 4e-3
+        with pytest.raises(ValueError, match="query's dtype"):
+            c.decode_attention(qd.half(), 0)
 
     # a second reassignment requantizes from the dequantized values
     S2 = c.get_seq_length(0)

@@ -295,7 +295,7 @@ def test_tiered_decode_rotation_rejects(dev):
         (2, 8, 4, 777, 4, 64, 3),  # G=2
         (1, 4, 1, 300, 0, 37, 1),  # one kv head, ragged recent window
         (2, 12, 4, 2000, 4, 256, 0),  # G=3, config-2 windows
-        (1, 16, 2, 900, 4, 64, 0),  # G=8: two head passes
+        (1, 16, 2, 900, 4, 64, 0),  # G=8: eight heads in one pass
         (2, 24, 4, 700, 4, 64, 3),  # G=6
     ],
 )
@@ -411,7 +411,8 @@ def _row_slice_mid(omid, b, lm):
 @pytest.mark.parametrize("Hq,Hkv,fmt", [(28, 4, "int4"), (20, 4, "int4"), (16, 2, "asym"), (56, 8, "int4")])
 def test_tiered_decode_ragged_paged_gqa_5_to_8(dev, Hq, Hkv, fmt):
     """GQA groups of 5-8 query heads (Qwen2.5-7B's 28/4, 20/4, 16/2, 56/8) with per-row
-    lengths and a paged middle tier: the INT4 kernel runs two head passes per kv head.
+    lengths and a paged middle tier: the INT4 kernel serves all heads of a kv head in
+    one pass (reference INT4 format) or in two head passes (asymmetric format).
     Each row against the oracle over its own tokens; paged == padded bit for bit in
     deterministic mode; repeated plans on one stream share a workspace."""
     from fade_amd.kernels.tiered_attn import paginate_middle
@@ -427,19 +428,55 @@ def test_tiered_decode_ragged_paged_gqa_5_to_8(dev, Hq, Hkv, fmt):
     rec = (t(k[:, :, S - nr_c :]), t(v[:, :, S - nr_c :]))
     n_pages = int(sum(-(-int(x) // 64) for x in lens[:, 1]))
     paged = paginate_middle(mid, lens[:, 1], order=np.random.default_rng(2).permutation(n_pages))
-    out_r = tiered_decode_attention(t(q), sink, mid, rec, lens=t(lens), deterministic=True)
-    out_p = tiered_decode_attention(t(q), sink, paged, rec, lens=t(lens), deterministic=True)
-    assert torch.equal(out_r, out_p)
-    out = out_r.float().cpu().numpy()
-    for b, (ls, lm, lr) in enumerate(lens):
-        ref = oatt.tiered_decode(
-            q[b : b + 1], k[b : b + 1, :, :ls], v[b : b + 1, :, :ls], _row_slice_mid(omid, b, lm),
-            k[b : b + 1, :, S - nr_c : S - nr_c + lr], v[b : b + 1, :, S - nr_c : S - nr_c + lr],
-        )
-        assert np.abs(out[b : b + 1] - ref).max() <= ATOL, b
-    for n_splits in (1, 5):  # other split counts, claims on: still within the oracle's tolerance
-        o = tiered_decode_attention(t(q), sink, paged, rec, lens=t(lens), n_splits=n_splits)
-        assert (o.float() - out_r.float()).abs().max().item() <= 1e-3
+    # kernel 4 (int4): all heads of a kv head in one pass whatever the size
+    for kernel in ((0, 4) if fmt == "int4" else (0,)):
+        out_r = tiered_decode_attention(t(q), sink, mid, rec, lens=t(lens), deterministic=True, kernel=kernel)
+        out_p = tiered_decode_attention(t(q), sink, paged, rec, lens=t(lens), deterministic=True, kernel=kernel)
+        assert torch.equal(out_r, out_p)
+        out = out_r.float().cpu().numpy()
+        for b, (ls, lm, lr) in enumerate(lens):
+            ref = oatt.tiered_decode(
+                q[b : b + 1], k[b : b + 1, :, :ls], v[b : b + 1, :, :ls], _row_slice_mid(omid, b, lm),
+                k[b : b + 1, :, S - nr_c : S - nr_c + lr], v[b : b + 1, :, S - nr_c : S - nr_c + lr],
+            )
+            assert np.abs(out[b : b + 1] - ref).max() <= ATOL, (kernel, b)
+        for n_splits in (1, 5):  # other split counts, claims on: still within the oracle's tolerance
+            o = tiered_decode_attention(t(q), sink, paged, rec, lens=t(lens), n_splits=n_splits, kernel=kernel)
+            assert (o.float() - out_r.float()).abs().max().item() <= 1e-3
+
+
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,S,ns,nr,n_splits",
+    [
+        (2, 20, 4, 900, 4, 64, 0),  # G=5
+        (1, 24, 4, 333, 4, 0, 3),  # G=6, no recent tier, a ragged last tile
+        (2, 64, 8, 1200, 4, 64, 0),  # G=8 (Llama-3-70B heads)
+        (1, 8, 1, 70, 2, 5, 1),  # G=8, one split, a short middle tier
+        (3, 56, 8, 2100, 4, 256, 7),  # G=7
+    ],
+)
+@pytest.mark.parametrize("det", [False, True])
+def test_tiered_decode_int4_eight_heads_one_pass(dev, B, Hq, Hkv, S, ns, nr, n_splits, det):
+    """GQA 5-8 on the reference INT4 format: every query head of a kv head in one
+    pass of the matrix-core kernel (eight heads x two sub-tiles in the QK^T
+    columns), each kv tile read once; against the oracle, and bitwise repeatable
+    in deterministic mode."""
+    print(f"case decode int4 eight heads B={B} Hq={Hq} Hkv={Hkv} S={S} splits={n_splits} det={det}", flush=True)
+    q, k, v, ns, nr = _case(B, Hq, Hkv, S, ns, nr, seed=5000 + S + Hq)
+    mid, omid = _int4_mid(dev, k, v, ns, nr)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    sink = (t(k[:, :, :ns]), t(v[:, :, :ns])) if ns else None
+    rec = (t(k[:, :, S - nr :]), t(v[:, :, S - nr :])) if nr else None
+    ref = oatt.tiered_decode(q, k[:, :, :ns], v[:, :, :ns], omid, k[:, :, S - nr :], v[:, :, S - nr :])
+    # kernel 4: the eight-head instance whatever the size; 0: the automatic choice
+    # (two head passes at these sizes)
+    for kernel in (4, 0):
+        out = tiered_decode_attention(t(q), sink, mid, rec, n_splits=n_splits, deterministic=det, kernel=kernel)
+        err = np.abs(out.float().cpu().numpy() - ref)
+        assert err.max() <= ATOL, (kernel, [(int(b), int(h)) for b, h in zip(*np.nonzero(err.max(axis=(2, 3)) > ATOL))][:8])
+        if det:
+            again = tiered_decode_attention(t(q), sink, mid, rec, n_splits=n_splits, deterministic=True, kernel=kernel)
+            assert torch.equal(out, again)
 
 
 @pytest.mark.parametrize("fmt", ["int4", "asym42"])
