@@ -71,6 +71,9 @@ constexpr int kKT = 64;       // keys per tile
 // halves per K row in LDS: D + 8 (16-byte reads of 16 rows: distinct banks at D = 128)
 template <int D>
 constexpr int kKPitch = D + 8;
+// waves per SIMD the register allocation is sized for: 1 at head_dim 256 (512 registers), else 2
+template <int D>
+constexpr int kWavesPerEu = D > 128 ? 1 : 2;
 constexpr int kVtPitch = 72;  // halves per V^T row in LDS (16-byte accesses of 8 consecutive rows: distinct banks)
 constexpr float kNegBig = -1.0e30f;
 // The running max moves only when a score exceeds it by kTau = 8 (log2 units),
@@ -148,10 +151,11 @@ __device__ __forceinline__ uint32_t dequant_pair_bf16(uint32_t o72, uint32_t s2)
 // Position of key k (0..63) of a tile in a V^T row: bits 2 and 3 exchanged.
 __host__ __device__ constexpr int swap23(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
-// Head dims up to the capacity DP = 32, 64 or 128: QK^T takes DP/16 k-steps,
-// PV DP/32 column blocks; a fetch thread covers DP/4 channels of a token (fp16
-// tiles), and DP/32 threads stage a middle token's code bytes, 16 (32
-// channels) each.  A head_dim D < DP (p.D) leaves the channels past D as
+// Head dims up to the capacity DP = 32, 64, 128 or 256: QK^T takes DP/16
+// k-steps, PV DP/32 column blocks; a fetch thread covers DP/4 channels of a
+// token (fp16 tiles), and DP/32 threads stage a middle token's code bytes, 16
+// (32 channels) each (at DP = 256 in two passes of 32 tokens, the same
+// channels, so the same K scales).  A head_dim D < DP (p.D) leaves the channels past D as
 // zeros in the K rows and the query (so they add nothing to the scores) and
 // never stores them; V channels past D feed only output columns that are not
 // stored.  fp16 rows move in 8-channel units, packed rows in 32-channel ones.
@@ -161,8 +165,13 @@ __host__ __device__ constexpr int swap23(int k) { return (k & ~12) | ((k & 4) <<
 // BF: q, out, the fp16-layout tiers and the middle tier's scales are bfloat16;
 // middle codes dequantize to bf16(code * scale), the MFMAs take bfloat16
 // operands (the probabilities too), accumulating in fp32.
+// DP = 256 runs NQB = 1 at one wave per SIMD: its O accumulators alone take 128
+// registers per lane, and its LDS (two 33 KB K and two 36 KB V^T buffers) one
+// workgroup per CU.
 template <int DP, int NQB, bool BF>
-__global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PParams p) {
+__global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<DP>, kWavesPerEu<DP>)))
+void prefill_kernel(PParams p) {
+  static_assert(DP <= 128 || NQB == 1, "head_dim 256 runs one query block per workgroup");
   constexpr int D = DP;           // channel capacity of the LDS rows and MFMA tiles
   constexpr int KROW = D / 2;     // staged bytes of one token's packed 4-bit codes
   constexpr int CPT = D / 4;      // channels per fetch thread (fp16 tiles)
@@ -171,6 +180,10 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
   constexpr int NKS = D / 16;     // QK^T k-steps
   constexpr int NCB = D / 32;     // PV column blocks
   constexpr int KP = kKPitch<D>;
+  constexpr int TPP = kThreads / KTHR < kKT ? kThreads / KTHR : kKT;  // middle tokens one K staging pass covers
+  constexpr int KPS = kKT / TPP;                  // K staging passes (2 at D = 256)
+  constexpr int VPS = (16 * UPR + 63) / 64;       // V staging loads per lane (2 at D = 256)
+  constexpr int VWB = 16 * KROW > 1024 ? 16 * KROW : 1024;  // staged V code bytes of one wave's 16 keys
   const int Dr = p.D;             // the rows' channels (<= D)
   const int krow = Dr / 2;        // bytes of one token's packed codes in HBM
   const int qb = blockIdx.x / p.passes;
@@ -242,20 +255,20 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
   __shared__ __attribute__((aligned(16))) uint16_t kt[2][kKT][KP];
   __shared__ __attribute__((aligned(16))) uint16_t vtt[2][D][kVtPitch];
   __shared__ __attribute__((aligned(16))) float rowf[4 * NQB][32];  // per-wave factors of the 32 query rows
-  // middle-tile staging: thread tid's 16 bytes of K codes at 16 tid (token
-  // tid / KTHR, channels 32 (tid % KTHR) ..); keys 16 w + rho (rho < 16) in
-  // stg_v[1024 w ..], 16-byte unit u of row rho at unit
+  // middle-tile staging: thread tid's 16 bytes of K codes of pass i at
+  // 16 (tid + kThreads i) (token tid / KTHR + TPP i, channels 32 (tid % KTHR) ..);
+  // keys 16 w + rho (rho < 16) in stg_v[VWB w ..], 16-byte unit u of row rho at unit
   // UPR rho + (u ^ ((rho >> 1) & (UPR - 1))); their V scales in dwords
   // 64 w + l, key 16 w + (l & 15) (a 2-byte direct load fills one dword per lane)
-  __shared__ __attribute__((aligned(16))) uint8_t stg_k[kThreads * 16];
-  __shared__ __attribute__((aligned(16))) uint8_t stg_v[kThreads * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t stg_k[KPS * kThreads * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t stg_v[4 * VWB];
   __shared__ __attribute__((aligned(16))) uint32_t stg_s[kThreads];
 
   // ---- tile fetch: thread = token r of the tile, channels CPT*cp .. CPT*cp+CPT-1 ----
   const int r = gtid >> 2, cp = gtid & 3;
-  // middle K staging: thread = token mr, channels 32*mc .. 32*mc+31 (threads gtid < 64 KTHR)
+  // middle K staging: thread = tokens mr + TPP i, channels 32*mc .. 32*mc+31 (threads gtid < TPP KTHR)
   const int mr = gtid / KTHR, mc = gtid % KTHR;
-  const bool kstage = do_k && (kKT * KTHR == kThreads || gtid < kKT * KTHR);
+  const bool kstage = do_k && (TPP * KTHR == kThreads || gtid < TPP * KTHR);
   // fp16 rows of each segment (0 sink, 1 fp16 middle tier, 2 recent, 3 chunk)
   // of this (row, kv head): K and V row pointers and row strides in halves.
   // They sit in LDS, read (one broadcast per tile) by the few fp16 tiles of a
@@ -291,20 +304,18 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int e = 0; e < 4; ++e) ksc[4 * i + e] = st[e];
   }
-  int fok = 0;  // this thread's staged middle row is a real token of the tile
+  int fok = 0;  // bit i: this thread's staged middle row of pass i is a real token of the tile
   // staging slots of this wave's lanes (a direct load writes lane l's bytes at base + l * size)
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   const uint32_t stk = __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_k[16 * 64 * wq])));
   const uint32_t stv = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_v[16 * 64 * wq])));
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_v[VWB * wq])));
   const uint32_t sts = __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)&stg_s[64 * wq])));
   // Middle tile: codes and V scale to the staging area.  Nothing waits for
   // these loads before store_mid(), so they fly during the current tile's compute.
   auto fetch_mid = [&](const TileRef& tr) {
-    const bool ok = mr < tr.cnt;
-    fok = ok;
     // the tile's rows: from row tr.base of this (row, kv head)'s padded tensors,
     // or from row 0 of its page's (page, kv head) block in the pools
     const uint8_t* kq_t = kq;
@@ -318,17 +329,29 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
       vs_t = p.vs + blk * kKT;
       row0 = 0;
     }
-    const int key = row0 + (ok ? mr : tr.cnt - 1);  // rows past the tile: a valid row, zeroed in store_mid()
-    if (kstage && 32 * mc < Dr) lds_dma16(kq_t + static_cast<int64_t>(key) * krow + 16 * mc, stk);
-    // V: lane l < 16 UPR of wave w fills unit l of the wave's block: row
-    // rho = l / UPR, source unit (l % UPR) ^ ((rho >> 1) & (UPR - 1)).  Rows
-    // past the tile read the last valid key (finite; their probabilities are zero).
+    fok = 0;
+#pragma unroll
+    for (int i = 0; i < KPS; ++i) {
+      const bool ok = mr + TPP * i < tr.cnt;
+      fok |= ok ? 1 << i : 0;
+      const int key = row0 + (ok ? mr + TPP * i : tr.cnt - 1);  // rows past the tile: a valid row, zeroed in store_mid()
+      if (kstage && 32 * mc < Dr) lds_dma16(kq_t + static_cast<int64_t>(key) * krow + 16 * mc, stk + 16 * kThreads * i);
+    }
+    // V: unit ul = l + 64 i < 16 UPR of wave w (lane l, load i) fills unit ul
+    // of the wave's block: row rho = ul / UPR, source unit
+    // (ul % UPR) ^ ((rho >> 1) & (UPR - 1)).  Rows past the tile read the last
+    // valid key (finite; their probabilities are zero).
     if (do_v) {
-      const int vr = lane / UPR;
-      const int vk = 16 * wq + vr, sk2 = 16 * wq + (lane & 15);
-      const int vu = (lane % UPR) ^ ((vr >> 1) & (UPR - 1));  // the unit's 32 channels in the row
-      if ((UPR == 4 || lane < 16 * UPR) && 32 * vu < Dr)
-        lds_dma16(vq_t + static_cast<int64_t>(row0 + (vk < tr.cnt ? vk : tr.cnt - 1)) * krow + 16 * vu, stv);
+#pragma unroll
+      for (int i = 0; i < VPS; ++i) {
+        const int ul = lane + 64 * i;
+        const int vr = ul / UPR;
+        const int vk = 16 * wq + vr;
+        const int vu = (ul % UPR) ^ ((vr >> 1) & (UPR - 1));  // the unit's 32 channels in the row
+        if ((16 * UPR >= 64 * (i + 1) || ul < 16 * UPR) && 32 * vu < Dr)
+          lds_dma16(vq_t + static_cast<int64_t>(row0 + (vk < tr.cnt ? vk : tr.cnt - 1)) * krow + 16 * vu, stv + 1024 * i);
+      }
+      const int sk2 = 16 * wq + (lane & 15);
       lds_dma2(vs_t + row0 + (sk2 < tr.cnt ? sk2 : tr.cnt - 1), sts);
     }
   };
@@ -338,8 +361,11 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const f16x2 m72 = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
     if (do_k) {
+#pragma unroll
+    for (int pi = 0; pi < KPS; ++pi) {
     uint4 kraw = make_uint4(0, 0, 0, 0);
-    if (kstage && fok && 32 * mc < Dr) kraw = *reinterpret_cast<const uint4*>(&stg_k[16 * gtid]);
+    if (kstage && ((fok >> pi) & 1) && 32 * mc < Dr)
+      kraw = *reinterpret_cast<const uint4*>(&stg_k[16 * (gtid + kThreads * pi)]);
     // codes -> fp16 72 + c -> c -> fp16(c * scale), already in the stored channel order
     const uint32_t kw[4] = {kraw.x, kraw.y, kraw.z, kraw.w};
 #pragma unroll
@@ -352,7 +378,8 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
         kd[e] = BF ? dequant_pair_bf16(o[e], ksc[4 * i + e])
                    : __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, o[e]) + m72) *
                                                       __builtin_bit_cast(f16x2, ksc[4 * i + e]));
-      if (kstage) *reinterpret_cast<u32x4*>(&kt[buf][mr][32 * mc + 8 * i]) = kd;
+      if (kstage) *reinterpret_cast<u32x4*>(&kt[buf][mr + TPP * pi][32 * mc + 8 * i]) = kd;
+    }
     }
     }
     if (!do_v) return;
@@ -372,7 +399,7 @@ __global__ __launch_bounds__(kThreads * NQB) __attribute__((amdgpu_waves_per_eu(
     // of those rows, nibble s' <-> position offset o(s'), so the fp16 pairs
     // come out as position pairs (2 j, 2 j + 1), rows (swap23(2 j), + 1).
     const int so = swap23(2 * (n16 & 3) + ((n16 >> 2) & 1) + 8 * (n16 >> 3));
-    const uint8_t* vrow = &stg_v[1024 * wq + KROW * so];
+    const uint8_t* vrow = &stg_v[VWB * wq + KROW * so];
     // channel units of 16: D/16 of them, four per pass of the lane groups
     // (D = 32: groups 2 and 3 repeat units 0 and 1 and store nothing)
 #pragma unroll
@@ -667,8 +694,8 @@ using namespace fade::prefill;
 
 FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) {
   if (a == nullptr) return einval("fade_tiered_prefill_attn: null args");
-  if (a->D < 8 || a->D > 128 || a->D % 8 != 0)
-    return einval("fade_tiered_prefill_attn: head_dim must be a multiple of 8 in [8, 128], got %lld", (long long)a->D);
+  if (a->D < 8 || a->D > 256 || a->D % 8 != 0)
+    return einval("fade_tiered_prefill_attn: head_dim must be a multiple of 8 in [8, 256], got %lld", (long long)a->D);
   if (a->B <= 0 || a->Hq <= 0 || a->Hkv <= 0 || a->Sq <= 0)
     return einval("fade_tiered_prefill_attn: B, Hq, Hkv and Sq must be positive");
   if (a->Hq % a->Hkv != 0 || a->Hq / a->Hkv > 8)
@@ -738,8 +765,8 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   p.mask_mode = a->mask_mode;
   p.chunk_len = static_cast<int>(a->chunk.len);
   p.D = static_cast<int>(a->D);
-  // two query blocks per workgroup once there are more than 32 queries
-  const int nqb = a->Sq > kQB ? 2 : 1;
+  // two query blocks per workgroup once there are more than 32 queries (one at head_dim > 128)
+  const int nqb = a->Sq > kQB && a->D <= 128 ? 2 : 1;
   const dim3 grid(static_cast<unsigned>(cdiv(a->Sq, kQB * nqb) * p.passes), static_cast<unsigned>(a->Hkv),
                   static_cast<unsigned>(a->B));
   const bool bf = a->dtype == FADE_DTYPE_BF16;
@@ -751,7 +778,9 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   // the smallest instance whose capacity covers the head_dim
   if (a->D <= 32) { FADE_PREFILL_LAUNCH(32) }
   else if (a->D <= 64) { FADE_PREFILL_LAUNCH(64) }
-  else { FADE_PREFILL_LAUNCH(128) }
+  else if (a->D <= 128) { FADE_PREFILL_LAUNCH(128) }
+  else if (bf) hipLaunchKernelGGL((prefill_kernel<256, 1, true>), grid, dim3(kThreads), 0, as_stream(stream), p);
+  else hipLaunchKernelGGL((prefill_kernel<256, 1, false>), grid, dim3(kThreads), 0, as_stream(stream), p);
 #undef FADE_PREFILL_LAUNCH
   return check_launch("fade_tiered_prefill_attn");
 }

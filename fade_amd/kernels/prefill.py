@@ -26,7 +26,7 @@ class TieredPrefillPlan:
     """Validated launch for fixed tensors; ``run()`` enqueues one kernel.
 
     Args:
-        q: [B, Hq, Sq, D] fp16 or bf16 queries of the chunk; D a multiple of 8 up to 128.
+        q: [B, Hq, Sq, D] fp16 or bf16 queries of the chunk; D a multiple of 8 up to 256.
             Every other 16-bit tensor (tiers, scales, the output) is of q's dtype.
         chunk: (K, V) [B, Hkv, Sq, D] fp16, the chunk's own keys/values
             (with ``mask`` ``"top_left"`` / ``"none"``: any length, or None).

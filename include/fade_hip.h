@@ -396,7 +396,7 @@ int fade_tiered_decode_attn_noalloc(const fade_decode_args* args, void* stream);
  * padded along S (row b uses the first lens[3b+0..2] tokens of sink / middle /
  * recent); the middle tier is FADE_MID_SYM 4-bit (padded, or paged: mid.pages,
  * separate pools, pages_per_row * 64 >= mid.len; D % 32 == 0), FADE_MID_FP16
- * or FADE_MID_NONE.  D a multiple of 8 in [8, 128], Hq/Hkv <= 8.  `order` (optional, device int32 [B]) lists batch rows in the
+ * or FADE_MID_NONE.  D a multiple of 8 in [8, 256], Hq/Hkv <= 8.  `order` (optional, device int32 [B]) lists batch rows in the
  * order their workgroups are dispatched (longest first balances the tail).
  * Replaces the reference's prefill path: update() returning the materialized
  * tiers (fade/cache.py:347-379,683-842) followed by causal SDPA in the model. */

@@ -151,6 +151,12 @@ def test_prefill_argument_errors():
     a.Hq, a.Hkv = 32, 8
     assert lib.fade_tiered_prefill_attn(ctypes.byref(a), None) == _lib.FADE_EINVAL
     assert b"null q, out or lens" in lib.fade_hip_last_error()
+    a.D = 264
+    assert lib.fade_tiered_prefill_attn(ctypes.byref(a), None) == _lib.FADE_EINVAL
+    assert b"head_dim must be a multiple of 8 in [8, 256]" in lib.fade_hip_last_error()
+    a.D = 256  # taken: the next check is the pointers
+    assert lib.fade_tiered_prefill_attn(ctypes.byref(a), None) == _lib.FADE_EINVAL
+    assert b"null q, out or lens" in lib.fade_hip_last_error()
 
 
 def test_argument_errors_come_back_as_value_errors():

@@ -165,7 +165,7 @@ def test_decode_bf16_refusals(dev):
         tiered_decode_attention(q, None, MiddleTier("asym", kq, vq, ks, vs, kz, vz, group=32), None)
 
 
-@pytest.mark.parametrize("D,Hq,Hkv", [(128, 32, 8), (64, 28, 4)])
+@pytest.mark.parametrize("D,Hq,Hkv", [(128, 32, 8), (64, 28, 4), (256, 8, 4)])
 @pytest.mark.parametrize("with_mid", [True, False])
 def test_prefill_bf16(dev, D, Hq, Hkv, with_mid):
     """Ragged chunk prefill on bf16 tiers: the middle tier dequantized in the kernel

@@ -6,8 +6,9 @@ tests/test_fused_blackwell.py:50-109, its INT4 SDPA tests D = 32,
 tests/test_perf.py:17, its model tests D = 16, tests/test_models.py:43-49).
 Here every multiple of 8 up to 256 is taken: decode at D != 128 runs the
 portable kernel (every middle format; instances of capacity 32/64/128/256,
-channels past D idle), the MFMA prefill kernel takes D up to 128 (a packed
-middle tier in place at multiples of 32, its fp16 dequantization otherwise).  Tolerance: max-abs 2e-3 against fp32 attention over the oracle's
+channels past D idle), the MFMA prefill kernel takes D up to 256 (a packed
+middle tier in place at multiples of 32, its fp16 dequantization otherwise;
+D > 128 on the capacity-256 instance, one wave per SIMD).  Tolerance: max-abs 2e-3 against fp32 attention over the oracle's
 dequantized tiers, as for D = 128.
 """
 
@@ -128,7 +129,7 @@ def _ragged(dev, D, B, Hq, Hkv, Sq, rows, seed, fmt="int4"):
     return _t(dev, qs), (_t(dev, chunk_k), _t(dev, chunk_v)), sink, mid, rec, lens, ref
 
 
-@pytest.mark.parametrize("D", [32, 64, 16, 48, 80, 96])
+@pytest.mark.parametrize("D", [32, 64, 16, 48, 80, 96, 256, 160, 200, 136])
 @pytest.mark.parametrize("fmt", ["int4", "fp16"])
 @pytest.mark.parametrize(
     "B,Hq,Hkv,Sq,rows",

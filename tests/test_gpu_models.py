@@ -135,10 +135,10 @@ def _steps(model, cache, ids, n, chunk):
     return logits
 
 
-@pytest.mark.parametrize("head_dim,heads,kv_heads", [(16, 4, 2), (80, 8, 2), (96, 8, 4), (48, 6, 2)])
+@pytest.mark.parametrize("head_dim,heads,kv_heads", [(16, 4, 2), (80, 8, 2), (96, 8, 4), (48, 6, 2), (256, 8, 4)])
 def test_fused_logits_match_materialized_other_head_dims(dev, head_dim, heads, kv_heads):
-    """Head dims outside 32/64/128/256 (the reference's tiny models use 16; phi-2 80,
-    phi-3 96): prompt, INT4 middle, decode steps and a chunk through the fused kernels,
+    """Head dims other than 128 (the reference's tiny models use 16; phi-2 80,
+    phi-3 96, Gemma 256): prompt, INT4 middle, decode steps and a chunk through the fused kernels,
     against the model's SDPA over the same cache's materialized tiers."""
     print(f"case fused vs materialized head_dim {head_dim} heads {heads}/{kv_heads}", flush=True)
     model, cfg = _tiny_fp16(dev, "fade", heads, kv_heads, head_dim)
