@@ -1066,12 +1066,19 @@ class TieredKVCache(DynamicCache):
             ns_c = 0 if sink is None else int(sink[0].shape[-2])
             nm_c = 0 if midp is None else int(midp[0].shape[-2])
             nr_c = 0 if rec is None else int(rec[0].shape[-2])
-            S = ns_c + nm_c + nr_c
             pos_parts = [p for p in (
                 None if sink is None else (st.sink_pos if st.sink_k is not None else st.fp16_pos[:ns_c]),
                 st.int4_pos, None if rec is None else st.fp16_pos[rec_start:],
             ) if p is not None]
             pos_old = torch.cat(pos_parts).to(torch.long).contiguous()
+            # The reference's zero-padded per-sequence layout keeps row 0's positions
+            # (fade/cache.py:1161-1167), fewer than the padded rows where row 0 is not the
+            # longest.  Its next reassignment indexes the concatenated tiers by position
+            # index, so token j is row j of sink | middle | recent with position pos_old[j]
+            # (fade/cache.py:701-713,1084,1124-1133); the gather maps j the same way.
+            S = int(pos_old.shape[0])
+            if S > ns_c + nm_c + nr_c:
+                raise ValueError(f"layer {layer_idx}: {S} positions for {ns_c + nm_c + nr_c} rows")
             table_rows = st.next_position
             row_len = None
         else:
@@ -1141,6 +1148,10 @@ class TieredKVCache(DynamicCache):
         buf = (torch.zeros(B, H, cap, D, **kd), torch.zeros(B, H, cap, D, **kd))
         mid = (torch.zeros(B, H, cm, D, **kd), torch.zeros(B, H, cm, D, **kd)) if cm else None
         evicting = any(f + i4 < (S if row_len is None else row_len[b]) for b, (f, i4, _) in enumerate(rows_counts))
+        if evicting and row_len is None and S != ns_c + nm_c + nr_c:
+            # the reference un-RoPEs the padded rows with the S positions' tables, which
+            # fails on the shapes (fade/cache.py:1108-1110); the host path raises as well
+            raise NotImplementedError("eviction over a zero-padded layout whose positions are row 0's")
         tab = self._rope_tables(max(table_rows, S), dev) if evicting else None
         src_lens = st.lens
 
@@ -1220,7 +1231,7 @@ class TieredKVCache(DynamicCache):
         st = self._layers[layer_idx]
         if (self.dtype != torch.float16 or not isinstance(self._quant_backend, SymmetricINT4Backend) or self.middle_v_bits != 4
                 or st.int2_kq is not None or st.backend_k is not None or st.lens is not None
-                or self.page_pool is not None or st._padded_rows):
+                or self.page_pool is not None):
             return False
         kept = {f: getattr(st, f) for f in ("sink_k", "sink_v", "sink_pos", "_fp16_buf_k", "_fp16_buf_v",
                                             "_fp16_buf_pos", "_fp16_len", "_compressed_bytes")}

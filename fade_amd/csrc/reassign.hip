@@ -304,14 +304,16 @@ FADE_API int fade_reassign_gather(const FadeReassignArgs* args, void* stream) {
   if (args == nullptr) return einval("%s: null argument", fn);
   const FadeReassignArgs& a = *args;
   if (a.D <= 0 || a.D % 2 != 0 || a.D > 512) return einval("%s: head_dim must be even and <= 512", fn);
-  if (a.B < 0 || a.H < 0 || a.S < 0 || a.n_sink_old < 0 || a.n_mid_old < 0 || a.n_rec_cap < 0 ||
-      (a.src_lens == nullptr && a.n_sink_old + a.n_mid_old > a.S))
+  if (a.B < 0 || a.H < 0 || a.S < 0 || a.n_sink_old < 0 || a.n_mid_old < 0 || a.n_rec_cap < 0)
     return einval("%s: inconsistent tier lengths", fn);
   if (a.dst == nullptr || a.newpos == nullptr || a.src_of == nullptr || a.counts == nullptr || a.pos_old == nullptr)
     return einval("%s: null plan pointer", fn);
   if (a.n_mid_old > 0 && (a.mid_kq == nullptr || a.mid_ks == nullptr || a.mid_vq == nullptr || a.mid_vs == nullptr))
     return einval("%s: null middle tier", fn);
-  const int64_t rec_rows = a.src_lens != nullptr ? a.n_rec_cap : a.S - a.n_sink_old - a.n_mid_old;
+  // without src_lens, token j >= sink + middle rows is recent row j - sink - middle: none
+  // when S is at most sink + middle (a zero-padded layout whose positions are row 0's)
+  const int64_t rec_tail = a.S - a.n_sink_old - a.n_mid_old;
+  const int64_t rec_rows = a.src_lens != nullptr ? a.n_rec_cap : (rec_tail > 0 ? rec_tail : 0);
   if ((a.n_sink_old > 0 && (a.sink_k == nullptr || a.sink_v == nullptr)) ||
       (rec_rows > 0 && (a.rec_k == nullptr || a.rec_v == nullptr)))
     return einval("%s: null fp16 tier", fn);

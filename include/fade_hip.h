@@ -219,8 +219,12 @@ int fade_reassign_plan(const int64_t* tiers, int64_t tiers_row_stride, int64_t r
  * tables). */
 typedef struct FadeReassignArgs {
   int64_t B, H, D, S;
-  int64_t n_sink_old, n_mid_old; /* recent = S - sink - middle; with src_lens: the capacities
-                                    (rows of the sink / middle tensors) */
+  int64_t n_sink_old, n_mid_old; /* rows of the sink / middle tensors.  Without src_lens,
+                                    token j of the position order is sink row j, middle row
+                                    j - sink or recent row j - sink - middle; S may be below
+                                    sink + middle (+ recent) rows, as in the reference's
+                                    zero-padded per-sequence layout, whose positions are row
+                                    0's (fade/cache.py:1161-1167) */
   const int32_t* src_lens;       /* optional device [B][3]: each row's current sink / middle /
                                     recent tokens (a ragged layout); row b's position order is
                                     its own sink | middle | recent, tokens past them absent */

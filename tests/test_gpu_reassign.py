@@ -127,9 +127,7 @@ def test_reassign_int2_falls_back(dev):
 def test_per_sequence_device_matches_host(dev, tiers_on, budgets):
     """The reference's per-sequence mode (rows zero-padded to the longest) on the device
     path equals the host path (the reference's op sequence) field for field, bit for bit,
-    with eviction in some rows or all, and after later appends.  (One round: the padded
-    layout keeps row 0's positions, so rows of different lengths cannot be reassigned
-    per sequence again, on either path.)"""
+    with eviction in some rows or all, and after later appends."""
     print(f"case per-sequence device vs host tiers_on={tiers_on} budgets={budgets}", flush=True)
     B, H = 3, 2
     host, devc = _pair(n_sink=4, recent_window=16, int4_budget=None, int2_budget=0)
@@ -147,6 +145,63 @@ def test_per_sequence_device_matches_host(dev, tiers_on, budgets):
     for rnd in range(2):
         _append((host, devc), B, H, 5, 23 + rnd, dev)
         _same(host, devc, f"append {rnd}")
+    kh, vh = host._materialize(0)
+    kd, vd = devc._materialize(0)
+    assert torch.equal(kh, kd) and torch.equal(vh, vd)
+
+
+@pytest.mark.parametrize("case,tiers_on", [("mismatch_keep", "cpu"), ("mismatch_keep", "cuda"),
+                                           ("match_evict", "cpu"), ("match_evict", "cuda"), ("mismatch_evict", "cpu")])
+def test_per_sequence_second_reassignment(dev, case, tiers_on):
+    """A second per-sequence reassignment of a zero-padded layer.  The padded layout
+    keeps row 0's positions (fade/cache.py:1161-1167); where row 0 is not the longest
+    they are fewer than the padded rows, and the reference's next call indexes the
+    concatenated tiers by position index (token j = row j of sink | middle | recent,
+    fade/cache.py:701-713,1084,1124-1133).  The device path (plan + gather) must equal
+    the host path bit for bit; eviction over mismatched lengths fails in the reference
+    (fade/cache.py:1108-1110) and raises on both paths, the layer untouched."""
+    print(f"case per-sequence second reassignment {case} tiers_on={tiers_on}", flush=True)
+    B, H = 3, 2
+    host, devc = _pair(n_sink=4, recent_window=16, int4_budget=None, int2_budget=0)
+    _append((host, devc), B, H, 150, 31, dev)
+    rng = np.random.default_rng(32)
+    S = host.get_seq_length(0)
+    first = (30, None, 70) if case.startswith("mismatch") else (None, None, None)
+    tiers = torch.stack([_assign_one_layer(S, torch.from_numpy(rng.exponential(size=S).astype(np.float32)),
+                                           4, 16, first[b], 0) for b in range(B)])
+    for c in (host, devc):
+        c.apply_tier_assignment_per_sequence(0, tiers.clone())
+    _same(host, devc, "first reassignment")
+    _append((host, devc), B, H, 7, 33, dev)
+    _same(host, devc, "append")
+    k_full = host._all_in_position_order(0)[0]
+    S2 = int(host._all_in_position_order(0)[2].shape[0])
+    assert (S2 < int(k_full.shape[-2])) == case.startswith("mismatch")
+    second = (None, None, None) if case == "mismatch_keep" else (20, 45, 90)
+    tiers2 = torch.stack([_assign_one_layer(S2, torch.from_numpy(rng.exponential(size=S2).astype(np.float32)),
+                                            4, 16, second[b], 0) for b in range(B)])
+    if tiers_on == "cuda":
+        tiers2 = tiers2.to(dev)
+    taken = []
+    ragged = devc._apply_per_sequence_ragged
+
+    def spy(*args):
+        taken.append(1)
+        return ragged(*args)
+
+    devc._apply_per_sequence_ragged = spy
+    if case == "mismatch_evict":
+        for c in (host, devc):
+            with pytest.raises(ValueError):
+                c.apply_tier_assignment_per_sequence(0, tiers2.clone())
+        _same(host, devc, "refused")
+        return
+    for c in (host, devc):
+        c.apply_tier_assignment_per_sequence(0, tiers2.clone())
+    assert taken, "device path not taken"
+    _same(host, devc, "second reassignment")
+    _append((host, devc), B, H, 5, 34, dev)
+    _same(host, devc, "append after the second reassignment")
     kh, vh = host._materialize(0)
     kd, vd = devc._materialize(0)
     assert torch.equal(kh, kd) and torch.equal(vh, vd)
