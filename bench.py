@@ -390,12 +390,21 @@ def per_sequence_case(dev, n_inst: int = 4):
     return out
 
 
+def gqa_cfg(B: int = 8, S: int = 4096, Hq: int = 28, Hkv: int = 4):
+    """Config 3's model shape (Hq=28, Hkv=4: 7 query heads per kv head), reference INT4
+    middle, sink 4, recent 128."""
+    return type("Cfg", (), dict(B=B, Hq=Hq, Hkv=Hkv, S=S, D=128, n_sink=4, recent=128, mid=S - 132))
+
+
+# --pmc-config 3: the GQA-7 decode at B=16, S=8192 (the eight-head one-pass instance)
+PMC_CONFIGS = {1: CONFIGS[1], 2: CONFIGS[2], 3: gqa_cfg(16, 8192)}
+
+
 def gqa7_decode_case(dev, B: int = 8, S: int = 4096, Hq: int = 28, Hkv: int = 4):
-    """Decode at config 3's model shape (Hq=28, Hkv=4: 7 query heads per kv head,
-    reference INT4 middle, sink 4, recent 128; B=8, S=4096 by default): the INT4
-    kernel with all heads of a kv head in one pass (the default) against the
-    general matrix-core kernel (kernel=3)."""
-    cfg = type("Cfg", (), dict(B=B, Hq=Hq, Hkv=Hkv, S=S, D=128, n_sink=4, recent=128, mid=S - 132))
+    """Decode at config 3's model shape (B=8, S=4096 by default): the INT4 kernel with
+    all heads of a kv head in one pass (the default) against the general matrix-core
+    kernel (kernel=3)."""
+    cfg = gqa_cfg(B, S, Hq, Hkv)
     plans = build_instances(cfg, "int4", dev, 1003, N_INSTANCES)
     general = [TieredDecodePlan(*p._keep[:4], kernel=3) for p in plans]
     return plans, general, decode_bytes(cfg, "int4")
@@ -523,6 +532,7 @@ def cpu_baseline(cfg, plans) -> dict:
 COPY_MIB = 256
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_int4_c1_traffic.json")
 TRAFFIC_FILE_C2 = os.path.join(ROOT, "profiles", "decode_c2_32k_traffic.json")
+TRAFFIC_FILE_GQA = os.path.join(ROOT, "profiles", "decode_gqa7_traffic.json")
 
 
 def pmc_pass(steps: int, config: int = 1, fmt: str = "int4") -> int:
@@ -535,7 +545,7 @@ def pmc_pass(steps: int, config: int = 1, fmt: str = "int4") -> int:
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    plans = build_instances(CONFIGS[config], fmt, dev, 1000 + config, N_INSTANCES)
+    plans = build_instances(PMC_CONFIGS[config], fmt, dev, 1000 + config, N_INSTANCES)
     for i in range(steps):
         plans[i % len(plans)].run()
     torch.cuda.synchronize()
@@ -586,7 +596,8 @@ def summarize_pmc(fetch_dir: str, write_dir: str, config: int = 1, fmt: str = "i
     """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the decode kernel, scaled by
     what the same counters read for the copy kernel (which moves COPY_MIB each way).
     Config 1 INT4 goes to TRAFFIC_FILE (the headline line's ``traffic``); config-2
-    formats go to one entry each of TRAFFIC_FILE_C2."""
+    formats go to one entry each of TRAFFIC_FILE_C2, the GQA-7 shape (config 3) to
+    TRAFFIC_FILE_GQA."""
     import csv
 
     def per_kernel(d: str, counter: str):
@@ -620,7 +631,7 @@ def summarize_pmc(fetch_dir: str, write_dir: str, config: int = 1, fmt: str = "i
         out[f"{key}_scale"] = round(factor, 4)
         out[f"{key}_bytes"] = int(dec_kib * 1024 * factor)
     out["hbm_bytes_per_call"] = out["fetch_bytes"] + out["write_bytes"]
-    out["algorithmic_bytes_per_call"] = decode_bytes(CONFIGS[config], fmt)
+    out["algorithmic_bytes_per_call"] = decode_bytes(PMC_CONFIGS[config], fmt)
     out["traffic_ratio"] = round(out["hbm_bytes_per_call"] / out["algorithmic_bytes_per_call"], 4)
     os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
     if config == 1 and fmt == "int4":
@@ -628,12 +639,13 @@ def summarize_pmc(fetch_dir: str, write_dir: str, config: int = 1, fmt: str = "i
             json.dump(out, f, indent=1)
             f.write("\n")
     else:
+        path = TRAFFIC_FILE_C2 if config == 2 else TRAFFIC_FILE_GQA
         allf = {}
-        if os.path.exists(TRAFFIC_FILE_C2):
-            with open(TRAFFIC_FILE_C2) as f:
+        if os.path.exists(path):
+            with open(path) as f:
                 allf = json.load(f)
         allf[f"c{config}_{fmt}"] = out
-        with open(TRAFFIC_FILE_C2, "w") as f:
+        with open(path, "w") as f:
             json.dump(allf, f, indent=1, sort_keys=True)
             f.write("\n")
     print(json.dumps(out))
@@ -653,8 +665,8 @@ def main() -> int:
                     help="--steps config-4 prefill calls only, for rocprofv3 --pmc SQ counters")
     ap.add_argument("--portable-pass", type=int, metavar="HEAD_DIM",
                     help="--steps calls of the portable decode kernel at HEAD_DIM (32, 64, 256), for rocprofv3")
-    ap.add_argument("--pmc-config", type=int, default=1, choices=(1, 2),
-                    help="config of --pmc-pass / --summarize-pmc (default 1)")
+    ap.add_argument("--pmc-config", type=int, default=1, choices=(1, 2, 3),
+                    help="config of --pmc-pass / --summarize-pmc (default 1; 3: GQA-7 at B=16, S=8192)")
     ap.add_argument("--pmc-fmt", default="int4", help="middle format of --pmc-pass / --summarize-pmc (default int4)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc output folders into " + os.path.relpath(TRAFFIC_FILE, ROOT))
