@@ -426,15 +426,16 @@ def copy_peak(dev, stream) -> float:
     return 2 * (1 << 30) * 10 / (a.elapsed_time(b) * 1e-3) / 1e9
 
 
-def prefill_case(dev, seed: int = 1004):
+def prefill_case(dev, seed: int = 1004, B: int = 32, Hq: int = 32, Hkv: int = 8, D: int = 128, Lmax: int = 16384):
     """Config 4: 32 rows, cached lengths ~U[512, 16384], 128-token chunk, 32/8 heads, reference INT4
     middle tier (sink 4, recent 64).  Codes, scales and fp16 tiers are random device tensors (the
-    kernel's timing does not depend on their values); rows are dispatched longest first."""
+    kernel's timing does not depend on their values); rows are dispatched longest first.  The
+    keyword arguments give other shapes of the same kind (the head_dim-256 line)."""
     from fade_amd.kernels.prefill import TieredPrefillPlan
 
-    B, Hq, Hkv, D, Sq, ns, nr = 32, 32, 8, 128, 128, 4, 64
+    Sq, ns, nr = 128, 4, 64
     gen = torch.Generator().manual_seed(seed)
-    L = torch.randint(512, 16385, (B,), generator=gen)
+    L = torch.randint(512, Lmax + 1, (B,), generator=gen)
     nm = L - ns - nr
     cap = int(nm.max())
     g = torch.Generator(device=dev).manual_seed(seed)
@@ -751,6 +752,16 @@ def main() -> int:
             "us": round(pmean * 1e3, 1), "TFLOPs": round(pflops / (pmean * 1e-3) / 1e12, 1),
             "mfma_frac_f16_dense": round(pflops / (pmean * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 3),
             "useful_flops": pflops, "GBps": round(pbytes / (pmean * 1e-3) / 1e9, 1),
+        }
+        del pf
+        # the same kind of ragged chunk prefill at head_dim 256 (Gemma-style 16/8 heads;
+        # 16 rows of L ~U[512, 8192]): the capacity-256 instance at one wave per SIMD
+        pf, pflops, pbytes = prefill_case(dev, 1005, B=16, Hq=16, Hkv=8, D=256, Lmax=8192)
+        _, _, pmean, _ = time_plans([pf], max(10, args.steps // 10), 40, stream)
+        extra["c4_prefill_ragged_d256_16_8"] = {
+            "us": round(pmean * 1e3, 1), "TFLOPs": round(pflops / (pmean * 1e-3) / 1e12, 1),
+            "mfma_frac_f16_dense": round(pflops / (pmean * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 3),
+            "useful_flops": pflops,
         }
         del pf
         torch.cuda.empty_cache()

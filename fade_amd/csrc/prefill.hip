@@ -9,7 +9,8 @@
 // groups of 4 waves (interleaved: wave w belongs to group w % NQB), group q
 // serving the q-th 32-query block; wave w of a group serves query head kvh*G + 4*pass + w (G = Hq/Hkv <= 8: one pass of up
 // to 4 heads for G <= 4, two passes for G = 5..8), its 32 query rows as one
-// 32-row M tile.  With two groups, the first stages and dequantizes each
+// 32-row M tile.  With G = 1 or 2 the four waves of a group cover 4 or 2
+// query blocks instead (wave w: head w % G of block w / G), so no wave idles.  With two groups, the first stages and dequantizes each
 // tile's K and the second its V, so one dequantization serves 64 queries per
 // head.  The row's key
 // sequence is walked in 64-token tiles that never straddle a tier (sink,
@@ -90,6 +91,7 @@ struct PParams {
   int64_t B, Hq, Hkv, Sq;
   int G;       // query heads per kv head (Hq / Hkv), <= 8
   int passes;  // workgroups per (query block, kv head): ceil(G / 4)
+  int hpw;     // query heads per group of 4 waves: 4, or G = 1 / 2 (then 4 / 2 query blocks per group)
   const uint16_t* q;
   int64_t q_sb, q_sh, q_ss;
   uint16_t* out;
@@ -204,6 +206,10 @@ void prefill_kernel(PParams p) {
   const bool do_k = NQB == 1 || qblk == 0, do_v = NQB == 1 || qblk == NQB - 1;
   const int n16 = lane & 15, g = lane >> 4;
   const int G = p.G - h0 < 4 ? p.G - h0 : 4;  // query heads this workgroup serves
+  // wave wq of a group serves head wq % hpw of the group's query block wq / hpw
+  const int hpw = p.hpw, lhpw = hpw == 4 ? 2 : (hpw == 2 ? 1 : 0);
+  const int qpg = 4 >> lhpw;                     // query blocks per group
+  const int wh = wq & (hpw - 1), wsub = wq >> lhpw;
   const int64_t bkv = b * p.Hkv + kvh;
   // per-row tier lengths, clamped to the padded capacities (no read past a tier)
   auto clampi = [](int x, int64_t cap) { return x < 0 ? 0 : (x > cap ? static_cast<int>(cap) : x); };
@@ -211,9 +217,9 @@ void prefill_kernel(PParams p) {
   const int nm = clampi(__builtin_amdgcn_readfirstlane(p.lens[3 * b + 1]), p.mid_cap);
   const int nr = clampi(__builtin_amdgcn_readfirstlane(p.lens[3 * b + 2]), p.recent_cap);
   const int Sq = static_cast<int>(p.Sq);
-  const int jw = qb * kQB * NQB;                       // the workgroup's first query
-  const int jwn = Sq - jw < kQB * NQB ? Sq - jw : kQB * NQB;  // its queries
-  const int j0 = jw + kQB * qblk;                      // this wave's query block
+  const int jw = qb * kQB * NQB * qpg;                 // the workgroup's first query
+  const int jwn = Sq - jw < kQB * NQB * qpg ? Sq - jw : kQB * NQB * qpg;  // its queries
+  const int j0 = jw + kQB * (qblk + NQB * wsub);       // this wave's query block
   const int mode = p.mask_mode;
   // chunk keys any query of the workgroup can see (bottom-right: chunk keys 0..j)
   const int cv = mode == FADE_MASK_BOTTOM_RIGHT ? jw + jwn : p.chunk_len;
@@ -477,8 +483,8 @@ void prefill_kernel(PParams p) {
   // ---- query fragments: B operand of S^T = K Q^T; lane (n32, h) holds query
   // row j0 + n32, channels 16 ks + 8 h .. + 7 in the stored order ----
   const int n32 = lane & 31, h = lane >> 5;
-  const bool active = wq < G && j0 < Sq;
-  const int64_t hq = kvh * p.G + h0 + (active ? wq : 0);
+  const bool active = wh < G && j0 < Sq;
+  const int64_t hq = kvh * p.G + h0 + (active ? wh : 0);
   u32x4 qf[NKS];
   {
     const int j = j0 + n32;
@@ -741,6 +747,8 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   p.Sq = a->Sq;
   p.G = static_cast<int>(a->Hq / a->Hkv);
   p.passes = (p.G + 3) / 4;
+  p.hpw = p.G >= 3 ? 4 : p.G;
+  const int qpg = 4 / p.hpw;  // query blocks per group of 4 waves
   p.q = static_cast<const uint16_t*>(a->q);
   p.q_sb = a->q_sb; p.q_sh = a->q_sh; p.q_ss = a->q_ss;
   p.out = static_cast<uint16_t*>(a->out);
@@ -765,9 +773,10 @@ FADE_API int fade_tiered_prefill_attn(const fade_prefill_args* a, void* stream) 
   p.mask_mode = a->mask_mode;
   p.chunk_len = static_cast<int>(a->chunk.len);
   p.D = static_cast<int>(a->D);
-  // two query blocks per workgroup once there are more than 32 queries (one at head_dim > 128)
-  const int nqb = a->Sq > kQB && a->D <= 128 ? 2 : 1;
-  const dim3 grid(static_cast<unsigned>(cdiv(a->Sq, kQB * nqb) * p.passes), static_cast<unsigned>(a->Hkv),
+  // two groups of 4 waves once one group's query blocks do not cover the chunk
+  // (one at head_dim > 128)
+  const int nqb = a->Sq > kQB * qpg && a->D <= 128 ? 2 : 1;
+  const dim3 grid(static_cast<unsigned>(cdiv(a->Sq, kQB * nqb * qpg) * p.passes), static_cast<unsigned>(a->Hkv),
                   static_cast<unsigned>(a->B));
   const bool bf = a->dtype == FADE_DTYPE_BF16;
 #define FADE_PREFILL_LAUNCH(DD)                                                                                        \

@@ -78,6 +78,9 @@ def _ragged(dev, B, Hq, Hkv, Sq, rows, seed, with_mid=True):
         (2, 28, 4, 70, [(4, 500, 64), (2, 130, 20)]),  # G=7 (Qwen2.5-7B heads): two head passes
         (1, 40, 8, 33, [(4, 200, 10)]),  # G=5: a second pass of one head
         (1, 16, 2, 96, [(4, 300, 64)]),  # G=8
+        (2, 8, 4, 128, [(4, 600, 64), (2, 70, 10)]),  # G=2: each group of 4 waves covers 2 query blocks
+        (1, 4, 4, 200, [(4, 333, 64)]),  # MHA: 4 query blocks per group, two groups, a partial last block
+        (2, 6, 2, 100, [(3, 250, 64), (4, 64, 1)]),  # G=3: 4-head groups with one idle wave
     ],
 )
 def test_tiered_prefill_ragged(dev, B, Hq, Hkv, Sq, rows):
