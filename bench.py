@@ -809,6 +809,20 @@ def main() -> int:
         }
         del g2, gg
         torch.cuda.empty_cache()
+        # config 1's shape at head_dim 64: the general matrix-core kernel (the automatic
+        # choice at this head_dim) against the portable one (kernel=1)
+        c64 = type("Cfg", (), dict(B=16, Hq=32, Hkv=8, S=8192, D=64, n_sink=4, recent=64, mid=8192 - 68))
+        m64 = build_instances(c64, "int4", dev, 1006, N_INSTANCES)
+        v64 = [TieredDecodePlan(*pl._keep[:4], kernel=1) for pl in m64]
+        mmean, vmean = graph_us(m64) * 1e-3, graph_us(v64) * 1e-3
+        b64 = decode_bytes(c64, "int4")
+        extra["c1_shape_d64_decode_int4"] = {
+            "us": round(mmean * 1e3, 2), "us_portable_kernel": round(vmean * 1e3, 2), "bytes": b64,
+            "GBps": round(b64 / (mmean * 1e-3) / 1e9, 1),
+            "frac_of_peak": round(b64 / (mmean * 1e-3) / 1e9 / HBM_PEAK_GBPS, 3),
+        }
+        del m64, v64
+        torch.cuda.empty_cache()
         # GQA 8 (Llama-3-70B / Qwen2-72B heads: 64 / 8) at config 1's batch and length
         g2, gg, gb = gqa7_decode_case(dev, B=16, S=8192, Hq=64, Hkv=8)
         g2mean = graph_us(g2) * 1e-3

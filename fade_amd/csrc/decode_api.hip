@@ -198,7 +198,9 @@ enum class Kern { kValu, kMfma, kInt4 };
 Kern choose(const fade_decode_args* a, const Params& p) {
   if (a->kernel == 1) return Kern::kValu;
   if (a->kernel != 3 && int4_supports(p)) return Kern::kInt4;
-  if (!p.bf16 && mfma_supports(p)) return Kern::kMfma;  // the general kernel reads fp16 only
+  // the general kernel reads fp16 only and takes no per-row lengths (auto falls back
+  // to the portable kernel there; kernels 2 and 3 report the error)
+  if (!p.bf16 && mfma_supports(p) && (a->lens == nullptr || a->kernel >= 2)) return Kern::kMfma;
   return Kern::kValu;
 }
 

@@ -46,11 +46,25 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8;
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kTileT = 64;
-constexpr int kStageK = 0, kStageV = 4096, kStageVS = 8192;
-constexpr int kStageBytes = 8192 + 256;  // the 2-byte DMA writes one dword per lane
 constexpr float kQMax = 32000.0f;
 constexpr float kNegBig = -1.0e30f;  // running-max sentinel (finite: no inf-inf guards)
-constexpr int kV16Pitch = 136;  // halfs per staged fp16 V row (16 rows = 4352 B fit the V tile buffer)
+
+// Head-dim geometry (DK = 128 or 64).  A stage holds one packed tile: K codes
+// (64 rows of DK/2 bytes) | V codes (the same) | V scales (64 dwords).  Lane
+// group g of a QK^T MFMA covers channels DK/4 g .. + DK/4 - 1 (two int8
+// k-steps of 64 at DK = 128, one at 64); PV has DK/16 column blocks.
+template <int DK>
+struct Geo {
+  static constexpr int kRowB = DK / 2;                 // packed bytes per token
+  static constexpr int kUnits = DK / 32;               // 16-byte units per packed row
+  static constexpr int kStageK = 0, kStageV = 32 * DK, kStageVS = 64 * DK;
+  static constexpr int kStageBytes = 64 * DK + 256;    // the 2-byte DMA writes one dword per lane
+  static constexpr int kKS = DK / 64;                  // int8 QK^T k-steps
+  static constexpr int kCPL = DK / 4;                  // channels per lane group
+  static constexpr int kNC = DK / 16;                  // PV column blocks
+  static constexpr int kV16Pitch = DK + 8;             // halfs per staged fp16 V row (16 rows fit the V region)
+  static constexpr int kOpsPerStage = 2 * kUnits + 1;  // direct loads per packed tile
+};
 
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
@@ -89,7 +103,7 @@ struct FpTok {  // one fp16 token row (K and V pointers)
 };
 
 // Row pointers of virtual fp16 token f: sink, (fp16 middle), recent.
-template <bool MID_F16>
+template <bool MID_F16, int DK>
 __device__ __forceinline__ FpTok fp16_token(const Params& p, int64_t b, int64_t kvh, int64_t f) {
   FpTok r;
   const int64_t ns = p.sink.len;
@@ -102,8 +116,8 @@ __device__ __forceinline__ FpTok fp16_token(const Params& p, int64_t b, int64_t 
   if (MID_F16) {
     if (f < p.mid.len) {
       const int64_t row = (b * p.Hkv + kvh) * p.mid.len + f;
-      r.k = reinterpret_cast<const uint16_t*>(p.mid.k_codes) + row * kD;
-      r.v = reinterpret_cast<const uint16_t*>(p.mid.v_codes) + row * kD;
+      r.k = reinterpret_cast<const uint16_t*>(p.mid.k_codes) + row * DK;
+      r.v = reinterpret_cast<const uint16_t*>(p.mid.v_codes) + row * DK;
       return r;
     }
     f -= p.mid.len;
@@ -113,8 +127,11 @@ __device__ __forceinline__ FpTok fp16_token(const Params& p, int64_t b, int64_t 
   return r;
 }
 
-template <bool MID_F16>
+template <bool MID_F16, int DK>
 __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
+  using GE = Geo<DK>;
+  constexpr int kStageK = GE::kStageK, kStageV = GE::kStageV, kStageVS = GE::kStageVS, kStageBytes = GE::kStageBytes;
+  constexpr int kKS = GE::kKS, kCPL = GE::kCPL, kNC = GE::kNC, kV16Pitch = GE::kV16Pitch;
   const int split = blockIdx.x;
   const int64_t kvh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -132,28 +149,28 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t ring1[kWaves][kStageBytes];
   __shared__ __attribute__((aligned(16))) float alpha_s[kWaves][16];
   __shared__ float red_m[kWaves][16], red_l[kWaves][16];
-  __shared__ __attribute__((aligned(16))) uint16_t q16_s[16][kD + 8];
+  __shared__ __attribute__((aligned(16))) uint16_t q16_s[16][DK + 8];
 
-  // ---- query operands (lane = head n16, k-group grp) ----
+  // ---- query operands (lane = head n16, k-group grp: channels kCPL grp ..) ----
   const bool hvalid = n16 < G;
-  uint4 qraw[4];
+  uint4 qraw[kCPL / 8];
   {
-    const uint16_t* qp = p.q + b * p.q_sb + (kvh * G + (hvalid ? n16 : 0)) * p.q_sh + 32 * grp;
+    const uint16_t* qp = p.q + b * p.q_sb + (kvh * G + (hvalid ? n16 : 0)) * p.q_sh + kCPL * grp;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) qraw[c] = hvalid ? ldg16(qp + 8 * c) : make_uint4(0, 0, 0, 0);
+    for (int c = 0; c < kCPL / 8; ++c) qraw[c] = hvalid ? ldg16(qp + 8 * c) : make_uint4(0, 0, 0, 0);
   }
   // fp16 query rows for the fp16 tiles' QK^T (B operand read from LDS when needed)
   if (wave == 0) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) *reinterpret_cast<uint4*>(&q16_s[n16][32 * grp + 8 * c]) = qraw[c];
+    for (int c = 0; c < kCPL / 8; ++c) *reinterpret_cast<uint4*>(&q16_s[n16][kCPL * grp + 8 * c]) = qraw[c];
   }
-  i32x4 qd_hi[2], qd_lo[2];  // int8 digits of q * k_scale for the packed middle
+  i32x4 qd_hi[kKS], qd_lo[kKS];  // int8 digits of q * k_scale for the packed middle
   int corr = 0;
   float qscale = 0.0f;
   if (!MID_F16 && M > 0) {
-    float qf[32];
+    float qf[kCPL];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < kCPL / 8; ++c) {
       const uint32_t u[4] = {qraw[c].x, qraw[c].y, qraw[c].z, qraw[c].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -161,9 +178,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
         qf[8 * c + 2 * e + 1] = h2f(static_cast<uint16_t>(u[e] >> 16));
       }
     }
-    const uint16_t* ksp = p.mid.k_scale + bkv * kD + 32 * grp;
+    const uint16_t* ksp = p.mid.k_scale + bkv * DK + kCPL * grp;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < kCPL / 8; ++c) {
       const uint4 w = ldg16(ksp + 8 * c);
       const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -174,24 +191,24 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
     }
     float mx = 0.0f;
 #pragma unroll
-    for (int d = 0; d < 32; ++d) mx = fmaxf(mx, fabsf(qf[d]));
+    for (int d = 0; d < kCPL; ++d) mx = fmaxf(mx, fabsf(qf[d]));
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float inv = mx > 0.0f ? kQMax / mx : 0.0f;
     qscale = mx > 0.0f ? (mx / kQMax) * p.scale_log2 : 0.0f;
-    int qi[32];
+    int qi[kCPL];
     int sum = 0;
 #pragma unroll
-    for (int d = 0; d < 32; ++d) {
+    for (int d = 0; d < kCPL; ++d) {
       qi[d] = static_cast<int>(rintf(qf[d] * inv));
       sum += qi[d];
     }
     sum += __shfl_xor(sum, 16, 64);
     sum += __shfl_xor(sum, 32, 64);
     corr = 8 * sum;
-    // k-step ks, dword js, byte e  <->  channel 32*grp + 8*(2ks + js/2) + 2e + (js even ? 1 : 0)
+    // k-step ks, dword js, byte e  <->  channel kCPL*grp + 8*(2ks + js/2) + 2e + (js even ? 1 : 0)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < kKS; ++ks) {
 #pragma unroll
       for (int js = 0; js < 4; ++js) {
         uint32_t whi = 0, wlo = 0;
@@ -209,7 +226,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
     }
   } else {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) qd_hi[ks] = qd_lo[ks] = i32x4{0, 0, 0, 0};
+    for (int ks = 0; ks < kKS; ++ks) qd_hi[ks] = qd_lo[ks] = i32x4{0, 0, 0, 0};
   }
 
   // ---- tiles of this split; wave w takes tiles w, w+4, ... ----
@@ -221,9 +238,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   __syncthreads();
   // acc holds 2 * sum(P V) + 48 * sum_{packed tiles}(P'), acc48 the 48 * sum(P') part.
   float m_run = kNegBig, l_lane = 0.0f;
-  f32x4 acc[8];
+  f32x4 acc[kNC];
 #pragma unroll
-  for (int c = 0; c < 8; ++c) acc[c] = f32x4{0, 0, 0, 0};
+  for (int c = 0; c < kNC; ++c) acc[c] = f32x4{0, 0, 0, 0};
   f32x4 acc48 = {0, 0, 0, 0};
 
   uint8_t* my_vtile = ring0[wave];  // fp16 tiles stage V chunks here (before the packed ring starts)
@@ -250,7 +267,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       __builtin_amdgcn_wave_barrier();
       const f32x4 al = *reinterpret_cast<const f32x4*>(&alpha_s[wave][4 * grp]);
 #pragma unroll
-      for (int c = 0; c < 8; ++c) acc[c] *= al;
+      for (int c = 0; c < kNC; ++c) acc[c] *= al;
       acc48 *= al;
     }
     float psum = 0.0f;
@@ -281,11 +298,11 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
     for (int j = 0; j < 4; ++j) {
       const int rloc = 16 * (n16 >> 2) + 4 * j + (n16 & 3);
       const int64_t f = f0 + rloc < F ? f0 + rloc : F - 1;
-      const uint16_t* kr = fp16_token<MID_F16>(p, b, kvh, f).k + 32 * grp;
+      const uint16_t* kr = fp16_token<MID_F16, DK>(p, b, kvh, f).k + kCPL * grp;
       f32x4 c4 = {0, 0, 0, 0};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const f16x8 qb = *reinterpret_cast<const f16x8*>(&q16_s[n16][32 * grp + 8 * ks]);
+      for (int ks = 0; ks < kCPL / 8; ++ks) {
+        const f16x8 qb = *reinterpret_cast<const f16x8*>(&q16_s[n16][kCPL * grp + 8 * ks]);
         c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ldg16(kr + 8 * ks)), qb, c4, 0, 0, 0);
       }
 #pragma unroll
@@ -306,16 +323,16 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       {
         const int r = lane >> 2;  // staged row: g = r/4, i = r%4
         const int64_t tok = f0 + 16 * (r >> 2) + 4 * q + (r & 3);
-        const uint16_t* src = fp16_token<MID_F16>(p, b, kvh, tok < F ? tok : F - 1).v + 32 * (lane & 3);
+        const uint16_t* src = fp16_token<MID_F16, DK>(p, b, kvh, tok < F ? tok : F - 1).v + kCPL * (lane & 3);
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          *reinterpret_cast<uint4*>(vt16 + r * kV16Pitch + 32 * (lane & 3) + 8 * c) = ldg16(src + 8 * c);
+        for (int c = 0; c < kCPL / 8; ++c)
+          *reinterpret_cast<uint4*>(vt16 + r * kV16Pitch + kCPL * (lane & 3) + 8 * c) = ldg16(src + 8 * c);
       }
       __builtin_amdgcn_wave_barrier();
       const f16x4 pa4 = {static_cast<_Float16>(2.0f * pw[q][0]), static_cast<_Float16>(2.0f * pw[q][1]),
                          static_cast<_Float16>(2.0f * pw[q][2]), static_cast<_Float16>(2.0f * pw[q][3])};
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
+      for (int c = 0; c < kNC; ++c) {
         const int d = 16 * c + (n16 ^ 1);
         const f16x4 vb = {__builtin_bit_cast(_Float16, vt16[(4 * grp + 0) * kV16Pitch + d]),
                           __builtin_bit_cast(_Float16, vt16[(4 * grp + 1) * kV16Pitch + d]),
@@ -334,27 +351,39 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   // hit 16 different bank groups:
   //   K unit (row r, chunk q) at 4r + (q ^ ((r >> 4) & 3))
   //   V unit (row r, chunk q) at 4r + (q ^ ((r >> 2) & 3))
+  // (DK = 64: two units per row, unit 2r + q, unswizzled)
   int64_t tau = t0 + wave;
   if (tau < nF) tau += ((nF - tau + kWaves - 1) / kWaves) * kWaves;
   if (!MID_F16 && tau < t1) {
-    const uint8_t* kc = p.mid.k_codes + bkv * M * 64;
-    const uint8_t* vc = p.mid.v_codes + bkv * M * 64;
+    constexpr int kRowB = GE::kRowB;
+    const uint8_t* kc = p.mid.k_codes + bkv * M * kRowB;
+    const uint8_t* vc = p.mid.v_codes + bkv * M * kRowB;
     const uint16_t* vsg = p.mid.v_scale + bkv * M;
     auto issue = [&](int64_t t, uint32_t st) {
       const int64_t m0 = (t - nF) * kTileT;
+      if constexpr (DK == 128) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int r = 16 * k + (lane >> 2);
-        const int64_t row = m0 + r < M ? m0 + r : M - 1;
-        const int qk = (lane & 3) ^ k;
-        lds_dma16(kc + row * 64 + 16 * qk, st + kStageK + 1024 * k);
-        const int qv = (lane & 3) ^ ((lane >> 4) & 3);
-        lds_dma16(vc + row * 64 + 16 * qv, st + kStageV + 1024 * k);
+        for (int k = 0; k < 4; ++k) {
+          const int r = 16 * k + (lane >> 2);
+          const int64_t row = m0 + r < M ? m0 + r : M - 1;
+          const int qk = (lane & 3) ^ k;
+          lds_dma16(kc + row * 64 + 16 * qk, st + kStageK + 1024 * k);
+          const int qv = (lane & 3) ^ ((lane >> 4) & 3);
+          lds_dma16(vc + row * 64 + 16 * qv, st + kStageV + 1024 * k);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const int r = 32 * k + (lane >> 1);
+          const int64_t row = m0 + r < M ? m0 + r : M - 1;
+          lds_dma16(kc + row * 32 + 16 * (lane & 1), st + kStageK + 1024 * k);
+          lds_dma16(vc + row * 32 + 16 * (lane & 1), st + kStageV + 1024 * k);
+        }
       }
       const int64_t vrow = m0 + lane < M ? m0 + lane : M - 1;
       lds_dma2(vsg + vrow, st + kStageVS);
     };
-    constexpr int kOpsPerStage = 9;
+    constexpr int kOpsPerStage = GE::kOpsPerStage;
     // vmcnt operand of s_waitcnt with expcnt / lgkmcnt left unconstrained
     auto wait_vm = [](bool keep_one_stage) {
       if (keep_one_stage) __builtin_amdgcn_s_waitcnt((kOpsPerStage & 15) | (7 << 4) | (15 << 8));
@@ -368,20 +397,31 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int rloc = 16 * (n16 >> 2) + 4 * j + (n16 & 3);
-        const int unit = 4 * rloc + (grp ^ ((rloc >> 4) & 3));
-        const uint4 w = *reinterpret_cast<const uint4*>(st + kStageK + 16 * unit);
-        uint32_t lo0, hi0, lo1, hi1, lo2, hi2, lo3, hi3;
-        nib_to_u8(w.x, lo0, hi0);
-        nib_to_u8(w.y, lo1, hi1);
-        nib_to_u8(w.z, lo2, hi2);
-        nib_to_u8(w.w, lo3, hi3);
-        const i32x4 a0 = {static_cast<int>(lo0), static_cast<int>(hi0), static_cast<int>(lo1), static_cast<int>(hi1)};
-        const i32x4 a1 = {static_cast<int>(lo2), static_cast<int>(hi2), static_cast<int>(lo3), static_cast<int>(hi3)};
         i32x4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
-        chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qd_hi[0], chi, 0, 0, 0);
-        chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, qd_hi[1], chi, 0, 0, 0);
-        clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qd_lo[0], clo, 0, 0, 0);
-        clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, qd_lo[1], clo, 0, 0, 0);
+        if constexpr (DK == 128) {
+          const int unit = 4 * rloc + (grp ^ ((rloc >> 4) & 3));
+          const uint4 w = *reinterpret_cast<const uint4*>(st + kStageK + 16 * unit);
+          uint32_t lo0, hi0, lo1, hi1, lo2, hi2, lo3, hi3;
+          nib_to_u8(w.x, lo0, hi0);
+          nib_to_u8(w.y, lo1, hi1);
+          nib_to_u8(w.z, lo2, hi2);
+          nib_to_u8(w.w, lo3, hi3);
+          const i32x4 a0 = {static_cast<int>(lo0), static_cast<int>(hi0), static_cast<int>(lo1), static_cast<int>(hi1)};
+          const i32x4 a1 = {static_cast<int>(lo2), static_cast<int>(hi2), static_cast<int>(lo3), static_cast<int>(hi3)};
+          chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qd_hi[0], chi, 0, 0, 0);
+          chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, qd_hi[kKS - 1], chi, 0, 0, 0);
+          clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qd_lo[0], clo, 0, 0, 0);
+          clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, qd_lo[kKS - 1], clo, 0, 0, 0);
+        } else {
+          // the lane's 16 channels: bytes 8 grp .. 8 grp + 7 of the 32-byte row
+          const uint2 w = *reinterpret_cast<const uint2*>(st + kStageK + 32 * rloc + 8 * grp);
+          uint32_t lo0, hi0, lo1, hi1;
+          nib_to_u8(w.x, lo0, hi0);
+          nib_to_u8(w.y, lo1, hi1);
+          const i32x4 a0 = {static_cast<int>(lo0), static_cast<int>(hi0), static_cast<int>(lo1), static_cast<int>(hi1)};
+          chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qd_hi[0], chi, 0, 0, 0);
+          clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qd_lo[0], clo, 0, 0, 0);
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) sc[j][i] = static_cast<float>(chi[i] * 256 + clo[i] - corr) * qscale;
       }
@@ -407,8 +447,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       softmax_tile(sc, vsc, pw, pa0, pa1);
       const int vrow = 16 * grp + n16;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const int unit = 4 * vrow + ((c >> 1) ^ ((vrow >> 2) & 3));
+      for (int c = 0; c < kNC; ++c) {
+        const int unit = DK == 128 ? 4 * vrow + ((c >> 1) ^ ((vrow >> 2) & 3)) : 2 * vrow + (c >> 1);
         const i32x2 x = __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2*)(st_lds + kStageV + 16 * unit + 8 * (c & 1)));
         uint32_t vb0[4], vb1[4];
         nib8_to_f16(static_cast<uint32_t>(x[0]), vb0);
@@ -456,7 +496,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
     red_l[wave][n16] = l_tot;
   }
   __syncthreads();
-  float* red_acc = reinterpret_cast<float*>(&ring0[0][0]);  // [wave][h < G][128] (spans ring0, ring1)
+  float* red_acc = reinterpret_cast<float*>(&ring0[0][0]);  // [wave][h < G][DK] (spans ring0, ring1)
+  static_assert(2 * kWaves * kStageBytes >= kWaves * kMaxG * DK * 4, "the wave merge fits the two rings");
   {
     // scale of each of this lane's accumulator rows (heads 4*grp + i)
     float wscale[4];
@@ -469,24 +510,24 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       wscale[i] = 0.5f * exp2f(red_m[wave][h] - Mh);
     }
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+    for (int c = 0; c < kNC; ++c)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int h = 4 * grp + i;
-        if (h < G) red_acc[(wave * G + h) * kD + 16 * c + (n16 ^ 1)] = (acc[c][i] - acc48[i]) * wscale[i];
+        if (h < G) red_acc[(wave * G + h) * DK + 16 * c + (n16 ^ 1)] = (acc[c][i] - acc48[i]) * wscale[i];
       }
   }
   __syncthreads();
-  for (int idx = tid; idx < G * kD; idx += kThreads) {
-    const int h = idx / kD, d = idx % kD;
+  for (int idx = tid; idx < G * DK; idx += kThreads) {
+    const int h = idx / DK, d = idx % DK;
     float Mh = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) Mh = fmaxf(Mh, red_m[w][h]);
     float o = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) o += red_acc[(w * G + h) * kD + d];
+    for (int w = 0; w < kWaves; ++w) o += red_acc[(w * G + h) * DK + d];
     const int64_t pidx = (b * p.Hq + kvh * G + h) * p.n_splits + split;
-    p.ws_acc[pidx * kD + d] = o;
+    p.ws_acc[pidx * DK + d] = o;
     if (d == 0) {
       float L = 0.0f;
 #pragma unroll
@@ -507,7 +548,7 @@ bool fp16_tier_ok(const Fp16Tier& t) {
 }  // namespace
 
 bool mfma_supports(const Params& p) {
-  if (p.D != kD) return false;
+  if (p.D != 128 && p.D != 64) return false;
   if (!fp16_tier_ok(p.sink) || !fp16_tier_ok(p.recent)) return false;
   if (p.G > kMaxG) return false;
   if (reinterpret_cast<uintptr_t>(p.q) % 16 || p.q_sb % 8 || p.q_sh % 8) return false;
@@ -535,10 +576,14 @@ int64_t mfma_tiles(const Params& p) {
 
 int launch_mfma(const Params& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv), static_cast<unsigned>(p.B));
-  if (p.mid.fmt == FADE_MID_FP16 || p.mid.fmt == FADE_MID_NONE)
-    hipLaunchKernelGGL(decode_mfma_kernel<true>, grid, dim3(kThreads), 0, st, p);
-  else
-    hipLaunchKernelGGL(decode_mfma_kernel<false>, grid, dim3(kThreads), 0, st, p);
+  const bool f16 = p.mid.fmt == FADE_MID_FP16 || p.mid.fmt == FADE_MID_NONE;
+  if (p.D == 64) {
+    if (f16) hipLaunchKernelGGL((decode_mfma_kernel<true, 64>), grid, dim3(kThreads), 0, st, p);
+    else hipLaunchKernelGGL((decode_mfma_kernel<false, 64>), grid, dim3(kThreads), 0, st, p);
+  } else {
+    if (f16) hipLaunchKernelGGL((decode_mfma_kernel<true, 128>), grid, dim3(kThreads), 0, st, p);
+    else hipLaunchKernelGGL((decode_mfma_kernel<false, 128>), grid, dim3(kThreads), 0, st, p);
+  }
   return check_launch("fade_tiered_decode_attn(mfma)");
 }
 

@@ -74,6 +74,36 @@ def test_decode_head_dims(dev, D, fmt, B, Hq, Hkv, S, ns, nr):
         assert np.abs(out.float().cpu().numpy() - ref).max() <= ATOL, n_splits
 
 
+@pytest.mark.parametrize("fmt", ["int4", "fp16", None])
+@pytest.mark.parametrize("B,Hq,Hkv,S,ns,nr", [(2, 14, 2, 900, 4, 64), (3, 8, 8, 333, 2, 17), (1, 32, 8, 4100, 4, 128)])
+def test_decode_head_dim_64_matrix_core(dev, fmt, B, Hq, Hkv, S, ns, nr):
+    """head_dim 64 on the general matrix-core kernel (kernel=3, the automatic choice at this
+    head_dim for the reference INT4, fp16 and empty middle tiers): Qwen2.5-0.5B's 14/2 heads,
+    MHA, a partial last tile; against the oracle and the portable kernel (kernel=1)."""
+    D = 64
+    print(f"case decode D=64 matrix-core {fmt} B={B} Hq={Hq} Hkv={Hkv} S={S}", flush=True)
+    q, k, v = (x.numpy() for x in kv_tensors(B, Hkv, S, D, seed=640 + S, Hq=Hq))
+    if fmt is None:
+        mid, omid = None, None
+        ref = oatt.sdpa_fp32(q, k, v)
+        sink, rec = (_t(dev, k), _t(dev, v)), None
+    else:
+        mid, omid = _mid(dev, fmt, k[:, :, ns : S - nr], v[:, :, ns : S - nr])
+        ref = oatt.tiered_decode(q, k[:, :, :ns], v[:, :, :ns], omid, k[:, :, S - nr :], v[:, :, S - nr :])
+        sink = (_t(dev, k[:, :, :ns]), _t(dev, v[:, :, :ns])) if ns else None
+        rec = (_t(dev, k[:, :, S - nr :]), _t(dev, v[:, :, S - nr :])) if nr else None
+    qd = _t(dev, q)
+    outs = {}
+    for kern in (3, 0, 1):
+        for n_splits in (0, 1, 5):
+            out = tiered_decode_attention(qd, sink, mid, rec, n_splits=n_splits, kernel=kern)
+            assert out.shape == (B, Hq, 1, D)
+            err = np.abs(out.float().cpu().numpy() - ref).max()
+            assert err <= ATOL, (kern, n_splits, err)
+            outs[(kern, n_splits)] = out
+    assert (outs[(3, 0)].float() - outs[(1, 0)].float()).abs().max().item() <= ATOL
+
+
 def _ragged(dev, D, B, Hq, Hkv, Sq, rows, seed, fmt="int4"):
     """rows: per-row (n_sink, n_mid, n_recent), tiers padded to common capacities."""
     caps = [max(r[i] for r in rows) for i in range(3)]
@@ -300,8 +330,8 @@ def test_cache_decode_and_prefill_head_dim_64(dev, backend, v_bits):
 
 
 def test_cache_per_sequence_head_dim_64(dev):
-    """Per-sequence assignment (ragged rows) at head_dim 64: decode and chunk prefill
-    per row equal a single-row cache of that row."""
+    """Per-sequence assignment (ragged rows) at head_dim 64: each row's tiers equal a
+    single-row cache of that row, and both decode it within the parity bar."""
     from fade_amd import TieredKVCache
     from fade_amd.policy import _assign_one_layer
 
@@ -321,8 +351,14 @@ def test_cache_per_sequence_head_dim_64(dev):
         cb.update(k[b : b + 1].to(dev), v[b : b + 1].to(dev), 0)
         cb.apply_tier_assignment(0, t[b].to(dev))
         ob = cb.decode_attention(q[b : b + 1], 0)
-        e = (out[b : b + 1].float() - ob.float()).abs().max().item()
-        if e > 1e-3:  # say which tier differs and whether the decodes repeat
+        # The ragged layout decodes with per-row lengths (portable kernel), the single-row
+        # cache on the matrix-core kernel: both against fp32 attention over the single-row
+        # cache's materialized tiers, at the parity bar.
+        km, vm = cb._materialize(0)
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            q[b : b + 1].float(), km.float().repeat_interleave(4, 1), vm.float().repeat_interleave(4, 1))
+        e = max((out[b : b + 1].float() - ref).abs().max().item(), (ob.float() - ref).abs().max().item())
+        if e > ATOL:  # say which tier differs and whether the decodes repeat
             st, sb = c._layers[0], cb._layers[0]
             ls, lm, lr = st.lens_host[b]
             tiers = {
