@@ -823,6 +823,19 @@ def main() -> int:
         }
         del m64, v64
         torch.cuda.empty_cache()
+        # head_dim 256 (Gemma-style 16/8 heads), B=16, S=8192, on the same kernel
+        c256 = type("Cfg", (), dict(B=16, Hq=16, Hkv=8, S=8192, D=256, n_sink=4, recent=64, mid=8192 - 68))
+        m256 = build_instances(c256, "int4", dev, 1007, N_INSTANCES)
+        v256 = [TieredDecodePlan(*pl._keep[:4], kernel=1) for pl in m256]
+        mmean, vmean = graph_us(m256) * 1e-3, graph_us(v256) * 1e-3
+        b256 = decode_bytes(c256, "int4")
+        extra["c1_shape_d256_16_8_decode_int4"] = {
+            "us": round(mmean * 1e3, 2), "us_portable_kernel": round(vmean * 1e3, 2), "bytes": b256,
+            "GBps": round(b256 / (mmean * 1e-3) / 1e9, 1),
+            "frac_of_peak": round(b256 / (mmean * 1e-3) / 1e9 / HBM_PEAK_GBPS, 3),
+        }
+        del m256, v256
+        torch.cuda.empty_cache()
         # GQA 8 (Llama-3-70B / Qwen2-72B heads: 64 / 8) at config 1's batch and length
         g2, gg, gb = gqa7_decode_case(dev, B=16, S=8192, Hq=64, Hkv=8)
         g2mean = graph_us(g2) * 1e-3

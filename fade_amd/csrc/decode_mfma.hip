@@ -49,10 +49,10 @@ constexpr int kTileT = 64;
 constexpr float kQMax = 32000.0f;
 constexpr float kNegBig = -1.0e30f;  // running-max sentinel (finite: no inf-inf guards)
 
-// Head-dim geometry (DK = 128 or 64).  A stage holds one packed tile: K codes
-// (64 rows of DK/2 bytes) | V codes (the same) | V scales (64 dwords).  Lane
-// group g of a QK^T MFMA covers channels DK/4 g .. + DK/4 - 1 (two int8
-// k-steps of 64 at DK = 128, one at 64); PV has DK/16 column blocks.
+// Head-dim geometry (DK = 64, 128 or 256).  A stage holds one packed tile: K
+// codes (64 rows of DK/2 bytes) | V codes (the same) | V scales (64 dwords).
+// Lane group g of a QK^T MFMA covers channels DK/4 g .. + DK/4 - 1 (DK/64
+// int8 k-steps of 64, 16 channels of the lane's each); PV has DK/16 column blocks.
 template <int DK>
 struct Geo {
   static constexpr int kRowB = DK / 2;                 // packed bytes per token
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   // hit 16 different bank groups:
   //   K unit (row r, chunk q) at 4r + (q ^ ((r >> 4) & 3))
   //   V unit (row r, chunk q) at 4r + (q ^ ((r >> 2) & 3))
-  // (DK = 64: two units per row, unit 2r + q, unswizzled)
+  // (DK = 64 / 256: U = DK / 32 units per row, unit U r + q, unswizzled)
   int64_t tau = t0 + wave;
   if (tau < nF) tau += ((nF - tau + kWaves - 1) / kWaves) * kWaves;
   if (!MID_F16 && tau < t1) {
@@ -372,12 +372,14 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
           lds_dma16(vc + row * 64 + 16 * qv, st + kStageV + 1024 * k);
         }
       } else {
+        // load k fills units 64 k + lane: row (64 k + lane) / U, chunk (64 k + lane) % U
+        constexpr int U = GE::kUnits;
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          const int r = 32 * k + (lane >> 1);
+        for (int k = 0; k < U; ++k) {
+          const int r = (64 * k + lane) / U, qc = (64 * k + lane) % U;
           const int64_t row = m0 + r < M ? m0 + r : M - 1;
-          lds_dma16(kc + row * 32 + 16 * (lane & 1), st + kStageK + 1024 * k);
-          lds_dma16(vc + row * 32 + 16 * (lane & 1), st + kStageV + 1024 * k);
+          lds_dma16(kc + row * kRowB + 16 * qc, st + kStageK + 1024 * k);
+          lds_dma16(vc + row * kRowB + 16 * qc, st + kStageV + 1024 * k);
         }
       }
       const int64_t vrow = m0 + lane < M ? m0 + lane : M - 1;
@@ -413,14 +415,18 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
           clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qd_lo[0], clo, 0, 0, 0);
           clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, qd_lo[kKS - 1], clo, 0, 0, 0);
         } else {
-          // the lane's 16 channels: bytes 8 grp .. 8 grp + 7 of the 32-byte row
-          const uint2 w = *reinterpret_cast<const uint2*>(st + kStageK + 32 * rloc + 8 * grp);
-          uint32_t lo0, hi0, lo1, hi1;
-          nib_to_u8(w.x, lo0, hi0);
-          nib_to_u8(w.y, lo1, hi1);
-          const i32x4 a0 = {static_cast<int>(lo0), static_cast<int>(hi0), static_cast<int>(lo1), static_cast<int>(hi1)};
-          chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qd_hi[0], chi, 0, 0, 0);
-          clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, qd_lo[0], clo, 0, 0, 0);
+          // k-step ks: the lane's channels kCPL grp + 16 ks .. + 15, bytes
+          // kCPL/2 grp + 8 ks .. + 7 of the row
+#pragma unroll
+          for (int ks = 0; ks < kKS; ++ks) {
+            const uint2 w = *reinterpret_cast<const uint2*>(st + kStageK + GE::kRowB * rloc + (kCPL / 2) * grp + 8 * ks);
+            uint32_t lo0, hi0, lo1, hi1;
+            nib_to_u8(w.x, lo0, hi0);
+            nib_to_u8(w.y, lo1, hi1);
+            const i32x4 a = {static_cast<int>(lo0), static_cast<int>(hi0), static_cast<int>(lo1), static_cast<int>(hi1)};
+            chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qd_hi[ks], chi, 0, 0, 0);
+            clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qd_lo[ks], clo, 0, 0, 0);
+          }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) sc[j][i] = static_cast<float>(chi[i] * 256 + clo[i] - corr) * qscale;
@@ -448,7 +454,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       const int vrow = 16 * grp + n16;
 #pragma unroll
       for (int c = 0; c < kNC; ++c) {
-        const int unit = DK == 128 ? 4 * vrow + ((c >> 1) ^ ((vrow >> 2) & 3)) : 2 * vrow + (c >> 1);
+        const int unit = DK == 128 ? 4 * vrow + ((c >> 1) ^ ((vrow >> 2) & 3)) : GE::kUnits * vrow + (c >> 1);
         const i32x2 x = __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2*)(st_lds + kStageV + 16 * unit + 8 * (c & 1)));
         uint32_t vb0[4], vb1[4];
         nib8_to_f16(static_cast<uint32_t>(x[0]), vb0);
@@ -548,7 +554,7 @@ bool fp16_tier_ok(const Fp16Tier& t) {
 }  // namespace
 
 bool mfma_supports(const Params& p) {
-  if (p.D != 128 && p.D != 64) return false;
+  if (p.D != 128 && p.D != 64 && p.D != 256) return false;
   if (!fp16_tier_ok(p.sink) || !fp16_tier_ok(p.recent)) return false;
   if (p.G > kMaxG) return false;
   if (reinterpret_cast<uintptr_t>(p.q) % 16 || p.q_sb % 8 || p.q_sh % 8) return false;
@@ -580,6 +586,9 @@ int launch_mfma(const Params& p, hipStream_t st) {
   if (p.D == 64) {
     if (f16) hipLaunchKernelGGL((decode_mfma_kernel<true, 64>), grid, dim3(kThreads), 0, st, p);
     else hipLaunchKernelGGL((decode_mfma_kernel<false, 64>), grid, dim3(kThreads), 0, st, p);
+  } else if (p.D == 256) {
+    if (f16) hipLaunchKernelGGL((decode_mfma_kernel<true, 256>), grid, dim3(kThreads), 0, st, p);
+    else hipLaunchKernelGGL((decode_mfma_kernel<false, 256>), grid, dim3(kThreads), 0, st, p);
   } else {
     if (f16) hipLaunchKernelGGL((decode_mfma_kernel<true, 128>), grid, dim3(kThreads), 0, st, p);
     else hipLaunchKernelGGL((decode_mfma_kernel<false, 128>), grid, dim3(kThreads), 0, st, p);

@@ -74,15 +74,15 @@ def test_decode_head_dims(dev, D, fmt, B, Hq, Hkv, S, ns, nr):
         assert np.abs(out.float().cpu().numpy() - ref).max() <= ATOL, n_splits
 
 
+@pytest.mark.parametrize("D", [64, 256])
 @pytest.mark.parametrize("fmt", ["int4", "fp16", None])
 @pytest.mark.parametrize("B,Hq,Hkv,S,ns,nr", [(2, 14, 2, 900, 4, 64), (3, 8, 8, 333, 2, 17), (1, 32, 8, 4100, 4, 128)])
-def test_decode_head_dim_64_matrix_core(dev, fmt, B, Hq, Hkv, S, ns, nr):
-    """head_dim 64 on the general matrix-core kernel (kernel=3, the automatic choice at this
-    head_dim for the reference INT4, fp16 and empty middle tiers): Qwen2.5-0.5B's 14/2 heads,
-    MHA, a partial last tile; against the oracle and the portable kernel (kernel=1)."""
-    D = 64
-    print(f"case decode D=64 matrix-core {fmt} B={B} Hq={Hq} Hkv={Hkv} S={S}", flush=True)
-    q, k, v = (x.numpy() for x in kv_tensors(B, Hkv, S, D, seed=640 + S, Hq=Hq))
+def test_decode_head_dim_64_256_matrix_core(dev, D, fmt, B, Hq, Hkv, S, ns, nr):
+    """head_dims 64 and 256 on the general matrix-core kernel (kernel=3, the automatic choice
+    at these head_dims for the reference INT4, fp16 and empty middle tiers): Qwen2.5-0.5B's
+    14/2 heads, MHA, a partial last tile; against the oracle and the portable kernel (kernel=1)."""
+    print(f"case decode D={D} matrix-core {fmt} B={B} Hq={Hq} Hkv={Hkv} S={S}", flush=True)
+    q, k, v = (x.numpy() for x in kv_tensors(B, Hkv, S, D, seed=640 + S + D, Hq=Hq))
     if fmt is None:
         mid, omid = None, None
         ref = oatt.sdpa_fp32(q, k, v)
