@@ -127,9 +127,6 @@ int validate(const fade_decode_args* a) {
   if (a->dtype != FADE_DTYPE_F16 && a->dtype != FADE_DTYPE_BF16)
     return einval("fade_tiered_decode_attn: dtype must be FADE_DTYPE_F16 or FADE_DTYPE_BF16, got %d", a->dtype);
   if (a->dtype == FADE_DTYPE_BF16) {
-    if (a->kernel == 3)
-      return einval("fade_tiered_decode_attn: bfloat16 runs the INT4 matrix-core kernel or the portable one "
-                    "(kernel 0, 1 or 2), not kernel 3");
     if (a->mid.len > 0 && a->mid.fmt == FADE_MID_ASYM)
       return einval("fade_tiered_decode_attn: the asymmetric middle format holds fp16 tensors; bfloat16 calls "
                     "take FADE_MID_SYM, FADE_MID_K4V2G or FADE_MID_FP16");
@@ -198,9 +195,9 @@ enum class Kern { kValu, kMfma, kInt4 };
 Kern choose(const fade_decode_args* a, const Params& p) {
   if (a->kernel == 1) return Kern::kValu;
   if (a->kernel != 3 && int4_supports(p)) return Kern::kInt4;
-  // the general kernel reads fp16 only and takes no per-row lengths (auto falls back
-  // to the portable kernel there; kernels 2 and 3 report the error)
-  if (!p.bf16 && mfma_supports(p) && (a->lens == nullptr || a->kernel >= 2)) return Kern::kMfma;
+  // the general kernel takes no per-row lengths (auto falls back to the portable
+  // kernel there; kernels 2 and 3 report the error)
+  if (mfma_supports(p) && (a->lens == nullptr || a->kernel >= 2)) return Kern::kMfma;
   return Kern::kValu;
 }
 

@@ -37,6 +37,9 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
@@ -97,6 +100,37 @@ __device__ __forceinline__ void nib8_to_f16(uint32_t w, uint32_t* out) {
   out[3] = ((w >> 6) & 0x03C003C0u) ^ 0x52005200u;
 }
 
+// The same for bfloat16 values 72 + c: the nibble moves to mantissa bits 1..4
+// of 64.0 (0x4280, ulp 1/2, one code step = 1.0), bit 3 flipped.
+__device__ __forceinline__ void nib8_to_bf16(uint32_t w, uint32_t* out) {
+  out[0] = ((w << 1) & 0x001E001Eu) ^ 0x42904290u;
+  out[1] = ((w >> 3) & 0x001E001Eu) ^ 0x42904290u;
+  out[2] = ((w >> 7) & 0x001E001Eu) ^ 0x42904290u;
+  out[3] = ((w >> 11) & 0x001E001Eu) ^ 0x42904290u;
+}
+
+// 16-bit operands of the call's dtype (BF: bfloat16, else fp16) as bit patterns.
+template <bool BF>
+__device__ __forceinline__ f32x4 mfma_k32(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (BF)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+template <bool BF>
+__device__ __forceinline__ f32x4 mfma_k16(i32x2 a, i32x2 b, f32x4 c) {
+  if constexpr (BF)
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4, a), __builtin_bit_cast(bf16x4, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+}
+template <bool BF>
+__device__ __forceinline__ uint32_t pack_w2(float a, float b) {
+  if constexpr (BF) return pack_bf16(a, b);
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
+}
+
 struct FpTok {  // one fp16 token row (K and V pointers)
   const uint16_t* k;
   const uint16_t* v;
@@ -127,9 +161,15 @@ __device__ __forceinline__ FpTok fp16_token(const Params& p, int64_t b, int64_t 
   return r;
 }
 
-template <bool MID_F16, int DK>
+// BF: q, the tiers, the scales and the output are bfloat16; probabilities and
+// V values enter the PV MFMAs as bfloat16.  Packed V codes become 72 + c
+// (bfloat16) instead of 48 + 2c (fp16), so the fp16-tier tiles' PV takes P
+// once instead of twice and the constant removed is 72 instead of 48.
+template <bool MID_F16, int DK, bool BF>
 __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   using GE = Geo<DK>;
+  constexpr float kVMul = BF ? 1.0f : 2.0f;   // V value per code step
+  constexpr float kVOff = BF ? 72.0f : 48.0f;  // V value offset per token of a packed tile
   constexpr int kStageK = GE::kStageK, kStageV = GE::kStageV, kStageVS = GE::kStageVS, kStageBytes = GE::kStageBytes;
   constexpr int kKS = GE::kKS, kCPL = GE::kCPL, kNC = GE::kNC, kV16Pitch = GE::kV16Pitch;
   const int split = blockIdx.x;
@@ -174,8 +214,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       const uint32_t u[4] = {qraw[c].x, qraw[c].y, qraw[c].z, qraw[c].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        qf[8 * c + 2 * e] = h2f(static_cast<uint16_t>(u[e] & 0xFFFFu));
-        qf[8 * c + 2 * e + 1] = h2f(static_cast<uint16_t>(u[e] >> 16));
+        qf[8 * c + 2 * e] = w2f<BF>(static_cast<uint16_t>(u[e] & 0xFFFFu));
+        qf[8 * c + 2 * e + 1] = w2f<BF>(static_cast<uint16_t>(u[e] >> 16));
       }
     }
     const uint16_t* ksp = p.mid.k_scale + bkv * DK + kCPL * grp;
@@ -185,8 +225,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        qf[8 * c + 2 * e] *= h2f(static_cast<uint16_t>(u[e] & 0xFFFFu));
-        qf[8 * c + 2 * e + 1] *= h2f(static_cast<uint16_t>(u[e] >> 16));
+        qf[8 * c + 2 * e] *= w2f<BF>(static_cast<uint16_t>(u[e] & 0xFFFFu));
+        qf[8 * c + 2 * e + 1] *= w2f<BF>(static_cast<uint16_t>(u[e] >> 16));
       }
     }
     float mx = 0.0f;
@@ -236,7 +276,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   const int64_t t1 = t0 + tiles_per_split < nT ? t0 + tiles_per_split : nT;
 
   __syncthreads();
-  // acc holds 2 * sum(P V) + 48 * sum_{packed tiles}(P'), acc48 the 48 * sum(P') part.
+  // acc holds kVMul * sum(P V) + kVOff * sum_{packed tiles}(P'), acc48 the kVOff * sum(P') part.
   float m_run = kNegBig, l_lane = 0.0f;
   f32x4 acc[kNC];
 #pragma unroll
@@ -250,7 +290,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   // Online-softmax update of head n16 with the 64 scores of one tile.  P
   // times pscale[token] leaves as the two PV A operands (fp16), plain P in pw.
   // Accumulators are rescaled only when some head's running max rises.
-  auto softmax_tile = [&](float (&sc)[4][4], const float* pscale, float (&pw)[4][4], f16x8& pa0, f16x8& pa1) {
+  auto softmax_tile = [&](float (&sc)[4][4], const float* pscale, float (&pw)[4][4], u32x4& pa0, u32x4& pa1) {
     float tmax = sc[0][0];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -271,7 +311,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       acc48 *= al;
     }
     float psum = 0.0f;
-    f16x2 pa[2][4];  // k-step s, VGPR v = tokens (16g+8s+v, 16g+8s+v+4)
+    uint32_t pa[2][4];  // k-step s, VGPR v = tokens (16g+8s+v, 16g+8s+v+4)
 #pragma unroll
     for (int sk = 0; sk < 2; ++sk) {
 #pragma unroll
@@ -281,12 +321,12 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
         psum += p0 + p1;
         pw[2 * sk][v] = p0;
         pw[2 * sk + 1][v] = p1;
-        pa[sk][v] = f16x2{static_cast<_Float16>(p0 * pscale[8 * sk + v]), static_cast<_Float16>(p1 * pscale[8 * sk + v + 4])};
+        pa[sk][v] = pack_w2<BF>(p0 * pscale[8 * sk + v], p1 * pscale[8 * sk + v + 4]);
       }
     }
     l_lane += psum;
-    pa0 = __builtin_bit_cast(f16x8, pa[0]);
-    pa1 = __builtin_bit_cast(f16x8, pa[1]);
+    pa0 = u32x4{pa[0][0], pa[0][1], pa[0][2], pa[0][3]};
+    pa1 = u32x4{pa[1][0], pa[1][1], pa[1][2], pa[1][3]};
   };
 
   // -------------------------------------------------------------- fp16 tiles
@@ -302,8 +342,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       f32x4 c4 = {0, 0, 0, 0};
 #pragma unroll
       for (int ks = 0; ks < kCPL / 8; ++ks) {
-        const f16x8 qb = *reinterpret_cast<const f16x8*>(&q16_s[n16][kCPL * grp + 8 * ks]);
-        c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ldg16(kr + 8 * ks)), qb, c4, 0, 0, 0);
+        const u32x4 qb = *reinterpret_cast<const u32x4*>(&q16_s[n16][kCPL * grp + 8 * ks]);
+        const uint4 kw = ldg16(kr + 8 * ks);
+        c4 = mfma_k32<BF>(u32x4{kw.x, kw.y, kw.z, kw.w}, qb, c4);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -312,8 +353,8 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       }
     }
 #pragma unroll
-    for (int k = 0; k < 16; ++k) vsc[k] = 2.0f;
-    f16x8 pa0, pa1;
+    for (int k = 0; k < 16; ++k) vsc[k] = kVMul;
+    u32x4 pa0, pa1;
     softmax_tile(sc, vsc, pw, pa0, pa1);
     // fp16 V in four 16-token chunks through LDS; chunk q = tokens 16g + 4q + i
     uint16_t* vt16 = reinterpret_cast<uint16_t*>(my_vtile);
@@ -329,16 +370,14 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
           *reinterpret_cast<uint4*>(vt16 + r * kV16Pitch + kCPL * (lane & 3) + 8 * c) = ldg16(src + 8 * c);
       }
       __builtin_amdgcn_wave_barrier();
-      const f16x4 pa4 = {static_cast<_Float16>(2.0f * pw[q][0]), static_cast<_Float16>(2.0f * pw[q][1]),
-                         static_cast<_Float16>(2.0f * pw[q][2]), static_cast<_Float16>(2.0f * pw[q][3])};
+      const i32x2 pa4 = {static_cast<int>(pack_w2<BF>(kVMul * pw[q][0], kVMul * pw[q][1])),
+                         static_cast<int>(pack_w2<BF>(kVMul * pw[q][2], kVMul * pw[q][3]))};
 #pragma unroll
       for (int c = 0; c < kNC; ++c) {
         const int d = 16 * c + (n16 ^ 1);
-        const f16x4 vb = {__builtin_bit_cast(_Float16, vt16[(4 * grp + 0) * kV16Pitch + d]),
-                          __builtin_bit_cast(_Float16, vt16[(4 * grp + 1) * kV16Pitch + d]),
-                          __builtin_bit_cast(_Float16, vt16[(4 * grp + 2) * kV16Pitch + d]),
-                          __builtin_bit_cast(_Float16, vt16[(4 * grp + 3) * kV16Pitch + d])};
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa4, vb, acc[c], 0, 0, 0);
+        const i32x2 vb = {static_cast<int>(vt16[(4 * grp + 0) * kV16Pitch + d] | (static_cast<uint32_t>(vt16[(4 * grp + 1) * kV16Pitch + d]) << 16)),
+                          static_cast<int>(vt16[(4 * grp + 2) * kV16Pitch + d] | (static_cast<uint32_t>(vt16[(4 * grp + 3) * kV16Pitch + d]) << 16))};
+        acc[c] = mfma_k16<BF>(pa4, vb, acc[c]);
       }
     }
   }
@@ -443,13 +482,13 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const uint4 v = *reinterpret_cast<const uint4*>(st + kStageVS + 64 * grp + 16 * c);
-          vsc[4 * c + 0] = h2f(static_cast<uint16_t>(v.x & 0xFFFFu));
-          vsc[4 * c + 1] = h2f(static_cast<uint16_t>(v.y & 0xFFFFu));
-          vsc[4 * c + 2] = h2f(static_cast<uint16_t>(v.z & 0xFFFFu));
-          vsc[4 * c + 3] = h2f(static_cast<uint16_t>(v.w & 0xFFFFu));
+          vsc[4 * c + 0] = w2f<BF>(static_cast<uint16_t>(v.x & 0xFFFFu));
+          vsc[4 * c + 1] = w2f<BF>(static_cast<uint16_t>(v.y & 0xFFFFu));
+          vsc[4 * c + 2] = w2f<BF>(static_cast<uint16_t>(v.z & 0xFFFFu));
+          vsc[4 * c + 3] = w2f<BF>(static_cast<uint16_t>(v.w & 0xFFFFu));
         }
       }
-      f16x8 pa0, pa1;
+      u32x4 pa0, pa1;
       softmax_tile(sc, vsc, pw, pa0, pa1);
       const int vrow = 16 * grp + n16;
 #pragma unroll
@@ -457,16 +496,21 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
         const int unit = DK == 128 ? 4 * vrow + ((c >> 1) ^ ((vrow >> 2) & 3)) : GE::kUnits * vrow + (c >> 1);
         const i32x2 x = __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2*)(st_lds + kStageV + 16 * unit + 8 * (c & 1)));
         uint32_t vb0[4], vb1[4];
-        nib8_to_f16(static_cast<uint32_t>(x[0]), vb0);
-        nib8_to_f16(static_cast<uint32_t>(x[1]), vb1);
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa0, __builtin_bit_cast(f16x8, vb0), acc[c], 0, 0, 0);
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa1, __builtin_bit_cast(f16x8, vb1), acc[c], 0, 0, 0);
+        if constexpr (BF) {
+          nib8_to_bf16(static_cast<uint32_t>(x[0]), vb0);
+          nib8_to_bf16(static_cast<uint32_t>(x[1]), vb1);
+        } else {
+          nib8_to_f16(static_cast<uint32_t>(x[0]), vb0);
+          nib8_to_f16(static_cast<uint32_t>(x[1]), vb1);
+        }
+        acc[c] = mfma_k32<BF>(pa0, u32x4{vb0[0], vb0[1], vb0[2], vb0[3]}, acc[c]);
+        acc[c] = mfma_k32<BF>(pa1, u32x4{vb1[0], vb1[1], vb1[2], vb1[3]}, acc[c]);
       }
-      {  // 48 * sum(P') per head, accumulated exactly like acc
-        const _Float16 h48 = static_cast<_Float16>(48.0f);
-        const f16x8 b48 = {h48, h48, h48, h48, h48, h48, h48, h48};
-        acc48 = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa0, b48, acc48, 0, 0, 0);
-        acc48 = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa1, b48, acc48, 0, 0, 0);
+      {  // kVOff * sum(P') per head, accumulated exactly like acc
+        const uint32_t o2 = pack_w2<BF>(kVOff, kVOff);
+        const u32x4 b48 = {o2, o2, o2, o2};
+        acc48 = mfma_k32<BF>(pa0, b48, acc48);
+        acc48 = mfma_k32<BF>(pa1, b48, acc48);
       }
       // every LDS read of this stage has returned before it is refilled
       __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4));
@@ -513,7 +557,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       float Mh = -INFINITY;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) Mh = fmaxf(Mh, red_m[w][h]);
-      wscale[i] = 0.5f * exp2f(red_m[wave][h] - Mh);
+      wscale[i] = (1.0f / kVMul) * exp2f(red_m[wave][h] - Mh);
     }
 #pragma unroll
     for (int c = 0; c < kNC; ++c)
@@ -583,16 +627,15 @@ int64_t mfma_tiles(const Params& p) {
 int launch_mfma(const Params& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(p.n_splits), static_cast<unsigned>(p.Hkv), static_cast<unsigned>(p.B));
   const bool f16 = p.mid.fmt == FADE_MID_FP16 || p.mid.fmt == FADE_MID_NONE;
-  if (p.D == 64) {
-    if (f16) hipLaunchKernelGGL((decode_mfma_kernel<true, 64>), grid, dim3(kThreads), 0, st, p);
-    else hipLaunchKernelGGL((decode_mfma_kernel<false, 64>), grid, dim3(kThreads), 0, st, p);
-  } else if (p.D == 256) {
-    if (f16) hipLaunchKernelGGL((decode_mfma_kernel<true, 256>), grid, dim3(kThreads), 0, st, p);
-    else hipLaunchKernelGGL((decode_mfma_kernel<false, 256>), grid, dim3(kThreads), 0, st, p);
-  } else {
-    if (f16) hipLaunchKernelGGL((decode_mfma_kernel<true, 128>), grid, dim3(kThreads), 0, st, p);
-    else hipLaunchKernelGGL((decode_mfma_kernel<false, 128>), grid, dim3(kThreads), 0, st, p);
-  }
+#define FADE_MFMA_LAUNCH(DK)                                                                                         \
+  if (p.bf16 && f16) hipLaunchKernelGGL((decode_mfma_kernel<true, DK, true>), grid, dim3(kThreads), 0, st, p);   \
+  else if (p.bf16) hipLaunchKernelGGL((decode_mfma_kernel<false, DK, true>), grid, dim3(kThreads), 0, st, p);    \
+  else if (f16) hipLaunchKernelGGL((decode_mfma_kernel<true, DK, false>), grid, dim3(kThreads), 0, st, p);       \
+  else hipLaunchKernelGGL((decode_mfma_kernel<false, DK, false>), grid, dim3(kThreads), 0, st, p);
+  if (p.D == 64) { FADE_MFMA_LAUNCH(64) }
+  else if (p.D == 256) { FADE_MFMA_LAUNCH(256) }
+  else { FADE_MFMA_LAUNCH(128) }
+#undef FADE_MFMA_LAUNCH
   return check_launch("fade_tiered_decode_attn(mfma)");
 }
 

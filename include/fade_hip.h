@@ -360,8 +360,7 @@ typedef struct fade_decode_args {
                                   an fp16-format middle tier and the FADE_MID_SYM /
                                   FADE_MID_K4V2G scales (the reference's cache keeps every
                                   tier and scale in the model's dtype).  FADE_MID_ASYM (fp16
-                                  scale / zero by format) takes FADE_DTYPE_F16 only;
-                                  bfloat16 runs kernel 0, 1 or 2. */
+                                  scale / zero by format) takes FADE_DTYPE_F16 only. */
 } fade_decode_args;
 
 /* Replaces dequantize + torch.cat (fade/cache.py:683-842) + SDPA and the

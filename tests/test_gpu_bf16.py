@@ -97,15 +97,34 @@ def test_decode_bf16_formats(dev, B, Hq, Hkv, S, ns, nr, fmt, kernel):
     assert _excess(out, ref) <= ATOL
 
 
-@pytest.mark.parametrize("D", [64, 80, 256])
-def test_decode_bf16_head_dims_portable(dev, D):
-    """Head dims other than 128 run the portable kernel (bf16 dot products)."""
-    print(f"case bf16 decode head_dim={D}", flush=True)
+@pytest.mark.parametrize("D,kernel", [(64, 0), (64, 1), (64, 3), (80, 0), (256, 0), (256, 1), (256, 3), (128, 3)])
+def test_decode_bf16_head_dims(dev, D, kernel):
+    """Head dims other than 128: 64 and 256 on the general matrix-core kernel (the automatic
+    choice; kernel 3), 80 on the portable one (bf16 dot products; kernel 1 everywhere)."""
+    print(f"case bf16 decode head_dim={D} kernel={kernel}", flush=True)
     B, Hq, Hkv, S, ns, nr = 2, 16, 4, 300, 4, 32
     q, k, v = _kv(dev, B, Hq, Hkv, S, D, seed=800 + D)
     mid, omid = _middle("int4", k[:, :, ns : S - nr].contiguous(), v[:, :, ns : S - nr].contiguous())
-    out = tiered_decode_attention(q, (k[:, :, :ns], v[:, :, :ns]), mid, (k[:, :, S - nr :], v[:, :, S - nr :]))
+    out = tiered_decode_attention(q, (k[:, :, :ns], v[:, :, :ns]), mid, (k[:, :, S - nr :], v[:, :, S - nr :]),
+                                  kernel=kernel)
     kb, vb = _bits(k), _bits(v)
+    ref = oatt.tiered_decode(_bits(q), kb[:, :, :ns], vb[:, :, :ns], omid, kb[:, :, S - nr :], vb[:, :, S - nr :],
+                             dtype="bf16")
+    assert _excess(out, ref) <= ATOL
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_decode_bf16_general_kernel_fp16_layout_middle(dev, D):
+    """The general matrix-core kernel (kernel 3) over bf16 rows only: a plain-row middle
+    tier joined to the sink and recent tiers, GQA 7 (Qwen2.5-0.5B's 14/2 heads)."""
+    print(f"case bf16 decode general kernel fp16-layout middle D={D}", flush=True)
+    B, Hq, Hkv, S, ns, nr = 2, 14, 2, 333, 4, 17
+    q, k, v = _kv(dev, B, Hq, Hkv, S, D, seed=910 + D)
+    mk, mv = k[:, :, ns : S - nr].contiguous(), v[:, :, ns : S - nr].contiguous()
+    out = tiered_decode_attention(q, (k[:, :, :ns], v[:, :, :ns]), MiddleTier("fp16", mk, mv),
+                                  (k[:, :, S - nr :], v[:, :, S - nr :]), kernel=3)
+    kb, vb = _bits(k), _bits(v)
+    omid = {"fmt": "fp16", "dtype": "bf16", "k": _bits(mk), "v": _bits(mv)}
     ref = oatt.tiered_decode(_bits(q), kb[:, :, :ns], vb[:, :, :ns], omid, kb[:, :, S - nr :], vb[:, :, S - nr :],
                              dtype="bf16")
     assert _excess(out, ref) <= ATOL
