@@ -195,9 +195,7 @@ enum class Kern { kValu, kMfma, kInt4 };
 Kern choose(const fade_decode_args* a, const Params& p) {
   if (a->kernel == 1) return Kern::kValu;
   if (a->kernel != 3 && int4_supports(p)) return Kern::kInt4;
-  // the general kernel takes no per-row lengths (auto falls back to the portable
-  // kernel there; kernels 2 and 3 report the error)
-  if (mfma_supports(p) && (a->lens == nullptr || a->kernel >= 2)) return Kern::kMfma;
+  if (mfma_supports(p)) return Kern::kMfma;
   return Kern::kValu;
 }
 
@@ -269,8 +267,6 @@ int run_plan(const fade_decode_args* a, Params& p, const Plan& pl, uint32_t* cou
   if (a->mid.pages != nullptr && pl.k != Kern::kInt4)
     return einval("fade_tiered_decode_attn: paged middle tiers need the matrix-core INT4 "
                   "kernel (middle tier FADE_MID_SYM or FADE_MID_ASYM, GQA <= 8)");
-  if (a->lens != nullptr && pl.k == Kern::kMfma)
-    return einval("fade_tiered_decode_attn: per-row lengths need the INT4 kernel or the portable one (kernel 1)");
   if (pl.n > 65535) return einval("fade_tiered_decode_attn: too many splits");
   const WsLayout ws = ws_layout(a, pl.n);
   p.n_splits = static_cast<int>(pl.n);

@@ -136,11 +136,12 @@ struct FpTok {  // one fp16 token row (K and V pointers)
   const uint16_t* v;
 };
 
-// Row pointers of virtual fp16 token f: sink, (fp16 middle), recent.
+// Row pointers of virtual fp16 token f: sink, (fp16 middle), recent; ns / nm
+// are the row's sink and fp16-middle tokens (the middle rows are mid.len apart).
 template <bool MID_F16, int DK>
-__device__ __forceinline__ FpTok fp16_token(const Params& p, int64_t b, int64_t kvh, int64_t f) {
+__device__ __forceinline__ FpTok fp16_token(const Params& p, int64_t b, int64_t kvh, int64_t f, int64_t ns,
+                                            int64_t nm) {
   FpTok r;
-  const int64_t ns = p.sink.len;
   if (f < ns) {
     r.k = p.sink.k + b * p.sink.k_sb + kvh * p.sink.k_sh + f * p.sink.k_ss;
     r.v = p.sink.v + b * p.sink.v_sb + kvh * p.sink.v_sh + f * p.sink.v_ss;
@@ -148,13 +149,13 @@ __device__ __forceinline__ FpTok fp16_token(const Params& p, int64_t b, int64_t 
   }
   f -= ns;
   if (MID_F16) {
-    if (f < p.mid.len) {
+    if (f < nm) {
       const int64_t row = (b * p.Hkv + kvh) * p.mid.len + f;
       r.k = reinterpret_cast<const uint16_t*>(p.mid.k_codes) + row * DK;
       r.v = reinterpret_cast<const uint16_t*>(p.mid.v_codes) + row * DK;
       return r;
     }
-    f -= p.mid.len;
+    f -= nm;
   }
   r.k = p.recent.k + b * p.recent.k_sb + kvh * p.recent.k_sh + f * p.recent.k_ss;
   r.v = p.recent.v + b * p.recent.v_sb + kvh * p.recent.v_sh + f * p.recent.v_ss;
@@ -179,8 +180,20 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   const int n16 = lane & 15, grp = lane >> 4;
   const int G = p.G;
   const int64_t bkv = b * p.Hkv + kvh;
-  const int64_t M = MID_F16 ? 0 : p.mid.len;                  // packed middle tokens
-  const int64_t F = p.total - M;                               // fp16 tokens
+  // this row's sink, middle and recent tokens: the tiers' lengths, or the row's
+  // own (per-row lengths, clamped to the padded capacities)
+  const int64_t Mc = p.mid.len;                                // middle rows per (row, kv head)
+  int64_t ns = p.sink.len, nm = Mc, nr = p.recent.len;
+  if (p.lens != nullptr) {
+    const int64_t ls = __builtin_amdgcn_readfirstlane(p.lens[3 * b]);
+    const int64_t lm = __builtin_amdgcn_readfirstlane(p.lens[3 * b + 1]);
+    const int64_t lr = __builtin_amdgcn_readfirstlane(p.lens[3 * b + 2]);
+    ns = ls < 0 ? 0 : (ls < p.sink.len ? ls : p.sink.len);
+    nm = lm < 0 ? 0 : (lm < Mc ? lm : Mc);
+    nr = lr < 0 ? 0 : (lr < p.recent.len ? lr : p.recent.len);
+  }
+  const int64_t M = MID_F16 ? 0 : nm;                          // packed middle tokens
+  const int64_t F = ns + nr + (MID_F16 ? nm : 0);              // fp16 tokens
   const int64_t nF = (F + kTileT - 1) / kTileT;
 
   // Per-wave ring of two stages; a stage holds one packed tile:
@@ -338,7 +351,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
     for (int j = 0; j < 4; ++j) {
       const int rloc = 16 * (n16 >> 2) + 4 * j + (n16 & 3);
       const int64_t f = f0 + rloc < F ? f0 + rloc : F - 1;
-      const uint16_t* kr = fp16_token<MID_F16, DK>(p, b, kvh, f).k + kCPL * grp;
+      const uint16_t* kr = fp16_token<MID_F16, DK>(p, b, kvh, f, ns, nm).k + kCPL * grp;
       f32x4 c4 = {0, 0, 0, 0};
 #pragma unroll
       for (int ks = 0; ks < kCPL / 8; ++ks) {
@@ -364,7 +377,7 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
       {
         const int r = lane >> 2;  // staged row: g = r/4, i = r%4
         const int64_t tok = f0 + 16 * (r >> 2) + 4 * q + (r & 3);
-        const uint16_t* src = fp16_token<MID_F16, DK>(p, b, kvh, tok < F ? tok : F - 1).v + kCPL * (lane & 3);
+        const uint16_t* src = fp16_token<MID_F16, DK>(p, b, kvh, tok < F ? tok : F - 1, ns, nm).v + kCPL * (lane & 3);
 #pragma unroll
         for (int c = 0; c < kCPL / 8; ++c)
           *reinterpret_cast<uint4*>(vt16 + r * kV16Pitch + kCPL * (lane & 3) + 8 * c) = ldg16(src + 8 * c);
@@ -395,9 +408,9 @@ __global__ __launch_bounds__(kThreads) void decode_mfma_kernel(Params p) {
   if (tau < nF) tau += ((nF - tau + kWaves - 1) / kWaves) * kWaves;
   if (!MID_F16 && tau < t1) {
     constexpr int kRowB = GE::kRowB;
-    const uint8_t* kc = p.mid.k_codes + bkv * M * kRowB;
-    const uint8_t* vc = p.mid.v_codes + bkv * M * kRowB;
-    const uint16_t* vsg = p.mid.v_scale + bkv * M;
+    const uint8_t* kc = p.mid.k_codes + bkv * Mc * kRowB;
+    const uint8_t* vc = p.mid.v_codes + bkv * Mc * kRowB;
+    const uint16_t* vsg = p.mid.v_scale + bkv * Mc;
     auto issue = [&](int64_t t, uint32_t st) {
       const int64_t m0 = (t - nF) * kTileT;
       if constexpr (DK == 128) {

@@ -309,7 +309,7 @@ typedef struct fade_mid_tier {
 typedef struct fade_decode_args {
   int64_t B, Hq, Hkv, D;       /* D a multiple of 8 in [8, 256] (the matrix-core kernels take
                                   128, the general one also 64 and 256 for FADE_MID_SYM 4-bit, FADE_MID_FP16
-                                  and FADE_MID_NONE without lens; other cases run the portable
+                                  and FADE_MID_NONE; other cases run the portable
                                   kernel, which reads every middle format and per-row lens, not
                                   pages or a rotation); Hq % Hkv == 0; Hq/Hkv <= 8 */
   const void* q;               /* [B,Hq,1,D] fp16 */

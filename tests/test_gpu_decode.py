@@ -510,15 +510,32 @@ def test_tiered_decode_ragged_lens(dev, fmt, n_splits, kernel):
         assert err <= ATOL, (b, err)
 
 
-def test_tiered_decode_ragged_lens_rejected_on_other_kernels(dev):
-    """Per-row lengths are read by the INT4 and portable kernels; the general matrix-core kernel refuses them."""
-    q, k, v, ns, nr = _case(1, 8, 4, 200, 4, 16, seed=3)
-    mid, _ = _int4_mid(dev, k, v, ns, nr)
+@pytest.mark.parametrize("D", [128, 64, 256])
+@pytest.mark.parametrize("n_splits", [0, 1, 7])
+def test_tiered_decode_ragged_lens_general_kernel(dev, D, n_splits):
+    """Per-row tier lengths on the general matrix-core kernel (kernel=3; the automatic
+    choice at head dims 64 and 256): each row against the oracle over its own tokens,
+    rows with no sink, no middle or no recent tokens included."""
+    print(f"case decode ragged general kernel D={D} n_splits={n_splits}", flush=True)
+    ns_c, mc, nr_c = 4, 600, 64
+    S = ns_c + mc + nr_c
+    B = 5
+    q, k, v = (x.numpy() for x in kv_tensors(B, 4, S, D, seed=78 + D, Hq=16))
+    mid, omid = _int4_mid(dev, k, v, ns_c, nr_c)
+    lens = np.array([[4, 600, 64], [2, 130, 17], [4, 1, 0], [0, 333, 64], [1, 0, 5]], dtype=np.int32)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
-    lens = torch.tensor([[4, 100, 16]], dtype=torch.int32, device=dev)
-    with pytest.raises(ValueError, match="per-row lengths"):
-        tiered_decode_attention(t(q), (t(k[:, :, :4]), t(v[:, :, :4])), mid, (t(k[:, :, 184:]), t(v[:, :, 184:])),
-                                lens=lens, kernel=3)
+    sink = (t(k[:, :, :ns_c]), t(v[:, :, :ns_c]))
+    rec = (t(k[:, :, S - nr_c :]), t(v[:, :, S - nr_c :]))
+    for kernel in (3, 0):
+        out = tiered_decode_attention(t(q), sink, mid, rec, lens=t(lens), n_splits=n_splits,
+                                      kernel=kernel).float().cpu().numpy()
+        for b, (ls, lm, lr) in enumerate(lens):
+            ref = oatt.tiered_decode(
+                q[b : b + 1], k[b : b + 1, :, :ls], v[b : b + 1, :, :ls], _row_slice_mid(omid, b, lm),
+                k[b : b + 1, :, S - nr_c : S - nr_c + lr], v[b : b + 1, :, S - nr_c : S - nr_c + lr],
+            )
+            err = np.abs(out[b : b + 1] - ref).max()
+            assert err <= ATOL, (kernel, b, err)
 
 
 @pytest.mark.parametrize("fmt", ["int4", "asym42"])
