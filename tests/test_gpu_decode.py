@@ -36,6 +36,53 @@ class _Err(float):
         return f"{float(self)!r} ({self.note})" if self.note else repr(float(self))
 
 
+def _stored_partials_err(qt, sink, mid_gpu, rec, kernel, n_splits, ref):
+    """Max-abs error against ``ref`` of the split partials that the last call
+    left in the workspace shared by the calls on the current stream, merged
+    on the CPU; None when that call had one split.
+
+    The packed INT4 kernel stores partial (m, l, acc) of split j, kv pair bkv
+    and group head h at index ((P bkv + h // 4) n + j) 4 + h % 4 (P head
+    passes, n splits), (m, l) after the counters and acc after those, and
+    its last workgroup merges them.  After a wrong output, a small error here
+    says that every split's partial was right and the merge read something
+    else; a large one says that a split computed a wrong partial."""
+    import ctypes
+
+    from fade_amd import _lib
+    from fade_amd.kernels.tiered_attn import TieredDecodePlan
+
+    s = torch.cuda.current_stream(qt.device).cuda_stream
+    plan = TieredDecodePlan(qt, sink, mid_gpu, rec, n_splits=n_splits, kernel=kernel, stream=s)
+    nb = ctypes.c_int64(0)
+    _lib.check(plan._lib.fade_tiered_decode_workspace_bytes(plan._argp, nb), "fade_tiered_decode_workspace_bytes")
+    B, Hq, _, D = qt.shape
+    Hkv = int(plan.args.Hkv)
+    G = Hq // Hkv
+    P = -(-G // 4)
+    rows = B * max(Hq, Hkv * 4 * P)
+    r256 = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    ml_off = r256(4 * B * Hkv * P)
+    n = next((n for n in range(1, 1 << 16) if ml_off + r256(rows * n * 8) + rows * n * D * 4 == nb.value), None)
+    if n is None or n == 1:
+        return None
+    ws = plan.workspace.cpu().numpy()
+    acc_off = ml_off + r256(rows * n * 8)
+    ml = ws[ml_off : ml_off + rows * n * 8].view(np.float32)
+    acc = ws[acc_off : acc_off + rows * n * D * 4].view(np.float32)
+    out = np.zeros((B, Hq, D), np.float64)
+    for b in range(B):
+        for kvh in range(Hkv):
+            for h in range(G):
+                pis = [((P * (b * Hkv + kvh) + h // 4) * n + j) * 4 + h % 4 for j in range(n)]
+                m = np.array([ml[2 * pi] for pi in pis], np.float64)
+                w = np.exp2(m - m.max())
+                L = sum(w[j] * ml[2 * pi + 1] for j, pi in enumerate(pis))
+                o = sum(w[j] * acc[pi * D : pi * D + D].astype(np.float64) for j, pi in enumerate(pis))
+                out[b, kvh * G + h] = o / L
+    return float(np.abs(out - ref.reshape(B, Hq, D)).max())
+
+
 def _run(dev, q, k, v, ns, nr, mid_gpu, mid_oracle, kernel=0, n_splits=0):
     S = k.shape[2]
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
@@ -46,8 +93,11 @@ def _run(dev, q, k, v, ns, nr, mid_gpu, mid_oracle, kernel=0, n_splits=0):
     err = np.abs(out.float().cpu().numpy() - ref).max()
     if err <= ATOL:
         return err
-    # a failure says whether the same call, run again, agrees, and whether the
-    # GPU-quantized middle tier equals the oracle's codes and scales
+    # a failure says whether the split partials the call stored were right
+    # (read before anything else runs on the shared workspace), whether the
+    # same call, run again, agrees, and whether the GPU-quantized middle tier
+    # equals the oracle's codes and scales
+    part = _stored_partials_err(t(q), sink, mid_gpu, rec, kernel, n_splits, ref) if kernel == 2 else None
     again = tiered_decode_attention(t(q), sink, mid_gpu, rec, kernel=kernel, n_splits=n_splits)
     err2 = np.abs(again.float().cpu().numpy() - ref).max()
     same_mid = None
@@ -56,7 +106,9 @@ def _run(dev, q, k, v, ns, nr, mid_gpu, mid_oracle, kernel=0, n_splits=0):
             np.array_equal(getattr(mid_gpu, a).cpu().numpy().view(np.uint8), np.asarray(mid_oracle[b]).view(np.uint8))
             for a, b in (("k_codes", "kq"), ("v_codes", "vq"), ("k_scale", "ks"), ("v_scale", "vs"))
         )
-    return _Err(err, f"re-run error {err2:.3g}, middle tier equal to the oracle's: {same_mid}")
+    stored = "n/a" if part is None else f"{part:.3g}"
+    return _Err(err, f"stored split partials merged on the CPU: error {stored}, re-run error {err2:.3g}, "
+                     f"middle tier equal to the oracle's: {same_mid}")
 
 
 def _int4_mid(dev, k, v, ns, nr):
@@ -105,6 +157,33 @@ def test_tiered_decode_int4_fast_path_shapes(dev, B, Hq, Hkv, S, ns, nr):
     mid, omid = _int4_mid(dev, k, v, ns, nr)
     for n_splits in (0, 1, 5):
         assert _run(dev, q, k, v, ns, nr, mid, omid, kernel=2, n_splits=n_splits) <= ATOL, n_splits
+
+
+@pytest.mark.parametrize(
+    "B,Hq,Hkv,S,ns,nr,n_splits",
+    [
+        (1, 4, 1, 300, 0, 37, 0),  # eight one-tile splits
+        (2, 8, 4, 777, 4, 64, 3),  # G=2
+        (2, 28, 4, 700, 4, 64, 5),  # G=7: heads 4..6 in the second pass's slot
+        (1, 32, 8, 2048, 4, 64, 0),  # config 0
+    ],
+)
+def test_stored_split_partials_merge_to_the_output(dev, B, Hq, Hkv, S, ns, nr, n_splits):
+    """The split partials a packed-kernel call leaves in the shared workspace,
+    merged on the CPU, match the oracle: the layout the failure diagnosis
+    decodes is the kernel's."""
+    print(f"case stored partials B={B} Hq={Hq} Hkv={Hkv} S={S} n_splits={n_splits}", flush=True)
+    q, k, v, ns, nr = _case(B, Hq, Hkv, S, ns, nr, seed=3000 + S)
+    mid, omid = _int4_mid(dev, k, v, ns, nr)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    sink = (t(k[:, :, :ns]), t(v[:, :, :ns])) if ns else None
+    rec = (t(k[:, :, S - nr :]), t(v[:, :, S - nr :])) if nr else None
+    out = tiered_decode_attention(t(q), sink, mid, rec, kernel=2, n_splits=n_splits)
+    ref = oatt.tiered_decode(q, k[:, :, :ns], v[:, :, :ns], omid, k[:, :, S - nr :], v[:, :, S - nr :])
+    part = _stored_partials_err(t(q), sink, mid, rec, 2, n_splits, ref)
+    assert part is not None, "the call ran one split"
+    assert part <= ATOL, part
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= ATOL
 
 
 def test_tiered_decode_int4_plan_replays(dev):
