@@ -235,7 +235,7 @@ Plan make_plan(const fade_decode_args* a, const Params& p) {
     return pl;
   }
   if (pl.k == Kern::kMfma) {
-    plan_splits(a, mfma_tile(), &pl.n, &pl.tps, mfma_tiles(p) * mfma_tile(), 512);
+    plan_splits(a, mfma_tile(), &pl.n, &pl.tps, mfma_tiles(p) * mfma_tile(), mfma_target_wgs(p));
     return pl;
   }
   // Portable kernel: at least four 64-token tiles per split, about 1024

@@ -130,6 +130,7 @@ PackedChoice packed_kernel_bf16(const Params& p);
 int mfma_tile();
 // Number of 64-token tiles the matrix-core kernel walks (fp16 tokens, then packed).
 int64_t mfma_tiles(const Params& p);
+int64_t mfma_target_wgs(const Params& p);  // workgroups of one machine-wide wave at the call's head dim
 
 // Split partials and their merge reads: device-coherent (agent-scope) accesses,
 // per instruction, with no whole-cache write-back or invalidate.

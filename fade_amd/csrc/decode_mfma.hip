@@ -630,6 +630,24 @@ bool mfma_supports(const Params& p) {
 
 int mfma_tile() { return kTileT; }
 
+// Workgroups of one machine-wide wave at the call's head dim: LDS and registers
+// allow 3 resident workgroups per CU at head_dim 64, 2 at 128 and 1 at 256
+// (measured at B=16, S=8192: 6 splits of 128 (row, kv head) pairs at 64 and 2
+// at 256 beat the D=128 choice of 4 by 3.5% and 10%).
+int64_t mfma_target_wgs(const Params& p) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        n > 0)
+      cus = n;
+    else
+      (void)hipGetLastError();
+  }
+  const int64_t per_cu = p.D == 64 ? 3 : (p.D == 256 ? 1 : 2);
+  return static_cast<int64_t>(cus > 0 ? cus : 256) * per_cu;
+}
+
 // Token tiles: fp16 tokens first (sink, [fp16 middle], recent), then packed middle tiles.
 int64_t mfma_tiles(const Params& p) {
   const bool mid_f16 = p.mid.fmt == FADE_MID_FP16 || p.mid.fmt == FADE_MID_NONE;
