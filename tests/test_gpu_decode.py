@@ -376,6 +376,13 @@ def test_tiered_decode_rotation_rejects(dev):
         (2, 12, 4, 2000, 4, 256, 0),  # G=3, config-2 windows
         (1, 16, 2, 900, 4, 64, 0),  # G=8: eight heads in one pass
         (2, 24, 4, 700, 4, 64, 3),  # G=6
+        # short fp16 windows: a partial tile, half a tile, one tile and a token, sink only;
+        # several tiles in one split and one tile per split
+        (2, 8, 2, 400, 0, 5, 0),
+        (1, 8, 2, 400, 0, 8, 4),
+        (2, 16, 4, 500, 1, 8, 1),
+        (1, 8, 2, 400, 3, 0, 0),
+        (1, 32, 8, 700, 4, 9, 0),
     ],
 )
 def test_tiered_decode_sym2_fast_path(dev, B, Hq, Hkv, S, ns, nr, n_splits):
@@ -403,6 +410,38 @@ def test_tiered_decode_sym2_fast_path(dev, B, Hq, Hkv, S, ns, nr, n_splits):
     krn, vrn, qrn = kr.cpu().numpy(), vr.cpu().numpy(), qr.cpu().numpy()
     ref = oatt.tiered_decode(qrn, krn[:, :, :ns], vrn[:, :, :ns], omid, krn[:, :, S - nr :], vrn[:, :, S - nr :])
     assert np.abs(out - ref).max() <= ATOL
+
+
+@pytest.mark.parametrize("n_splits", [0, 1, 7])
+def test_tiered_decode_sym2_ragged_lens(dev, n_splits):
+    """Per-row tier lengths on the symmetric 2-bit instance (fp16 tiles counted per row in
+    the kernel): each row against the oracle over its own tokens, in the rotated basis as
+    in the fast-path test."""
+    print(f"case decode sym2 ragged n_splits={n_splits}", flush=True)
+    R = torch.from_numpy(np.load(__file__.rsplit("/", 1)[0] + "/golden/rotation_d128_seed42.npy")).to(dev)
+    ns_c, mc, nr_c, B = 4, 600, 64, 5
+    S = ns_c + mc + nr_c
+    q, k, v, _, _ = _case(B, 16, 4, S, ns_c, nr_c, seed=79)
+    rot = lambda a: (torch.from_numpy(np.ascontiguousarray(a)).to(dev).float() @ R.T).to(torch.float16)  # noqa: E731
+    qr, kr, vr = rot(q), rot(k), rot(v)
+    kp, ks = frq.rotated_quant_k(torch.from_numpy(np.ascontiguousarray(k[:, :, ns_c : S - nr_c])).to(dev), R, 2)
+    vp, vs = frq.rotated_quant_v(torch.from_numpy(np.ascontiguousarray(v[:, :, ns_c : S - nr_c])).to(dev), R, 2)
+    mid = MiddleTier("sym", kp, vp, ks, vs, k_bits=2, v_bits=2)
+    omid = {"fmt": "rot", "kq": kp.cpu().numpy(), "ks": ks.cpu().numpy(), "vq": vp.cpu().numpy(),
+            "vs": vs.cpu().numpy(), "R": np.eye(128, dtype=np.float32), "k_bits": 2, "v_bits": 2}
+    lens = np.array([[4, 600, 64], [2, 130, 9], [4, 1, 0], [0, 333, 8], [1, 0, 5]], dtype=np.int32)
+    sink = (kr[:, :, :ns_c].contiguous(), vr[:, :, :ns_c].contiguous())
+    rec = (kr[:, :, S - nr_c :].contiguous(), vr[:, :, S - nr_c :].contiguous())
+    out = tiered_decode_attention(qr, sink, mid, rec, lens=torch.from_numpy(lens).to(dev), n_splits=n_splits,
+                                  kernel=2).float().cpu().numpy()
+    krn, vrn, qrn = kr.cpu().numpy(), vr.cpu().numpy(), qr.cpu().numpy()
+    for b, (ls, lm, lr) in enumerate(lens):
+        ref = oatt.tiered_decode(
+            qrn[b : b + 1], krn[b : b + 1, :, :ls], vrn[b : b + 1, :, :ls], _row_slice_mid(omid, b, lm),
+            krn[b : b + 1, :, S - nr_c : S - nr_c + lr], vrn[b : b + 1, :, S - nr_c : S - nr_c + lr],
+        )
+        err = np.abs(out[b : b + 1] - ref).max()
+        assert err <= ATOL, (b, err)
 
 
 def _asym_mid(dev, k, v, ns, nr, k_bits, v_bits):
@@ -478,9 +517,9 @@ def _row_slice_mid(omid, b, lm):
     """The oracle middle tier of batch row b restricted to its first lm tokens."""
     out = {}
     for key, val in omid.items():
-        if not isinstance(val, np.ndarray):
+        if not isinstance(val, np.ndarray) or key == "R":
             out[key] = val
-        elif key == "ks" and omid["fmt"] == "int4":
+        elif key == "ks" and omid["fmt"] in ("int4", "rot"):
             out[key] = val[b : b + 1]  # per-channel K scale [B,H,1,D]
         else:
             out[key] = val[b : b + 1, :, :lm]
