@@ -144,6 +144,56 @@ __device__ __forceinline__ void store_codes(uint8_t* dst, const int* c) {
   }
 }
 
+// ---- packed fp16 INT4 codes (the fp16 reference INT4 quantizers' fast path) ----
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+// Eight fp16 values (four packed pairs, element 2k in the low half of pair k)
+// hold neither inf nor NaN.
+__device__ __forceinline__ bool finite8(const uint4& w) {
+  auto mag = [](uint32_t a) { return __builtin_bit_cast(u16x2, a & 0x7FFF7FFFu); };
+  const u16x2 t = __builtin_elementwise_max(__builtin_elementwise_max(mag(w.x), mag(w.y)),
+                                            __builtin_elementwise_max(mag(w.z), mag(w.w)));
+  return (t[0] < 0x7C00) & (t[1] < 0x7C00);
+}
+
+__device__ __forceinline__ void f16x8_to_f32(const uint4& w, float* v) {
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = h2f(static_cast<uint16_t>(u[i] & 0xFFFFu));
+    v[2 * i + 1] = h2f(static_cast<uint16_t>(u[i] >> 16));
+  }
+}
+
+// The INT4 codes of eight fp16 values x times fp16 inverse scales inv (pairs
+// laid out alike), packed as store_codes<4> packs them, two elements per
+// instruction: p = x * inv rounded once to fp16 (the reference's fp16
+// multiply); p + 1536 rounds p half-to-even to an integer held in the sum's
+// low mantissa bits (the fp16 ulp at 1536 is 1, and 1536 is even); the clamp
+// to [1528, 1543] is the clamp of the code to [-8, 7]; the sum's low 4 bits
+// are the code's two's-complement nibble.  Equal to sym_code<MODE_F16, -8, 7>
+// for finite x and finite inv > 0 (p is then never NaN; an inf p clamps);
+// callers take the scalar path otherwise.
+__device__ __forceinline__ uint32_t codes4_f16(const uint4& x, const uint4& inv) {
+#pragma clang fp contract(off)
+  const h2_t bias = {static_cast<_Float16>(1536.0f), static_cast<_Float16>(1536.0f)};
+  const h2_t lo = {static_cast<_Float16>(1528.0f), static_cast<_Float16>(1528.0f)};
+  const h2_t hi = {static_cast<_Float16>(1543.0f), static_cast<_Float16>(1543.0f)};
+  auto pair = [&](uint32_t a, uint32_t b) {
+    const h2_t p = __builtin_bit_cast(h2_t, a) * __builtin_bit_cast(h2_t, b);
+    const h2_t c = __builtin_elementwise_min(__builtin_elementwise_max(p + bias, lo), hi);
+    return __builtin_bit_cast(uint32_t, c);
+  };
+  const uint32_t d0 = pair(x.x, inv.x), d1 = pair(x.y, inv.y), d2 = pair(x.z, inv.z), d3 = pair(x.w, inv.w);
+  // low byte of every half (the nibble in its low 4 bits), element order
+  const uint32_t t = __builtin_amdgcn_perm(d1, d0, 0x06040200u) & 0x0F0F0F0Fu;
+  const uint32_t u = __builtin_amdgcn_perm(d3, d2, 0x06040200u) & 0x0F0F0F0Fu;
+  // bytes 0 and 2: (nibble 2j << 4) | nibble 2j + 1
+  const uint32_t ty = (t << 4) | (t >> 8), uy = (u << 4) | (u >> 8);
+  return __builtin_amdgcn_perm(uy, ty, 0x06040200u);
+}
+
 // Unpack 8 signed codes of one lane.
 template <int BITS>
 __device__ __forceinline__ void load_codes(const uint8_t* src, int* c) {
@@ -188,10 +238,20 @@ __global__ __launch_bounds__(kBlock) void quant_token_kernel(const InT* __restri
   const int row_bytes = (D / 8) * lane_bytes<BITS>();
   const int c = threadIdx.x % LPR;
   const bool on = c * 8 < D;  // lanes past the row's D / 8 groups of 8 channels idle
+  constexpr bool kPk = MODE == MODE_F16 && BITS == 4 && std::is_same<InT, uint16_t>::value;
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; r < rows;
        r += static_cast<int64_t>(gridDim.x) * RP) {
     float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (on) load8(x + (fs ? r * fs : row_offset(r, H, S, sb, sh, ss)) + c * 8, v);
+    uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+    const InT* src = x + (fs ? r * fs : row_offset(r, H, S, sb, sh, ss)) + c * 8;
+    if constexpr (kPk) {
+      if (on) {
+        raw = *reinterpret_cast<const uint4*>(src);
+        f16x8_to_f32(raw, v);
+      }
+    } else {
+      if (on) load8(src, v);
+    }
     float a = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) a = absmax_nan(a, v[j]);
@@ -199,6 +259,14 @@ __global__ __launch_bounds__(kBlock) void quant_token_kernel(const InT* __restri
     float inv;
     typename ScaleOf<MODE>::T sc;
     sym_params<MODE, QRange<BITS>::hi>(a, inv, sc);
+    if constexpr (kPk) {
+      if (on && inv > 0.0f && inv < INFINITY && finite8(raw)) {
+        const uint32_t ih = static_cast<uint32_t>(f2h(inv)) * 0x10001u;  // inv is an fp16 value
+        *reinterpret_cast<uint32_t*>(packed + r * row_bytes + c * 4) = codes4_f16(raw, make_uint4(ih, ih, ih, ih));
+        if (c == 0) scale[r] = sc;
+        continue;
+      }
+    }
     int code[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) code[j] = sym_code<MODE, QRange<BITS>::lo, QRange<BITS>::hi>(v[j], inv);
@@ -273,6 +341,34 @@ __global__ __launch_bounds__(kBlock) void quant_channel_kernel(
   const int64_t s0 = blk * rows_per_block;
   const int64_t s1 = s0 + rows_per_block < S ? s0 + rows_per_block : S;
   const InT* base = x + (bh / H) * sb + (bh % H) * sh + c * 8;
+  constexpr bool kPk = MODE == MODE_F16 && BITS == 4 && std::is_same<InT, uint16_t>::value;
+  if constexpr (kPk) {
+    // fp16 inverse scales as packed pairs; any non-finite or zero one sends
+    // this lane's rows through the scalar path
+    bool inv_ok = true;
+    uint32_t ivp[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      inv_ok = inv_ok && iv[2 * j] > 0.0f && iv[2 * j] < INFINITY && iv[2 * j + 1] > 0.0f && iv[2 * j + 1] < INFINITY;
+      ivp[j] = static_cast<uint32_t>(f2h(iv[2 * j])) | (static_cast<uint32_t>(f2h(iv[2 * j + 1])) << 16);
+    }
+    const uint4 invv = make_uint4(ivp[0], ivp[1], ivp[2], ivp[3]);
+    for (int64_t s = s0 + rs; s < s1; s += RP) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(base + s * ss);
+      uint8_t* dst = packed + (bh * S + s) * row_bytes + c * 4;
+      if (inv_ok && finite8(raw)) {
+        *reinterpret_cast<uint32_t*>(dst) = codes4_f16(raw, invv);
+      } else {
+        float v[8];
+        f16x8_to_f32(raw, v);
+        int code[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) code[j] = sym_code<MODE, QRange<BITS>::lo, QRange<BITS>::hi>(v[j], iv[j]);
+        store_codes<BITS>(dst, code);
+      }
+    }
+    return;
+  }
   for (int64_t s = s0 + rs; s < s1; s += RP) {
     float v[8];
     load8(base + s * ss, v);

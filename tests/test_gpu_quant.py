@@ -101,6 +101,24 @@ def test_quant_strided_views(dev):
     assert torch.equal(c[0], d[0]) and torch.equal(c[1], d[1])
 
 
+@pytest.mark.parametrize("shape", SHAPES)
+def test_quant_int4_nan_inf_bit_exact(dev, shape):
+    """fp16 K and V with a NaN, a +inf and a -inf: the rows and channels they
+    touch take the quantizers' scalar path (NaN scales and codes 0, inf scales
+    with codes 0: finite x * 0, inf * 0 -> NaN -> 0), the rest the packed fp16
+    path; both bit-exact against the oracle."""
+    print(f"case quant_int4 nan/inf {shape}", flush=True)
+    x = _edge_tensor(shape, 5)
+    x[0, 0, 2, 9] = np.nan
+    x[0, -1, 3, 10] = np.inf
+    x[-1, 0, x.shape[2] - 1, 11] = -np.inf
+    for quant, oquant in ((fq.quant_k_int4, oq.quant_k_int4), (fq.quant_v_int4, oq.quant_v_int4)):
+        packed, scale = quant(torch.from_numpy(x).to(dev))
+        op, osc = oquant(x)
+        assert np.array_equal(packed.cpu().numpy(), op)
+        _same(scale.cpu().numpy(), osc, "f16")
+
+
 @pytest.mark.parametrize("D", [128, 96, 16])
 def test_dequant_int4_bit_exact(dev, D):
     print(f"case dequant_int4 D={D}", flush=True)
