@@ -318,10 +318,7 @@ __global__ __launch_bounds__(kBlock) void quant_channel_kernel(
   constexpr int RP = kBlock / LPR;
   constexpr int DP = LPR * 8;  // the instance's channel capacity (>= D)
   const int row_bytes = (D / 8) * lane_bytes<BITS>();
-  // S-blocks in the reverse of pass 1's dispatch order: the rows pass 1 read
-  // last are read first, while the device's last-level cache still holds them
-  const int64_t bh = gridDim.y - 1 - blockIdx.y;
-  const int64_t blk = gridDim.x - 1 - blockIdx.x;
+  const int64_t bh = blockIdx.y;
   __shared__ float inv_s[DP];
   for (int d = threadIdx.x; d < D; d += kBlock) {
     float a = 0.0f;
@@ -330,7 +327,7 @@ __global__ __launch_bounds__(kBlock) void quant_channel_kernel(
     typename ScaleOf<MODE>::T sc;
     sym_params<MODE, QRange<BITS>::hi>(a, inv, sc);
     inv_s[d] = inv;
-    if (blk == 0) scale[bh * D + d] = sc;
+    if (blockIdx.x == 0) scale[bh * D + d] = sc;
   }
   __syncthreads();
   const int c = threadIdx.x % LPR, rs = threadIdx.x / LPR;
@@ -338,7 +335,7 @@ __global__ __launch_bounds__(kBlock) void quant_channel_kernel(
   float iv[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) iv[j] = inv_s[c * 8 + j];
-  const int64_t s0 = blk * rows_per_block;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
   const int64_t s1 = s0 + rows_per_block < S ? s0 + rows_per_block : S;
   const InT* base = x + (bh / H) * sb + (bh % H) * sh + c * 8;
   constexpr bool kPk = MODE == MODE_F16 && BITS == 4 && std::is_same<InT, uint16_t>::value;

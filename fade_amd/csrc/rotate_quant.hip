@@ -330,21 +330,18 @@ __global__ __launch_bounds__(kThreads) void rotq_channel_kernel(const uint16_t* 
   __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][2 * kRows * StagePitch<BITS>::value];
   __shared__ float inv_s[kD];
   load_r(R, rt);
-  // S-blocks in the reverse of pass 1's dispatch order: the rows pass 1 read
-  // last are read first, while the device's last-level cache still holds them
-  const int64_t bh = gridDim.y - 1 - blockIdx.y;
-  const int64_t blk = gridDim.x - 1 - blockIdx.x;
+  const int64_t bh = blockIdx.y;
   const int nsb = gridDim.x;
   for (int d = threadIdx.x; d < kD; d += kThreads) {
     float a = 0.0f;
     for (int k = 0; k < nsb; ++k) a = fmaxf(a, partial[(bh * nsb + k) * kD + d]);
     uint16_t sc;
     inv_s[d] = sym_inv(a, QMAX, &sc);
-    if (blk == 0) scale[bh * kD + d] = sc;
+    if (blockIdx.x == 0) scale[bh * kD + d] = sc;
   }
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 31, h = lane >> 5;
-  const int64_t s0 = blk * rows_per_block;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
   const int64_t s1 = s0 + rows_per_block < gm.S ? s0 + rows_per_block : gm.S;
   const uint16_t* base = x + (bh / gm.H) * gm.sb + (bh % gm.H) * gm.sh;
   uint8_t* out = packed + bh * gm.S * RB;
