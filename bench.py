@@ -270,6 +270,17 @@ def quant_cases(dev):
         out.append((name, CallPlan("fade_quant_asym", lambda s_, xm=xm, pk=pk, sc=sc, zp=zp, xs=xs, bits=bits, sh=(B, H, S, D): (
             xm.data_ptr(), *sh, *xs, bits, 32, pk.data_ptr(), sc.data_ptr(), zp.data_ptr(), s_), (xm, pk, sc, zp)),
             xm.numel() * 2 + pk.numel() + 2 * sc.numel() * 2))
+    # config 2's V in the reference's literal grouped INT2 (the K4 + V2 format's V, the INT2
+    # tier): int8 codes and a per-(64-token group, channel) fp16 scale
+    xm = v2[:, :, c2.n_sink : c2.S - c2.recent].contiguous().to(dev)
+    B, H, S, D = xm.shape
+    S_pad = -(-S // 64) * 64
+    cq = torch.empty(B, H, S_pad, D, dtype=torch.int8, device=dev)
+    cs = torch.empty(B, H, S_pad // 64, D, dtype=torch.float16, device=dev)
+    xs = (xm.stride(0), xm.stride(1), xm.stride(2))
+    out.append(("c2_quant_int2_grouped_v", CallPlan("fade_quant_int2_grouped", lambda s_, xm=xm, cq=cq, cs=cs, xs=xs, sh=(B, H, S, S_pad, D): (
+        xm.data_ptr(), *sh, *xs, 64, cq.data_ptr(), cs.data_ptr(), s_), (xm, cq, cs)),
+        xm.numel() * 2 + cq.numel() + cs.numel() * 2))
     # rotated backend at config 2's 2-bit middle tier: fused MFMA rotation + quantize
     R = torch.from_numpy(np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden",
                                               "rotation_d128_seed42.npy"))).to(dev)

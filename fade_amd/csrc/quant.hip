@@ -194,6 +194,23 @@ __device__ __forceinline__ uint32_t codes4_f16(const uint4& x, const uint4& inv)
   return __builtin_amdgcn_perm(uy, ty, 0x06040200u);
 }
 
+// The INT2 codes (clamped to [-2, 1]) of eight fp16 values, as eight int8
+// bytes: the same rounding as codes4_f16, clamped to [1534, 1537], whose low
+// byte is the code's two's complement.  Same validity as codes4_f16.
+__device__ __forceinline__ uint2 codes2_i8_f16(const uint4& x, const uint4& inv) {
+#pragma clang fp contract(off)
+  const h2_t bias = {static_cast<_Float16>(1536.0f), static_cast<_Float16>(1536.0f)};
+  const h2_t lo = {static_cast<_Float16>(1534.0f), static_cast<_Float16>(1534.0f)};
+  const h2_t hi = {static_cast<_Float16>(1537.0f), static_cast<_Float16>(1537.0f)};
+  auto pair = [&](uint32_t a, uint32_t b) {
+    const h2_t p = __builtin_bit_cast(h2_t, a) * __builtin_bit_cast(h2_t, b);
+    const h2_t c = __builtin_elementwise_min(__builtin_elementwise_max(p + bias, lo), hi);
+    return __builtin_bit_cast(uint32_t, c);
+  };
+  const uint32_t d0 = pair(x.x, inv.x), d1 = pair(x.y, inv.y), d2 = pair(x.z, inv.z), d3 = pair(x.w, inv.w);
+  return make_uint2(__builtin_amdgcn_perm(d1, d0, 0x06040200u), __builtin_amdgcn_perm(d3, d2, 0x06040200u));
+}
+
 // Unpack 8 signed codes of one lane.
 template <int BITS>
 __device__ __forceinline__ void load_codes(const uint8_t* src, int* c) {
@@ -460,6 +477,96 @@ __global__ void quant_int2_grouped_kernel(const T* __restrict__ x, int64_t H, in
     const int64_t s = g * group + i;
     const float v = s < S ? to_f32(base[s * ss]) : 0.0f;
     codes[(bh * S_pad + s) * D + d] = static_cast<int8_t>(sym_code<MODE, -2, 1>(v, inv));
+  }
+}
+
+// One (S-group, (b, h)) per block in a single pass: each lane loads 8
+// channels (16 bytes) of up to NR of the group's rows once, the group's column
+// absmax is reduced through LDS, and the codes come from the registers.
+// Rows past S (the padding up to S_pad) count as zeros, as in the kernel above.
+template <typename T, int MODE, int LPR, int NR>
+__global__ __launch_bounds__(kBlock) void quant_int2_grouped_rows_kernel(
+    const T* __restrict__ x, int D, int64_t H, int64_t S, int64_t S_pad, int64_t sb, int64_t sh, int64_t ss,
+    int group, int8_t* __restrict__ codes, typename ScaleOf<MODE>::T* __restrict__ scale) {
+  constexpr int RP = kBlock / LPR;
+  constexpr int DP = LPR * 8;  // the instance's channel capacity (>= D)
+  const int c = threadIdx.x % LPR, rs = threadIdx.x / LPR;
+  const bool on = c * 8 < D;
+  const int64_t g = blockIdx.x, bh = blockIdx.y, G = gridDim.x;
+  const T* base = x + (bh / H) * sb + (bh % H) * sh + (on ? c * 8 : 0);
+  // fp16: the rows stay as their fp16 bits (4 registers a row) and the codes
+  // come from packed fp16 arithmetic where the values and scales are finite
+  constexpr bool kPk = MODE == MODE_F16 && std::is_same<T, uint16_t>::value;
+  float v[kPk ? 1 : NR][8];
+  uint4 raw[kPk ? NR : 1];
+  float m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int r = rs + i * RP;
+    const int64_t srow = g * group + r;
+    const bool ld = on && r < group && srow < S;
+    float t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if constexpr (kPk) {
+      raw[i] = ld ? *reinterpret_cast<const uint4*>(base + srow * ss) : make_uint4(0u, 0u, 0u, 0u);
+      f16x8_to_f32(raw[i], t);
+    } else {
+      if (ld) load8(base + srow * ss, t);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[i][j] = t[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m[j] = absmax_nan(m[j], t[j]);
+  }
+  __shared__ float red[RP][DP];
+  __shared__ float inv_s[DP];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) red[rs][c * 8 + j] = m[j];
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += kBlock) {
+    float a = 0.0f;
+    for (int k = 0; k < RP; ++k) a = absmax_nan(a, red[k][d]);
+    float inv;
+    typename ScaleOf<MODE>::T sc;
+    sym_params<MODE, 1>(a, inv, sc);
+    inv_s[d] = inv;
+    scale[(bh * G + g) * D + d] = sc;
+  }
+  __syncthreads();
+  if (!on) return;
+  float iv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) iv[j] = inv_s[c * 8 + j];
+  bool inv_ok = true;
+  uint32_t ivp[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    inv_ok = inv_ok && iv[2 * j] > 0.0f && iv[2 * j] < INFINITY && iv[2 * j + 1] > 0.0f && iv[2 * j + 1] < INFINITY;
+    ivp[j] = static_cast<uint32_t>(f2h(iv[2 * j])) | (static_cast<uint32_t>(f2h(iv[2 * j + 1])) << 16);
+  }
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int r = rs + i * RP;
+    if (r < group) {
+      uint2* dst = reinterpret_cast<uint2*>(codes + (bh * S_pad + g * group + r) * D + c * 8);
+      float t[8];
+      if constexpr (kPk) {
+        if (inv_ok && finite8(raw[i])) {
+          *dst = codes2_i8_f16(raw[i], make_uint4(ivp[0], ivp[1], ivp[2], ivp[3]));
+          continue;
+        }
+        f16x8_to_f32(raw[i], t);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = v[i][j];
+      }
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        lo |= static_cast<uint32_t>(sym_code<MODE, -2, 1>(t[j], iv[j]) & 0xFF) << (8 * j);
+        hi |= static_cast<uint32_t>(sym_code<MODE, -2, 1>(t[4 + j], iv[4 + j]) & 0xFF) << (8 * j);
+      }
+      *dst = make_uint2(lo, hi);
+    }
   }
 }
 
@@ -908,6 +1015,19 @@ int quant_int2_grouped(const char* fn, const void* x, int64_t B, int64_t H, int6
   if (BH == 0 || G == 0) return FADE_OK;
   if (BH > 65535) return einval("%s: B*H=%lld exceeds 65535", fn, (long long)BH);
   constexpr int MODE = Int2Mode<T>::value;
+  // single pass with register-resident rows: 8 channels per lane (D a
+  // multiple of 8 up to 256, 16-byte aligned rows) and at most 8 rows per lane
+  const int lpr = D <= 32 ? 4 : (D <= 64 ? 8 : (D <= 128 ? 16 : 32));
+  if (D % 8 == 0 && D <= 256 && group <= 8 * (kBlock / lpr) && aligned(x, 16) && (sb | sh | ss) % 8 == 0) {
+    const dim3 grid(static_cast<unsigned>(G), static_cast<unsigned>(BH));
+    FADE_DISPATCH_LPR(D, {
+      hipLaunchKernelGGL((quant_int2_grouped_rows_kernel<T, MODE, LPR, 8>), grid, dim3(kBlock), 0, as_stream(stream),
+                         static_cast<const T*>(x), static_cast<int>(D), H, S, S_pad, sb, sh, ss,
+                         static_cast<int>(group), static_cast<int8_t*>(codes_i8),
+                         static_cast<typename ScaleOf<MODE>::T*>(scale));
+    });
+    return check_launch(fn);
+  }
   hipLaunchKernelGGL((quant_int2_grouped_kernel<T, MODE>), dim3(static_cast<unsigned>(G), static_cast<unsigned>(BH)),
                      dim3(static_cast<unsigned>(D)), 0, as_stream(stream), static_cast<const T*>(x), H, S, S_pad,
                      sb, sh, ss, static_cast<int>(group), static_cast<int8_t*>(codes_i8),

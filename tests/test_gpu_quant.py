@@ -103,8 +103,8 @@ def test_quant_strided_views(dev):
 
 @pytest.mark.parametrize("shape", SHAPES)
 def test_quant_int4_nan_inf_bit_exact(dev, shape):
-    """fp16 K and V with a NaN, a +inf and a -inf: the rows and channels they
-    touch take the quantizers' scalar path (NaN scales and codes 0, inf scales
+    """fp16 K and V (and grouped INT2) with a NaN, a +inf and a -inf: the rows
+    and channels they touch take the quantizers' scalar path (NaN scales and codes 0, inf scales
     with codes 0: finite x * 0, inf * 0 -> NaN -> 0), the rest the packed fp16
     path; both bit-exact against the oracle."""
     print(f"case quant_int4 nan/inf {shape}", flush=True)
@@ -117,6 +117,11 @@ def test_quant_int4_nan_inf_bit_exact(dev, shape):
         op, osc = oquant(x)
         assert np.array_equal(packed.cpu().numpy(), op)
         _same(scale.cpu().numpy(), osc, "f16")
+    # the reference literal grouped INT2 (64-token groups) on the same input
+    q, sc = fq.quant_int2_padded(torch.from_numpy(x).to(dev), 64)
+    oqv, osc = oq.quant_int2_grouped(oq.pad_to_group(x, 64)[0], 64)
+    assert np.array_equal(q.cpu().numpy(), oqv)
+    _same(sc.cpu().numpy(), osc, "f16")
 
 
 @pytest.mark.parametrize("D", [128, 96, 16])
@@ -235,6 +240,23 @@ def test_quant_int2_grouped_bit_exact(dev, S):
     else:
         with pytest.raises(ValueError, match="divisible by group_size"):
             fq.quant_k_int2(torch.from_numpy(np.ascontiguousarray(x)).to(dev))
+
+
+@pytest.mark.parametrize("group,D,S", [(32, 128, 100), (128, 128, 300), (256, 128, 300), (128, 256, 200), (16, 48, 70)])
+def test_quant_int2_grouped_group_sizes(dev, group, D, S):
+    """Other group sizes, on a strided view: the single-pass kernel keeps up to
+    8 rows per lane in registers (group <= 8 * 256 / (D / 8) rows); beyond that
+    (group 256 at D=128, 128 at D=256) the per-channel loop kernel runs.  Both
+    bit-exact against the oracle."""
+    print(f"case int2 grouped group={group} D={D} S={S}", flush=True)
+    full = _edge_tensor((2, 3, S + 9, D), 11)
+    x = full[:, :, 4 : 4 + S]  # rows strided inside a larger tensor
+    xp, _ = oq.pad_to_group(np.ascontiguousarray(x), group)
+    oqv, osc = oq.quant_int2_grouped(xp, group)
+    xd = torch.from_numpy(full).to(dev)[:, :, 4 : 4 + S]
+    q, sc = fq.quant_int2_padded(xd, group)
+    assert np.array_equal(q.cpu().numpy(), oqv)
+    assert np.array_equal(_u16(sc.cpu().numpy()), _u16(osc))
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
