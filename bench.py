@@ -281,6 +281,12 @@ def quant_cases(dev):
     out.append(("c2_quant_int2_grouped_v", CallPlan("fade_quant_int2_grouped", lambda s_, xm=xm, cq=cq, cs=cs, xs=xs, sh=(B, H, S, S_pad, D): (
         xm.data_ptr(), *sh, *xs, 64, cq.data_ptr(), cs.data_ptr(), s_), (xm, cq, cs)),
         xm.numel() * 2 + cq.numel() + cs.numel() * 2))
+    # and back to fp16 (the INT2 tier's fp16 copy for the fused attention): reads the
+    # codes the line above wrote
+    dq = torch.empty_like(xm)
+    out.append(("c2_dequant_int2_grouped_v", CallPlan("fade_dequant_int2_grouped", lambda s_, cq=cq, cs=cs, dq=dq, sh=(B, H, S_pad, D), S_=S: (
+        cq.data_ptr(), cs.data_ptr(), *sh, 64, S_, dq.data_ptr(), s_), (cq, cs, dq)),
+        cq.numel() + cs.numel() * 2 + dq.numel() * 2))
     # rotated backend at config 2's 2-bit middle tier: fused MFMA rotation + quantize
     R = torch.from_numpy(np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden",
                                               "rotation_d128_seed42.npy"))).to(dev)

@@ -587,6 +587,32 @@ __global__ void dequant_int2_grouped_kernel(const int8_t* __restrict__ codes,
   }
 }
 
+// Row-vectorized form of the kernel above: each lane takes 8 channels of a row
+// (8 code bytes, 8 scales, 8 outputs); the same products and roundings.
+template <typename T, int LPR>
+__global__ __launch_bounds__(kBlock) void dequant_int2_grouped_rows_kernel(const int8_t* __restrict__ codes,
+                                                                           const T* __restrict__ scale, int D,
+                                                                           int64_t S_pad, int64_t group, int64_t S_out,
+                                                                           int64_t rows, T* __restrict__ out) {
+  constexpr int RP = kBlock / LPR;
+  const int c = threadIdx.x % LPR;
+  if (c * 8 >= D) return;  // past the row's channels
+  const int64_t G = S_pad / group;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; r < rows;
+       r += static_cast<int64_t>(gridDim.x) * RP) {
+    const int64_t bh = r / S_out, s = r - bh * S_out;
+    const uint2 w = *reinterpret_cast<const uint2*>(codes + (bh * S_pad + s) * D + c * 8);
+    const T* sp = scale + (bh * G + s / group) * D + c * 8;
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      y[j] = static_cast<float>(static_cast<int8_t>((w.x >> (8 * j)) & 0xFF)) * to_f32(sp[j]);
+      y[4 + j] = static_cast<float>(static_cast<int8_t>((w.y >> (8 * j)) & 0xFF)) * to_f32(sp[4 + j]);
+    }
+    store8(out + r * D + c * 8, y);
+  }
+}
+
 // ------------------------------------------------------ asymmetric groups
 template <int BITS, int LPG, int LPR>
 __global__ __launch_bounds__(kBlock) void quant_asym_kernel(const uint16_t* __restrict__ x, int D,
@@ -1042,6 +1068,15 @@ int dequant_int2_grouped(const char* fn, const void* codes_i8, const void* scale
                   (long long)S_out);
   const int64_t n = B * H * S_out * D;
   if (n == 0) return FADE_OK;
+  if (D % 8 == 0 && D >= 8 && D <= 256 && aligned(codes_i8, 8) && aligned(scale, 16) && aligned(out, 16)) {
+    const int64_t rows = B * H * S_out;
+    FADE_DISPATCH_LPR(D, {
+      hipLaunchKernelGGL((dequant_int2_grouped_rows_kernel<T, LPR>), dim3(grid_for_rows(rows, LPR)), dim3(kBlock), 0,
+                         as_stream(stream), static_cast<const int8_t*>(codes_i8), static_cast<const T*>(scale),
+                         static_cast<int>(D), S_pad, group, S_out, rows, static_cast<T*>(out));
+    });
+    return check_launch(fn);
+  }
   const int grid = static_cast<int>(cdiv(n, 256) < 16384 ? cdiv(n, 256) : 16384);
   hipLaunchKernelGGL(dequant_int2_grouped_kernel<T>, dim3(grid), dim3(256), 0, as_stream(stream),
                      static_cast<const int8_t*>(codes_i8), static_cast<const T*>(scale), B * H, S_pad, D, group,
