@@ -132,25 +132,27 @@ int mfma_tile();
 int64_t mfma_tiles(const Params& p);
 int64_t mfma_target_wgs(const Params& p);  // workgroups of one machine-wide wave at the call's head dim
 
-// Split partials and their merge reads: device-coherent (agent-scope) accesses,
-// per instruction, with no whole-cache write-back or invalidate.
-__device__ __forceinline__ void store_agent(float* p, float v) {
+// Split partials and their merge reads: system-scope accesses (sc0 sc1), which
+// go past the XCD's L2 to memory (stores written through, loads fetched), so a
+// partial whose store has completed is in memory for a merging workgroup on
+// any XCD; per instruction, with no whole-cache write-back or invalidate.
+__device__ __forceinline__ void store_sys(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+                     __HIP_MEMORY_SCOPE_SYSTEM);
 }
-__device__ __forceinline__ float load_agent(const float* p) {
+__device__ __forceinline__ float load_sys(const float* p) {
   return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT));
+                                                     __HIP_MEMORY_SCOPE_SYSTEM));
 }
-// (m, l) of one partial as one 8-byte device-coherent access
-__device__ __forceinline__ void store_agent2(float* p, float a, float b) {
+// (m, l) of one partial as one 8-byte access
+__device__ __forceinline__ void store_sys2(float* p, float a, float b) {
   const uint64_t v = static_cast<uint64_t>(__builtin_bit_cast(uint32_t, a)) |
                      (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, b)) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
-__device__ __forceinline__ void load_agent2(const float* p, float& a, float& b) {
+__device__ __forceinline__ void load_sys2(const float* p, float& a, float& b) {
   const uint64_t v =
-      __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   a = __builtin_bit_cast(float, static_cast<uint32_t>(v));
   b = __builtin_bit_cast(float, static_cast<uint32_t>(v >> 32));
 }

@@ -1277,27 +1277,26 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     } else {
       // H8: heads 4..7 in the second pass's slot (the two-pass layout)
       const int64_t pi = ((slot + (h >> 2)) * n + split) * 4 + (h & 3);
-      store_agent(&p.ws_acc[pi * kD + d], o);
-      if (d == 0) store_agent2(&p.ws_ml[2 * pi], Mh, L);
+      store_sys(&p.ws_acc[pi * kD + d], o);
+      if (d == 0) store_sys2(&p.ws_ml[2 * pi], Mh, L);
     }
   }
   if (n == 1) return;
 
   // ---- the last workgroup of this (batch row, kv head) merges the splits ----
-  // Cross-workgroup protocol at agent scope (the XCDs' L2s are separate caches):
-  // - writers: every (m, l, acc) partial is an agent-scope atomic store
-  //   (global_store ... sc1: written through the L2 to the agent's coherence
-  //   point, so no line of it stays dirty in an L2); every wave waits for the
+  // Cross-workgroup protocol (the XCDs' L2s are separate caches):
+  // - writers: every (m, l, acc) partial is a system-scope store (global_store
+  //   ... sc0 sc1: written through the L2 to memory); every wave waits for the
   //   completion of its own stores (vmcnt(0); the workgroup barrier alone does
   //   not wait for other waves' stores), then thread 0 increments the counter.
-  //   No release fence: its buffer_wbl2 sc1 writes back an XCD's whole L2 for
-  //   the sake of non-atomic stores, which this merge has none of (it cost
-  //   12 us per call at config 1);
+  //   No release fence: its buffer_wbl2 writes back an XCD's whole L2 for the
+  //   sake of non-atomic stores, which this merge has none of (an agent-scope
+  //   release cost 12 us per call at config 1);
   // - the workgroup whose increment returns n - 1 has seen every other
-  //   increment, each issued after its partials completed; it acquires
-  //   (buffer_inv sc1: no L1 or L2 line of an earlier call's partials
-  //   survives) before the barrier that lets its waves issue the partial
-  //   loads, which are agent-scope atomic loads as well.
+  //   increment, each issued after its partials reached memory; it acquires
+  //   (buffer_inv sc1) before the barrier that lets its waves issue the partial
+  //   loads, which are system-scope loads (sc0 sc1: fetched from memory, never
+  //   an L2 line of an earlier call).
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
   __syncthreads();
   if (tid == 0) {
@@ -1347,8 +1346,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             const int idx = tid + e * kThreads;
             const int h = idx < G * kD ? idx >> 7 : 0, d = idx & (kD - 1);
             const int64_t pi = ((slot + (h >> 2)) * n + s0 + j) * 4 + (h & 3);
-            load_agent2(&p.ws_ml[2 * pi], mm[e][j], ll[e][j]);
-            aa[e][j] = load_agent(&p.ws_acc[pi * kD + d]);
+            load_sys2(&p.ws_ml[2 * pi], mm[e][j], ll[e][j]);
+            aa[e][j] = load_sys(&p.ws_acc[pi * kD + d]);
           }
         } else {
 #pragma unroll
