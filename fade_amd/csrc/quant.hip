@@ -148,14 +148,18 @@ __device__ __forceinline__ void store_codes(uint8_t* dst, const int* c) {
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
-// Eight fp16 values (four packed pairs, element 2k in the low half of pair k)
-// hold neither inf nor NaN.
-__device__ __forceinline__ bool finite8(const uint4& w) {
+// The largest magnitude of eight fp16 values (four packed pairs, element 2k in
+// the low half of pair k) as fp16 bits: non-negative fp16 bit patterns order
+// as their values, so an unsigned 16-bit max finds it.  >= 0x7C00: an inf or
+// NaN among them.
+__device__ __forceinline__ uint32_t maxmag8(const uint4& w) {
   auto mag = [](uint32_t a) { return __builtin_bit_cast(u16x2, a & 0x7FFF7FFFu); };
   const u16x2 t = __builtin_elementwise_max(__builtin_elementwise_max(mag(w.x), mag(w.y)),
                                             __builtin_elementwise_max(mag(w.z), mag(w.w)));
-  return (t[0] < 0x7C00) & (t[1] < 0x7C00);
+  return t[0] > t[1] ? t[0] : t[1];
 }
+// Eight fp16 values hold neither inf nor NaN.
+__device__ __forceinline__ bool finite8(const uint4& w) { return maxmag8(w) < 0x7C00u; }
 
 __device__ __forceinline__ void f16x8_to_f32(const uint4& w, float* v) {
   const uint32_t u[4] = {w.x, w.y, w.z, w.w};
@@ -261,28 +265,36 @@ __global__ __launch_bounds__(kBlock) void quant_token_kernel(const InT* __restri
     float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint4 raw = make_uint4(0u, 0u, 0u, 0u);
     const InT* src = x + (fs ? r * fs : row_offset(r, H, S, sb, sh, ss)) + c * 8;
+    float a = 0.0f;
+    bool fin = false;  // fp16 fast path: this lane's 8 values are finite
     if constexpr (kPk) {
-      if (on) {
-        raw = *reinterpret_cast<const uint4*>(src);
+      if (on) raw = *reinterpret_cast<const uint4*>(src);
+      const uint32_t mm = maxmag8(raw);
+      fin = mm < 0x7C00u;
+      if (fin) {
+        a = h2f(static_cast<uint16_t>(mm));  // the lane's absmax, exact
+      } else {
         f16x8_to_f32(raw, v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a = absmax_nan(a, v[j]);
       }
     } else {
       if (on) load8(src, v);
-    }
-    float a = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) a = absmax_nan(a, v[j]);
+      for (int j = 0; j < 8; ++j) a = absmax_nan(a, v[j]);
+    }
     a = group_max_abs<LPR>(a);
     float inv;
     typename ScaleOf<MODE>::T sc;
     sym_params<MODE, QRange<BITS>::hi>(a, inv, sc);
     if constexpr (kPk) {
-      if (on && inv > 0.0f && inv < INFINITY && finite8(raw)) {
+      if (on && inv > 0.0f && inv < INFINITY && fin) {
         const uint32_t ih = static_cast<uint32_t>(f2h(inv)) * 0x10001u;  // inv is an fp16 value
         *reinterpret_cast<uint32_t*>(packed + r * row_bytes + c * 4) = codes4_f16(raw, make_uint4(ih, ih, ih, ih));
         if (c == 0) scale[r] = sc;
         continue;
       }
+      if (fin) f16x8_to_f32(raw, v);  // the scalar path below reads v
     }
     int code[8];
 #pragma unroll
