@@ -1054,9 +1054,11 @@ int quant_int2_grouped(const char* fn, const void* x, int64_t B, int64_t H, int6
   if (BH > 65535) return einval("%s: B*H=%lld exceeds 65535", fn, (long long)BH);
   constexpr int MODE = Int2Mode<T>::value;
   // single pass with register-resident rows: 8 channels per lane (D a
-  // multiple of 8 up to 256, 16-byte aligned rows) and at most 8 rows per lane
+  // multiple of 8 up to 256, 16-byte aligned rows, 8-byte aligned codes) and
+  // at most 8 rows per lane
   const int lpr = D <= 32 ? 4 : (D <= 64 ? 8 : (D <= 128 ? 16 : 32));
-  if (D % 8 == 0 && D <= 256 && group <= 8 * (kBlock / lpr) && aligned(x, 16) && (sb | sh | ss) % 8 == 0) {
+  if (D % 8 == 0 && D <= 256 && group <= 8 * (kBlock / lpr) && aligned(x, 16) && (sb | sh | ss) % 8 == 0 &&
+      aligned(codes_i8, 8)) {
     const dim3 grid(static_cast<unsigned>(G), static_cast<unsigned>(BH));
     FADE_DISPATCH_LPR(D, {
       hipLaunchKernelGGL((quant_int2_grouped_rows_kernel<T, MODE, LPR, 8>), grid, dim3(kBlock), 0, as_stream(stream),
