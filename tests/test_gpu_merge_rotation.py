@@ -6,7 +6,9 @@ read a partial of the previous call (or a tile stage holding a previous tile)
 would return another cache's numbers.  Deterministic calls must reproduce
 their cache's first output bit for bit, and every call must stay within the
 bar of the one-split result, which merges nothing.  The configs' full shapes:
-config 1 (B=16, S=8192) and config 2 (B=4, S=32768).
+config 1 (B=16, S=8192) and config 2 (B=4, S=32768); and one or two kv heads
+of a short row, where every split holds one tile and all the workgroups of a
+(row, kv head) reach the merge together.
 """
 
 import pytest
@@ -32,12 +34,13 @@ def _cache(dev, B, Hkv, S, ns, nr, seed):
     return q, sink, MiddleTier("int4", kq, vq, ks, vs), rec
 
 
-@pytest.mark.parametrize("B,S,nr", [(16, 8192, 64), (4, 32768, 256)])
-def test_split_merge_rotating_caches(dev, B, S, nr):
-    print(f"case merge rotation B={B} S={S}", flush=True)
+@pytest.mark.parametrize("B,Hkv,S,ns,nr", [(16, 8, 8192, 4, 64), (4, 8, 32768, 4, 256), (1, 1, 300, 0, 37),
+                                            (1, 2, 160, 4, 17)])
+def test_split_merge_rotating_caches(dev, B, Hkv, S, ns, nr):
+    print(f"case merge rotation B={B} Hkv={Hkv} S={S}", flush=True)
     cases = []
     for seed in (21, 22, 23):
-        args = _cache(dev, B, 8, S, 4, nr, seed)
+        args = _cache(dev, B, Hkv, S, ns, nr, seed)
         one = tiered_decode_attention(*args, n_splits=1, deterministic=True)
         first = tiered_decode_attention(*args, deterministic=True)
         cases.append((args, one, first))
