@@ -258,6 +258,13 @@ def quant_cases(dev):
     out.append(("c1_quant_v_int4", CallPlan("fade_quant_v_int4", lambda s_, vm=vm, vp=vp, vs=vs, st=st, sh=(B, H, S, D): (
         vm.data_ptr(), *sh, *st, vp.data_ptr(), vs.data_ptr(), s_), (vm, vp, vs)),
         vm.numel() * 2 + vp.numel() + vs.numel() * 2))
+    # dequant_int4 of the two tiers above back to fp16 (materialize's middle tier):
+    # K with its per-channel scale, V with its per-token scale
+    for name, pk, sc, axis in (("c1_dequant_int4_k", kp, ks, _lib.AXIS_CHANNEL), ("c1_dequant_int4_v", vp, vs, _lib.AXIS_TOKEN)):
+        dq = torch.empty(B, H, S, D, dtype=torch.float16, device=dev)
+        out.append((name, CallPlan("fade_dequant_sym", lambda s_, pk=pk, sc=sc, dq=dq, axis=axis, sh=(B, H, S, D): (
+            pk.data_ptr(), sc.data_ptr(), 4, axis, *sh, dq.data_ptr(), s_), (pk, sc, dq)),
+            pk.numel() + sc.numel() * 2 + dq.numel() * 2))
     c2 = CONFIGS[2]
     _, k2, v2 = kv_tensors(c2.B, c2.Hkv, c2.S, c2.D, seed=1002, Hq=c2.Hq)
     for name, x, bits in (("c2_quant_asym_k4", k2, 4), ("c2_quant_asym_v2", v2, 2)):

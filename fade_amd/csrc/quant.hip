@@ -436,6 +436,46 @@ __global__ __launch_bounds__(kBlock) void dequant_sym_kernel(const uint8_t* __re
   const int row_bytes = (D / 8) * lane_bytes<BITS>();
   const int c = threadIdx.x % LPR;
   if (c * 8 >= D) return;  // past the row's channels
+  if constexpr (BITS == 4 && std::is_same<T, uint16_t>::value) {
+    // fp16 out: packed fp16 arithmetic, two elements per instruction.  Byte k
+    // of the lane's 4 code bytes holds elements 2k (high nibble) and 2k + 1
+    // (low nibble); v_perm puts the byte in both halves, a (0, 4) packed
+    // shift brings each nibble to bits 4..7 of its half, and (x & 0x00F0) ^
+    // 0x5480 is the fp16 72 + code (the nibble as offset binary in the
+    // mantissa of 64.0).  72 + code - 72 is exact, and the product with the
+    // fp16 scale is rounded once: fp16(float(code) * float(scale)), the
+    // reference's dequantization, for every scale (inf and NaN included).
+    const h2_t k72 = {static_cast<_Float16>(72.0f), static_cast<_Float16>(72.0f)};
+    const u16x2 sh = {0, 4};
+    // per-channel scales are read 8 at a time (16 bytes): an unaligned scale
+    // tensor takes the scalar loop below
+    const bool vec_ok = axis == FADE_AXIS_TOKEN || (reinterpret_cast<uintptr_t>(scale) & 15) == 0;
+    for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; vec_ok && r < rows;
+         r += static_cast<int64_t>(gridDim.x) * RP) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(packed + r * row_bytes + c * 4);
+      uint32_t sp[4];
+      if (axis == FADE_AXIS_TOKEN) {
+        const uint32_t s1 = scale[r];
+        sp[0] = sp[1] = sp[2] = sp[3] = s1 | (s1 << 16);
+      } else {
+        // the (b, h) of row r: a 32-bit division wherever the values fit
+        const int64_t bh = ((r | S) >> 31) == 0 ? static_cast<int64_t>(static_cast<uint32_t>(r) / static_cast<uint32_t>(S))
+                                                : r / S;
+        const uint4 sv = *reinterpret_cast<const uint4*>(scale + bh * D + c * 8);
+        sp[0] = sv.x, sp[1] = sv.y, sp[2] = sv.z, sp[3] = sv.w;
+      }
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t t = __builtin_amdgcn_perm(w, w, 0x0C000C00u | (k << 16) | k);  // byte k in both halves
+        const uint32_t x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, t) << sh);
+        const h2_t v = __builtin_bit_cast(h2_t, (x & 0x00F000F0u) ^ 0x54805480u) - k72;
+        o[k] = __builtin_bit_cast(uint32_t, v * __builtin_bit_cast(h2_t, sp[k]));
+      }
+      *reinterpret_cast<uint4*>(out + r * D + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    if (vec_ok) return;
+  }
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * RP + threadIdx.x / LPR; r < rows;
        r += static_cast<int64_t>(gridDim.x) * RP) {
     int code[8];

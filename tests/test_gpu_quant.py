@@ -136,6 +136,20 @@ def test_dequant_int4_bit_exact(dev, D):
     assert np.array_equal(_u16(out.cpu().numpy()), _u16(oq.dequant_int4(op, osc)))
 
 
+def test_dequant_int4_unaligned_channel_scale(dev):
+    """A per-channel scale tensor at a 2-byte offset (a contiguous view into a
+    larger buffer) takes the dequantizer's scalar loop; still bit-exact."""
+    print("case dequant_int4 unaligned scale", flush=True)
+    x = _edge_tensor((2, 2, 40, 128), 6)
+    op, osc = oq.quant_k_int4(x)
+    buf = torch.empty(osc.size + 1, dtype=torch.float16, device=dev)
+    buf[1:] = torch.from_numpy(osc.reshape(-1)).to(dev)
+    sc = buf[1:].view(osc.shape)
+    assert sc.data_ptr() % 16 != 0
+    out = fq.dequant_int4(torch.from_numpy(op).to(dev), sc)
+    assert np.array_equal(_u16(out.cpu().numpy()), _u16(oq.dequant_int4(op, osc)))
+
+
 # -------------------------------------------- bfloat16 / float32 K/V input
 _TDT = {"bf16": torch.bfloat16, "f32": torch.float32, "f16": torch.float16}
 
