@@ -58,6 +58,75 @@ __global__ void rerope_gather_kernel(const T* __restrict__ k, int64_t ksb, int64
   }
 }
 
+// Four element pairs (i .. i+3, i+D/2 .. i+D/2+3) per thread: the same
+// arithmetic per element as the kernel above, with 4-element K/V accesses and
+// 16-byte table reads (D/2 a multiple of 4; K/V rows 4-element aligned).
+template <typename T>
+struct alignas(4 * sizeof(T)) Vec4 {
+  T e[4];
+};
+template <typename T>
+__global__ void rerope_gather_vec4_kernel(const T* __restrict__ k, int64_t ksb, int64_t ksh, int64_t kss,
+                                          const T* __restrict__ v, int64_t vsb, int64_t vsh, int64_t vss, int64_t H,
+                                          int64_t S, int D, const int64_t* __restrict__ keep, int64_t n_kept,
+                                          const float* __restrict__ cos_old, const float* __restrict__ sin_old,
+                                          const float* __restrict__ cos_new, const float* __restrict__ sin_new,
+                                          T* __restrict__ k_out, T* __restrict__ v_out) {
+  const int half = D / 2, tpr = half / 4;  // threads per row
+  const int rows_per_block = blockDim.x / tpr;
+  const int i = 4 * (threadIdx.x % tpr);
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * rows_per_block + threadIdx.x / tpr;
+  const int64_t bh = blockIdx.y;
+  if (j >= n_kept) return;
+  const int64_t src = keep[j];
+  T* ko = k_out + (bh * n_kept + j) * D;
+  T* vo = v_out ? v_out + (bh * n_kept + j) * D : nullptr;
+  Vec4<T> klo, khi, vlo, vhi;
+  if (src < 0 || src >= S) {  // never produced by the host; keep the access in bounds
+#pragma unroll
+    for (int e = 0; e < 4; ++e) klo.e[e] = khi.e[e] = from_f32<T>(0.0f);
+    *reinterpret_cast<Vec4<T>*>(ko + i) = klo;
+    *reinterpret_cast<Vec4<T>*>(ko + i + half) = khi;
+    if (vo) {
+      *reinterpret_cast<Vec4<T>*>(vo + i) = klo;
+      *reinterpret_cast<Vec4<T>*>(vo + i + half) = khi;
+    }
+    return;
+  }
+  const T* kr = k + (bh / H) * ksb + (bh % H) * ksh + src * kss;
+  const Vec4<T> a4 = *reinterpret_cast<const Vec4<T>*>(kr + i);
+  const Vec4<T> b4 = *reinterpret_cast<const Vec4<T>*>(kr + i + half);
+  const float4 col = *reinterpret_cast<const float4*>(cos_old + src * D + i);
+  const float4 coh = *reinterpret_cast<const float4*>(cos_old + src * D + i + half);
+  const float4 sol = *reinterpret_cast<const float4*>(sin_old + src * D + i);
+  const float4 soh = *reinterpret_cast<const float4*>(sin_old + src * D + i + half);
+  const float4 cnl = *reinterpret_cast<const float4*>(cos_new + j * D + i);
+  const float4 cnh = *reinterpret_cast<const float4*>(cos_new + j * D + i + half);
+  const float4 snl = *reinterpret_cast<const float4*>(sin_new + j * D + i);
+  const float4 snh = *reinterpret_cast<const float4*>(sin_new + j * D + i + half);
+  const float co_l[4] = {col.x, col.y, col.z, col.w}, co_h[4] = {coh.x, coh.y, coh.z, coh.w};
+  const float so_l[4] = {sol.x, sol.y, sol.z, sol.w}, so_h[4] = {soh.x, soh.y, soh.z, soh.w};
+  const float cn_l[4] = {cnl.x, cnl.y, cnl.z, cnl.w}, cn_h[4] = {cnh.x, cnh.y, cnh.z, cnh.w};
+  const float sn_l[4] = {snl.x, snl.y, snl.z, snl.w}, sn_h[4] = {snh.x, snh.y, snh.z, snh.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float a = to_f32(a4.e[e]), b = to_f32(b4.e[e]);
+    const float u_lo = round_to<T>(a * co_l[e] - (-b) * so_l[e]);
+    const float u_hi = round_to<T>(b * co_h[e] - a * so_h[e]);
+    klo.e[e] = from_f32<T>(u_lo * cn_l[e] + (-u_hi) * sn_l[e]);
+    khi.e[e] = from_f32<T>(u_hi * cn_h[e] + u_lo * sn_h[e]);
+  }
+  *reinterpret_cast<Vec4<T>*>(ko + i) = klo;
+  *reinterpret_cast<Vec4<T>*>(ko + i + half) = khi;
+  if (vo) {
+    const T* vr = v + (bh / H) * vsb + (bh % H) * vsh + src * vss;
+    vlo = *reinterpret_cast<const Vec4<T>*>(vr + i);
+    vhi = *reinterpret_cast<const Vec4<T>*>(vr + i + half);
+    *reinterpret_cast<Vec4<T>*>(vo + i) = vlo;
+    *reinterpret_cast<Vec4<T>*>(vo + i + half) = vhi;
+  }
+}
+
 }  // namespace
 }  // namespace fade
 
@@ -78,6 +147,19 @@ int rerope_gather(const char* fn, const void* k, int64_t ksb, int64_t ksh, int64
   if (BH == 0 || n_kept == 0) return FADE_OK;
   if (BH > 65535) return einval("%s: B*H=%lld exceeds 65535", fn, (long long)BH);
   const int half = static_cast<int>(D / 2);
+  auto al = [](const void* p, int b) { return (reinterpret_cast<uintptr_t>(p) % b) == 0; };
+  const int vb = 4 * static_cast<int>(sizeof(T));  // bytes of 4 elements
+  if (half % 4 == 0 && half / 4 <= 256 && al(k, vb) && al(k_out, vb) && (ksb | ksh | kss) % 4 == 0 &&
+      (v == nullptr || (al(v, vb) && al(v_out, vb) && (vsb | vsh | vss) % 4 == 0)) && al(cos_old, 16) &&
+      al(sin_old, 16) && al(cos_new, 16) && al(sin_new, 16)) {
+    const int tpr = half / 4, rpb4 = 256 / tpr;
+    const dim3 grid4(static_cast<unsigned>(cdiv(n_kept, rpb4)), static_cast<unsigned>(BH));
+    hipLaunchKernelGGL(rerope_gather_vec4_kernel<T>, grid4, dim3(rpb4 * tpr), 0, as_stream(stream),
+                       static_cast<const T*>(k), ksb, ksh, kss, static_cast<const T*>(v), vsb, vsh, vss, H, S,
+                       static_cast<int>(D), keep_idx, n_kept, cos_old, sin_old, cos_new, sin_new,
+                       static_cast<T*>(k_out), static_cast<T*>(v_out));
+    return check_launch(fn);
+  }
   const int rpb = half >= 256 ? 1 : 256 / half;
   const dim3 grid(static_cast<unsigned>(cdiv(n_kept, rpb)), static_cast<unsigned>(BH));
   hipLaunchKernelGGL(rerope_gather_kernel<T>, grid, dim3(rpb * half), 0, as_stream(stream), static_cast<const T*>(k),

@@ -77,7 +77,7 @@ def test_rerope_llama3_scheme_tables(dev):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("D", [128, 64, 32, 256])
+@pytest.mark.parametrize("D", [128, 64, 32, 256, 24, 20])  # 20: D/2 not a multiple of 4 (one element pair per thread)
 def test_rerope_typed_bit_exact(dev, dtype, D):
     """A bfloat16 / float32 cache: fp32 math, un-RoPE and re-RoPE each rounded
     to the cache dtype; bf16 tables are not rounded (fade/rope.py:83-93)."""
